@@ -1,0 +1,191 @@
+"""ctypes binding of libckv_amd.so (include/ckv_amd.h).
+
+The structures below mirror the C ABI field for field.  Every device call goes
+through :func:`lib`, which raises when the library is missing: there is no CPU
+fallback anywhere in the product path.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import functools
+import os
+import subprocess
+
+import torch
+
+PACKAGE_DIR = os.path.dirname(os.path.abspath(__file__))
+REPO_DIR = os.path.dirname(PACKAGE_DIR)
+LIB_PATH = os.path.join(PACKAGE_DIR, "libckv_amd.so")
+SOURCES = [
+    os.path.join(PACKAGE_DIR, "csrc", "ckv_decode.hip"),
+    os.path.join(PACKAGE_DIR, "csrc", "ckv_prefill.hip"),
+]
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+HIP_FLAGS = [
+    "--offload-arch=gfx950",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-shared",
+    "-ffp-contract=off",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+
+ABI_VERSION = 1
+
+CKV_BF16, CKV_F32, CKV_E4M3 = 0, 1, 2
+CKV_SELECT_BUDGET, CKV_SELECT_TOPK = 0, 1
+CKV_ASSIGN_NONE, CKV_ASSIGN_DELTA_Q, CKV_ASSIGN_NEAREST = 0, 1, 2
+
+TILE = 64
+KAPPA = 8
+SCORE_BLOCK = 64
+MAX_GROUP = 16
+MAX_COMMUNITIES = 8192
+MAX_DESCRIPTORS = 4096
+
+EXPORTED_SYMBOLS = (
+    "ckv_score_select",
+    "ckv_segmented_attention",
+    "ckv_decode_layer",
+    "ckv_dense_decode",
+    "ckv_prefill_attention_topk",
+    "ckv_host_numerics",
+    "ckv_abi_version",
+    "ckv_last_error",
+)
+
+_p = ctypes.c_void_p
+_i32 = ctypes.c_int32
+_i64 = ctypes.c_int64
+_f32 = ctypes.c_float
+
+
+class KvCache(ctypes.Structure):
+    _fields_ = [("query", _p), ("key", _p), ("value", _p), ("head_stride", _i64),
+                ("token_stride", _i64), ("capacity", _i64), ("query_heads", _i32),
+                ("kv_heads", _i32), ("dtype", _i32), ("reserved", _i32)]
+
+
+class PrefillCsr(ctypes.Structure):
+    _fields_ = [("member_offsets", _p), ("member_positions", _p), ("member_stride", _i64)]
+
+
+class DeltaChunks(ctypes.Structure):
+    _fields_ = [("positions", _p), ("chunk_start", _p), ("chunk_capacity", _p), ("chunk_size", _p),
+                ("chunk_next", _p), ("chunk_previous", _p), ("community_head", _p),
+                ("community_tail", _p), ("community_sizes", _p), ("next_free_chunk", _p),
+                ("next_free_position", _p), ("position_capacity", _i32), ("chunks_per_graph", _i32)]
+
+
+class GraphState(ctypes.Structure):
+    _fields_ = [("centroids", _p), ("community_sizes", _p), ("community_counts", _p),
+                ("community_weight", _p), ("total_weight", _p), ("token_communities", _p),
+                ("retrieval_to_graph", _p), ("retrieval_to_kv", _p), ("current_position", _p),
+                ("token_capacity", _i64), ("retrieval_heads", _i32), ("graph_count", _i32),
+                ("community_capacity", _i32), ("centroid_dtype", _i32)]
+
+
+class DecodeConfig(ctypes.Structure):
+    _fields_ = [("sink_positions", _p), ("group_size", _i32), ("num_sink", _i32),
+                ("token_budget", _i32), ("selection_mode", _i32), ("topk_communities", _i32),
+                ("max_selected", _i32), ("local_window", _i32), ("include_current", _i32),
+                ("assignment", _i32), ("score_coverage", _i32), ("softmax_scale", _f32),
+                ("lam", _f32)]
+
+
+class DecodeWorkspace(ctypes.Structure):
+    _fields_ = [("scores", _p), ("communities", _p), ("cumulative_ends", _p),
+                ("descriptor_counts", _p), ("tile_descriptors", _p), ("selected_counts", _p),
+                ("slot_positions", _p), ("nearest_partial", _p), ("nearest", _p),
+                ("block_counters", _p), ("partial_max", _p), ("partial_sum", _p),
+                ("partial_acc", _p), ("partial_topk", _p), ("output", _p), ("lse", _p),
+                ("topk_scores", _p), ("topk_positions", _p), ("assigned", _p), ("overflow", _p),
+                ("descriptor_capacity", _i32), ("slot_capacity", _i32), ("budget_tiles", _i32),
+                ("score_blocks", _i32)]
+
+
+class PrefillArgs(ctypes.Structure):
+    _fields_ = [("query", _p), ("key", _p), ("value", _p), ("output", _p), ("lse", _p),
+                ("topk_scores", _p), ("topk_indices", _p), ("q_row_stride", _i64),
+                ("q_head_stride", _i64), ("k_row_stride", _i64), ("k_head_stride", _i64),
+                ("o_row_stride", _i64), ("o_head_stride", _i64), ("seq_len", _i32),
+                ("query_heads", _i32), ("kv_heads", _i32), ("num_sink", _i32), ("kappa", _i32),
+                ("topk_rows", _i32), ("topk_skip", _i32), ("score_kind", _i32),
+                ("softmax_scale", _f32), ("reserved", _f32)]
+
+
+def build(verbose: bool = False) -> str:
+    """Compiles libckv_amd.so for gfx950 in-tree (always recompiles)."""
+    sources = [s for s in SOURCES if os.path.exists(s)]
+    cmd = [HIPCC, *HIP_FLAGS, "-I", os.path.join(REPO_DIR, "include"), "-o", LIB_PATH + ".tmp", *sources]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{proc.stderr[-4000:]}")
+    os.replace(LIB_PATH + ".tmp", LIB_PATH)
+    if verbose:
+        print(" ".join(cmd))
+    lib.cache_clear()
+    return LIB_PATH
+
+
+@functools.cache
+def lib() -> ctypes.CDLL:
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(
+            f"{LIB_PATH} is not built; run __graft_entry__.build() (hipcc --offload-arch=gfx950)")
+    handle = ctypes.CDLL(LIB_PATH)
+    for name in ("ckv_score_select", "ckv_segmented_attention", "ckv_decode_layer"):
+        fn = getattr(handle, name)
+        fn.argtypes = [ctypes.POINTER(KvCache), ctypes.POINTER(GraphState), ctypes.POINTER(PrefillCsr),
+                       ctypes.POINTER(DeltaChunks), ctypes.POINTER(DecodeConfig),
+                       ctypes.POINTER(DecodeWorkspace), _p]
+        fn.restype = ctypes.c_int
+    handle.ckv_dense_decode.argtypes = [ctypes.POINTER(KvCache), _i32, _f32, _p, _p, _p, _p, _p, _p]
+    handle.ckv_dense_decode.restype = ctypes.c_int
+    if hasattr(handle, "ckv_prefill_attention_topk"):
+        handle.ckv_prefill_attention_topk.argtypes = [ctypes.POINTER(PrefillArgs), _p]
+        handle.ckv_prefill_attention_topk.restype = ctypes.c_int
+    handle.ckv_host_numerics.argtypes = [ctypes.c_int, _p, _p, _i64]
+    handle.ckv_host_numerics.restype = ctypes.c_int
+    handle.ckv_last_error.restype = ctypes.c_char_p
+    handle.ckv_abi_version.restype = ctypes.c_int
+    if handle.ckv_abi_version() != ABI_VERSION:
+        raise RuntimeError("libckv_amd.so ABI version mismatch; rebuild it")
+    return handle
+
+
+def check(rc: int) -> None:
+    if rc != 0:
+        message = lib().ckv_last_error().decode(errors="replace")
+        raise RuntimeError(f"ckv error {rc}: {message}")
+
+
+def ptr(tensor: torch.Tensor | None) -> int | None:
+    return None if tensor is None else tensor.data_ptr()
+
+
+def stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def require_device(*tensors: torch.Tensor) -> torch.device:
+    """All tensors must live on one HIP device; CPU tensors are rejected."""
+    device = tensors[0].device
+    if device.type != "cuda":
+        raise RuntimeError("CommunityKV kernels run on the GPU only (got a CPU tensor)")
+    for t in tensors:
+        if t.device != device:
+            raise ValueError("all tensors must share one device")
+    return device
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    if dtype == torch.bfloat16:
+        return CKV_BF16
+    if dtype == torch.float32:
+        return CKV_F32
+    if dtype == torch.float8_e4m3fn:
+        return CKV_E4M3
+    raise TypeError(f"unsupported dtype {dtype}")

@@ -1,0 +1,225 @@
+"""Decode-state assembly from community labels (reference: community_kv/graph/partition.py).
+
+These builders run once per request (not per token).  They turn per-token
+community labels and the prefill keys into the tensors the decode kernels use:
+FP8 centroids with decode headroom, the recency-descending member CSR, and the
+modularity weights.  ``build_adjacency`` restates the reference's top-k edge
+graph.  Leiden itself (``partition_graphs``) is outside this build: callers
+supply labels through ``build_layer_from_labels`` or a ``PartitionRuntime``
+label provider.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, fields, replace
+
+import torch
+
+from community_kv_amd.config import GraphAggregation
+
+
+def leiden_max_iterations(input_context_length: int) -> int:
+    """Leiden sweep limit for a context length (partition.py:14-23)."""
+    if (not isinstance(input_context_length, int) or isinstance(input_context_length, bool)
+            or input_context_length <= 0):
+        raise ValueError("input_context_length must be a positive integer")
+    return max(1, math.floor(math.log10(input_context_length)))
+
+
+@dataclass(slots=True)
+class PartitionResult:
+    community_ids: torch.Tensor
+    community_counts: torch.Tensor
+    modularity: float
+    edge_src: torch.Tensor
+    edge_dst: torch.Tensor
+    edge_weight: torch.Tensor
+
+
+@dataclass(slots=True)
+class PartitionedLayer:
+    """Compact per-layer tensors handed to the decode runtime (partition.py:36-68)."""
+
+    layer_idx: int
+    prefill_seq_len: int
+    aggregation: GraphAggregation
+    query_heads: int
+    kv_heads: int
+    retrieval_to_graph: torch.Tensor
+    retrieval_to_kv: torch.Tensor
+    member_offsets: torch.Tensor
+    member_positions: torch.Tensor
+    community_counts: torch.Tensor
+    centroids: torch.Tensor
+    community_sizes: torch.Tensor
+    community_weight: torch.Tensor
+    total_weight: torch.Tensor
+    token_communities: torch.Tensor
+
+    def to(self, device: torch.device | str, *, non_blocking: bool = False) -> "PartitionedLayer":
+        target = torch.device(device)
+        updates = {f.name: getattr(self, f.name).to(target, non_blocking=non_blocking)
+                   for f in fields(self) if isinstance(getattr(self, f.name), torch.Tensor)}
+        return replace(self, **updates)
+
+
+def aggregation_mappings(aggregation: GraphAggregation, *, query_heads: int, kv_heads: int,
+                         device: torch.device | str) -> tuple[torch.Tensor, torch.Tensor]:
+    """Retrieval head -> (graph, KV head) (partition.py:71-94)."""
+    aggregation = GraphAggregation(aggregation)
+    count = aggregation.retrieval_head_count(query_heads=query_heads, kv_heads=kv_heads)
+    heads = torch.arange(count, dtype=torch.int32, device=device)
+    if aggregation is GraphAggregation.PER_QUERY_HEAD:
+        return heads, heads // (query_heads // kv_heads)
+    if aggregation is GraphAggregation.QUERY_GROUP:
+        return heads, heads.clone()
+    return torch.zeros_like(heads), heads
+
+
+def build_adjacency(topk_indices: torch.Tensor, topk_scores: torch.Tensor, query_positions: torch.Tensor,
+                    *, seq_len: int, lam: float) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Coalesced disjoint batched token graph from top-k edges (partition.py:168-249):
+    direct edges weighted lam/2 * p, co-occurrence edges (1 - lam) * p_i * p_j."""
+    graphs, _, kappa = topk_indices.shape
+    device = topk_indices.device
+    total = graphs * seq_len
+    offset = torch.arange(graphs, device=device, dtype=torch.int64).unsqueeze(1) * seq_len
+    src = (query_positions.long() + offset).unsqueeze(-1).expand_as(topk_indices)
+    dst = topk_indices.long() + offset.unsqueeze(-1)
+    ok = (topk_indices >= 0) & (topk_indices < seq_len)
+    a_src, a_dst, a_w = [src[ok]], [dst[ok]], [topk_scores.float()[ok] * (lam / 2.0)]
+    if lam < 1.0:
+        row, col = torch.triu_indices(kappa, kappa, device=device)
+        ci, cj = topk_indices[..., row], topk_indices[..., col]
+        ok2 = (ci >= 0) & (ci < seq_len) & (cj >= 0) & (cj < seq_len)
+        a_src.append((ci.long() + offset.unsqueeze(-1))[ok2])
+        a_dst.append((cj.long() + offset.unsqueeze(-1))[ok2])
+        a_w.append((topk_scores[..., row].float() * topk_scores[..., col].float())[ok2] * (1.0 - lam))
+    s = torch.cat(a_src)
+    d = torch.cat(a_dst)
+    lo, hi = torch.minimum(s, d), torch.maximum(s, d)
+    keys = lo * total + hi
+    unique, inverse = keys.unique(return_inverse=True)
+    weight = torch.zeros(unique.shape[0], dtype=torch.float32, device=device)
+    weight.scatter_add_(0, inverse, torch.cat(a_w))
+    return (unique // total).to(torch.int32), (unique % total).to(torch.int32), weight
+
+
+def compute_centroids(community_ids: torch.Tensor, community_counts: torch.Tensor, keys: torch.Tensor, *,
+                      retrieval_to_graph: torch.Tensor | None = None,
+                      retrieval_to_kv: torch.Tensor | None = None, num_sink: int,
+                      max_decode_tokens: int, fp8: bool = True) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-retrieval-head centroid tables: mean of each community's non-sink
+    keys, clamped to +-448 and stored as FP8 E4M3, with ``max_decode_tokens``
+    rows of headroom (partition.py:382-454)."""
+    graphs, seq_len = community_ids.shape
+    if keys.ndim != 3 or keys.shape[1] != seq_len:
+        raise ValueError("keys must have shape [KV heads, sequence, head dim]")
+    if retrieval_to_graph is None or retrieval_to_kv is None:
+        if keys.shape[0] != graphs:
+            raise ValueError("aggregation mappings are required when graph and KV counts differ")
+        retrieval_to_graph = torch.arange(graphs, dtype=torch.int32, device=community_ids.device)
+        retrieval_to_kv = retrieval_to_graph
+    heads = retrieval_to_graph.numel()
+    active = int(community_counts.max().item())
+    capacity = active + max_decode_tokens
+    dim = keys.shape[-1]
+    sums = torch.zeros((heads, capacity, dim), dtype=torch.float32, device=keys.device)
+    sizes = torch.zeros((heads, capacity), dtype=torch.int32, device=keys.device)
+    ids = community_ids[retrieval_to_graph.long(), num_sink:].long()
+    sums.scatter_add_(1, ids.unsqueeze(-1).expand(-1, -1, dim), keys[retrieval_to_kv.long(), num_sink:].float())
+    sizes.scatter_add_(1, ids, torch.ones_like(ids, dtype=torch.int32))
+    sums[:, :active].div_(sizes[:, :active].float().clamp_min(1).unsqueeze(-1))
+    limit = torch.finfo(torch.float8_e4m3fn).max
+    sums.clamp_(min=-limit, max=limit)
+    return (sums.to(torch.float8_e4m3fn) if fp8 else sums), sizes
+
+
+def build_member_csr(community_ids: torch.Tensor, community_counts: torch.Tensor, *,
+                     num_sink: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """Recency-descending membership CSR over non-sink positions (partition.py:457-492)."""
+    graphs, seq_len = community_ids.shape
+    maxc = int(community_counts.max().item())
+    ids = community_ids[:, num_sink:].long()
+    positions = torch.arange(num_sink, seq_len, dtype=torch.int64,
+                             device=community_ids.device).unsqueeze(0).expand(graphs, -1)
+    order = (ids * seq_len + (seq_len - 1 - positions)).argsort(dim=1)
+    member_positions = torch.gather(positions, 1, order).to(torch.int32)
+    counts = torch.zeros((graphs, maxc), dtype=torch.int64, device=community_ids.device)
+    counts.scatter_add_(1, ids, torch.ones_like(ids))
+    offsets = torch.zeros((graphs, maxc + 1), dtype=torch.int32, device=community_ids.device)
+    offsets[:, 1:] = counts.cumsum(dim=1).to(torch.int32)
+    return offsets, member_positions
+
+
+def init_modularity_state(result: PartitionResult, *, community_capacity: int,
+                          seq_len: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """Community degree weights and 2m from the coalesced edges (partition.py:495-535)."""
+    graphs = result.community_ids.shape[0]
+    device = result.community_ids.device
+    weight = torch.zeros((graphs, community_capacity), dtype=torch.float32, device=device)
+    total = torch.zeros((graphs,), dtype=torch.float32, device=device)
+    if not result.edge_src.numel():
+        return weight, total
+    src = result.edge_src.long()
+    dst = result.edge_dst.long()
+    graph = src // seq_len
+    sc = result.community_ids[graph, src % seq_len].long()
+    dc = result.community_ids[graph, dst % seq_len].long()
+    w = result.edge_weight.float()
+    flat = weight.view(-1)
+    flat.scatter_add_(0, graph * community_capacity + sc, w)
+    flat.scatter_add_(0, graph * community_capacity + dc, w)
+    total.scatter_add_(0, graph, 2.0 * w)
+    return weight, total
+
+
+def build_layer_from_labels(*, layer_idx: int, community_ids: torch.Tensor, keys: torch.Tensor,
+                            num_sink: int, max_decode_tokens: int, query_heads: int,
+                            aggregation: GraphAggregation = GraphAggregation.PER_QUERY_HEAD,
+                            edges: tuple[torch.Tensor, torch.Tensor, torch.Tensor] | None = None,
+                            fp8: bool = True) -> PartitionedLayer:
+    """Everything ``build_partitioned_layer`` (partition.py:538-618) produces
+    after Leiden, from given dense labels ``community_ids [graphs, S]``."""
+    if max_decode_tokens <= 0:
+        raise ValueError("max_decode_tokens must be positive")
+    kv_heads, seq_len, _ = keys.shape
+    aggregation = GraphAggregation(aggregation)
+    to_graph, to_kv = aggregation_mappings(aggregation, query_heads=query_heads, kv_heads=kv_heads,
+                                           device=keys.device)
+    ids = community_ids.to(device=keys.device, dtype=torch.int32)
+    counts = (ids[:, num_sink:].amax(dim=1) + 1).to(torch.int32)
+    centroids, sizes = compute_centroids(ids, counts, keys, retrieval_to_graph=to_graph, retrieval_to_kv=to_kv,
+                                         num_sink=num_sink, max_decode_tokens=max_decode_tokens, fp8=fp8)
+    offsets, positions = build_member_csr(ids, counts, num_sink=num_sink)
+    empty_i = torch.zeros(0, dtype=torch.int32, device=keys.device)
+    src, dst, w = edges if edges is not None else (empty_i, empty_i, torch.zeros(0, device=keys.device))
+    result = PartitionResult(ids, counts, 0.0, src, dst, w)
+    weight, total = init_modularity_state(result, community_capacity=centroids.shape[1], seq_len=seq_len)
+    tokens = torch.full((ids.shape[0], seq_len + max_decode_tokens), -1, dtype=torch.int32, device=keys.device)
+    tokens[:, :seq_len].copy_(ids)
+    return PartitionedLayer(layer_idx=layer_idx, prefill_seq_len=seq_len, aggregation=aggregation,
+                            query_heads=query_heads, kv_heads=kv_heads, retrieval_to_graph=to_graph,
+                            retrieval_to_kv=to_kv, member_offsets=offsets, member_positions=positions,
+                            community_counts=counts, centroids=centroids, community_sizes=sizes,
+                            community_weight=weight, total_weight=total, token_communities=tokens)
+
+
+def partition_graphs(*args, **kwargs) -> PartitionResult:
+    """Leiden partitioning (partition.py:289-353) is not part of this build."""
+    raise NotImplementedError(
+        "Leiden partitioning is outside the MI355X decode build; supply community labels "
+        "(build_layer_from_labels or a PartitionRuntime label provider)")
+
+
+def partition_query_groups(*args, **kwargs) -> PartitionResult:
+    """Query-group wrapper of :func:`partition_graphs` (partition.py:356-379)."""
+    return partition_graphs(*args, **kwargs)
+
+
+__all__ = [
+    "PartitionResult", "PartitionedLayer", "aggregation_mappings", "build_adjacency", "build_layer_from_labels",
+    "build_member_csr", "compute_centroids", "init_modularity_state", "leiden_max_iterations",
+    "partition_graphs", "partition_query_groups",
+]

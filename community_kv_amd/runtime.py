@@ -1,0 +1,373 @@
+"""Request runtime: prefill state conversion, per-layer decode, generate().
+
+Reference: community_kv/runtime.py.  ``CommunityKVRuntime`` keeps the
+reference constructor, context-manager protocol and ``generate`` contract
+(batch 1, greedy, model configured with ``attn_implementation="community_kv"``).
+State is validated once per layer in ``prepare_layer``; ``decode`` is a single
+native call per layer with no host synchronisation.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from types import TracebackType
+from typing import Any, Mapping, Sequence
+
+import torch
+
+from community_kv_amd.attention.decode import DecodeLayerWorkspace, decode_layer
+from community_kv_amd.config import CommunityKVConfig, GraphAggregation, PartitionConfig
+from community_kv_amd.graph.partition import PartitionedLayer
+from community_kv_amd.graph.runtime import PartitionRuntime
+from community_kv_amd.graph.state import DecodeDeltaChunks, MutableGraphState, PrefillCSR
+
+HEAD_DIM = 128
+ATTENTION_TILE = 64
+
+
+def _effective_token_budget(*, configured_budget: int, prefill_seq_len: int, num_sink: int) -> int:
+    """Largest whole-tile budget the prefill can fill exactly (runtime.py:22-34)."""
+    available = ((prefill_seq_len + 1) // ATTENTION_TILE) * ATTENTION_TILE
+    effective = min(configured_budget, available)
+    if effective <= num_sink + 1:
+        raise ValueError("prefill sequence is too short for the fixed 64-token decode kernel")
+    return effective
+
+
+@dataclass(slots=True)
+class ConvertedPrefillState:
+    csr: PrefillCSR
+    mutable: MutableGraphState
+    current_position: torch.Tensor
+    initial_community_counts: tuple[int, ...]
+    prefill_seq_len: int
+    decode_capacity: int
+    group_size: int
+    aggregation: GraphAggregation
+    query_heads: int
+    kv_heads: int
+
+
+@dataclass(slots=True)
+class DecodeLayerState:
+    converted: ConvertedPrefillState
+    workspace: DecodeLayerWorkspace
+    sink_positions: torch.Tensor
+
+
+def _pad_member_offsets(member_offsets: torch.Tensor, *, community_capacity: int) -> torch.Tensor:
+    if member_offsets.dtype != torch.int32 or member_offsets.ndim != 2:
+        raise TypeError("member_offsets must be a rank-two int32 tensor")
+    width = community_capacity + 1
+    if member_offsets.shape[1] > width:
+        raise ValueError("member offsets exceed centroid community capacity")
+    if member_offsets.shape[1] == width:
+        return member_offsets.contiguous()
+    padded = torch.empty((member_offsets.shape[0], width), dtype=torch.int32, device=member_offsets.device)
+    padded[:, :member_offsets.shape[1]].copy_(member_offsets)
+    padded[:, member_offsets.shape[1]:].copy_(member_offsets[:, -1:])
+    return padded
+
+
+def convert_prefill_tensors(*, member_offsets: torch.Tensor, member_positions: torch.Tensor,
+                            num_communities: torch.Tensor, centroids: torch.Tensor, community_sizes: torch.Tensor,
+                            community_weight: torch.Tensor, total_weight: torch.Tensor,
+                            token_communities: torch.Tensor, retrieval_to_graph: torch.Tensor | None = None,
+                            retrieval_to_kv: torch.Tensor | None = None, prefill_seq_len: int,
+                            max_decode_tokens: int, group_size: int = 4,
+                            aggregation: GraphAggregation = GraphAggregation.PER_QUERY_HEAD,
+                            query_heads: int | None = None, kv_heads: int | None = None) -> ConvertedPrefillState:
+    """Validates explicit prefill tensors and allocates decode-delta pages (runtime.py:85-234)."""
+    if centroids.ndim != 3 or centroids.shape[-1] != HEAD_DIM:
+        raise ValueError("centroids must have shape [retrieval heads, communities, 128]")
+    if centroids.dtype not in (torch.float8_e4m3fn, torch.float32):
+        raise TypeError("centroids must use FP8 E4M3")
+    heads, capacity, _ = centroids.shape
+    graphs = member_offsets.shape[0]
+    if min(heads, graphs, capacity) <= 0:
+        raise ValueError("prefill state must contain active graphs and centroids")
+    if member_positions.dtype != torch.int32 or member_positions.ndim != 2:
+        raise TypeError("member_positions must be a rank-two int32 tensor")
+    if member_positions.shape[0] != graphs:
+        raise ValueError("member positions must contain one row per graph")
+    if num_communities.dtype != torch.int32:
+        raise TypeError("num_communities must use int32")
+    if num_communities.shape != (graphs,):
+        raise ValueError("num_communities must contain one value per graph")
+    if community_sizes.shape != centroids.shape[:2]:
+        raise ValueError("community_sizes must match centroids")
+    if community_sizes.dtype != torch.int32:
+        raise TypeError("community_sizes must use int32")
+    if community_weight.shape != (graphs, capacity):
+        raise ValueError("community_weight must have one row per graph")
+    if community_weight.dtype != torch.float32:
+        raise TypeError("community_weight must use float32")
+    if total_weight.shape != (graphs,) or total_weight.dtype != torch.float32:
+        raise TypeError("total_weight must be one float32 value per graph")
+    if token_communities.dtype != torch.int32 or token_communities.ndim != 2:
+        raise TypeError("token_communities must be a rank-two int32 tensor")
+    if token_communities.shape[0] != graphs:
+        raise ValueError("token_communities must contain one row per graph")
+    if prefill_seq_len <= 0 or max_decode_tokens <= 0:
+        raise ValueError("prefill and decode capacities must be positive")
+    if not 1 <= group_size <= 16:
+        raise ValueError("group_size must be in [1, 16]")
+    aggregation = GraphAggregation(aggregation)
+    if retrieval_to_graph is None or retrieval_to_kv is None:
+        if heads != graphs:
+            raise ValueError("aggregation mappings are required for non-identity state")
+        retrieval_to_graph = torch.arange(heads, dtype=torch.int32, device=centroids.device)
+        retrieval_to_kv = retrieval_to_graph
+    if (retrieval_to_graph.dtype != torch.int32 or retrieval_to_graph.shape != (heads,)
+            or retrieval_to_kv.dtype != torch.int32 or retrieval_to_kv.shape != (heads,)):
+        raise TypeError("aggregation mappings must be int32 retrieval-head vectors")
+    inferred = heads * group_size
+    query_heads = inferred if query_heads is None else query_heads
+    max_kv = int(retrieval_to_kv.max().item())
+    kv_heads = max_kv + 1 if kv_heads is None else kv_heads
+    if query_heads != inferred:
+        raise ValueError("query-head count does not match retrieval-head geometry")
+    if kv_heads <= 0 or max_kv >= kv_heads:
+        raise ValueError("KV-head count does not cover retrieval mappings")
+    if token_communities.shape[1] < prefill_seq_len + max_decode_tokens:
+        raise ValueError("token_communities lacks requested decode headroom")
+    tensors = (member_offsets, member_positions, num_communities, community_sizes, community_weight,
+               total_weight, token_communities, retrieval_to_graph, retrieval_to_kv)
+    if any(t.device != centroids.device for t in tensors):
+        raise ValueError("all converted tensors must share one device")
+    head_counts = num_communities[retrieval_to_graph.long()].contiguous()
+    initial = tuple(int(v) for v in head_counts.cpu().tolist())
+    if any(c <= 0 or c > capacity for c in initial):
+        raise ValueError("active community counts must fit centroid capacity")
+    csr = PrefillCSR(_pad_member_offsets(member_offsets, community_capacity=capacity),
+                     member_positions.contiguous(), num_communities.clone())
+    mutable = MutableGraphState(
+        centroids=centroids.contiguous(), community_sizes=community_sizes.contiguous(),
+        community_counts=head_counts.clone(), community_weight=community_weight.contiguous(),
+        total_weight=total_weight.contiguous(), token_communities=token_communities.contiguous(),
+        deltas=DecodeDeltaChunks.allocate(graph_count=graphs, community_capacity=capacity,
+                                          max_decode_tokens=max_decode_tokens, device=centroids.device),
+        retrieval_to_graph=retrieval_to_graph.contiguous(), retrieval_to_kv=retrieval_to_kv.contiguous())
+    current = torch.full((graphs,), prefill_seq_len, dtype=torch.int32, device=centroids.device)
+    csr.validate()
+    mutable.validate()
+    return ConvertedPrefillState(csr, mutable, current, initial, prefill_seq_len, max_decode_tokens, group_size,
+                                 aggregation, query_heads, kv_heads)
+
+
+class DecodeRuntime:
+    """Fixed-address collection of prepared layer states."""
+
+    def __init__(self, config: CommunityKVConfig) -> None:
+        self.config = config
+        self.layers: dict[int, DecodeLayerState] = {}
+
+    def reset(self) -> None:
+        self.layers.clear()
+
+    def prepare_partitioned_layer(self, state: PartitionedLayer) -> DecodeLayerState:
+        return self.prepare_layer(
+            state.layer_idx, member_offsets=state.member_offsets, member_positions=state.member_positions,
+            num_communities=state.community_counts, centroids=state.centroids,
+            community_sizes=state.community_sizes, community_weight=state.community_weight,
+            total_weight=state.total_weight, token_communities=state.token_communities,
+            retrieval_to_graph=state.retrieval_to_graph, retrieval_to_kv=state.retrieval_to_kv,
+            prefill_seq_len=state.prefill_seq_len,
+            max_decode_tokens=state.token_communities.shape[1] - state.prefill_seq_len,
+            group_size=state.query_heads // state.retrieval_to_graph.numel(), aggregation=state.aggregation,
+            query_heads=state.query_heads, kv_heads=state.kv_heads)
+
+    def prepare_layer(self, layer_idx: int, *, member_offsets, member_positions, num_communities, centroids,
+                      community_sizes, community_weight, total_weight, token_communities, retrieval_to_graph=None,
+                      retrieval_to_kv=None, prefill_seq_len: int, max_decode_tokens: int, group_size: int = 4,
+                      aggregation: GraphAggregation = GraphAggregation.PER_QUERY_HEAD, query_heads=None,
+                      kv_heads=None) -> DecodeLayerState:
+        if layer_idx in self.layers:
+            raise ValueError(f"layer {layer_idx} is already prepared")
+        converted = convert_prefill_tensors(
+            member_offsets=member_offsets, member_positions=member_positions, num_communities=num_communities,
+            centroids=centroids, community_sizes=community_sizes, community_weight=community_weight,
+            total_weight=total_weight, token_communities=token_communities, retrieval_to_graph=retrieval_to_graph,
+            retrieval_to_kv=retrieval_to_kv, prefill_seq_len=prefill_seq_len, max_decode_tokens=max_decode_tokens,
+            group_size=group_size, aggregation=aggregation, query_heads=query_heads, kv_heads=kv_heads)
+        mutable = converted.mutable
+        cfg = self.config
+        budget = _effective_token_budget(configured_budget=cfg.token_budget, prefill_seq_len=prefill_seq_len,
+                                         num_sink=cfg.num_sink)
+        workspace = DecodeLayerWorkspace.allocate(
+            retrieval_head_count=mutable.retrieval_head_count, graph_count=mutable.graph_count,
+            group_size=converted.group_size, community_capacity=mutable.community_capacity, token_budget=budget,
+            num_sink=cfg.num_sink, dtype=torch.bfloat16, device=mutable.centroids.device,
+            score_community_counts=converted.initial_community_counts, score_headroom=max_decode_tokens,
+            local_window=cfg.local_window, include_current=cfg.include_current, selection=cfg.selection,
+            topk_communities=cfg.topk_communities, max_selected=cfg.max_selected, assignment=cfg.assignment)
+        layer = DecodeLayerState(converted, workspace,
+                                 torch.arange(cfg.num_sink, dtype=torch.int32, device=mutable.centroids.device))
+        self.layers[layer_idx] = layer
+        return layer
+
+    def decode(self, *, layer_idx: int, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+               softmax_scale: float) -> torch.Tensor:
+        layer = self.layers.get(layer_idx)
+        if layer is None:
+            raise RuntimeError(f"decode layer {layer_idx} is not prepared")
+        if query.ndim != 4 or query.shape[0] != 1 or query.shape[2] != 1 or query.shape[-1] != HEAD_DIM:
+            raise ValueError("decode requires query shape [1, Hq, 1, 128]")
+        if query.shape[1] != layer.converted.query_heads:
+            raise ValueError(f"decode expected {layer.converted.query_heads} query heads, found {query.shape[1]}")
+        if key.ndim != 4 or key.shape[0] != 1 or value.shape != key.shape:
+            raise ValueError("decode requires key/value shape [1, Hkv, S, 128]")
+        if key.shape[1] != layer.converted.kv_heads:
+            raise ValueError(f"decode expected {layer.converted.kv_heads} KV heads, found {key.shape[1]}")
+        output, *_ = decode_layer(
+            query=query[0, :, 0, :].contiguous(), key=key[0], value=value[0], csr=layer.converted.csr,
+            state=layer.converted.mutable, sink_positions=layer.sink_positions,
+            current_position=layer.converted.current_position, softmax_scale=softmax_scale, lam=self.config.lam,
+            workspace=layer.workspace)
+        return output.view(1, 1, query.shape[1], HEAD_DIM)
+
+    def assert_no_overflow(self) -> None:
+        failures = {idx: layer.workspace.update.overflow.detach().cpu().tolist()
+                    for idx, layer in self.layers.items()
+                    if torch.count_nonzero(layer.workspace.update.overflow).item()}
+        if failures:
+            raise RuntimeError(f"decode state overflow: {failures}")
+
+
+class CommunityKVRuntime:
+    """Request runtime spanning prefill, partition hand-off and decode (runtime.py:402-614)."""
+
+    def __init__(self, *, config: CommunityKVConfig, partition: PartitionConfig, num_layers: int,
+                 max_decode_tokens: int, label_provider=None) -> None:
+        if num_layers <= 0 or max_decode_tokens <= 0:
+            raise ValueError("num_layers and max_decode_tokens must be positive")
+        self.config = config
+        self.num_layers = num_layers
+        self.max_decode_tokens = max_decode_tokens
+        self.decode_runtime = DecodeRuntime(config)
+        self.partition_runtime = PartitionRuntime(algorithm=config, scheduling=partition, max_layers=num_layers,
+                                                  label_provider=label_provider)
+        self.resolutions: dict[int, float] = {}
+        self._ready = False
+        self._generation_cache: Any | None = None
+
+    def __enter__(self) -> "CommunityKVRuntime":
+        return self
+
+    def __exit__(self, exc_type: type[BaseException] | None, exc_value: BaseException | None,
+                 traceback: TracebackType | None) -> None:
+        self.close()
+
+    def start_request(self, *, resolutions: Mapping[int, float] | Sequence[float] | None = None,
+                      max_decode_tokens: int | None = None) -> None:
+        self.partition_runtime.reset()
+        self.decode_runtime.reset()
+        self._ready = False
+        if max_decode_tokens is not None:
+            if max_decode_tokens <= 0:
+                raise ValueError("max_decode_tokens must be positive")
+            self.max_decode_tokens = max_decode_tokens
+        if resolutions is None:
+            self.resolutions = {}
+        elif isinstance(resolutions, Mapping):
+            self.resolutions = {int(k): float(v) for k, v in resolutions.items()}
+        else:
+            if len(resolutions) != self.num_layers:
+                raise ValueError("resolution vector must contain one value per layer")
+            self.resolutions = {i: float(v) for i, v in enumerate(resolutions)}
+        if any(v <= 0 for v in self.resolutions.values()):
+            raise ValueError("all layer resolutions must be positive")
+
+    def submit_prefill_layer(self, *, layer_idx: int, topk_indices: torch.Tensor, topk_scores: torch.Tensor,
+                             keys: torch.Tensor, completion_event: Any) -> None:
+        self.partition_runtime.submit(
+            layer_idx=layer_idx, topk_indices=topk_indices, topk_scores=topk_scores, keys=keys,
+            completion_event=completion_event,
+            resolution=self.resolutions.get(layer_idx, self.config.leiden_resolution),
+            max_decode_tokens=self.max_decode_tokens)
+
+    def finish_prefill(self) -> None:
+        if self._ready:
+            return
+        self.partition_runtime.wait(self.decode_runtime.prepare_partitioned_layer)
+        actual = set(self.decode_runtime.layers)
+        expected = set(range(self.num_layers))
+        if actual != expected:
+            raise RuntimeError("partitioned layer set is incomplete: "
+                               f"missing={sorted(expected - actual)}, extra={sorted(actual - expected)}")
+        self._ready = True
+        if self._generation_cache is not None:
+            self._generation_cache.enable_device_updates()
+
+    def ensure_ready(self) -> None:
+        if not self._ready:
+            self.finish_prefill()
+
+    def generate(self, model: Any, inputs: torch.Tensor | None = None, *,
+                 resolutions: Mapping[int, float] | Sequence[float] | None = None, **kwargs: Any) -> Any:
+        """Generates one sequence with runtime-managed request state and cache (runtime.py:510-608)."""
+        if inputs is not None and "input_ids" in kwargs:
+            raise ValueError("pass input_ids either positionally or by keyword")
+        input_ids = kwargs.get("input_ids", inputs)
+        if not isinstance(input_ids, torch.Tensor) or input_ids.ndim != 2:
+            raise ValueError("generate requires rank-two input_ids")
+        if input_ids.shape[0] != 1:
+            raise ValueError("CommunityKV generate currently requires batch size 1")
+        if getattr(model.config, "_attn_implementation", None) != "community_kv":
+            raise ValueError("model.config._attn_implementation must be 'community_kv'")
+        for name, message in (("past_key_values", "CommunityKV generate manages past_key_values"),
+                              ("cache_implementation", "CommunityKV generate manages the cache implementation"),
+                              ("assistant_model", "CommunityKV generate does not support assisted generation"),
+                              ("penalty_alpha", "CommunityKV generate does not support contrastive search")):
+            if kwargs.get(name) is not None:
+                raise ValueError(message)
+        if kwargs.get("do_sample") not in (None, False):
+            raise ValueError("CommunityKV generate supports greedy decoding only")
+        generation_config = kwargs.get("generation_config", getattr(model, "generation_config", None))
+
+        def option(name: str, default: Any) -> Any:
+            return kwargs[name] if name in kwargs else getattr(generation_config, name, default)
+
+        if option("num_beams", 1) != 1:
+            raise ValueError("CommunityKV generate does not support beam search")
+        if option("num_return_sequences", 1) != 1:
+            raise ValueError("CommunityKV generate supports one returned sequence per prompt")
+        prompt_tokens = int(input_ids.shape[-1])
+        max_new_tokens = option("max_new_tokens", None)
+        if max_new_tokens is None:
+            max_length = option("max_length", None)
+            if max_length is None:
+                raise ValueError("generate requires max_new_tokens or max_length")
+            max_new_tokens = int(max_length) - prompt_tokens
+        if not isinstance(max_new_tokens, int) or isinstance(max_new_tokens, bool) or max_new_tokens <= 0:
+            raise ValueError("max_new_tokens must be a positive integer")
+        if int(model.config.num_hidden_layers) != self.num_layers:
+            raise ValueError(f"runtime has {self.num_layers} layers but model has {model.config.num_hidden_layers}")
+        from community_kv_amd.attention.cache import StaticCache
+
+        cache = StaticCache(num_hidden_layers=self.num_layers, max_cache_len=prompt_tokens + max_new_tokens)
+        if getattr(self, "_generation_cache", None) is not None:
+            raise RuntimeError("CommunityKV runtime is already generating")
+        self.start_request(resolutions=resolutions, max_decode_tokens=max(1, max_new_tokens - 1))
+        generate_kwargs = dict(kwargs)
+        generate_kwargs.update(past_key_values=cache, do_sample=False, num_beams=1, num_return_sequences=1)
+        if hasattr(generation_config, "disable_compile"):
+            generate_kwargs["disable_compile"] = True
+        self._generation_cache = cache
+        try:
+            output = model.generate(**generate_kwargs) if inputs is None else model.generate(inputs, **generate_kwargs)
+            self.finish_prefill()
+            self.assert_no_overflow()
+            return output
+        finally:
+            self._generation_cache = None
+
+    def close(self) -> None:
+        self.partition_runtime.shutdown()
+
+    def assert_no_overflow(self) -> None:
+        self.decode_runtime.assert_no_overflow()
+
+
+__all__ = ["CommunityKVRuntime", "ConvertedPrefillState", "DecodeLayerState", "DecodeRuntime",
+           "convert_prefill_tensors"]

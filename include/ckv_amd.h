@@ -1,0 +1,242 @@
+/*
+ * ckv_amd.h -- C ABI of the MI355X (gfx950) CommunityKV sparse-decode library
+ * (libckv_amd.so, built from community_kv_amd/csrc/).
+ *
+ * Every entry point takes plain device pointers and sizes, never allocates,
+ * never synchronises the host, runs on the HIP stream it is given, and returns
+ * 0 on success or a nonzero CKV_E* code with a message readable through
+ * ckv_last_error().  Tensors are dense row-major; the only strides are those
+ * of the KV cache.
+ *
+ * Reference interfaces replaced (paths relative to the reference repository):
+ *   ckv_score_select        score_and_select()                attention/kernels/centroid_selection.py:537-556
+ *                           = score_centroids()               attention/kernels/centroid_selection.py:330-445
+ *                           + select_weighted_descriptors()   attention/kernels/_csrc/bindings.cpp:3-21,
+ *                                                             attention/kernels/_csrc/descriptor_selection.cu:852-1189
+ *   ckv_segmented_attention triton_segmented_attention()      attention/kernels/segmented_attention.py:1016-1273
+ *                           (partials kernel 31-365, fused reduce+update kernel 368-864,
+ *                            shared-graph centroid sync 867-950)
+ *   ckv_decode_layer        decode_layer()                    attention/decode.py:67-111
+ *   ckv_dense_decode        (baseline only) dense bf16 decode over the whole cache, the
+ *                           FlashAttention decode the reference compares against (paper Table 5)
+ *   ckv_prefill_attention_topk
+ *                           prefill_attention_topk()          attention/flash_attention.py:23-51
+ *                           (patched FA3 op, third_party/flash_attention/community-kv.patch:31-120)
+ */
+#ifndef CKV_AMD_H
+#define CKV_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CKV_ABI_VERSION 1
+#define CKV_HEAD_DIM 128
+#define CKV_TILE 64
+#define CKV_KAPPA 8
+#define CKV_SCORE_BLOCK 64
+#define CKV_MAX_GROUP 16
+#define CKV_MAX_COMMUNITIES 8192
+#define CKV_MAX_DESCRIPTORS 4096
+
+enum ckv_status {
+  CKV_OK = 0,
+  CKV_E_INVALID = 1,   /* bad argument: shapes, modes, null pointers */
+  CKV_E_LIMIT = 2,     /* a size exceeds a compiled-in limit */
+  CKV_E_LAUNCH = 3     /* the HIP runtime reported a launch error */
+};
+
+enum ckv_dtype { CKV_BF16 = 0, CKV_F32 = 1, CKV_E4M3 = 2 };
+enum ckv_selection_mode { CKV_SELECT_BUDGET = 0, CKV_SELECT_TOPK = 1 };
+enum ckv_assignment { CKV_ASSIGN_NONE = 0, CKV_ASSIGN_DELTA_Q = 1, CKV_ASSIGN_NEAREST = 2 };
+
+/* Query and KV cache of one layer (reference: decode_layer query/key/value). */
+typedef struct ckv_kv_cache {
+  const void* query;        /* [query_heads][128], dtype */
+  const void* key;          /* key[h*head_stride + t*token_stride + d] */
+  const void* value;        /* same layout as key */
+  int64_t head_stride;      /* elements */
+  int64_t token_stride;     /* elements */
+  int64_t capacity;         /* tokens addressable per head (key.shape[1]) */
+  int32_t query_heads;
+  int32_t kv_heads;
+  int32_t dtype;            /* CKV_BF16 or CKV_F32 */
+  int32_t reserved;
+} ckv_kv_cache;
+
+/* Immutable prefill membership (reference: PrefillCSR, graph/state.py:15-61). */
+typedef struct ckv_prefill_csr {
+  const int32_t* member_offsets;    /* [graphs][community_capacity + 1] */
+  const int32_t* member_positions;  /* [graphs][member_stride], recency descending */
+  int64_t member_stride;
+} ckv_prefill_csr;
+
+/* Geometric decode-delta chunks (reference: DecodeDeltaChunks, graph/state.py:64-248). */
+typedef struct ckv_delta_chunks {
+  int32_t* positions;          /* [graphs][position_capacity] */
+  int32_t* chunk_start;        /* [graphs][chunks_per_graph] */
+  int32_t* chunk_capacity;
+  int32_t* chunk_size;
+  int32_t* chunk_next;
+  int32_t* chunk_previous;
+  int32_t* community_head;     /* [graphs][community_capacity] */
+  int32_t* community_tail;
+  int32_t* community_sizes;
+  int32_t* next_free_chunk;    /* [graphs] */
+  int32_t* next_free_position; /* [graphs] */
+  int32_t position_capacity;
+  int32_t chunks_per_graph;
+} ckv_delta_chunks;
+
+/* Mutable graph + centroid state (reference: MutableGraphState, graph/state.py:251-349). */
+typedef struct ckv_graph_state {
+  void* centroids;                   /* [retrieval_heads][community_capacity][128], centroid_dtype */
+  int32_t* community_sizes;          /* [retrieval_heads][community_capacity] */
+  int32_t* community_counts;         /* [retrieval_heads] */
+  float* community_weight;           /* [graph_count][community_capacity] */
+  float* total_weight;               /* [graph_count] */
+  int32_t* token_communities;        /* [graph_count][token_capacity] */
+  const int32_t* retrieval_to_graph; /* [retrieval_heads] */
+  const int32_t* retrieval_to_kv;    /* [retrieval_heads] */
+  int32_t* current_position;         /* [graph_count] */
+  int64_t token_capacity;
+  int32_t retrieval_heads;
+  int32_t graph_count;
+  int32_t community_capacity;
+  int32_t centroid_dtype;            /* CKV_E4M3 or CKV_F32 */
+} ckv_graph_state;
+
+/* Per-layer decode configuration (reference: CommunityKVConfig, config.py:33-58,
+ * plus this build's selection/window/assignment options). */
+typedef struct ckv_decode_config {
+  const int32_t* sink_positions; /* [num_sink] device */
+  int32_t group_size;            /* query heads per retrieval head, 1..16 */
+  int32_t num_sink;
+  int32_t token_budget;          /* multiple of 64 (reference semantics) */
+  int32_t selection_mode;        /* ckv_selection_mode */
+  int32_t topk_communities;      /* CKV_SELECT_TOPK only */
+  int32_t max_selected;          /* selected-token slots (budget mode: token_budget-num_sink-include_current) */
+  int32_t local_window;          /* recent tokens before the current one, set-union with the selection */
+  int32_t include_current;       /* 1: attend the current token (reference) */
+  int32_t assignment;            /* ckv_assignment */
+  int32_t score_coverage;        /* communities per head scored (<= community_capacity) */
+  float softmax_scale;
+  float lam;
+} ckv_decode_config;
+
+/* Preallocated workspace (reference: CentroidSelectionWorkspace centroid_selection.py:191-327,
+ * TritonSegmentedAttentionWorkspace segmented_attention.py:953-1013,
+ * OnlineUpdateWorkspace graph/kernels/online_update.py:10-35). */
+typedef struct ckv_decode_workspace {
+  uint16_t* scores;            /* [retrieval_heads][community_capacity] fp16 bits */
+  int32_t* communities;        /* [retrieval_heads][descriptor_capacity] */
+  int32_t* cumulative_ends;    /* [retrieval_heads][descriptor_capacity] */
+  int32_t* descriptor_counts;  /* [retrieval_heads] */
+  int32_t* tile_descriptors;   /* [retrieval_heads][budget_tiles] */
+  int32_t* selected_counts;    /* [retrieval_heads] */
+  int32_t* slot_positions;     /* [retrieval_heads][slot_capacity] KV position per attended slot, -1 = none */
+  uint64_t* nearest_partial;   /* [retrieval_heads][score_blocks] */
+  int32_t* nearest;            /* [retrieval_heads] */
+  uint32_t* block_counters;    /* [retrieval_heads], zero before first use; kernels leave it zero */
+  float* partial_max;          /* [query_heads][slot_tiles] */
+  float* partial_sum;          /* [query_heads][slot_tiles] */
+  float* partial_acc;          /* [query_heads][slot_tiles][128] */
+  uint64_t* partial_topk;      /* [retrieval_heads][slot_tiles][8] */
+  void* output;                /* [query_heads][128], kv dtype */
+  float* lse;                  /* [query_heads] */
+  float* topk_scores;          /* [retrieval_heads][8] */
+  int32_t* topk_positions;     /* [retrieval_heads][8] */
+  int32_t* assigned;           /* [graph_count] */
+  int32_t* overflow;           /* [graph_count] bit 1 community, 2 chunk pool, 4 position pool, 8 position */
+  int32_t descriptor_capacity;
+  int32_t slot_capacity;       /* multiple of 64 */
+  int32_t budget_tiles;        /* token_budget / 64 */
+  int32_t score_blocks;        /* ceil(score_coverage / 64) */
+} ckv_decode_workspace;
+
+/* Causal prefill attention with per-row top-kappa edge export (reference:
+ * patched FlashAttention-3 forward, community-kv.patch:31-120, 477-723).
+ * bf16 q [S][query_heads][128], k/v [S][kv_heads][128] (row/head strides in
+ * elements), GQA head h uses KV head h / (query_heads / kv_heads).
+ * Outputs: output like q (bf16), lse [query_heads][S] (natural log of the
+ * scaled softmax denominator), and for rows q >= topk_skip the kappa best
+ * columns c in [num_sink, q] of row q: topk_indices/topk_scores
+ * [query_heads][topk_rows][kappa].  Ranking key: the raw q.k score quantised as
+ * clamp(rint((s + 48) * 256), 0, 32767), ties to the larger column (the
+ * reference's packed key).  score_kind 0 stores the reference value
+ * exp((key/256 - 48) * scale - lse); 1 stores the raw score q.k. */
+typedef struct ckv_prefill_args {
+  const void* query;
+  const void* key;
+  const void* value;
+  void* output;
+  float* lse;
+  float* topk_scores;
+  int32_t* topk_indices;
+  int64_t q_row_stride;
+  int64_t q_head_stride;
+  int64_t k_row_stride;
+  int64_t k_head_stride;
+  int64_t o_row_stride;
+  int64_t o_head_stride;
+  int32_t seq_len;
+  int32_t query_heads;
+  int32_t kv_heads;
+  int32_t num_sink;
+  int32_t kappa;         /* 1..16 */
+  int32_t topk_rows;     /* seq_len - topk_skip */
+  int32_t topk_skip;     /* num_sink + kappa - 1 */
+  int32_t score_kind;
+  float softmax_scale;
+  float reserved;
+} ckv_prefill_args;
+
+int ckv_prefill_attention_topk(const ckv_prefill_args* args, void* stream);
+
+/* Score every retrieval head's centroids against its query group, select the
+ * communities that fill the budget (reference order: strictly-above-threshold
+ * communities by id, then threshold communities by id, last one truncated),
+ * emit descriptors, tile starts and the attended KV position of every slot.
+ * With CKV_ASSIGN_NEAREST also finds the current key's nearest centroid. */
+int ckv_score_select(const ckv_kv_cache* kv, const ckv_graph_state* state,
+                     const ckv_prefill_csr* csr, const ckv_delta_chunks* deltas,
+                     const ckv_decode_config* config, ckv_decode_workspace* ws,
+                     void* stream);
+
+/* Exact online-softmax attention over the slots chosen by ckv_score_select,
+ * then (assignment != NONE) the fused online update of the graph state. */
+int ckv_segmented_attention(const ckv_kv_cache* kv, const ckv_graph_state* state,
+                            const ckv_prefill_csr* csr, const ckv_delta_chunks* deltas,
+                            const ckv_decode_config* config, ckv_decode_workspace* ws,
+                            void* stream);
+
+/* ckv_score_select followed by ckv_segmented_attention. */
+int ckv_decode_layer(const ckv_kv_cache* kv, const ckv_graph_state* state,
+                     const ckv_prefill_csr* csr, const ckv_delta_chunks* deltas,
+                     const ckv_decode_config* config, ckv_decode_workspace* ws,
+                     void* stream);
+
+/* Dense decode baseline: every query head attends positions [0, seq_len) of its
+ * KV head (query head h uses KV head h / (query_heads / kv_heads)).  partial_*
+ * hold [query_heads][ceil(seq_len/64)] splits. */
+int ckv_dense_decode(const ckv_kv_cache* kv, int32_t seq_len, float softmax_scale,
+                     float* partial_max, float* partial_sum, float* partial_acc,
+                     void* output, float* lse, void* stream);
+
+/* Diagnostic, no counterpart in the reference: evaluates the library's scalar
+ * numerics on the host over n inputs, for parity tests without a GPU.
+ * op 0 exp -> f32, 1 log -> f32, 2 fp16 bits -> u16, 3 bf16 bits -> u16,
+ * 4 E4M3 code -> u8, 5 E4M3 code (given as float) -> f32. */
+int ckv_host_numerics(int op, const float* in, void* out, int64_t n);
+
+/* Library version and last error message of the calling thread. */
+int ckv_abi_version(void);
+const char* ckv_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CKV_AMD_H */
