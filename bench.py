@@ -1,0 +1,269 @@
+"""Sparse-decode benchmark on one MI355X (stacked to a
+36-layer Qwen3-8B attention stack).
+
+A step is one decode token through 36 independent Qwen3-8B-shaped attention
+layers (32 query / 8 KV heads, head_dim 128, bf16 KV, 32,768-token context,
+QUERY_GROUP graphs with 512 Zipf(1.1) communities per KV head, 2,048-token
+budget + 128-token recent window, 10 sinks, modularity-gain online update).
+Each layer owns its own KV cache and graph state (4.8 GB in total), so no layer
+finds another's data in the 256 MB Infinity Cache.  The whole step is captured
+in one HIP graph; inputs are resident in HBM before timing starts.
+
+Prints one JSON line (see DESIGN.md for the fields).
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+from community_kv_amd import _native as nat  # noqa: E402
+from community_kv_amd.attention.kernels import _abi  # noqa: E402
+from community_kv_amd.config import CommunityKVConfig, GraphAggregation  # noqa: E402
+from community_kv_amd.graph.partition import build_layer_from_labels  # noqa: E402
+from community_kv_amd.runtime import DecodeRuntime  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+LAYERS = 36
+HQ, HKV, D = 32, 8, 128
+SEQ = 32768
+COMMUNITIES = 512
+BUDGET = 2048
+WINDOW = 128
+SINKS = 10
+
+
+def zipf_labels(rng, seq, sinks, communities):
+    n = seq - sinks
+    raw = np.clip(rng.zipf(1.1, size=communities).astype(np.float64), 8, 1024)
+    sizes = np.maximum(1, np.round(raw * (n / raw.sum()))).astype(np.int64)
+    diff = n - int(sizes.sum())
+    order = np.argsort(-sizes, kind="stable")
+    i = 0
+    while diff:
+        j = order[i % communities]
+        step = 1 if diff > 0 else -1
+        if sizes[j] + step >= 1:
+            sizes[j] += step
+            diff -= step
+        i += 1
+    lab = np.repeat(np.arange(communities, dtype=np.int32), sizes)
+    rng.shuffle(lab)
+    out = np.zeros(seq, np.int32)
+    out[sinks:] = lab
+    return out
+
+
+def build_stack(device, layers, max_decode, seed=0):
+    cfg = CommunityKVConfig(token_budget=BUDGET, num_sink=SINKS, lam=0.5, aggregation=GraphAggregation.QUERY_GROUP,
+                            local_window=WINDOW)
+    runtime = DecodeRuntime(cfg)
+    rng = np.random.default_rng(seed)
+    gen = torch.Generator(device=device).manual_seed(seed)
+    cap = SEQ + max_decode + 1
+    stack = []
+    for li in range(layers):
+        labels = torch.from_numpy(np.stack([zipf_labels(rng, SEQ, SINKS, COMMUNITIES) for _ in range(HKV)])).to(device)
+        centers = torch.randn(HKV, COMMUNITIES, D, device=device, generator=gen)
+        key = torch.empty(HKV, cap, D, device=device, dtype=torch.bfloat16)
+        for h in range(HKV):
+            noise = torch.randn(SEQ, D, device=device, generator=gen)
+            key[h, :SEQ] = (centers[h, labels[h].long()] + 0.3 * noise).to(torch.bfloat16)
+            extra = torch.randint(0, COMMUNITIES, (cap - SEQ,), device=device, generator=gen)
+            key[h, SEQ:] = (centers[h, extra] + 0.3 * torch.randn(cap - SEQ, D, device=device, generator=gen)).to(
+                torch.bfloat16)
+        value = torch.randn(HKV, cap, D, device=device, generator=gen).to(torch.bfloat16)
+        part = build_layer_from_labels(layer_idx=li, community_ids=labels, keys=key[:, :SEQ], num_sink=SINKS,
+                                       max_decode_tokens=max_decode, query_heads=HQ,
+                                       aggregation=GraphAggregation.QUERY_GROUP)
+        part.community_weight.uniform_(0.5, 2.0, generator=gen)
+        part.total_weight.fill_(float(part.community_weight[0].sum()))
+        layer = runtime.prepare_partitioned_layer(part)
+        pick = torch.randint(0, COMMUNITIES, (HKV,), device=device, generator=gen)
+        query = (centers[torch.arange(HKV, device=device), pick].repeat_interleave(HQ // HKV, 0)
+                 + 0.5 * torch.randn(HQ, D, device=device, generator=gen)).to(torch.bfloat16).contiguous()
+        conv = layer.converted
+        call = layer.workspace.call(query=query, key=key, value=value, csr=conv.csr, state=conv.mutable,
+                                    sink_positions=layer.sink_positions, current_position=conv.current_position,
+                                    softmax_scale=D ** -0.5, lam=cfg.lam)
+        stack.append(dict(layer=layer, query=query, key=key, value=value, call=call))
+    return runtime, stack
+
+
+def capture(fn, device):
+    stream = torch.cuda.Stream(device)
+    stream.wait_stream(torch.cuda.current_stream(device))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        fn()
+    torch.cuda.synchronize(device)
+    return graph
+
+
+def time_graph(graph, reps, device):
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize(device)
+    start.record()
+    for _ in range(reps):
+        graph.replay()
+    stop.record()
+    torch.cuda.synchronize(device)
+    return start.elapsed_time(stop) / reps  # ms
+
+
+def algorithmic_bytes(stack):
+    """Per-layer bytes: attention (K+V rows of valid slots, slot indices, q)
+    and whole step (+ centroid table, sizes, scores, update)."""
+    att, step = [], []
+    for entry in stack:
+        sel = entry["layer"].workspace.selection
+        slots = sel.slot_positions
+        valid = int((slots >= 0).sum().item())
+        q_bytes = HQ * D * 2
+        a = valid * 2 * D * 2 + slots.numel() * 4 + q_bytes
+        counts = entry["layer"].converted.mutable.community_counts
+        c_bytes = int(counts.sum().item()) * (D * 1 + 4 + 2)
+        s = a + c_bytes + HQ * D * 2 + (D * 2 + 256) * HKV
+        att.append(a)
+        step.append(s)
+    return float(np.mean(att)), float(np.mean(step)), float(np.mean([int((e["layer"].workspace.selection.slot_positions >= 0).sum()) / HKV for e in stack]))
+
+
+def cpu_baseline(entry, seconds=20.0):
+    """Oracle decode step (numpy port of the reference semantics) on one layer's
+    state, single-threaded, for a bounded number of steps."""
+    from threadpoolctl import threadpool_limits
+
+    from oracle import ckv_oracle as co
+
+    layer = entry["layer"]
+    conv = layer.converted
+    m = conv.mutable
+    d = m.deltas
+    npy = lambda t: t.detach().cpu().numpy().copy()
+    deltas = co.DeltaChunks(*(npy(t) for t in d.tensors()))
+    st = co.LayerState(
+        centroids=npy(m.centroids.view(torch.uint8)), community_sizes=npy(m.community_sizes),
+        community_counts=npy(m.community_counts), community_weight=npy(m.community_weight),
+        total_weight=npy(m.total_weight), token_communities=npy(m.token_communities), deltas=deltas,
+        to_graph=npy(m.retrieval_to_graph), to_kv=npy(m.retrieval_to_kv), member_offsets=npy(conv.csr.member_offsets),
+        member_positions=npy(conv.csr.member_positions), current_position=npy(conv.current_position), fp8=True)
+    q = entry["query"].float().cpu().numpy()
+    k = entry["key"].float().cpu().numpy()
+    v = entry["value"].float().cpu().numpy()
+    params = co.StepParams(group_size=HQ // HKV, num_sink=SINKS, token_budget=BUDGET, local_window=WINDOW)
+    steps = 0
+    t0 = time.perf_counter()
+    with threadpool_limits(limits=1):
+        while True:
+            co.decode_step(st, q, k, v, params)
+            steps += 1
+            el = time.perf_counter() - t0
+            if el >= seconds or steps >= 50:
+                break
+    per_layer_step = el / steps
+    return {"value": 1.0 / (LAYERS * per_layer_step), "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"{steps} decode layer-steps of one config-2 layer through the numpy oracle "
+                      f"({per_layer_step * 1e3:.1f} ms per layer-step), scaled to 36 layers"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--layers", type=int, default=LAYERS)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1"}))
+        sys.exit(2)
+    device = torch.device("cuda:0")
+    max_decode = args.warmup + args.steps + 16
+    runtime, stack = build_stack(device, args.layers, max_decode)
+    torch.cuda.synchronize(device)
+
+    # whole step: 36 layer transitions (score/select, attention, update) in one graph
+    step_graph = capture(lambda: [e["call"].decode() for e in stack], device)
+    for _ in range(args.warmup):
+        step_graph.replay()
+    torch.cuda.synchronize(device)
+    ms = time_graph(step_graph, args.steps, device)
+    att_bytes, step_bytes, tokens_per_head = algorithmic_bytes(stack)
+    overflow = sum(int(e["layer"].workspace.update.overflow.sum().item()) for e in stack)
+
+    # dominant kernel alone: split-partials attention, 36 launches per replay
+    part_graph = capture(lambda: [e["call"].attention_partials() for e in stack], device)
+    part_graph.replay()
+    att_ms = time_graph(part_graph, max(10, args.steps), device) / len(stack)
+
+    # dense bf16 decode over the same 32k caches (baseline)
+    tiles = -(-SEQ // 64)
+    dense_ws = dict(pm=torch.empty(HQ, tiles, device=device), ps=torch.empty(HQ, tiles, device=device),
+                    pa=torch.empty(HQ, tiles, D, device=device), out=torch.empty(HQ, D, device=device,
+                                                                                 dtype=torch.bfloat16),
+                    lse=torch.empty(HQ, device=device))
+    dense_kv = [_abi.kv_struct(e["query"], e["key"], e["value"]) for e in stack]
+
+    def dense_step():
+        s = ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+        for kv in dense_kv:
+            nat.check(nat.lib().ckv_dense_decode(ctypes.byref(kv), SEQ, D ** -0.5, dense_ws["pm"].data_ptr(),
+                                                 dense_ws["ps"].data_ptr(), dense_ws["pa"].data_ptr(),
+                                                 dense_ws["out"].data_ptr(), dense_ws["lse"].data_ptr(), s))
+
+    dense_graph = capture(dense_step, device)
+    dense_graph.replay()
+    dense_ms = time_graph(dense_graph, max(5, args.steps // 5), device)
+
+    us_layer = ms * 1e3 / len(stack)
+    dense_us_layer = dense_ms * 1e3 / len(stack)
+    achieved = att_bytes / (att_ms * 1e-3) / 1e9
+    result = {
+        "metric": "sparse_decode_tokens_per_s_32k_qwen3_8b_attention_stack",
+        "value": 1e3 / ms,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (Gaussian-mixture keys, Zipf(1.1) community sizes, random-init state)",
+        "config": {"workload": "BASELINE config 2 layer x36: Qwen3-8B attention shape, batch 1, ctx 32768, "
+                               "512 communities/KV head, budget 2048 + window 128, QUERY_GROUP, delta-Q update",
+                   "layers": len(stack), "query_heads": HQ, "kv_heads": HKV, "head_dim": D, "context": SEQ,
+                   "token_budget": BUDGET, "local_window": WINDOW, "num_sink": SINKS},
+        "us_per_step_layer": us_layer,
+        "dense_us_per_step_layer": dense_us_layer,
+        "speedup_vs_dense": dense_us_layer / us_layer,
+        "attention_kernel_us": att_ms * 1e3,
+        "attended_tokens_per_head": tokens_per_head,
+        "step_algorithmic_bytes_per_layer": step_bytes,
+        "step_hbm_frac": step_bytes / (us_layer * 1e-6) / 1e9 / HBM_PEAK_GBS,
+        "overflow_flags": overflow,
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "kernel": "attend (split partials)", "bytes_per_launch": att_bytes},
+    }
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(stack[0], args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -17,10 +17,8 @@ import torch
 PACKAGE_DIR = os.path.dirname(os.path.abspath(__file__))
 REPO_DIR = os.path.dirname(PACKAGE_DIR)
 LIB_PATH = os.path.join(PACKAGE_DIR, "libckv_amd.so")
-SOURCES = [
-    os.path.join(PACKAGE_DIR, "csrc", "ckv_decode.hip"),
-    os.path.join(PACKAGE_DIR, "csrc", "ckv_prefill.hip"),
-]
+SOURCES = [os.path.join(PACKAGE_DIR, "csrc", name)
+           for name in ("ckv_decode.hip", "ckv_select.hip", "ckv_attend.hip", "ckv_prefill.hip")]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 HIP_FLAGS = [
     "--offload-arch=gfx950",
@@ -48,6 +46,7 @@ MAX_DESCRIPTORS = 4096
 EXPORTED_SYMBOLS = (
     "ckv_score_select",
     "ckv_segmented_attention",
+    "ckv_attention_partials",
     "ckv_decode_layer",
     "ckv_dense_decode",
     "ckv_prefill_attention_topk",
@@ -136,7 +135,7 @@ def lib() -> ctypes.CDLL:
         raise RuntimeError(
             f"{LIB_PATH} is not built; run __graft_entry__.build() (hipcc --offload-arch=gfx950)")
     handle = ctypes.CDLL(LIB_PATH)
-    for name in ("ckv_score_select", "ckv_segmented_attention", "ckv_decode_layer"):
+    for name in ("ckv_score_select", "ckv_segmented_attention", "ckv_attention_partials", "ckv_decode_layer"):
         fn = getattr(handle, name)
         fn.argtypes = [ctypes.POINTER(KvCache), ctypes.POINTER(GraphState), ctypes.POINTER(PrefillCsr),
                        ctypes.POINTER(DeltaChunks), ctypes.POINTER(DecodeConfig),

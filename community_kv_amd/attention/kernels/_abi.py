@@ -108,5 +108,8 @@ class DecodeCall:
     def attention(self, stream=None) -> None:
         nat.check(nat.lib().ckv_segmented_attention(*self._args(self._stream(stream))))
 
+    def attention_partials(self, stream=None) -> None:
+        nat.check(nat.lib().ckv_attention_partials(*self._args(self._stream(stream))))
+
     def decode(self, stream=None) -> None:
         nat.check(nat.lib().ckv_decode_layer(*self._args(self._stream(stream))))

@@ -38,7 +38,7 @@ class CentroidSelectionWorkspace:
     slot_positions: torch.Tensor    # [R, slot capacity] int32
     nearest_partial: torch.Tensor   # [R, score blocks] uint64
     nearest: torch.Tensor           # [R] int32
-    block_counters: torch.Tensor    # [R] int32 (zero; the kernel leaves it zero)
+    block_counters: torch.Tensor    # [2R] int32 arrival counters (zero; the kernels leave them zero)
     token_budget: int
     num_sink: int
     score_coverage: int
@@ -109,7 +109,7 @@ class CentroidSelectionWorkspace:
             slot_positions=i32((kv_heads, slots), -1),
             nearest_partial=torch.zeros((kv_heads, score_blocks), dtype=torch.uint64, device=device),
             nearest=i32((kv_heads,), -1),
-            block_counters=i32((kv_heads,)),
+            block_counters=i32((2 * kv_heads,)),
             token_budget=token_budget,
             num_sink=num_sink,
             score_coverage=coverage,

@@ -1,0 +1,780 @@
+// Attention over the selected slots, split merge and the fused online update.
+#include <type_traits>
+
+#include "ckv_device.h"
+
+namespace ckv {
+
+// ---------------------------------------------------------------------------
+// Kernel 2: attention partials (portable wave64 VALU version)
+// ---------------------------------------------------------------------------
+
+// One wave per 64-slot tile.  DENSE: rows come from [0, dense_len) and
+// blockIdx.y is a KV head; otherwise from the slot table of retrieval head
+// blockIdx.y.
+template <int DT, bool DENSE>
+__global__ __launch_bounds__(64) void attend_generic_kernel(DecodeArgs a, int dense_len, int dense_group) {
+  const int tile = blockIdx.x;
+  const int head = blockIdx.y;
+  const int lane = threadIdx.x;
+  const int tiles = gridDim.x;
+  const int G = DENSE ? dense_group : a.cfg.group_size;
+  const int kvh = DENSE ? head : a.st.retrieval_to_kv[head];
+  const float scale = a.cfg.softmax_scale;
+
+  __shared__ float q_s[CKV_MAX_GROUP * D];
+  __shared__ float p_s[CKV_MAX_GROUP * TILE];
+  __shared__ int pos_s[TILE];
+
+  int pos;
+  if (DENSE) {
+    const int t = tile * TILE + lane;
+    pos = t < dense_len ? t : -1;
+  } else {
+    pos = a.ws.slot_positions[(int64_t)head * a.ws.slot_capacity + tile * TILE + lane];
+  }
+  const bool valid = pos >= 0 && pos < a.kv.capacity;
+  pos_s[lane] = valid ? pos : -1;
+  for (int i = lane; i < G * D; i += 64) q_s[i] = load_elem<DT>(a.kv.query, (int64_t)head * G * D + i);
+  __syncthreads();
+
+  float s[CKV_MAX_GROUP];
+#pragma unroll
+  for (int g = 0; g < CKV_MAX_GROUP; ++g) s[g] = 0.0f;
+  if (valid) {
+    const int64_t row = kvh * a.kv.head_stride + (int64_t)pos * a.kv.token_stride;
+    for (int d0 = 0; d0 < D; d0 += 8) {
+      float k[8];
+      load8<DT>(a.kv.key, row + d0, k);
+#pragma unroll
+      for (int g = 0; g < CKV_MAX_GROUP; ++g) {
+        if (g < G) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) s[g] = s[g] + q_s[g * D + d0 + i] * k[i];
+        }
+      }
+    }
+  }
+  float m_g[CKV_MAX_GROUP];
+#pragma unroll
+  for (int g = 0; g < CKV_MAX_GROUP; ++g) {
+    if (g < G) {
+      const float sc = valid ? s[g] * scale : NEG_INF;
+      s[g] = sc;
+      const float m = wave_max(sc);
+      m_g[g] = m;
+      float p = (valid && m != NEG_INF) ? __expf(sc - m) : 0.0f;
+      const float l = wave_sum_tree(p);
+      if (DT == CKV_BF16) p = ckv_bf16_to_f32(ckv_f32_to_bf16_bits(p));
+      p_s[g * TILE + lane] = p;
+      if (lane == 0) {
+        const int qh = head * G + g;
+        a.ws.partial_max[(int64_t)qh * tiles + tile] = m;
+        a.ws.partial_sum[(int64_t)qh * tiles + tile] = l;
+      }
+    }
+  }
+  __syncthreads();
+  // P.V: lane owns dims 2*lane, 2*lane+1.
+  float o[CKV_MAX_GROUP][2];
+#pragma unroll
+  for (int g = 0; g < CKV_MAX_GROUP; ++g) o[g][0] = o[g][1] = 0.0f;
+  for (int t = 0; t < TILE; ++t) {
+    const int pt = pos_s[t];
+    if (pt < 0) continue;
+    const int64_t idx = kvh * a.kv.head_stride + (int64_t)pt * a.kv.token_stride + 2 * lane;
+    const float v0 = load_elem<DT>(a.kv.value, idx);
+    const float v1 = load_elem<DT>(a.kv.value, idx + 1);
+#pragma unroll
+    for (int g = 0; g < CKV_MAX_GROUP; ++g) {
+      if (g < G) {
+        const float p = p_s[g * TILE + t];
+        o[g][0] = o[g][0] + p * v0;
+        o[g][1] = o[g][1] + p * v1;
+      }
+    }
+  }
+#pragma unroll
+  for (int g = 0; g < CKV_MAX_GROUP; ++g) {
+    if (g < G) {
+      const int qh = head * G + g;
+      float* dst = a.ws.partial_acc + ((int64_t)qh * tiles + tile) * D + 2 * lane;
+      dst[0] = o[g][0];
+      dst[1] = o[g][1];
+    }
+  }
+  if (!DENSE && a.cfg.assignment != CKV_ASSIGN_NONE) {
+    const int slot = tile * TILE + lane;
+    uint64_t cand = (valid && slot >= a.cfg.num_sink) ? pack_candidate(s[0], pos) : 0ull;
+    for (int r = 0; r < KAPPA; ++r) {
+      const uint64_t best = wave_max_u64(cand);
+      if (lane == 0) a.ws.partial_topk[((int64_t)head * tiles + tile) * KAPPA + r] = best;
+      if (cand == best) cand = 0ull;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Kernel 3: split merge + fused online update
+// ---------------------------------------------------------------------------
+
+constexpr int MERGE_MAX_SPLITS = 2048;
+
+// Merges the split partials of query head qh into out/lse with any block size.
+// Splits whose max is -inf (no attended slot) are skipped.  Order: the max over
+// splits, then sums in split order with the library's deterministic exp/log.
+template <int DT>
+__device__ inline void merge_head(const DecodeArgs& a, int qh, int tiles, void* out, float* lse_out,
+                                  float* lse_keep) {
+  __shared__ float scale_s[MERGE_MAX_SPLITS];
+  __shared__ float m_s, denom_s;
+  const int tid = threadIdx.x;
+  const float* pm = a.ws.partial_max + (int64_t)qh * tiles;
+  const float* ps = a.ws.partial_sum + (int64_t)qh * tiles;
+  __syncthreads();
+  if (tid < 64) {
+    float M = NEG_INF;
+    for (int t = tid; t < tiles; t += 64) M = fmax_exact(M, pm[t]);
+    M = wave_max(M);
+    if (tid == 0) m_s = M;
+  }
+  __syncthreads();
+  const float M = m_s;
+  for (int t = tid; t < tiles; t += blockDim.x) {
+    const float mt = pm[t];
+    scale_s[t] = (mt == NEG_INF) ? 0.0f : ckv_expf(mt - M);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float denom = 0.0f;
+    for (int t = 0; t < tiles; ++t) {
+      if (scale_s[t] != 0.0f) denom = denom + ps[t] * scale_s[t];
+    }
+    denom_s = denom;
+  }
+  __syncthreads();
+  for (int d = tid; d < D; d += blockDim.x) {
+    float acc = 0.0f;
+    for (int t = 0; t < tiles; ++t) {
+      const float sc = scale_s[t];
+      if (sc != 0.0f) acc = acc + a.ws.partial_acc[((int64_t)qh * tiles + t) * D + d] * sc;
+    }
+    const float r = acc / denom_s;
+    if constexpr (DT == CKV_BF16) {
+      reinterpret_cast<uint16_t*>(out)[(int64_t)qh * D + d] = ckv_f32_to_bf16_bits(r);
+    } else {
+      reinterpret_cast<float*>(out)[(int64_t)qh * D + d] = r;
+    }
+  }
+  __syncthreads();
+  if (tid == 0) {
+    const float l = M + ckv_logf(denom_s);
+    lse_out[qh] = l;
+    if (lse_keep) *lse_keep = l;
+  }
+}
+
+// Split merge of retrieval head rh's G query heads, then (graph owners) the
+// fused online update.  Any block size >= 64.
+template <int CT, int DT>
+__device__ void merge_update(const DecodeArgs& a, const int rh, const int tiles) {
+  const int tid = threadIdx.x;
+  const int G = a.cfg.group_size;
+  __shared__ float s_lse0;
+  for (int g = 0; g < G; ++g) {
+    merge_head<DT>(a, rh * G + g, tiles, a.ws.output, a.ws.lse, g == 0 ? &s_lse0 : nullptr);
+  }
+  const int graph = a.st.retrieval_to_graph[rh];
+  if (a.cfg.assignment == CKV_ASSIGN_NONE || rh != graph) return;
+  __syncthreads();
+
+  const int C = a.st.community_capacity;
+  __shared__ uint64_t top[KAPPA];
+  __shared__ int s_assigned, s_comm_ov, s_old_size, s_valid_pos, s_cur;
+
+  // Exact top-8 merge over every tile's candidates (wave 0).
+  if (tid < 64) {
+    const int n = tiles * KAPPA;
+    const uint64_t* cand = a.ws.partial_topk + (int64_t)rh * n;
+    uint64_t taken_hi = 0ull;  // candidates are unique; exclude by value
+    for (int r = 0; r < KAPPA; ++r) {
+      uint64_t best = 0ull;
+      for (int i = tid; i < n; i += 64) {
+        const uint64_t v = cand[i];
+        if (v < taken_hi || taken_hi == 0ull) best = v > best ? v : best;
+      }
+      best = wave_max_u64(best);
+      if (tid == 0) top[r] = best;
+      taken_hi = best == 0ull ? 1ull : best;  // next round takes values strictly below
+      if (best == 0ull) {
+        for (int rr = r + 1; rr < KAPPA; ++rr) {
+          if (tid == 0) top[rr] = 0ull;
+        }
+        break;
+      }
+    }
+  }
+  __syncthreads();
+
+  if (tid == 0) {
+    float sc[KAPPA];
+    int ps[KAPPA];
+    for (int r = 0; r < KAPPA; ++r) {
+      const uint64_t v = top[r];
+      if (v == 0ull) {
+        sc[r] = NEG_INF;
+        ps[r] = -1;
+      } else {
+        sc[r] = unordered_f32((uint32_t)(v >> 32));
+        ps[r] = (int)(0xffffffffu - (uint32_t)(v & 0xffffffffu));
+      }
+      a.ws.topk_scores[(int64_t)rh * KAPPA + r] = sc[r];
+      a.ws.topk_positions[(int64_t)rh * KAPPA + r] = ps[r];
+    }
+    const int cur = a.st.current_position[graph];
+    const int64_t tc_cap = a.st.token_capacity < a.kv.capacity ? a.st.token_capacity : a.kv.capacity;
+    const int active = a.st.community_counts[rh];
+    const int active_c = active < C ? active : C;
+    int assigned;
+    bool comm_ov;
+    if (a.cfg.assignment == CKV_ASSIGN_DELTA_Q) {
+      const float lse0 = s_lse0;
+      float p[KAPPA], dw[KAPPA], cw[KAPPA], oldw[KAPPA], dq[KAPPA];
+      int comm[KAPPA];
+      bool cand[KAPPA], leader[KAPPA];
+      const float half_lam = a.cfg.lam * 0.5f;
+      float nd = 0.0f, ssum = 0.0f, sq = 0.0f;
+      for (int r = 0; r < KAPPA; ++r) {
+        const bool valid = ps[r] >= 0 && ps[r] < tc_cap;
+        p[r] = valid ? ckv_expf(sc[r] - lse0) : 0.0f;
+        dw[r] = p[r] * half_lam;
+        nd = nd + dw[r];
+        ssum = ssum + p[r];
+        sq = sq + p[r] * p[r];
+        comm[r] = valid ? a.st.token_communities[(int64_t)graph * a.st.token_capacity + ps[r]] : -1;
+        cand[r] = valid && comm[r] >= 0 && comm[r] < active_c;
+      }
+      const float pair = (ssum * ssum - sq) * (0.5f * (1.0f - a.cfg.lam));
+      for (int r = 0; r < KAPPA; ++r) {
+        float acc = 0.0f;
+        int first = KAPPA;
+        for (int j = 0; j < KAPPA; ++j) {
+          if (cand[j] && comm[j] == comm[r]) {
+            acc = acc + dw[j];
+            first = j < first ? j : first;
+          }
+        }
+        cw[r] = acc;
+        leader[r] = cand[r] && first == r;
+      }
+      const float old_total = a.st.total_weight[graph];
+      float two_m = 2.0f * old_total;
+      two_m = two_m > 1.0f ? two_m : 1.0f;
+      float best = NEG_INF;
+      for (int r = 0; r < KAPPA; ++r) {
+        oldw[r] = cand[r] ? a.st.community_weight[(int64_t)graph * C + comm[r]] : 0.0f;
+        dq[r] = (cand[r] && cw[r] > 0.0f) ? (cw[r] - (nd * oldw[r]) / two_m) : NEG_INF;
+        best = fmax_exact(best, dq[r]);
+      }
+      int best_comm = 0x7fffffff;
+      for (int r = 0; r < KAPPA; ++r) {
+        if (cand[r] && dq[r] == best && comm[r] < best_comm) best_comm = comm[r];
+      }
+      const bool join = best > 0.0f;
+      assigned = join ? best_comm : active;
+      comm_ov = assigned >= C;
+      if (!comm_ov) {
+        for (int r = 0; r < KAPPA; ++r) {
+          if (leader[r]) {
+            const float inc = cw[r] + ((join && comm[r] == assigned) ? nd : 0.0f);
+            a.st.community_weight[(int64_t)graph * C + comm[r]] = oldw[r] + inc;
+          }
+        }
+        if (!join) a.st.community_weight[(int64_t)graph * C + assigned] = nd;
+        a.st.community_counts[rh] = active + (join ? 0 : 1);
+        a.st.total_weight[graph] = (old_total + nd) + pair;
+      }
+    } else {
+      const int nearest = a.ws.nearest[rh];
+      assigned = nearest >= 0 ? nearest : active;
+      comm_ov = assigned >= C;
+      if (nearest < 0 && !comm_ov) a.st.community_counts[rh] = active + 1;
+    }
+    a.ws.assigned[graph] = comm_ov ? -1 : assigned;
+    const bool valid_pos = cur >= 0 && cur < tc_cap;
+    int old_size = 0;
+    if (!comm_ov) {
+      old_size = a.st.community_sizes[(int64_t)rh * C + assigned];
+      a.st.community_sizes[(int64_t)rh * C + assigned] = old_size + 1;
+      if (valid_pos) a.st.token_communities[(int64_t)graph * a.st.token_capacity + cur] = assigned;
+    }
+    s_assigned = assigned;
+    s_comm_ov = comm_ov ? 1 : 0;
+    s_old_size = old_size;
+    s_valid_pos = valid_pos ? 1 : 0;
+    s_cur = cur;
+  }
+  __syncthreads();
+  const int kvh = a.st.retrieval_to_kv[rh];
+  for (int d = tid; d < D && !s_comm_ov && s_valid_pos; d += blockDim.x) {
+    const int asg = s_assigned;
+    const int old_size = s_old_size;
+    const int64_t ci = ((int64_t)rh * C + asg) * D + d;
+    const float key = load_elem<DT>(a.kv.key, kvh * a.kv.head_stride + (int64_t)s_cur * a.kv.token_stride + d);
+    float upd;
+    if (old_size > 0) {
+      const float old = load_centroid1<CT>(a.st.centroids, ci);
+      upd = (old * (float)old_size + key) / (float)(old_size + 1);
+    } else {
+      upd = key;
+    }
+    store_centroid1<CT>(a.st.centroids, ci, upd);
+  }
+  if (tid == 0) {
+    const int asg = s_assigned;
+    const bool comm_ov = s_comm_ov != 0;
+    const bool valid_pos = s_valid_pos != 0;
+    const int cur = s_cur;
+    bool chunk_ov = false, pos_ov = false;
+    if (!comm_ov) {
+      const int64_t tb = (int64_t)graph * C + asg;
+      const int64_t cb = (int64_t)graph * a.dl.chunks_per_graph;
+      const int delta_size = a.dl.community_sizes[tb];
+      const int old_tail = a.dl.community_tail[tb];
+      const int old_cs = old_tail >= 0 ? a.dl.chunk_size[cb + old_tail] : 0;
+      const int old_cc = old_tail >= 0 ? a.dl.chunk_capacity[cb + old_tail] : 0;
+      const bool allocate = old_tail < 0 || old_cs >= old_cc;
+      const int free_chunk = a.dl.next_free_chunk[graph];
+      const int free_pos = a.dl.next_free_position[graph];
+      const int new_cap = old_tail < 0 ? 1 : old_cc * 2;
+      chunk_ov = allocate && free_chunk >= a.dl.chunks_per_graph;
+      pos_ov = allocate && free_pos + new_cap > a.dl.position_capacity;
+      const bool alloc_ov = chunk_ov || pos_ov;
+      const int chunk = allocate ? free_chunk : old_tail;
+      const bool valid_chunk = !alloc_ov && chunk >= 0 && chunk < a.dl.chunks_per_graph;
+      if (allocate && !alloc_ov) {
+        a.dl.next_free_chunk[graph] = free_chunk + 1;
+        a.dl.next_free_position[graph] = free_pos + new_cap;
+        a.dl.chunk_start[cb + free_chunk] = free_pos;
+        a.dl.chunk_capacity[cb + free_chunk] = new_cap;
+        a.dl.chunk_previous[cb + free_chunk] = old_tail;
+        if (old_tail < 0) {
+          a.dl.community_head[tb] = free_chunk;
+        } else {
+          a.dl.chunk_next[cb + old_tail] = free_chunk;
+        }
+        a.dl.community_tail[tb] = free_chunk;
+      }
+      if (valid_chunk && valid_pos) {
+        const int start = allocate ? free_pos : a.dl.chunk_start[cb + old_tail];
+        const int slot = allocate ? 0 : old_cs;
+        a.dl.positions[(int64_t)graph * a.dl.position_capacity + start + slot] = cur;
+        a.dl.chunk_size[cb + chunk] = slot + 1;
+        a.dl.community_sizes[tb] = delta_size + 1;
+      }
+    }
+    const int overflow = (comm_ov ? 1 : 0) | (chunk_ov ? 2 : 0) | (pos_ov ? 4 : 0) | (valid_pos ? 0 : 8);
+    a.ws.overflow[graph] = overflow;
+    if (overflow == 0) a.st.current_position[graph] = cur + 1;
+  }
+}
+
+template <int CT, int DT>
+__global__ __launch_bounds__(REDUCE_THREADS) void reduce_update_kernel(DecodeArgs a) {
+  merge_update<CT, DT>(a, blockIdx.x, a.ws.slot_capacity / TILE);
+}
+
+template <int CT, int DT>
+__global__ __launch_bounds__(REDUCE_THREADS) void sync_shared_kernel(DecodeArgs a) {
+  const int rh = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int graph = a.st.retrieval_to_graph[rh];
+  if (rh == graph) return;
+  const int C = a.st.community_capacity;
+  const int community = a.ws.assigned[graph];
+  const bool valid = a.ws.overflow[graph] == 0 && community >= 0;
+  if (!valid) return;
+  const int cur = a.st.current_position[graph] - 1;
+  const int64_t tc_cap = a.st.token_capacity < a.kv.capacity ? a.st.token_capacity : a.kv.capacity;
+  const bool valid_pos = cur >= 0 && cur < tc_cap;
+  const int old_size = a.st.community_sizes[(int64_t)rh * C + community];
+  __syncthreads();
+  const int kvh = a.st.retrieval_to_kv[rh];
+  if (valid_pos && tid < D) {
+    const int64_t ci = ((int64_t)rh * C + community) * D + tid;
+    const float key = load_elem<DT>(a.kv.key, kvh * a.kv.head_stride + (int64_t)cur * a.kv.token_stride + tid);
+    float upd;
+    if (old_size > 0) {
+      const float old = load_centroid1<CT>(a.st.centroids, ci);
+      upd = (old * (float)old_size + key) / (float)(old_size + 1);
+    } else {
+      upd = key;
+    }
+    store_centroid1<CT>(a.st.centroids, ci, upd);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    a.st.community_sizes[(int64_t)rh * C + community] = old_size + 1;
+    a.st.community_counts[rh] = a.st.community_counts[graph];
+  }
+}
+
+// Merge-only reduce for the dense baseline.
+template <int DT>
+__global__ __launch_bounds__(REDUCE_THREADS) void dense_reduce_kernel(DecodeArgs a, int tiles) {
+  merge_head<DT>(a, blockIdx.x, tiles, a.ws.output, a.ws.lse, nullptr);
+}
+
+// ---------------------------------------------------------------------------
+// MFMA attention (bf16): one wave per 64-slot tile
+// ---------------------------------------------------------------------------
+//
+// QK^T: v_mfma_f32_16x16x32_bf16 with A = 16 gathered K rows (M = slots,
+// K = 32 dims per step) and B = Q^T (N = the query group, zero-padded to 16).
+// The 64 slots of a tile are four 16-row sub-tiles; sub-tile j row r holds
+// tile slot tau(j, r), chosen so that the accumulator layout (lane l: query
+// l % 16, rows 4*(l/16)+i) is exactly the A operand of the P.V MFMA (lane l:
+// query l % 16, 8 consecutive K-slots 32*s + 8*(l/16) + u).  P.V: A = P (bf16,
+// as the reference rounds P before its dot), B = V^T read from an LDS copy of
+// the V tile (16 KB, chunk-swizzled so the four lane groups hit disjoint banks).
+
+constexpr int CKV_DENSE_CHUNK_TILES = 8;  // 512 tokens per dense wave
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ inline int tau(int j, int r) { return 32 * (j >> 1) + 8 * (r >> 2) + 4 * (j & 1) + (r & 3); }
+
+// LDS index of element (row, dim) of a 64 x 128 bf16 tile with swizzled 16-byte chunks.
+__device__ inline int vidx(int row, int dim) {
+  const int chunk = (dim >> 3) ^ (((row >> 3) & 3) << 1);
+  return row * D + (chunk << 3) + (dim & 7);
+}
+
+__device__ inline f32x4_t mfma_bf16(uint4 a, uint4 b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c,
+                                                 0, 0, 0);
+}
+
+__device__ inline uint32_t pack_bf16x2(float lo, float hi) {
+  return (uint32_t)ckv_f32_to_bf16_bits(lo) | ((uint32_t)ckv_f32_to_bf16_bits(hi) << 16);
+}
+
+// Computes one tile: scores (scaled, -inf where pos_s < 0), per-query max and
+// sum, and accumulates P.V into o (rows g = 4*(lane/16)+i, dims 16*nb + lane%16).
+// Returns through the references; `corr` rescales o before accumulation.
+struct TileResult {
+  float m;      // tile max of query lane%16 (scaled scores)
+  float l;      // sum of exp(score - m)
+};
+
+__device__ inline TileResult mfma_tile(const uint16_t* __restrict__ K, const uint16_t* __restrict__ V, int64_t kbase,
+                                       int64_t tstride, const int* pos_s, uint16_t* v_s, float* cand_s,
+                                       const uint4* qop, float scale, float m_prev, f32x4_t* o) {
+  const int lane = threadIdx.x;
+  const int L = lane >> 4;
+  const int c16 = lane & 15;
+  const uint4 zero = {0u, 0u, 0u, 0u};
+  uint4 kreg[4][4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int p = pos_s[tau(j, c16)];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      kreg[j][s] = p >= 0 ? *reinterpret_cast<const uint4*>(K + kbase + (int64_t)p * tstride + 32 * s + 8 * L) : zero;
+    }
+  }
+  uint4 vreg[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int p = pos_s[4 * i + L];
+    vreg[i] = p >= 0 ? *reinterpret_cast<const uint4*>(V + kbase + (int64_t)p * tstride + 8 * c16) : zero;
+  }
+  f32x4_t sacc[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    sacc[j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int s = 0; s < 4; ++s) sacc[j] = mfma_bf16(kreg[j][s], qop[s], sacc[j]);
+  }
+  // V tile -> LDS (row 4i+L, chunk c16), swizzled.
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int row = 4 * i + L;
+    *reinterpret_cast<uint4*>(v_s + vidx(row, 8 * c16)) = vreg[i];
+  }
+  float sc[4][4];
+  float mloc = NEG_INF;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const bool ok = pos_s[tau(j, 4 * L + i)] >= 0;
+      const float v = ok ? sacc[j][i] * scale : NEG_INF;
+      sc[j][i] = v;
+      mloc = fmax_exact(mloc, v);
+    }
+  }
+  if (cand_s != nullptr && c16 == 0) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) cand_s[tau(j, 4 * L + i)] = sc[j][i];
+    }
+  }
+  mloc = fmax_exact(mloc, __shfl_xor(mloc, 16, 64));
+  mloc = fmax_exact(mloc, __shfl_xor(mloc, 32, 64));
+  TileResult res;
+  const float m_new = fmax_exact(m_prev, mloc);
+  res.m = m_new;
+  float lsum = 0.0f;
+  uint32_t pk[4][2];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    float p[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      p[i] = sc[j][i] == NEG_INF ? 0.0f : __expf(sc[j][i] - m_new);
+      lsum = lsum + p[i];
+    }
+    pk[j][0] = pack_bf16x2(p[0], p[1]);
+    pk[j][1] = pack_bf16x2(p[2], p[3]);
+  }
+  lsum = lsum + __shfl_xor(lsum, 16, 64);
+  lsum = lsum + __shfl_xor(lsum, 32, 64);
+  res.l = lsum;
+  // rescale the running accumulator rows (query 4L+i) by exp(m_prev - m_new) of that query
+  {
+    const float corr_mine = (m_prev == NEG_INF) ? 0.0f : __expf(m_prev - m_new);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float c = __shfl(corr_mine, 4 * L + i, 64);
+#pragma unroll
+      for (int nb = 0; nb < 8; ++nb) o[nb][i] = o[nb][i] * c;
+    }
+  }
+  __syncthreads();  // V tile and candidates visible
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    const uint4 aop = {pk[2 * s][0], pk[2 * s][1], pk[2 * s + 1][0], pk[2 * s + 1][1]};
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) {
+      const int dim = 16 * nb + c16;
+      const int r0 = 32 * s + 8 * L;
+      uint32_t w[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        w[u] = (uint32_t)v_s[vidx(r0 + 2 * u, dim)] | ((uint32_t)v_s[vidx(r0 + 2 * u + 1, dim)] << 16);
+      }
+      const uint4 bop = {w[0], w[1], w[2], w[3]};
+      o[nb] = mfma_bf16(aop, bop, o[nb]);
+    }
+  }
+  return res;
+}
+
+template <int CT, bool FUSED>
+__global__ __launch_bounds__(64) void attend_mfma_kernel(DecodeArgs a) {
+  const int tile = blockIdx.x;
+  const int rh = blockIdx.y;
+  const int lane = threadIdx.x;
+  const int L = lane >> 4;
+  const int c16 = lane & 15;
+  const int tiles = gridDim.x;
+  const int G = a.cfg.group_size;
+  const int kvh = a.st.retrieval_to_kv[rh];
+  const uint16_t* K = reinterpret_cast<const uint16_t*>(a.kv.key);
+  const uint16_t* V = reinterpret_cast<const uint16_t*>(a.kv.value);
+  const uint16_t* Q = reinterpret_cast<const uint16_t*>(a.kv.query);
+
+  __shared__ __align__(16) uint16_t v_s[TILE * D];
+  __shared__ int pos_s[TILE];
+  __shared__ float cand_s[TILE];
+  __shared__ int last_block;
+
+  const int slot = tile * TILE + lane;
+  int pos = a.ws.slot_positions[(int64_t)rh * a.ws.slot_capacity + slot];
+  const bool valid = pos >= 0 && pos < a.kv.capacity;
+  if (!valid) pos = -1;
+  pos_s[lane] = pos;
+  const bool any = __ballot(valid) != 0ull;
+  const uint4 zero = {0u, 0u, 0u, 0u};
+  uint4 qop[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    qop[s] = c16 < G ? *reinterpret_cast<const uint4*>(Q + ((int64_t)rh * G + c16) * D + 32 * s + 8 * L) : zero;
+  }
+  __syncthreads();
+  const bool want_topk = a.cfg.assignment != CKV_ASSIGN_NONE;
+  if (any) {
+    f32x4_t o[8];
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) o[nb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    const TileResult r = mfma_tile(K, V, kvh * a.kv.head_stride, a.kv.token_stride, pos_s, v_s,
+                                   want_topk ? cand_s : nullptr, qop, a.cfg.softmax_scale, NEG_INF, o);
+    if (L == 0 && c16 < G) {
+      const int qh = rh * G + c16;
+      a.ws.partial_max[(int64_t)qh * tiles + tile] = r.m;
+      a.ws.partial_sum[(int64_t)qh * tiles + tile] = r.l;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int g = 4 * L + i;
+      if (g < G) {
+        float* dst = a.ws.partial_acc + ((int64_t)(rh * G + g) * tiles + tile) * D + c16;
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb) dst[16 * nb] = o[nb][i];
+      }
+    }
+    if (want_topk) {
+      uint64_t cand = (pos >= 0 && slot >= a.cfg.num_sink) ? pack_candidate(cand_s[lane], pos) : 0ull;
+      for (int k = 0; k < KAPPA; ++k) {
+        const uint64_t best = wave_max_u64(cand);
+        if (lane == 0) a.ws.partial_topk[((int64_t)rh * tiles + tile) * KAPPA + k] = best;
+        if (cand == best) cand = 0ull;
+      }
+    }
+  } else {
+    if (L == 0 && c16 < G) {
+      const int qh = rh * G + c16;
+      a.ws.partial_max[(int64_t)qh * tiles + tile] = NEG_INF;
+      a.ws.partial_sum[(int64_t)qh * tiles + tile] = 0.0f;
+    }
+    if (want_topk && lane < KAPPA) a.ws.partial_topk[((int64_t)rh * tiles + tile) * KAPPA + lane] = 0ull;
+  }
+  if (!FUSED) return;
+  // The last tile of this head to finish merges the splits and runs the update.
+  __threadfence();
+  __syncthreads();
+  if (lane == 0) {
+    uint32_t* counter = a.ws.block_counters + a.st.retrieval_heads + rh;
+    const unsigned prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    last_block = (prev == (unsigned)tiles - 1u) ? 1 : 0;
+    if (last_block) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!last_block) return;
+  __threadfence();
+  merge_update<CT, CKV_BF16>(a, rh, tiles);
+}
+
+// Dense bf16 decode baseline: each wave streams `chunk_tiles` consecutive
+// 64-token tiles of one KV head with an online softmax across tiles and writes
+// one split partial per query of its group.
+__global__ __launch_bounds__(64) void dense_mfma_kernel(DecodeArgs a, int seq_len, int group, int chunk_tiles) {
+  const int chunk = blockIdx.x;
+  const int kvh = blockIdx.y;
+  const int lane = threadIdx.x;
+  const int L = lane >> 4;
+  const int c16 = lane & 15;
+  const int chunks = gridDim.x;
+  const uint16_t* K = reinterpret_cast<const uint16_t*>(a.kv.key);
+  const uint16_t* V = reinterpret_cast<const uint16_t*>(a.kv.value);
+  const uint16_t* Q = reinterpret_cast<const uint16_t*>(a.kv.query);
+  __shared__ __align__(16) uint16_t v_s[TILE * D];
+  __shared__ int pos_s[TILE];
+  const uint4 zero = {0u, 0u, 0u, 0u};
+  uint4 qop[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    qop[s] = c16 < group ? *reinterpret_cast<const uint4*>(Q + ((int64_t)kvh * group + c16) * D + 32 * s + 8 * L)
+                         : zero;
+  }
+  f32x4_t o[8];
+#pragma unroll
+  for (int nb = 0; nb < 8; ++nb) o[nb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  float m = NEG_INF, l = 0.0f;
+  for (int t = 0; t < chunk_tiles; ++t) {
+    const int base = (chunk * chunk_tiles + t) * TILE;
+    if (base >= seq_len) break;
+    __syncthreads();
+    pos_s[lane] = base + lane < seq_len ? base + lane : -1;
+    __syncthreads();
+    const TileResult r = mfma_tile(K, V, kvh * a.kv.head_stride, a.kv.token_stride, pos_s, v_s, nullptr, qop,
+                                   a.cfg.softmax_scale, m, o);
+    const float corr = (m == NEG_INF) ? 0.0f : __expf(m - r.m);
+    l = l * corr + r.l;
+    m = r.m;
+  }
+  if (L == 0 && c16 < group) {
+    const int qh = kvh * group + c16;
+    a.ws.partial_max[(int64_t)qh * chunks + chunk] = m;
+    a.ws.partial_sum[(int64_t)qh * chunks + chunk] = l;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int g = 4 * L + i;
+    if (g < group) {
+      float* dst = a.ws.partial_acc + ((int64_t)(kvh * group + g) * chunks + chunk) * D + c16;
+#pragma unroll
+      for (int nb = 0; nb < 8; ++nb) dst[16 * nb] = o[nb][i];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Launchers
+// ---------------------------------------------------------------------------
+
+int launch_attention(const DecodeArgs& a, hipStream_t s, bool partials_only) {
+  const int tiles = a.ws.slot_capacity / TILE;
+  const dim3 grid(tiles, a.st.retrieval_heads);
+  const bool e4m3 = a.st.centroid_dtype == CKV_E4M3;
+  int r;
+  if (a.kv.dtype == CKV_BF16) {
+    if (partials_only) {
+      hipLaunchKernelGGL((attend_mfma_kernel<CKV_E4M3, false>), grid, dim3(64), 0, s, a);
+      return launch_check("attend_mfma");
+    }
+    if (e4m3) {
+      hipLaunchKernelGGL((attend_mfma_kernel<CKV_E4M3, true>), grid, dim3(64), 0, s, a);
+    } else {
+      hipLaunchKernelGGL((attend_mfma_kernel<CKV_F32, true>), grid, dim3(64), 0, s, a);
+    }
+    r = launch_check("attend_mfma");
+  } else {
+    hipLaunchKernelGGL((attend_generic_kernel<CKV_F32, false>), grid, dim3(64), 0, s, a, 0, 0);
+    r = launch_check("attend");
+    if (r || partials_only) return r;
+    if (e4m3) {
+      hipLaunchKernelGGL((reduce_update_kernel<CKV_E4M3, CKV_F32>), dim3(a.st.retrieval_heads), dim3(REDUCE_THREADS), 0,
+                         s, a);
+    } else {
+      hipLaunchKernelGGL((reduce_update_kernel<CKV_F32, CKV_F32>), dim3(a.st.retrieval_heads), dim3(REDUCE_THREADS), 0,
+                         s, a);
+    }
+    r = launch_check("reduce_update");
+  }
+  if (r) return r;
+  if (a.cfg.assignment != CKV_ASSIGN_NONE && a.st.retrieval_heads != a.st.graph_count) {
+    const dim3 g(a.st.retrieval_heads);
+    if (e4m3 && a.kv.dtype == CKV_BF16) hipLaunchKernelGGL((sync_shared_kernel<CKV_E4M3, CKV_BF16>), g, dim3(REDUCE_THREADS), 0, s, a);
+    else if (e4m3) hipLaunchKernelGGL((sync_shared_kernel<CKV_E4M3, CKV_F32>), g, dim3(REDUCE_THREADS), 0, s, a);
+    else if (a.kv.dtype == CKV_BF16) hipLaunchKernelGGL((sync_shared_kernel<CKV_F32, CKV_BF16>), g, dim3(REDUCE_THREADS), 0, s, a);
+    else hipLaunchKernelGGL((sync_shared_kernel<CKV_F32, CKV_F32>), g, dim3(REDUCE_THREADS), 0, s, a);
+    r = launch_check("sync_shared");
+  }
+  return r;
+}
+
+int dense_chunks(int seq_len, int chunk_tiles) { return (seq_len + TILE * chunk_tiles - 1) / (TILE * chunk_tiles); }
+
+int launch_dense(const DecodeArgs& a, int seq_len, int group, hipStream_t s) {
+  if (a.kv.dtype == CKV_BF16) {
+    const int chunk_tiles = CKV_DENSE_CHUNK_TILES;
+    const int chunks = dense_chunks(seq_len, chunk_tiles);
+    hipLaunchKernelGGL(dense_mfma_kernel, dim3(chunks, a.kv.kv_heads), dim3(64), 0, s, a, seq_len, group, chunk_tiles);
+    int r = launch_check("dense_mfma");
+    if (r) return r;
+    hipLaunchKernelGGL((dense_reduce_kernel<CKV_BF16>), dim3(a.kv.query_heads), dim3(REDUCE_THREADS), 0, s, a, chunks);
+    return launch_check("dense_reduce");
+  }
+  const int tiles = (seq_len + TILE - 1) / TILE;
+  hipLaunchKernelGGL((attend_generic_kernel<CKV_F32, true>), dim3(tiles, a.kv.kv_heads), dim3(64), 0, s, a, seq_len, group);
+  int r = launch_check("dense attend");
+  if (r) return r;
+  hipLaunchKernelGGL((dense_reduce_kernel<CKV_F32>), dim3(a.kv.query_heads), dim3(REDUCE_THREADS), 0, s, a, tiles);
+  return launch_check("dense reduce");
+}
+
+}  // namespace ckv

@@ -139,7 +139,7 @@ typedef struct ckv_decode_workspace {
   int32_t* slot_positions;     /* [retrieval_heads][slot_capacity] KV position per attended slot, -1 = none */
   uint64_t* nearest_partial;   /* [retrieval_heads][score_blocks] */
   int32_t* nearest;            /* [retrieval_heads] */
-  uint32_t* block_counters;    /* [retrieval_heads], zero before first use; kernels leave it zero */
+  uint32_t* block_counters;    /* [2 * retrieval_heads], zero before first use; kernels leave it zero */
   float* partial_max;          /* [query_heads][slot_tiles] */
   float* partial_sum;          /* [query_heads][slot_tiles] */
   float* partial_acc;          /* [query_heads][slot_tiles][128] */
@@ -211,6 +211,13 @@ int ckv_segmented_attention(const ckv_kv_cache* kv, const ckv_graph_state* state
                             const ckv_prefill_csr* csr, const ckv_delta_chunks* deltas,
                             const ckv_decode_config* config, ckv_decode_workspace* ws,
                             void* stream);
+
+/* Diagnostic, no counterpart in the reference: only the split-partials kernel
+ * of ckv_segmented_attention, for per-kernel timing and profiling. */
+int ckv_attention_partials(const ckv_kv_cache* kv, const ckv_graph_state* state,
+                           const ckv_prefill_csr* csr, const ckv_delta_chunks* deltas,
+                           const ckv_decode_config* config, ckv_decode_workspace* ws,
+                           void* stream);
 
 /* ckv_score_select followed by ckv_segmented_attention. */
 int ckv_decode_layer(const ckv_kv_cache* kv, const ckv_graph_state* state,
