@@ -2,6 +2,7 @@
 #include <type_traits>
 
 #include "ckv_device.h"
+#include "ckv_error.h"
 
 namespace ckv {
 
@@ -140,24 +141,41 @@ __device__ inline void merge_head(const DecodeArgs& a, int qh, int tiles, void* 
   }
   __syncthreads();
   const float M = m_s;
+  __shared__ float ls_s[MERGE_MAX_SPLITS];
   for (int t = tid; t < tiles; t += blockDim.x) {
     const float mt = pm[t];
-    scale_s[t] = (mt == NEG_INF) ? 0.0f : ckv_expf(mt - M);
+    const float sc = (mt == NEG_INF) ? 0.0f : ckv_expf(mt - M);
+    scale_s[t] = sc;
+    const float lt = ps[t];
+    ls_s[t] = sc != 0.0f ? lt * sc : 0.0f;
   }
   __syncthreads();
   if (tid == 0) {
     float denom = 0.0f;
-    for (int t = 0; t < tiles; ++t) {
-      if (scale_s[t] != 0.0f) denom = denom + ps[t] * scale_s[t];
-    }
+    for (int t = 0; t < tiles; ++t) denom = denom + ls_s[t];
     denom_s = denom;
   }
   __syncthreads();
+  const float* acc_base = a.ws.partial_acc + (int64_t)qh * tiles * D;
   for (int d = tid; d < D; d += blockDim.x) {
+    // Loads are unconditional (skipped splits contribute through a select, so
+    // stale values of empty splits are never multiplied) and pipelined 8 deep.
     float acc = 0.0f;
-    for (int t = 0; t < tiles; ++t) {
+    int t = 0;
+    for (; t + 8 <= tiles; t += 8) {
+      float v[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) v[k] = acc_base[(int64_t)(t + k) * D + d];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const float sc = scale_s[t + k];
+        acc = acc + (sc != 0.0f ? v[k] * sc : 0.0f);
+      }
+    }
+    for (; t < tiles; ++t) {
+      const float v = acc_base[(int64_t)t * D + d];
       const float sc = scale_s[t];
-      if (sc != 0.0f) acc = acc + a.ws.partial_acc[((int64_t)qh * tiles + t) * D + d] * sc;
+      acc = acc + (sc != 0.0f ? v * sc : 0.0f);
     }
     const float r = acc / denom_s;
     if constexpr (DT == CKV_BF16) {
@@ -174,16 +192,14 @@ __device__ inline void merge_head(const DecodeArgs& a, int qh, int tiles, void* 
   }
 }
 
-// Split merge of retrieval head rh's G query heads, then (graph owners) the
-// fused online update.  Any block size >= 64.
+// Fused online update of the graph owned by retrieval head rh (no-op for
+// non-owners and assignment NONE): exact top-8 merge over the splits'
+// candidates, assignment, running-mean centroid, delta append, overflow.
+// s_lse0 is the merged lse of the head's first query (read by thread 0 only).
+// Any block size >= 64.
 template <int CT, int DT>
-__device__ void merge_update(const DecodeArgs& a, const int rh, const int tiles) {
+__device__ void owner_update(const DecodeArgs& a, const int rh, const int tiles, const float s_lse0) {
   const int tid = threadIdx.x;
-  const int G = a.cfg.group_size;
-  __shared__ float s_lse0;
-  for (int g = 0; g < G; ++g) {
-    merge_head<DT>(a, rh * G + g, tiles, a.ws.output, a.ws.lse, g == 0 ? &s_lse0 : nullptr);
-  }
   const int graph = a.st.retrieval_to_graph[rh];
   if (a.cfg.assignment == CKV_ASSIGN_NONE || rh != graph) return;
   __syncthreads();
@@ -192,27 +208,50 @@ __device__ void merge_update(const DecodeArgs& a, const int rh, const int tiles)
   __shared__ uint64_t top[KAPPA];
   __shared__ int s_assigned, s_comm_ov, s_old_size, s_valid_pos, s_cur;
 
-  // Exact top-8 merge over every tile's candidates (wave 0).
+  __shared__ int s_comm[KAPPA];
+  __shared__ float s_oldw[KAPPA];
+  // Exact top-8 merge over every tile's candidates (wave 0): each lane keeps a
+  // sorted top-8 of its strided share (every candidate is read once), then 8
+  // rounds of a wave-wide max over the lanes' current heads.
   if (tid < 64) {
     const int n = tiles * KAPPA;
     const uint64_t* cand = a.ws.partial_topk + (int64_t)rh * n;
-    uint64_t taken_hi = 0ull;  // candidates are unique; exclude by value
-    for (int r = 0; r < KAPPA; ++r) {
-      uint64_t best = 0ull;
-      for (int i = tid; i < n; i += 64) {
-        const uint64_t v = cand[i];
-        if (v < taken_hi || taken_hi == 0ull) best = v > best ? v : best;
-      }
-      best = wave_max_u64(best);
-      if (tid == 0) top[r] = best;
-      taken_hi = best == 0ull ? 1ull : best;  // next round takes values strictly below
-      if (best == 0ull) {
-        for (int rr = r + 1; rr < KAPPA; ++rr) {
-          if (tid == 0) top[rr] = 0ull;
-        }
-        break;
+    uint64_t loc[KAPPA];
+#pragma unroll
+    for (int k = 0; k < KAPPA; ++k) loc[k] = 0ull;
+    for (int i = tid; i < n; i += 64) {
+      uint64_t v = cand[i];
+#pragma unroll
+      for (int k = 0; k < KAPPA; ++k) {
+        const uint64_t hi = v > loc[k] ? v : loc[k];
+        v = v > loc[k] ? loc[k] : v;
+        loc[k] = hi;
       }
     }
+    for (int r = 0; r < KAPPA; ++r) {
+      const uint64_t best = wave_max_u64(loc[0]);
+      if (tid == 0) top[r] = best;
+      if (best != 0ull && loc[0] == best) {
+#pragma unroll
+        for (int k = 0; k < KAPPA - 1; ++k) loc[k] = loc[k + 1];
+        loc[KAPPA - 1] = 0ull;
+      }
+    }
+  }
+  __syncthreads();
+  // Candidate communities and their weights, one lane per rank.
+  if (tid < KAPPA) {
+    const uint64_t v = top[tid];
+    const int pos = v == 0ull ? -1 : (int)(0xffffffffu - (uint32_t)(v & 0xffffffffu));
+    const int64_t tc_cap = a.st.token_capacity < a.kv.capacity ? a.st.token_capacity : a.kv.capacity;
+    int comm = -1;
+    float w = 0.0f;
+    if (pos >= 0 && pos < tc_cap) {
+      comm = a.st.token_communities[(int64_t)graph * a.st.token_capacity + pos];
+      if (comm >= 0 && comm < C) w = a.st.community_weight[(int64_t)graph * C + comm];
+    }
+    s_comm[tid] = comm;
+    s_oldw[tid] = w;
   }
   __syncthreads();
 
@@ -251,7 +290,7 @@ __device__ void merge_update(const DecodeArgs& a, const int rh, const int tiles)
         nd = nd + dw[r];
         ssum = ssum + p[r];
         sq = sq + p[r] * p[r];
-        comm[r] = valid ? a.st.token_communities[(int64_t)graph * a.st.token_capacity + ps[r]] : -1;
+        comm[r] = valid ? s_comm[r] : -1;
         cand[r] = valid && comm[r] >= 0 && comm[r] < active_c;
       }
       const float pair = (ssum * ssum - sq) * (0.5f * (1.0f - a.cfg.lam));
@@ -272,7 +311,7 @@ __device__ void merge_update(const DecodeArgs& a, const int rh, const int tiles)
       two_m = two_m > 1.0f ? two_m : 1.0f;
       float best = NEG_INF;
       for (int r = 0; r < KAPPA; ++r) {
-        oldw[r] = cand[r] ? a.st.community_weight[(int64_t)graph * C + comm[r]] : 0.0f;
+        oldw[r] = cand[r] ? s_oldw[r] : 0.0f;
         dq[r] = (cand[r] && cw[r] > 0.0f) ? (cw[r] - (nd * oldw[r]) / two_m) : NEG_INF;
         best = fmax_exact(best, dq[r]);
       }
@@ -379,6 +418,18 @@ __device__ void merge_update(const DecodeArgs& a, const int rh, const int tiles)
   }
 }
 
+// Split merge of retrieval head rh's G query heads one at a time, then the
+// owner update.  Any block size >= 64.
+template <int CT, int DT>
+__device__ void merge_update(const DecodeArgs& a, const int rh, const int tiles) {
+  __shared__ float s_lse0;
+  for (int g = 0; g < a.cfg.group_size; ++g) {
+    merge_head<DT>(a, rh * a.cfg.group_size + g, tiles, a.ws.output, a.ws.lse, g == 0 ? &s_lse0 : nullptr);
+  }
+  __syncthreads();
+  owner_update<CT, DT>(a, rh, tiles, s_lse0);
+}
+
 template <int CT, int DT>
 __global__ __launch_bounds__(REDUCE_THREADS) void reduce_update_kernel(DecodeArgs a) {
   merge_update<CT, DT>(a, blockIdx.x, a.ws.slot_capacity / TILE);
@@ -439,6 +490,7 @@ __global__ __launch_bounds__(REDUCE_THREADS) void dense_reduce_kernel(DecodeArgs
 // the V tile (16 KB, chunk-swizzled so the four lane groups hit disjoint banks).
 
 constexpr int CKV_DENSE_CHUNK_TILES = 8;  // 512 tokens per dense wave
+constexpr int V_HALF_ROWS = 32;          // rows of a V tile staged in LDS at a time
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
@@ -460,6 +512,27 @@ __device__ inline uint32_t pack_bf16x2(float lo, float hi) {
   return (uint32_t)ckv_f32_to_bf16_bits(lo) | ((uint32_t)ckv_f32_to_bf16_bits(hi) << 16);
 }
 
+// Unconditional 16-byte load through the global address space (one
+// global_load_dwordx4, no flat addressing).
+__device__ inline uint4 gload16(const uint16_t* p) {
+  typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+  typedef const __attribute__((address_space(1))) u32x4_t* global_u32x4_ptr;
+  const u32x4_t v = *(global_u32x4_ptr)(p);
+  return uint4{v[0], v[1], v[2], v[3]};
+}
+
+struct QOperand {
+  uint4 s[4];  // Q^T B-operand chunks for the four 32-dim steps
+};
+
+// Orders this wave's LDS accesses (writes before the barrier are visible to
+// every lane of the wave after it) without synchronising other waves.
+__device__ inline void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // Computes one tile: scores (scaled, -inf where pos_s < 0), per-query max and
 // sum, and accumulates P.V into o (rows g = 4*(lane/16)+i, dims 16*nb + lane%16).
 // Returns through the references; `corr` rescales o before accumulation.
@@ -470,38 +543,31 @@ struct TileResult {
 
 __device__ inline TileResult mfma_tile(const uint16_t* __restrict__ K, const uint16_t* __restrict__ V, int64_t kbase,
                                        int64_t tstride, const int* pos_s, uint16_t* v_s, float* cand_s,
-                                       const uint4* qop, float scale, float m_prev, f32x4_t* o) {
-  const int lane = threadIdx.x;
+                                       const QOperand qop, float scale, float m_prev, f32x4_t* o) {
+  const int lane = threadIdx.x & 63;  // lane within the wave (workgroups may hold several waves)
   const int L = lane >> 4;
   const int c16 = lane & 15;
-  const uint4 zero = {0u, 0u, 0u, 0u};
+  // Masked slots (position -1) read row 0 and are masked out of the softmax,
+  // so every load is unconditional and all 32 are in flight together.
   uint4 kreg[4][4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const int p = pos_s[tau(j, c16)];
+    const int p = max(pos_s[tau(j, c16)], 0);
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      kreg[j][s] = p >= 0 ? *reinterpret_cast<const uint4*>(K + kbase + (int64_t)p * tstride + 32 * s + 8 * L) : zero;
-    }
+    for (int s = 0; s < 4; ++s) kreg[j][s] = gload16(K + kbase + (int64_t)p * tstride + 32 * s + 8 * L);
   }
   uint4 vreg[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
-    const int p = pos_s[4 * i + L];
-    vreg[i] = p >= 0 ? *reinterpret_cast<const uint4*>(V + kbase + (int64_t)p * tstride + 8 * c16) : zero;
+    const int p = max(pos_s[4 * i + L], 0);
+    vreg[i] = gload16(V + kbase + (int64_t)p * tstride + 8 * c16);
   }
   f32x4_t sacc[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     sacc[j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int s = 0; s < 4; ++s) sacc[j] = mfma_bf16(kreg[j][s], qop[s], sacc[j]);
-  }
-  // V tile -> LDS (row 4i+L, chunk c16), swizzled.
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int row = 4 * i + L;
-    *reinterpret_cast<uint4*>(v_s + vidx(row, 8 * c16)) = vreg[i];
+    for (int s = 0; s < 4; ++s) sacc[j] = mfma_bf16(kreg[j][s], qop.s[s], sacc[j]);
   }
   float sc[4][4];
   float mloc = NEG_INF;
@@ -553,14 +619,21 @@ __device__ inline TileResult mfma_tile(const uint16_t* __restrict__ K, const uin
       for (int nb = 0; nb < 8; ++nb) o[nb][i] = o[nb][i] * c;
     }
   }
-  __syncthreads();  // V tile and candidates visible
+  // P.V in two 32-slot halves; each half of the V tile goes through the wave's
+  // 8 KB LDS buffer (row 4i+L of the tile -> buffer row 4(i mod 8)+L, swizzled).
 #pragma unroll
   for (int s = 0; s < 2; ++s) {
+    wave_sync();  // previous half fully read
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      *reinterpret_cast<uint4*>(v_s + vidx(4 * i + L, 8 * c16)) = vreg[8 * s + i];
+    }
+    wave_sync();  // this half (and the candidates) visible to every lane of the wave
     const uint4 aop = {pk[2 * s][0], pk[2 * s][1], pk[2 * s + 1][0], pk[2 * s + 1][1]};
 #pragma unroll
     for (int nb = 0; nb < 8; ++nb) {
       const int dim = 16 * nb + c16;
-      const int r0 = 32 * s + 8 * L;
+      const int r0 = 8 * L;
       uint32_t w[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
@@ -573,89 +646,224 @@ __device__ inline TileResult mfma_tile(const uint16_t* __restrict__ K, const uin
   return res;
 }
 
+constexpr int ATT_WAVES = 4;  // 64-slot tiles per attention workgroup
+
+// Split merge of all G query heads of retrieval head rh at once (any block
+// size); `scratch` holds 3 * G * splits floats.
+template <int DT>
+__device__ inline void merge_group(const DecodeArgs& a, const int rh, const int splits, float* scratch,
+                                   float* lse0_out) {
+  const int tid = threadIdx.x;
+  const int nt = blockDim.x;
+  const int G = a.cfg.group_size;
+  const int n = G * splits;
+  float* m_s = scratch;
+  float* l_s = scratch + n;
+  float* sc_s = scratch + 2 * n;
+  __shared__ float gm_s[CKV_MAX_GROUP], gden_s[CKV_MAX_GROUP];
+  const int64_t base = (int64_t)rh * G * splits;  // partial_max/sum rows of this head group
+  for (int i = tid; i < n; i += nt) {
+    m_s[i] = a.ws.partial_max[base + i];
+    l_s[i] = a.ws.partial_sum[base + i];
+  }
+  __syncthreads();
+  if (tid < G) {
+    float M = NEG_INF;
+    for (int t = 0; t < splits; ++t) M = fmax_exact(M, m_s[tid * splits + t]);
+    gm_s[tid] = M;
+  }
+  __syncthreads();
+  for (int i = tid; i < n; i += nt) {
+    const float mt = m_s[i];
+    sc_s[i] = mt == NEG_INF ? 0.0f : ckv_expf(mt - gm_s[i / splits]);
+  }
+  __syncthreads();
+  if (tid < G) {
+    float den = 0.0f;
+    for (int t = 0; t < splits; ++t) {
+      const float sc = sc_s[tid * splits + t];
+      den = den + (sc != 0.0f ? l_s[tid * splits + t] * sc : 0.0f);
+    }
+    gden_s[tid] = den;
+    const float lse = gm_s[tid] + ckv_logf(den);
+    a.ws.lse[(int64_t)rh * G + tid] = lse;
+    if (tid == 0 && lse0_out) *lse0_out = lse;
+  }
+  __syncthreads();
+  const float* acc_base = a.ws.partial_acc + base * D;
+  for (int i = tid; i < G * D; i += nt) {
+    const int g = i >> 7;
+    const int d = i & (D - 1);
+    const float* src = acc_base + (int64_t)g * splits * D + d;
+    const float* scg = sc_s + g * splits;
+    float acc = 0.0f;
+    int t = 0;
+    for (; t + 16 <= splits; t += 16) {
+      float v[16];
+#pragma unroll
+      for (int k = 0; k < 16; ++k) v[k] = src[(int64_t)(t + k) * D];
+#pragma unroll
+      for (int k = 0; k < 16; ++k) acc = acc + (scg[t + k] != 0.0f ? v[k] * scg[t + k] : 0.0f);
+    }
+    {
+      float v[16];
+#pragma unroll
+      for (int k = 0; k < 16; ++k) v[k] = t + k < splits ? src[(int64_t)(t + k) * D] : 0.0f;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        if (t + k < splits) acc = acc + (scg[t + k] != 0.0f ? v[k] * scg[t + k] : 0.0f);
+      }
+    }
+    const float r = acc / gden_s[g];
+    if constexpr (DT == CKV_BF16) {
+      reinterpret_cast<uint16_t*>(a.ws.output)[((int64_t)rh * G + g) * D + d] = ckv_f32_to_bf16_bits(r);
+    } else {
+      reinterpret_cast<float*>(a.ws.output)[((int64_t)rh * G + g) * D + d] = r;
+    }
+  }
+  __syncthreads();
+}
+
+// Sparse bf16 attention: a workgroup of ATT_WAVES waves covers ATT_WAVES
+// consecutive 64-slot tiles of one retrieval head; each wave runs mfma_tile on
+// its tile, the workgroup combines its waves in LDS into one split partial
+// (max, sum, unnormalised P.V per query, top-8 candidates).  With FUSED the
+// last workgroup of a head to finish merges the splits and runs the update.
 template <int CT, bool FUSED>
-__global__ __launch_bounds__(64) void attend_mfma_kernel(DecodeArgs a) {
-  const int tile = blockIdx.x;
+__global__ __launch_bounds__(64 * ATT_WAVES) void attend_mfma_kernel(DecodeArgs a) {
+  // Per-wave V half-tile buffers (8 KB each); reused for the waves' P.V rows
+  // and, in the last workgroup, as the split-merge scratch.
+  __shared__ __align__(16) unsigned char att_dyn[ATT_WAVES * V_HALF_ROWS * D * sizeof(uint16_t)];
+  const int wgi = blockIdx.x;
   const int rh = blockIdx.y;
-  const int lane = threadIdx.x;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int tid = threadIdx.x;
   const int L = lane >> 4;
   const int c16 = lane & 15;
-  const int tiles = gridDim.x;
+  const int splits = gridDim.x;
+  const int tiles = a.ws.slot_capacity / TILE;
   const int G = a.cfg.group_size;
   const int kvh = a.st.retrieval_to_kv[rh];
   const uint16_t* K = reinterpret_cast<const uint16_t*>(a.kv.key);
   const uint16_t* V = reinterpret_cast<const uint16_t*>(a.kv.value);
   const uint16_t* Q = reinterpret_cast<const uint16_t*>(a.kv.query);
+  uint16_t* v_s = reinterpret_cast<uint16_t*>(att_dyn) + wave * (V_HALF_ROWS * D);
+  float* o_s = reinterpret_cast<float*>(v_s);  // reused for this wave's P.V rows after the tile
 
-  __shared__ __align__(16) uint16_t v_s[TILE * D];
-  __shared__ int pos_s[TILE];
-  __shared__ float cand_s[TILE];
+  __shared__ int pos_s[ATT_WAVES][TILE];
+  __shared__ float cand_s[ATT_WAVES][TILE];
+  __shared__ float wm_s[ATT_WAVES][CKV_MAX_GROUP];
+  __shared__ float wl_s[ATT_WAVES][CKV_MAX_GROUP];
+  __shared__ uint64_t wtop_s[ATT_WAVES][KAPPA];
   __shared__ int last_block;
+  __shared__ float s_lse0;
 
+  const int tile = wgi * ATT_WAVES + wave;
   const int slot = tile * TILE + lane;
-  int pos = a.ws.slot_positions[(int64_t)rh * a.ws.slot_capacity + slot];
+  int pos = tile < tiles ? a.ws.slot_positions[(int64_t)rh * a.ws.slot_capacity + slot] : -1;
   const bool valid = pos >= 0 && pos < a.kv.capacity;
   if (!valid) pos = -1;
-  pos_s[lane] = pos;
+  pos_s[wave][lane] = pos;
   const bool any = __ballot(valid) != 0ull;
   const uint4 zero = {0u, 0u, 0u, 0u};
-  uint4 qop[4];
+  QOperand qop;
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
-    qop[s] = c16 < G ? *reinterpret_cast<const uint4*>(Q + ((int64_t)rh * G + c16) * D + 32 * s + 8 * L) : zero;
+    const uint4 v = gload16(Q + ((int64_t)rh * G + min(c16, G - 1)) * D + 32 * s + 8 * L);
+    qop.s[s] = c16 < G ? v : zero;
   }
-  __syncthreads();
+  wave_sync();
   const bool want_topk = a.cfg.assignment != CKV_ASSIGN_NONE;
   if (any) {
     f32x4_t o[8];
 #pragma unroll
     for (int nb = 0; nb < 8; ++nb) o[nb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    const TileResult r = mfma_tile(K, V, kvh * a.kv.head_stride, a.kv.token_stride, pos_s, v_s,
-                                   want_topk ? cand_s : nullptr, qop, a.cfg.softmax_scale, NEG_INF, o);
+    const TileResult r = mfma_tile(K, V, kvh * a.kv.head_stride, a.kv.token_stride, pos_s[wave], v_s,
+                                   want_topk ? cand_s[wave] : nullptr, qop, a.cfg.softmax_scale, NEG_INF, o);
+    wave_sync();
     if (L == 0 && c16 < G) {
-      const int qh = rh * G + c16;
-      a.ws.partial_max[(int64_t)qh * tiles + tile] = r.m;
-      a.ws.partial_sum[(int64_t)qh * tiles + tile] = r.l;
+      wm_s[wave][c16] = r.m;
+      wl_s[wave][c16] = r.l;
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int g = 4 * L + i;
       if (g < G) {
-        float* dst = a.ws.partial_acc + ((int64_t)(rh * G + g) * tiles + tile) * D + c16;
 #pragma unroll
-        for (int nb = 0; nb < 8; ++nb) dst[16 * nb] = o[nb][i];
+        for (int nb = 0; nb < 8; ++nb) o_s[g * D + 16 * nb + c16] = o[nb][i];
       }
     }
     if (want_topk) {
-      uint64_t cand = (pos >= 0 && slot >= a.cfg.num_sink) ? pack_candidate(cand_s[lane], pos) : 0ull;
+      uint64_t cand = (pos >= 0 && slot >= a.cfg.num_sink) ? pack_candidate(cand_s[wave][lane], pos) : 0ull;
       for (int k = 0; k < KAPPA; ++k) {
         const uint64_t best = wave_max_u64(cand);
-        if (lane == 0) a.ws.partial_topk[((int64_t)rh * tiles + tile) * KAPPA + k] = best;
+        if (lane == k) wtop_s[wave][k] = best;
         if (cand == best) cand = 0ull;
       }
     }
   } else {
     if (L == 0 && c16 < G) {
-      const int qh = rh * G + c16;
-      a.ws.partial_max[(int64_t)qh * tiles + tile] = NEG_INF;
-      a.ws.partial_sum[(int64_t)qh * tiles + tile] = 0.0f;
+      wm_s[wave][c16] = NEG_INF;
+      wl_s[wave][c16] = 0.0f;
     }
-    if (want_topk && lane < KAPPA) a.ws.partial_topk[((int64_t)rh * tiles + tile) * KAPPA + lane] = 0ull;
+    if (lane < KAPPA) wtop_s[wave][lane] = 0ull;
+  }
+  __syncthreads();
+  // Combine this workgroup's waves into one split partial.
+  for (int i = tid; i < G * D; i += 64 * ATT_WAVES) {
+    const int g = i >> 7;
+    const int d = i & (D - 1);
+    float M = NEG_INF;
+#pragma unroll
+    for (int w = 0; w < ATT_WAVES; ++w) M = fmax_exact(M, wm_s[w][g]);
+    float acc = 0.0f;
+#pragma unroll
+    for (int w = 0; w < ATT_WAVES; ++w) {
+      const float mw = wm_s[w][g];
+      if (mw != NEG_INF) {
+        const float* ow = reinterpret_cast<const float*>(reinterpret_cast<uint16_t*>(att_dyn) + w * (V_HALF_ROWS * D));
+        acc = acc + ow[g * D + d] * __expf(mw - M);
+      }
+    }
+    a.ws.partial_acc[(((int64_t)rh * G + g) * splits + wgi) * D + d] = acc;
+  }
+  if (tid < G) {
+    float M = NEG_INF;
+#pragma unroll
+    for (int w = 0; w < ATT_WAVES; ++w) M = fmax_exact(M, wm_s[w][tid]);
+    float l = 0.0f;
+#pragma unroll
+    for (int w = 0; w < ATT_WAVES; ++w) {
+      const float mw = wm_s[w][tid];
+      if (mw != NEG_INF) l = l + wl_s[w][tid] * __expf(mw - M);
+    }
+    a.ws.partial_max[((int64_t)rh * G + tid) * splits + wgi] = M;
+    a.ws.partial_sum[((int64_t)rh * G + tid) * splits + wgi] = l;
+  }
+  if (want_topk && wave == 0) {
+    uint64_t cand = lane < ATT_WAVES * KAPPA ? wtop_s[lane / KAPPA][lane % KAPPA] : 0ull;
+    for (int k = 0; k < KAPPA; ++k) {
+      const uint64_t best = wave_max_u64(cand);
+      if (lane == k) a.ws.partial_topk[((int64_t)rh * splits + wgi) * KAPPA + k] = best;
+      if (cand == best) cand = 0ull;
+    }
   }
   if (!FUSED) return;
-  // The last tile of this head to finish merges the splits and runs the update.
+  // The last workgroup of this head to finish merges the splits and runs the update.
   __threadfence();
   __syncthreads();
-  if (lane == 0) {
+  if (tid == 0) {
     uint32_t* counter = a.ws.block_counters + a.st.retrieval_heads + rh;
     const unsigned prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    last_block = (prev == (unsigned)tiles - 1u) ? 1 : 0;
+    last_block = (prev == (unsigned)splits - 1u) ? 1 : 0;
     if (last_block) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
   if (!last_block) return;
   __threadfence();
-  merge_update<CT, CKV_BF16>(a, rh, tiles);
+  merge_group<CKV_BF16>(a, rh, splits, reinterpret_cast<float*>(att_dyn), &s_lse0);
+  owner_update<CT, CKV_BF16>(a, rh, splits, s_lse0);
 }
 
 // Dense bf16 decode baseline: each wave streams `chunk_tiles` consecutive
@@ -671,14 +879,14 @@ __global__ __launch_bounds__(64) void dense_mfma_kernel(DecodeArgs a, int seq_le
   const uint16_t* K = reinterpret_cast<const uint16_t*>(a.kv.key);
   const uint16_t* V = reinterpret_cast<const uint16_t*>(a.kv.value);
   const uint16_t* Q = reinterpret_cast<const uint16_t*>(a.kv.query);
-  __shared__ __align__(16) uint16_t v_s[TILE * D];
+  __shared__ __align__(16) uint16_t v_s[V_HALF_ROWS * D];
   __shared__ int pos_s[TILE];
   const uint4 zero = {0u, 0u, 0u, 0u};
-  uint4 qop[4];
+  QOperand qop;
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
-    qop[s] = c16 < group ? *reinterpret_cast<const uint4*>(Q + ((int64_t)kvh * group + c16) * D + 32 * s + 8 * L)
-                         : zero;
+    const uint4 v = gload16(Q + ((int64_t)kvh * group + min(c16, group - 1)) * D + 32 * s + 8 * L);
+    qop.s[s] = c16 < group ? v : zero;
   }
   f32x4_t o[8];
 #pragma unroll
@@ -722,16 +930,18 @@ int launch_attention(const DecodeArgs& a, hipStream_t s, bool partials_only) {
   const bool e4m3 = a.st.centroid_dtype == CKV_E4M3;
   int r;
   if (a.kv.dtype == CKV_BF16) {
-    if (partials_only) {
-      hipLaunchKernelGGL((attend_mfma_kernel<CKV_E4M3, false>), grid, dim3(64), 0, s, a);
+    const int splits = (tiles + ATT_WAVES - 1) / ATT_WAVES;
+    const dim3 wg_grid(splits, a.st.retrieval_heads);
+    const size_t lds = (size_t)ATT_WAVES * V_HALF_ROWS * D * sizeof(uint16_t);
+    if ((size_t)3 * a.cfg.group_size * splits * sizeof(float) > lds) {
+      return ckv_internal::set_error(CKV_E_LIMIT, "too many attention splits for the merge scratch");
+    }
+    auto run = [&](auto kernel) {
+      hipLaunchKernelGGL(kernel, wg_grid, dim3(64 * ATT_WAVES), 0, s, a);
       return launch_check("attend_mfma");
-    }
-    if (e4m3) {
-      hipLaunchKernelGGL((attend_mfma_kernel<CKV_E4M3, true>), grid, dim3(64), 0, s, a);
-    } else {
-      hipLaunchKernelGGL((attend_mfma_kernel<CKV_F32, true>), grid, dim3(64), 0, s, a);
-    }
-    r = launch_check("attend_mfma");
+    };
+    if (partials_only) return run(attend_mfma_kernel<CKV_E4M3, false>);
+    r = e4m3 ? run(attend_mfma_kernel<CKV_E4M3, true>) : run(attend_mfma_kernel<CKV_F32, true>);
   } else {
     hipLaunchKernelGGL((attend_generic_kernel<CKV_F32, false>), grid, dim3(64), 0, s, a, 0, 0);
     r = launch_check("attend");

@@ -16,8 +16,13 @@
 #include <type_traits>
 
 #include "ckv_device.h"
+#include "ckv_error.h"
 
 namespace ckv {
+
+namespace {
+int ckv_internal_limit(const char* message) { return ckv_internal::set_error(CKV_E_LIMIT, message); }
+}  // namespace
 
 // ---------------------------------------------------------------------------
 // Kernel 1: centroid scoring + (last block per head) exact selection
@@ -285,54 +290,87 @@ __global__ __launch_bounds__(SELECT_THREADS) void score_select_kernel(DecodeArgs
   const int slot_cap = a.ws.slot_capacity;
   int32_t* slots = a.ws.slot_positions + (int64_t)rh * slot_cap;
   const int64_t tbl = (int64_t)graph * C;
-  for (int s = tid; s < slot_cap; s += SELECT_THREADS) {
-    int pos = -1;
-    if (s < ns) {
-      pos = a.cfg.sink_positions[s];
-    } else if (s < ns + sel_count) {
-      const int j = s - ns;
-      if (j < sel_count) {
+  // Per-descriptor membership: decode-delta count and prefill CSR start, one
+  // parallel round of loads.
+  int* desc_dc = reinterpret_cast<int*>(key16 + ((C + 7) & ~7));
+  int* desc_lo = desc_dc + dcap;
+  for (int d = tid; d < n_desc; d += SELECT_THREADS) {
+    const int c = desc_comm[d];
+    desc_dc[d] = a.dl.community_sizes[tbl + c];
+    desc_lo[d] = a.csr.member_offsets[(int64_t)graph * (C + 1) + c];
+  }
+  __syncthreads();
+  // Slots in batches of 8 per thread so that the member-position gathers of a
+  // batch are in flight together; decode-delta members (newest first) walk
+  // their chunk chain afterwards.
+  constexpr int BATCH = 8;
+  const int32_t* members = a.csr.member_positions + (int64_t)graph * a.csr.member_stride;
+  for (int s0 = 0; s0 < slot_cap; s0 += SELECT_THREADS * BATCH) {
+    int spos[BATCH];
+    int64_t at[BATCH];
+    int dm[BATCH];   // member index into the delta chain, or -1
+    int dcm[BATCH];  // community of a delta member
+#pragma unroll
+    for (int k = 0; k < BATCH; ++k) {
+      const int s = s0 + k * SELECT_THREADS + tid;
+      spos[k] = -1;
+      at[k] = -1;
+      dm[k] = -1;
+      dcm[k] = 0;
+      if (s >= slot_cap) continue;
+      if (s < ns) {
+        spos[k] = a.cfg.sink_positions[s];
+      } else if (s < ns + sel_count) {
+        const int j = s - ns;
         int lo = 0, hi = n_desc;
         while (lo < hi) {
           const int mid = (lo + hi) >> 1;
           if (desc_end[mid] <= j) lo = mid + 1; else hi = mid;
         }
-        const int d = lo;
-        const int prev = d > 0 ? desc_end[d - 1] : 0;
+        const int prev = lo > 0 ? desc_end[lo - 1] : 0;
         const int m = j - prev;
-        const int c = desc_comm[d];
-        const int dc = a.dl.community_sizes[tbl + c];
+        const int dc = desc_dc[lo];
         if (m < dc) {
-          int rem = m;
-          int ch = a.dl.community_tail[tbl + c];
-          const int64_t cb = (int64_t)graph * a.dl.chunks_per_graph;
-          for (int guard = 0; guard < 64 && ch >= 0 && ch < a.dl.chunks_per_graph; ++guard) {
-            const int cs = a.dl.chunk_size[cb + ch];
-            if (rem < cs) {
-              const int at = a.dl.chunk_start[cb + ch] + cs - 1 - rem;
-              if (at >= 0 && at < a.dl.position_capacity) {
-                pos = a.dl.positions[(int64_t)graph * a.dl.position_capacity + at];
-              }
-              break;
-            }
-            rem -= cs;
-            ch = a.dl.chunk_previous[cb + ch];
-          }
+          dm[k] = m;
+          dcm[k] = desc_comm[lo];
         } else {
-          const int64_t ob = (int64_t)graph * (C + 1) + c;
-          const int at = a.csr.member_offsets[ob] + (m - dc);
-          if (at < a.csr.member_offsets[ob + 1] && at < a.csr.member_stride) {
-            pos = a.csr.member_positions[(int64_t)graph * a.csr.member_stride + at];
-          }
+          const int64_t idx = (int64_t)desc_lo[lo] + (m - dc);
+          if (idx < a.csr.member_stride) at[k] = idx;
         }
-        if (j == sel_count - 1) s_last_sel_pos = pos;
+      } else if (inc && s == ns + sel_count + W) {
+        spos[k] = cur;
       }
-    } else if (s < ns + sel_count + W) {
-      continue;  // window slots are resolved after the barrier below
-    } else if (inc && s == ns + sel_count + W) {
-      pos = cur;
     }
-    slots[s] = pos;
+#pragma unroll
+    for (int k = 0; k < BATCH; ++k) {
+      const int v = members[at[k] >= 0 ? at[k] : 0];
+      if (at[k] >= 0) spos[k] = v;
+    }
+#pragma unroll
+    for (int k = 0; k < BATCH; ++k) {
+      if (dm[k] < 0) continue;
+      int rem = dm[k];
+      int ch = a.dl.community_tail[tbl + dcm[k]];
+      const int64_t cb = (int64_t)graph * a.dl.chunks_per_graph;
+      for (int guard = 0; guard < 64 && ch >= 0 && ch < a.dl.chunks_per_graph; ++guard) {
+        const int cs = a.dl.chunk_size[cb + ch];
+        if (rem < cs) {
+          const int p = a.dl.chunk_start[cb + ch] + cs - 1 - rem;
+          if (p >= 0 && p < a.dl.position_capacity) spos[k] = a.dl.positions[(int64_t)graph * a.dl.position_capacity + p];
+          break;
+        }
+        rem -= cs;
+        ch = a.dl.chunk_previous[cb + ch];
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < BATCH; ++k) {
+      const int s = s0 + k * SELECT_THREADS + tid;
+      if (s >= slot_cap) continue;
+      if (s >= ns + sel_count && s < ns + sel_count + W) continue;  // window: resolved below
+      slots[s] = spos[k];
+      if (s == ns + sel_count - 1 && sel_count > 0) s_last_sel_pos = spos[k];
+    }
   }
   __syncthreads();
   if (W > 0) {
@@ -377,14 +415,23 @@ __global__ __launch_bounds__(SELECT_THREADS) void score_select_kernel(DecodeArgs
 }
 
 int launch_score_select(const DecodeArgs& a, hipStream_t s) {
-  const size_t lds = (size_t)a.ws.descriptor_capacity * 8 + (((size_t)a.st.community_capacity * 2 + 15) & ~(size_t)15);
+  // Dynamic LDS: descriptor communities/ends/delta counts/CSR starts + fp16 keys.
+  const size_t lds = (size_t)a.ws.descriptor_capacity * 16 + (((size_t)a.st.community_capacity + 7) & ~(size_t)7) * 2;
   const dim3 grid(a.ws.score_blocks, a.st.retrieval_heads);
   const int ct = a.st.centroid_dtype, dt = a.kv.dtype;
-  if (ct == CKV_E4M3 && dt == CKV_BF16) hipLaunchKernelGGL((score_select_kernel<CKV_E4M3, CKV_BF16>), grid, dim3(SELECT_THREADS), lds, s, a);
-  else if (ct == CKV_E4M3) hipLaunchKernelGGL((score_select_kernel<CKV_E4M3, CKV_F32>), grid, dim3(SELECT_THREADS), lds, s, a);
-  else if (dt == CKV_BF16) hipLaunchKernelGGL((score_select_kernel<CKV_F32, CKV_BF16>), grid, dim3(SELECT_THREADS), lds, s, a);
-  else hipLaunchKernelGGL((score_select_kernel<CKV_F32, CKV_F32>), grid, dim3(SELECT_THREADS), lds, s, a);
-  return launch_check("score_select");
+  auto launch = [&](auto kernel) {
+    if (lds > 48 * 1024) {
+      const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+      if (e != hipSuccess) return ckv_internal_limit("selection LDS exceeds the device limit");
+    }
+    hipLaunchKernelGGL(kernel, grid, dim3(SELECT_THREADS), lds, s, a);
+    return launch_check("score_select");
+  };
+  if (ct == CKV_E4M3 && dt == CKV_BF16) return launch(score_select_kernel<CKV_E4M3, CKV_BF16>);
+  if (ct == CKV_E4M3) return launch(score_select_kernel<CKV_E4M3, CKV_F32>);
+  if (dt == CKV_BF16) return launch(score_select_kernel<CKV_F32, CKV_BF16>);
+  return launch(score_select_kernel<CKV_F32, CKV_F32>);
 }
 
 }  // namespace ckv
