@@ -18,7 +18,7 @@ PACKAGE_DIR = os.path.dirname(os.path.abspath(__file__))
 REPO_DIR = os.path.dirname(PACKAGE_DIR)
 LIB_PATH = os.path.join(PACKAGE_DIR, "libckv_amd.so")
 SOURCES = [os.path.join(PACKAGE_DIR, "csrc", name)
-           for name in ("ckv_decode.hip", "ckv_select.hip", "ckv_attend.hip", "ckv_prefill.hip")]
+           for name in ("ckv_decode.hip", "ckv_select.hip", "ckv_attend.hip", "ckv_prefill.hip", "ckv_diag.hip")]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 HIP_FLAGS = [
     "--offload-arch=gfx950",
@@ -42,6 +42,8 @@ SCORE_BLOCK = 64
 MAX_GROUP = 16
 MAX_COMMUNITIES = 8192
 MAX_DESCRIPTORS = 4096
+MAX_SINKS = 256
+MAX_WINDOW = 1024
 
 EXPORTED_SYMBOLS = (
     "ckv_score_select",
@@ -51,6 +53,7 @@ EXPORTED_SYMBOLS = (
     "ckv_dense_decode",
     "ckv_prefill_attention_topk",
     "ckv_host_numerics",
+    "ckv_device_numerics",
     "ckv_abi_version",
     "ckv_last_error",
 )
@@ -148,6 +151,8 @@ def lib() -> ctypes.CDLL:
         handle.ckv_prefill_attention_topk.restype = ctypes.c_int
     handle.ckv_host_numerics.argtypes = [ctypes.c_int, _p, _p, _i64]
     handle.ckv_host_numerics.restype = ctypes.c_int
+    handle.ckv_device_numerics.argtypes = [ctypes.c_int, _p, _p, _i64, _p]
+    handle.ckv_device_numerics.restype = ctypes.c_int
     handle.ckv_last_error.restype = ctypes.c_char_p
     handle.ckv_abi_version.restype = ctypes.c_int
     if handle.ckv_abi_version() != ABI_VERSION:

@@ -60,6 +60,8 @@ class CentroidSelectionWorkspace:
             raise ValueError("token budget must be a positive multiple of 64")
         if num_sink < 0 or num_sink + 1 >= token_budget:
             raise ValueError("num_sink leaves no selected-token capacity")
+        if num_sink > nat.MAX_SINKS or local_window > nat.MAX_WINDOW:
+            raise ValueError(f"num_sink <= {nat.MAX_SINKS} and local_window <= {nat.MAX_WINDOW} are supported")
         if score_headroom < 0:
             raise ValueError("score_headroom must be nonnegative")
         if selection not in SELECTION_MODES:

@@ -6,6 +6,12 @@
 
 namespace ckv {
 
+namespace {
+#ifdef CKV_PHASE_TIMING
+__device__ unsigned long long phase_stamp[32];
+#endif
+}  // namespace
+
 // ---------------------------------------------------------------------------
 // Kernel 2: attention partials (portable wave64 VALU version)
 // ---------------------------------------------------------------------------
@@ -195,8 +201,12 @@ __device__ inline void merge_head(const DecodeArgs& a, int qh, int tiles, void* 
 // Fused online update of the graph owned by retrieval head rh (no-op for
 // non-owners and assignment NONE): exact top-8 merge over the splits'
 // candidates, assignment, running-mean centroid, delta append, overflow.
-// s_lse0 is the merged lse of the head's first query (read by thread 0 only).
-// Any block size >= 64.
+// s_lse0 is the merged lse of the head's first query.  Any block size >= 64.
+//
+// Dependent memory rounds: (1) candidates + cursor/count/total, (2) candidate
+// communities + current key row, (3) per-candidate weight/size/delta tail and
+// centroid rows (slot KAPPA holds the community a new token would open, or the
+// nearest centroid), (4) the assigned community's tail-chunk state.
 template <int CT, int DT>
 __device__ void owner_update(const DecodeArgs& a, const int rh, const int tiles, const float s_lse0) {
   const int tid = threadIdx.x;
@@ -204,16 +214,28 @@ __device__ void owner_update(const DecodeArgs& a, const int rh, const int tiles,
   if (a.cfg.assignment == CKV_ASSIGN_NONE || rh != graph) return;
   __syncthreads();
 
+  constexpr int NS = KAPPA + 1;  // candidate slots
   const int C = a.st.community_capacity;
+  const int64_t tc_cap = a.st.token_capacity < a.kv.capacity ? a.st.token_capacity : a.kv.capacity;
+  const bool delta_q = a.cfg.assignment == CKV_ASSIGN_DELTA_Q;
+  const int kvh = a.st.retrieval_to_kv[rh];
   __shared__ uint64_t top[KAPPA];
-  __shared__ int s_assigned, s_comm_ov, s_old_size, s_valid_pos, s_cur;
+  __shared__ int s_cur, s_active, s_nearest;
+  __shared__ float s_total;
+  __shared__ int s_pos[NS], s_comm[NS], s_size[NS], s_dsize[NS], s_tail[NS];
+  __shared__ float s_w[NS], s_sc[KAPPA], s_p[KAPPA], s_dw[KAPPA];
+  __shared__ float s_key[D];
+  __shared__ float s_cent[NS][D];
+  __shared__ int s_assigned, s_slot, s_comm_ov;
 
-  __shared__ int s_comm[KAPPA];
-  __shared__ float s_oldw[KAPPA];
-  // Exact top-8 merge over every tile's candidates (wave 0): each lane keeps a
-  // sorted top-8 of its strided share (every candidate is read once), then 8
-  // rounds of a wave-wide max over the lanes' current heads.
-  if (tid < 64) {
+  // ---- round 1: exact top-8 merge (wave 0); cursor state (wave 1) ----------
+  if (tid < 64 && tiles * KAPPA <= 64) {
+    const int n = tiles * KAPPA;
+    const uint64_t v = wave_sort_desc_u64(tid < n ? a.ws.partial_topk[(int64_t)rh * n + tid] : 0ull);
+    if (tid < KAPPA) top[tid] = v;
+  } else if (tid < 64) {
+    // Each lane keeps a sorted top-8 of its strided share, then 8 rounds of a
+    // wave-wide max over the lanes' heads.
     const int n = tiles * KAPPA;
     const uint64_t* cand = a.ws.partial_topk + (int64_t)rh * n;
     uint64_t loc[KAPPA];
@@ -238,153 +260,169 @@ __device__ void owner_update(const DecodeArgs& a, const int rh, const int tiles,
       }
     }
   }
+  if (tid == 64) {
+    s_cur = a.st.current_position[graph];
+    s_active = a.st.community_counts[rh];
+    s_total = a.st.total_weight[graph];
+    s_nearest = delta_q ? -1 : a.ws.nearest[rh];
+  }
   __syncthreads();
-  // Candidate communities and their weights, one lane per rank.
-  if (tid < KAPPA) {
-    const uint64_t v = top[tid];
-    const int pos = v == 0ull ? -1 : (int)(0xffffffffu - (uint32_t)(v & 0xffffffffu));
-    const int64_t tc_cap = a.st.token_capacity < a.kv.capacity ? a.st.token_capacity : a.kv.capacity;
-    int comm = -1;
-    float w = 0.0f;
-    if (pos >= 0 && pos < tc_cap) {
-      comm = a.st.token_communities[(int64_t)graph * a.st.token_capacity + pos];
-      if (comm >= 0 && comm < C) w = a.st.community_weight[(int64_t)graph * C + comm];
+  const int cur = s_cur;
+  const int active = s_active;
+  const bool valid_pos = cur >= 0 && cur < tc_cap;
+
+  // ---- round 2: candidate communities; the current key row ----------------
+  if (tid < NS) {
+    int pos = -1, comm = -1;
+    if (tid < KAPPA) {
+      const uint64_t v = top[tid];
+      float sc = NEG_INF;
+      if (v != 0ull) {
+        sc = unordered_f32((uint32_t)(v >> 32));
+        pos = (int)(0xffffffffu - (uint32_t)(v & 0xffffffffu));
+      }
+      s_sc[tid] = sc;
+      a.ws.topk_scores[(int64_t)rh * KAPPA + tid] = sc;
+      a.ws.topk_positions[(int64_t)rh * KAPPA + tid] = pos;
+      if (delta_q && pos >= 0 && pos < tc_cap) comm = a.st.token_communities[(int64_t)graph * a.st.token_capacity + pos];
+    } else {
+      comm = (!delta_q && s_nearest >= 0) ? s_nearest : active;  // community a new token would open
     }
+    s_pos[tid] = pos;
     s_comm[tid] = comm;
-    s_oldw[tid] = w;
+  }
+  for (int d = tid; d < D; d += blockDim.x) {
+    s_key[d] = valid_pos ? load_elem<DT>(a.kv.key, kvh * a.kv.head_stride + (int64_t)cur * a.kv.token_stride + d) : 0.0f;
   }
   __syncthreads();
 
-  if (tid == 0) {
-    float sc[KAPPA];
-    int ps[KAPPA];
-    for (int r = 0; r < KAPPA; ++r) {
-      const uint64_t v = top[r];
-      if (v == 0ull) {
-        sc[r] = NEG_INF;
-        ps[r] = -1;
-      } else {
-        sc[r] = unordered_f32((uint32_t)(v >> 32));
-        ps[r] = (int)(0xffffffffu - (uint32_t)(v & 0xffffffffu));
-      }
-      a.ws.topk_scores[(int64_t)rh * KAPPA + r] = sc[r];
-      a.ws.topk_positions[(int64_t)rh * KAPPA + r] = ps[r];
-    }
-    const int cur = a.st.current_position[graph];
-    const int64_t tc_cap = a.st.token_capacity < a.kv.capacity ? a.st.token_capacity : a.kv.capacity;
-    const int active = a.st.community_counts[rh];
-    const int active_c = active < C ? active : C;
-    int assigned;
-    bool comm_ov;
-    if (a.cfg.assignment == CKV_ASSIGN_DELTA_Q) {
-      const float lse0 = s_lse0;
-      float p[KAPPA], dw[KAPPA], cw[KAPPA], oldw[KAPPA], dq[KAPPA];
-      int comm[KAPPA];
-      bool cand[KAPPA], leader[KAPPA];
-      const float half_lam = a.cfg.lam * 0.5f;
-      float nd = 0.0f, ssum = 0.0f, sq = 0.0f;
-      for (int r = 0; r < KAPPA; ++r) {
-        const bool valid = ps[r] >= 0 && ps[r] < tc_cap;
-        p[r] = valid ? ckv_expf(sc[r] - lse0) : 0.0f;
-        dw[r] = p[r] * half_lam;
-        nd = nd + dw[r];
-        ssum = ssum + p[r];
-        sq = sq + p[r] * p[r];
-        comm[r] = valid ? s_comm[r] : -1;
-        cand[r] = valid && comm[r] >= 0 && comm[r] < active_c;
-      }
-      const float pair = (ssum * ssum - sq) * (0.5f * (1.0f - a.cfg.lam));
-      for (int r = 0; r < KAPPA; ++r) {
-        float acc = 0.0f;
-        int first = KAPPA;
-        for (int j = 0; j < KAPPA; ++j) {
-          if (cand[j] && comm[j] == comm[r]) {
-            acc = acc + dw[j];
-            first = j < first ? j : first;
-          }
-        }
-        cw[r] = acc;
-        leader[r] = cand[r] && first == r;
-      }
-      const float old_total = a.st.total_weight[graph];
-      float two_m = 2.0f * old_total;
-      two_m = two_m > 1.0f ? two_m : 1.0f;
-      float best = NEG_INF;
-      for (int r = 0; r < KAPPA; ++r) {
-        oldw[r] = cand[r] ? s_oldw[r] : 0.0f;
-        dq[r] = (cand[r] && cw[r] > 0.0f) ? (cw[r] - (nd * oldw[r]) / two_m) : NEG_INF;
-        best = fmax_exact(best, dq[r]);
-      }
-      int best_comm = 0x7fffffff;
-      for (int r = 0; r < KAPPA; ++r) {
-        if (cand[r] && dq[r] == best && comm[r] < best_comm) best_comm = comm[r];
-      }
-      const bool join = best > 0.0f;
-      assigned = join ? best_comm : active;
-      comm_ov = assigned >= C;
-      if (!comm_ov) {
-        for (int r = 0; r < KAPPA; ++r) {
-          if (leader[r]) {
-            const float inc = cw[r] + ((join && comm[r] == assigned) ? nd : 0.0f);
-            a.st.community_weight[(int64_t)graph * C + comm[r]] = oldw[r] + inc;
-          }
-        }
-        if (!join) a.st.community_weight[(int64_t)graph * C + assigned] = nd;
-        a.st.community_counts[rh] = active + (join ? 0 : 1);
-        a.st.total_weight[graph] = (old_total + nd) + pair;
-      }
-    } else {
-      const int nearest = a.ws.nearest[rh];
-      assigned = nearest >= 0 ? nearest : active;
-      comm_ov = assigned >= C;
-      if (nearest < 0 && !comm_ov) a.st.community_counts[rh] = active + 1;
-    }
-    a.ws.assigned[graph] = comm_ov ? -1 : assigned;
-    const bool valid_pos = cur >= 0 && cur < tc_cap;
-    int old_size = 0;
-    if (!comm_ov) {
-      old_size = a.st.community_sizes[(int64_t)rh * C + assigned];
-      a.st.community_sizes[(int64_t)rh * C + assigned] = old_size + 1;
-      if (valid_pos) a.st.token_communities[(int64_t)graph * a.st.token_capacity + cur] = assigned;
-    }
-    s_assigned = assigned;
-    s_comm_ov = comm_ov ? 1 : 0;
-    s_old_size = old_size;
-    s_valid_pos = valid_pos ? 1 : 0;
-    s_cur = cur;
+  // ---- round 3: per-candidate state and centroid rows ----------------------
+  if (tid < NS) {
+    const int comm = s_comm[tid];
+    const bool ok = comm >= 0 && comm < C;
+    s_w[tid] = (ok && delta_q) ? a.st.community_weight[(int64_t)graph * C + comm] : 0.0f;
+    s_size[tid] = ok ? a.st.community_sizes[(int64_t)rh * C + comm] : 0;
+    s_dsize[tid] = ok ? a.dl.community_sizes[(int64_t)graph * C + comm] : 0;
+    s_tail[tid] = ok ? a.dl.community_tail[(int64_t)graph * C + comm] : -1;
+  }
+  for (int i = tid; i < NS * D; i += blockDim.x) {
+    const int k = i / D, d = i % D;
+    const int comm = s_comm[k];
+    s_cent[k][d] = (comm >= 0 && comm < C) ? load_centroid1<CT>(a.st.centroids, ((int64_t)rh * C + comm) * D + d) : 0.0f;
   }
   __syncthreads();
-  const int kvh = a.st.retrieval_to_kv[rh];
-  for (int d = tid; d < D && !s_comm_ov && s_valid_pos; d += blockDim.x) {
-    const int asg = s_assigned;
-    const int old_size = s_old_size;
-    const int64_t ci = ((int64_t)rh * C + asg) * D + d;
-    const float key = load_elem<DT>(a.kv.key, kvh * a.kv.head_stride + (int64_t)s_cur * a.kv.token_stride + d);
-    float upd;
-    if (old_size > 0) {
-      const float old = load_centroid1<CT>(a.st.centroids, ci);
-      upd = (old * (float)old_size + key) / (float)(old_size + 1);
+
+  // ---- assignment (lanes 0..7 of wave 0) ------------------------------------
+  if (tid < 64) {
+    const int r = tid & 7;
+    const int active_c = active < C ? active : C;
+    const bool valid = s_pos[r] >= 0 && s_pos[r] < tc_cap;
+    const int comm = s_comm[r];
+    const bool cand = valid && comm >= 0 && comm < active_c;
+    int assigned, slot;
+    bool comm_ov;
+    if (delta_q) {
+      const float half_lam = a.cfg.lam * 0.5f;
+      const float p = valid ? ckv_expf(s_sc[r] - s_lse0) : 0.0f;
+      const float dw = p * half_lam;
+      if (tid < KAPPA) {
+        s_p[r] = p;
+        s_dw[r] = dw;
+      }
+      wave_sync();
+      // Sequential sums in rank order (reference op order).
+      float nd = 0.0f, ssum = 0.0f, sq = 0.0f, cw = 0.0f;
+      int first = KAPPA;
+#pragma unroll
+      for (int j = 0; j < KAPPA; ++j) {
+        const float pj = s_p[j], dwj = s_dw[j];
+        nd = nd + dwj;
+        ssum = ssum + pj;
+        sq = sq + pj * pj;
+        const int cj = s_comm[j];
+        const bool candj = s_pos[j] >= 0 && s_pos[j] < tc_cap && cj >= 0 && cj < active_c;
+        if (candj && cj == comm) {
+          cw = cw + dwj;
+          first = j < first ? j : first;
+        }
+      }
+      const bool leader = cand && first == r;
+      const float pair = (ssum * ssum - sq) * (0.5f * (1.0f - a.cfg.lam));
+      const float old_total = s_total;
+      float two_m = 2.0f * old_total;
+      two_m = two_m > 1.0f ? two_m : 1.0f;
+      const float oldw = cand ? s_w[r] : 0.0f;
+      const float dq = (cand && cw > 0.0f) ? (cw - (nd * oldw) / two_m) : NEG_INF;
+      float best = dq;  // max over the 8 lanes of this half-row
+      best = fmax_exact(best, ckv_u2f(dpp_u32<0xB1>(ckv_f2u(best))));
+      best = fmax_exact(best, ckv_u2f(dpp_u32<0x4E>(ckv_f2u(best))));
+      best = fmax_exact(best, ckv_u2f(dpp_u32<0x141>(ckv_f2u(best))));
+      int bc = (cand && dq == best) ? comm : 0x7fffffff;
+      bc = min(bc, (int)dpp_u32<0xB1>((uint32_t)bc));
+      bc = min(bc, (int)dpp_u32<0x4E>((uint32_t)bc));
+      bc = min(bc, (int)dpp_u32<0x141>((uint32_t)bc));
+      const bool join = best > 0.0f;
+      assigned = join ? bc : active;
+      comm_ov = assigned >= C;
+      // candidate slot that holds the assigned community's prefetched state
+      const uint64_t hit = __ballot(tid < KAPPA && comm == assigned);
+      slot = join ? (__ffsll((unsigned long long)hit) - 1) : KAPPA;
+      if (!comm_ov && tid < KAPPA) {
+        if (leader) {
+          const float inc = cw + ((join && comm == assigned) ? nd : 0.0f);
+          a.st.community_weight[(int64_t)graph * C + comm] = oldw + inc;
+        }
+        if (tid == 0) {
+          if (!join) a.st.community_weight[(int64_t)graph * C + assigned] = nd;
+          a.st.community_counts[rh] = active + (join ? 0 : 1);
+          a.st.total_weight[graph] = (old_total + nd) + pair;
+        }
+      }
     } else {
-      upd = key;
+      const int nearest = s_nearest;
+      assigned = nearest >= 0 ? nearest : active;
+      comm_ov = assigned >= C;
+      slot = KAPPA;
+      if (tid == 0 && nearest < 0 && !comm_ov) a.st.community_counts[rh] = active + 1;
     }
-    store_centroid1<CT>(a.st.centroids, ci, upd);
+    if (tid == 0) {
+      a.ws.assigned[graph] = comm_ov ? -1 : assigned;
+      if (!comm_ov) {
+        a.st.community_sizes[(int64_t)rh * C + assigned] = s_size[slot] + 1;
+        if (valid_pos) a.st.token_communities[(int64_t)graph * a.st.token_capacity + cur] = assigned;
+      }
+      s_assigned = assigned;
+      s_slot = slot;
+      s_comm_ov = comm_ov ? 1 : 0;
+    }
   }
+  __syncthreads();
+  const int slot = s_slot;
+  const int asg = s_assigned;
+  const bool comm_ov = s_comm_ov != 0;
+  // Running-mean centroid (FP8 satfinite or f32).
+  if (!comm_ov && valid_pos) {
+    const int old_size = s_size[slot];
+    for (int d = tid; d < D; d += blockDim.x) {
+      const float key = s_key[d];
+      const float upd = old_size > 0 ? (s_cent[slot][d] * (float)old_size + key) / (float)(old_size + 1) : key;
+      store_centroid1<CT>(a.st.centroids, ((int64_t)rh * C + asg) * D + d, upd);
+    }
+  }
+  // ---- round 4: decode-delta append ----------------------------------------
   if (tid == 0) {
-    const int asg = s_assigned;
-    const bool comm_ov = s_comm_ov != 0;
-    const bool valid_pos = s_valid_pos != 0;
-    const int cur = s_cur;
     bool chunk_ov = false, pos_ov = false;
     if (!comm_ov) {
       const int64_t tb = (int64_t)graph * C + asg;
       const int64_t cb = (int64_t)graph * a.dl.chunks_per_graph;
-      const int delta_size = a.dl.community_sizes[tb];
-      const int old_tail = a.dl.community_tail[tb];
+      const int delta_size = s_dsize[slot];
+      const int old_tail = s_tail[slot];
       const int old_cs = old_tail >= 0 ? a.dl.chunk_size[cb + old_tail] : 0;
       const int old_cc = old_tail >= 0 ? a.dl.chunk_capacity[cb + old_tail] : 0;
-      const bool allocate = old_tail < 0 || old_cs >= old_cc;
+      const int old_start = old_tail >= 0 ? a.dl.chunk_start[cb + old_tail] : 0;
       const int free_chunk = a.dl.next_free_chunk[graph];
       const int free_pos = a.dl.next_free_position[graph];
+      const bool allocate = old_tail < 0 || old_cs >= old_cc;
       const int new_cap = old_tail < 0 ? 1 : old_cc * 2;
       chunk_ov = allocate && free_chunk >= a.dl.chunks_per_graph;
       pos_ov = allocate && free_pos + new_cap > a.dl.position_capacity;
@@ -405,10 +443,10 @@ __device__ void owner_update(const DecodeArgs& a, const int rh, const int tiles,
         a.dl.community_tail[tb] = free_chunk;
       }
       if (valid_chunk && valid_pos) {
-        const int start = allocate ? free_pos : a.dl.chunk_start[cb + old_tail];
-        const int slot = allocate ? 0 : old_cs;
-        a.dl.positions[(int64_t)graph * a.dl.position_capacity + start + slot] = cur;
-        a.dl.chunk_size[cb + chunk] = slot + 1;
+        const int start = allocate ? free_pos : old_start;
+        const int at = allocate ? 0 : old_cs;
+        a.dl.positions[(int64_t)graph * a.dl.position_capacity + start + at] = cur;
+        a.dl.chunk_size[cb + chunk] = at + 1;
         a.dl.community_sizes[tb] = delta_size + 1;
       }
     }
@@ -508,30 +546,20 @@ __device__ inline f32x4_t mfma_bf16(uint4 a, uint4 b, f32x4_t c) {
                                                  0, 0, 0);
 }
 
-__device__ inline uint32_t pack_bf16x2(float lo, float hi) {
-  return (uint32_t)ckv_f32_to_bf16_bits(lo) | ((uint32_t)ckv_f32_to_bf16_bits(hi) << 16);
-}
+__device__ inline uint32_t pack_bf16x2(float lo, float hi) { return pack_bf16x2_hw(lo, hi); }
 
-// Unconditional 16-byte load through the global address space (one
-// global_load_dwordx4, no flat addressing).
-__device__ inline uint4 gload16(const uint16_t* p) {
-  typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
-  typedef const __attribute__((address_space(1))) u32x4_t* global_u32x4_ptr;
-  const u32x4_t v = *(global_u32x4_ptr)(p);
-  return uint4{v[0], v[1], v[2], v[3]};
+// ds_read_b64_tr_b16: within each group of 16 lanes, lane i receives element
+// i % 4 of the 8-byte words addressed by lanes i / 4 + 4k, k = 0..3.
+__device__ inline uint2 lds_read_tr16(const uint16_t* p) {
+  typedef short s16x4_t __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) s16x4_t* lds_s16x4_ptr;
+  const s16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(const_cast<uint16_t*>(p)));
+  return __builtin_bit_cast(uint2, v);
 }
 
 struct QOperand {
   uint4 s[4];  // Q^T B-operand chunks for the four 32-dim steps
 };
-
-// Orders this wave's LDS accesses (writes before the barrier are visible to
-// every lane of the wave after it) without synchronising other waves.
-__device__ inline void wave_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
 
 // Computes one tile: scores (scaled, -inf where pos_s < 0), per-query max and
 // sum, and accumulates P.V into o (rows g = 4*(lane/16)+i, dims 16*nb + lane%16).
@@ -588,8 +616,8 @@ __device__ inline TileResult mfma_tile(const uint16_t* __restrict__ K, const uin
       for (int i = 0; i < 4; ++i) cand_s[tau(j, 4 * L + i)] = sc[j][i];
     }
   }
-  mloc = fmax_exact(mloc, __shfl_xor(mloc, 16, 64));
-  mloc = fmax_exact(mloc, __shfl_xor(mloc, 32, 64));
+  mloc = max_xor16(mloc);
+  mloc = max_xor32(mloc);
   TileResult res;
   const float m_new = fmax_exact(m_prev, mloc);
   res.m = m_new;
@@ -606,8 +634,8 @@ __device__ inline TileResult mfma_tile(const uint16_t* __restrict__ K, const uin
     pk[j][0] = pack_bf16x2(p[0], p[1]);
     pk[j][1] = pack_bf16x2(p[2], p[3]);
   }
-  lsum = lsum + __shfl_xor(lsum, 16, 64);
-  lsum = lsum + __shfl_xor(lsum, 32, 64);
+  lsum = add_xor16(lsum);
+  lsum = add_xor32(lsum);
   res.l = lsum;
   // rescale the running accumulator rows (query 4L+i) by exp(m_prev - m_new) of that query
   {
@@ -630,16 +658,15 @@ __device__ inline TileResult mfma_tile(const uint16_t* __restrict__ K, const uin
     }
     wave_sync();  // this half (and the candidates) visible to every lane of the wave
     const uint4 aop = {pk[2 * s][0], pk[2 * s][1], pk[2 * s + 1][0], pk[2 * s + 1][1]};
+    // B operand (8 tokens x 16 dims per lane group) by two transposing reads:
+    // lane (L, c16) addresses token 8L + 4h + c16/4, dims 16nb + 4(c16%4)..+3
+    // and receives tokens 8L + 4h .. +3 of dim 16nb + c16.
 #pragma unroll
     for (int nb = 0; nb < 8; ++nb) {
-      const int dim = 16 * nb + c16;
-      const int r0 = 8 * L;
-      uint32_t w[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        w[u] = (uint32_t)v_s[vidx(r0 + 2 * u, dim)] | ((uint32_t)v_s[vidx(r0 + 2 * u + 1, dim)] << 16);
-      }
-      const uint4 bop = {w[0], w[1], w[2], w[3]};
+      const int dim = 16 * nb + 4 * (c16 & 3);
+      const uint2 lo = lds_read_tr16(v_s + vidx(8 * L + (c16 >> 2), dim));
+      const uint2 hi = lds_read_tr16(v_s + vidx(8 * L + 4 + (c16 >> 2), dim));
+      const uint4 bop = {lo.x, lo.y, hi.x, hi.y};
       o[nb] = mfma_bf16(aop, bop, o[nb]);
     }
   }
@@ -760,6 +787,7 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attend_mfma_kernel(DecodeArgs 
   __shared__ float s_lse0;
 
   const int tile = wgi * ATT_WAVES + wave;
+  CKV_STAMP(rh == 0 && wgi == 0, 0);
   const int slot = tile * TILE + lane;
   int pos = tile < tiles ? a.ws.slot_positions[(int64_t)rh * a.ws.slot_capacity + slot] : -1;
   const bool valid = pos >= 0 && pos < a.kv.capacity;
@@ -774,6 +802,7 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attend_mfma_kernel(DecodeArgs 
     qop.s[s] = c16 < G ? v : zero;
   }
   wave_sync();
+  CKV_STAMP(rh == 0 && wgi == 0, 9);
   const bool want_topk = a.cfg.assignment != CKV_ASSIGN_NONE;
   if (any) {
     f32x4_t o[8];
@@ -782,6 +811,7 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attend_mfma_kernel(DecodeArgs 
     const TileResult r = mfma_tile(K, V, kvh * a.kv.head_stride, a.kv.token_stride, pos_s[wave], v_s,
                                    want_topk ? cand_s[wave] : nullptr, qop, a.cfg.softmax_scale, NEG_INF, o);
     wave_sync();
+    CKV_STAMP(rh == 0 && wgi == 0, 1);
     if (L == 0 && c16 < G) {
       wm_s[wave][c16] = r.m;
       wl_s[wave][c16] = r.l;
@@ -796,11 +826,8 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attend_mfma_kernel(DecodeArgs 
     }
     if (want_topk) {
       uint64_t cand = (pos >= 0 && slot >= a.cfg.num_sink) ? pack_candidate(cand_s[wave][lane], pos) : 0ull;
-      for (int k = 0; k < KAPPA; ++k) {
-        const uint64_t best = wave_max_u64(cand);
-        if (lane == k) wtop_s[wave][k] = best;
-        if (cand == best) cand = 0ull;
-      }
+      cand = wave_sort_desc_u64(cand);
+      if (lane < KAPPA) wtop_s[wave][lane] = cand;
     }
   } else {
     if (L == 0 && c16 < G) {
@@ -810,6 +837,7 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attend_mfma_kernel(DecodeArgs 
     if (lane < KAPPA) wtop_s[wave][lane] = 0ull;
   }
   __syncthreads();
+  CKV_STAMP(rh == 0 && wgi == 0, 10);
   // Combine this workgroup's waves into one split partial.
   for (int i = tid; i < G * D; i += 64 * ATT_WAVES) {
     const int g = i >> 7;
@@ -841,14 +869,13 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attend_mfma_kernel(DecodeArgs 
     a.ws.partial_max[((int64_t)rh * G + tid) * splits + wgi] = M;
     a.ws.partial_sum[((int64_t)rh * G + tid) * splits + wgi] = l;
   }
+  CKV_STAMP(rh == 0 && wgi == 0, 11);
   if (want_topk && wave == 0) {
     uint64_t cand = lane < ATT_WAVES * KAPPA ? wtop_s[lane / KAPPA][lane % KAPPA] : 0ull;
-    for (int k = 0; k < KAPPA; ++k) {
-      const uint64_t best = wave_max_u64(cand);
-      if (lane == k) a.ws.partial_topk[((int64_t)rh * splits + wgi) * KAPPA + k] = best;
-      if (cand == best) cand = 0ull;
-    }
+    cand = wave_sort_desc_u64(cand);
+    if (lane < KAPPA) a.ws.partial_topk[((int64_t)rh * splits + wgi) * KAPPA + lane] = cand;
   }
+  CKV_STAMP(rh == 0 && wgi == 0, 2);
   if (!FUSED) return;
   // The last workgroup of this head to finish merges the splits and runs the update.
   __threadfence();
@@ -862,8 +889,11 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attend_mfma_kernel(DecodeArgs 
   __syncthreads();
   if (!last_block) return;
   __threadfence();
+  CKV_STAMP(rh == 0, 3);
   merge_group<CKV_BF16>(a, rh, splits, reinterpret_cast<float*>(att_dyn), &s_lse0);
+  CKV_STAMP(rh == 0, 4);
   owner_update<CT, CKV_BF16>(a, rh, splits, s_lse0);
+  CKV_STAMP(rh == 0, 8);
 }
 
 // Dense bf16 decode baseline: each wave streams `chunk_tiles` consecutive
@@ -988,3 +1018,9 @@ int launch_dense(const DecodeArgs& a, int seq_len, int group, hipStream_t s) {
 }
 
 }  // namespace ckv
+
+#ifdef CKV_PHASE_TIMING
+extern "C" int ckv_phase_stamps_attend(unsigned long long* out) {
+  return (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(ckv::phase_stamp), sizeof(unsigned long long) * 32);
+}
+#endif

@@ -44,6 +44,8 @@ int validate(const ckv_kv_cache* kv, const ckv_graph_state* st, const ckv_prefil
     return fail(CKV_E_INVALID, "slot capacity must be a positive multiple of 64, at most 131072");
   if (cfg->num_sink < 0 || cfg->max_selected < 0 || cfg->local_window < 0)
     return fail(CKV_E_INVALID, "negative slot counts");
+  if (cfg->num_sink > CKV_MAX_SINKS) return fail(CKV_E_LIMIT, "num_sink exceeds 256");
+  if (cfg->local_window > CKV_MAX_WINDOW) return fail(CKV_E_LIMIT, "local_window exceeds 1024");
   if (cfg->num_sink + cfg->max_selected + cfg->local_window + (cfg->include_current ? 1 : 0) > ws->slot_capacity)
     return fail(CKV_E_INVALID, "slot capacity smaller than sinks + selected + window + current");
   if (csr->member_offsets && cfg->num_sink > 0 && !cfg->sink_positions)
@@ -64,7 +66,7 @@ int validate(const ckv_kv_cache* kv, const ckv_graph_state* st, const ckv_prefil
     return fail(CKV_E_INVALID, "score_blocks must equal ceil(score_coverage / 64)");
   if (!ws->scores || !ws->communities || !ws->cumulative_ends || !ws->descriptor_counts || !ws->tile_descriptors ||
       !ws->selected_counts || !ws->slot_positions || !ws->block_counters ||
-      (cfg->assignment == CKV_ASSIGN_NEAREST && (!ws->nearest_partial || !ws->nearest)))
+      (cfg->assignment == CKV_ASSIGN_NEAREST && !ws->nearest))
     return fail(CKV_E_INVALID, "selection workspace is incomplete");
   if (kv->head_stride % 8 || kv->token_stride % 8)
     return fail(CKV_E_INVALID, "kv strides must be multiples of 8 elements");

@@ -10,12 +10,25 @@
 
 namespace ckv {
 
+// Phase timestamps (100 MHz wall clock) for latency-profiling builds compiled
+// with -DCKV_PHASE_TIMING; each kernel file then defines its own
+// `phase_stamp` array and a host getter.  Expands to nothing otherwise.
+#ifdef CKV_PHASE_TIMING
+#define CKV_STAMP(cond, slot)                                         \
+  do {                                                               \
+    if ((cond) && threadIdx.x == 0) phase_stamp[(slot)] = wall_clock64(); \
+  } while (0)
+#else
+#define CKV_STAMP(cond, slot) \
+  do {                        \
+  } while (0)
+#endif
 
 constexpr int D = CKV_HEAD_DIM;
 constexpr int TILE = CKV_TILE;
 constexpr int KAPPA = CKV_KAPPA;
 constexpr int SCORE_BLOCK = CKV_SCORE_BLOCK;
-constexpr int SELECT_THREADS = 256;
+constexpr int SELECT_THREADS = 1024;  // one selection workgroup per retrieval head
 constexpr int REDUCE_THREADS = 128;
 constexpr float NEG_INF = -__builtin_huge_valf();
 
@@ -100,41 +113,209 @@ __device__ inline void store_centroid1(void* base, int64_t index, float v) {
   }
 }
 
+// Hardware conversions of gfx950 (single instructions).  Each matches the
+// library's reference rounding bit for bit (IEEE round-to-nearest-even, OCP
+// e4m3); ckv_device_numerics exposes them for the parity tests.
+__device__ inline uint16_t f16_bits_hw(float x) { return __builtin_bit_cast(uint16_t, (_Float16)x); }
+
+__device__ inline uint32_t pack_bf16x2_hw(float lo, float hi) {
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  const f32x2_t v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+}
+
+__device__ inline float e4m3_to_f32_hw(uint32_t code) {
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  const f32x2_t v = __builtin_amdgcn_cvt_pk_f32_fp8((int)code, false);
+  return v[0];
+}
+
+// Loads through the global address space (global_load_*, never flat), so that
+// waits on LDS traffic do not also wait on these.
+__device__ inline uint4 gload16(const void* p) {
+  typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+  typedef const __attribute__((address_space(1))) u32x4_t* global_u32x4_ptr;
+  const u32x4_t v = *(global_u32x4_ptr)(p);
+  return uint4{v[0], v[1], v[2], v[3]};
+}
+
+__device__ inline int32_t gload_i32(const int32_t* p) {
+  typedef const __attribute__((address_space(1))) int32_t* global_i32_ptr;
+  return *(global_i32_ptr)(p);
+}
+
+__device__ inline float gload_f32(const float* p) {
+  typedef const __attribute__((address_space(1))) float* global_f32_ptr;
+  return *(global_f32_ptr)(p);
+}
+
+
+// ---------------------------------------------------------------------------
+// Cross-lane moves on the VALU (DPP and the gfx950 permlane swaps).  A lone
+// wave pays the full latency of every dependent instruction, and an LDS
+// permute costs several times a DPP move, so reductions and scans use these.
+// ---------------------------------------------------------------------------
+
+__device__ inline int lane_id() { return (int)__lane_id(); }
+
+// Orders this wave's LDS accesses (writes before the barrier are visible to
+// every lane of the wave after it) without synchronising other waves.
+__device__ inline void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+template <int CTRL>
+__device__ inline uint32_t dpp_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xF, 0xF, false);
+}
+
+// Value held by lane (lane ^ X), X in {1, 2, 4, 8, 16, 32}.
+template <int X>
+__device__ inline uint32_t xor_u32(uint32_t v) {
+  if constexpr (X == 1) {
+    return dpp_u32<0xB1>(v);  // quad_perm [1,0,3,2]
+  } else if constexpr (X == 2) {
+    return dpp_u32<0x4E>(v);  // quad_perm [2,3,0,1]
+  } else if constexpr (X == 4) {
+    return dpp_u32<0x141>(dpp_u32<0x1B>(v));  // half-row mirror of the quad reverse
+  } else if constexpr (X == 8) {
+    return dpp_u32<0x141>(dpp_u32<0x140>(v));  // half-row mirror of the row mirror
+  } else if constexpr (X == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return (lane_id() & 16) ? (uint32_t)r[0] : (uint32_t)r[1];
+  } else {
+    static_assert(X == 32, "xor distance");
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return (lane_id() & 32) ? (uint32_t)r[0] : (uint32_t)r[1];
+  }
+}
+
+template <int X>
+__device__ inline float xor_f32(float v) {
+  return ckv_u2f(xor_u32<X>(ckv_f2u(v)));
+}
+
+// v + v[lane ^ 16] (resp. 32) on every lane, as one swap and one add.
+__device__ inline float add_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(ckv_f2u(v), ckv_f2u(v), false, false);
+  return ckv_u2f((uint32_t)r[0]) + ckv_u2f((uint32_t)r[1]);
+}
+__device__ inline float add_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(ckv_f2u(v), ckv_f2u(v), false, false);
+  return ckv_u2f((uint32_t)r[0]) + ckv_u2f((uint32_t)r[1]);
+}
+
 __device__ inline float fmax_exact(float a, float b) { return a > b ? a : b; }
 
+__device__ inline float max_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(ckv_f2u(v), ckv_f2u(v), false, false);
+  return fmax_exact(ckv_u2f((uint32_t)r[0]), ckv_u2f((uint32_t)r[1]));
+}
+__device__ inline float max_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(ckv_f2u(v), ckv_f2u(v), false, false);
+  return fmax_exact(ckv_u2f((uint32_t)r[0]), ckv_u2f((uint32_t)r[1]));
+}
+
+// Wave-wide max (any pairing gives the same max), result on every lane.
 __device__ inline float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmax_exact(v, __shfl_xor(v, o, 64));
-  return v;
+  v = fmax_exact(v, ckv_u2f(dpp_u32<0xB1>(ckv_f2u(v))));
+  v = fmax_exact(v, ckv_u2f(dpp_u32<0x4E>(ckv_f2u(v))));
+  v = fmax_exact(v, ckv_u2f(dpp_u32<0x141>(ckv_f2u(v))));
+  v = fmax_exact(v, ckv_u2f(dpp_u32<0x140>(ckv_f2u(v))));
+  v = max_xor16(v);
+  return max_xor32(v);
 }
 
+// Butterfly sum in the fixed order xor 32, 16, 8, 4, 2, 1 (bit-reproducible).
 __device__ inline float wave_sum_tree(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = v + __shfl_xor(v, o, 64);
-  return v;
+  v = add_xor32(v);
+  v = add_xor16(v);
+  v = v + xor_f32<8>(v);
+  v = v + xor_f32<4>(v);
+  v = v + xor_f32<2>(v);
+  return v + xor_f32<1>(v);
 }
 
-__device__ inline uint64_t shfl_xor_u64(uint64_t v, int o) {
-  const uint32_t lo = __shfl_xor((uint32_t)(v & 0xffffffffu), o, 64);
-  const uint32_t hi = __shfl_xor((uint32_t)(v >> 32), o, 64);
-  return ((uint64_t)hi << 32) | lo;
+template <int CTRL>
+__device__ inline uint64_t dpp_u64(uint64_t v) {
+  return ((uint64_t)dpp_u32<CTRL>((uint32_t)(v >> 32)) << 32) | dpp_u32<CTRL>((uint32_t)(v & 0xffffffffu));
 }
 
-__device__ inline uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const uint64_t w = shfl_xor_u64(v, o);
-    v = w > v ? w : v;
+template <bool MAX>
+__device__ inline uint64_t pick_u64(uint64_t a, uint64_t b) {
+  return MAX ? (a > b ? a : b) : (a < b ? a : b);
+}
+
+template <bool MAX>
+__device__ inline uint64_t wave_reduce_u64(uint64_t v) {
+  v = pick_u64<MAX>(v, dpp_u64<0xB1>(v));
+  v = pick_u64<MAX>(v, dpp_u64<0x4E>(v));
+  v = pick_u64<MAX>(v, dpp_u64<0x141>(v));
+  v = pick_u64<MAX>(v, dpp_u64<0x140>(v));
+  {
+    const uint32_t lo = (uint32_t)(v & 0xffffffffu), hi = (uint32_t)(v >> 32);
+    const auto rl = __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+    const auto rh = __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+    v = pick_u64<MAX>(((uint64_t)(uint32_t)rh[0] << 32) | (uint32_t)rl[0],
+                      ((uint64_t)(uint32_t)rh[1] << 32) | (uint32_t)rl[1]);
+  }
+  {
+    const uint32_t lo = (uint32_t)(v & 0xffffffffu), hi = (uint32_t)(v >> 32);
+    const auto rl = __builtin_amdgcn_permlane32_swap(lo, lo, false, false);
+    const auto rh = __builtin_amdgcn_permlane32_swap(hi, hi, false, false);
+    v = pick_u64<MAX>(((uint64_t)(uint32_t)rh[0] << 32) | (uint32_t)rl[0],
+                      ((uint64_t)(uint32_t)rh[1] << 32) | (uint32_t)rl[1]);
   }
   return v;
 }
 
-__device__ inline uint64_t wave_min_u64(uint64_t v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const uint64_t w = shfl_xor_u64(v, o);
-    v = w < v ? w : v;
+__device__ inline uint64_t wave_max_u64(uint64_t v) { return wave_reduce_u64<true>(v); }
+__device__ inline uint64_t wave_min_u64(uint64_t v) { return wave_reduce_u64<false>(v); }
+
+template <int X>
+__device__ inline uint64_t xor_u64(uint64_t v) {
+  return ((uint64_t)xor_u32<X>((uint32_t)(v >> 32)) << 32) | xor_u32<X>((uint32_t)(v & 0xffffffffu));
+}
+
+// Bitonic sort across the 64 lanes, descending (lane 0 holds the largest key).
+template <int K, int J>
+__device__ inline uint64_t bitonic_stage(uint64_t v, int lane) {
+  const uint64_t other = xor_u64<J>(v);
+  const bool ascending_block = (lane & K) == 0;  // blocks of the final descending order alternate
+  const bool lower = (lane & J) == 0;
+  const bool keep_max = ascending_block == lower;
+  v = keep_max ? (other > v ? other : v) : (other < v ? other : v);
+  if constexpr (J > 1) {
+    return bitonic_stage<K, J / 2>(v, lane);
+  } else {
+    return v;
   }
+}
+
+template <int K>
+__device__ inline uint64_t bitonic_phase(uint64_t v, int lane) {
+  v = bitonic_stage<K, K / 2>(v, lane);
+  if constexpr (K < 64) {
+    return bitonic_phase<K * 2>(v, lane);
+  } else {
+    return v;
+  }
+}
+
+__device__ inline uint64_t wave_sort_desc_u64(uint64_t v) { return bitonic_phase<2>(v, lane_id()); }
+
+// Inclusive prefix sum over the 64 lanes: shifts within each row of 16, then
+// the row broadcasts of lanes 15 and 31.
+__device__ inline int wave_inclusive_scan(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);  // row_bcast:15 into rows 1, 3
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);  // row_bcast:31 into rows 2, 3
   return v;
 }
 
@@ -153,20 +334,12 @@ __device__ inline uint64_t pack_candidate(float score, int32_t position) {
   return ((uint64_t)ordered_f32(score) << 32) | (uint64_t)(0xffffffffu - (uint32_t)position);
 }
 
-// Exclusive block scan of two ints over SELECT_THREADS threads; also returns totals.
+// Exclusive block scan of two ints over the workgroup; also returns totals.
 __device__ inline void block_scan2(int a, int b, int& ea, int& eb, int& ta, int& tb, int* scratch) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  int ia = a, ib = b;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int xa = __shfl_up(ia, o, 64);
-    const int xb = __shfl_up(ib, o, 64);
-    if (lane >= o) {
-      ia += xa;
-      ib += xb;
-    }
-  }
+  const int ia = wave_inclusive_scan(a);
+  const int ib = wave_inclusive_scan(b);
   if (lane == 63) {
     scratch[2 * wave] = ia;
     scratch[2 * wave + 1] = ib;
@@ -175,13 +348,15 @@ __device__ inline void block_scan2(int a, int b, int& ea, int& eb, int& ta, int&
   int ba = 0, bb = 0;
   ta = 0;
   tb = 0;
-  for (int w = 0; w < SELECT_THREADS / 64; ++w) {
+  const int waves = (int)(blockDim.x >> 6);
+  for (int w = 0; w < waves; ++w) {
+    const int xa = scratch[2 * w], xb = scratch[2 * w + 1];
     if (w < wave) {
-      ba += scratch[2 * w];
-      bb += scratch[2 * w + 1];
+      ba += xa;
+      bb += xb;
     }
-    ta += scratch[2 * w];
-    tb += scratch[2 * w + 1];
+    ta += xa;
+    tb += xb;
   }
   ea = ba + ia - a;
   eb = bb + ib - b;
@@ -196,13 +371,9 @@ __device__ inline void find_threshold_bin(const int* hist, int target, int* out_
   const int b0 = 4 * lane;
   const int h0 = hist[b0], h1 = hist[b0 + 1], h2 = hist[b0 + 2], h3 = hist[b0 + 3];
   const int local = h0 + h1 + h2 + h3;
-  int suffix = local;  // inclusive suffix over lanes >= lane
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int x = __shfl_down(suffix, o, 64);
-    if (lane + o < 64) suffix += x;
-  }
-  int above = suffix - local;  // weight of bins above this lane's four
+  const int prefix = wave_inclusive_scan(local);
+  const int total = __builtin_amdgcn_readlane(prefix, 63);
+  int above = total - prefix;  // weight of bins above this lane's four
   int bin = -1, bin_above = 0;
   const int hs[4] = {h0, h1, h2, h3};
 #pragma unroll

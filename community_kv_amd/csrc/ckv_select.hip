@@ -1,18 +1,25 @@
 // Centroid scoring + exact community selection + slot materialisation.
 //
-// score_select_kernel: grid (score_blocks, retrieval_heads) x 256.  Every
-// workgroup scores 64 communities of one retrieval head: 8 lanes per centroid
-// row (16 dims each, one 16-byte fp8 load), pinned fp32 summation order (each
-// lane sums its 16 products in order, then a butterfly over the 8 lanes), fp16
-// round-to-nearest-even key.  The last workgroup of each head to finish
-// (agent-scope counter, no spinning) runs the exact weighted threshold
-// selection in LDS (two 8-bit radix passes over order-preserving fp16 keys),
-// emits descriptors in the reference order and materialises the KV position of
-// every attended slot.
+// select_kernel: one 1024-thread workgroup per retrieval head.  Every decode
+// layer-step is a chain of dependent memory round trips, so the kernel is laid
+// out to need as few of them as possible:
+//   R0  head mapping, query group, centroid rows, community sizes, sinks
+//   R1  graph-indexed fields of every scored community: CSR start, decode-delta
+//       member count and tail chunk; the current position
+//   R2  tail-chunk start and fill of every community with decode deltas (and,
+//       for nearest-centroid assignment, the current key row)
+//   --  scoring and the exact weighted selection run while R2 is in flight
+//   R3  one gather round for every attended slot (CSR member, delta member,
+//       sink, window community)
+// Scoring: 8 lanes per centroid row (16 dims each), pinned fp32 summation order
+// (each lane sums its 16 products in order, then a butterfly over the 8 lanes),
+// fp16 round-to-nearest-even key.  Selection: two 8-bit radix passes over
+// order-preserving fp16 keys in LDS, descriptors in the reference order.
 //
 // Reference: attention/kernels/centroid_selection.py:32-188 (scoring),
 // attention/kernels/_csrc/descriptor_selection.cu:164-487 (selection),
 // attention/kernels/segmented_attention.py:98-282 (slot -> position mapping).
+#include <algorithm>
 #include <type_traits>
 
 #include "ckv_device.h"
@@ -21,144 +28,286 @@
 namespace ckv {
 
 namespace {
-int ckv_internal_limit(const char* message) { return ckv_internal::set_error(CKV_E_LIMIT, message); }
+#ifdef CKV_PHASE_TIMING
+__device__ unsigned long long phase_stamp[32];
+#endif
+
+int limit_error(const char* message) { return ckv_internal::set_error(CKV_E_LIMIT, message); }
+
+constexpr int ROWS_PER_PASS = SELECT_THREADS / 8;          // centroid rows scored per pass
+constexpr int MAT_BATCH = 4;                               // slots per thread gathered together
+constexpr int DESC_ARRAYS = 7;                             // per-descriptor LDS arrays
 }  // namespace
 
-// ---------------------------------------------------------------------------
-// Kernel 1: centroid scoring + (last block per head) exact selection
-// ---------------------------------------------------------------------------
+// Centroid row fragment of one lane: 16 dims (e4m3: 16 bytes, f32: 64 bytes).
+template <int CT>
+struct CentroidFrag {
+  static constexpr int N = CT == CKV_E4M3 ? 1 : 4;
+  uint4 v[N];
+};
 
-template <int CT, int DT>
-__global__ __launch_bounds__(SELECT_THREADS) void score_select_kernel(DecodeArgs a) {
-  const int rh = blockIdx.y;
-  const int blk = blockIdx.x;
+template <int CT>
+__device__ inline void load_frag(const void* base, int64_t row, int d0, CentroidFrag<CT>& f) {
+  if constexpr (CT == CKV_E4M3) {
+    f.v[0] = gload16(reinterpret_cast<const uint8_t*>(base) + row * D + d0);
+  } else {
+    const float* p = reinterpret_cast<const float*>(base) + row * D + d0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) f.v[i] = gload16(p + 4 * i);
+  }
+}
+
+template <int CT>
+__device__ inline void decode_frag(const CentroidFrag<CT>& f, float* out) {
+  if constexpr (CT == CKV_E4M3) {
+    // Hardware OCP e4m3 -> f32 (exact: every e4m3 value is an f32), two bytes per instruction.
+    typedef float f32x2_t __attribute__((ext_vector_type(2)));
+    const uint32_t w[4] = {f.v[0].x, f.v[0].y, f.v[0].z, f.v[0].w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const f32x2_t lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[i], false);
+      const f32x2_t hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[i], true);
+      out[4 * i] = lo[0];
+      out[4 * i + 1] = lo[1];
+      out[4 * i + 2] = hi[0];
+      out[4 * i + 3] = hi[1];
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      out[4 * i] = ckv_u2f(f.v[i].x);
+      out[4 * i + 1] = ckv_u2f(f.v[i].y);
+      out[4 * i + 2] = ckv_u2f(f.v[i].z);
+      out[4 * i + 3] = ckv_u2f(f.v[i].w);
+    }
+  }
+}
+
+// OWN: communities owned per thread (c = k*1024 + tid, k < OWN), chosen from
+// the scored community count so that the per-community fields stay in registers.
+template <int CT, int DT, int OWN>
+__global__ __launch_bounds__(SELECT_THREADS) void select_kernel(DecodeArgs a) {
+  constexpr int PB = CT == CKV_E4M3 ? 4 : 2;  // scoring passes whose loads are in flight together
+  const int rh = blockIdx.x;
   const int tid = threadIdx.x;
   const int G = a.cfg.group_size;
   const int C = a.st.community_capacity;
-  int count = a.st.community_counts[rh];
-  count = count < 0 ? 0 : (count > C ? C : count);
-  const int graph = a.st.retrieval_to_graph[rh];
-  const int kvh = a.st.retrieval_to_kv[rh];
+  const int nscore = min(C, a.ws.score_blocks * SCORE_BLOCK);
   const bool nearest_mode = a.cfg.assignment == CKV_ASSIGN_NEAREST;
-  const int cur = a.st.current_position[graph];
+  const bool materialise = a.csr.member_offsets != nullptr;
+  const int ns = a.cfg.num_sink;
+  const int cpg = a.dl.chunks_per_graph;
+  CKV_STAMP(rh == 0, 0);
 
   __shared__ float q_s[CKV_MAX_GROUP * D];
   __shared__ float key_s[D];
-  __shared__ uint64_t red_u64[SELECT_THREADS / 64];
-  __shared__ int last_block;
-
-  for (int i = tid; i < G * D; i += SELECT_THREADS) {
-    q_s[i] = load_elem<DT>(a.kv.query, (int64_t)rh * G * D + i);
-  }
-  if (nearest_mode && tid < D) {
-    const bool ok = cur >= 0 && cur < a.kv.capacity;
-    key_s[tid] = ok ? load_elem<DT>(a.kv.key, kvh * a.kv.head_stride + (int64_t)cur * a.kv.token_stride + tid) : 0.0f;
-  }
-  __syncthreads();
-
-  const int lane8 = tid & 7;
-  const int sub = tid >> 3;
-  uint64_t best_nearest = ~0ull;
-  for (int pass = 0; pass < SCORE_BLOCK / (SELECT_THREADS / 8); ++pass) {
-    const int c = blk * SCORE_BLOCK + pass * (SELECT_THREADS / 8) + sub;
-    const bool active = c < count;
-    float cv[16];
-    int size = 0;
-    if (active) {
-      load_centroid16<CT>(a.st.centroids, (int64_t)rh * C + c, 16 * lane8, cv);
-      size = a.st.community_sizes[(int64_t)rh * C + c];
-    } else {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) cv[i] = 0.0f;
-    }
-    float best = NEG_INF;
-    for (int g = 0; g < G; ++g) {
-      const float* q = q_s + g * D + 16 * lane8;
-      float acc = q[0] * cv[0];
-#pragma unroll
-      for (int i = 1; i < 16; ++i) acc = acc + q[i] * cv[i];
-      acc = acc + __shfl_xor(acc, 4, 64);
-      acc = acc + __shfl_xor(acc, 2, 64);
-      acc = acc + __shfl_xor(acc, 1, 64);
-      best = fmax_exact(best, acc);
-    }
-    const float score = (active && size > 0) ? best : NEG_INF;
-    if (lane8 == 0 && c < C) a.ws.scores[(int64_t)rh * C + c] = ckv_f32_to_f16_bits(score);
-    if (nearest_mode) {
-      float acc;
-      {
-        const float d0 = key_s[16 * lane8] - cv[0];
-        acc = d0 * d0;
-      }
-#pragma unroll
-      for (int i = 1; i < 16; ++i) {
-        const float di = key_s[16 * lane8 + i] - cv[i];
-        acc = acc + di * di;
-      }
-      acc = acc + __shfl_xor(acc, 4, 64);
-      acc = acc + __shfl_xor(acc, 2, 64);
-      acc = acc + __shfl_xor(acc, 1, 64);
-      if (active && size > 0) {
-        const uint64_t cand = ((uint64_t)ckv_f2u(acc) << 32) | (uint32_t)c;
-        best_nearest = cand < best_nearest ? cand : best_nearest;
-      }
-    }
-  }
-  if (nearest_mode) {
-    const uint64_t w = wave_min_u64(best_nearest);
-    if ((tid & 63) == 0) red_u64[tid >> 6] = w;
-    __syncthreads();
-    if (tid == 0) {
-      uint64_t m = red_u64[0];
-      for (int i = 1; i < SELECT_THREADS / 64; ++i) m = red_u64[i] < m ? red_u64[i] : m;
-      a.ws.nearest_partial[(int64_t)rh * a.ws.score_blocks + blk] = m;
-    }
-  }
-
-  // Last-arriving workgroup of this head performs the selection.
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) {
-    const unsigned prev = __hip_atomic_fetch_add(a.ws.block_counters + rh, 1u, __ATOMIC_ACQ_REL,
-                                                 __HIP_MEMORY_SCOPE_AGENT);
-    last_block = (prev == gridDim.x - 1) ? 1 : 0;
-    if (last_block) {
-      __hip_atomic_store(a.ws.block_counters + rh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
-  __syncthreads();
-  if (!last_block) return;
-  __threadfence();
+  __shared__ int hist[256];
+  __shared__ int scan_s[2 * (SELECT_THREADS / 64)];
+  __shared__ uint64_t near_s[SELECT_THREADS / 64];
+  __shared__ int sink_s[CKV_MAX_SINKS];
+  __shared__ int win_s[CKV_MAX_WINDOW];
+  __shared__ int s_bin, s_above, s_desc_count, s_sel_count, s_last_sel_pos, s_last_size;
 
   extern __shared__ __align__(16) unsigned char dyn[];
+  uint16_t* key16 = reinterpret_cast<uint16_t*>(dyn);  // masked fp16 score bits of every scored community
   const int dcap = a.ws.descriptor_capacity;
-  int* desc_comm = reinterpret_cast<int*>(dyn);
-  int* desc_end = desc_comm + dcap;
-  uint16_t* key16 = reinterpret_cast<uint16_t*>(desc_end + dcap);
+  int* desc_comm = reinterpret_cast<int*>(dyn + (size_t)((C + 7) & ~7) * 2);
+  int* desc_end = desc_comm + dcap;  // cumulative selected-token end
+  int* desc_lo = desc_end + dcap;    // CSR start of the community
+  int* desc_dc = desc_lo + dcap;     // decode-delta member count
+  int* desc_tl = desc_dc + dcap;     // tail chunk id
+  int* desc_ts = desc_tl + dcap;     // tail chunk start
+  int* desc_tn = desc_ts + dcap;     // tail chunk fill
+  int* blk_first = desc_tn + dcap;   // first descriptor reaching each 64-slot block of the selection
 
-  __shared__ int hist[256];
-  __shared__ int scan_scratch[2 * (SELECT_THREADS / 64)];
-  __shared__ int s_bin, s_above, s_hb, s_mass_above_hb;
-  __shared__ int s_high_stored, s_high_count, s_high_mass, s_desc_count, s_sel_count;
-  __shared__ int s_last_sel_pos;
+  // Every prefetch load below is unconditional (indices clamped, results
+  // masked afterwards) and no global store is issued before the last gather:
+  // loads and stores share one completion counter, so a branch around a load
+  // or an early store would make later waits cover them too.
 
-  // Only scored communities take part (score_coverage bounds the active count).
-  if (count > (int)gridDim.x * SCORE_BLOCK) count = (int)gridDim.x * SCORE_BLOCK;
+  // ---- R0 -------------------------------------------------------------------
+  int count = a.st.community_counts[rh];
+  const int graph = a.st.retrieval_to_graph[rh];
+  const int kvh = a.st.retrieval_to_kv[rh];
+  count = count < 0 ? 0 : (count > nscore ? nscore : count);
+
+  const int sub = tid >> 3;
+  const int lane8 = tid & 7;
+  const int passes = (nscore + ROWS_PER_PASS - 1) / ROWS_PER_PASS;
+  CentroidFrag<CT> frag[PB];
+  int rsize[PB];
+  auto load_batch = [&](int p0) {
+#pragma unroll
+    for (int pb = 0; pb < PB; ++pb) {
+      const int row = min((p0 + pb) * ROWS_PER_PASS + sub, nscore - 1);
+      load_frag<CT>(a.st.centroids, (int64_t)rh * C + row, 16 * lane8, frag[pb]);
+      rsize[pb] = gload_i32(a.st.community_sizes + (int64_t)rh * C + row);
+    }
+  };
+  load_batch(0);
+  // Query group: two elements per thread (G * 128 <= 2048).
+  const int qe = min(2 * tid, G * D - 2);
+  float q0, q1;
+  if constexpr (DT == CKV_BF16) {
+    const uint32_t w = (uint32_t)gload_i32(reinterpret_cast<const int32_t*>(
+        reinterpret_cast<const uint16_t*>(a.kv.query) + (int64_t)rh * G * D + qe));
+    q0 = ckv_u2f(w << 16);
+    q1 = ckv_u2f(w & 0xffff0000u);
+  } else {
+    const float* qp = reinterpret_cast<const float*>(a.kv.query) + (int64_t)rh * G * D + qe;
+    q0 = gload_f32(qp);
+    q1 = gload_f32(qp + 1);
+  }
+  const int sink_v = (materialise && ns > 0) ? gload_i32(a.cfg.sink_positions + min(tid, ns - 1)) : -1;
+  const int orounds = (nscore + SELECT_THREADS - 1) / SELECT_THREADS;
+  int o_size[OWN];
+#pragma unroll
+  for (int k = 0; k < OWN; ++k) {
+    const int c = min(k * SELECT_THREADS + tid, nscore - 1);
+    o_size[k] = gload_i32(a.st.community_sizes + (int64_t)rh * C + c);
+  }
+
+  // ---- R1 -------------------------------------------------------------------
+  const int cur = a.st.current_position[graph];
+  const int64_t tbl = (int64_t)graph * C;
+  const int64_t cb = (int64_t)graph * cpg;
+  int o_lo[OWN], o_dc[OWN], o_tl[OWN], o_ts[OWN], o_tn[OWN];
+#pragma unroll
+  for (int k = 0; k < OWN; ++k) {
+    o_lo[k] = 0;
+    o_dc[k] = 0;
+    o_tl[k] = -1;
+    o_ts[k] = 0;
+    o_tn[k] = 0;
+  }
+  if (materialise) {
+#pragma unroll
+    for (int k = 0; k < OWN; ++k) {
+      const int c = min(k * SELECT_THREADS + tid, C - 1);
+      o_lo[k] = gload_i32(a.csr.member_offsets + (int64_t)graph * (C + 1) + c);
+      o_dc[k] = gload_i32(a.dl.community_sizes + tbl + c);
+      o_tl[k] = gload_i32(a.dl.community_tail + tbl + c);
+    }
+  }
+  float key_v = 0.0f;
+  if (nearest_mode) {
+    const int64_t cp = cur < 0 ? 0 : (cur >= a.kv.capacity ? a.kv.capacity - 1 : cur);
+    key_v = load_elem<DT>(a.kv.key, kvh * a.kv.head_stride + cp * a.kv.token_stride + (tid & (D - 1)));
+  }
+
+  // ---- R2 -------------------------------------------------------------------
+  if (materialise && cpg > 0) {
+#pragma unroll
+    for (int k = 0; k < OWN; ++k) {
+      const int t = min(max(o_tl[k], 0), cpg - 1);
+      o_ts[k] = gload_i32(a.dl.chunk_start + cb + t);
+      o_tn[k] = gload_i32(a.dl.chunk_size + cb + t);
+    }
+  }
+  // masks (after the loads were issued)
+#pragma unroll
+  for (int k = 0; k < OWN; ++k) {
+    const int c = k * SELECT_THREADS + tid;
+    const bool own = k < orounds && c < count;
+    if (!(k < orounds && c < nscore)) o_size[k] = 0;
+    if (!own) {
+      o_lo[k] = 0;
+      o_dc[k] = 0;
+      o_tl[k] = -1;
+    }
+  }  // (tail-chunk fields stay raw until a descriptor is stored: masking them here would wait for R2)
+  if (2 * tid < G * D) {
+    q_s[2 * tid] = q0;
+    q_s[2 * tid + 1] = q1;
+  }
+  if (tid < ns) sink_s[tid] = sink_v;
+  if (tid < D) key_s[tid] = (cur >= 0 && cur < a.kv.capacity) ? key_v : 0.0f;
+  hist[tid & 255] = 0;
+  __syncthreads();  // q_s, key_s, sink_s, hist
+  CKV_STAMP(rh == 0, 6);
+
+  // ---- scoring ----------------------------------------------------------------
+  uint64_t best_nearest = ~0ull;
+  auto score_batch = [&](int p0) {
+#pragma unroll
+    for (int pb = 0; pb < PB; ++pb) {
+      const int c = (p0 + pb) * ROWS_PER_PASS + sub;
+      float cv[16];
+      decode_frag<CT>(frag[pb], cv);
+      // Four queries per step as independent chains (q_s rows beyond G are
+      // never selected into `best`); pinned order per query as documented above.
+      float best = NEG_INF;
+#pragma unroll 1
+      for (int g = 0; g < G; g += 4) {
+        const float* q = q_s + g * D + 16 * lane8;
+        float acc[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc[u] = q[u * D] * cv[0];
+#pragma unroll
+        for (int i = 1; i < 16; ++i) {
+#pragma unroll
+          for (int u = 0; u < 4; ++u) acc[u] = acc[u] + q[u * D + i] * cv[i];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          acc[u] = acc[u] + xor_f32<4>(acc[u]);
+          acc[u] = acc[u] + xor_f32<2>(acc[u]);
+          acc[u] = acc[u] + xor_f32<1>(acc[u]);
+          if (g + u < G) best = fmax_exact(best, acc[u]);
+        }
+      }
+      const bool live = c < count && rsize[pb] > 0;
+      if (lane8 == 0 && c < nscore) key16[c] = f16_bits_hw(live ? best : NEG_INF);
+      if (nearest_mode) {
+        float acc;
+        {
+          const float d0 = key_s[16 * lane8] - cv[0];
+          acc = d0 * d0;
+        }
+#pragma unroll
+        for (int i = 1; i < 16; ++i) {
+          const float di = key_s[16 * lane8 + i] - cv[i];
+          acc = acc + di * di;
+        }
+        acc = acc + xor_f32<4>(acc);
+        acc = acc + xor_f32<2>(acc);
+        acc = acc + xor_f32<1>(acc);
+        if (live) {
+          const uint64_t cand = ((uint64_t)ckv_f2u(acc) << 32) | (uint32_t)c;
+          best_nearest = cand < best_nearest ? cand : best_nearest;
+        }
+      }
+    }
+  };
+  score_batch(0);
+  for (int p0 = PB; p0 < passes; p0 += PB) {
+    load_batch(p0);
+    score_batch(p0);
+  }
+  CKV_STAMP(rh == 0, 7);
+  if (nearest_mode) {
+    const uint64_t w = wave_min_u64(best_nearest);
+    if ((tid & 63) == 0) near_s[tid >> 6] = w;
+  }
+  __syncthreads();  // key16, near_s
+  CKV_STAMP(rh == 0, 1);
+
+  // ---- exact weighted selection ---------------------------------------------
   const bool budget_mode = a.cfg.selection_mode == CKV_SELECT_BUDGET;
   const int sel_slots = a.cfg.max_selected;
   const int target = budget_mode ? sel_slots : a.cfg.topk_communities;
-
-  for (int c = tid; c < count; c += SELECT_THREADS) {
-    key16[c] = ckv_ordered_key16(a.ws.scores[(int64_t)rh * C + c]);
-  }
-  hist[tid] = 0;
-  __syncthreads();
-  // Pass 1: weighted histogram of the high key byte.
-  for (int c = tid; c < count; c += SELECT_THREADS) {
-    const int size = a.st.community_sizes[(int64_t)rh * C + c];
-    if (size > 0) atomicAdd(hist + (key16[c] >> 8), budget_mode ? size : 1);
+  uint32_t o_key[OWN];
+#pragma unroll
+  for (int k = 0; k < OWN; ++k) {
+    const int c = k * SELECT_THREADS + tid;
+    const bool live = k < orounds && c < count && o_size[k] > 0;
+    o_key[k] = live ? ckv_ordered_key16(key16[c]) : 0u;
+    if (live) atomicAdd(hist + (o_key[k] >> 8), budget_mode ? o_size[k] : 1);
   }
   __syncthreads();
+  // key16 is dead from here on; it becomes the community -> descriptor table.
+  uint16_t* comm_desc = key16;
+  for (int c = tid; c < nscore; c += SELECT_THREADS) comm_desc[c] = 0xffffu;
   if (tid < 64) find_threshold_bin(hist, target, &s_bin, &s_above);
   __syncthreads();
   const int hb = s_bin;
@@ -167,77 +316,69 @@ __global__ __launch_bounds__(SELECT_THREADS) void score_select_kernel(DecodeArgs
     threshold = -1;
   } else {
     const int above_hb = s_above;
-    hist[tid] = 0;
     __syncthreads();
-    for (int c = tid; c < count; c += SELECT_THREADS) {
-      const int size = a.st.community_sizes[(int64_t)rh * C + c];
-      if (size > 0 && (key16[c] >> 8) == hb) atomicAdd(hist + (key16[c] & 0xff), budget_mode ? size : 1);
+    hist[tid & 255] = 0;
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < OWN; ++k) {
+      const int c = k * SELECT_THREADS + tid;
+      const bool live = k < orounds && c < count && o_size[k] > 0;
+      if (live && (int)(o_key[k] >> 8) == hb) atomicAdd(hist + (o_key[k] & 0xff), budget_mode ? o_size[k] : 1);
     }
     __syncthreads();
     if (tid < 64) find_threshold_bin(hist, target - above_hb, &s_bin, &s_above);
     __syncthreads();
     threshold = (hb << 8) | s_bin;
   }
+  CKV_STAMP(rh == 0, 2);
 
   // Compaction, high keys first (id order), then threshold keys (id order).
   const int cap_tokens = sel_slots;
-  int base_cnt = 0, base_mass = 0, stored = 0;
-  for (int start = 0; start < count; start += SELECT_THREADS) {
-    const int c = start + tid;
-    int size = 0;
-    bool high = false;
-    if (c < count) {
-      size = a.st.community_sizes[(int64_t)rh * C + c];
-      high = size > 0 && (int)key16[c] > threshold;
-    }
+  auto store_desc = [&](int idx, int c, int end, int k) {
+    desc_comm[idx] = c;
+    desc_end[idx] = end;
+    desc_lo[idx] = o_lo[k];
+    desc_dc[idx] = o_dc[k];
+    desc_tl[idx] = o_tl[k];
+    const bool has = o_dc[k] > 0 && o_tl[k] >= 0 && o_tl[k] < cpg;
+    desc_ts[idx] = has ? o_ts[k] : 0;
+    desc_tn[idx] = has ? o_tn[k] : 0;
+  };
+  int high_count = 0, high_mass = 0, high_stored = 0;
+#pragma unroll
+  for (int k = 0; k < OWN; ++k) {
+    if (k >= orounds) break;
+    const int c = k * SELECT_THREADS + tid;
+    const int size = o_size[k];
+    const bool high = c < count && size > 0 && (int)o_key[k] > threshold;
     int ec, em, tc, tm;
-    block_scan2(high ? 1 : 0, high ? size : 0, ec, em, tc, tm, scan_scratch);
-    if (high) {
-      const int idx = base_cnt + ec;
-      const int st0 = base_mass + em;
-      if (st0 < cap_tokens && idx < dcap) {
-        desc_comm[idx] = c;
-        desc_end[idx] = min(cap_tokens, st0 + size);
-      }
-    }
-    // number of stored high descriptors: those whose start is below the cap
-    int sc_local = (high && base_mass + em < cap_tokens) ? 1 : 0;
-    int e2, e3, t2, t3;
-    block_scan2(sc_local, 0, e2, e3, t2, t3, scan_scratch);
-    stored += t2;
-    base_cnt += tc;
-    base_mass += tm;
+    block_scan2(high ? 1 : 0, high ? size : 0, ec, em, tc, tm, scan_s);
+    const int st0 = high_mass + em;
+    const bool stored = high && st0 < cap_tokens;
+    if (stored && high_count + ec < dcap) store_desc(high_count + ec, c, min(cap_tokens, st0 + size), k);
+    high_stored += __syncthreads_count(stored);
+    high_count += tc;
+    high_mass += tm;
   }
-  const int high_count = base_cnt;
-  const int high_mass = base_mass;
-  const int high_stored = stored;
   int eq_cnt = 0, eq_mass = 0, eq_stored = 0;
   if (threshold >= 0) {
-    for (int start = 0; start < count; start += SELECT_THREADS) {
-      const int c = start + tid;
-      int size = 0;
-      bool eq = false;
-      if (c < count) {
-        size = a.st.community_sizes[(int64_t)rh * C + c];
-        eq = size > 0 && (int)key16[c] == threshold;
-      }
+#pragma unroll
+    for (int k = 0; k < OWN; ++k) {
+      if (k >= orounds) break;
+      const int c = k * SELECT_THREADS + tid;
+      const int size = o_size[k];
+      const bool eq = c < count && size > 0 && (int)o_key[k] == threshold;
       int ec, em, tc, tm;
-      block_scan2(eq ? 1 : 0, eq ? size : 0, ec, em, tc, tm, scan_scratch);
+      block_scan2(eq ? 1 : 0, eq ? size : 0, ec, em, tc, tm, scan_s);
       bool take = false;
       if (eq) {
         const int st0 = high_mass + eq_mass + em;
-        const bool within = budget_mode ? (st0 < sel_slots)
-                                        : (eq_cnt + ec < a.cfg.topk_communities - high_count);
+        const bool within = budget_mode ? (st0 < sel_slots) : (eq_cnt + ec < a.cfg.topk_communities - high_count);
         take = within && st0 < cap_tokens;
         const int idx = high_count + eq_cnt + ec;
-        if (take && idx < dcap) {
-          desc_comm[idx] = c;
-          desc_end[idx] = min(cap_tokens, st0 + size);
-        }
+        if (take && idx < dcap) store_desc(idx, c, min(cap_tokens, st0 + size), k);
       }
-      int e2, e3, t2, t3;
-      block_scan2(take ? 1 : 0, 0, e2, e3, t2, t3, scan_scratch);
-      eq_stored += t2;
+      eq_stored += __syncthreads_count(take);
       eq_cnt += tc;
       eq_mass += tm;
     }
@@ -245,24 +386,180 @@ __global__ __launch_bounds__(SELECT_THREADS) void score_select_kernel(DecodeArgs
   int desc_count = high_stored + eq_stored;
   if (desc_count > dcap) desc_count = dcap;
   if (tid == 0) {
-    const int sel_count = desc_count > 0 ? desc_end[desc_count - 1] : 0;
     s_desc_count = desc_count;
-    s_sel_count = sel_count;
-    s_high_stored = high_stored < desc_count ? high_stored : desc_count;
-    s_high_count = high_count;
-    s_high_mass = high_mass;
+    s_sel_count = desc_count > 0 ? desc_end[desc_count - 1] : 0;
     s_last_sel_pos = -1;
-    a.ws.descriptor_counts[rh] = desc_count;
-    a.ws.selected_counts[rh] = sel_count;
+    s_last_size = 0;
   }
   __syncthreads();
   const int n_desc = s_desc_count;
   const int sel_count = s_sel_count;
+  const int nblk = (sel_count + 63) / 64;
+  for (int b = tid; b <= nblk; b += SELECT_THREADS) {
+    const int j = 64 * b;
+    int lo = 0, hi = n_desc;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (desc_end[mid] <= j) lo = mid + 1; else hi = mid;
+    }
+    blk_first[b] = lo;
+  }
+  for (int d = tid; d < n_desc; d += SELECT_THREADS) comm_desc[desc_comm[d]] = (uint16_t)d;
+  // Only the last descriptor can be truncated; remember its community size.
+  if (n_desc > 0) {
+    const int last_c = desc_comm[n_desc - 1];
+    if (last_c % SELECT_THREADS == tid) {
+#pragma unroll
+      for (int k = 0; k < OWN; ++k) {
+        if (k * SELECT_THREADS + tid == last_c) s_last_size = o_size[k];
+      }
+    }
+  }
+  CKV_STAMP(rh == 0, 3);
+
+  if (materialise) {
+    __syncthreads();  // blk_first, comm_desc
+    // ---- R3: slot materialisation ---------------------------------------------
+    // Layout: sinks, selected members (newest first: decode deltas from the
+    // tail chunk backwards, then the recency-descending CSR), window, current.
+    const int W = a.cfg.local_window;
+    const int inc = a.cfg.include_current ? 1 : 0;
+    const int slot_cap = a.ws.slot_capacity;
+    int32_t* slots = a.ws.slot_positions + (int64_t)rh * slot_cap;
+    const int32_t* members = a.csr.member_positions + (int64_t)graph * a.csr.member_stride;
+    const int32_t* dpos = a.dl.positions + (int64_t)graph * a.dl.position_capacity;
+    const int32_t* tcomm = a.st.token_communities + (int64_t)graph * a.st.token_capacity;
+    const int wbeg = ns + sel_count;
+    for (int s0 = 0; s0 < slot_cap; s0 += SELECT_THREADS * MAT_BATCH) {
+      const int32_t* src[MAT_BATCH];
+      int val[MAT_BATCH];
+      bool gathered[MAT_BATCH];
+      int slow_d[MAT_BATCH], slow_rem[MAT_BATCH];  // delta members beyond the tail chunk
+#pragma unroll
+      for (int k = 0; k < MAT_BATCH; ++k) {
+        const int s = s0 + k * SELECT_THREADS + tid;
+        src[k] = a.st.community_counts + rh;  // in-bounds dummy address when nothing is gathered
+        val[k] = -1;
+        slow_d[k] = -1;
+        slow_rem[k] = 0;
+        bool gather = false;
+        if (s >= slot_cap) {
+        } else if (s < ns) {
+          val[k] = sink_s[s];
+        } else if (s < wbeg) {
+          const int j = s - ns;
+          int lo = blk_first[j >> 6], hi = min(blk_first[(j >> 6) + 1], n_desc - 1) + 1;
+          while (lo < hi) {
+            const int mid = (lo + hi) >> 1;
+            if (desc_end[mid] <= j) lo = mid + 1; else hi = mid;
+          }
+          const int m = j - (lo > 0 ? desc_end[lo - 1] : 0);
+          const int dc = desc_dc[lo];
+          if (m < dc) {
+            const int tn = desc_tn[lo];
+            if (m < tn) {
+              const int p = desc_ts[lo] + tn - 1 - m;
+              if (p >= 0 && p < a.dl.position_capacity) {
+                src[k] = dpos + p;
+                gather = true;
+              }
+            } else {
+              slow_d[k] = lo;
+              slow_rem[k] = m - tn;
+            }
+          } else {
+            const int64_t idx = (int64_t)desc_lo[lo] + (m - dc);
+            if (idx >= 0 && idx < a.csr.member_stride) {
+              src[k] = members + idx;
+              gather = true;
+            }
+          }
+        } else if (s < wbeg + W) {
+          const int p = cur - W + (s - wbeg);
+          if (p >= 0 && p < a.st.token_capacity) {
+            src[k] = tcomm + p;
+            gather = true;
+          }
+        } else if (inc && s == wbeg + W) {
+          val[k] = cur;
+        }
+        gathered[k] = gather;
+      }
+      int got[MAT_BATCH];
+#pragma unroll
+      for (int k = 0; k < MAT_BATCH; ++k) got[k] = gload_i32(src[k]);
+#pragma unroll
+      for (int k = 0; k < MAT_BATCH; ++k) {
+        if (gathered[k]) val[k] = got[k];
+      }
+      // Delta members older than the tail chunk: walk the chunk chain backwards.
+#pragma unroll
+      for (int k = 0; k < MAT_BATCH; ++k) {
+        if (slow_d[k] < 0) continue;
+        const int tail = desc_tl[slow_d[k]];
+        if (tail < 0 || tail >= cpg) continue;
+        int rem = slow_rem[k];
+        int ch = a.dl.chunk_previous[cb + tail];
+        for (int guard = 0; guard < 64 && ch >= 0 && ch < cpg; ++guard) {
+          const int cs = a.dl.chunk_size[cb + ch];
+          if (rem < cs) {
+            const int p = a.dl.chunk_start[cb + ch] + cs - 1 - rem;
+            if (p >= 0 && p < a.dl.position_capacity) val[k] = dpos[p];
+            break;
+          }
+          rem -= cs;
+          ch = a.dl.chunk_previous[cb + ch];
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < MAT_BATCH; ++k) {
+        const int s = s0 + k * SELECT_THREADS + tid;
+        if (s >= slot_cap) continue;
+        if (s >= wbeg && s < wbeg + W) {
+          win_s[s - wbeg] = val[k];  // community of the window token (resolved below)
+          continue;
+        }
+        slots[s] = val[k];
+        if (s == wbeg - 1 && sel_count > 0) s_last_sel_pos = val[k];
+      }
+    }
+    __syncthreads();
+    CKV_STAMP(rh == 0, 4);
+    // Window: positions cur-W .. cur-1 not already attended (sinks, or members
+    // of a selected community at or after the selection's oldest position).
+    if (W > 0) {
+      const int last_pos = s_last_sel_pos;
+      for (int i = tid; i < W; i += SELECT_THREADS) {
+        const int p = cur - W + i;
+        int pos = p < 0 ? -1 : p;
+        for (int k = 0; k < ns && pos >= 0; ++k) {
+          if (sink_s[k] == p) pos = -1;
+        }
+        if (pos >= 0 && p < a.st.token_capacity) {
+          const int c = win_s[i];
+          if (c >= 0 && c < count) {
+            const int found = comm_desc[c] == 0xffffu ? -1 : (int)comm_desc[c];
+            if (found >= 0) {
+              const int take = desc_end[found] - (found > 0 ? desc_end[found - 1] : 0);
+              const bool full = found < n_desc - 1 || take >= s_last_size;
+              if (full || p >= last_pos) pos = -1;
+            }
+          }
+        }
+        slots[wbeg + i] = pos;
+      }
+    }
+  }
+
+  // ---- outputs that nothing in this kernel reads back --------------------------
+  if (tid == 0) {
+    a.ws.descriptor_counts[rh] = n_desc;
+    a.ws.selected_counts[rh] = sel_count;
+  }
   for (int i = tid; i < n_desc; i += SELECT_THREADS) {
     a.ws.communities[(int64_t)rh * dcap + i] = desc_comm[i];
     a.ws.cumulative_ends[(int64_t)rh * dcap + i] = desc_end[i];
   }
-  const int ns = a.cfg.num_sink;
   for (int t = tid; t < a.ws.budget_tiles; t += SELECT_THREADS) {
     const int off = max(t * TILE - ns, 0);
     int lo = 0, hi = n_desc;
@@ -272,166 +569,65 @@ __global__ __launch_bounds__(SELECT_THREADS) void score_select_kernel(DecodeArgs
     }
     a.ws.tile_descriptors[(int64_t)rh * a.ws.budget_tiles + t] = max(0, min(lo, n_desc - 1));
   }
-
+#pragma unroll
+  for (int k = 0; k < OWN; ++k) {
+    const int c = k * SELECT_THREADS + tid;
+    if (k < orounds && c < nscore) {
+      const bool live = c < count && o_size[k] > 0;
+      const uint32_t key = o_key[k];
+      const uint16_t bits = live ? (uint16_t)((key & 0x8000u) ? (key ^ 0x8000u) : (key ^ 0xffffu)) : (uint16_t)0xfc00u;
+      a.ws.scores[(int64_t)rh * C + c] = bits;
+    }
+  }
   if (nearest_mode && tid == 0) {
     uint64_t m = ~0ull;
-    for (int b = 0; b < a.ws.score_blocks; ++b) {
-      const uint64_t v = a.ws.nearest_partial[(int64_t)rh * a.ws.score_blocks + b];
-      m = v < m ? v : m;
-    }
+    for (int w = 0; w < SELECT_THREADS / 64; ++w) m = near_s[w] < m ? near_s[w] : m;
     a.ws.nearest[rh] = (m == ~0ull) ? -1 : (int)(m & 0xffffffffu);
   }
-  // Without a membership CSR the call only scores and selects.
-  if (a.csr.member_offsets == nullptr) return;
+  CKV_STAMP(rh == 0, 5);
+}
 
-  // Slot materialisation: sinks, selected members (newest first), window, current.
-  const int W = a.cfg.local_window;
-  const int inc = a.cfg.include_current ? 1 : 0;
-  const int slot_cap = a.ws.slot_capacity;
-  int32_t* slots = a.ws.slot_positions + (int64_t)rh * slot_cap;
-  const int64_t tbl = (int64_t)graph * C;
-  // Per-descriptor membership: decode-delta count and prefill CSR start, one
-  // parallel round of loads.
-  int* desc_dc = reinterpret_cast<int*>(key16 + ((C + 7) & ~7));
-  int* desc_lo = desc_dc + dcap;
-  for (int d = tid; d < n_desc; d += SELECT_THREADS) {
-    const int c = desc_comm[d];
-    desc_dc[d] = a.dl.community_sizes[tbl + c];
-    desc_lo[d] = a.csr.member_offsets[(int64_t)graph * (C + 1) + c];
-  }
-  __syncthreads();
-  // Slots in batches of 8 per thread so that the member-position gathers of a
-  // batch are in flight together; decode-delta members (newest first) walk
-  // their chunk chain afterwards.
-  constexpr int BATCH = 8;
-  const int32_t* members = a.csr.member_positions + (int64_t)graph * a.csr.member_stride;
-  for (int s0 = 0; s0 < slot_cap; s0 += SELECT_THREADS * BATCH) {
-    int spos[BATCH];
-    int64_t at[BATCH];
-    int dm[BATCH];   // member index into the delta chain, or -1
-    int dcm[BATCH];  // community of a delta member
-#pragma unroll
-    for (int k = 0; k < BATCH; ++k) {
-      const int s = s0 + k * SELECT_THREADS + tid;
-      spos[k] = -1;
-      at[k] = -1;
-      dm[k] = -1;
-      dcm[k] = 0;
-      if (s >= slot_cap) continue;
-      if (s < ns) {
-        spos[k] = a.cfg.sink_positions[s];
-      } else if (s < ns + sel_count) {
-        const int j = s - ns;
-        int lo = 0, hi = n_desc;
-        while (lo < hi) {
-          const int mid = (lo + hi) >> 1;
-          if (desc_end[mid] <= j) lo = mid + 1; else hi = mid;
-        }
-        const int prev = lo > 0 ? desc_end[lo - 1] : 0;
-        const int m = j - prev;
-        const int dc = desc_dc[lo];
-        if (m < dc) {
-          dm[k] = m;
-          dcm[k] = desc_comm[lo];
-        } else {
-          const int64_t idx = (int64_t)desc_lo[lo] + (m - dc);
-          if (idx < a.csr.member_stride) at[k] = idx;
-        }
-      } else if (inc && s == ns + sel_count + W) {
-        spos[k] = cur;
-      }
-    }
-#pragma unroll
-    for (int k = 0; k < BATCH; ++k) {
-      const int v = members[at[k] >= 0 ? at[k] : 0];
-      if (at[k] >= 0) spos[k] = v;
-    }
-#pragma unroll
-    for (int k = 0; k < BATCH; ++k) {
-      if (dm[k] < 0) continue;
-      int rem = dm[k];
-      int ch = a.dl.community_tail[tbl + dcm[k]];
-      const int64_t cb = (int64_t)graph * a.dl.chunks_per_graph;
-      for (int guard = 0; guard < 64 && ch >= 0 && ch < a.dl.chunks_per_graph; ++guard) {
-        const int cs = a.dl.chunk_size[cb + ch];
-        if (rem < cs) {
-          const int p = a.dl.chunk_start[cb + ch] + cs - 1 - rem;
-          if (p >= 0 && p < a.dl.position_capacity) spos[k] = a.dl.positions[(int64_t)graph * a.dl.position_capacity + p];
-          break;
-        }
-        rem -= cs;
-        ch = a.dl.chunk_previous[cb + ch];
-      }
-    }
-#pragma unroll
-    for (int k = 0; k < BATCH; ++k) {
-      const int s = s0 + k * SELECT_THREADS + tid;
-      if (s >= slot_cap) continue;
-      if (s >= ns + sel_count && s < ns + sel_count + W) continue;  // window: resolved below
-      slots[s] = spos[k];
-      if (s == ns + sel_count - 1 && sel_count > 0) s_last_sel_pos = spos[k];
-    }
-  }
-  __syncthreads();
-  if (W > 0) {
-    const int last_pos = s_last_sel_pos;
-    const int hs = s_high_stored;
-    for (int i = tid; i < W; i += SELECT_THREADS) {
-      const int p = cur - W + i;
-      int pos = p;
-      if (p < 0) pos = -1;
-      for (int k = 0; k < ns && pos >= 0; ++k) {
-        if (a.cfg.sink_positions[k] == p) pos = -1;
-      }
-      if (pos >= 0 && p < a.st.token_capacity) {
-        const int c = a.st.token_communities[(int64_t)graph * a.st.token_capacity + p];
-        if (c >= 0 && c < count) {
-          int found = -1;
-          int lo = 0, hi = hs;
-          while (lo < hi) {
-            const int mid = (lo + hi) >> 1;
-            if (desc_comm[mid] < c) lo = mid + 1; else hi = mid;
-          }
-          if (lo < hs && desc_comm[lo] == c) found = lo;
-          if (found < 0) {
-            lo = hs;
-            hi = n_desc;
-            while (lo < hi) {
-              const int mid = (lo + hi) >> 1;
-              if (desc_comm[mid] < c) lo = mid + 1; else hi = mid;
-            }
-            if (lo < n_desc && desc_comm[lo] == c) found = lo;
-          }
-          if (found >= 0) {
-            const int take = desc_end[found] - (found > 0 ? desc_end[found - 1] : 0);
-            const int size = a.st.community_sizes[(int64_t)rh * C + c];
-            if (take >= size || p >= last_pos) pos = -1;
-          }
-        }
-      }
-      slots[ns + sel_count + i] = pos;
-    }
-  }
+// key16 / community table, the descriptor arrays, the per-block descriptor index.
+size_t select_lds_bytes(int community_capacity, int descriptor_capacity, int max_selected) {
+  return (size_t)((community_capacity + 7) & ~7) * 2 + (size_t)descriptor_capacity * DESC_ARRAYS * 4 +
+         (size_t)((max_selected + 63) / 64 + 2) * 4;
 }
 
 int launch_score_select(const DecodeArgs& a, hipStream_t s) {
-  // Dynamic LDS: descriptor communities/ends/delta counts/CSR starts + fp16 keys.
-  const size_t lds = (size_t)a.ws.descriptor_capacity * 16 + (((size_t)a.st.community_capacity + 7) & ~(size_t)7) * 2;
-  const dim3 grid(a.ws.score_blocks, a.st.retrieval_heads);
+  const size_t lds = select_lds_bytes(a.st.community_capacity, a.ws.descriptor_capacity, a.cfg.max_selected);
   const int ct = a.st.centroid_dtype, dt = a.kv.dtype;
+  const int nscore = std::min(a.st.community_capacity, a.ws.score_blocks * SCORE_BLOCK);
+  const int own = (nscore + SELECT_THREADS - 1) / SELECT_THREADS;
   auto launch = [&](auto kernel) {
     if (lds > 48 * 1024) {
       const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-      if (e != hipSuccess) return ckv_internal_limit("selection LDS exceeds the device limit");
+      if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return limit_error("selection LDS (communities x 2 + descriptors x 28 + selected / 16 bytes) exceeds the device limit");
+      }
     }
-    hipLaunchKernelGGL(kernel, grid, dim3(SELECT_THREADS), lds, s, a);
-    return launch_check("score_select");
+    hipLaunchKernelGGL(kernel, dim3(a.st.retrieval_heads), dim3(SELECT_THREADS), lds, s, a);
+    return launch_check("select");
   };
-  if (ct == CKV_E4M3 && dt == CKV_BF16) return launch(score_select_kernel<CKV_E4M3, CKV_BF16>);
-  if (ct == CKV_E4M3) return launch(score_select_kernel<CKV_E4M3, CKV_F32>);
-  if (dt == CKV_BF16) return launch(score_select_kernel<CKV_F32, CKV_BF16>);
-  return launch(score_select_kernel<CKV_F32, CKV_F32>);
+  auto by_own = [&](auto k1, auto k2, auto k8) { return own <= 1 ? launch(k1) : own <= 2 ? launch(k2) : launch(k8); };
+  if (ct == CKV_E4M3 && dt == CKV_BF16)
+    return by_own(select_kernel<CKV_E4M3, CKV_BF16, 1>, select_kernel<CKV_E4M3, CKV_BF16, 2>,
+                  select_kernel<CKV_E4M3, CKV_BF16, 8>);
+  if (ct == CKV_E4M3)
+    return by_own(select_kernel<CKV_E4M3, CKV_F32, 1>, select_kernel<CKV_E4M3, CKV_F32, 2>,
+                  select_kernel<CKV_E4M3, CKV_F32, 8>);
+  if (dt == CKV_BF16)
+    return by_own(select_kernel<CKV_F32, CKV_BF16, 1>, select_kernel<CKV_F32, CKV_BF16, 2>,
+                  select_kernel<CKV_F32, CKV_BF16, 8>);
+  return by_own(select_kernel<CKV_F32, CKV_F32, 1>, select_kernel<CKV_F32, CKV_F32, 2>,
+                select_kernel<CKV_F32, CKV_F32, 8>);
 }
 
 }  // namespace ckv
+
+#ifdef CKV_PHASE_TIMING
+extern "C" int ckv_phase_stamps_select(unsigned long long* out) {
+  return (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(ckv::phase_stamp), sizeof(unsigned long long) * 32);
+}
+#endif

@@ -40,6 +40,8 @@ extern "C" {
 #define CKV_MAX_GROUP 16
 #define CKV_MAX_COMMUNITIES 8192
 #define CKV_MAX_DESCRIPTORS 4096
+#define CKV_MAX_SINKS 256
+#define CKV_MAX_WINDOW 1024
 
 enum ckv_status {
   CKV_OK = 0,
@@ -137,7 +139,7 @@ typedef struct ckv_decode_workspace {
   int32_t* tile_descriptors;   /* [retrieval_heads][budget_tiles] */
   int32_t* selected_counts;    /* [retrieval_heads] */
   int32_t* slot_positions;     /* [retrieval_heads][slot_capacity] KV position per attended slot, -1 = none */
-  uint64_t* nearest_partial;   /* [retrieval_heads][score_blocks] */
+  uint64_t* nearest_partial;   /* reserved (may be null): the selection kernel reduces in LDS */
   int32_t* nearest;            /* [retrieval_heads] */
   uint32_t* block_counters;    /* [2 * retrieval_heads], zero before first use; kernels leave it zero */
   float* partial_max;          /* [query_heads][slot_tiles] */
@@ -237,6 +239,11 @@ int ckv_dense_decode(const ckv_kv_cache* kv, int32_t seq_len, float softmax_scal
  * op 0 exp -> f32, 1 log -> f32, 2 fp16 bits -> u16, 3 bf16 bits -> u16,
  * 4 E4M3 code -> u8, 5 E4M3 code (given as float) -> f32. */
 int ckv_host_numerics(int op, const float* in, void* out, int64_t n);
+
+/* Diagnostic (no reference counterpart): the same ops evaluated by the device
+ * functions and gfx950 hardware conversions the kernels use; in/out are device
+ * pointers, asynchronous on `stream`. */
+int ckv_device_numerics(int op, const float* in, void* out, int64_t n, void* stream);
 
 /* Library version and last error message of the calling thread. */
 int ckv_abi_version(void);

@@ -78,7 +78,20 @@ CASES = {
                                    max_decode_tokens=24, aggregation=co.QUERY_GROUP),
                               dict(group_size=4, num_sink=10, token_budget=512, local_window=128,
                                    assignment="nearest_centroid")),
+    # more than 1024 / 2048 scored communities per head (two / eight per thread in the selection kernel)
+    "communities_1500_bf16": (dict(query_heads=8, kv_heads=2, seq_len=16384, communities=1500, num_sink=10,
+                                   max_decode_tokens=8, aggregation=co.QUERY_GROUP),
+                              dict(group_size=4, num_sink=10, token_budget=2048, local_window=128)),
+    "communities_2600_nearest": (dict(query_heads=4, kv_heads=1, seq_len=16384, communities=2600, num_sink=10,
+                                      max_decode_tokens=8, aggregation=co.QUERY_GROUP),
+                                 dict(group_size=4, num_sink=10, token_budget=1024, local_window=64,
+                                      assignment="nearest_centroid")),
+    # few large communities: decode deltas pile up in a few chains of several geometric chunks
+    "deep_delta_chains_bf16": (dict(query_heads=8, kv_heads=2, seq_len=2048, communities=6, num_sink=10,
+                                    max_decode_tokens=40, aggregation=co.QUERY_GROUP),
+                               dict(group_size=4, num_sink=10, token_budget=512, local_window=32)),
 }
+STEPS = {"communities_1500_bf16": 4, "communities_2600_nearest": 4, "deep_delta_chains_bf16": 36}
 
 
 @pytest.mark.parametrize("name", list(CASES))
@@ -90,7 +103,7 @@ def test_decode_steps_match_oracle(device, name):
     dstate = h.to_device(fx, device)
     ws = h.workspace_for(fx, params, device)
     rng = np.random.default_rng(5)
-    steps = 12
+    steps = STEPS.get(name, 12)
     for step in range(steps):
         before = fx.state.copy()
         dstate, ws, out, lse, tks, tkp = _run_step(fx, params, device, dstate, ws)
