@@ -50,6 +50,8 @@ EXPORTED_SYMBOLS = (
     "ckv_segmented_attention",
     "ckv_attention_partials",
     "ckv_decode_layer",
+    "ckv_online_update",
+    "ckv_score_select_after_update",
     "ckv_dense_decode",
     "ckv_prefill_attention_topk",
     "ckv_host_numerics",
@@ -108,6 +110,12 @@ class DecodeWorkspace(ctypes.Structure):
                 ("score_blocks", _i32)]
 
 
+class LayerArgs(ctypes.Structure):
+    _fields_ = [("kv", ctypes.POINTER(KvCache)), ("state", ctypes.POINTER(GraphState)),
+                ("csr", ctypes.POINTER(PrefillCsr)), ("deltas", ctypes.POINTER(DeltaChunks)),
+                ("config", ctypes.POINTER(DecodeConfig)), ("ws", ctypes.POINTER(DecodeWorkspace))]
+
+
 class PrefillArgs(ctypes.Structure):
     _fields_ = [("query", _p), ("key", _p), ("value", _p), ("output", _p), ("lse", _p),
                 ("topk_scores", _p), ("topk_indices", _p), ("q_row_stride", _i64),
@@ -138,12 +146,15 @@ def lib() -> ctypes.CDLL:
         raise RuntimeError(
             f"{LIB_PATH} is not built; run __graft_entry__.build() (hipcc --offload-arch=gfx950)")
     handle = ctypes.CDLL(LIB_PATH)
-    for name in ("ckv_score_select", "ckv_segmented_attention", "ckv_attention_partials", "ckv_decode_layer"):
+    for name in ("ckv_score_select", "ckv_segmented_attention", "ckv_attention_partials", "ckv_decode_layer",
+                 "ckv_online_update"):
         fn = getattr(handle, name)
         fn.argtypes = [ctypes.POINTER(KvCache), ctypes.POINTER(GraphState), ctypes.POINTER(PrefillCsr),
                        ctypes.POINTER(DeltaChunks), ctypes.POINTER(DecodeConfig),
                        ctypes.POINTER(DecodeWorkspace), _p]
         fn.restype = ctypes.c_int
+    handle.ckv_score_select_after_update.argtypes = [ctypes.POINTER(LayerArgs), ctypes.POINTER(LayerArgs), _p]
+    handle.ckv_score_select_after_update.restype = ctypes.c_int
     handle.ckv_dense_decode.argtypes = [ctypes.POINTER(KvCache), _i32, _f32, _p, _p, _p, _p, _p, _p]
     handle.ckv_dense_decode.restype = ctypes.c_int
     if hasattr(handle, "ckv_prefill_attention_topk"):

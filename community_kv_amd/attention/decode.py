@@ -1,11 +1,12 @@
 """Allocation-free decode-layer transition (reference: attention/decode.py:22-111).
 
-``decode_layer`` keeps the reference signature and return value.  Its three
-HIP launches (score+select, attention partials, merge+update) read and mutate
-the caller's fixed-address tensors; the packed C argument structures are cached
-on the workspace and rebuilt only when a tensor address changes, so a step is a
-single ctypes call with no host synchronisation and can be captured in a HIP
-graph.
+``decode_layer`` keeps the reference signature and return value.  Its HIP
+launches (score+select, attention with split merge, online update) read and
+mutate the caller's fixed-address tensors; the packed C argument structures are
+cached on the workspace and rebuilt only when a tensor address changes, so a
+step needs no host synchronisation and can be captured in a HIP graph.
+``DecodeRuntime(defer_updates=True)`` instead runs each layer's online update
+inside the next layer's selection launch (``DecodeCall.score_select_after``).
 """
 
 from __future__ import annotations
@@ -68,7 +69,9 @@ class DecodeLayerWorkspace:
                 _abi.config_struct(self.selection, group_size=self.attention.group_size,
                                    sink_positions=sink_positions, softmax_scale=softmax_scale, lam=lam,
                                    assignment=self.update.assignment),
-                _abi.workspace_struct(self.selection, self.attention, self.update), device)
+                _abi.workspace_struct(self.selection, self.attention, self.update), device,
+                # the packed structures hold raw device addresses: keep every tensor they point to alive
+                keepalive=(query, key, value, csr, state, sink_positions, current_position))
             self._call_key = cache_key
         return self._call
 

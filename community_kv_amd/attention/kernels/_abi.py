@@ -83,7 +83,7 @@ def workspace_struct(selection, attention, update) -> nat.DecodeWorkspace:
 
 @dataclass
 class DecodeCall:
-    """One packed argument set for the three decode entry points."""
+    """One packed argument set for the decode entry points."""
 
     kv: nat.KvCache
     state: nat.GraphState
@@ -110,6 +110,23 @@ class DecodeCall:
 
     def attention_partials(self, stream=None) -> None:
         nat.check(nat.lib().ckv_attention_partials(*self._args(self._stream(stream))))
+
+    def layer_args(self) -> nat.LayerArgs:
+        if getattr(self, "_layer_args", None) is None:
+            self._layer_args = nat.LayerArgs(ctypes.pointer(self.kv), ctypes.pointer(self.state),
+                                             ctypes.pointer(self.csr), ctypes.pointer(self.deltas),
+                                             ctypes.pointer(self.config), ctypes.pointer(self.workspace))
+        return self._layer_args
+
+    def score_select_after(self, pending: "DecodeCall | None", stream=None) -> None:
+        """Selection of this layer plus, in the same launch, the deferred
+        online update of ``pending`` (another layer whose attention has run)."""
+        nat.check(nat.lib().ckv_score_select_after_update(
+            ctypes.byref(self.layer_args()), None if pending is None else ctypes.byref(pending.layer_args()),
+            ctypes.c_void_p(self._stream(stream))))
+
+    def update(self, stream=None) -> None:
+        nat.check(nat.lib().ckv_online_update(*self._args(self._stream(stream))))
 
     def decode(self, stream=None) -> None:
         nat.check(nat.lib().ckv_decode_layer(*self._args(self._stream(stream))))

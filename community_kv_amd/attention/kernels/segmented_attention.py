@@ -93,6 +93,7 @@ def segmented_attention(*, query: torch.Tensor, key: torch.Tensor, value: torch.
                            softmax_scale=softmax_scale, lam=update_lam, assignment=update_workspace.assignment),
         _abi.workspace_struct(selection, workspace, update_workspace), device)
     call.attention()
+    call.update()
     return workspace.output, workspace.lse, workspace.topk_scores, workspace.topk_positions
 
 

@@ -3,6 +3,7 @@
 
 #include "ckv_device.h"
 #include "ckv_error.h"
+#include "ckv_update.h"
 
 namespace ckv {
 
@@ -198,279 +199,22 @@ __device__ inline void merge_head(const DecodeArgs& a, int qh, int tiles, void* 
   }
 }
 
-// Fused online update of the graph owned by retrieval head rh (no-op for
-// non-owners and assignment NONE): exact top-8 merge over the splits'
-// candidates, assignment, running-mean centroid, delta append, overflow.
-// s_lse0 is the merged lse of the head's first query.  Any block size >= 64.
-//
-// Dependent memory rounds: (1) candidates + cursor/count/total, (2) candidate
-// communities + current key row, (3) per-candidate weight/size/delta tail and
-// centroid rows (slot KAPPA holds the community a new token would open, or the
-// nearest centroid), (4) the assigned community's tail-chunk state.
-template <int CT, int DT>
-__device__ void owner_update(const DecodeArgs& a, const int rh, const int tiles, const float s_lse0) {
-  const int tid = threadIdx.x;
-  const int graph = a.st.retrieval_to_graph[rh];
-  if (a.cfg.assignment == CKV_ASSIGN_NONE || rh != graph) return;
-  __syncthreads();
-
-  constexpr int NS = KAPPA + 1;  // candidate slots
-  const int C = a.st.community_capacity;
-  const int64_t tc_cap = a.st.token_capacity < a.kv.capacity ? a.st.token_capacity : a.kv.capacity;
-  const bool delta_q = a.cfg.assignment == CKV_ASSIGN_DELTA_Q;
-  const int kvh = a.st.retrieval_to_kv[rh];
-  __shared__ uint64_t top[KAPPA];
-  __shared__ int s_cur, s_active, s_nearest;
-  __shared__ float s_total;
-  __shared__ int s_pos[NS], s_comm[NS], s_size[NS], s_dsize[NS], s_tail[NS];
-  __shared__ float s_w[NS], s_sc[KAPPA], s_p[KAPPA], s_dw[KAPPA];
-  __shared__ float s_key[D];
-  __shared__ float s_cent[NS][D];
-  __shared__ int s_assigned, s_slot, s_comm_ov;
-
-  // ---- round 1: exact top-8 merge (wave 0); cursor state (wave 1) ----------
-  if (tid < 64 && tiles * KAPPA <= 64) {
-    const int n = tiles * KAPPA;
-    const uint64_t v = wave_sort_desc_u64(tid < n ? a.ws.partial_topk[(int64_t)rh * n + tid] : 0ull);
-    if (tid < KAPPA) top[tid] = v;
-  } else if (tid < 64) {
-    // Each lane keeps a sorted top-8 of its strided share, then 8 rounds of a
-    // wave-wide max over the lanes' heads.
-    const int n = tiles * KAPPA;
-    const uint64_t* cand = a.ws.partial_topk + (int64_t)rh * n;
-    uint64_t loc[KAPPA];
-#pragma unroll
-    for (int k = 0; k < KAPPA; ++k) loc[k] = 0ull;
-    for (int i = tid; i < n; i += 64) {
-      uint64_t v = cand[i];
-#pragma unroll
-      for (int k = 0; k < KAPPA; ++k) {
-        const uint64_t hi = v > loc[k] ? v : loc[k];
-        v = v > loc[k] ? loc[k] : v;
-        loc[k] = hi;
-      }
-    }
-    for (int r = 0; r < KAPPA; ++r) {
-      const uint64_t best = wave_max_u64(loc[0]);
-      if (tid == 0) top[r] = best;
-      if (best != 0ull && loc[0] == best) {
-#pragma unroll
-        for (int k = 0; k < KAPPA - 1; ++k) loc[k] = loc[k + 1];
-        loc[KAPPA - 1] = 0ull;
-      }
-    }
-  }
-  if (tid == 64) {
-    s_cur = a.st.current_position[graph];
-    s_active = a.st.community_counts[rh];
-    s_total = a.st.total_weight[graph];
-    s_nearest = delta_q ? -1 : a.ws.nearest[rh];
-  }
-  __syncthreads();
-  const int cur = s_cur;
-  const int active = s_active;
-  const bool valid_pos = cur >= 0 && cur < tc_cap;
-
-  // ---- round 2: candidate communities; the current key row ----------------
-  if (tid < NS) {
-    int pos = -1, comm = -1;
-    if (tid < KAPPA) {
-      const uint64_t v = top[tid];
-      float sc = NEG_INF;
-      if (v != 0ull) {
-        sc = unordered_f32((uint32_t)(v >> 32));
-        pos = (int)(0xffffffffu - (uint32_t)(v & 0xffffffffu));
-      }
-      s_sc[tid] = sc;
-      a.ws.topk_scores[(int64_t)rh * KAPPA + tid] = sc;
-      a.ws.topk_positions[(int64_t)rh * KAPPA + tid] = pos;
-      if (delta_q && pos >= 0 && pos < tc_cap) comm = a.st.token_communities[(int64_t)graph * a.st.token_capacity + pos];
-    } else {
-      comm = (!delta_q && s_nearest >= 0) ? s_nearest : active;  // community a new token would open
-    }
-    s_pos[tid] = pos;
-    s_comm[tid] = comm;
-  }
-  for (int d = tid; d < D; d += blockDim.x) {
-    s_key[d] = valid_pos ? load_elem<DT>(a.kv.key, kvh * a.kv.head_stride + (int64_t)cur * a.kv.token_stride + d) : 0.0f;
-  }
-  __syncthreads();
-
-  // ---- round 3: per-candidate state and centroid rows ----------------------
-  if (tid < NS) {
-    const int comm = s_comm[tid];
-    const bool ok = comm >= 0 && comm < C;
-    s_w[tid] = (ok && delta_q) ? a.st.community_weight[(int64_t)graph * C + comm] : 0.0f;
-    s_size[tid] = ok ? a.st.community_sizes[(int64_t)rh * C + comm] : 0;
-    s_dsize[tid] = ok ? a.dl.community_sizes[(int64_t)graph * C + comm] : 0;
-    s_tail[tid] = ok ? a.dl.community_tail[(int64_t)graph * C + comm] : -1;
-  }
-  for (int i = tid; i < NS * D; i += blockDim.x) {
-    const int k = i / D, d = i % D;
-    const int comm = s_comm[k];
-    s_cent[k][d] = (comm >= 0 && comm < C) ? load_centroid1<CT>(a.st.centroids, ((int64_t)rh * C + comm) * D + d) : 0.0f;
-  }
-  __syncthreads();
-
-  // ---- assignment (lanes 0..7 of wave 0) ------------------------------------
-  if (tid < 64) {
-    const int r = tid & 7;
-    const int active_c = active < C ? active : C;
-    const bool valid = s_pos[r] >= 0 && s_pos[r] < tc_cap;
-    const int comm = s_comm[r];
-    const bool cand = valid && comm >= 0 && comm < active_c;
-    int assigned, slot;
-    bool comm_ov;
-    if (delta_q) {
-      const float half_lam = a.cfg.lam * 0.5f;
-      const float p = valid ? ckv_expf(s_sc[r] - s_lse0) : 0.0f;
-      const float dw = p * half_lam;
-      if (tid < KAPPA) {
-        s_p[r] = p;
-        s_dw[r] = dw;
-      }
-      wave_sync();
-      // Sequential sums in rank order (reference op order).
-      float nd = 0.0f, ssum = 0.0f, sq = 0.0f, cw = 0.0f;
-      int first = KAPPA;
-#pragma unroll
-      for (int j = 0; j < KAPPA; ++j) {
-        const float pj = s_p[j], dwj = s_dw[j];
-        nd = nd + dwj;
-        ssum = ssum + pj;
-        sq = sq + pj * pj;
-        const int cj = s_comm[j];
-        const bool candj = s_pos[j] >= 0 && s_pos[j] < tc_cap && cj >= 0 && cj < active_c;
-        if (candj && cj == comm) {
-          cw = cw + dwj;
-          first = j < first ? j : first;
-        }
-      }
-      const bool leader = cand && first == r;
-      const float pair = (ssum * ssum - sq) * (0.5f * (1.0f - a.cfg.lam));
-      const float old_total = s_total;
-      float two_m = 2.0f * old_total;
-      two_m = two_m > 1.0f ? two_m : 1.0f;
-      const float oldw = cand ? s_w[r] : 0.0f;
-      const float dq = (cand && cw > 0.0f) ? (cw - (nd * oldw) / two_m) : NEG_INF;
-      float best = dq;  // max over the 8 lanes of this half-row
-      best = fmax_exact(best, ckv_u2f(dpp_u32<0xB1>(ckv_f2u(best))));
-      best = fmax_exact(best, ckv_u2f(dpp_u32<0x4E>(ckv_f2u(best))));
-      best = fmax_exact(best, ckv_u2f(dpp_u32<0x141>(ckv_f2u(best))));
-      int bc = (cand && dq == best) ? comm : 0x7fffffff;
-      bc = min(bc, (int)dpp_u32<0xB1>((uint32_t)bc));
-      bc = min(bc, (int)dpp_u32<0x4E>((uint32_t)bc));
-      bc = min(bc, (int)dpp_u32<0x141>((uint32_t)bc));
-      const bool join = best > 0.0f;
-      assigned = join ? bc : active;
-      comm_ov = assigned >= C;
-      // candidate slot that holds the assigned community's prefetched state
-      const uint64_t hit = __ballot(tid < KAPPA && comm == assigned);
-      slot = join ? (__ffsll((unsigned long long)hit) - 1) : KAPPA;
-      if (!comm_ov && tid < KAPPA) {
-        if (leader) {
-          const float inc = cw + ((join && comm == assigned) ? nd : 0.0f);
-          a.st.community_weight[(int64_t)graph * C + comm] = oldw + inc;
-        }
-        if (tid == 0) {
-          if (!join) a.st.community_weight[(int64_t)graph * C + assigned] = nd;
-          a.st.community_counts[rh] = active + (join ? 0 : 1);
-          a.st.total_weight[graph] = (old_total + nd) + pair;
-        }
-      }
-    } else {
-      const int nearest = s_nearest;
-      assigned = nearest >= 0 ? nearest : active;
-      comm_ov = assigned >= C;
-      slot = KAPPA;
-      if (tid == 0 && nearest < 0 && !comm_ov) a.st.community_counts[rh] = active + 1;
-    }
-    if (tid == 0) {
-      a.ws.assigned[graph] = comm_ov ? -1 : assigned;
-      if (!comm_ov) {
-        a.st.community_sizes[(int64_t)rh * C + assigned] = s_size[slot] + 1;
-        if (valid_pos) a.st.token_communities[(int64_t)graph * a.st.token_capacity + cur] = assigned;
-      }
-      s_assigned = assigned;
-      s_slot = slot;
-      s_comm_ov = comm_ov ? 1 : 0;
-    }
-  }
-  __syncthreads();
-  const int slot = s_slot;
-  const int asg = s_assigned;
-  const bool comm_ov = s_comm_ov != 0;
-  // Running-mean centroid (FP8 satfinite or f32).
-  if (!comm_ov && valid_pos) {
-    const int old_size = s_size[slot];
-    for (int d = tid; d < D; d += blockDim.x) {
-      const float key = s_key[d];
-      const float upd = old_size > 0 ? (s_cent[slot][d] * (float)old_size + key) / (float)(old_size + 1) : key;
-      store_centroid1<CT>(a.st.centroids, ((int64_t)rh * C + asg) * D + d, upd);
-    }
-  }
-  // ---- round 4: decode-delta append ----------------------------------------
-  if (tid == 0) {
-    bool chunk_ov = false, pos_ov = false;
-    if (!comm_ov) {
-      const int64_t tb = (int64_t)graph * C + asg;
-      const int64_t cb = (int64_t)graph * a.dl.chunks_per_graph;
-      const int delta_size = s_dsize[slot];
-      const int old_tail = s_tail[slot];
-      const int old_cs = old_tail >= 0 ? a.dl.chunk_size[cb + old_tail] : 0;
-      const int old_cc = old_tail >= 0 ? a.dl.chunk_capacity[cb + old_tail] : 0;
-      const int old_start = old_tail >= 0 ? a.dl.chunk_start[cb + old_tail] : 0;
-      const int free_chunk = a.dl.next_free_chunk[graph];
-      const int free_pos = a.dl.next_free_position[graph];
-      const bool allocate = old_tail < 0 || old_cs >= old_cc;
-      const int new_cap = old_tail < 0 ? 1 : old_cc * 2;
-      chunk_ov = allocate && free_chunk >= a.dl.chunks_per_graph;
-      pos_ov = allocate && free_pos + new_cap > a.dl.position_capacity;
-      const bool alloc_ov = chunk_ov || pos_ov;
-      const int chunk = allocate ? free_chunk : old_tail;
-      const bool valid_chunk = !alloc_ov && chunk >= 0 && chunk < a.dl.chunks_per_graph;
-      if (allocate && !alloc_ov) {
-        a.dl.next_free_chunk[graph] = free_chunk + 1;
-        a.dl.next_free_position[graph] = free_pos + new_cap;
-        a.dl.chunk_start[cb + free_chunk] = free_pos;
-        a.dl.chunk_capacity[cb + free_chunk] = new_cap;
-        a.dl.chunk_previous[cb + free_chunk] = old_tail;
-        if (old_tail < 0) {
-          a.dl.community_head[tb] = free_chunk;
-        } else {
-          a.dl.chunk_next[cb + old_tail] = free_chunk;
-        }
-        a.dl.community_tail[tb] = free_chunk;
-      }
-      if (valid_chunk && valid_pos) {
-        const int start = allocate ? free_pos : old_start;
-        const int at = allocate ? 0 : old_cs;
-        a.dl.positions[(int64_t)graph * a.dl.position_capacity + start + at] = cur;
-        a.dl.chunk_size[cb + chunk] = at + 1;
-        a.dl.community_sizes[tb] = delta_size + 1;
-      }
-    }
-    const int overflow = (comm_ov ? 1 : 0) | (chunk_ov ? 2 : 0) | (pos_ov ? 4 : 0) | (valid_pos ? 0 : 8);
-    a.ws.overflow[graph] = overflow;
-    if (overflow == 0) a.st.current_position[graph] = cur + 1;
-  }
-}
-
-// Split merge of retrieval head rh's G query heads one at a time, then the
-// owner update.  Any block size >= 64.
-template <int CT, int DT>
-__device__ void merge_update(const DecodeArgs& a, const int rh, const int tiles) {
-  __shared__ float s_lse0;
+// Split merge of retrieval head rh's G query heads, one at a time (f32 path).
+template <int DT>
+__global__ __launch_bounds__(REDUCE_THREADS) void reduce_kernel(DecodeArgs a) {
+  const int rh = blockIdx.x;
+  const int tiles = a.ws.slot_capacity / TILE;
   for (int g = 0; g < a.cfg.group_size; ++g) {
-    merge_head<DT>(a, rh * a.cfg.group_size + g, tiles, a.ws.output, a.ws.lse, g == 0 ? &s_lse0 : nullptr);
+    merge_head<DT>(a, rh * a.cfg.group_size + g, tiles, a.ws.output, a.ws.lse, nullptr);
   }
-  __syncthreads();
-  owner_update<CT, DT>(a, rh, tiles, s_lse0);
 }
 
+// Online update of every owned graph, after the attention merge: reads the
+// splits' top-8 candidates and the merged lse of each head's first query.
 template <int CT, int DT>
-__global__ __launch_bounds__(REDUCE_THREADS) void reduce_update_kernel(DecodeArgs a) {
-  merge_update<CT, DT>(a, blockIdx.x, a.ws.slot_capacity / TILE);
+__global__ __launch_bounds__(256) void update_kernel(DecodeArgs a, int splits) {
+  const int rh = blockIdx.x;
+  owner_update<CT, DT>(a, rh, splits, a.ws.lse[(int64_t)rh * a.cfg.group_size]);
 }
 
 template <int CT, int DT>
@@ -754,9 +498,9 @@ __device__ inline void merge_group(const DecodeArgs& a, const int rh, const int 
 // Sparse bf16 attention: a workgroup of ATT_WAVES waves covers ATT_WAVES
 // consecutive 64-slot tiles of one retrieval head; each wave runs mfma_tile on
 // its tile, the workgroup combines its waves in LDS into one split partial
-// (max, sum, unnormalised P.V per query, top-8 candidates).  With FUSED the
-// last workgroup of a head to finish merges the splits and runs the update.
-template <int CT, bool FUSED>
+// (max, sum, unnormalised P.V per query, top-8 candidates).  With MERGE the
+// last workgroup of a head to finish merges the splits into output and lse.
+template <bool MERGE>
 __global__ __launch_bounds__(64 * ATT_WAVES) void attend_mfma_kernel(DecodeArgs a) {
   // Per-wave V half-tile buffers (8 KB each); reused for the waves' P.V rows
   // and, in the last workgroup, as the split-merge scratch.
@@ -876,8 +620,8 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attend_mfma_kernel(DecodeArgs 
     if (lane < KAPPA) a.ws.partial_topk[((int64_t)rh * splits + wgi) * KAPPA + lane] = cand;
   }
   CKV_STAMP(rh == 0 && wgi == 0, 2);
-  if (!FUSED) return;
-  // The last workgroup of this head to finish merges the splits and runs the update.
+  if (!MERGE) return;
+  // The last workgroup of this head to finish merges the splits.
   __threadfence();
   __syncthreads();
   if (tid == 0) {
@@ -890,10 +634,8 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attend_mfma_kernel(DecodeArgs 
   if (!last_block) return;
   __threadfence();
   CKV_STAMP(rh == 0, 3);
-  merge_group<CKV_BF16>(a, rh, splits, reinterpret_cast<float*>(att_dyn), &s_lse0);
+  merge_group<CKV_BF16>(a, rh, splits, reinterpret_cast<float*>(att_dyn), nullptr);
   CKV_STAMP(rh == 0, 4);
-  owner_update<CT, CKV_BF16>(a, rh, splits, s_lse0);
-  CKV_STAMP(rh == 0, 8);
 }
 
 // Dense bf16 decode baseline: each wave streams `chunk_tiles` consecutive
@@ -954,47 +696,61 @@ __global__ __launch_bounds__(64) void dense_mfma_kernel(DecodeArgs a, int seq_le
 // Launchers
 // ---------------------------------------------------------------------------
 
+// Candidate groups per retrieval head written by the attention kernels.
+int candidate_splits(const DecodeArgs& a) {
+  const int tiles = a.ws.slot_capacity / TILE;
+  return a.kv.dtype == CKV_BF16 ? (tiles + ATT_WAVES - 1) / ATT_WAVES : tiles;
+}
+
 int launch_attention(const DecodeArgs& a, hipStream_t s, bool partials_only) {
   const int tiles = a.ws.slot_capacity / TILE;
-  const dim3 grid(tiles, a.st.retrieval_heads);
-  const bool e4m3 = a.st.centroid_dtype == CKV_E4M3;
-  int r;
   if (a.kv.dtype == CKV_BF16) {
-    const int splits = (tiles + ATT_WAVES - 1) / ATT_WAVES;
-    const dim3 wg_grid(splits, a.st.retrieval_heads);
+    const int splits = candidate_splits(a);
     const size_t lds = (size_t)ATT_WAVES * V_HALF_ROWS * D * sizeof(uint16_t);
     if ((size_t)3 * a.cfg.group_size * splits * sizeof(float) > lds) {
       return ckv_internal::set_error(CKV_E_LIMIT, "too many attention splits for the merge scratch");
     }
-    auto run = [&](auto kernel) {
-      hipLaunchKernelGGL(kernel, wg_grid, dim3(64 * ATT_WAVES), 0, s, a);
-      return launch_check("attend_mfma");
-    };
-    if (partials_only) return run(attend_mfma_kernel<CKV_E4M3, false>);
-    r = e4m3 ? run(attend_mfma_kernel<CKV_E4M3, true>) : run(attend_mfma_kernel<CKV_F32, true>);
-  } else {
-    hipLaunchKernelGGL((attend_generic_kernel<CKV_F32, false>), grid, dim3(64), 0, s, a, 0, 0);
-    r = launch_check("attend");
-    if (r || partials_only) return r;
-    if (e4m3) {
-      hipLaunchKernelGGL((reduce_update_kernel<CKV_E4M3, CKV_F32>), dim3(a.st.retrieval_heads), dim3(REDUCE_THREADS), 0,
-                         s, a);
+    const dim3 grid(splits, a.st.retrieval_heads);
+    if (partials_only) {
+      hipLaunchKernelGGL(attend_mfma_kernel<false>, grid, dim3(64 * ATT_WAVES), 0, s, a);
     } else {
-      hipLaunchKernelGGL((reduce_update_kernel<CKV_F32, CKV_F32>), dim3(a.st.retrieval_heads), dim3(REDUCE_THREADS), 0,
-                         s, a);
+      hipLaunchKernelGGL(attend_mfma_kernel<true>, grid, dim3(64 * ATT_WAVES), 0, s, a);
     }
-    r = launch_check("reduce_update");
+    return launch_check("attend_mfma");
   }
-  if (r) return r;
-  if (a.cfg.assignment != CKV_ASSIGN_NONE && a.st.retrieval_heads != a.st.graph_count) {
-    const dim3 g(a.st.retrieval_heads);
-    if (e4m3 && a.kv.dtype == CKV_BF16) hipLaunchKernelGGL((sync_shared_kernel<CKV_E4M3, CKV_BF16>), g, dim3(REDUCE_THREADS), 0, s, a);
-    else if (e4m3) hipLaunchKernelGGL((sync_shared_kernel<CKV_E4M3, CKV_F32>), g, dim3(REDUCE_THREADS), 0, s, a);
-    else if (a.kv.dtype == CKV_BF16) hipLaunchKernelGGL((sync_shared_kernel<CKV_F32, CKV_BF16>), g, dim3(REDUCE_THREADS), 0, s, a);
-    else hipLaunchKernelGGL((sync_shared_kernel<CKV_F32, CKV_F32>), g, dim3(REDUCE_THREADS), 0, s, a);
-    r = launch_check("sync_shared");
-  }
-  return r;
+  hipLaunchKernelGGL((attend_generic_kernel<CKV_F32, false>), dim3(tiles, a.st.retrieval_heads), dim3(64), 0, s, a, 0,
+                     0);
+  int r = launch_check("attend");
+  if (r || partials_only) return r;
+  hipLaunchKernelGGL(reduce_kernel<CKV_F32>, dim3(a.st.retrieval_heads), dim3(REDUCE_THREADS), 0, s, a);
+  return launch_check("reduce");
+}
+
+int launch_update(const DecodeArgs& a, hipStream_t s) {
+  if (a.cfg.assignment == CKV_ASSIGN_NONE) return CKV_OK;
+  const bool e4m3 = a.st.centroid_dtype == CKV_E4M3;
+  const bool bf16 = a.kv.dtype == CKV_BF16;
+  const int splits = candidate_splits(a);
+  const dim3 g(a.st.retrieval_heads);
+  if (e4m3 && bf16) hipLaunchKernelGGL((update_kernel<CKV_E4M3, CKV_BF16>), g, dim3(256), 0, s, a, splits);
+  else if (e4m3) hipLaunchKernelGGL((update_kernel<CKV_E4M3, CKV_F32>), g, dim3(256), 0, s, a, splits);
+  else if (bf16) hipLaunchKernelGGL((update_kernel<CKV_F32, CKV_BF16>), g, dim3(256), 0, s, a, splits);
+  else hipLaunchKernelGGL((update_kernel<CKV_F32, CKV_F32>), g, dim3(256), 0, s, a, splits);
+  const int r = launch_check("update");
+  return r ? r : launch_sync_shared(a, s);
+}
+
+// Layer-wise aggregation: copy the owner's updated community state to the heads sharing its graph.
+int launch_sync_shared(const DecodeArgs& a, hipStream_t s) {
+  if (a.cfg.assignment == CKV_ASSIGN_NONE || a.st.retrieval_heads == a.st.graph_count) return CKV_OK;
+  const bool e4m3 = a.st.centroid_dtype == CKV_E4M3;
+  const bool bf16 = a.kv.dtype == CKV_BF16;
+  const dim3 g(a.st.retrieval_heads);
+  if (e4m3 && bf16) hipLaunchKernelGGL((sync_shared_kernel<CKV_E4M3, CKV_BF16>), g, dim3(REDUCE_THREADS), 0, s, a);
+  else if (e4m3) hipLaunchKernelGGL((sync_shared_kernel<CKV_E4M3, CKV_F32>), g, dim3(REDUCE_THREADS), 0, s, a);
+  else if (bf16) hipLaunchKernelGGL((sync_shared_kernel<CKV_F32, CKV_BF16>), g, dim3(REDUCE_THREADS), 0, s, a);
+  else hipLaunchKernelGGL((sync_shared_kernel<CKV_F32, CKV_F32>), g, dim3(REDUCE_THREADS), 0, s, a);
+  return launch_check("sync_shared");
 }
 
 int dense_chunks(int seq_len, int chunk_tiles) { return (seq_len + TILE * chunk_tiles - 1) / (TILE * chunk_tiles); }

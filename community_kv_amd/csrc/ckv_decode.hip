@@ -167,8 +167,41 @@ extern "C" int ckv_decode_layer(const ckv_kv_cache* kv, const ckv_graph_state* s
   const ckv::DecodeArgs a = pack(kv, st, csr, dl, cfg, ws);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   rc = ckv::launch_score_select(a, s);
+  if (!rc) rc = ckv::launch_attention(a, s, false);
+  if (!rc) rc = ckv::launch_update(a, s);
+  return rc;
+}
+
+extern "C" int ckv_score_select_after_update(const ckv_layer_args* layer, const ckv_layer_args* pending,
+                                             void* stream) {
+  if (!layer) return fail(CKV_E_INVALID, "null layer arguments");
+  int rc = validate(layer->kv, layer->state, layer->csr, layer->deltas, layer->config, layer->ws);
   if (rc) return rc;
-  return ckv::launch_attention(a, s, false);
+  const ckv::DecodeArgs a = pack(layer->kv, layer->state, layer->csr, layer->deltas, layer->config, layer->ws);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (!pending) return ckv::launch_score_select(a, s);
+  rc = validate(pending->kv, pending->state, pending->csr, pending->deltas, pending->config, pending->ws);
+  if (!rc) rc = validate_attention(pending->state, pending->deltas, pending->config, pending->ws);
+  if (rc) return rc;
+  if (pending->state->centroids == layer->state->centroids || pending->ws->lse == layer->ws->lse)
+    return fail(CKV_E_INVALID, "the pending update must belong to another layer");
+  const ckv::DecodeArgs u =
+      pack(pending->kv, pending->state, pending->csr, pending->deltas, pending->config, pending->ws);
+  if (u.st.centroid_dtype != a.st.centroid_dtype || u.kv.dtype != a.kv.dtype) {
+    rc = ckv::launch_update(u, s);  // different dtypes: a launch of its own, before the selection
+    return rc ? rc : ckv::launch_score_select(a, s);
+  }
+  rc = ckv::launch_score_select(a, s, &u);
+  return rc ? rc : ckv::launch_sync_shared(u, s);
+}
+
+extern "C" int ckv_online_update(const ckv_kv_cache* kv, const ckv_graph_state* st, const ckv_prefill_csr* csr,
+                                 const ckv_delta_chunks* dl, const ckv_decode_config* cfg,
+                                 ckv_decode_workspace* ws, void* stream) {
+  int rc = validate(kv, st, csr, dl, cfg, ws);
+  if (!rc) rc = validate_attention(st, dl, cfg, ws);
+  if (rc) return rc;
+  return ckv::launch_update(pack(kv, st, csr, dl, cfg, ws), reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int ckv_dense_decode(const ckv_kv_cache* kv, int32_t seq_len, float softmax_scale, float* partial_max,

@@ -20,10 +20,12 @@
 // attention/kernels/_csrc/descriptor_selection.cu:164-487 (selection),
 // attention/kernels/segmented_attention.py:98-282 (slot -> position mapping).
 #include <algorithm>
+#include <cstring>
 #include <type_traits>
 
 #include "ckv_device.h"
 #include "ckv_error.h"
+#include "ckv_update.h"
 
 namespace ckv {
 
@@ -85,9 +87,16 @@ __device__ inline void decode_frag(const CentroidFrag<CT>& f, float* out) {
 
 // OWN: communities owned per thread (c = k*1024 + tid, k < OWN), chosen from
 // the scored community count so that the per-community fields stay in registers.
+// Workgroups beyond a.st.retrieval_heads run the pending online update of
+// another layer `u` (same dtypes, disjoint state) on otherwise idle CUs.
 template <int CT, int DT, int OWN>
-__global__ __launch_bounds__(SELECT_THREADS) void select_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(SELECT_THREADS) void select_kernel(DecodeArgs a, DecodeArgs u, int u_splits) {
   constexpr int PB = CT == CKV_E4M3 ? 4 : 2;  // scoring passes whose loads are in flight together
+  if ((int)blockIdx.x >= a.st.retrieval_heads) {
+    const int urh = (int)blockIdx.x - a.st.retrieval_heads;
+    owner_update<CT, DT>(u, urh, u_splits, u.ws.lse[(int64_t)urh * u.cfg.group_size]);
+    return;
+  }
   const int rh = blockIdx.x;
   const int tid = threadIdx.x;
   const int G = a.cfg.group_size;
@@ -593,7 +602,7 @@ size_t select_lds_bytes(int community_capacity, int descriptor_capacity, int max
          (size_t)((max_selected + 63) / 64 + 2) * 4;
 }
 
-int launch_score_select(const DecodeArgs& a, hipStream_t s) {
+int launch_score_select(const DecodeArgs& a, hipStream_t s, const DecodeArgs* pending) {
   const size_t lds = select_lds_bytes(a.st.community_capacity, a.ws.descriptor_capacity, a.cfg.max_selected);
   const int ct = a.st.centroid_dtype, dt = a.kv.dtype;
   const int nscore = std::min(a.st.community_capacity, a.ws.score_blocks * SCORE_BLOCK);
@@ -607,7 +616,15 @@ int launch_score_select(const DecodeArgs& a, hipStream_t s) {
         return limit_error("selection LDS (communities x 2 + descriptors x 28 + selected / 16 bytes) exceeds the device limit");
       }
     }
-    hipLaunchKernelGGL(kernel, dim3(a.st.retrieval_heads), dim3(SELECT_THREADS), lds, s, a);
+    DecodeArgs u;
+    memset(&u, 0, sizeof(u));
+    int extra = 0, u_splits = 0;
+    if (pending != nullptr && pending->cfg.assignment != CKV_ASSIGN_NONE) {
+      u = *pending;
+      extra = pending->st.retrieval_heads;
+      u_splits = candidate_splits(*pending);
+    }
+    hipLaunchKernelGGL(kernel, dim3(a.st.retrieval_heads + extra), dim3(SELECT_THREADS), lds, s, a, u, u_splits);
     return launch_check("select");
   };
   auto by_own = [&](auto k1, auto k2, auto k8) { return own <= 1 ? launch(k1) : own <= 2 ? launch(k2) : launch(k8); };

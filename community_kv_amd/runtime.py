@@ -158,12 +158,19 @@ def convert_prefill_tensors(*, member_offsets: torch.Tensor, member_positions: t
 class DecodeRuntime:
     """Fixed-address collection of prepared layer states."""
 
-    def __init__(self, config: CommunityKVConfig) -> None:
+    def __init__(self, config: CommunityKVConfig, *, defer_updates: bool = False) -> None:
+        """``defer_updates``: run each layer's online update inside the next
+        decode call's selection launch (idle compute units), which takes it off
+        the critical path; ``flush_updates`` runs the last pending one and every
+        reader of the graph state calls it first."""
         self.config = config
         self.layers: dict[int, DecodeLayerState] = {}
+        self.defer_updates = defer_updates
+        self._pending = None  # (layer state, DecodeCall) whose online update has not run yet
 
     def reset(self) -> None:
         self.layers.clear()
+        self._pending = None
 
     def prepare_partitioned_layer(self, state: PartitionedLayer) -> DecodeLayerState:
         return self.prepare_layer(
@@ -219,14 +226,32 @@ class DecodeRuntime:
             raise ValueError("decode requires key/value shape [1, Hkv, S, 128]")
         if key.shape[1] != layer.converted.kv_heads:
             raise ValueError(f"decode expected {layer.converted.kv_heads} KV heads, found {key.shape[1]}")
-        output, *_ = decode_layer(
-            query=query[0, :, 0, :].contiguous(), key=key[0], value=value[0], csr=layer.converted.csr,
-            state=layer.converted.mutable, sink_positions=layer.sink_positions,
-            current_position=layer.converted.current_position, softmax_scale=softmax_scale, lam=self.config.lam,
-            workspace=layer.workspace)
-        return output.view(1, 1, query.shape[1], HEAD_DIM)
+        q = query[0, :, 0, :].contiguous()
+        if not self.defer_updates:
+            output, *_ = decode_layer(
+                query=q, key=key[0], value=value[0], csr=layer.converted.csr, state=layer.converted.mutable,
+                sink_positions=layer.sink_positions, current_position=layer.converted.current_position,
+                softmax_scale=softmax_scale, lam=self.config.lam, workspace=layer.workspace)
+            return output.view(1, 1, query.shape[1], HEAD_DIM)
+        if self._pending is not None and self._pending[0] is layer:
+            self.flush_updates()  # the same layer again: its update must come first
+        call = layer.workspace.call(query=q, key=key[0], value=value[0], csr=layer.converted.csr,
+                                    state=layer.converted.mutable, sink_positions=layer.sink_positions,
+                                    current_position=layer.converted.current_position,
+                                    softmax_scale=softmax_scale, lam=self.config.lam)
+        call.score_select_after(None if self._pending is None else self._pending[1])
+        call.attention()
+        self._pending = (layer, call)
+        return layer.workspace.attention.output.view(1, 1, query.shape[1], HEAD_DIM)
+
+    def flush_updates(self) -> None:
+        """Runs the pending deferred online update, if any (on the current stream)."""
+        if self._pending is not None:
+            self._pending[1].update()
+            self._pending = None
 
     def assert_no_overflow(self) -> None:
+        self.flush_updates()
         failures = {idx: layer.workspace.update.overflow.detach().cpu().tolist()
                     for idx, layer in self.layers.items()
                     if torch.count_nonzero(layer.workspace.update.overflow).item()}
@@ -244,7 +269,7 @@ class CommunityKVRuntime:
         self.config = config
         self.num_layers = num_layers
         self.max_decode_tokens = max_decode_tokens
-        self.decode_runtime = DecodeRuntime(config)
+        self.decode_runtime = DecodeRuntime(config, defer_updates=True)
         self.partition_runtime = PartitionRuntime(algorithm=config, scheduling=partition, max_layers=num_layers,
                                                   label_provider=label_provider)
         self.resolutions: dict[int, float] = {}

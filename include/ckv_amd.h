@@ -14,8 +14,11 @@
  *                           + select_weighted_descriptors()   attention/kernels/_csrc/bindings.cpp:3-21,
  *                                                             attention/kernels/_csrc/descriptor_selection.cu:852-1189
  *   ckv_segmented_attention triton_segmented_attention()      attention/kernels/segmented_attention.py:1016-1273
- *                           (partials kernel 31-365, fused reduce+update kernel 368-864,
- *                            shared-graph centroid sync 867-950)
+ *                           (partials kernel 31-365, split reduce of the fused reduce+update
+ *                            kernel 368-864)
+ *   ckv_online_update       the update half of that fused kernel (segmented_attention.py:368-864,
+ *                           launched at 1164-1273) and the shared-graph centroid sync 867-950;
+ *                           a separate entry point so that callers can run it on another stream
  *   ckv_decode_layer        decode_layer()                    attention/decode.py:67-111
  *   ckv_dense_decode        (baseline only) dense bf16 decode over the whole cache, the
  *                           FlashAttention decode the reference compares against (paper Table 5)
@@ -207,8 +210,8 @@ int ckv_score_select(const ckv_kv_cache* kv, const ckv_graph_state* state,
                      const ckv_decode_config* config, ckv_decode_workspace* ws,
                      void* stream);
 
-/* Exact online-softmax attention over the slots chosen by ckv_score_select,
- * then (assignment != NONE) the fused online update of the graph state. */
+/* Exact online-softmax attention over the slots chosen by ckv_score_select:
+ * split partials, top-8 candidates per split, and the merged output and lse. */
 int ckv_segmented_attention(const ckv_kv_cache* kv, const ckv_graph_state* state,
                             const ckv_prefill_csr* csr, const ckv_delta_chunks* deltas,
                             const ckv_decode_config* config, ckv_decode_workspace* ws,
@@ -221,7 +224,38 @@ int ckv_attention_partials(const ckv_kv_cache* kv, const ckv_graph_state* state,
                            const ckv_decode_config* config, ckv_decode_workspace* ws,
                            void* stream);
 
-/* ckv_score_select followed by ckv_segmented_attention. */
+/* Online update after ckv_segmented_attention (no-op for CKV_ASSIGN_NONE):
+ * exact top-8 merge of the splits' candidates, delta-Q or nearest-centroid
+ * assignment, running-mean FP8 centroid, decode-delta append, overflow flags,
+ * and the layer-wise shared-graph sync.  It may run on a different stream
+ * than the next layer's work; it must complete before this layer's next
+ * ckv_score_select. */
+int ckv_online_update(const ckv_kv_cache* kv, const ckv_graph_state* state,
+                      const ckv_prefill_csr* csr, const ckv_delta_chunks* deltas,
+                      const ckv_decode_config* config, ckv_decode_workspace* ws,
+                      void* stream);
+
+/* The six argument blocks of one layer's decode call. */
+typedef struct ckv_layer_args {
+  const ckv_kv_cache* kv;
+  const ckv_graph_state* state;
+  const ckv_prefill_csr* csr;
+  const ckv_delta_chunks* deltas;
+  const ckv_decode_config* config;
+  ckv_decode_workspace* ws;
+} ckv_layer_args;
+
+/* Scheduling variant, no counterpart in the reference (whose update is fused
+ * into its attention kernel): ckv_score_select of `layer` and, in the same
+ * launch on otherwise idle compute units, the deferred ckv_online_update of
+ * another layer `pending` (null: none), whose ckv_segmented_attention has
+ * already run on this stream.  The two layers' state must be disjoint.  A
+ * runtime that defers each layer's update to the next layer's selection takes
+ * the update off the decode critical path; it flushes the last one with
+ * ckv_online_update. */
+int ckv_score_select_after_update(const ckv_layer_args* layer, const ckv_layer_args* pending, void* stream);
+
+/* ckv_score_select, ckv_segmented_attention and ckv_online_update on one stream. */
 int ckv_decode_layer(const ckv_kv_cache* kv, const ckv_graph_state* state,
                      const ckv_prefill_csr* csr, const ckv_delta_chunks* deltas,
                      const ckv_decode_config* config, ckv_decode_workspace* ws,
