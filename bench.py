@@ -9,7 +9,10 @@ Each layer owns its own KV cache and graph state (4.8 GB in total), so no layer
 finds another's data in the 256 MB Infinity Cache.  The whole step is captured
 in one HIP graph; inputs are resident in HBM before timing starts.
 
-Prints one JSON line (see DESIGN.md for the fields).
+Prints one JSON line: the benchmark contract's fields plus `roofline`
+(attention kernel: algorithmic bytes per launch over its graph-timed duration;
+`traffic` from the committed rocprofv3 counter summary when present) and
+`cpu_baseline` (the numpy oracle on one layer, one core).
 """
 
 from __future__ import annotations
@@ -140,6 +143,20 @@ def algorithmic_bytes(stack):
     return float(np.mean(att)), float(np.mean(step)), float(np.mean([int((e["layer"].workspace.selection.slot_positions >= 0).sum()) / HKV for e in stack]))
 
 
+def profiled_traffic():
+    """HBM bytes per attention launch from the committed rocprofv3 counter
+    summary (FETCH_SIZE + WRITE_SIZE per dispatch, scaled by a plain copy of
+    known size), or None when that summary is absent."""
+    path = os.path.join(ROOT, "profiles", "attend_mfma_config2_traffic.txt")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        for line in f:
+            if line.startswith("traffic_bytes_per_launch:"):
+                return float(line.split(":", 1)[1])
+    return None
+
+
 def cpu_baseline(entry, seconds=20.0):
     """Oracle decode step (numpy port of the reference semantics) on one layer's
     state, single-threaded, for a bounded number of steps."""
@@ -186,6 +203,8 @@ def main():
     ap.add_argument("--layers", type=int, default=LAYERS)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="after timing, one plain 256 MiB device-to-device copy (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1"}))
@@ -218,10 +237,14 @@ def main():
     att_bytes, step_bytes, tokens_per_head = algorithmic_bytes(stack)
     overflow = sum(int(e["layer"].workspace.update.overflow.sum().item()) for e in stack)
 
-    # dominant kernel alone: split-partials attention, 36 launches per replay
+    # the attention kernel as the step runs it (split partials + last-workgroup
+    # merge), 36 launches per replay over the slots of the last step
+    att_graph = capture(lambda: [e["call"].attention() for e in stack], device)
+    att_graph.replay()
+    att_ms = time_graph(att_graph, max(10, args.steps), device) / len(stack)
     part_graph = capture(lambda: [e["call"].attention_partials() for e in stack], device)
     part_graph.replay()
-    att_ms = time_graph(part_graph, max(10, args.steps), device) / len(stack)
+    part_ms = time_graph(part_graph, max(10, args.steps), device) / len(stack)
 
     # dense bf16 decode over the same 32k caches (baseline)
     tiles = -(-SEQ // 64)
@@ -263,18 +286,24 @@ def main():
                    "layers": len(stack), "query_heads": HQ, "kv_heads": HKV, "head_dim": D, "context": SEQ,
                    "token_budget": BUDGET, "local_window": WINDOW, "num_sink": SINKS},
         "us_per_step_layer": us_layer,
-        "us_per_step_layer_single_stream": serial_ms * 1e3 / len(stack),
+        "us_per_step_layer_update_inline": serial_ms * 1e3 / len(stack),
         "dense_us_per_step_layer": dense_us_layer,
         "speedup_vs_dense": dense_us_layer / us_layer,
         "attention_kernel_us": att_ms * 1e3,
+        "attention_partials_kernel_us": part_ms * 1e3,
         "attended_tokens_per_head": tokens_per_head,
         "step_algorithmic_bytes_per_layer": step_bytes,
         "step_hbm_frac": step_bytes / (us_layer * 1e-6) / 1e9 / HBM_PEAK_GBS,
         "overflow_flags": overflow,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
-                     "kernel": "attend (split partials)", "bytes_per_launch": att_bytes},
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": profiled_traffic(),
+                     "kernel": "attend_mfma_kernel<true> (split partials + merge)", "bytes_per_launch": att_bytes},
     }
+    if args.copy_probe:
+        src = torch.empty(64 << 20, dtype=torch.int32, device=device)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize(device)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(stack[0], args.cpu_seconds)
     print(json.dumps(result), flush=True)
