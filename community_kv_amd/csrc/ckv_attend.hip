@@ -420,10 +420,13 @@ __device__ inline TileResult mfma_tile(const uint16_t* __restrict__ K, const uin
 constexpr int ATT_WAVES = 4;  // 64-slot tiles per attention workgroup
 
 // Split merge of all G query heads of retrieval head rh at once (any block
-// size); `scratch` holds 3 * G * splits floats.
+// size); `scratch` holds 3 * G * splits floats.  When every thread has at most
+// two (query, dim) pairs and there are at most 16 splits, the accumulators are
+// loaded in the same round as the maxima and sums.
 template <int DT>
 __device__ inline void merge_group(const DecodeArgs& a, const int rh, const int splits, float* scratch,
                                    float* lse0_out) {
+  constexpr int PRE = 16;
   const int tid = threadIdx.x;
   const int nt = blockDim.x;
   const int G = a.cfg.group_size;
@@ -433,6 +436,21 @@ __device__ inline void merge_group(const DecodeArgs& a, const int rh, const int 
   float* sc_s = scratch + 2 * n;
   __shared__ float gm_s[CKV_MAX_GROUP], gden_s[CKV_MAX_GROUP];
   const int64_t base = (int64_t)rh * G * splits;  // partial_max/sum rows of this head group
+  const float* acc_base = a.ws.partial_acc + base * D;
+  const bool fast = G * D <= 2 * nt && splits <= PRE;
+  float v0[PRE], v1[PRE];
+  const int i0 = tid, i1 = tid + nt;
+  if (fast) {
+    const int p0 = min(i0, G * D - 1), p1 = min(i1, G * D - 1);
+    const float* s0 = acc_base + (int64_t)(p0 >> 7) * splits * D + (p0 & (D - 1));
+    const float* s1 = acc_base + (int64_t)(p1 >> 7) * splits * D + (p1 & (D - 1));
+#pragma unroll
+    for (int k = 0; k < PRE; ++k) {
+      const int kk = min(k, splits - 1);
+      v0[k] = gload_f32(s0 + (int64_t)kk * D);
+      v1[k] = gload_f32(s1 + (int64_t)kk * D);
+    }
+  }
   for (int i = tid; i < n; i += nt) {
     m_s[i] = a.ws.partial_max[base + i];
     l_s[i] = a.ws.partial_sum[base + i];
@@ -461,35 +479,48 @@ __device__ inline void merge_group(const DecodeArgs& a, const int rh, const int 
     if (tid == 0 && lse0_out) *lse0_out = lse;
   }
   __syncthreads();
-  const float* acc_base = a.ws.partial_acc + base * D;
-  for (int i = tid; i < G * D; i += nt) {
-    const int g = i >> 7;
-    const int d = i & (D - 1);
-    const float* src = acc_base + (int64_t)g * splits * D + d;
-    const float* scg = sc_s + g * splits;
-    float acc = 0.0f;
-    int t = 0;
-    for (; t + 16 <= splits; t += 16) {
-      float v[16];
-#pragma unroll
-      for (int k = 0; k < 16; ++k) v[k] = src[(int64_t)(t + k) * D];
-#pragma unroll
-      for (int k = 0; k < 16; ++k) acc = acc + (scg[t + k] != 0.0f ? v[k] * scg[t + k] : 0.0f);
-    }
-    {
-      float v[16];
-#pragma unroll
-      for (int k = 0; k < 16; ++k) v[k] = t + k < splits ? src[(int64_t)(t + k) * D] : 0.0f;
-#pragma unroll
-      for (int k = 0; k < 16; ++k) {
-        if (t + k < splits) acc = acc + (scg[t + k] != 0.0f ? v[k] * scg[t + k] : 0.0f);
-      }
-    }
-    const float r = acc / gden_s[g];
+  auto store = [&](int g, int d, float r) {
     if constexpr (DT == CKV_BF16) {
       reinterpret_cast<uint16_t*>(a.ws.output)[((int64_t)rh * G + g) * D + d] = ckv_f32_to_bf16_bits(r);
     } else {
       reinterpret_cast<float*>(a.ws.output)[((int64_t)rh * G + g) * D + d] = r;
+    }
+  };
+  if (fast) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int i = h == 0 ? i0 : i1;
+      if (i < G * D) {
+        const int g = i >> 7;
+        const float* scg = sc_s + g * splits;
+        float acc = 0.0f;
+#pragma unroll
+        for (int k = 0; k < PRE; ++k) {
+          if (k < splits) acc = acc + (scg[k] != 0.0f ? (h == 0 ? v0[k] : v1[k]) * scg[k] : 0.0f);
+        }
+        store(g, i & (D - 1), acc / gden_s[g]);
+      }
+    }
+  } else {
+    for (int i = tid; i < G * D; i += nt) {
+      const int g = i >> 7;
+      const int d = i & (D - 1);
+      const float* src = acc_base + (int64_t)g * splits * D + d;
+      const float* scg = sc_s + g * splits;
+      float acc = 0.0f;
+      int t = 0;
+      for (; t + 16 <= splits; t += 16) {
+        float v[16];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) v[k] = src[(int64_t)(t + k) * D];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) acc = acc + (scg[t + k] != 0.0f ? v[k] * scg[t + k] : 0.0f);
+      }
+      for (; t < splits; ++t) {
+        const float v = src[(int64_t)t * D];
+        acc = acc + (scg[t] != 0.0f ? v * scg[t] : 0.0f);
+      }
+      store(g, d, acc / gden_s[g]);
     }
   }
   __syncthreads();

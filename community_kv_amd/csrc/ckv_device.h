@@ -28,7 +28,7 @@ constexpr int D = CKV_HEAD_DIM;
 constexpr int TILE = CKV_TILE;
 constexpr int KAPPA = CKV_KAPPA;
 constexpr int SCORE_BLOCK = CKV_SCORE_BLOCK;
-constexpr int SELECT_THREADS = 1024;  // one selection workgroup per retrieval head
+constexpr int SELECT_THREADS = 512;  // one selection workgroup per retrieval head
 constexpr int REDUCE_THREADS = 128;
 constexpr float NEG_INF = -__builtin_huge_valf();
 
@@ -273,6 +273,28 @@ __device__ inline uint64_t wave_reduce_u64(uint64_t v) {
 }
 
 __device__ inline uint64_t wave_max_u64(uint64_t v) { return wave_reduce_u64<true>(v); }
+// Wave-wide OR of a 64-bit value, result on every lane.
+__device__ inline uint64_t wave_or_u64(uint64_t v) {
+  v |= dpp_u64<0xB1>(v);
+  v |= dpp_u64<0x4E>(v);
+  v |= dpp_u64<0x141>(v);
+  v |= dpp_u64<0x140>(v);
+  {
+    const uint32_t lo = (uint32_t)(v & 0xffffffffu), hi = (uint32_t)(v >> 32);
+    const auto rl = __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+    const auto rh = __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+    v = (((uint64_t)(uint32_t)rh[0] << 32) | (uint32_t)rl[0]) | (((uint64_t)(uint32_t)rh[1] << 32) | (uint32_t)rl[1]);
+  }
+  {
+    const uint32_t lo = (uint32_t)(v & 0xffffffffu), hi = (uint32_t)(v >> 32);
+    const auto rl = __builtin_amdgcn_permlane32_swap(lo, lo, false, false);
+    const auto rh = __builtin_amdgcn_permlane32_swap(hi, hi, false, false);
+    v = (((uint64_t)(uint32_t)rh[0] << 32) | (uint32_t)rl[0]) | (((uint64_t)(uint32_t)rh[1] << 32) | (uint32_t)rl[1]);
+  }
+  return v;
+}
+
+
 __device__ inline uint64_t wave_min_u64(uint64_t v) { return wave_reduce_u64<false>(v); }
 
 template <int X>
@@ -287,7 +309,8 @@ __device__ inline uint64_t bitonic_stage(uint64_t v, int lane) {
   const bool ascending_block = (lane & K) == 0;  // blocks of the final descending order alternate
   const bool lower = (lane & J) == 0;
   const bool keep_max = ascending_block == lower;
-  v = keep_max ? (other > v ? other : v) : (other < v ? other : v);
+  // keep_max lanes take the larger key, the others the smaller (equal keys: either)
+  v = ((other > v) == keep_max) ? other : v;
   if constexpr (J > 1) {
     return bitonic_stage<K, J / 2>(v, lane);
   } else {

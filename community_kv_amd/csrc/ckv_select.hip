@@ -1,6 +1,6 @@
 // Centroid scoring + exact community selection + slot materialisation.
 //
-// select_kernel: one 1024-thread workgroup per retrieval head.  Every decode
+// select_kernel: one 512-thread workgroup per retrieval head.  Every decode
 // layer-step is a chain of dependent memory round trips, so the kernel is laid
 // out to need as few of them as possible:
 //   R0  head mapping, query group, centroid rows, community sizes, sinks
@@ -37,7 +37,7 @@ __device__ unsigned long long phase_stamp[32];
 int limit_error(const char* message) { return ckv_internal::set_error(CKV_E_LIMIT, message); }
 
 constexpr int ROWS_PER_PASS = SELECT_THREADS / 8;          // centroid rows scored per pass
-constexpr int MAT_BATCH = 4;                               // slots per thread gathered together
+constexpr int MAT_BATCH = 4;                               // 64-slot blocks per wave gathered together
 constexpr int DESC_ARRAYS = 7;                             // per-descriptor LDS arrays
 }  // namespace
 
@@ -85,13 +85,16 @@ __device__ inline void decode_frag(const CentroidFrag<CT>& f, float* out) {
   }
 }
 
-// OWN: communities owned per thread (c = k*1024 + tid, k < OWN), chosen from
-// the scored community count so that the per-community fields stay in registers.
-// Workgroups beyond a.st.retrieval_heads run the pending online update of
-// another layer `u` (same dtypes, disjoint state) on otherwise idle CUs.
+// OWN: communities owned per thread (thread t owns [t*OWN, (t+1)*OWN), so id
+// order is thread order then k order), chosen from the scored community count
+// so that the per-community fields stay in registers.  Workgroups beyond
+// a.st.retrieval_heads run the pending online update of another layer `u`
+// (same dtypes, disjoint state) on otherwise idle CUs.
 template <int CT, int DT, int OWN>
 __global__ __launch_bounds__(SELECT_THREADS) void select_kernel(DecodeArgs a, DecodeArgs u, int u_splits) {
   constexpr int PB = CT == CKV_E4M3 ? 4 : 2;  // scoring passes whose loads are in flight together
+  constexpr int WAVES = SELECT_THREADS / 64;
+  constexpr int WIN_PER_THREAD = (CKV_MAX_WINDOW + SELECT_THREADS - 1) / SELECT_THREADS;
   if ((int)blockIdx.x >= a.st.retrieval_heads) {
     const int urh = (int)blockIdx.x - a.st.retrieval_heads;
     owner_update<CT, DT>(u, urh, u_splits, u.ws.lse[(int64_t)urh * u.cfg.group_size]);
@@ -105,17 +108,17 @@ __global__ __launch_bounds__(SELECT_THREADS) void select_kernel(DecodeArgs a, De
   const bool nearest_mode = a.cfg.assignment == CKV_ASSIGN_NEAREST;
   const bool materialise = a.csr.member_offsets != nullptr;
   const int ns = a.cfg.num_sink;
+  const int W = a.cfg.local_window;
   const int cpg = a.dl.chunks_per_graph;
   CKV_STAMP(rh == 0, 0);
 
   __shared__ float q_s[CKV_MAX_GROUP * D];
   __shared__ float key_s[D];
   __shared__ int hist[256];
-  __shared__ int scan_s[2 * (SELECT_THREADS / 64)];
-  __shared__ uint64_t near_s[SELECT_THREADS / 64];
+  __shared__ __align__(16) int scan_s[4 * WAVES];
+  __shared__ uint64_t near_s[WAVES];
   __shared__ int sink_s[CKV_MAX_SINKS];
-  __shared__ int win_s[CKV_MAX_WINDOW];
-  __shared__ int s_bin, s_above, s_desc_count, s_sel_count, s_last_sel_pos, s_last_size;
+  __shared__ int s_bin, s_above, s_max_idx, s_sel_count, s_last_sel_pos, s_last_size, s_sink_max;
 
   extern __shared__ __align__(16) unsigned char dyn[];
   uint16_t* key16 = reinterpret_cast<uint16_t*>(dyn);  // masked fp16 score bits of every scored community
@@ -154,27 +157,27 @@ __global__ __launch_bounds__(SELECT_THREADS) void select_kernel(DecodeArgs a, De
     }
   };
   load_batch(0);
-  // Query group: two elements per thread (G * 128 <= 2048).
-  const int qe = min(2 * tid, G * D - 2);
-  float q0, q1;
-  if constexpr (DT == CKV_BF16) {
-    const uint32_t w = (uint32_t)gload_i32(reinterpret_cast<const int32_t*>(
-        reinterpret_cast<const uint16_t*>(a.kv.query) + (int64_t)rh * G * D + qe));
-    q0 = ckv_u2f(w << 16);
-    q1 = ckv_u2f(w & 0xffff0000u);
-  } else {
-    const float* qp = reinterpret_cast<const float*>(a.kv.query) + (int64_t)rh * G * D + qe;
-    q0 = gload_f32(qp);
-    q1 = gload_f32(qp + 1);
+  // Query group: two elements per thread (G * 128 <= 2048 <= 4 * threads).
+  float qv[4];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int qe = min(2 * (tid + h * SELECT_THREADS), G * D - 2);
+    if constexpr (DT == CKV_BF16) {
+      const uint32_t w = (uint32_t)gload_i32(reinterpret_cast<const int32_t*>(
+          reinterpret_cast<const uint16_t*>(a.kv.query) + (int64_t)rh * G * D + qe));
+      qv[2 * h] = ckv_u2f(w << 16);
+      qv[2 * h + 1] = ckv_u2f(w & 0xffff0000u);
+    } else {
+      const float* qp = reinterpret_cast<const float*>(a.kv.query) + (int64_t)rh * G * D + qe;
+      qv[2 * h] = gload_f32(qp);
+      qv[2 * h + 1] = gload_f32(qp + 1);
+    }
   }
   const int sink_v = (materialise && ns > 0) ? gload_i32(a.cfg.sink_positions + min(tid, ns - 1)) : -1;
-  const int orounds = (nscore + SELECT_THREADS - 1) / SELECT_THREADS;
+  const int c0 = tid * OWN;  // first owned community
   int o_size[OWN];
 #pragma unroll
-  for (int k = 0; k < OWN; ++k) {
-    const int c = min(k * SELECT_THREADS + tid, nscore - 1);
-    o_size[k] = gload_i32(a.st.community_sizes + (int64_t)rh * C + c);
-  }
+  for (int k = 0; k < OWN; ++k) o_size[k] = gload_i32(a.st.community_sizes + (int64_t)rh * C + min(c0 + k, nscore - 1));
 
   // ---- R1 -------------------------------------------------------------------
   const int cur = a.st.current_position[graph];
@@ -192,7 +195,7 @@ __global__ __launch_bounds__(SELECT_THREADS) void select_kernel(DecodeArgs a, De
   if (materialise) {
 #pragma unroll
     for (int k = 0; k < OWN; ++k) {
-      const int c = min(k * SELECT_THREADS + tid, C - 1);
+      const int c = min(c0 + k, C - 1);
       o_lo[k] = gload_i32(a.csr.member_offsets + (int64_t)graph * (C + 1) + c);
       o_dc[k] = gload_i32(a.dl.community_sizes + tbl + c);
       o_tl[k] = gload_i32(a.dl.community_tail + tbl + c);
@@ -204,70 +207,115 @@ __global__ __launch_bounds__(SELECT_THREADS) void select_kernel(DecodeArgs a, De
     key_v = load_elem<DT>(a.kv.key, kvh * a.kv.head_stride + cp * a.kv.token_stride + (tid & (D - 1)));
   }
 
-  // ---- R2 -------------------------------------------------------------------
-  if (materialise && cpg > 0) {
+  // ---- R2: tail-chunk fields; communities of the window tokens ---------------
+  int wcomm[WIN_PER_THREAD];
 #pragma unroll
-    for (int k = 0; k < OWN; ++k) {
-      const int t = min(max(o_tl[k], 0), cpg - 1);
-      o_ts[k] = gload_i32(a.dl.chunk_start + cb + t);
-      o_tn[k] = gload_i32(a.dl.chunk_size + cb + t);
+  for (int h = 0; h < WIN_PER_THREAD; ++h) wcomm[h] = -1;
+  if (materialise) {
+    if (cpg > 0) {
+#pragma unroll
+      for (int k = 0; k < OWN; ++k) {
+        const int t = min(max(o_tl[k], 0), cpg - 1);
+        o_ts[k] = gload_i32(a.dl.chunk_start + cb + t);
+        o_tn[k] = gload_i32(a.dl.chunk_size + cb + t);
+      }
+    }
+    if (W > 0) {
+      const int32_t* tcomm = a.st.token_communities + (int64_t)graph * a.st.token_capacity;
+#pragma unroll
+      for (int h = 0; h < WIN_PER_THREAD; ++h) {
+        const int64_t p = (int64_t)cur - W + tid + h * SELECT_THREADS;
+        wcomm[h] = gload_i32(tcomm + (p < 0 ? 0 : (p >= a.st.token_capacity ? a.st.token_capacity - 1 : p)));
+      }
     }
   }
-  // masks (after the loads were issued)
+  // masks of the R0/R1 fields (R2 fields stay raw until used: masking them here would wait for R2)
 #pragma unroll
   for (int k = 0; k < OWN; ++k) {
-    const int c = k * SELECT_THREADS + tid;
-    const bool own = k < orounds && c < count;
-    if (!(k < orounds && c < nscore)) o_size[k] = 0;
-    if (!own) {
+    const int c = c0 + k;
+    if (c >= nscore) o_size[k] = 0;
+    if (c >= count) {
       o_lo[k] = 0;
       o_dc[k] = 0;
       o_tl[k] = -1;
     }
-  }  // (tail-chunk fields stay raw until a descriptor is stored: masking them here would wait for R2)
-  if (2 * tid < G * D) {
-    q_s[2 * tid] = q0;
-    q_s[2 * tid + 1] = q1;
+  }
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int e = 2 * (tid + h * SELECT_THREADS);
+    if (e < G * D) {
+      q_s[e] = qv[2 * h];
+      q_s[e + 1] = qv[2 * h + 1];
+    }
   }
   if (tid < ns) sink_s[tid] = sink_v;
   if (tid < D) key_s[tid] = (cur >= 0 && cur < a.kv.capacity) ? key_v : 0.0f;
   hist[tid & 255] = 0;
+  if (tid == 0) s_max_idx = -1;
   __syncthreads();  // q_s, key_s, sink_s, hist
   CKV_STAMP(rh == 0, 6);
+  if (tid < 64) {  // largest sink position: window tokens beyond it skip the sink test
+    int m = -1;
+    for (int i = tid; i < ns; i += 64) m = max(m, sink_s[i]);
+    m = max(m, (int)dpp_u32<0xB1>((uint32_t)m));
+    m = max(m, (int)dpp_u32<0x4E>((uint32_t)m));
+    m = max(m, (int)dpp_u32<0x141>((uint32_t)m));
+    m = max(m, (int)dpp_u32<0x140>((uint32_t)m));
+    m = max(m, __builtin_amdgcn_readlane(m, 0));
+    m = max(max(m, __builtin_amdgcn_readlane(m, 16)), max(__builtin_amdgcn_readlane(m, 32), __builtin_amdgcn_readlane(m, 48)));
+    if (tid == 0) s_sink_max = m;
+  }
 
   // ---- scoring ----------------------------------------------------------------
   uint64_t best_nearest = ~0ull;
   auto score_batch = [&](int p0) {
+    // Queries two at a time, held in registers across the batch's passes (one
+    // LDS read of each query slice per batch); q_s rows beyond G are read but
+    // never selected into `best`.  Pinned order per (row, query) as above.
+    float best[PB];
+#pragma unroll
+    for (int pb = 0; pb < PB; ++pb) best[pb] = NEG_INF;
+#pragma unroll 1
+    for (int g = 0; g < G; g += 2) {
+      float qa[16], qb[16];
+      {
+        const float4* pa = reinterpret_cast<const float4*>(q_s + g * D + 16 * lane8);
+        const float4* pq = reinterpret_cast<const float4*>(q_s + (g + 1) * D + 16 * lane8);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float4 x = pa[i], y = pq[i];
+          qa[4 * i] = x.x; qa[4 * i + 1] = x.y; qa[4 * i + 2] = x.z; qa[4 * i + 3] = x.w;
+          qb[4 * i] = y.x; qb[4 * i + 1] = y.y; qb[4 * i + 2] = y.z; qb[4 * i + 3] = y.w;
+        }
+      }
+#pragma unroll
+      for (int pb = 0; pb < PB; ++pb) {
+        float cv[16];
+        decode_frag<CT>(frag[pb], cv);
+        float a0 = qa[0] * cv[0], a1 = qb[0] * cv[0];
+#pragma unroll
+        for (int i = 1; i < 16; ++i) {
+          a0 = a0 + qa[i] * cv[i];
+          a1 = a1 + qb[i] * cv[i];
+        }
+        a0 = a0 + xor_f32<4>(a0);
+        a1 = a1 + xor_f32<4>(a1);
+        a0 = a0 + xor_f32<2>(a0);
+        a1 = a1 + xor_f32<2>(a1);
+        a0 = a0 + xor_f32<1>(a0);
+        a1 = a1 + xor_f32<1>(a1);
+        best[pb] = fmax_exact(best[pb], a0);
+        if (g + 1 < G) best[pb] = fmax_exact(best[pb], a1);
+      }
+    }
 #pragma unroll
     for (int pb = 0; pb < PB; ++pb) {
       const int c = (p0 + pb) * ROWS_PER_PASS + sub;
-      float cv[16];
-      decode_frag<CT>(frag[pb], cv);
-      // Four queries per step as independent chains (q_s rows beyond G are
-      // never selected into `best`); pinned order per query as documented above.
-      float best = NEG_INF;
-#pragma unroll 1
-      for (int g = 0; g < G; g += 4) {
-        const float* q = q_s + g * D + 16 * lane8;
-        float acc[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) acc[u] = q[u * D] * cv[0];
-#pragma unroll
-        for (int i = 1; i < 16; ++i) {
-#pragma unroll
-          for (int u = 0; u < 4; ++u) acc[u] = acc[u] + q[u * D + i] * cv[i];
-        }
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          acc[u] = acc[u] + xor_f32<4>(acc[u]);
-          acc[u] = acc[u] + xor_f32<2>(acc[u]);
-          acc[u] = acc[u] + xor_f32<1>(acc[u]);
-          if (g + u < G) best = fmax_exact(best, acc[u]);
-        }
-      }
       const bool live = c < count && rsize[pb] > 0;
-      if (lane8 == 0 && c < nscore) key16[c] = f16_bits_hw(live ? best : NEG_INF);
+      if (lane8 == 0 && c < nscore) key16[c] = f16_bits_hw(live ? best[pb] : NEG_INF);
       if (nearest_mode) {
+        float cv[16];
+        decode_frag<CT>(frag[pb], cv);
         float acc;
         {
           const float d0 = key_s[16 * lane8] - cv[0];
@@ -308,17 +356,19 @@ __global__ __launch_bounds__(SELECT_THREADS) void select_kernel(DecodeArgs a, De
   uint32_t o_key[OWN];
 #pragma unroll
   for (int k = 0; k < OWN; ++k) {
-    const int c = k * SELECT_THREADS + tid;
-    const bool live = k < orounds && c < count && o_size[k] > 0;
+    const int c = c0 + k;
+    const bool live = c < count && o_size[k] > 0;
     o_key[k] = live ? ckv_ordered_key16(key16[c]) : 0u;
     if (live) atomicAdd(hist + (o_key[k] >> 8), budget_mode ? o_size[k] : 1);
   }
   __syncthreads();
+  CKV_STAMP(rh == 0, 12);
   // key16 is dead from here on; it becomes the community -> descriptor table.
   uint16_t* comm_desc = key16;
   for (int c = tid; c < nscore; c += SELECT_THREADS) comm_desc[c] = 0xffffu;
   if (tid < 64) find_threshold_bin(hist, target, &s_bin, &s_above);
   __syncthreads();
+  CKV_STAMP(rh == 0, 13);
   const int hb = s_bin;
   int threshold;  // 16-bit key threshold; -1 selects every non-empty community
   if (hb < 0) {
@@ -330,8 +380,8 @@ __global__ __launch_bounds__(SELECT_THREADS) void select_kernel(DecodeArgs a, De
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < OWN; ++k) {
-      const int c = k * SELECT_THREADS + tid;
-      const bool live = k < orounds && c < count && o_size[k] > 0;
+      const int c = c0 + k;
+      const bool live = c < count && o_size[k] > 0;
       if (live && (int)(o_key[k] >> 8) == hb) atomicAdd(hist + (o_key[k] & 0xff), budget_mode ? o_size[k] : 1);
     }
     __syncthreads();
@@ -341,8 +391,47 @@ __global__ __launch_bounds__(SELECT_THREADS) void select_kernel(DecodeArgs a, De
   }
   CKV_STAMP(rh == 0, 2);
 
-  // Compaction, high keys first (id order), then threshold keys (id order).
+  // Compaction, high keys first (id order), then threshold keys (id order): one
+  // four-component block scan (high count/mass, threshold count/mass).
   const int cap_tokens = sel_slots;
+  int v4[4] = {0, 0, 0, 0};
+#pragma unroll
+  for (int k = 0; k < OWN; ++k) {
+    const int c = c0 + k;
+    const int size = o_size[k];
+    const bool ok = c < count && size > 0;
+    const bool high = ok && (int)o_key[k] > threshold;
+    const bool eq = ok && threshold >= 0 && (int)o_key[k] == threshold;
+    v4[0] += high ? 1 : 0;
+    v4[1] += high ? size : 0;
+    v4[2] += eq ? 1 : 0;
+    v4[3] += eq ? size : 0;
+  }
+  int b4[4], t4[4];
+  {
+    const int lane = tid & 63, wave = tid >> 6;
+    int inc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) inc[i] = wave_inclusive_scan(v4[i]);
+    if (lane == 63) *reinterpret_cast<int4*>(scan_s + 4 * wave) = int4{inc[0], inc[1], inc[2], inc[3]};
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      b4[i] = inc[i] - v4[i];
+      t4[i] = 0;
+    }
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) {
+      const int4 x = *reinterpret_cast<const int4*>(scan_s + 4 * w);
+      const int xs[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (w < wave) b4[i] += xs[i];
+        t4[i] += xs[i];
+      }
+    }
+  }
+  const int high_count = t4[0], high_mass = t4[1];
   auto store_desc = [&](int idx, int c, int end, int k) {
     desc_comm[idx] = c;
     desc_end[idx] = end;
@@ -353,56 +442,41 @@ __global__ __launch_bounds__(SELECT_THREADS) void select_kernel(DecodeArgs a, De
     desc_ts[idx] = has ? o_ts[k] : 0;
     desc_tn[idx] = has ? o_tn[k] : 0;
   };
-  int high_count = 0, high_mass = 0, high_stored = 0;
-#pragma unroll
-  for (int k = 0; k < OWN; ++k) {
-    if (k >= orounds) break;
-    const int c = k * SELECT_THREADS + tid;
-    const int size = o_size[k];
-    const bool high = c < count && size > 0 && (int)o_key[k] > threshold;
-    int ec, em, tc, tm;
-    block_scan2(high ? 1 : 0, high ? size : 0, ec, em, tc, tm, scan_s);
-    const int st0 = high_mass + em;
-    const bool stored = high && st0 < cap_tokens;
-    if (stored && high_count + ec < dcap) store_desc(high_count + ec, c, min(cap_tokens, st0 + size), k);
-    high_stored += __syncthreads_count(stored);
-    high_count += tc;
-    high_mass += tm;
-  }
-  int eq_cnt = 0, eq_mass = 0, eq_stored = 0;
-  if (threshold >= 0) {
+  {
+    int hc = b4[0], hm = b4[1], ec = b4[2], em = b4[3];
+    int my_max = -1;
 #pragma unroll
     for (int k = 0; k < OWN; ++k) {
-      if (k >= orounds) break;
-      const int c = k * SELECT_THREADS + tid;
+      const int c = c0 + k;
       const int size = o_size[k];
-      const bool eq = c < count && size > 0 && (int)o_key[k] == threshold;
-      int ec, em, tc, tm;
-      block_scan2(eq ? 1 : 0, eq ? size : 0, ec, em, tc, tm, scan_s);
-      bool take = false;
-      if (eq) {
-        const int st0 = high_mass + eq_mass + em;
-        const bool within = budget_mode ? (st0 < sel_slots) : (eq_cnt + ec < a.cfg.topk_communities - high_count);
-        take = within && st0 < cap_tokens;
-        const int idx = high_count + eq_cnt + ec;
-        if (take && idx < dcap) store_desc(idx, c, min(cap_tokens, st0 + size), k);
+      const bool ok = c < count && size > 0;
+      const bool high = ok && (int)o_key[k] > threshold;
+      const bool eq = ok && threshold >= 0 && (int)o_key[k] == threshold;
+      if (high) {
+        if (hm < cap_tokens && hc < dcap) {
+          store_desc(hc, c, min(cap_tokens, hm + size), k);
+          my_max = max(my_max, hc);  // (a later high-key community has a smaller index than an earlier threshold one)
+        }
+        hc += 1;
+        hm += size;
+      } else if (eq) {
+        const int st0 = high_mass + em;
+        const bool within = budget_mode ? (st0 < sel_slots) : (ec < a.cfg.topk_communities - high_count);
+        const int idx = high_count + ec;
+        if (within && st0 < cap_tokens && idx < dcap) {
+          store_desc(idx, c, min(cap_tokens, st0 + size), k);
+          my_max = max(my_max, idx);
+        }
+        ec += 1;
+        em += size;
       }
-      eq_stored += __syncthreads_count(take);
-      eq_cnt += tc;
-      eq_mass += tm;
     }
+    if (my_max >= 0) atomicMax(&s_max_idx, my_max);
   }
-  int desc_count = high_stored + eq_stored;
-  if (desc_count > dcap) desc_count = dcap;
-  if (tid == 0) {
-    s_desc_count = desc_count;
-    s_sel_count = desc_count > 0 ? desc_end[desc_count - 1] : 0;
-    s_last_sel_pos = -1;
-    s_last_size = 0;
-  }
-  __syncthreads();
-  const int n_desc = s_desc_count;
-  const int sel_count = s_sel_count;
+  __syncthreads();  // descriptors, s_max_idx
+  const int n_desc = s_max_idx + 1;
+  const int sel_count = n_desc > 0 ? desc_end[n_desc - 1] : 0;
+  CKV_STAMP(rh == 0, 15);
   const int nblk = (sel_count + 63) / 64;
   for (int b = tid; b <= nblk; b += SELECT_THREADS) {
     const int j = 64 * b;
@@ -417,103 +491,100 @@ __global__ __launch_bounds__(SELECT_THREADS) void select_kernel(DecodeArgs a, De
   // Only the last descriptor can be truncated; remember its community size.
   if (n_desc > 0) {
     const int last_c = desc_comm[n_desc - 1];
-    if (last_c % SELECT_THREADS == tid) {
+    if (last_c / OWN == tid) {
 #pragma unroll
       for (int k = 0; k < OWN; ++k) {
-        if (k * SELECT_THREADS + tid == last_c) s_last_size = o_size[k];
+        if (c0 + k == last_c) s_last_size = o_size[k];
       }
     }
   }
+  if (tid == 0) s_last_sel_pos = -1;
   CKV_STAMP(rh == 0, 3);
 
+  const int slot_cap = a.ws.slot_capacity;
+  int32_t* slots = a.ws.slot_positions + (int64_t)rh * slot_cap;
+  const int inc = a.cfg.include_current ? 1 : 0;
+  const int wbeg = ns + sel_count;
   if (materialise) {
-    __syncthreads();  // blk_first, comm_desc
+    __syncthreads();  // blk_first, comm_desc, s_last_size
+    CKV_STAMP(rh == 0, 16);
     // ---- R3: slot materialisation ---------------------------------------------
     // Layout: sinks, selected members (newest first: decode deltas from the
     // tail chunk backwards, then the recency-descending CSR), window, current.
-    const int W = a.cfg.local_window;
-    const int inc = a.cfg.include_current ? 1 : 0;
-    const int slot_cap = a.ws.slot_capacity;
-    int32_t* slots = a.ws.slot_positions + (int64_t)rh * slot_cap;
+    // Each wave resolves 64-slot blocks of the selection, lane = slot (coalesced
+    // gathers): a lane's descriptor is the block's first descriptor plus the
+    // number of descriptor ends at or before it, read off a wave-wide bit mask
+    // of the ends that fall inside the block (no search chains).
     const int32_t* members = a.csr.member_positions + (int64_t)graph * a.csr.member_stride;
     const int32_t* dpos = a.dl.positions + (int64_t)graph * a.dl.position_capacity;
-    const int32_t* tcomm = a.st.token_communities + (int64_t)graph * a.st.token_capacity;
-    const int wbeg = ns + sel_count;
-    for (int s0 = 0; s0 < slot_cap; s0 += SELECT_THREADS * MAT_BATCH) {
+    const int lane = tid & 63, wave = tid >> 6;
+    const int nblk_sel = (sel_count + 63) / 64;
+    for (int b0 = wave; b0 < nblk_sel; b0 += WAVES * MAT_BATCH) {
       const int32_t* src[MAT_BATCH];
-      int val[MAT_BATCH];
       bool gathered[MAT_BATCH];
       int slow_d[MAT_BATCH], slow_rem[MAT_BATCH];  // delta members beyond the tail chunk
 #pragma unroll
-      for (int k = 0; k < MAT_BATCH; ++k) {
-        const int s = s0 + k * SELECT_THREADS + tid;
-        src[k] = a.st.community_counts + rh;  // in-bounds dummy address when nothing is gathered
-        val[k] = -1;
-        slow_d[k] = -1;
-        slow_rem[k] = 0;
-        bool gather = false;
-        if (s >= slot_cap) {
-        } else if (s < ns) {
-          val[k] = sink_s[s];
-        } else if (s < wbeg) {
-          const int j = s - ns;
-          int lo = blk_first[j >> 6], hi = min(blk_first[(j >> 6) + 1], n_desc - 1) + 1;
-          while (lo < hi) {
-            const int mid = (lo + hi) >> 1;
-            if (desc_end[mid] <= j) lo = mid + 1; else hi = mid;
-          }
-          const int m = j - (lo > 0 ? desc_end[lo - 1] : 0);
-          const int dc = desc_dc[lo];
-          if (m < dc) {
-            const int tn = desc_tn[lo];
-            if (m < tn) {
-              const int p = desc_ts[lo] + tn - 1 - m;
-              if (p >= 0 && p < a.dl.position_capacity) {
-                src[k] = dpos + p;
-                gather = true;
+      for (int q = 0; q < MAT_BATCH; ++q) {
+        const int b = b0 + q * WAVES;
+        src[q] = a.st.community_counts + rh;  // in-bounds dummy address when nothing is gathered
+        gathered[q] = false;
+        slow_d[q] = -1;
+        slow_rem[q] = 0;
+        if (b < nblk_sel) {  // wave-uniform
+          const int base = 64 * b;
+          const int j = base + lane;
+          const int d0 = blk_first[b];
+          const int e = d0 + lane < n_desc ? desc_end[d0 + lane] : 0x7fffffff;
+          const int off = e - base;
+          const uint64_t mask = wave_or_u64(off >= 1 && off <= 63 ? (1ull << off) : 0ull);
+          const uint64_t below = lane == 63 ? ~0ull : ((2ull << lane) - 1ull);
+          const int d = d0 + __popcll(mask & below);
+          if (j < sel_count) {
+            const int m = j - (d > 0 ? desc_end[d - 1] : 0);
+            const int dc = desc_dc[d];
+            if (m < dc) {
+              const int tn = desc_tn[d];
+              if (m < tn) {
+                const int p = desc_ts[d] + tn - 1 - m;
+                if (p >= 0 && p < a.dl.position_capacity) {
+                  src[q] = dpos + p;
+                  gathered[q] = true;
+                }
+              } else {
+                slow_d[q] = d;
+                slow_rem[q] = m - tn;
               }
             } else {
-              slow_d[k] = lo;
-              slow_rem[k] = m - tn;
-            }
-          } else {
-            const int64_t idx = (int64_t)desc_lo[lo] + (m - dc);
-            if (idx >= 0 && idx < a.csr.member_stride) {
-              src[k] = members + idx;
-              gather = true;
+              const int64_t idx = (int64_t)desc_lo[d] + (m - dc);
+              if (idx >= 0 && idx < a.csr.member_stride) {
+                src[q] = members + idx;
+                gathered[q] = true;
+              }
             }
           }
-        } else if (s < wbeg + W) {
-          const int p = cur - W + (s - wbeg);
-          if (p >= 0 && p < a.st.token_capacity) {
-            src[k] = tcomm + p;
-            gather = true;
-          }
-        } else if (inc && s == wbeg + W) {
-          val[k] = cur;
         }
-        gathered[k] = gather;
       }
-      int got[MAT_BATCH];
+      CKV_STAMP(rh == 0 && b0 == 0, 17);
+      int val[MAT_BATCH];
 #pragma unroll
-      for (int k = 0; k < MAT_BATCH; ++k) got[k] = gload_i32(src[k]);
+      for (int q = 0; q < MAT_BATCH; ++q) val[q] = gload_i32(src[q]);
 #pragma unroll
-      for (int k = 0; k < MAT_BATCH; ++k) {
-        if (gathered[k]) val[k] = got[k];
+      for (int q = 0; q < MAT_BATCH; ++q) {
+        if (!gathered[q]) val[q] = -1;
       }
       // Delta members older than the tail chunk: walk the chunk chain backwards.
 #pragma unroll
-      for (int k = 0; k < MAT_BATCH; ++k) {
-        if (slow_d[k] < 0) continue;
-        const int tail = desc_tl[slow_d[k]];
+      for (int q = 0; q < MAT_BATCH; ++q) {
+        if (slow_d[q] < 0) continue;
+        const int tail = desc_tl[slow_d[q]];
         if (tail < 0 || tail >= cpg) continue;
-        int rem = slow_rem[k];
+        int rem = slow_rem[q];
         int ch = a.dl.chunk_previous[cb + tail];
         for (int guard = 0; guard < 64 && ch >= 0 && ch < cpg; ++guard) {
           const int cs = a.dl.chunk_size[cb + ch];
           if (rem < cs) {
             const int p = a.dl.chunk_start[cb + ch] + cs - 1 - rem;
-            if (p >= 0 && p < a.dl.position_capacity) val[k] = dpos[p];
+            if (p >= 0 && p < a.dl.position_capacity) val[q] = dpos[p];
             break;
           }
           rem -= cs;
@@ -521,31 +592,34 @@ __global__ __launch_bounds__(SELECT_THREADS) void select_kernel(DecodeArgs a, De
         }
       }
 #pragma unroll
-      for (int k = 0; k < MAT_BATCH; ++k) {
-        const int s = s0 + k * SELECT_THREADS + tid;
-        if (s >= slot_cap) continue;
-        if (s >= wbeg && s < wbeg + W) {
-          win_s[s - wbeg] = val[k];  // community of the window token (resolved below)
-          continue;
+      for (int q = 0; q < MAT_BATCH; ++q) {
+        const int j = 64 * (b0 + q * WAVES) + lane;
+        if (j < sel_count) {
+          slots[ns + j] = val[q];
+          if (j == sel_count - 1) s_last_sel_pos = val[q];
         }
-        slots[s] = val[k];
-        if (s == wbeg - 1 && sel_count > 0) s_last_sel_pos = val[k];
       }
     }
-    __syncthreads();
+    if (tid < ns) slots[tid] = sink_s[tid];
+    __syncthreads();  // s_last_sel_pos
     CKV_STAMP(rh == 0, 4);
     // Window: positions cur-W .. cur-1 not already attended (sinks, or members
     // of a selected community at or after the selection's oldest position).
-    if (W > 0) {
-      const int last_pos = s_last_sel_pos;
-      for (int i = tid; i < W; i += SELECT_THREADS) {
+    const int last_pos = s_last_sel_pos;
+    const int sink_max = s_sink_max;
+#pragma unroll
+    for (int h = 0; h < WIN_PER_THREAD; ++h) {
+      const int i = tid + h * SELECT_THREADS;
+      if (i < W) {
         const int p = cur - W + i;
         int pos = p < 0 ? -1 : p;
-        for (int k = 0; k < ns && pos >= 0; ++k) {
-          if (sink_s[k] == p) pos = -1;
+        if (pos >= 0 && p <= sink_max) {
+          for (int k = 0; k < ns; ++k) {
+            if (sink_s[k] == p) pos = -1;
+          }
         }
         if (pos >= 0 && p < a.st.token_capacity) {
-          const int c = win_s[i];
+          const int c = wcomm[h];
           if (c >= 0 && c < count) {
             const int found = comm_desc[c] == 0xffffu ? -1 : (int)comm_desc[c];
             if (found >= 0) {
@@ -558,6 +632,8 @@ __global__ __launch_bounds__(SELECT_THREADS) void select_kernel(DecodeArgs a, De
         slots[wbeg + i] = pos;
       }
     }
+    if (inc && tid == 0) slots[wbeg + W] = cur;
+    for (int s = wbeg + W + inc + tid; s < slot_cap; s += SELECT_THREADS) slots[s] = -1;
   }
 
   // ---- outputs that nothing in this kernel reads back --------------------------
@@ -580,8 +656,8 @@ __global__ __launch_bounds__(SELECT_THREADS) void select_kernel(DecodeArgs a, De
   }
 #pragma unroll
   for (int k = 0; k < OWN; ++k) {
-    const int c = k * SELECT_THREADS + tid;
-    if (k < orounds && c < nscore) {
+    const int c = c0 + k;
+    if (c < nscore) {
       const bool live = c < count && o_size[k] > 0;
       const uint32_t key = o_key[k];
       const uint16_t bits = live ? (uint16_t)((key & 0x8000u) ? (key ^ 0x8000u) : (key ^ 0xffffu)) : (uint16_t)0xfc00u;
@@ -590,7 +666,7 @@ __global__ __launch_bounds__(SELECT_THREADS) void select_kernel(DecodeArgs a, De
   }
   if (nearest_mode && tid == 0) {
     uint64_t m = ~0ull;
-    for (int w = 0; w < SELECT_THREADS / 64; ++w) m = near_s[w] < m ? near_s[w] : m;
+    for (int w = 0; w < WAVES; ++w) m = near_s[w] < m ? near_s[w] : m;
     a.ws.nearest[rh] = (m == ~0ull) ? -1 : (int)(m & 0xffffffffu);
   }
   CKV_STAMP(rh == 0, 5);
@@ -627,18 +703,21 @@ int launch_score_select(const DecodeArgs& a, hipStream_t s, const DecodeArgs* pe
     hipLaunchKernelGGL(kernel, dim3(a.st.retrieval_heads + extra), dim3(SELECT_THREADS), lds, s, a, u, u_splits);
     return launch_check("select");
   };
-  auto by_own = [&](auto k1, auto k2, auto k8) { return own <= 1 ? launch(k1) : own <= 2 ? launch(k2) : launch(k8); };
+  constexpr int OWN_MAX = CKV_MAX_COMMUNITIES / SELECT_THREADS;
+  auto by_own = [&](auto k1, auto k2, auto kmax) {
+    return own <= 1 ? launch(k1) : own <= 2 ? launch(k2) : launch(kmax);
+  };
   if (ct == CKV_E4M3 && dt == CKV_BF16)
     return by_own(select_kernel<CKV_E4M3, CKV_BF16, 1>, select_kernel<CKV_E4M3, CKV_BF16, 2>,
-                  select_kernel<CKV_E4M3, CKV_BF16, 8>);
+                  select_kernel<CKV_E4M3, CKV_BF16, OWN_MAX>);
   if (ct == CKV_E4M3)
     return by_own(select_kernel<CKV_E4M3, CKV_F32, 1>, select_kernel<CKV_E4M3, CKV_F32, 2>,
-                  select_kernel<CKV_E4M3, CKV_F32, 8>);
+                  select_kernel<CKV_E4M3, CKV_F32, OWN_MAX>);
   if (dt == CKV_BF16)
     return by_own(select_kernel<CKV_F32, CKV_BF16, 1>, select_kernel<CKV_F32, CKV_BF16, 2>,
-                  select_kernel<CKV_F32, CKV_BF16, 8>);
+                  select_kernel<CKV_F32, CKV_BF16, OWN_MAX>);
   return by_own(select_kernel<CKV_F32, CKV_F32, 1>, select_kernel<CKV_F32, CKV_F32, 2>,
-                select_kernel<CKV_F32, CKV_F32, 8>);
+                select_kernel<CKV_F32, CKV_F32, OWN_MAX>);
 }
 
 }  // namespace ckv
