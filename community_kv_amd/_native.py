@@ -30,7 +30,7 @@ HIP_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 CKV_BF16, CKV_F32, CKV_E4M3 = 0, 1, 2
 CKV_SELECT_BUDGET, CKV_SELECT_TOPK = 0, 1
@@ -104,7 +104,7 @@ class DecodeWorkspace(ctypes.Structure):
                 ("descriptor_counts", _p), ("tile_descriptors", _p), ("selected_counts", _p),
                 ("slot_positions", _p), ("nearest_partial", _p), ("nearest", _p),
                 ("block_counters", _p), ("partial_max", _p), ("partial_sum", _p),
-                ("partial_acc", _p), ("partial_topk", _p), ("output", _p), ("lse", _p),
+                ("partial_acc", _p), ("slot_scores", _p), ("output", _p), ("lse", _p),
                 ("topk_scores", _p), ("topk_positions", _p), ("assigned", _p), ("overflow", _p),
                 ("descriptor_capacity", _i32), ("slot_capacity", _i32), ("budget_tiles", _i32),
                 ("score_blocks", _i32)]

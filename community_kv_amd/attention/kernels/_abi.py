@@ -74,7 +74,7 @@ def workspace_struct(selection, attention, update) -> nat.DecodeWorkspace:
         p(selection.slot_positions), p(selection.nearest_partial), p(selection.nearest),
         p(selection.block_counters),
         p(attention.partial_max) if attention else None, p(attention.partial_sum) if attention else None,
-        p(attention.partial_acc) if attention else None, p(attention.partial_topk_packed) if attention else None,
+        p(attention.partial_acc) if attention else None, p(attention.slot_scores) if attention else None,
         p(attention.output) if attention else None, p(attention.lse) if attention else None,
         p(attention.topk_scores) if attention else None, p(attention.topk_positions) if attention else None,
         p(update.assigned_communities) if update else None, p(update.overflow) if update else None,

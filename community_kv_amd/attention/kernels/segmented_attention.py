@@ -28,7 +28,8 @@ class SegmentedAttentionWorkspace:
     partial_max: torch.Tensor          # [Hq, tiles] float32
     partial_sum: torch.Tensor          # [Hq, tiles] float32
     partial_acc: torch.Tensor          # [Hq, tiles, 128] float32
-    partial_topk_packed: torch.Tensor  # [R, tiles, 8] uint64
+    partial_topk_packed: torch.Tensor  # [R, tiles, 8] uint64 (reference layout, kept for interface parity)
+    slot_scores: torch.Tensor          # [R, slot capacity] float32: first query's score per slot (top-8 candidates)
     output: torch.Tensor               # [Hq, 128]
     lse: torch.Tensor                  # [Hq] float32
     topk_scores: torch.Tensor          # [R, 8] float32
@@ -56,6 +57,7 @@ class SegmentedAttentionWorkspace:
             partial_sum=torch.empty((heads, tiles), dtype=torch.float32, device=device),
             partial_acc=torch.empty((heads, tiles, HEAD_DIM), dtype=torch.float32, device=device),
             partial_topk_packed=torch.empty((kv_heads, tiles, KAPPA), dtype=torch.uint64, device=device),
+            slot_scores=torch.empty((kv_heads, slots), dtype=torch.float32, device=device),
             output=torch.empty((heads, HEAD_DIM), dtype=dtype, device=device),
             lse=torch.empty((heads,), dtype=torch.float32, device=device),
             topk_scores=torch.empty((kv_heads, KAPPA), dtype=torch.float32, device=device),

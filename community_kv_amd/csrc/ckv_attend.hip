@@ -112,13 +112,7 @@ __global__ __launch_bounds__(64) void attend_generic_kernel(DecodeArgs a, int de
     }
   }
   if (!DENSE && a.cfg.assignment != CKV_ASSIGN_NONE) {
-    const int slot = tile * TILE + lane;
-    uint64_t cand = (valid && slot >= a.cfg.num_sink) ? pack_candidate(s[0], pos) : 0ull;
-    for (int r = 0; r < KAPPA; ++r) {
-      const uint64_t best = wave_max_u64(cand);
-      if (lane == 0) a.ws.partial_topk[((int64_t)head * tiles + tile) * KAPPA + r] = best;
-      if (cand == best) cand = 0ull;
-    }
+    a.ws.slot_scores[(int64_t)head * a.ws.slot_capacity + tile * TILE + lane] = s[0];
   }
 }
 
@@ -210,11 +204,11 @@ __global__ __launch_bounds__(REDUCE_THREADS) void reduce_kernel(DecodeArgs a) {
 }
 
 // Online update of every owned graph, after the attention merge: reads the
-// splits' top-8 candidates and the merged lse of each head's first query.
+// slots' candidate scores and the merged lse of each head's first query.
 template <int CT, int DT>
-__global__ __launch_bounds__(256) void update_kernel(DecodeArgs a, int splits) {
+__global__ __launch_bounds__(256) void update_kernel(DecodeArgs a) {
   const int rh = blockIdx.x;
-  owner_update<CT, DT>(a, rh, splits, a.ws.lse[(int64_t)rh * a.cfg.group_size]);
+  owner_update<CT, DT>(a, rh, a.ws.lse[(int64_t)rh * a.cfg.group_size]);
 }
 
 template <int CT, int DT>
@@ -313,38 +307,42 @@ struct TileResult {
   float l;      // sum of exp(score - m)
 };
 
+// NH: number of 32-token halves (2: a 64-slot tile, 1: one half; positions are
+// then local tokens 0..31 of pos_s).
+template <int NH>
 __device__ inline TileResult mfma_tile(const uint16_t* __restrict__ K, const uint16_t* __restrict__ V, int64_t kbase,
                                        int64_t tstride, const int* pos_s, uint16_t* v_s, float* cand_s,
                                        const QOperand qop, float scale, float m_prev, f32x4_t* o) {
+  constexpr int NJ = 2 * NH;  // 16-token MFMA row blocks
   const int lane = threadIdx.x & 63;  // lane within the wave (workgroups may hold several waves)
   const int L = lane >> 4;
   const int c16 = lane & 15;
   // Masked slots (position -1) read row 0 and are masked out of the softmax,
-  // so every load is unconditional and all 32 are in flight together.
-  uint4 kreg[4][4];
+  // so every load is unconditional and all of them are in flight together.
+  uint4 kreg[NJ][4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < NJ; ++j) {
     const int p = max(pos_s[tau(j, c16)], 0);
 #pragma unroll
     for (int s = 0; s < 4; ++s) kreg[j][s] = gload16(K + kbase + (int64_t)p * tstride + 32 * s + 8 * L);
   }
-  uint4 vreg[16];
+  uint4 vreg[8 * NH];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
+  for (int i = 0; i < 8 * NH; ++i) {
     const int p = max(pos_s[4 * i + L], 0);
     vreg[i] = gload16(V + kbase + (int64_t)p * tstride + 8 * c16);
   }
-  f32x4_t sacc[4];
+  f32x4_t sacc[NJ];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < NJ; ++j) {
     sacc[j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int s = 0; s < 4; ++s) sacc[j] = mfma_bf16(kreg[j][s], qop.s[s], sacc[j]);
   }
-  float sc[4][4];
+  float sc[NJ][4];
   float mloc = NEG_INF;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < NJ; ++j) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const bool ok = pos_s[tau(j, 4 * L + i)] >= 0;
@@ -355,7 +353,7 @@ __device__ inline TileResult mfma_tile(const uint16_t* __restrict__ K, const uin
   }
   if (cand_s != nullptr && c16 == 0) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < NJ; ++j) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) cand_s[tau(j, 4 * L + i)] = sc[j][i];
     }
@@ -366,9 +364,9 @@ __device__ inline TileResult mfma_tile(const uint16_t* __restrict__ K, const uin
   const float m_new = fmax_exact(m_prev, mloc);
   res.m = m_new;
   float lsum = 0.0f;
-  uint32_t pk[4][2];
+  uint32_t pk[NJ][2];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < NJ; ++j) {
     float p[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -382,8 +380,8 @@ __device__ inline TileResult mfma_tile(const uint16_t* __restrict__ K, const uin
   lsum = add_xor32(lsum);
   res.l = lsum;
   // rescale the running accumulator rows (query 4L+i) by exp(m_prev - m_new) of that query
-  {
-    const float corr_mine = (m_prev == NEG_INF) ? 0.0f : __expf(m_prev - m_new);
+  if (m_prev != NEG_INF) {
+    const float corr_mine = __expf(m_prev - m_new);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const float c = __shfl(corr_mine, 4 * L + i, 64);
@@ -391,10 +389,10 @@ __device__ inline TileResult mfma_tile(const uint16_t* __restrict__ K, const uin
       for (int nb = 0; nb < 8; ++nb) o[nb][i] = o[nb][i] * c;
     }
   }
-  // P.V in two 32-slot halves; each half of the V tile goes through the wave's
+  // P.V in 32-slot halves; each half of the V tile goes through the wave's
   // 8 KB LDS buffer (row 4i+L of the tile -> buffer row 4(i mod 8)+L, swizzled).
 #pragma unroll
-  for (int s = 0; s < 2; ++s) {
+  for (int s = 0; s < NH; ++s) {
     wave_sync();  // previous half fully read
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -417,7 +415,8 @@ __device__ inline TileResult mfma_tile(const uint16_t* __restrict__ K, const uin
   return res;
 }
 
-constexpr int ATT_WAVES = 4;  // 64-slot tiles per attention workgroup
+constexpr int ATT_WAVES = 4;  // waves (one 64-slot tile each) per attention workgroup
+constexpr int ATT_TILES = ATT_WAVES;  // 64-slot tiles per attention workgroup
 
 // Split merge of all G query heads of retrieval head rh at once (any block
 // size); `scratch` holds 3 * G * splits floats.  When every thread has at most
@@ -451,34 +450,64 @@ __device__ inline void merge_group(const DecodeArgs& a, const int rh, const int 
       v1[k] = gload_f32(s1 + (int64_t)kk * D);
     }
   }
-  for (int i = tid; i < n; i += nt) {
-    m_s[i] = a.ws.partial_max[base + i];
-    l_s[i] = a.ws.partial_sum[base + i];
-  }
-  __syncthreads();
-  if (tid < G) {
-    float M = NEG_INF;
-    for (int t = 0; t < splits; ++t) M = fmax_exact(M, m_s[tid * splits + t]);
-    gm_s[tid] = M;
-  }
-  __syncthreads();
-  for (int i = tid; i < n; i += nt) {
-    const float mt = m_s[i];
-    sc_s[i] = mt == NEG_INF ? 0.0f : ckv_expf(mt - gm_s[i / splits]);
-  }
-  __syncthreads();
-  if (tid < G) {
-    float den = 0.0f;
-    for (int t = 0; t < splits; ++t) {
-      const float sc = sc_s[tid * splits + t];
-      den = den + (sc != 0.0f ? l_s[tid * splits + t] * sc : 0.0f);
+  if (fast && splits <= 16 && 16 * G <= nt) {
+    // One row of 16 lanes per query (lane = split): max, scales, denominator
+    // and lse by DPP row reductions, published behind a single barrier.
+    if (tid < 16 * G) {
+      const int g = tid >> 4, t = tid & 15;
+      const bool ok = t < splits;
+      const float mt = ok ? a.ws.partial_max[base + g * splits + t] : NEG_INF;
+      const float lt = ok ? a.ws.partial_sum[base + g * splits + t] : 0.0f;
+      float M = mt;
+      M = fmax_exact(M, ckv_u2f(dpp_u32<0xB1>(ckv_f2u(M))));
+      M = fmax_exact(M, ckv_u2f(dpp_u32<0x4E>(ckv_f2u(M))));
+      M = fmax_exact(M, ckv_u2f(dpp_u32<0x141>(ckv_f2u(M))));
+      M = fmax_exact(M, ckv_u2f(dpp_u32<0x140>(ckv_f2u(M))));
+      const float sc = mt == NEG_INF ? 0.0f : ckv_expf(mt - M);
+      float den = sc != 0.0f ? lt * sc : 0.0f;
+      den = den + ckv_u2f(dpp_u32<0xB1>(ckv_f2u(den)));
+      den = den + ckv_u2f(dpp_u32<0x4E>(ckv_f2u(den)));
+      den = den + ckv_u2f(dpp_u32<0x141>(ckv_f2u(den)));
+      den = den + ckv_u2f(dpp_u32<0x140>(ckv_f2u(den)));
+      if (ok) sc_s[g * splits + t] = sc;
+      if (t == 0) {
+        gden_s[g] = den;
+        const float lse = M + ckv_logf(den);
+        a.ws.lse[(int64_t)rh * G + g] = lse;
+        if (g == 0 && lse0_out) *lse0_out = lse;
+      }
     }
-    gden_s[tid] = den;
-    const float lse = gm_s[tid] + ckv_logf(den);
-    a.ws.lse[(int64_t)rh * G + tid] = lse;
-    if (tid == 0 && lse0_out) *lse0_out = lse;
+    __syncthreads();
+  } else {
+    for (int i = tid; i < n; i += nt) {
+      m_s[i] = a.ws.partial_max[base + i];
+      l_s[i] = a.ws.partial_sum[base + i];
+    }
+    __syncthreads();
+    if (tid < G) {
+      float M = NEG_INF;
+      for (int t = 0; t < splits; ++t) M = fmax_exact(M, m_s[tid * splits + t]);
+      gm_s[tid] = M;
+    }
+    __syncthreads();
+    for (int i = tid; i < n; i += nt) {
+      const float mt = m_s[i];
+      sc_s[i] = mt == NEG_INF ? 0.0f : ckv_expf(mt - gm_s[i / splits]);
+    }
+    __syncthreads();
+    if (tid < G) {
+      float den = 0.0f;
+      for (int t = 0; t < splits; ++t) {
+        const float sc = sc_s[tid * splits + t];
+        den = den + (sc != 0.0f ? l_s[tid * splits + t] * sc : 0.0f);
+      }
+      gden_s[tid] = den;
+      const float lse = gm_s[tid] + ckv_logf(den);
+      a.ws.lse[(int64_t)rh * G + tid] = lse;
+      if (tid == 0 && lse0_out) *lse0_out = lse;
+    }
+    __syncthreads();
   }
-  __syncthreads();
   auto store = [&](int g, int d, float r) {
     if constexpr (DT == CKV_BF16) {
       reinterpret_cast<uint16_t*>(a.ws.output)[((int64_t)rh * G + g) * D + d] = ckv_f32_to_bf16_bits(r);
@@ -526,10 +555,11 @@ __device__ inline void merge_group(const DecodeArgs& a, const int rh, const int 
   __syncthreads();
 }
 
-// Sparse bf16 attention: a workgroup of ATT_WAVES waves covers ATT_WAVES
+// Sparse bf16 attention: a workgroup of ATT_WAVES waves covers ATT_TILES
 // consecutive 64-slot tiles of one retrieval head; each wave runs mfma_tile on
-// its tile, the workgroup combines its waves in LDS into one split partial
-// (max, sum, unnormalised P.V per query, top-8 candidates).  With MERGE the
+// one tile, the workgroup combines its waves in LDS into one split partial
+// (max, sum, unnormalised P.V per query) plus the first query's score of every
+// slot (the candidates of the online update's top-8).  With MERGE the
 // last workgroup of a head to finish merges the splits into output and lse.
 template <bool MERGE>
 __global__ __launch_bounds__(64 * ATT_WAVES) void attend_mfma_kernel(DecodeArgs a) {
@@ -557,15 +587,15 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attend_mfma_kernel(DecodeArgs 
   __shared__ float cand_s[ATT_WAVES][TILE];
   __shared__ float wm_s[ATT_WAVES][CKV_MAX_GROUP];
   __shared__ float wl_s[ATT_WAVES][CKV_MAX_GROUP];
-  __shared__ uint64_t wtop_s[ATT_WAVES][KAPPA];
   __shared__ int last_block;
   __shared__ float s_lse0;
 
   const int tile = wgi * ATT_WAVES + wave;
   CKV_STAMP(rh == 0 && wgi == 0, 0);
   const int slot = tile * TILE + lane;
-  int pos = tile < tiles ? a.ws.slot_positions[(int64_t)rh * a.ws.slot_capacity + slot] : -1;
-  const bool valid = pos >= 0 && pos < a.kv.capacity;
+  const bool in_range = tile < tiles;
+  int pos = a.ws.slot_positions[(int64_t)rh * a.ws.slot_capacity + (in_range ? slot : 0)];
+  const bool valid = in_range && pos >= 0 && pos < a.kv.capacity;
   if (!valid) pos = -1;
   pos_s[wave][lane] = pos;
   const bool any = __ballot(valid) != 0ull;
@@ -583,8 +613,8 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attend_mfma_kernel(DecodeArgs 
     f32x4_t o[8];
 #pragma unroll
     for (int nb = 0; nb < 8; ++nb) o[nb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    const TileResult r = mfma_tile(K, V, kvh * a.kv.head_stride, a.kv.token_stride, pos_s[wave], v_s,
-                                   want_topk ? cand_s[wave] : nullptr, qop, a.cfg.softmax_scale, NEG_INF, o);
+    const TileResult r = mfma_tile<2>(K, V, kvh * a.kv.head_stride, a.kv.token_stride, pos_s[wave], v_s,
+                                      want_topk ? cand_s[wave] : nullptr, qop, a.cfg.softmax_scale, NEG_INF, o);
     wave_sync();
     CKV_STAMP(rh == 0 && wgi == 0, 1);
     if (L == 0 && c16 < G) {
@@ -599,17 +629,13 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attend_mfma_kernel(DecodeArgs 
         for (int nb = 0; nb < 8; ++nb) o_s[g * D + 16 * nb + c16] = o[nb][i];
       }
     }
-    if (want_topk) {
-      uint64_t cand = (pos >= 0 && slot >= a.cfg.num_sink) ? pack_candidate(cand_s[wave][lane], pos) : 0ull;
-      cand = wave_sort_desc_u64(cand);
-      if (lane < KAPPA) wtop_s[wave][lane] = cand;
-    }
+    // the first query's score of every slot: candidates of the update's top-8
+    if (want_topk && in_range) a.ws.slot_scores[(int64_t)rh * a.ws.slot_capacity + slot] = cand_s[wave][lane];
   } else {
     if (L == 0 && c16 < G) {
       wm_s[wave][c16] = NEG_INF;
       wl_s[wave][c16] = 0.0f;
     }
-    if (lane < KAPPA) wtop_s[wave][lane] = 0ull;
   }
   __syncthreads();
   CKV_STAMP(rh == 0 && wgi == 0, 10);
@@ -645,11 +671,6 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attend_mfma_kernel(DecodeArgs 
     a.ws.partial_sum[((int64_t)rh * G + tid) * splits + wgi] = l;
   }
   CKV_STAMP(rh == 0 && wgi == 0, 11);
-  if (want_topk && wave == 0) {
-    uint64_t cand = lane < ATT_WAVES * KAPPA ? wtop_s[lane / KAPPA][lane % KAPPA] : 0ull;
-    cand = wave_sort_desc_u64(cand);
-    if (lane < KAPPA) a.ws.partial_topk[((int64_t)rh * splits + wgi) * KAPPA + lane] = cand;
-  }
   CKV_STAMP(rh == 0 && wgi == 0, 2);
   if (!MERGE) return;
   // The last workgroup of this head to finish merges the splits.
@@ -701,7 +722,7 @@ __global__ __launch_bounds__(64) void dense_mfma_kernel(DecodeArgs a, int seq_le
     __syncthreads();
     pos_s[lane] = base + lane < seq_len ? base + lane : -1;
     __syncthreads();
-    const TileResult r = mfma_tile(K, V, kvh * a.kv.head_stride, a.kv.token_stride, pos_s, v_s, nullptr, qop,
+    const TileResult r = mfma_tile<2>(K, V, kvh * a.kv.head_stride, a.kv.token_stride, pos_s, v_s, nullptr, qop,
                                    a.cfg.softmax_scale, m, o);
     const float corr = (m == NEG_INF) ? 0.0f : __expf(m - r.m);
     l = l * corr + r.l;
@@ -727,16 +748,16 @@ __global__ __launch_bounds__(64) void dense_mfma_kernel(DecodeArgs a, int seq_le
 // Launchers
 // ---------------------------------------------------------------------------
 
-// Candidate groups per retrieval head written by the attention kernels.
-int candidate_splits(const DecodeArgs& a) {
+// Split partials per retrieval head written by the attention kernels.
+static int attention_splits(const DecodeArgs& a) {
   const int tiles = a.ws.slot_capacity / TILE;
-  return a.kv.dtype == CKV_BF16 ? (tiles + ATT_WAVES - 1) / ATT_WAVES : tiles;
+  return a.kv.dtype == CKV_BF16 ? (tiles + ATT_TILES - 1) / ATT_TILES : tiles;
 }
 
 int launch_attention(const DecodeArgs& a, hipStream_t s, bool partials_only) {
   const int tiles = a.ws.slot_capacity / TILE;
   if (a.kv.dtype == CKV_BF16) {
-    const int splits = candidate_splits(a);
+    const int splits = attention_splits(a);
     const size_t lds = (size_t)ATT_WAVES * V_HALF_ROWS * D * sizeof(uint16_t);
     if ((size_t)3 * a.cfg.group_size * splits * sizeof(float) > lds) {
       return ckv_internal::set_error(CKV_E_LIMIT, "too many attention splits for the merge scratch");
@@ -761,12 +782,11 @@ int launch_update(const DecodeArgs& a, hipStream_t s) {
   if (a.cfg.assignment == CKV_ASSIGN_NONE) return CKV_OK;
   const bool e4m3 = a.st.centroid_dtype == CKV_E4M3;
   const bool bf16 = a.kv.dtype == CKV_BF16;
-  const int splits = candidate_splits(a);
   const dim3 g(a.st.retrieval_heads);
-  if (e4m3 && bf16) hipLaunchKernelGGL((update_kernel<CKV_E4M3, CKV_BF16>), g, dim3(256), 0, s, a, splits);
-  else if (e4m3) hipLaunchKernelGGL((update_kernel<CKV_E4M3, CKV_F32>), g, dim3(256), 0, s, a, splits);
-  else if (bf16) hipLaunchKernelGGL((update_kernel<CKV_F32, CKV_BF16>), g, dim3(256), 0, s, a, splits);
-  else hipLaunchKernelGGL((update_kernel<CKV_F32, CKV_F32>), g, dim3(256), 0, s, a, splits);
+  if (e4m3 && bf16) hipLaunchKernelGGL((update_kernel<CKV_E4M3, CKV_BF16>), g, dim3(256), 0, s, a);
+  else if (e4m3) hipLaunchKernelGGL((update_kernel<CKV_E4M3, CKV_F32>), g, dim3(256), 0, s, a);
+  else if (bf16) hipLaunchKernelGGL((update_kernel<CKV_F32, CKV_BF16>), g, dim3(256), 0, s, a);
+  else hipLaunchKernelGGL((update_kernel<CKV_F32, CKV_F32>), g, dim3(256), 0, s, a);
   const int r = launch_check("update");
   return r ? r : launch_sync_shared(a, s);
 }

@@ -78,7 +78,7 @@ int validate_attention(const ckv_graph_state* st, const ckv_delta_chunks* dl, co
   if (!ws->partial_max || !ws->partial_sum || !ws->partial_acc || !ws->output || !ws->lse)
     return fail(CKV_E_INVALID, "attention workspace is incomplete");
   if (cfg->assignment != CKV_ASSIGN_NONE &&
-      (!ws->partial_topk || !ws->topk_scores || !ws->topk_positions || !ws->assigned || !ws->overflow ||
+      (!ws->slot_scores || !ws->topk_scores || !ws->topk_positions || !ws->assigned || !ws->overflow ||
        !st->token_communities || !st->community_weight || !st->total_weight || !dl->positions ||
        !dl->chunk_start || !dl->chunk_capacity || !dl->chunk_size || !dl->chunk_next || !dl->chunk_previous ||
        !dl->community_head || !dl->community_tail || !dl->community_sizes || !dl->next_free_chunk ||

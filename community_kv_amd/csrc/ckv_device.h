@@ -425,7 +425,6 @@ __device__ inline void find_threshold_bin(const int* hist, int target, int* out_
 // Host-side launchers (one per translation unit), called after validation.
 int launch_score_select(const DecodeArgs& a, hipStream_t stream, const DecodeArgs* pending_update = nullptr);
 int launch_sync_shared(const DecodeArgs& a, hipStream_t stream);
-int candidate_splits(const DecodeArgs& a);
 int launch_attention(const DecodeArgs& a, hipStream_t stream, bool partials_only);
 int launch_update(const DecodeArgs& a, hipStream_t stream);
 int launch_dense(const DecodeArgs& a, int seq_len, int group, hipStream_t stream);

@@ -91,13 +91,13 @@ __device__ inline void decode_frag(const CentroidFrag<CT>& f, float* out) {
 // a.st.retrieval_heads run the pending online update of another layer `u`
 // (same dtypes, disjoint state) on otherwise idle CUs.
 template <int CT, int DT, int OWN>
-__global__ __launch_bounds__(SELECT_THREADS) void select_kernel(DecodeArgs a, DecodeArgs u, int u_splits) {
+__global__ __launch_bounds__(SELECT_THREADS) void select_kernel(DecodeArgs a, DecodeArgs u) {
   constexpr int PB = CT == CKV_E4M3 ? 4 : 2;  // scoring passes whose loads are in flight together
   constexpr int WAVES = SELECT_THREADS / 64;
   constexpr int WIN_PER_THREAD = (CKV_MAX_WINDOW + SELECT_THREADS - 1) / SELECT_THREADS;
   if ((int)blockIdx.x >= a.st.retrieval_heads) {
     const int urh = (int)blockIdx.x - a.st.retrieval_heads;
-    owner_update<CT, DT>(u, urh, u_splits, u.ws.lse[(int64_t)urh * u.cfg.group_size]);
+    owner_update<CT, DT>(u, urh, u.ws.lse[(int64_t)urh * u.cfg.group_size]);
     return;
   }
   const int rh = blockIdx.x;
@@ -694,13 +694,12 @@ int launch_score_select(const DecodeArgs& a, hipStream_t s, const DecodeArgs* pe
     }
     DecodeArgs u;
     memset(&u, 0, sizeof(u));
-    int extra = 0, u_splits = 0;
+    int extra = 0;
     if (pending != nullptr && pending->cfg.assignment != CKV_ASSIGN_NONE) {
       u = *pending;
       extra = pending->st.retrieval_heads;
-      u_splits = candidate_splits(*pending);
     }
-    hipLaunchKernelGGL(kernel, dim3(a.st.retrieval_heads + extra), dim3(SELECT_THREADS), lds, s, a, u, u_splits);
+    hipLaunchKernelGGL(kernel, dim3(a.st.retrieval_heads + extra), dim3(SELECT_THREADS), lds, s, a, u);
     return launch_check("select");
   };
   constexpr int OWN_MAX = CKV_MAX_COMMUNITIES / SELECT_THREADS;

@@ -9,14 +9,14 @@ namespace ckv {
 // Online update of the graph owned by retrieval head rh (no-op for
 // non-owners and assignment NONE): exact top-8 merge over the splits'
 // candidates, assignment, running-mean centroid, delta append, overflow.
-// s_lse0 is the merged lse of the head's first query.  Any block size >= 64.
+// s_lse0 is the merged lse of the head's first query.  Block size 128..512.
 //
 // Dependent memory rounds: (1) candidates + cursor/count/total, (2) candidate
 // communities + current key row, (3) per-candidate weight/size/delta tail and
 // centroid rows (slot KAPPA holds the community a new token would open, or the
 // nearest centroid), (4) the assigned community's tail-chunk state.
 template <int CT, int DT>
-__device__ void owner_update(const DecodeArgs& a, const int rh, const int tiles, const float s_lse0) {
+__device__ void owner_update(const DecodeArgs& a, const int rh, const float s_lse0) {
   const int tid = threadIdx.x;
   const int graph = a.st.retrieval_to_graph[rh];
   if (a.cfg.assignment == CKV_ASSIGN_NONE || rh != graph) return;
@@ -36,36 +36,58 @@ __device__ void owner_update(const DecodeArgs& a, const int rh, const int tiles,
   __shared__ float s_cent[NS][D];
   __shared__ int s_assigned, s_slot, s_comm_ov;
 
-  // ---- round 1: exact top-8 merge (wave 0); cursor state (wave 1) ----------
-  if (tid < 64 && tiles * KAPPA <= 64) {
-    const int n = tiles * KAPPA;
-    const uint64_t v = wave_sort_desc_u64(tid < n ? a.ws.partial_topk[(int64_t)rh * n + tid] : 0ull);
-    if (tid < KAPPA) top[tid] = v;
-  } else if (tid < 64) {
-    // Each lane keeps a sorted top-8 of its strided share, then 8 rounds of a
-    // wave-wide max over the lanes' heads.
-    const int n = tiles * KAPPA;
-    const uint64_t* cand = a.ws.partial_topk + (int64_t)rh * n;
+  // ---- round 1: exact top-8 over every attended non-sink slot (score desc,
+  // position asc); cursor state (one thread of wave 1).  Each thread keeps a
+  // sorted top-8 of its strided share (loaded 8 at a time, one round per
+  // chunk), each wave merges its lanes' lists in 8 rounds of a wave-wide max,
+  // and wave 0 sorts the waves' survivors.
+  {
+    constexpr int CH = 8;
+    __shared__ uint64_t wtop[8 * KAPPA];
+    const int nt = blockDim.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int scap = a.ws.slot_capacity;
+    const float* scs = a.ws.slot_scores + (int64_t)rh * scap;
+    const int32_t* sps = a.ws.slot_positions + (int64_t)rh * scap;
     uint64_t loc[KAPPA];
 #pragma unroll
     for (int k = 0; k < KAPPA; ++k) loc[k] = 0ull;
-    for (int i = tid; i < n; i += 64) {
-      uint64_t v = cand[i];
+    for (int s0 = 0; s0 < scap; s0 += CH * nt) {
+      float sv[CH];
+      int pv[CH];
 #pragma unroll
-      for (int k = 0; k < KAPPA; ++k) {
-        const uint64_t hi = v > loc[k] ? v : loc[k];
-        v = v > loc[k] ? loc[k] : v;
-        loc[k] = hi;
+      for (int c = 0; c < CH; ++c) {
+        const int s = min(s0 + c * nt + tid, scap - 1);
+        sv[c] = gload_f32(scs + s);
+        pv[c] = gload_i32(sps + s);
+      }
+#pragma unroll
+      for (int c = 0; c < CH; ++c) {
+        const int s = s0 + c * nt + tid;
+        const bool ok = s < scap && s >= a.cfg.num_sink && pv[c] >= 0 && pv[c] < a.kv.capacity;
+        uint64_t v = ok ? pack_candidate(sv[c], pv[c]) : 0ull;
+#pragma unroll
+        for (int k = 0; k < KAPPA; ++k) {
+          const uint64_t hi = v > loc[k] ? v : loc[k];
+          v = v > loc[k] ? loc[k] : v;
+          loc[k] = hi;
+        }
       }
     }
     for (int r = 0; r < KAPPA; ++r) {
       const uint64_t best = wave_max_u64(loc[0]);
-      if (tid == 0) top[r] = best;
+      if (lane == 0) wtop[wave * KAPPA + r] = best;
       if (best != 0ull && loc[0] == best) {
 #pragma unroll
         for (int k = 0; k < KAPPA - 1; ++k) loc[k] = loc[k + 1];
         loc[KAPPA - 1] = 0ull;
       }
+    }
+    __syncthreads();
+    if (wave == 0) {
+      const int n = (nt >> 6) * KAPPA;  // at most 64 (blocks of at most 512 threads)
+      const uint64_t v = wave_sort_desc_u64(lane < n ? wtop[lane] : 0ull);
+      if (lane < KAPPA) top[lane] = v;
     }
   }
   if (tid == 64) {

@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define CKV_ABI_VERSION 1
+#define CKV_ABI_VERSION 2
 #define CKV_HEAD_DIM 128
 #define CKV_TILE 64
 #define CKV_KAPPA 8
@@ -148,7 +148,8 @@ typedef struct ckv_decode_workspace {
   float* partial_max;          /* [query_heads][slot_tiles] */
   float* partial_sum;          /* [query_heads][slot_tiles] */
   float* partial_acc;          /* [query_heads][slot_tiles][128] */
-  uint64_t* partial_topk;      /* [retrieval_heads][slot_tiles][8] */
+  float* slot_scores;          /* [retrieval_heads][slot_capacity]: scaled score of the group's first query for
+                                  every attended slot, the candidates of the update's exact top-8 */
   void* output;                /* [query_heads][128], kv dtype */
   float* lse;                  /* [query_heads] */
   float* topk_scores;          /* [retrieval_heads][8] */
