@@ -555,6 +555,16 @@ __device__ inline void merge_group(const DecodeArgs& a, const int rh, const int 
   __syncthreads();
 }
 
+// Split merge of the bf16 path: one workgroup per retrieval head.  A kernel of
+// its own: on this GPU an agent-scope release/acquire pair around a
+// last-arriving-workgroup counter costs more than the kernel boundary.
+constexpr int MERGE_SCRATCH = 3 * 1024;  // floats: 3 * G * splits at most
+
+__global__ __launch_bounds__(256) void merge_kernel(DecodeArgs a, int splits) {
+  __shared__ __align__(16) float scratch[MERGE_SCRATCH];
+  merge_group<CKV_BF16>(a, blockIdx.x, splits, scratch, nullptr);
+}
+
 // Sparse bf16 attention: a workgroup of ATT_WAVES waves covers ATT_TILES
 // consecutive 64-slot tiles of one retrieval head; each wave runs mfma_tile on
 // one tile, the workgroup combines its waves in LDS into one split partial
@@ -674,20 +684,24 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attend_mfma_kernel(DecodeArgs 
   CKV_STAMP(rh == 0 && wgi == 0, 2);
   if (!MERGE) return;
   // The last workgroup of this head to finish merges the splits.
+  CKV_STAMP_MAX(rh == 0, 12);
   __threadfence();
   __syncthreads();
+  CKV_STAMP_MAX(rh == 0, 13);
   if (tid == 0) {
     uint32_t* counter = a.ws.block_counters + a.st.retrieval_heads + rh;
     const unsigned prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
     last_block = (prev == (unsigned)splits - 1u) ? 1 : 0;
     if (last_block) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
+  CKV_STAMP_MAX(rh == 0, 14);
   __syncthreads();
   if (!last_block) return;
   __threadfence();
   CKV_STAMP(rh == 0, 3);
   merge_group<CKV_BF16>(a, rh, splits, reinterpret_cast<float*>(att_dyn), nullptr);
   CKV_STAMP(rh == 0, 4);
+  CKV_STAMP_MAX(true, 15);
 }
 
 // Dense bf16 decode baseline: each wave streams `chunk_tiles` consecutive
@@ -758,17 +772,15 @@ int launch_attention(const DecodeArgs& a, hipStream_t s, bool partials_only) {
   const int tiles = a.ws.slot_capacity / TILE;
   if (a.kv.dtype == CKV_BF16) {
     const int splits = attention_splits(a);
-    const size_t lds = (size_t)ATT_WAVES * V_HALF_ROWS * D * sizeof(uint16_t);
-    if ((size_t)3 * a.cfg.group_size * splits * sizeof(float) > lds) {
+    if (3 * a.cfg.group_size * splits > MERGE_SCRATCH) {
       return ckv_internal::set_error(CKV_E_LIMIT, "too many attention splits for the merge scratch");
     }
     const dim3 grid(splits, a.st.retrieval_heads);
-    if (partials_only) {
-      hipLaunchKernelGGL(attend_mfma_kernel<false>, grid, dim3(64 * ATT_WAVES), 0, s, a);
-    } else {
-      hipLaunchKernelGGL(attend_mfma_kernel<true>, grid, dim3(64 * ATT_WAVES), 0, s, a);
-    }
-    return launch_check("attend_mfma");
+    hipLaunchKernelGGL(attend_mfma_kernel<false>, grid, dim3(64 * ATT_WAVES), 0, s, a);
+    const int r = launch_check("attend_mfma");
+    if (r || partials_only) return r;
+    hipLaunchKernelGGL(merge_kernel, dim3(a.st.retrieval_heads), dim3(256), 0, s, a, splits);
+    return launch_check("merge");
   }
   hipLaunchKernelGGL((attend_generic_kernel<CKV_F32, false>), dim3(tiles, a.st.retrieval_heads), dim3(64), 0, s, a, 0,
                      0);

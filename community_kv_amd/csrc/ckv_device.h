@@ -18,9 +18,16 @@ namespace ckv {
   do {                                                               \
     if ((cond) && threadIdx.x == 0) phase_stamp[(slot)] = wall_clock64(); \
   } while (0)
+#define CKV_STAMP_MAX(cond, slot)                                                            \
+  do {                                                                                       \
+    if ((cond) && threadIdx.x == 0) atomicMax(&phase_stamp[(slot)], (unsigned long long)wall_clock64()); \
+  } while (0)
 #else
 #define CKV_STAMP(cond, slot) \
   do {                        \
+  } while (0)
+#define CKV_STAMP_MAX(cond, slot) \
+  do {                            \
   } while (0)
 #endif
 
