@@ -292,11 +292,18 @@ __global__ __launch_bounds__(SELECT_THREADS) void select_kernel(DecodeArgs a, De
       for (int pb = 0; pb < PB; ++pb) {
         float cv[16];
         decode_frag<CT>(frag[pb], cv);
+        // bf16 x e4m3 products have at most 12 significant bits, so they are
+        // exact in f32 and a fused multiply-add equals the pinned multiply-then-add.
         float a0 = qa[0] * cv[0], a1 = qb[0] * cv[0];
 #pragma unroll
         for (int i = 1; i < 16; ++i) {
-          a0 = a0 + qa[i] * cv[i];
-          a1 = a1 + qb[i] * cv[i];
+          if constexpr (CT == CKV_E4M3 && DT == CKV_BF16) {
+            a0 = __builtin_fmaf(qa[i], cv[i], a0);
+            a1 = __builtin_fmaf(qb[i], cv[i], a1);
+          } else {
+            a0 = a0 + qa[i] * cv[i];
+            a1 = a1 + qb[i] * cv[i];
+          }
         }
         a0 = a0 + xor_f32<4>(a0);
         a1 = a1 + xor_f32<4>(a1);
