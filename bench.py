@@ -67,6 +67,38 @@ def zipf_labels(rng, seq, sinks, communities):
     return out
 
 
+PREFILL_SEQ = 32768
+PREFILL_CLUSTERS = 256
+PREFILL_KAPPA = 16
+
+
+def planted_prefill_inputs(device, seq=PREFILL_SEQ, hq=HQ, hkv=HKV, clusters=PREFILL_CLUSTERS, cosine=0.6,
+                           block=128, seed=0):
+    """BASELINE config 5 inputs: q/k/v [1, seq, heads, 128] bf16.  Each
+    ``block``-token block belongs to one of ``clusters`` clusters; a q/k row is
+    sqrt(cosine) * center + sqrt(1 - cosine) * noise with center and noise
+    ~N(0, 1/128) (unit expected norm), so two rows of one cluster have cosine
+    ~``cosine``.  Values ~N(0, 1/128)."""
+    gen = torch.Generator(device=device).manual_seed(seed)
+    blocks = -(-seq // block)
+    lab = torch.randint(0, clusters, (blocks,), device=device, generator=gen).repeat_interleave(block)[:seq]
+    scale = D ** -0.5
+    centers = torch.randn(hkv, clusters, D, device=device, generator=gen) * scale
+    a, b = cosine ** 0.5, (1 - cosine) ** 0.5
+
+    def rows(heads, group):
+        x = torch.empty(1, seq, heads, D, device=device, dtype=torch.bfloat16)
+        for h in range(heads):
+            noise = torch.randn(seq, D, device=device, generator=gen) * scale
+            x[0, :, h] = (a * centers[h // group, lab] + b * noise).to(torch.bfloat16)
+        return x
+
+    k = rows(hkv, 1)
+    q = rows(hq, hq // hkv)  # a query row shares its KV head's cluster centers
+    v = (torch.randn(1, seq, hkv, D, device=device, generator=gen) * scale).to(torch.bfloat16)
+    return q, k, v
+
+
 def build_stack(device, layers, max_decode, seed=0):
     cfg = CommunityKVConfig(token_budget=BUDGET, num_sink=SINKS, lam=0.5, aggregation=GraphAggregation.QUERY_GROUP,
                             local_window=WINDOW)
@@ -195,6 +227,81 @@ def cpu_baseline(entry, seconds=20.0):
                       f"({per_layer_step * 1e3:.1f} ms per layer-step), scaled to 36 layers"}
 
 
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def prefill_cpu_baseline(q, k, v, scale, sinks, kappa, seconds):
+    """Oracle prefill rows (numpy, one core) at evenly spaced positions of the
+    same inputs, scaled to the whole prefill by each row's causal length."""
+    from threadpoolctl import threadpool_limits
+
+    from oracle import prefill as op
+
+    S, Hq = q.shape[1], q.shape[2]
+    qn = q[0].float().cpu().numpy()
+    kn = k[0].float().cpu().numpy()
+    vn = v[0].float().cpu().numpy()
+    rng = np.random.default_rng(1)
+    done_cols, n, t0 = 0, 0, time.perf_counter()
+    with threadpool_limits(limits=1):
+        while time.perf_counter() - t0 < seconds and n < 4096:
+            r = int(rng.integers(0, S))
+            h = int(rng.integers(0, Hq))
+            op.prefill_rows(qn, kn, vn, [r], [h], softmax_scale=scale, num_sink=sinks, kappa=kappa)
+            done_cols += r + 1
+            n += 1
+    el = time.perf_counter() - t0
+    total_cols = Hq * S * (S + 1) / 2
+    seconds_full = el * total_cols / done_cols
+    return {"value": 1.0 / seconds_full, "unit": "prefills/s", "cores": 1, "kind": "port",
+            "sample": f"{n} random (row, head) pairs of the config-5 prefill through the numpy oracle "
+                      f"({done_cols} score columns in {el:.1f} s), scaled by causal columns to the whole prefill"}
+
+
+def run_prefill(args, device):
+    from community_kv_amd.attention.flash_attention import prefill_attention_topk
+
+    q, k, v = planted_prefill_inputs(device, seq=args.prefill_seq)
+    S = q.shape[1]
+    scale = D ** -0.5
+    run = lambda: prefill_attention_topk(q, k, v, softmax_scale=scale, num_sink=SINKS, kappa=PREFILL_KAPPA)
+    for _ in range(args.warmup):
+        run()
+    torch.cuda.synchronize(device)
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(args.steps):
+        run()
+    stop.record()
+    torch.cuda.synchronize(device)
+    ms = start.elapsed_time(stop) / args.steps
+    flops = 4.0 * D * HQ * S * (S + 1) / 2  # causal QK^T + PV
+    tflops = flops / (ms * 1e-3) / 1e12
+    result = {
+        "metric": "prefill_edge_export_ms_32k_qwen3_8b_layer",
+        "value": ms,
+        "unit": "ms",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (planted 256-cluster q/k blocks, cosine 0.6; N(0,1/128) values)",
+        "config": {"workload": "BASELINE config 5: causal prefill, 32/8 heads, head_dim 128, top-16 edges per row",
+                   "seq_len": S, "query_heads": HQ, "kv_heads": HKV, "kappa": PREFILL_KAPPA, "num_sink": SINKS},
+        "roofline": {"bound": "mfma", "achieved": tflops, "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": tflops / MFMA_BF16_PEAK_TFLOPS, "traffic": None,
+                     "kernel": "prefill_mfma_kernel<16>", "flops_per_launch": flops},
+    }
+    if not args.no_cpu:
+        result["cpu_baseline"] = prefill_cpu_baseline(q, k, v, scale, SINKS, PREFILL_KAPPA, args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -203,6 +310,9 @@ def main():
     ap.add_argument("--layers", type=int, default=LAYERS)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--workload", choices=["decode", "prefill"], default="decode",
+                    help="decode: the 36-layer sparse decode step (default); prefill: config-5 edge export")
+    ap.add_argument("--prefill-seq", type=int, default=PREFILL_SEQ)
     ap.add_argument("--copy-probe", action="store_true",
                     help="after timing, one plain 256 MiB device-to-device copy (counter calibration)")
     args = ap.parse_args()
@@ -210,6 +320,9 @@ def main():
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1"}))
         sys.exit(2)
     device = torch.device("cuda:0")
+    if args.workload == "prefill":
+        run_prefill(args, device)
+        return
     max_decode = args.warmup + args.steps + max(5, args.steps // 2) + 16  # every full step replay appends one token
     runtime, stack = build_stack(device, args.layers, max_decode)
     torch.cuda.synchronize(device)

@@ -23,8 +23,9 @@ def prefill_attention_topk(query: torch.Tensor, key: torch.Tensor, value: torch.
     """Causal GQA attention over q [B=1, S, Hq, 128], k/v [1, S, Hkv, 128] (bf16)
     plus each row's top-``kappa`` columns in [num_sink, row] for rows
     >= num_sink + kappa - 1.  ``topk_val`` holds the reference probability
-    exp(s_q * scale - lse) of the quantised score, or the raw q.k score when
-    ``raw_scores``."""
+    exp(s_q * scale - lse) of the quantised score s_q, or s_q itself (the raw
+    q.k score to within 1/512) when ``raw_scores``.  Selection is exact per row:
+    largest quantised score first, equal scores to the larger column."""
     if query.ndim != 4 or key.ndim != 4 or value.shape != key.shape:
         raise ValueError("prefill expects q [B, S, Hq, 128] and k/v [B, S, Hkv, 128]")
     if query.shape[0] != 1 or key.shape[0] != 1:

@@ -5,164 +5,361 @@
 // fused selection 250-357, WarpSelect 477-723).  Differences by design: the
 // per-row selection is exact (the reference keeps six candidates per lane and
 // merges four lanes, an approximation), kappa is a parameter (<= 16) and the
-// stored value can be the reference probability or the raw q.k score.
+// stored value can be the reference probability or the dequantised raw score.
 //
-// prefill_rowwise_kernel: grid (ceil(S/64), query_heads) x 64.  One lane owns
-// one query row: q and the output accumulator live in registers, K/V tiles of
-// 64 rows are staged through LDS as bf16, the softmax is online per tile, and
-// the row's candidates are kept in a sorted register queue of packed
-// (quantised score << 17 | column) keys.
+// prefill_mfma_kernel: one workgroup = 4 waves = 128 packed rows
+// (row r <-> position r / G, query head kv_head * G + r % G, PackGQA), so every
+// K/V tile staged in LDS serves all G query heads of the KV head.  Each wave
+// owns 32 packed rows and computes S^T = K Q^T with v_mfma_f32_32x32x16_bf16:
+// the accumulator puts one query row in each lane (lane % 32) and 16 of the
+// tile's keys per lane half, so the row max / sum / top-kappa are per-lane
+// register work plus one lane ^ 32 exchange.  O^T = V^T P^T uses the same row
+// mapping; V^T operands come from LDS with ds_read_b64_tr_b16.
+//
+// Top-kappa: each lane keeps a sorted queue of packed keys
+// (quantised score << 17 | column + 1) for the columns of its half; a tile is
+// inspected only when the lane's tile maximum reaches the current threshold
+// (the larger of the two halves' worst kept keys), and the two queues are
+// merged exactly at the end.
 #include <hip/hip_runtime.h>
 
+#include <float.h>
 #include <stdio.h>
 #include <string.h>
 
-#include "../../include/ckv_amd.h"
+#include "ckv_device.h"
 #include "ckv_error.h"
-#include "ckv_numerics.h"
 
 namespace {
+using namespace ckv;
 
 constexpr int D = CKV_HEAD_DIM;
-constexpr int ROWS = 64;
-constexpr int COLS = 64;
+constexpr int PF_WAVES = 4;
+constexpr int PF_ROWS = 32 * PF_WAVES;  // packed (position, head) rows per workgroup
+constexpr int PF_KEYS = 64;             // keys per LDS tile
+constexpr int K_STRIDE = D + 8;         // 272-byte K rows: 16-lane b128 reads hit distinct banks
+constexpr int V_STRIDE = D + 32;        // 320-byte V rows: transposed b64 reads hit distinct banks
+constexpr int K_TILE = PF_KEYS * K_STRIDE;
+constexpr int V_TILE = PF_KEYS * V_STRIDE;
+constexpr int STAGE = K_TILE + V_TILE;  // elements per pipeline stage
+constexpr size_t PF_LDS_BYTES = 2 * STAGE * sizeof(uint16_t);
 constexpr int MAX_KAPPA = 16;
+constexpr int MAX_SEQ = (1 << 17) - 1;  // column + 1 must fit the 17-bit index field
 constexpr float NEG_INF = -__builtin_huge_valf();
+constexpr float LOG2E = 1.4426950408889634f;
+constexpr float LN2 = 0.6931471805599453f;
 
-// Reference quantisation (community-kv.patch:508-516): key = clamp(rint((s + 48) * 256), 0, 32767).
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+__device__ inline f32x16_t mfma32(uint4 a, uint4 b, f32x16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c,
+                                                 0, 0, 0);
+}
+
+__device__ inline uint2 lds_tr16(const uint16_t* p) {
+  typedef short s16x4_t __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) s16x4_t* lds_s16x4_ptr;
+  const s16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(const_cast<uint16_t*>(p)));
+  return __builtin_bit_cast(uint2, v);
+}
+
+__device__ inline uint32_t swap32_u32(uint32_t v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return (lane_id() & 32) ? (uint32_t)r[0] : (uint32_t)r[1];
+}
+
+// Reference quantisation (community-kv.patch:508-512), float32 operations:
+// clamp(rint((s + 48) * 256), 0, 32767).
 __device__ inline uint32_t quantise_score(float s) {
-  float k = (s + 48.0f) * 256.0f;
+  float k = __fmul_rn(__fadd_rn(s, 48.0f), 256.0f);
   k = __builtin_rintf(k);
   k = k < 0.0f ? 0.0f : (k > 32767.0f ? 32767.0f : k);
   return (uint32_t)k;
 }
 
-__global__ __launch_bounds__(ROWS) void prefill_rowwise_kernel(ckv_prefill_args a) {
-  const int lane = threadIdx.x;
-  const int qh = blockIdx.y;
-  const int row0 = blockIdx.x * ROWS;
-  const int row = row0 + lane;
+// Scores below this cannot reach a packed key above `thr`: quantise(s) >= key
+// needs s >= (key - 0.5) / 256 - 48, and a margin of half a step absorbs the
+// float32 rounding of (s + 48) * 256.  An empty threshold admits every finite
+// score.
+__device__ inline float prefilter(uint32_t thr) {
+  const uint32_t key = thr >> 17;
+  return key == 0 ? -FLT_MAX : (float)(int)(key - 1) * (1.0f / 256.0f) - 48.0f;
+}
+
+template <int QN>
+__device__ inline void queue_insert(uint32_t (&q)[QN], uint32_t cand) {
+#pragma unroll
+  for (int i = 0; i < QN; ++i) {
+    const uint32_t hi = q[i] > cand ? q[i] : cand;
+    cand = q[i] > cand ? cand : q[i];
+    q[i] = hi;
+  }
+}
+
+template <int QN>
+__global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_mfma_kernel(ckv_prefill_args a, int group, int blocks) {
+  extern __shared__ __align__(16) uint16_t pf_lds[];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int row = lane & 31;
+  const int half = lane >> 5;
+  const int kv_heads = a.kv_heads;
+  // Longest (latest) row blocks first; consecutive workgroups cycle over the KV
+  // heads, so each XCD streams the K/V of few heads through its L2.
+  const int blk = blocks - 1 - (int)(blockIdx.x / kv_heads);
+  const int kvh = (int)(blockIdx.x % kv_heads);
   const int S = a.seq_len;
-  const int group = a.query_heads / a.kv_heads;
-  const int kvh = qh / group;
-  const int kappa = a.kappa;
-  const float scale = a.softmax_scale;
+  const int64_t pr0 = (int64_t)blk * PF_ROWS;
+  const int64_t pr = pr0 + wave * 32 + row;
+  const int pos = (int)(pr / group);
+  const int head = kvh * group + (int)(pr % group);
+  const bool row_ok = pos < S;
+  const int pos_lo = (int)(pr0 / group);
+  const int pos_hi = min(S - 1, (int)((pr0 + PF_ROWS - 1) / group));
+  const int tiles = pos_hi / PF_KEYS + 1;
+  const float sl2 = a.softmax_scale * LOG2E;
+
   const uint16_t* Q = reinterpret_cast<const uint16_t*>(a.query);
-  const uint16_t* K = reinterpret_cast<const uint16_t*>(a.key);
-  const uint16_t* V = reinterpret_cast<const uint16_t*>(a.value);
+  const uint16_t* Kg = reinterpret_cast<const uint16_t*>(a.key) + (int64_t)kvh * a.k_head_stride;
+  const uint16_t* Vg = reinterpret_cast<const uint16_t*>(a.value) + (int64_t)kvh * a.k_head_stride;
+  const int64_t kstride = a.k_row_stride;
 
-  __shared__ uint16_t k_s[COLS][D + 8];
-  __shared__ uint16_t v_s[COLS][D + 8];
+  // Q^T B operand: lane (row, half) holds dims 16c + 8 half .. +7 for c = 0..7.
+  uint4 qreg[8];
+  {
+    const uint16_t* qp = Q + (int64_t)(row_ok ? pos : 0) * a.q_row_stride + (int64_t)head * a.q_head_stride + 8 * half;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) qreg[c] = row_ok ? gload16(qp + 16 * c) : uint4{0u, 0u, 0u, 0u};
+  }
 
-  const bool row_ok = row < S;
-  float q[D];
-  float acc[D];
+  // Staging: thread tid moves 16-byte chunks tid + 256 j (key chunk / 16, dims 8 * (chunk % 16)).
+  uint4 kr[4], vr[4];
+  auto load_tile = [&](int t) {
 #pragma unroll
-  for (int d = 0; d < D; ++d) {
-    q[d] = row_ok ? ckv_bf16_to_f32(Q[(int64_t)row * a.q_row_stride + (int64_t)qh * a.q_head_stride + d]) : 0.0f;
-    acc[d] = 0.0f;
-  }
-  uint32_t qkey[MAX_KAPPA];
-  float qraw[MAX_KAPPA];
-#pragma unroll
-  for (int i = 0; i < MAX_KAPPA; ++i) {
-    qkey[i] = 0u;
-    qraw[i] = NEG_INF;
-  }
-  float m = NEG_INF;
-  float l = 0.0f;
-  const int last_row = min(row0 + ROWS, S) - 1;
-  for (int c0 = 0; c0 <= last_row; c0 += COLS) {
-    __syncthreads();
-    for (int i = lane; i < COLS * (D / 8); i += ROWS) {
-      const int r = i / (D / 8);
-      const int d8 = (i % (D / 8)) * 8;
-      const int c = c0 + r;
-      uint4 kv = {0u, 0u, 0u, 0u}, vv = {0u, 0u, 0u, 0u};
-      if (c < S) {
-        const int64_t off = (int64_t)c * a.k_row_stride + (int64_t)kvh * a.k_head_stride + d8;
-        kv = *reinterpret_cast<const uint4*>(K + off);
-        vv = *reinterpret_cast<const uint4*>(V + off);
-      }
-      const uint16_t kw[8] = {(uint16_t)kv.x, (uint16_t)(kv.x >> 16), (uint16_t)kv.y, (uint16_t)(kv.y >> 16),
-                              (uint16_t)kv.z, (uint16_t)(kv.z >> 16), (uint16_t)kv.w, (uint16_t)(kv.w >> 16)};
-      const uint16_t vw[8] = {(uint16_t)vv.x, (uint16_t)(vv.x >> 16), (uint16_t)vv.y, (uint16_t)(vv.y >> 16),
-                              (uint16_t)vv.z, (uint16_t)(vv.z >> 16), (uint16_t)vv.w, (uint16_t)(vv.w >> 16)};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        k_s[r][d8 + e] = kw[e];
-        v_s[r][d8 + e] = vw[e];
+    for (int j = 0; j < 4; ++j) {
+      const int idx = tid + 64 * PF_WAVES * j;
+      const int key = t * PF_KEYS + (idx >> 4);
+      const int64_t off = (int64_t)min(key, S - 1) * kstride + (idx & 15) * 8;
+      kr[j] = gload16(Kg + off);
+      vr[j] = gload16(Vg + off);
+      if (key >= S) {
+        kr[j] = uint4{0u, 0u, 0u, 0u};
+        vr[j] = uint4{0u, 0u, 0u, 0u};
       }
     }
-    __syncthreads();
-    if (!row_ok) continue;
-    float s[COLS];
-    float tile_max = NEG_INF;
-    for (int j = 0; j < COLS; ++j) {
-      const int c = c0 + j;
-      float dot = 0.0f;
+  };
+  auto store_tile = [&](int stage) {
+    uint16_t* k_s = pf_lds + stage * STAGE;
+    uint16_t* v_s = k_s + K_TILE;
 #pragma unroll
-      for (int d = 0; d < D; ++d) dot = dot + q[d] * ckv_bf16_to_f32(k_s[j][d]);
-      const bool ok = c <= row && c < S;
-      s[j] = ok ? dot : NEG_INF;
-      if (ok) {
-        const float sc = dot * scale;
-        tile_max = sc > tile_max ? sc : tile_max;
-        if (c >= a.num_sink) {
-          const uint32_t cand = (quantise_score(dot) << 17) | ((uint32_t)c & 0x1ffffu);
-          if (cand > qkey[kappa - 1]) {
-            uint32_t ck = cand;
-            float cr = dot;
+    for (int j = 0; j < 4; ++j) {
+      const int idx = tid + 64 * PF_WAVES * j;
+      const int key = idx >> 4;
+      const int d8 = (idx & 15) * 8;
+      *reinterpret_cast<uint4*>(k_s + key * K_STRIDE + d8) = kr[j];
+      *reinterpret_cast<uint4*>(v_s + key * V_STRIDE + d8) = vr[j];
+    }
+  };
+
+  f32x16_t o[4];
 #pragma unroll
-            for (int i = 0; i < MAX_KAPPA; ++i) {
-              if (i < kappa && ck > qkey[i]) {
-                const uint32_t tk = qkey[i];
-                const float tr = qraw[i];
-                qkey[i] = ck;
-                qraw[i] = cr;
-                ck = tk;
-                cr = tr;
-              }
+  for (int db = 0; db < 4; ++db) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) o[db][v] = 0.0f;
+  }
+  uint32_t qk[QN];
+#pragma unroll
+  for (int i = 0; i < QN; ++i) qk[i] = 0u;
+  float m = NEG_INF;  // running max of the raw score (scale > 0)
+  float l = 0.0f;     // this half's share of the softmax denominator
+
+  load_tile(0);
+  store_tile(0);
+  __syncthreads();
+
+  for (int t = 0; t < tiles; ++t) {
+    const bool more = t + 1 < tiles;
+    if (more) load_tile(t + 1);
+    const uint16_t* k_s = pf_lds + (t & 1) * STAGE;
+    const uint16_t* v_s = k_s + K_TILE;
+
+    // S^T (keys x rows): accumulator b holds keys 32 b + 8 (v / 4) + 4 half + v % 4.
+    f32x16_t sacc[2];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) sacc[b][v] = 0.0f;
+    }
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        const uint4 kf = *reinterpret_cast<const uint4*>(k_s + (32 * b + row) * K_STRIDE + 16 * c + 8 * half);
+        sacc[b] = mfma32(kf, qreg[c], sacc[b]);
+      }
+    }
+    const int c0 = t * PF_KEYS;
+    if (c0 + PF_KEYS - 1 > pos_lo) {
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int col = c0 + 32 * b + 8 * (v >> 2) + 4 * half + (v & 3);
+          if (col > pos) sacc[b][v] = NEG_INF;
+        }
+      }
+    }
+    float lmax = NEG_INF;
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) lmax = fmax_exact(lmax, sacc[b][v]);
+    }
+
+    // Top-kappa candidates of this lane's 32 columns.
+    uint32_t thr = qk[QN - 1];
+    thr = max(thr, swap32_u32(thr));
+    float tf = prefilter(thr);
+    if (lmax >= tf) {
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const float s = sacc[b][v];
+          const int col = c0 + 32 * b + 8 * (v >> 2) + 4 * half + (v & 3);
+          if (s >= tf && col >= a.num_sink) {
+            const uint32_t cand = (quantise_score(s) << 17) | (uint32_t)(col + 1);
+            if (cand > thr) {
+              queue_insert<QN>(qk, cand);
+              thr = max(thr, qk[QN - 1]);
+              tf = prefilter(thr);
             }
           }
         }
       }
     }
-    if (tile_max == NEG_INF) continue;
-    const float m_new = m > tile_max ? m : tile_max;
-    const float corr = (m == NEG_INF) ? 0.0f : __expf(m - m_new);
-    l = l * corr;
-#pragma unroll
-    for (int d = 0; d < D; ++d) acc[d] = acc[d] * corr;
-    for (int j = 0; j < COLS; ++j) {
-      if (s[j] == NEG_INF) continue;
-      const float p = __expf(s[j] * scale - m_new);
-      l = l + p;
-      const float pb = ckv_bf16_to_f32(ckv_f32_to_bf16_bits(p));
-#pragma unroll
-      for (int d = 0; d < D; ++d) acc[d] = acc[d] + pb * ckv_bf16_to_f32(v_s[j][d]);
-    }
+
+    // Online softmax in base 2; both halves of a row share the max.
+    const float tmax = max_xor32(lmax);
+    const float m_new = fmax_exact(m, tmax);
+    const float mc = m_new == NEG_INF ? 0.0f : m_new * sl2;
+    const float alpha = m == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(m * sl2 - mc);
     m = m_new;
-  }
-  if (!row_ok) return;
-  uint16_t* O = reinterpret_cast<uint16_t*>(a.output);
-  const float inv = 1.0f / l;
+    l *= alpha;
 #pragma unroll
-  for (int d = 0; d < D; ++d) {
-    O[(int64_t)row * a.o_row_stride + (int64_t)qh * a.o_head_stride + d] = ckv_f32_to_bf16_bits(acc[d] * inv);
+    for (int db = 0; db < 4; ++db) o[db] *= alpha;
+    uint32_t pb[2][8];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+#pragma unroll
+      for (int v = 0; v < 16; v += 2) {
+        const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[b][v], sl2, -mc));
+        const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[b][v + 1], sl2, -mc));
+        l += p0;
+        l += p1;
+        pb[b][v >> 1] = pack_bf16x2_hw(p0, p1);
+      }
+    }
+
+    // O^T (dims x rows) += V^T P^T over four 16-key chunks.  Chunk kc pairs
+    // P registers 8 (kc % 2) .. +7 of accumulator kc / 2 (keys 16 kc + 4 half +
+    // e % 4 + 8 (e / 4)) with V^T rows read transposed for the same keys.
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc) {
+      const int b = kc >> 1;
+      const int vb = 4 * (kc & 1);
+      const uint4 bop = uint4{pb[b][vb], pb[b][vb + 1], pb[b][vb + 2], pb[b][vb + 3]};
+      const uint16_t* vrow = v_s + (16 * kc + 4 * half + ((lane & 15) >> 2)) * V_STRIDE + 16 * ((lane >> 4) & 1) +
+                             4 * (lane & 3);
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        const uint2 lo = lds_tr16(vrow + 32 * db);
+        const uint2 hi = lds_tr16(vrow + 8 * V_STRIDE + 32 * db);
+        o[db] = mfma32(uint4{lo.x, lo.y, hi.x, hi.y}, bop, o[db]);
+      }
+    }
+    if (more) store_tile((t + 1) & 1);
+    __syncthreads();
   }
-  const float lse = m + __logf(l);
-  a.lse[(int64_t)qh * S + row] = lse;
-  if (row >= a.topk_skip && a.topk_scores && a.topk_indices) {
-    const int64_t base = ((int64_t)qh * a.topk_rows + (row - a.topk_skip)) * kappa;
-    for (int i = 0; i < MAX_KAPPA; ++i) {
-      if (i >= kappa) break;
-      const uint32_t key = qkey[i] >> 17;
-      a.topk_indices[base + i] = (int32_t)(qkey[i] & 0x1ffffu);
-      a.topk_scores[base + i] =
-          a.score_kind == 0 ? __expf(((float)key * (1.0f / 256.0f) - 48.0f) * scale - lse) : qraw[i];
+
+  if (!row_ok) return;
+  const float l_tot = add_xor32(l);
+  const float inv = 1.0f / l_tot;
+  const float lse = (m * sl2 + __builtin_amdgcn_logf(l_tot)) * LN2;
+  uint16_t* O = reinterpret_cast<uint16_t*>(a.output) + (int64_t)pos * a.o_row_stride + (int64_t)head * a.o_head_stride;
+#pragma unroll
+  for (int db = 0; db < 4; ++db) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int dim = 32 * db + 8 * g + 4 * half;
+      const uint2 w = uint2{pack_bf16x2_hw(o[db][4 * g] * inv, o[db][4 * g + 1] * inv),
+                            pack_bf16x2_hw(o[db][4 * g + 2] * inv, o[db][4 * g + 3] * inv)};
+      *reinterpret_cast<uint2*>(O + dim) = w;
     }
   }
+  if (half == 0) a.lse[(int64_t)head * S + pos] = lse;
+
+  // Exact merge of the two halves' sorted queues: the larger of a[i] and
+  // b[QN-1-i] is a bitonic sequence holding the best QN of the union.
+  uint32_t c[QN];
+#pragma unroll
+  for (int i = 0; i < QN; ++i) c[i] = qk[i];
+  uint32_t other[QN];
+#pragma unroll
+  for (int i = 0; i < QN; ++i) other[i] = swap32_u32(qk[i]);
+#pragma unroll
+  for (int i = 0; i < QN; ++i) c[i] = max(c[i], other[QN - 1 - i]);
+#pragma unroll
+  for (int j = QN / 2; j >= 1; j >>= 1) {
+#pragma unroll
+    for (int i = 0; i < QN; ++i) {
+      if ((i & j) == 0) {
+        const uint32_t hi = max(c[i], c[i + j]);
+        const uint32_t lo = min(c[i], c[i + j]);
+        c[i] = hi;
+        c[i + j] = lo;
+      }
+    }
+  }
+  if (pos < a.topk_skip || !a.topk_scores || !a.topk_indices) return;
+  const int kappa = a.kappa;
+  const int64_t base = ((int64_t)head * a.topk_rows + (pos - a.topk_skip)) * kappa;
+#pragma unroll
+  for (int i = 0; i < QN; ++i) {
+    if (i < kappa) {
+      const float deq = (float)(c[i] >> 17) * (1.0f / 256.0f) - 48.0f;
+      if (half == 0) {
+        a.topk_scores[base + i] = a.score_kind == 0 ? expf(deq * a.softmax_scale - lse) : deq;
+      } else {
+        a.topk_indices[base + i] = c[i] == 0u ? -1 : (int32_t)(c[i] & 0x1ffffu) - 1;
+      }
+    }
+  }
+}
+
+template <int QN>
+int launch_prefill(const ckv_prefill_args& a, hipStream_t s) {
+  const int group = a.query_heads / a.kv_heads;
+  const int64_t packed = (int64_t)a.seq_len * group;
+  const int blocks = (int)((packed + PF_ROWS - 1) / PF_ROWS);
+  auto kernel = prefill_mfma_kernel<QN>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)PF_LDS_BYTES);
+    if (e != hipSuccess) {
+      (void)hipGetLastError();
+      return ckv_internal::set_error(CKV_E_LAUNCH, hipGetErrorString(e));
+    }
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(kernel, dim3((unsigned)blocks * a.kv_heads), dim3(64 * PF_WAVES), PF_LDS_BYTES, s, a, group,
+                     blocks);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return ckv_internal::set_error(CKV_E_LAUNCH, hipGetErrorString(e));
+  return CKV_OK;
 }
 
 }  // namespace
@@ -171,22 +368,30 @@ extern "C" int ckv_prefill_attention_topk(const ckv_prefill_args* a, void* strea
   if (!a || !a->query || !a->key || !a->value || !a->output || !a->lse) {
     return ckv_internal::set_error(CKV_E_INVALID, "null prefill argument");
   }
-  if (a->seq_len <= 0 || a->seq_len > (1 << 17)) {
-    return ckv_internal::set_error(CKV_E_LIMIT, "seq_len must be in [1, 131072] (17-bit column keys)");
+  if (a->seq_len <= 0 || a->seq_len > MAX_SEQ) {
+    return ckv_internal::set_error(CKV_E_LIMIT, "seq_len must be in [1, 131071] (column + 1 fills a 17-bit field)");
   }
-  if (a->kv_heads <= 0 || a->query_heads % a->kv_heads || a->kappa < 1 || a->kappa > MAX_KAPPA) {
+  if (a->kv_heads <= 0 || a->query_heads <= 0 || a->query_heads % a->kv_heads || a->kappa < 1 ||
+      a->kappa > MAX_KAPPA) {
     return ckv_internal::set_error(CKV_E_INVALID, "bad head counts or kappa (1..16)");
   }
-  if (a->topk_skip < 0 || a->topk_rows != (a->seq_len > a->topk_skip ? a->seq_len - a->topk_skip : 0)) {
-    return ckv_internal::set_error(CKV_E_INVALID, "topk_rows must equal seq_len - topk_skip");
+  if (a->num_sink < 0 || a->topk_skip != a->num_sink + a->kappa - 1 ||
+      a->topk_rows != (a->seq_len > a->topk_skip ? a->seq_len - a->topk_skip : 0)) {
+    return ckv_internal::set_error(CKV_E_INVALID,
+                                   "topk_skip must be num_sink + kappa - 1 and topk_rows seq_len - topk_skip");
   }
-  if (a->q_row_stride % 8 || a->q_head_stride % 8 || a->k_row_stride % 8 || a->k_head_stride % 8) {
-    return ckv_internal::set_error(CKV_E_INVALID, "q/k/v strides must be multiples of 8 elements");
+  if (a->topk_rows > 0 && (!a->topk_scores || !a->topk_indices)) {
+    return ckv_internal::set_error(CKV_E_INVALID, "null top-k output");
+  }
+  if (!(a->softmax_scale > 0.0f) || (a->score_kind != 0 && a->score_kind != 1)) {
+    return ckv_internal::set_error(CKV_E_INVALID, "softmax_scale must be positive and score_kind 0 or 1");
+  }
+  if (a->q_row_stride % 8 || a->q_head_stride % 8 || a->k_row_stride % 8 || a->k_head_stride % 8 ||
+      a->o_row_stride % 4 || a->o_head_stride % 4) {
+    return ckv_internal::set_error(CKV_E_INVALID, "q/k/v strides must be multiples of 8 elements, output of 4");
   }
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(prefill_rowwise_kernel, dim3((a->seq_len + ROWS - 1) / ROWS, a->query_heads), dim3(ROWS), 0,
-                     s, *a);
-  const hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return ckv_internal::set_error(CKV_E_LAUNCH, hipGetErrorString(e));
-  return CKV_OK;
+  if (a->kappa <= 4) return launch_prefill<4>(*a, s);
+  if (a->kappa <= 8) return launch_prefill<8>(*a, s);
+  return launch_prefill<16>(*a, s);
 }

@@ -172,7 +172,8 @@ typedef struct ckv_decode_workspace {
  * [query_heads][topk_rows][kappa].  Ranking key: the raw q.k score quantised as
  * clamp(rint((s + 48) * 256), 0, 32767), ties to the larger column (the
  * reference's packed key).  score_kind 0 stores the reference value
- * exp((key/256 - 48) * scale - lse); 1 stores the raw score q.k. */
+ * exp((key/256 - 48) * scale - lse); 1 stores the dequantised raw score
+ * key/256 - 48 (within 1/512 of q.k).  seq_len <= 131071. */
 typedef struct ckv_prefill_args {
   const void* query;
   const void* key;
@@ -194,7 +195,7 @@ typedef struct ckv_prefill_args {
   int32_t kappa;         /* 1..16 */
   int32_t topk_rows;     /* seq_len - topk_skip */
   int32_t topk_skip;     /* num_sink + kappa - 1 */
-  int32_t score_kind;
+  int32_t score_kind;    /* 0 probability, 1 dequantised raw score */
   float softmax_scale;
   float reserved;
 } ckv_prefill_args;
