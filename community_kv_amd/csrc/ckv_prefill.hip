@@ -27,6 +27,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <type_traits>
+
 #include "ckv_device.h"
 #include "ckv_error.h"
 
@@ -37,8 +39,8 @@ constexpr int D = CKV_HEAD_DIM;
 constexpr int PF_WAVES = 4;
 constexpr int PF_ROWS = 32 * PF_WAVES;  // packed (position, head) rows per workgroup
 constexpr int PF_KEYS = 64;             // keys per LDS tile
-constexpr int K_STRIDE = D + 8;         // 272-byte K rows: 16-lane b128 reads hit distinct banks
-constexpr int V_STRIDE = D + 32;        // 320-byte V rows: transposed b64 reads hit distinct banks
+constexpr int K_STRIDE = D + 8;         // 272-byte (17-chunk) K rows: 16-lane b128 reads hit distinct banks
+constexpr int V_STRIDE = D + 32;        // 320-byte (20-chunk) V rows: transposed b64 reads hit distinct banks
 constexpr int K_TILE = PF_KEYS * K_STRIDE;
 constexpr int V_TILE = PF_KEYS * V_STRIDE;
 constexpr int STAGE = K_TILE + V_TILE;  // elements per pipeline stage
@@ -48,6 +50,9 @@ constexpr int MAX_SEQ = (1 << 17) - 1;  // column + 1 must fit the 17-bit index 
 constexpr float NEG_INF = -__builtin_huge_valf();
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float LN2 = 0.6931471805599453f;
+constexpr float RESCALE_LOG2 = 8.0f;
+// s_waitcnt immediate for vmcnt(0) (expcnt and lgkmcnt left at their maxima).
+constexpr int VMCNT0 = 0x0F70;
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
@@ -64,6 +69,18 @@ __device__ inline uint2 lds_tr16(const uint16_t* p) {
   return __builtin_bit_cast(uint2, v);
 }
 
+// global_load_lds_dwordx4 with an SGPR base and a per-lane byte offset: lane
+// i's 16 bytes land at LDS byte address lds_addr + 16 i.  Written as inline
+// assembly so that the compiler does not order this wave's LDS reads behind
+// it; the caller waits (vmcnt) and synchronises before reading the chunks.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ inline void lds_dma16(const void* gbase, uint32_t voff, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(gbase), "s"(lds_addr)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
 __device__ inline uint32_t swap32_u32(uint32_t v) {
   const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
   return (lane_id() & 32) ? (uint32_t)r[0] : (uint32_t)r[1];
@@ -74,7 +91,7 @@ __device__ inline uint32_t swap32_u32(uint32_t v) {
 __device__ inline uint32_t quantise_score(float s) {
   float k = __fmul_rn(__fadd_rn(s, 48.0f), 256.0f);
   k = __builtin_rintf(k);
-  k = k < 0.0f ? 0.0f : (k > 32767.0f ? 32767.0f : k);
+  k = __builtin_amdgcn_fmed3f(k, 0.0f, 32767.0f);
   return (uint32_t)k;
 }
 
@@ -87,13 +104,17 @@ __device__ inline float prefilter(uint32_t thr) {
   return key == 0 ? -FLT_MAX : (float)(int)(key - 1) * (1.0f / 256.0f) - 48.0f;
 }
 
+// Insertion into a descending queue: the new entry i is the median of the
+// old entries i-1, i and the candidate (one v_med3_u32 per entry).
 template <int QN>
 __device__ inline void queue_insert(uint32_t (&q)[QN], uint32_t cand) {
+  uint32_t prev = q[0];
+  q[0] = max(q[0], cand);
 #pragma unroll
-  for (int i = 0; i < QN; ++i) {
-    const uint32_t hi = q[i] > cand ? q[i] : cand;
-    cand = q[i] > cand ? cand : q[i];
-    q[i] = hi;
+  for (int i = 1; i < QN; ++i) {
+    const uint32_t cur = q[i];
+    q[i] = max(min(prev, cur), min(max(prev, cur), cand));
+    prev = cur;
   }
 }
 
@@ -134,32 +155,43 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_mfma_kernel(ckv_pref
     for (int c = 0; c < 8; ++c) qreg[c] = row_ok ? gload16(qp + 16 * c) : uint4{0u, 0u, 0u, 0u};
   }
 
-  // Staging: thread tid moves 16-byte chunks tid + 256 j (key chunk / 16, dims 8 * (chunk % 16)).
-  uint4 kr[4], vr[4];
-  auto load_tile = [&](int t) {
+  // Staging: K/V tiles go straight from global memory to LDS
+  // (global_load_lds_dwordx4: lane i of a wave instruction fills the 16-byte
+  // LDS chunk base + i).  A K tile is 64 rows x 17 chunks (16 data + 1 pad),
+  // a V tile 64 rows x 20 chunks; wave w issues the instructions n = w + 4 j.
+  // Pad chunks load the row's first chunk (never read).  Byte offsets of each
+  // lane's source within a tile are fixed; the tile base is uniform.
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  int k_src[5], v_src[5];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int idx = tid + 64 * PF_WAVES * j;
-      const int key = t * PF_KEYS + (idx >> 4);
-      const int64_t off = (int64_t)min(key, S - 1) * kstride + (idx & 15) * 8;
-      kr[j] = gload16(Kg + off);
-      vr[j] = gload16(Vg + off);
-      if (key >= S) {
-        kr[j] = uint4{0u, 0u, 0u, 0u};
-        vr[j] = uint4{0u, 0u, 0u, 0u};
+  for (int j = 0; j < 5; ++j) {
+    const int p = (wave_u + 4 * j) * 64 + lane;
+    const int kc = p % 17;
+    k_src[j] = (int)((int64_t)(p / 17) * kstride * 2) + 16 * (kc == 16 ? 0 : kc);
+    const int vc = p % 20;
+    v_src[j] = (int)((int64_t)(p / 20) * kstride * 2) + 16 * (vc >= 16 ? 0 : vc);
+  }
+  const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)pf_lds;
+  auto issue_tile = [&](int t, int stage) {
+    const uint32_t k_s = lds_base + (uint32_t)(stage * STAGE * 2);
+    const uint32_t v_s = k_s + (uint32_t)(K_TILE * 2);
+    const int key0 = t * PF_KEYS;
+    const char* kb = reinterpret_cast<const char*>(Kg + (int64_t)key0 * kstride);
+    const char* vb = reinterpret_cast<const char*>(Vg + (int64_t)key0 * kstride);
+    const bool tail = key0 + PF_KEYS > S;  // rows past the sequence re-read row S - 1
+#pragma unroll
+    for (int j = 0; j < 5; ++j) {
+      const int n = wave_u + 4 * j;
+      int ko = k_src[j], vo = v_src[j];
+      if (tail) {
+        const int p = n * 64 + lane;
+        const int64_t over_k = (int64_t)max(key0 + p / 17 - (S - 1), 0) * kstride * 2;
+        const int64_t over_v = (int64_t)max(key0 + p / 20 - (S - 1), 0) * kstride * 2;
+        ko -= (int)over_k;
+        vo -= (int)over_v;
       }
-    }
-  };
-  auto store_tile = [&](int stage) {
-    uint16_t* k_s = pf_lds + stage * STAGE;
-    uint16_t* v_s = k_s + K_TILE;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int idx = tid + 64 * PF_WAVES * j;
-      const int key = idx >> 4;
-      const int d8 = (idx & 15) * 8;
-      *reinterpret_cast<uint4*>(k_s + key * K_STRIDE + d8) = kr[j];
-      *reinterpret_cast<uint4*>(v_s + key * V_STRIDE + d8) = vr[j];
+      if (n < 17) lds_dma16(kb, (uint32_t)ko, k_s + (uint32_t)(n * 1024));
+      lds_dma16(vb, (uint32_t)vo, v_s + (uint32_t)(n * 1024));
     }
   };
 
@@ -172,28 +204,31 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_mfma_kernel(ckv_pref
   uint32_t qk[QN];
 #pragma unroll
   for (int i = 0; i < QN; ++i) qk[i] = 0u;
-  float m = NEG_INF;  // running max of the raw score (scale > 0)
+  float m = NEG_INF;  // reference max of the raw score (scale > 0)
   float l = 0.0f;     // this half's share of the softmax denominator
 
-  load_tile(0);
-  store_tile(0);
+  issue_tile(tiles - 1, 0);
+  __builtin_amdgcn_s_waitcnt(VMCNT0);
   __syncthreads();
 
-  for (int t = 0; t < tiles; ++t) {
-    const bool more = t + 1 < tiles;
-    if (more) load_tile(t + 1);
-    const uint16_t* k_s = pf_lds + (t & 1) * STAGE;
+  // One 64-key tile.  EDGE tiles hold columns past some row's position
+  // (causal mask) or sink columns (excluded from the top-kappa); the others
+  // skip both checks.
+  auto tile = [&](int t, int stage, auto edge_tag) __attribute__((always_inline)) {
+    constexpr bool EDGE = decltype(edge_tag)::value;
+    if (t > 0) issue_tile(t - 1, stage ^ 1);
+    const uint16_t* k_s = pf_lds + stage * STAGE;
     const uint16_t* v_s = k_s + K_TILE;
 
     // S^T (keys x rows): accumulator b holds keys 32 b + 8 (v / 4) + 4 half + v % 4.
     f32x16_t sacc[2];
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
-#pragma unroll
-      for (int v = 0; v < 16; ++v) sacc[b][v] = 0.0f;
+      const uint4 kf = *reinterpret_cast<const uint4*>(k_s + (32 * b + row) * K_STRIDE + 8 * half);
+      sacc[b] = mfma32(kf, qreg[0], f32x16_t{});
     }
 #pragma unroll
-    for (int c = 0; c < 8; ++c) {
+    for (int c = 1; c < 8; ++c) {
 #pragma unroll
       for (int b = 0; b < 2; ++b) {
         const uint4 kf = *reinterpret_cast<const uint4*>(k_s + (32 * b + row) * K_STRIDE + 16 * c + 8 * half);
@@ -201,7 +236,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_mfma_kernel(ckv_pref
       }
     }
     const int c0 = t * PF_KEYS;
-    if (c0 + PF_KEYS - 1 > pos_lo) {
+    if constexpr (EDGE) {
 #pragma unroll
       for (int b = 0; b < 2; ++b) {
 #pragma unroll
@@ -211,45 +246,57 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_mfma_kernel(ckv_pref
         }
       }
     }
-    float lmax = NEG_INF;
+    // Maxima of the four groups of 8 (group g = accumulator g / 2, registers 8 (g % 2) ..).
+    float gmax[4];
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
+    for (int g = 0; g < 4; ++g) {
+      gmax[g] = sacc[g >> 1][8 * (g & 1)];
 #pragma unroll
-      for (int v = 0; v < 16; ++v) lmax = fmax_exact(lmax, sacc[b][v]);
+      for (int e = 1; e < 8; ++e) gmax[g] = __builtin_fmaxf(gmax[g], sacc[g >> 1][8 * (g & 1) + e]);
     }
+    const float lmax = __builtin_fmaxf(__builtin_fmaxf(gmax[0], gmax[1]), __builtin_fmaxf(gmax[2], gmax[3]));
 
-    // Top-kappa candidates of this lane's 32 columns.
+    // Top-kappa candidates of this lane's 32 columns, inspected by group.
     uint32_t thr = qk[QN - 1];
     thr = max(thr, swap32_u32(thr));
     float tf = prefilter(thr);
     if (lmax >= tf) {
 #pragma unroll
-      for (int b = 0; b < 2; ++b) {
+      for (int g = 0; g < 4; ++g) {
+        if (gmax[g] >= tf) {
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const float s = sacc[b][v];
-          const int col = c0 + 32 * b + 8 * (v >> 2) + 4 * half + (v & 3);
-          if (s >= tf && col >= a.num_sink) {
-            const uint32_t cand = (quantise_score(s) << 17) | (uint32_t)(col + 1);
-            if (cand > thr) {
-              queue_insert<QN>(qk, cand);
-              thr = max(thr, qk[QN - 1]);
-              tf = prefilter(thr);
+          for (int e = 0; e < 8; ++e) {
+            const int b = g >> 1;
+            const int v = 8 * (g & 1) + e;
+            const float sv = sacc[b][v];
+            const int col = c0 + 32 * b + 8 * (v >> 2) + 4 * half + (v & 3);
+            if (sv >= tf && (!EDGE || col >= a.num_sink)) {
+              const uint32_t cand = (quantise_score(sv) << 17) | (uint32_t)(col + 1);
+              if (cand > thr) {
+                queue_insert<QN>(qk, cand);
+                thr = max(thr, qk[QN - 1]);
+                tf = prefilter(thr);
+              }
             }
           }
         }
       }
     }
 
-    // Online softmax in base 2; both halves of a row share the max.
+    // Online softmax in base 2 against a reference max m that moves only when
+    // a tile exceeds it by more than 2^RESCALE_LOG2 (p <= 2^RESCALE_LOG2 stays
+    // exact in float32 and bf16 range); both halves of a row share m.
     const float tmax = max_xor32(lmax);
-    const float m_new = fmax_exact(m, tmax);
-    const float mc = m_new == NEG_INF ? 0.0f : m_new * sl2;
-    const float alpha = m == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(m * sl2 - mc);
-    m = m_new;
-    l *= alpha;
+    const bool grow = tmax > m + RESCALE_LOG2 / sl2;
+    if (__builtin_amdgcn_ballot_w64(grow)) {
+      const float m_new = grow ? tmax : m;
+      const float alpha = m == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f((m - m_new) * sl2);
+      m = m_new;
+      l *= alpha;
 #pragma unroll
-    for (int db = 0; db < 4; ++db) o[db] *= alpha;
+      for (int db = 0; db < 4; ++db) o[db] *= alpha;
+    }
+    const float mc = m == NEG_INF ? 0.0f : m * sl2;  // rows with no key seen yet get p = 0
     uint32_t pb[2][8];
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
@@ -280,8 +327,20 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_mfma_kernel(ckv_pref
         o[db] = mfma32(uint4{lo.x, lo.y, hi.x, hi.y}, bop, o[db]);
       }
     }
-    if (more) store_tile((t + 1) & 1);
+    __builtin_amdgcn_s_waitcnt(VMCNT0);
     __syncthreads();
+  };
+
+  const int num_sink = a.num_sink;
+  // Diagonal tile first, then backwards: the nearest keys tend to score
+  // highest, which raises the top-kappa threshold early.
+  for (int t = tiles - 1, stage = 0; t >= 0; --t, stage ^= 1) {
+    const int c0 = t * PF_KEYS;
+    if (c0 < num_sink || c0 + PF_KEYS - 1 > pos_lo) {
+      tile(t, stage, std::true_type{});
+    } else {
+      tile(t, stage, std::false_type{});
+    }
   }
 
   if (!row_ok) return;
