@@ -36,7 +36,7 @@ namespace {
 using namespace ckv;
 
 constexpr int D = CKV_HEAD_DIM;
-constexpr int PF_WAVES = 4;
+constexpr int PF_WAVES = 8;
 constexpr int PF_ROWS = 32 * PF_WAVES;  // packed (position, head) rows per workgroup
 constexpr int PF_KEYS = 64;             // keys per LDS tile
 constexpr int K_STRIDE = D + 8;         // 272-byte (17-chunk) K rows: 16-lane b128 reads hit distinct banks
@@ -44,7 +44,11 @@ constexpr int V_STRIDE = D + 32;        // 320-byte (20-chunk) V rows: transpose
 constexpr int K_TILE = PF_KEYS * K_STRIDE;
 constexpr int V_TILE = PF_KEYS * V_STRIDE;
 constexpr int STAGE = K_TILE + V_TILE;  // elements per pipeline stage
-constexpr size_t PF_LDS_BYTES = 2 * STAGE * sizeof(uint16_t);
+constexpr size_t PF_STAGE_BYTES = 2 * STAGE * sizeof(uint16_t);
+// Per-lane top-kappa queues live in LDS after the two stages: entry block j
+// (entries 4 j .. 4 j + 3) of thread tid at 16 (j * threads + tid).
+template <int QN>
+constexpr size_t pf_lds_bytes() { return PF_STAGE_BYTES + (size_t)QN * 4 * 64 * PF_WAVES; }
 constexpr int MAX_KAPPA = 16;
 constexpr int MAX_SEQ = (1 << 17) - 1;  // column + 1 must fit the 17-bit index field
 constexpr float NEG_INF = -__builtin_huge_valf();
@@ -158,14 +162,14 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_mfma_kernel(ckv_pref
   // Staging: K/V tiles go straight from global memory to LDS
   // (global_load_lds_dwordx4: lane i of a wave instruction fills the 16-byte
   // LDS chunk base + i).  A K tile is 64 rows x 17 chunks (16 data + 1 pad),
-  // a V tile 64 rows x 20 chunks; wave w issues the instructions n = w + 4 j.
+  // a V tile 64 rows x 20 chunks; wave w issues the instructions n = w + 8 j.
   // Pad chunks load the row's first chunk (never read).  Byte offsets of each
   // lane's source within a tile are fixed; the tile base is uniform.
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-  int k_src[5], v_src[5];
+  int k_src[3], v_src[3];
 #pragma unroll
-  for (int j = 0; j < 5; ++j) {
-    const int p = (wave_u + 4 * j) * 64 + lane;
+  for (int j = 0; j < 3; ++j) {
+    const int p = (wave_u + PF_WAVES * j) * 64 + lane;
     const int kc = p % 17;
     k_src[j] = (int)((int64_t)(p / 17) * kstride * 2) + 16 * (kc == 16 ? 0 : kc);
     const int vc = p % 20;
@@ -180,8 +184,8 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_mfma_kernel(ckv_pref
     const char* vb = reinterpret_cast<const char*>(Vg + (int64_t)key0 * kstride);
     const bool tail = key0 + PF_KEYS > S;  // rows past the sequence re-read row S - 1
 #pragma unroll
-    for (int j = 0; j < 5; ++j) {
-      const int n = wave_u + 4 * j;
+    for (int j = 0; j < 3; ++j) {
+      const int n = wave_u + PF_WAVES * j;
       int ko = k_src[j], vo = v_src[j];
       if (tail) {
         const int p = n * 64 + lane;
@@ -191,7 +195,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_mfma_kernel(ckv_pref
         vo -= (int)over_v;
       }
       if (n < 17) lds_dma16(kb, (uint32_t)ko, k_s + (uint32_t)(n * 1024));
-      lds_dma16(vb, (uint32_t)vo, v_s + (uint32_t)(n * 1024));
+      if (n < 20) lds_dma16(vb, (uint32_t)vo, v_s + (uint32_t)(n * 1024));
     }
   };
 
@@ -201,9 +205,22 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_mfma_kernel(ckv_pref
 #pragma unroll
     for (int v = 0; v < 16; ++v) o[db][v] = 0.0f;
   }
-  uint32_t qk[QN];
+  // This lane's queue (QN packed keys, descending) in LDS; only its worst
+  // entry stays in a register.
+  uint4* q_lds = reinterpret_cast<uint4*>(reinterpret_cast<char*>(pf_lds) + PF_STAGE_BYTES) + tid;
 #pragma unroll
-  for (int i = 0; i < QN; ++i) qk[i] = 0u;
+  for (int j = 0; j < QN / 4; ++j) q_lds[j * 64 * PF_WAVES] = uint4{0u, 0u, 0u, 0u};
+  auto load_queue = [&](uint32_t (&q)[QN]) {
+#pragma unroll
+    for (int j = 0; j < QN / 4; ++j) {
+      const uint4 w = q_lds[j * 64 * PF_WAVES];
+      q[4 * j] = w.x;
+      q[4 * j + 1] = w.y;
+      q[4 * j + 2] = w.z;
+      q[4 * j + 3] = w.w;
+    }
+  };
+  uint32_t q_min = 0u;
   float m = NEG_INF;  // reference max of the raw score (scale > 0)
   float l = 0.0f;     // this half's share of the softmax denominator
 
@@ -257,10 +274,11 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_mfma_kernel(ckv_pref
     const float lmax = __builtin_fmaxf(__builtin_fmaxf(gmax[0], gmax[1]), __builtin_fmaxf(gmax[2], gmax[3]));
 
     // Top-kappa candidates of this lane's 32 columns, inspected by group.
-    uint32_t thr = qk[QN - 1];
-    thr = max(thr, swap32_u32(thr));
+    uint32_t thr = max(q_min, swap32_u32(q_min));
     float tf = prefilter(thr);
     if (lmax >= tf) {
+      uint32_t qk[QN];
+      load_queue(qk);
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         if (gmax[g] >= tf) {
@@ -281,6 +299,9 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_mfma_kernel(ckv_pref
           }
         }
       }
+#pragma unroll
+      for (int j = 0; j < QN / 4; ++j) q_lds[j * 64 * PF_WAVES] = uint4{qk[4 * j], qk[4 * j + 1], qk[4 * j + 2], qk[4 * j + 3]};
+      q_min = qk[QN - 1];
     }
 
     // Online softmax in base 2 against a reference max m that moves only when
@@ -363,11 +384,10 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_mfma_kernel(ckv_pref
   // Exact merge of the two halves' sorted queues: the larger of a[i] and
   // b[QN-1-i] is a bitonic sequence holding the best QN of the union.
   uint32_t c[QN];
-#pragma unroll
-  for (int i = 0; i < QN; ++i) c[i] = qk[i];
+  load_queue(c);
   uint32_t other[QN];
 #pragma unroll
-  for (int i = 0; i < QN; ++i) other[i] = swap32_u32(qk[i]);
+  for (int i = 0; i < QN; ++i) other[i] = swap32_u32(c[i]);
 #pragma unroll
   for (int i = 0; i < QN; ++i) c[i] = max(c[i], other[QN - 1 - i]);
 #pragma unroll
@@ -407,14 +427,14 @@ int launch_prefill(const ckv_prefill_args& a, hipStream_t s) {
   static bool attr_set = false;
   if (!attr_set) {
     const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)PF_LDS_BYTES);
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)pf_lds_bytes<QN>());
     if (e != hipSuccess) {
       (void)hipGetLastError();
       return ckv_internal::set_error(CKV_E_LAUNCH, hipGetErrorString(e));
     }
     attr_set = true;
   }
-  hipLaunchKernelGGL(kernel, dim3((unsigned)blocks * a.kv_heads), dim3(64 * PF_WAVES), PF_LDS_BYTES, s, a, group,
+  hipLaunchKernelGGL(kernel, dim3((unsigned)blocks * a.kv_heads), dim3(64 * PF_WAVES), pf_lds_bytes<QN>(), s, a, group,
                      blocks);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return ckv_internal::set_error(CKV_E_LAUNCH, hipGetErrorString(e));
