@@ -228,11 +228,10 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_mfma_kernel(ckv_pref
   __builtin_amdgcn_s_waitcnt(VMCNT0);
   __syncthreads();
 
-  // One 64-key tile.  EDGE tiles hold columns past some row's position
-  // (causal mask) or sink columns (excluded from the top-kappa); the others
-  // skip both checks.
-  auto tile = [&](int t, int stage, auto edge_tag) __attribute__((always_inline)) {
-    constexpr bool EDGE = decltype(edge_tag)::value;
+  const int num_sink = a.num_sink;
+  // One 64-key tile.  Only edge tiles (columns past some row's position) run
+  // the causal mask; sink columns are excluded where candidates are taken.
+  auto tile = [&](int t, int stage, bool edge) __attribute__((always_inline)) {
     if (t > 0) issue_tile(t - 1, stage ^ 1);
     const uint16_t* k_s = pf_lds + stage * STAGE;
     const uint16_t* v_s = k_s + K_TILE;
@@ -253,7 +252,8 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_mfma_kernel(ckv_pref
       }
     }
     const int c0 = t * PF_KEYS;
-    if constexpr (EDGE) {
+    if (edge) {
+      asm volatile("");  // keeps the masking a branch (not selects on every tile)
 #pragma unroll
       for (int b = 0; b < 2; ++b) {
 #pragma unroll
@@ -288,7 +288,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_mfma_kernel(ckv_pref
             const int v = 8 * (g & 1) + e;
             const float sv = sacc[b][v];
             const int col = c0 + 32 * b + 8 * (v >> 2) + 4 * half + (v & 3);
-            if (sv >= tf && (!EDGE || col >= a.num_sink)) {
+            if (sv >= tf && col >= num_sink) {
               const uint32_t cand = (quantise_score(sv) << 17) | (uint32_t)(col + 1);
               if (cand > thr) {
                 queue_insert<QN>(qk, cand);
@@ -352,16 +352,11 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_mfma_kernel(ckv_pref
     __syncthreads();
   };
 
-  const int num_sink = a.num_sink;
   // Diagonal tile first, then backwards: the nearest keys tend to score
   // highest, which raises the top-kappa threshold early.
   for (int t = tiles - 1, stage = 0; t >= 0; --t, stage ^= 1) {
     const int c0 = t * PF_KEYS;
-    if (c0 < num_sink || c0 + PF_KEYS - 1 > pos_lo) {
-      tile(t, stage, std::true_type{});
-    } else {
-      tile(t, stage, std::false_type{});
-    }
+    tile(t, stage, c0 + PF_KEYS - 1 > pos_lo);
   }
 
   if (!row_ok) return;
