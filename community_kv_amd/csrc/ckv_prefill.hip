@@ -44,7 +44,8 @@ constexpr int V_STRIDE = D + 32;        // 320-byte (20-chunk) V rows: transpose
 constexpr int K_TILE = PF_KEYS * K_STRIDE;
 constexpr int V_TILE = PF_KEYS * V_STRIDE;
 constexpr int STAGE = K_TILE + V_TILE;  // elements per pipeline stage
-constexpr size_t PF_STAGE_BYTES = 2 * STAGE * sizeof(uint16_t);
+constexpr int PF_STAGES = 3;
+constexpr size_t PF_STAGE_BYTES = PF_STAGES * STAGE * sizeof(uint16_t);
 // Per-lane top-kappa queues live in LDS after the two stages: entry block j
 // (entries 4 j .. 4 j + 3) of thread tid at 16 (j * threads + tid).
 template <int QN>
@@ -224,20 +225,12 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_mfma_kernel(ckv_pref
   float m = NEG_INF;  // reference max of the raw score (scale > 0)
   float l = 0.0f;     // this half's share of the softmax denominator
 
-  issue_tile(tiles - 1, 0);
-  __builtin_amdgcn_s_waitcnt(VMCNT0);
-  __syncthreads();
-
   const int num_sink = a.num_sink;
-  // One 64-key tile.  Only edge tiles (columns past some row's position) run
-  // the causal mask; sink columns are excluded where candidates are taken.
-  auto tile = [&](int t, int stage, bool edge) __attribute__((always_inline)) {
-    if (t > 0) issue_tile(t - 1, stage ^ 1);
-    const uint16_t* k_s = pf_lds + stage * STAGE;
-    const uint16_t* v_s = k_s + K_TILE;
 
-    // S^T (keys x rows): accumulator b holds keys 32 b + 8 (v / 4) + 4 half + v % 4.
-    f32x16_t sacc[2];
+  // S^T (keys x rows) of the tile staged in `stage`: accumulator b holds keys
+  // 32 b + 8 (v / 4) + 4 half + v % 4 of the tile.
+  auto qk_tile = [&](int stage, f32x16_t (&sacc)[2]) __attribute__((always_inline)) {
+    const uint16_t* k_s = pf_lds + stage * STAGE;
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
       const uint4 kf = *reinterpret_cast<const uint4*>(k_s + (32 * b + row) * K_STRIDE + 8 * half);
@@ -251,8 +244,28 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_mfma_kernel(ckv_pref
         sacc[b] = mfma32(kf, qreg[c], sacc[b]);
       }
     }
+  };
+
+  // Software pipeline over three LDS stages, diagonal tile first and then
+  // backwards (the nearest keys tend to score highest, which raises the
+  // top-kappa threshold early).  Iteration t: tile t's scores are in
+  // registers, tile t - 1 is resident in LDS and tile t - 2 is in flight.  The
+  // QK^T MFMAs of tile t - 1 are issued next to tile t's softmax, so the
+  // matrix cores work while the vector ALUs do.
+  issue_tile(tiles - 1, 0);
+  if (tiles > 1) issue_tile(tiles - 2, 1);
+  __builtin_amdgcn_s_waitcnt(VMCNT0);
+  __syncthreads();
+  f32x16_t sacc[2];
+  qk_tile(0, sacc);
+
+  int stage = 0;
+  for (int t = tiles - 1; t >= 0; --t) {
+    const int nstage = stage == 2 ? 0 : stage + 1;
+    if (t >= 2) issue_tile(t - 2, nstage == 2 ? 0 : nstage + 1);
     const int c0 = t * PF_KEYS;
-    if (edge) {
+    // Causal mask: only tiles holding columns past some row's position.
+    if (c0 + PF_KEYS - 1 > pos_lo) {
       asm volatile("");  // keeps the masking a branch (not selects on every tile)
 #pragma unroll
       for (int b = 0; b < 2; ++b) {
@@ -273,7 +286,59 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_mfma_kernel(ckv_pref
     }
     const float lmax = __builtin_fmaxf(__builtin_fmaxf(gmax[0], gmax[1]), __builtin_fmaxf(gmax[2], gmax[3]));
 
-    // Top-kappa candidates of this lane's 32 columns, inspected by group.
+    // Online softmax in base 2 against a reference max m that moves only when
+    // a tile exceeds it by more than 2^RESCALE_LOG2 (p <= 2^RESCALE_LOG2 stays
+    // exact in float32 and bf16 range); both halves of a row share m.
+    const float tmax = max_xor32(lmax);
+    const bool grow = tmax > m + RESCALE_LOG2 / sl2;
+    if (__builtin_amdgcn_ballot_w64(grow)) {
+      const float m_new = grow ? tmax : m;
+      const float alpha = m == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f((m - m_new) * sl2);
+      m = m_new;
+      l *= alpha;
+#pragma unroll
+      for (int db = 0; db < 4; ++db) o[db] *= alpha;
+    }
+    const float mc = m == NEG_INF ? 0.0f : m * sl2;  // rows with no key seen yet get p = 0
+
+    // Next tile's scores on the matrix cores while this tile's exponentials run
+    // (on the last tile this reads a stale stage and the result is unused).
+    f32x16_t snext[2];
+    qk_tile(nstage, snext);
+    uint32_t pb[2][8];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+#pragma unroll
+      for (int v = 0; v < 16; v += 2) {
+        const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[b][v], sl2, -mc));
+        const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[b][v + 1], sl2, -mc));
+        l += p0;
+        l += p1;
+        pb[b][v >> 1] = pack_bf16x2_hw(p0, p1);
+      }
+    }
+
+    // O^T (dims x rows) += V^T P^T over four 16-key chunks.  Chunk kc pairs
+    // P registers 8 (kc % 2) .. +7 of accumulator kc / 2 (keys 16 kc + 4 half +
+    // e % 4 + 8 (e / 4)) with V^T rows read transposed for the same keys.
+    const uint16_t* v_s = pf_lds + stage * STAGE + K_TILE;
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc) {
+      const int b = kc >> 1;
+      const int vb = 4 * (kc & 1);
+      const uint4 bop = uint4{pb[b][vb], pb[b][vb + 1], pb[b][vb + 2], pb[b][vb + 3]};
+      const uint16_t* vrow = v_s + (16 * kc + 4 * half + ((lane & 15) >> 2)) * V_STRIDE + 16 * ((lane >> 4) & 1) +
+                             4 * (lane & 3);
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        const uint2 lo = lds_tr16(vrow + 32 * db);
+        const uint2 hi = lds_tr16(vrow + 8 * V_STRIDE + 32 * db);
+        o[db] = mfma32(uint4{lo.x, lo.y, hi.x, hi.y}, bop, o[db]);
+      }
+    }
+    // Top-kappa candidates of this lane's 32 columns, inspected by group
+    // against the larger of the two halves' worst kept keys.  Placed after the
+    // PV^T MFMAs are issued: the rare branch runs while they drain.
     uint32_t thr = max(q_min, swap32_u32(q_min));
     float tf = prefilter(thr);
     if (lmax >= tf) {
@@ -304,59 +369,11 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_mfma_kernel(ckv_pref
       q_min = qk[QN - 1];
     }
 
-    // Online softmax in base 2 against a reference max m that moves only when
-    // a tile exceeds it by more than 2^RESCALE_LOG2 (p <= 2^RESCALE_LOG2 stays
-    // exact in float32 and bf16 range); both halves of a row share m.
-    const float tmax = max_xor32(lmax);
-    const bool grow = tmax > m + RESCALE_LOG2 / sl2;
-    if (__builtin_amdgcn_ballot_w64(grow)) {
-      const float m_new = grow ? tmax : m;
-      const float alpha = m == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f((m - m_new) * sl2);
-      m = m_new;
-      l *= alpha;
-#pragma unroll
-      for (int db = 0; db < 4; ++db) o[db] *= alpha;
-    }
-    const float mc = m == NEG_INF ? 0.0f : m * sl2;  // rows with no key seen yet get p = 0
-    uint32_t pb[2][8];
-#pragma unroll
-    for (int b = 0; b < 2; ++b) {
-#pragma unroll
-      for (int v = 0; v < 16; v += 2) {
-        const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[b][v], sl2, -mc));
-        const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[b][v + 1], sl2, -mc));
-        l += p0;
-        l += p1;
-        pb[b][v >> 1] = pack_bf16x2_hw(p0, p1);
-      }
-    }
-
-    // O^T (dims x rows) += V^T P^T over four 16-key chunks.  Chunk kc pairs
-    // P registers 8 (kc % 2) .. +7 of accumulator kc / 2 (keys 16 kc + 4 half +
-    // e % 4 + 8 (e / 4)) with V^T rows read transposed for the same keys.
-#pragma unroll
-    for (int kc = 0; kc < 4; ++kc) {
-      const int b = kc >> 1;
-      const int vb = 4 * (kc & 1);
-      const uint4 bop = uint4{pb[b][vb], pb[b][vb + 1], pb[b][vb + 2], pb[b][vb + 3]};
-      const uint16_t* vrow = v_s + (16 * kc + 4 * half + ((lane & 15) >> 2)) * V_STRIDE + 16 * ((lane >> 4) & 1) +
-                             4 * (lane & 3);
-#pragma unroll
-      for (int db = 0; db < 4; ++db) {
-        const uint2 lo = lds_tr16(vrow + 32 * db);
-        const uint2 hi = lds_tr16(vrow + 8 * V_STRIDE + 32 * db);
-        o[db] = mfma32(uint4{lo.x, lo.y, hi.x, hi.y}, bop, o[db]);
-      }
-    }
+    sacc[0] = snext[0];
+    sacc[1] = snext[1];
     __builtin_amdgcn_s_waitcnt(VMCNT0);
     __syncthreads();
-  };
-
-  // Diagonal tile first, then backwards: the nearest keys tend to score
-  // highest, which raises the top-kappa threshold early.
-  for (int t = tiles - 1, stage = 0; t >= 0; --t, stage ^= 1) {
-    const int c0 = t * PF_KEYS;
-    tile(t, stage, c0 + PF_KEYS - 1 > pos_lo);
+    stage = nstage;
   }
 
   if (!row_ok) return;
