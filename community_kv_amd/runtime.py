@@ -351,7 +351,8 @@ class CommunityKVRuntime:
         generation_config = kwargs.get("generation_config", getattr(model, "generation_config", None))
 
         def option(name: str, default: Any) -> Any:
-            return kwargs[name] if name in kwargs else getattr(generation_config, name, default)
+            value = kwargs[name] if name in kwargs else getattr(generation_config, name, default)
+            return default if value is None else value  # unset GenerationConfig fields are None
 
         if option("num_beams", 1) != 1:
             raise ValueError("CommunityKV generate does not support beam search")

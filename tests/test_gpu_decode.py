@@ -90,8 +90,15 @@ CASES = {
     "deep_delta_chains_bf16": (dict(query_heads=8, kv_heads=2, seq_len=2048, communities=6, num_sink=10,
                                     max_decode_tokens=40, aggregation=co.QUERY_GROUP),
                                dict(group_size=4, num_sink=10, token_budget=512, local_window=32)),
+    # every community selected whole (the context is attended in full) while
+    # nearest-centroid decode tokens pile into a few communities' chains
+    "topk_all_nearest_bf16": (dict(query_heads=8, kv_heads=2, seq_len=300, communities=6, num_sink=10,
+                                   max_decode_tokens=12, aggregation=co.QUERY_GROUP),
+                              dict(group_size=4, num_sink=10, token_budget=4096, mode="topk", topk_communities=6,
+                                   max_selected=4096, assignment="nearest_centroid")),
 }
-STEPS = {"communities_1500_bf16": 4, "communities_2600_nearest": 4, "deep_delta_chains_bf16": 36}
+STEPS = {"communities_1500_bf16": 4, "communities_2600_nearest": 4, "deep_delta_chains_bf16": 36,
+         "topk_all_nearest_bf16": 12}
 
 
 @pytest.mark.parametrize("name", list(CASES))
