@@ -302,6 +302,90 @@ def run_prefill(args, device):
     print(json.dumps(result), flush=True)
 
 
+GEN_LAYERS = 36
+GEN_PROMPT = 65536
+GEN_STEPS = 128
+GEN_COMMUNITIES = 1024
+
+
+def qwen3_8b_config(layers):
+    from transformers import Qwen3Config
+
+    return Qwen3Config(vocab_size=151936, hidden_size=4096, intermediate_size=12288, num_hidden_layers=layers,
+                       num_attention_heads=HQ, num_key_value_heads=HKV, head_dim=D, max_position_embeddings=131072,
+                       rope_theta=1e6, rms_norm_eps=1e-6, tie_word_embeddings=False)
+
+
+def run_generate(args, device):
+    """random-init Qwen3-8B-architecture model, synthetic
+    prompt, greedy decode through CommunityKVRuntime.generate with
+    nearest-centroid assignment.  Decode throughput = (steps) / (wall time of a
+    prompt+steps generation - wall time of a prompt+1 generation)."""
+    from transformers import Qwen3ForCausalLM
+
+    from community_kv_amd import CommunityKVAttention, CommunityKVConfig, CommunityKVRuntime
+    from community_kv_amd.config import PartitionConfig
+
+    layers, prompt_len, steps = args.gen_layers, args.gen_prompt, args.gen_steps
+    torch.manual_seed(0)
+    with torch.device(device):
+        model = Qwen3ForCausalLM(qwen3_8b_config(layers))
+    model = model.to(torch.bfloat16).eval()
+    prompt = torch.randint(0, 151936, (1, prompt_len), generator=torch.Generator().manual_seed(1)).to(device)
+    rng = np.random.default_rng(7)
+    label_cache = {}
+
+    def labels(layer_idx, keys, topk_indices, topk_scores):
+        # seeded per layer and KV head: Zipf(1.1) sizes over ~1024 communities
+        if layer_idx not in label_cache:
+            label_cache[layer_idx] = torch.from_numpy(np.stack([
+                zipf_labels(rng, keys.shape[1], SINKS, GEN_COMMUNITIES) for _ in range(keys.shape[0])]))
+        return label_cache[layer_idx].to(keys.device)
+
+    cfg = CommunityKVConfig(token_budget=BUDGET, num_sink=SINKS, aggregation=GraphAggregation.QUERY_GROUP,
+                            local_window=WINDOW, assignment="nearest_centroid")
+    with CommunityKVRuntime(config=cfg, partition=PartitionConfig(), num_layers=layers, max_decode_tokens=steps,
+                            label_provider=labels) as runtime:
+        CommunityKVAttention(runtime).register()
+        model.set_attn_implementation("community_kv")
+
+        def timed(new_tokens):
+            torch.cuda.synchronize(device)
+            t0 = time.perf_counter()
+            with torch.inference_mode():
+                out = runtime.generate(model, prompt, max_new_tokens=new_tokens)
+            torch.cuda.synchronize(device)
+            return time.perf_counter() - t0, out
+
+        for _ in range(max(0, args.warmup)):
+            timed(2)
+        t_prefill, _ = timed(1)
+        t_full, out = timed(steps + 1)
+    decode_s = t_full - t_prefill
+    tps = steps / decode_s
+    result = {
+        "metric": "generate_decode_tokens_per_s_qwen3_8b_random_init",
+        "value": tps,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": decode_s * 1e3 / steps,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (uniform random prompt ids, random-init weights, Zipf(1.1) labels over ~1024 communities)",
+        "config": {"workload": "BASELINE config 3: random-init Qwen3-8B architecture, greedy decode through "
+                               "CommunityKVRuntime.generate, nearest-centroid assignment",
+                   "layers": layers, "prompt_tokens": prompt_len, "decode_steps": steps, "token_budget": BUDGET,
+                   "local_window": WINDOW, "num_sink": SINKS},
+        "prefill_plus_first_token_s": t_prefill,
+        "generated_tokens": int(out.shape[-1] - prompt_len),
+    }
+    print(json.dumps(result), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -310,8 +394,12 @@ def main():
     ap.add_argument("--layers", type=int, default=LAYERS)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
-    ap.add_argument("--workload", choices=["decode", "prefill"], default="decode",
-                    help="decode: the 36-layer sparse decode step (default); prefill: config-5 edge export")
+    ap.add_argument("--workload", choices=["decode", "prefill", "generate"], default="decode",
+                    help="decode: the 36-layer sparse decode step (default); prefill: config-5 edge export; "
+                         "generate: config-3 model decode loop")
+    ap.add_argument("--gen-layers", type=int, default=GEN_LAYERS)
+    ap.add_argument("--gen-prompt", type=int, default=GEN_PROMPT)
+    ap.add_argument("--gen-steps", type=int, default=GEN_STEPS)
     ap.add_argument("--prefill-seq", type=int, default=PREFILL_SEQ)
     ap.add_argument("--copy-probe", action="store_true",
                     help="after timing, one plain 256 MiB device-to-device copy (counter calibration)")
@@ -322,6 +410,9 @@ def main():
     device = torch.device("cuda:0")
     if args.workload == "prefill":
         run_prefill(args, device)
+        return
+    if args.workload == "generate":
+        run_generate(args, device)
         return
     max_decode = args.warmup + args.steps + max(5, args.steps // 2) + 16  # every full step replay appends one token
     runtime, stack = build_stack(device, args.layers, max_decode)
