@@ -415,7 +415,7 @@ __device__ inline TileResult mfma_tile(const uint16_t* __restrict__ K, const uin
   return res;
 }
 
-constexpr int ATT_WAVES = 4;  // waves (one 64-slot tile each) per attention workgroup
+constexpr int ATT_WAVES = 2;  // waves (one 64-slot tile each) per attention workgroup
 constexpr int ATT_TILES = ATT_WAVES;  // 64-slot tiles per attention workgroup
 
 // Split merge of all G query heads of retrieval head rh at once (any block
@@ -553,6 +553,55 @@ __device__ inline void merge_group(const DecodeArgs& a, const int rh, const int 
     }
   }
   __syncthreads();
+}
+
+// Split merge for up to PRE splits and G * 128 <= 512 outputs: 512 threads,
+// one output element per thread with all of its split accumulators loaded up
+// front (clamped, one round), and one wave per query reducing max, scales and
+// the denominator with lane = split.
+constexpr int MERGE_WIDE_THREADS = 512;
+
+template <int PRE>
+__global__ __launch_bounds__(MERGE_WIDE_THREADS) void merge_wide_kernel(DecodeArgs a, int splits) {
+  const int rh = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int G = a.cfg.group_size;
+  const int64_t base = (int64_t)rh * G * splits;
+  __shared__ float sc_s[MERGE_WIDE_THREADS / 64][PRE];
+  __shared__ float den_s[MERGE_WIDE_THREADS / 64];
+  const int i = min(tid, G * D - 1);
+  const float* src = a.ws.partial_acc + (base + (int64_t)(i >> 7) * splits) * D + (i & (D - 1));
+  float v[PRE];
+#pragma unroll
+  for (int k = 0; k < PRE; ++k) v[k] = gload_f32(src + (int64_t)min(k, splits - 1) * D);
+  if (wave < G) {
+    const bool ok = lane < splits;
+    const int64_t j = base + (int64_t)wave * splits + (ok ? lane : 0);
+    const float mt = ok ? gload_f32(a.ws.partial_max + j) : NEG_INF;
+    const float lt = ok ? gload_f32(a.ws.partial_sum + j) : 0.0f;
+    const float M = wave_max(mt);
+    const float sc = mt == NEG_INF ? 0.0f : ckv_expf(mt - M);
+    const float den = wave_sum_tree(sc != 0.0f ? lt * sc : 0.0f);
+    if (lane < PRE) sc_s[wave][lane] = sc;
+    if (lane == 0) {
+      den_s[wave] = den;
+      a.ws.lse[(int64_t)rh * G + wave] = M + ckv_logf(den);
+    }
+  }
+  __syncthreads();
+  if (tid < G * D) {
+    const int g = tid >> 7;
+    float acc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < PRE; ++k) {
+      const float sc = sc_s[g][k];
+      if (k < splits) acc = acc + (sc != 0.0f ? v[k] * sc : 0.0f);
+    }
+    reinterpret_cast<uint16_t*>(a.ws.output)[((int64_t)rh * G + g) * D + (tid & (D - 1))] =
+        ckv_f32_to_bf16_bits(acc / den_s[g]);
+  }
 }
 
 // Split merge of the bf16 path: one workgroup per retrieval head.  A kernel of
@@ -779,7 +828,14 @@ int launch_attention(const DecodeArgs& a, hipStream_t s, bool partials_only) {
     hipLaunchKernelGGL(attend_mfma_kernel<false>, grid, dim3(64 * ATT_WAVES), 0, s, a);
     const int r = launch_check("attend_mfma");
     if (r || partials_only) return r;
-    hipLaunchKernelGGL(merge_kernel, dim3(a.st.retrieval_heads), dim3(256), 0, s, a, splits);
+    const dim3 mg(a.st.retrieval_heads);
+    if (a.cfg.group_size * D <= MERGE_WIDE_THREADS && splits <= 64) {
+      if (splits <= 16) hipLaunchKernelGGL(merge_wide_kernel<16>, mg, dim3(MERGE_WIDE_THREADS), 0, s, a, splits);
+      else if (splits <= 32) hipLaunchKernelGGL(merge_wide_kernel<32>, mg, dim3(MERGE_WIDE_THREADS), 0, s, a, splits);
+      else hipLaunchKernelGGL(merge_wide_kernel<64>, mg, dim3(MERGE_WIDE_THREADS), 0, s, a, splits);
+    } else {
+      hipLaunchKernelGGL(merge_kernel, mg, dim3(256), 0, s, a, splits);
+    }
     return launch_check("merge");
   }
   hipLaunchKernelGGL((attend_generic_kernel<CKV_F32, false>), dim3(tiles, a.st.retrieval_heads), dim3(64), 0, s, a, 0,
