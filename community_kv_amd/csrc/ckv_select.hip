@@ -146,17 +146,20 @@ __global__ __launch_bounds__(SELECT_THREADS) void select_kernel(DecodeArgs a, De
   const int sub = tid >> 3;
   const int lane8 = tid & 7;
   const int passes = (nscore + ROWS_PER_PASS - 1) / ROWS_PER_PASS;
-  CentroidFrag<CT> frag[PB];
-  int rsize[PB];
-  auto load_batch = [&](int p0) {
+  // Two batches of centroid fragments: the next batch's loads are in flight
+  // while the current one is scored.
+  CentroidFrag<CT> frag[2][PB];
+  int rsize[2][PB];
+  auto load_batch = [&](int p0, int buf) {
 #pragma unroll
     for (int pb = 0; pb < PB; ++pb) {
       const int row = min((p0 + pb) * ROWS_PER_PASS + sub, nscore - 1);
-      load_frag<CT>(a.st.centroids, (int64_t)rh * C + row, 16 * lane8, frag[pb]);
-      rsize[pb] = gload_i32(a.st.community_sizes + (int64_t)rh * C + row);
+      load_frag<CT>(a.st.centroids, (int64_t)rh * C + row, 16 * lane8, frag[buf][pb]);
+      rsize[buf][pb] = gload_i32(a.st.community_sizes + (int64_t)rh * C + row);
     }
   };
-  load_batch(0);
+  load_batch(0, 0);
+  load_batch(PB, 1);  // clamped rows: harmless when there is no second batch
   // Query group: two elements per thread (G * 128 <= 2048 <= 4 * threads).
   float qv[4];
 #pragma unroll
@@ -268,7 +271,7 @@ __global__ __launch_bounds__(SELECT_THREADS) void select_kernel(DecodeArgs a, De
 
   // ---- scoring ----------------------------------------------------------------
   uint64_t best_nearest = ~0ull;
-  auto score_batch = [&](int p0) {
+  auto score_batch = [&](int p0, int buf) {
     // Queries two at a time, held in registers across the batch's passes (one
     // LDS read of each query slice per batch); q_s rows beyond G are read but
     // never selected into `best`.  Pinned order per (row, query) as above.
@@ -291,7 +294,7 @@ __global__ __launch_bounds__(SELECT_THREADS) void select_kernel(DecodeArgs a, De
 #pragma unroll
       for (int pb = 0; pb < PB; ++pb) {
         float cv[16];
-        decode_frag<CT>(frag[pb], cv);
+        decode_frag<CT>(frag[buf][pb], cv);
         // bf16 x e4m3 products have at most 12 significant bits, so they are
         // exact in f32 and a fused multiply-add equals the pinned multiply-then-add.
         float a0 = qa[0] * cv[0], a1 = qb[0] * cv[0];
@@ -318,11 +321,11 @@ __global__ __launch_bounds__(SELECT_THREADS) void select_kernel(DecodeArgs a, De
 #pragma unroll
     for (int pb = 0; pb < PB; ++pb) {
       const int c = (p0 + pb) * ROWS_PER_PASS + sub;
-      const bool live = c < count && rsize[pb] > 0;
+      const bool live = c < count && rsize[buf][pb] > 0;
       if (lane8 == 0 && c < nscore) key16[c] = f16_bits_hw(live ? best[pb] : NEG_INF);
       if (nearest_mode) {
         float cv[16];
-        decode_frag<CT>(frag[pb], cv);
+        decode_frag<CT>(frag[buf][pb], cv);
         float acc;
         {
           const float d0 = key_s[16 * lane8] - cv[0];
@@ -343,10 +346,12 @@ __global__ __launch_bounds__(SELECT_THREADS) void select_kernel(DecodeArgs a, De
       }
     }
   };
-  score_batch(0);
-  for (int p0 = PB; p0 < passes; p0 += PB) {
-    load_batch(p0);
-    score_batch(p0);
+  for (int p0 = 0; p0 < passes; p0 += 2 * PB) {
+    score_batch(p0, 0);
+    if (p0 + PB >= passes) break;
+    load_batch(p0 + 2 * PB, 0);
+    score_batch(p0 + PB, 1);
+    load_batch(p0 + 3 * PB, 1);
   }
   CKV_STAMP(rh == 0, 7);
   if (nearest_mode) {
