@@ -99,39 +99,44 @@ def planted_prefill_inputs(device, seq=PREFILL_SEQ, hq=HQ, hkv=HKV, clusters=PRE
     return q, k, v
 
 
-def build_stack(device, layers, max_decode, seed=0):
-    cfg = CommunityKVConfig(token_budget=BUDGET, num_sink=SINKS, lam=0.5, aggregation=GraphAggregation.QUERY_GROUP,
-                            local_window=WINDOW)
+def build_stack(device, layers, max_decode, seed=0, seq_lens=None, communities=None, budget=BUDGET, window=WINDOW):
+    """`layers` independent layer states (config 2 by default).  With
+    `seq_lens` / `communities` (one entry per layer) the entries are the
+    sequences of a ragged batch instead (config 4)."""
+    cfg = CommunityKVConfig(token_budget=budget, num_sink=SINKS, lam=0.5, aggregation=GraphAggregation.QUERY_GROUP,
+                            local_window=window)
     runtime = DecodeRuntime(cfg)
     rng = np.random.default_rng(seed)
     gen = torch.Generator(device=device).manual_seed(seed)
-    cap = SEQ + max_decode + 1
     stack = []
     for li in range(layers):
-        labels = torch.from_numpy(np.stack([zipf_labels(rng, SEQ, SINKS, COMMUNITIES) for _ in range(HKV)])).to(device)
-        centers = torch.randn(HKV, COMMUNITIES, D, device=device, generator=gen)
+        seq = SEQ if seq_lens is None else int(seq_lens[li])
+        comms = COMMUNITIES if communities is None else int(communities[li])
+        cap = seq + max_decode + 1
+        labels = torch.from_numpy(np.stack([zipf_labels(rng, seq, SINKS, comms) for _ in range(HKV)])).to(device)
+        centers = torch.randn(HKV, comms, D, device=device, generator=gen)
         key = torch.empty(HKV, cap, D, device=device, dtype=torch.bfloat16)
         for h in range(HKV):
-            noise = torch.randn(SEQ, D, device=device, generator=gen)
-            key[h, :SEQ] = (centers[h, labels[h].long()] + 0.3 * noise).to(torch.bfloat16)
-            extra = torch.randint(0, COMMUNITIES, (cap - SEQ,), device=device, generator=gen)
-            key[h, SEQ:] = (centers[h, extra] + 0.3 * torch.randn(cap - SEQ, D, device=device, generator=gen)).to(
+            noise = torch.randn(seq, D, device=device, generator=gen)
+            key[h, :seq] = (centers[h, labels[h].long()] + 0.3 * noise).to(torch.bfloat16)
+            extra = torch.randint(0, comms, (cap - seq,), device=device, generator=gen)
+            key[h, seq:] = (centers[h, extra] + 0.3 * torch.randn(cap - seq, D, device=device, generator=gen)).to(
                 torch.bfloat16)
         value = torch.randn(HKV, cap, D, device=device, generator=gen).to(torch.bfloat16)
-        part = build_layer_from_labels(layer_idx=li, community_ids=labels, keys=key[:, :SEQ], num_sink=SINKS,
+        part = build_layer_from_labels(layer_idx=li, community_ids=labels, keys=key[:, :seq], num_sink=SINKS,
                                        max_decode_tokens=max_decode, query_heads=HQ,
                                        aggregation=GraphAggregation.QUERY_GROUP)
         part.community_weight.uniform_(0.5, 2.0, generator=gen)
         part.total_weight.fill_(float(part.community_weight[0].sum()))
         layer = runtime.prepare_partitioned_layer(part)
-        pick = torch.randint(0, COMMUNITIES, (HKV,), device=device, generator=gen)
+        pick = torch.randint(0, comms, (HKV,), device=device, generator=gen)
         query = (centers[torch.arange(HKV, device=device), pick].repeat_interleave(HQ // HKV, 0)
                  + 0.5 * torch.randn(HQ, D, device=device, generator=gen)).to(torch.bfloat16).contiguous()
         conv = layer.converted
         call = layer.workspace.call(query=query, key=key, value=value, csr=conv.csr, state=conv.mutable,
                                     sink_positions=layer.sink_positions, current_position=conv.current_position,
                                     softmax_scale=D ** -0.5, lam=cfg.lam)
-        stack.append(dict(layer=layer, query=query, key=key, value=value, call=call))
+        stack.append(dict(layer=layer, query=query, key=key, value=value, call=call, seq=seq))
     return runtime, stack
 
 
@@ -386,6 +391,83 @@ def run_generate(args, device):
     print(json.dumps(result), flush=True)
 
 
+BATCH = 8
+BATCH_MIN, BATCH_MAX = 16384, 131072
+BATCH_BUDGET = 4096
+
+
+def run_batched(args, device):
+    """a ragged batch of 8 sequences (lengths uniform in
+    [16k, 128k], length/64 Zipf communities per KV head, 4096-token budget +
+    128 window), one Qwen3-8B-shaped layer; a step decodes one token of every
+    sequence with the batched entry point (one selection, attention, merge and
+    update launch for all 8 sequences), captured in one HIP graph; `steps` of
+    them with online (delta-Q) assignment.  The same step issued sequence by
+    sequence is reported beside it."""
+    rng = np.random.default_rng(3)
+    lens = rng.integers(BATCH_MIN, BATCH_MAX + 1, BATCH)
+    comms = [int(n) // 64 for n in lens]
+    max_decode = 2 * args.warmup + args.steps + max(5, args.steps // 4) + 12  # every replay appends one token
+    runtime, stack = build_stack(device, BATCH, max_decode, seed=1, seq_lens=lens, communities=comms,
+                                 budget=BATCH_BUDGET)
+    torch.cuda.synchronize(device)
+
+    from community_kv_amd.attention.kernels._abi import BatchDecode
+
+    batch = BatchDecode([e["call"] for e in stack])
+    graph = capture(batch.decode, device)
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize(device)
+    ms = time_graph(graph, args.steps, device)
+
+    def serial_step():  # the same step issued sequence by sequence (deferred updates)
+        pending = None
+        for e in stack:
+            e["call"].score_select_after(pending)
+            e["call"].attention()
+            pending = e["call"]
+        pending.update()
+
+    serial_graph = capture(serial_step, device)
+    serial_graph.replay()
+    serial_ms = time_graph(serial_graph, max(5, args.steps // 4), device)
+    att_bytes = []
+    for e in stack:
+        slots = e["layer"].workspace.selection.slot_positions
+        att_bytes.append(int((slots >= 0).sum().item()) * 2 * D * 2 + slots.numel() * 4 + HQ * D * 2)
+    att_graph = capture(lambda: [e["call"].attention_partials() for e in stack], device)
+    att_graph.replay()
+    part_ms = time_graph(att_graph, max(10, args.steps), device) / BATCH
+    achieved = float(np.mean(att_bytes)) / (part_ms * 1e-3) / 1e9
+    overflow = sum(int(e["layer"].workspace.update.overflow.sum().item()) for e in stack)
+    result = {
+        "metric": "batched_ragged_decode_tokens_per_s_qwen3_8b_layer",
+        "value": BATCH * 1e3 / ms,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (Gaussian-mixture keys, Zipf(1.1) community sizes, random-init state)",
+        "config": {"workload": "BASELINE config 4: batch 8, ragged contexts U[16384, 131072], length/64 communities "
+                               "per KV head, budget 4096 + window 128, one Qwen3-8B-shaped layer, delta-Q update",
+                   "context_lengths": [int(n) for n in lens], "token_budget": BATCH_BUDGET, "local_window": WINDOW},
+        "us_per_batch_step": ms * 1e3,
+        "us_per_batch_step_sequence_by_sequence": serial_ms * 1e3,
+        "overflow_flags": overflow,
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "kernel": "attend_mfma_kernel<false> (gather + split partials)",
+                     "bytes_per_launch": float(np.mean(att_bytes))},
+    }
+    print(json.dumps(result), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -394,9 +476,9 @@ def main():
     ap.add_argument("--layers", type=int, default=LAYERS)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
-    ap.add_argument("--workload", choices=["decode", "prefill", "generate"], default="decode",
+    ap.add_argument("--workload", choices=["decode", "prefill", "generate", "batched"], default="decode",
                     help="decode: the 36-layer sparse decode step (default); prefill: config-5 edge export; "
-                         "generate: config-3 model decode loop")
+                         "generate: config-3 model decode loop; batched: config-4 ragged batch")
     ap.add_argument("--gen-layers", type=int, default=GEN_LAYERS)
     ap.add_argument("--gen-prompt", type=int, default=GEN_PROMPT)
     ap.add_argument("--gen-steps", type=int, default=GEN_STEPS)
@@ -413,6 +495,9 @@ def main():
         return
     if args.workload == "generate":
         run_generate(args, device)
+        return
+    if args.workload == "batched":
+        run_batched(args, device)
         return
     max_decode = args.warmup + args.steps + max(5, args.steps // 2) + 16  # every full step replay appends one token
     runtime, stack = build_stack(device, args.layers, max_decode)

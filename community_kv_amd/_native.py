@@ -52,6 +52,9 @@ EXPORTED_SYMBOLS = (
     "ckv_decode_layer",
     "ckv_online_update",
     "ckv_score_select_after_update",
+    "ckv_batch_table_bytes",
+    "ckv_batch_prepare",
+    "ckv_batch_decode",
     "ckv_dense_decode",
     "ckv_prefill_attention_topk",
     "ckv_host_numerics",
@@ -155,6 +158,12 @@ def lib() -> ctypes.CDLL:
         fn.restype = ctypes.c_int
     handle.ckv_score_select_after_update.argtypes = [ctypes.POINTER(LayerArgs), ctypes.POINTER(LayerArgs), _p]
     handle.ckv_score_select_after_update.restype = ctypes.c_int
+    handle.ckv_batch_table_bytes.argtypes = [_i32]
+    handle.ckv_batch_table_bytes.restype = ctypes.c_size_t
+    handle.ckv_batch_prepare.argtypes = [ctypes.POINTER(LayerArgs), _i32, _p, _p]
+    handle.ckv_batch_prepare.restype = ctypes.c_int
+    handle.ckv_batch_decode.argtypes = [ctypes.POINTER(LayerArgs), _i32, _p, _p]
+    handle.ckv_batch_decode.restype = ctypes.c_int
     handle.ckv_dense_decode.argtypes = [ctypes.POINTER(KvCache), _i32, _f32, _p, _p, _p, _p, _p, _p]
     handle.ckv_dense_decode.restype = ctypes.c_int
     if hasattr(handle, "ckv_prefill_attention_topk"):

@@ -130,3 +130,28 @@ class DecodeCall:
 
     def decode(self, stream=None) -> None:
         nat.check(nat.lib().ckv_decode_layer(*self._args(self._stream(stream))))
+
+
+class BatchDecode:
+    """One decode step of several independent items (sequences of a ragged
+    batch, or layers whose inputs are all ready) in four launches that cover
+    all of them (``ckv_batch_decode``): selection, attention, split merge and
+    online update.  The items' packed arguments are uploaded once to a device
+    table (their tensors sit at fixed addresses); the step itself allocates
+    nothing and does not synchronise."""
+
+    def __init__(self, calls: "list[DecodeCall]") -> None:
+        if not calls:
+            raise ValueError("empty batch")
+        self.calls = list(calls)
+        self.device = calls[0].device
+        self.items = (nat.LayerArgs * len(self.calls))(*[c.layer_args() for c in self.calls])
+        size = int(nat.lib().ckv_batch_table_bytes(len(self.calls)))
+        self.table = torch.empty(size, dtype=torch.uint8, device=self.device)
+        nat.check(nat.lib().ckv_batch_prepare(self.items, len(self.calls), ctypes.c_void_p(self.table.data_ptr()),
+                                              ctypes.c_void_p(nat.stream_handle(self.device))))
+
+    def decode(self, stream=None) -> None:
+        s = nat.stream_handle(self.device) if stream is None else stream
+        nat.check(nat.lib().ckv_batch_decode(self.items, len(self.calls), ctypes.c_void_p(self.table.data_ptr()),
+                                             ctypes.c_void_p(s)))

@@ -211,9 +211,17 @@ __global__ __launch_bounds__(256) void update_kernel(DecodeArgs a) {
   owner_update<CT, DT>(a, rh, a.ws.lse[(int64_t)rh * a.cfg.group_size]);
 }
 
+// Batched launches read each item's arguments from a device table
+// (workgroup w serves item w / heads, head w % heads).
 template <int CT, int DT>
-__global__ __launch_bounds__(REDUCE_THREADS) void sync_shared_kernel(DecodeArgs a) {
-  const int rh = blockIdx.x;
+__global__ __launch_bounds__(256) void update_batch_kernel(const DecodeArgs* __restrict__ table, int heads) {
+  const DecodeArgs& a = table[blockIdx.x / heads];
+  const int rh = blockIdx.x % heads;
+  owner_update<CT, DT>(a, rh, a.ws.lse[(int64_t)rh * a.cfg.group_size]);
+}
+
+template <int CT, int DT>
+__device__ __forceinline__ void sync_shared_body(const DecodeArgs& a, const int rh) {
   const int tid = threadIdx.x;
   const int graph = a.st.retrieval_to_graph[rh];
   if (rh == graph) return;
@@ -244,6 +252,17 @@ __global__ __launch_bounds__(REDUCE_THREADS) void sync_shared_kernel(DecodeArgs 
     a.st.community_sizes[(int64_t)rh * C + community] = old_size + 1;
     a.st.community_counts[rh] = a.st.community_counts[graph];
   }
+}
+
+template <int CT, int DT>
+__global__ __launch_bounds__(REDUCE_THREADS) void sync_shared_kernel(DecodeArgs a) {
+  sync_shared_body<CT, DT>(a, blockIdx.x);
+}
+
+template <int CT, int DT>
+__global__ __launch_bounds__(REDUCE_THREADS) void sync_shared_batch_kernel(const DecodeArgs* __restrict__ table,
+                                                                           int heads) {
+  sync_shared_body<CT, DT>(table[blockIdx.x / heads], blockIdx.x % heads);
 }
 
 // Merge-only reduce for the dense baseline.
@@ -562,8 +581,7 @@ __device__ inline void merge_group(const DecodeArgs& a, const int rh, const int 
 constexpr int MERGE_WIDE_THREADS = 512;
 
 template <int PRE>
-__global__ __launch_bounds__(MERGE_WIDE_THREADS) void merge_wide_kernel(DecodeArgs a, int splits) {
-  const int rh = blockIdx.x;
+__device__ __forceinline__ void merge_wide_body(const DecodeArgs& a, const int rh, const int splits) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -604,6 +622,17 @@ __global__ __launch_bounds__(MERGE_WIDE_THREADS) void merge_wide_kernel(DecodeAr
   }
 }
 
+template <int PRE>
+__global__ __launch_bounds__(MERGE_WIDE_THREADS) void merge_wide_kernel(DecodeArgs a, int splits) {
+  merge_wide_body<PRE>(a, blockIdx.x, splits);
+}
+
+template <int PRE>
+__global__ __launch_bounds__(MERGE_WIDE_THREADS) void merge_wide_batch_kernel(const DecodeArgs* __restrict__ table,
+                                                                              int heads, int splits) {
+  merge_wide_body<PRE>(table[blockIdx.x / heads], blockIdx.x % heads, splits);
+}
+
 // Split merge of the bf16 path: one workgroup per retrieval head.  A kernel of
 // its own: on this GPU an agent-scope release/acquire pair around a
 // last-arriving-workgroup counter costs more than the kernel boundary.
@@ -621,12 +650,11 @@ __global__ __launch_bounds__(256) void merge_kernel(DecodeArgs a, int splits) {
 // slot (the candidates of the online update's top-8).  With MERGE the
 // last workgroup of a head to finish merges the splits into output and lse.
 template <bool MERGE>
-__global__ __launch_bounds__(64 * ATT_WAVES) void attend_mfma_kernel(DecodeArgs a) {
+__device__ __forceinline__ void attend_mfma_body(const DecodeArgs& a, const int rh) {
   // Per-wave V half-tile buffers (8 KB each); reused for the waves' P.V rows
   // and, in the last workgroup, as the split-merge scratch.
   __shared__ __align__(16) unsigned char att_dyn[ATT_WAVES * V_HALF_ROWS * D * sizeof(uint16_t)];
   const int wgi = blockIdx.x;
-  const int rh = blockIdx.y;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int tid = threadIdx.x;
@@ -753,6 +781,16 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attend_mfma_kernel(DecodeArgs 
   CKV_STAMP_MAX(true, 15);
 }
 
+template <bool MERGE>
+__global__ __launch_bounds__(64 * ATT_WAVES) void attend_mfma_kernel(DecodeArgs a) {
+  attend_mfma_body<MERGE>(a, blockIdx.y);
+}
+
+__global__ __launch_bounds__(64 * ATT_WAVES) void attend_mfma_batch_kernel(const DecodeArgs* __restrict__ table,
+                                                                           int heads) {
+  attend_mfma_body<false>(table[blockIdx.y / heads], blockIdx.y % heads);
+}
+
 // Dense bf16 decode baseline: each wave streams `chunk_tiles` consecutive
 // 64-token tiles of one KV head with an online softmax across tiles and writes
 // one split partial per query of its group.
@@ -870,6 +908,41 @@ int launch_sync_shared(const DecodeArgs& a, hipStream_t s) {
   else if (bf16) hipLaunchKernelGGL((sync_shared_kernel<CKV_F32, CKV_BF16>), g, dim3(REDUCE_THREADS), 0, s, a);
   else hipLaunchKernelGGL((sync_shared_kernel<CKV_F32, CKV_F32>), g, dim3(REDUCE_THREADS), 0, s, a);
   return launch_check("sync_shared");
+}
+
+int attention_batch_splits(const DecodeArgs& a) {
+  const int splits = attention_splits(a);
+  return (a.kv.dtype == CKV_BF16 && a.cfg.group_size * D <= MERGE_WIDE_THREADS && splits <= 64) ? splits : 0;
+}
+
+// Batched step (bf16 KV): attention + split merge + online update (+ layer-wise
+// sync) of `count` items whose DecodeArgs sit in the device table; `h` is the
+// host copy of the first item (all items share dtypes, group size, retrieval
+// heads and slot capacity).
+int launch_batch_attention(const DecodeArgs& h, const DecodeArgs* table, int count, hipStream_t s) {
+  const int heads = h.st.retrieval_heads;
+  const int splits = attention_splits(h);
+  hipLaunchKernelGGL(attend_mfma_batch_kernel, dim3(splits, count * heads), dim3(64 * ATT_WAVES), 0, s, table,
+                     heads);
+  int r = launch_check("attend_mfma_batch");
+  if (r) return r;
+  const dim3 mg(count * heads);
+  if (splits <= 16) hipLaunchKernelGGL(merge_wide_batch_kernel<16>, mg, dim3(MERGE_WIDE_THREADS), 0, s, table, heads, splits);
+  else if (splits <= 32) hipLaunchKernelGGL(merge_wide_batch_kernel<32>, mg, dim3(MERGE_WIDE_THREADS), 0, s, table, heads, splits);
+  else hipLaunchKernelGGL(merge_wide_batch_kernel<64>, mg, dim3(MERGE_WIDE_THREADS), 0, s, table, heads, splits);
+  return launch_check("merge_batch");
+}
+
+int launch_batch_update(const DecodeArgs& h, const DecodeArgs* table, int count, bool any_shared, hipStream_t s) {
+  const int heads = h.st.retrieval_heads;
+  const dim3 g(count * heads);
+  if (h.st.centroid_dtype == CKV_E4M3) hipLaunchKernelGGL((update_batch_kernel<CKV_E4M3, CKV_BF16>), g, dim3(256), 0, s, table, heads);
+  else hipLaunchKernelGGL((update_batch_kernel<CKV_F32, CKV_BF16>), g, dim3(256), 0, s, table, heads);
+  int r = launch_check("update_batch");
+  if (r || !any_shared) return r;
+  if (h.st.centroid_dtype == CKV_E4M3) hipLaunchKernelGGL((sync_shared_batch_kernel<CKV_E4M3, CKV_BF16>), g, dim3(REDUCE_THREADS), 0, s, table, heads);
+  else hipLaunchKernelGGL((sync_shared_batch_kernel<CKV_F32, CKV_BF16>), g, dim3(REDUCE_THREADS), 0, s, table, heads);
+  return launch_check("sync_shared_batch");
 }
 
 int dense_chunks(int seq_len, int chunk_tiles) { return (seq_len + TILE * chunk_tiles - 1) / (TILE * chunk_tiles); }

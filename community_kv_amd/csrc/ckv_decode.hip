@@ -9,6 +9,9 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
+#include <vector>
+
 #include "ckv_device.h"
 #include "ckv_error.h"
 
@@ -228,4 +231,83 @@ extern "C" int ckv_dense_decode(const ckv_kv_cache* kv, int32_t seq_len, float s
   a.ws.output = output;
   a.ws.lse = lse;
   return ckv::launch_dense(a, seq_len, group, reinterpret_cast<hipStream_t>(stream));
+}
+
+namespace {
+
+// Checks a batch and returns the launch maxima.  Every item must pass the
+// single-call checks, use bf16 KV, and share the first item's centroid dtype,
+// group size, retrieval heads, slot capacity and assignment mode; items must
+// not share state or workspace.
+int validate_batch(const ckv_layer_args* items, int count, std::vector<ckv::DecodeArgs>* packed, int* max_nscore,
+                   size_t* max_lds, bool* any_shared) {
+  if (!items || count <= 0) return fail(CKV_E_INVALID, "empty batch");
+  *max_nscore = 0;
+  *max_lds = 0;
+  *any_shared = false;
+  for (int i = 0; i < count; ++i) {
+    const ckv_layer_args& it = items[i];
+    int rc = validate(it.kv, it.state, it.csr, it.deltas, it.config, it.ws);
+    if (!rc) rc = validate_attention(it.state, it.deltas, it.config, it.ws);
+    if (rc) return rc;
+    const ckv::DecodeArgs a = pack(it.kv, it.state, it.csr, it.deltas, it.config, it.ws);
+    if (a.kv.dtype != CKV_BF16) return fail(CKV_E_INVALID, "batched decode requires bf16 KV");
+    if (ckv::attention_batch_splits(a) == 0)
+      return fail(CKV_E_LIMIT, "batched decode requires group_size * 128 <= 512 and at most 64 attention splits");
+    if (i > 0) {
+      const ckv::DecodeArgs& h = (*packed)[0];
+      if (a.st.centroid_dtype != h.st.centroid_dtype || a.cfg.group_size != h.cfg.group_size ||
+          a.st.retrieval_heads != h.st.retrieval_heads || a.ws.slot_capacity != h.ws.slot_capacity ||
+          a.cfg.assignment != h.cfg.assignment)
+        return fail(CKV_E_INVALID, "batch items must share dtypes, group size, heads, slot capacity and assignment");
+      for (const ckv::DecodeArgs& o : *packed) {
+        if (o.st.centroids == a.st.centroids || o.ws.lse == a.ws.lse || o.ws.slot_positions == a.ws.slot_positions)
+          return fail(CKV_E_INVALID, "batch items must not share state or workspace");
+      }
+    }
+    packed->push_back(a);
+    *max_nscore = std::max(*max_nscore, std::min(a.st.community_capacity, a.ws.score_blocks * CKV_SCORE_BLOCK));
+    *max_lds = std::max(*max_lds, ckv::select_lds_bytes(a.st.community_capacity, a.ws.descriptor_capacity,
+                                                        a.cfg.max_selected));
+    if (a.st.retrieval_heads != a.st.graph_count) *any_shared = true;
+  }
+  return CKV_OK;
+}
+
+}  // namespace
+
+extern "C" size_t ckv_batch_table_bytes(int32_t count) {
+  return count > 0 ? (size_t)count * sizeof(ckv::DecodeArgs) : 0;
+}
+
+extern "C" int ckv_batch_prepare(const ckv_layer_args* items, int32_t count, void* table, void* stream) {
+  std::vector<ckv::DecodeArgs> packed;
+  int max_nscore;
+  size_t max_lds;
+  bool any_shared;
+  const int rc = validate_batch(items, count, &packed, &max_nscore, &max_lds, &any_shared);
+  if (rc) return rc;
+  if (!table) return fail(CKV_E_INVALID, "null batch table");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  hipError_t e = hipMemcpyAsync(table, packed.data(), packed.size() * sizeof(ckv::DecodeArgs), hipMemcpyHostToDevice, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (e != hipSuccess) return fail(CKV_E_LAUNCH, hipGetErrorString(e));
+  return CKV_OK;
+}
+
+extern "C" int ckv_batch_decode(const ckv_layer_args* items, int32_t count, const void* table, void* stream) {
+  std::vector<ckv::DecodeArgs> packed;
+  int max_nscore;
+  size_t max_lds;
+  bool any_shared;
+  int rc = validate_batch(items, count, &packed, &max_nscore, &max_lds, &any_shared);
+  if (rc) return rc;
+  if (!table) return fail(CKV_E_INVALID, "null batch table");
+  const ckv::DecodeArgs* t = reinterpret_cast<const ckv::DecodeArgs*>(table);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const ckv::DecodeArgs& h = packed[0];
+  rc = ckv::launch_batch_select(h, t, count, max_nscore, max_lds, s);
+  if (!rc) rc = ckv::launch_batch_attention(h, t, count, s);
+  if (!rc && h.cfg.assignment != CKV_ASSIGN_NONE) rc = ckv::launch_batch_update(h, t, count, any_shared, s);
+  return rc;
 }

@@ -91,16 +91,10 @@ __device__ inline void decode_frag(const CentroidFrag<CT>& f, float* out) {
 // a.st.retrieval_heads run the pending online update of another layer `u`
 // (same dtypes, disjoint state) on otherwise idle CUs.
 template <int CT, int DT, int OWN>
-__global__ __launch_bounds__(SELECT_THREADS) void select_kernel(DecodeArgs a, DecodeArgs u) {
+__device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh) {
   constexpr int PB = CT == CKV_E4M3 ? 4 : 2;  // scoring passes whose loads are in flight together
   constexpr int WAVES = SELECT_THREADS / 64;
   constexpr int WIN_PER_THREAD = (CKV_MAX_WINDOW + SELECT_THREADS - 1) / SELECT_THREADS;
-  if ((int)blockIdx.x >= a.st.retrieval_heads) {
-    const int urh = (int)blockIdx.x - a.st.retrieval_heads;
-    owner_update<CT, DT>(u, urh, u.ws.lse[(int64_t)urh * u.cfg.group_size]);
-    return;
-  }
-  const int rh = blockIdx.x;
   const int tid = threadIdx.x;
   const int G = a.cfg.group_size;
   const int C = a.st.community_capacity;
@@ -684,6 +678,23 @@ __global__ __launch_bounds__(SELECT_THREADS) void select_kernel(DecodeArgs a, De
   CKV_STAMP(rh == 0, 5);
 }
 
+template <int CT, int DT, int OWN>
+__global__ __launch_bounds__(SELECT_THREADS) void select_kernel(DecodeArgs a, DecodeArgs u) {
+  if ((int)blockIdx.x >= a.st.retrieval_heads) {
+    const int urh = (int)blockIdx.x - a.st.retrieval_heads;
+    owner_update<CT, DT>(u, urh, u.ws.lse[(int64_t)urh * u.cfg.group_size]);
+    return;
+  }
+  select_body<CT, DT, OWN>(a, blockIdx.x);
+}
+
+// Batched selection: workgroup w serves item w / heads, head w % heads of the
+// device table.
+template <int CT, int DT, int OWN>
+__global__ __launch_bounds__(SELECT_THREADS) void select_batch_kernel(const DecodeArgs* __restrict__ table, int heads) {
+  select_body<CT, DT, OWN>(table[blockIdx.x / heads], blockIdx.x % heads);
+}
+
 // key16 / community table, the descriptor arrays, the per-block descriptor index.
 size_t select_lds_bytes(int community_capacity, int descriptor_capacity, int max_selected) {
   return (size_t)((community_capacity + 7) & ~7) * 2 + (size_t)descriptor_capacity * DESC_ARRAYS * 4 +
@@ -718,9 +729,11 @@ int launch_score_select(const DecodeArgs& a, hipStream_t s, const DecodeArgs* pe
   auto by_own = [&](auto k1, auto k2, auto kmax) {
     return own <= 1 ? launch(k1) : own <= 2 ? launch(k2) : launch(kmax);
   };
-  if (ct == CKV_E4M3 && dt == CKV_BF16)
+  if (ct == CKV_E4M3 && dt == CKV_BF16) {
+    if (own > 2 && own <= 4) return launch(select_kernel<CKV_E4M3, CKV_BF16, 4>);
     return by_own(select_kernel<CKV_E4M3, CKV_BF16, 1>, select_kernel<CKV_E4M3, CKV_BF16, 2>,
                   select_kernel<CKV_E4M3, CKV_BF16, OWN_MAX>);
+  }
   if (ct == CKV_E4M3)
     return by_own(select_kernel<CKV_E4M3, CKV_F32, 1>, select_kernel<CKV_E4M3, CKV_F32, 2>,
                   select_kernel<CKV_E4M3, CKV_F32, OWN_MAX>);
@@ -729,6 +742,36 @@ int launch_score_select(const DecodeArgs& a, hipStream_t s, const DecodeArgs* pe
                   select_kernel<CKV_F32, CKV_BF16, OWN_MAX>);
   return by_own(select_kernel<CKV_F32, CKV_F32, 1>, select_kernel<CKV_F32, CKV_F32, 2>,
                 select_kernel<CKV_F32, CKV_F32, OWN_MAX>);
+}
+
+// Batched selection of `count` items (bf16 KV); `max_nscore`, `max_lds` are the
+// maxima over the items.
+int launch_batch_select(const DecodeArgs& h, const DecodeArgs* table, int count, int max_nscore, size_t max_lds,
+                        hipStream_t s) {
+  const int own = (max_nscore + SELECT_THREADS - 1) / SELECT_THREADS;
+  auto launch = [&](auto kernel) {
+    if (max_lds > 48 * 1024) {
+      const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)max_lds);
+      if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return limit_error("batched selection LDS exceeds the device limit");
+      }
+    }
+    hipLaunchKernelGGL(kernel, dim3(count * h.st.retrieval_heads), dim3(SELECT_THREADS), max_lds, s, table,
+                       h.st.retrieval_heads);
+    return launch_check("select_batch");
+  };
+  constexpr int OWN_MAX = CKV_MAX_COMMUNITIES / SELECT_THREADS;
+  if (h.st.centroid_dtype == CKV_E4M3) {
+    return own <= 1 ? launch(select_batch_kernel<CKV_E4M3, CKV_BF16, 1>)
+           : own <= 2 ? launch(select_batch_kernel<CKV_E4M3, CKV_BF16, 2>)
+           : own <= 4 ? launch(select_batch_kernel<CKV_E4M3, CKV_BF16, 4>)
+                      : launch(select_batch_kernel<CKV_E4M3, CKV_BF16, OWN_MAX>);
+  }
+  return own <= 1 ? launch(select_batch_kernel<CKV_F32, CKV_BF16, 1>)
+         : own <= 2 ? launch(select_batch_kernel<CKV_F32, CKV_BF16, 2>)
+                    : launch(select_batch_kernel<CKV_F32, CKV_BF16, OWN_MAX>);
 }
 
 }  // namespace ckv

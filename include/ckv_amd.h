@@ -20,6 +20,8 @@
  *                           launched at 1164-1273) and the shared-graph centroid sync 867-950;
  *                           a separate entry point so that callers can run it on another stream
  *   ckv_decode_layer        decode_layer()                    attention/decode.py:67-111
+ *   ckv_batch_decode        a loop of decode_layer() over independent sequences (batched launches;
+ *                           ckv_batch_prepare is its set-up call and synchronises its stream)
  *   ckv_dense_decode        (baseline only) dense bf16 decode over the whole cache, the
  *                           FlashAttention decode the reference compares against (paper Table 5)
  *   ckv_prefill_attention_topk
@@ -29,6 +31,7 @@
 #ifndef CKV_AMD_H
 #define CKV_AMD_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -256,6 +259,24 @@ typedef struct ckv_layer_args {
  * the update off the decode critical path; it flushes the last one with
  * ckv_online_update. */
 int ckv_score_select_after_update(const ckv_layer_args* layer, const ckv_layer_args* pending, void* stream);
+
+/* Batched decode, no counterpart in the reference (whose runtime decodes one
+ * sequence at a time; it replaces a loop of decode_layer calls, decode.py:67-111,
+ * over independent items): one decode step of `count` items -- the sequences of
+ * a ragged batch, or layers whose queries are all ready -- as one selection
+ * launch, one attention launch, one split-merge launch and one update launch
+ * covering all items, instead of `count` launches of each.  Items must use bf16
+ * KV, share the centroid dtype, group size (group_size * 128 <= 512),
+ * retrieval-head count, slot capacity and assignment mode, and must not share
+ * state or workspace.  `table` is caller-owned device memory of
+ * ckv_batch_table_bytes(count) bytes; ckv_batch_prepare validates the items and
+ * copies their packed arguments into it, synchronising `stream` (a set-up call:
+ * the items' tensors sit at fixed addresses, so one table serves every step).
+ * ckv_batch_decode validates the host items again, allocates nothing and does
+ * not synchronise; results are identical to ckv_decode_layer on each item. */
+size_t ckv_batch_table_bytes(int32_t count);
+int ckv_batch_prepare(const ckv_layer_args* items, int32_t count, void* table, void* stream);
+int ckv_batch_decode(const ckv_layer_args* items, int32_t count, const void* table, void* stream);
 
 /* ckv_score_select, ckv_segmented_attention and ckv_online_update on one stream. */
 int ckv_decode_layer(const ckv_kv_cache* kv, const ckv_graph_state* state,

@@ -1,0 +1,76 @@
+"""Batched decode (``ckv_batch_decode``: selection, attention, merge and update
+of several items in one launch each) must leave every item's output and graph
+state bit-identical to running the items one by one with ``ckv_decode_layer``
+(the single-item path is itself checked against the oracle)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from community_kv_amd.attention.kernels._abi import BatchDecode
+from oracle import ckv_oracle as co
+from oracle import synthetic as syn
+from tests import _helpers as h
+
+pytestmark = pytest.mark.gpu
+
+ITEMS = [  # ragged: different contexts and community counts
+    dict(seq_len=4096, communities=64),
+    dict(seq_len=2500, communities=40),
+    dict(seq_len=6000, communities=150),
+]
+
+
+def _item(fx, params, device):
+    state, csr, cur, q, k, v = h.to_device(fx, device)
+    ws = h.workspace_for(fx, params, device)
+    sinks = torch.arange(params.num_sink, dtype=torch.int32, device=device)
+    call = ws.call(query=q, key=k, value=v, csr=csr, state=state, sink_positions=sinks, current_position=cur,
+                   softmax_scale=params.softmax_scale, lam=params.lam)
+    return dict(state=state, cur=cur, q=q, ws=ws, call=call)
+
+
+@pytest.mark.parametrize("aggregation,assignment,group", [
+    (co.QUERY_GROUP, "delta_q", 4), (co.QUERY_GROUP, "nearest_centroid", 4), (co.LAYER_WISE, "delta_q", 2)])
+def test_batch_decode_matches_single_items(device, aggregation, assignment, group):
+    print(f"batch decode {aggregation} {assignment}", flush=True)
+    params = co.StepParams(group_size=group, num_sink=10, token_budget=512, local_window=64, assignment=assignment)
+    qh = 4 * group
+    fxs = [syn.build_layer(seed=50 + i, query_heads=qh, kv_heads=4, num_sink=10, max_decode_tokens=16,
+                           aggregation=aggregation, **kw) for i, kw in enumerate(ITEMS)]
+    single = [_item(fx, params, device) for fx in fxs]
+    batched = [_item(fx, params, device) for fx in fxs]
+    batch = BatchDecode([b["call"] for b in batched])
+    rng = np.random.default_rng(9)
+    for step in range(8):
+        for it in single:
+            it["call"].decode()
+        batch.decode()
+        torch.cuda.synchronize(device)
+        for i, (a, b) in enumerate(zip(single, batched)):
+            case = f"step {step} item {i}"
+            assert torch.equal(a["ws"].attention.output, b["ws"].attention.output), case
+            assert torch.equal(a["ws"].attention.lse, b["ws"].attention.lse), case
+            assert torch.equal(a["ws"].selection.slot_positions, b["ws"].selection.slot_positions), case
+            h.assert_states_equal(h.state_to_numpy(a["state"], a["cur"], True),
+                                  h.state_to_numpy(b["state"], b["cur"], True))
+        for fx, a, b in zip(fxs, single, batched):
+            q = syn.fresh_query(fx, rng)
+            a["q"].copy_(h.torch_values(q, fx.dtype, device))
+            b["q"].copy_(h.torch_values(q, fx.dtype, device))
+
+
+def test_batch_rejects_mismatched_items(device):
+    params = co.StepParams(group_size=4, num_sink=10, token_budget=512)
+    other = co.StepParams(group_size=4, num_sink=10, token_budget=1024)
+    fx0 = syn.build_layer(seed=1, query_heads=16, kv_heads=4, seq_len=4096, communities=64, num_sink=10,
+                          max_decode_tokens=4, aggregation=co.QUERY_GROUP)
+    fx1 = syn.build_layer(seed=2, query_heads=16, kv_heads=4, seq_len=4096, communities=64, num_sink=10,
+                          max_decode_tokens=4, aggregation=co.QUERY_GROUP)
+    a, b = _item(fx0, params, device), _item(fx1, other, device)
+    with pytest.raises(RuntimeError, match="share"):
+        BatchDecode([a["call"], b["call"]])
+    with pytest.raises(RuntimeError, match="must not share"):
+        BatchDecode([a["call"], a["call"]])
