@@ -55,6 +55,7 @@ EXPORTED_SYMBOLS = (
     "ckv_batch_table_bytes",
     "ckv_batch_prepare",
     "ckv_batch_decode",
+    "ckv_batch_attention_partials",
     "ckv_dense_decode",
     "ckv_prefill_attention_topk",
     "ckv_host_numerics",
@@ -164,6 +165,8 @@ def lib() -> ctypes.CDLL:
     handle.ckv_batch_prepare.restype = ctypes.c_int
     handle.ckv_batch_decode.argtypes = [ctypes.POINTER(LayerArgs), _i32, _p, _p]
     handle.ckv_batch_decode.restype = ctypes.c_int
+    handle.ckv_batch_attention_partials.argtypes = [ctypes.POINTER(LayerArgs), _i32, _p, _p]
+    handle.ckv_batch_attention_partials.restype = ctypes.c_int
     handle.ckv_dense_decode.argtypes = [ctypes.POINTER(KvCache), _i32, _f32, _p, _p, _p, _p, _p, _p]
     handle.ckv_dense_decode.restype = ctypes.c_int
     if hasattr(handle, "ckv_prefill_attention_topk"):

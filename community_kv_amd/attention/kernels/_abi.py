@@ -155,3 +155,9 @@ class BatchDecode:
         s = nat.stream_handle(self.device) if stream is None else stream
         nat.check(nat.lib().ckv_batch_decode(self.items, len(self.calls), ctypes.c_void_p(self.table.data_ptr()),
                                              ctypes.c_void_p(s)))
+
+    def attention_partials(self, stream=None) -> None:
+        """The batched attention launch alone (profiling)."""
+        s = nat.stream_handle(self.device) if stream is None else stream
+        nat.check(nat.lib().ckv_batch_attention_partials(self.items, len(self.calls),
+                                                         ctypes.c_void_p(self.table.data_ptr()), ctypes.c_void_p(s)))

@@ -919,13 +919,14 @@ int attention_batch_splits(const DecodeArgs& a) {
 // sync) of `count` items whose DecodeArgs sit in the device table; `h` is the
 // host copy of the first item (all items share dtypes, group size, retrieval
 // heads and slot capacity).
-int launch_batch_attention(const DecodeArgs& h, const DecodeArgs* table, int count, hipStream_t s) {
+int launch_batch_attention(const DecodeArgs& h, const DecodeArgs* table, int count, hipStream_t s,
+                           bool partials_only) {
   const int heads = h.st.retrieval_heads;
   const int splits = attention_splits(h);
   hipLaunchKernelGGL(attend_mfma_batch_kernel, dim3(splits, count * heads), dim3(64 * ATT_WAVES), 0, s, table,
                      heads);
   int r = launch_check("attend_mfma_batch");
-  if (r) return r;
+  if (r || partials_only) return r;
   const dim3 mg(count * heads);
   if (splits <= 16) hipLaunchKernelGGL(merge_wide_batch_kernel<16>, mg, dim3(MERGE_WIDE_THREADS), 0, s, table, heads, splits);
   else if (splits <= 32) hipLaunchKernelGGL(merge_wide_batch_kernel<32>, mg, dim3(MERGE_WIDE_THREADS), 0, s, table, heads, splits);

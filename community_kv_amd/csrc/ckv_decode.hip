@@ -311,3 +311,16 @@ extern "C" int ckv_batch_decode(const ckv_layer_args* items, int32_t count, cons
   if (!rc && h.cfg.assignment != CKV_ASSIGN_NONE) rc = ckv::launch_batch_update(h, t, count, any_shared, s);
   return rc;
 }
+
+extern "C" int ckv_batch_attention_partials(const ckv_layer_args* items, int32_t count, const void* table,
+                                            void* stream) {
+  std::vector<ckv::DecodeArgs> packed;
+  int max_nscore;
+  size_t max_lds;
+  bool any_shared;
+  const int rc = validate_batch(items, count, &packed, &max_nscore, &max_lds, &any_shared);
+  if (rc) return rc;
+  if (!table) return fail(CKV_E_INVALID, "null batch table");
+  return ckv::launch_batch_attention(packed[0], reinterpret_cast<const ckv::DecodeArgs*>(table), count,
+                                     reinterpret_cast<hipStream_t>(stream), true);
+}

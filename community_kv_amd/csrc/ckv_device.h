@@ -438,7 +438,8 @@ size_t select_lds_bytes(int community_capacity, int descriptor_capacity, int max
 int attention_batch_splits(const DecodeArgs& a);  // 0 when the batched attention cannot serve `a`
 int launch_batch_select(const DecodeArgs& h, const DecodeArgs* table, int count, int max_nscore, size_t max_lds,
                         hipStream_t stream);
-int launch_batch_attention(const DecodeArgs& h, const DecodeArgs* table, int count, hipStream_t stream);
+int launch_batch_attention(const DecodeArgs& h, const DecodeArgs* table, int count, hipStream_t stream,
+                           bool partials_only = false);
 int launch_batch_update(const DecodeArgs& h, const DecodeArgs* table, int count, bool any_shared, hipStream_t stream);
 int launch_dense(const DecodeArgs& a, int seq_len, int group, hipStream_t stream);
 int launch_check(const char* what);

@@ -277,6 +277,8 @@ int ckv_score_select_after_update(const ckv_layer_args* layer, const ckv_layer_a
 size_t ckv_batch_table_bytes(int32_t count);
 int ckv_batch_prepare(const ckv_layer_args* items, int32_t count, void* table, void* stream);
 int ckv_batch_decode(const ckv_layer_args* items, int32_t count, const void* table, void* stream);
+/* (diagnostics) the attention launch of ckv_batch_decode alone, writing split partials. */
+int ckv_batch_attention_partials(const ckv_layer_args* items, int32_t count, const void* table, void* stream);
 
 /* ckv_score_select, ckv_segmented_attention and ckv_online_update on one stream. */
 int ckv_decode_layer(const ckv_kv_cache* kv, const ckv_graph_state* state,
