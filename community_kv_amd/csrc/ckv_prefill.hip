@@ -101,12 +101,14 @@ __device__ inline uint32_t quantise_score(float s) {
 }
 
 // Scores below this cannot reach a packed key above `thr`: quantise(s) >= key
-// needs s >= (key - 0.5) / 256 - 48, and a margin of half a step absorbs the
-// float32 rounding of (s + 48) * 256.  An empty threshold admits every finite
+// needs rint(fl(s + 48) * 256) >= key, i.e. fl(s + 48) >= (key - 0.5) / 256,
+// and fl(s + 48) exceeds s + 48 by at most 2^-18 (below 128), so
+// s >= (key - 0.5) / 256 - 48 - 2^-18.  The margin 0.504 / 256 covers that
+// and the rounding of this expression.  An empty threshold admits every finite
 // score.
 __device__ inline float prefilter(uint32_t thr) {
   const uint32_t key = thr >> 17;
-  return key == 0 ? -FLT_MAX : (float)(int)(key - 1) * (1.0f / 256.0f) - 48.0f;
+  return key == 0 ? -FLT_MAX : __builtin_fmaf((float)key, 1.0f / 256.0f, -(48.0f + 0.504f / 256.0f));
 }
 
 // Insertion into a descending queue: the new entry i is the median of the
