@@ -424,8 +424,7 @@ def run_batched(args, device):
     def serial_step():  # the same step issued sequence by sequence (deferred updates)
         pending = None
         for e in stack:
-            e["call"].score_select_after(pending)
-            e["call"].attention()
+            e["call"].decode_after(pending)
             pending = e["call"]
         pending.update()
 
@@ -511,8 +510,7 @@ def main():
     def step_overlapped():
         pending = None
         for e in stack:
-            e["call"].score_select_after(pending)
-            e["call"].attention()
+            e["call"].decode_after(pending)
             pending = e["call"]
         pending.update()
 

@@ -52,6 +52,7 @@ EXPORTED_SYMBOLS = (
     "ckv_decode_layer",
     "ckv_online_update",
     "ckv_score_select_after_update",
+    "ckv_decode_step_after_update",
     "ckv_batch_table_bytes",
     "ckv_batch_prepare",
     "ckv_batch_decode",
@@ -159,6 +160,8 @@ def lib() -> ctypes.CDLL:
         fn.restype = ctypes.c_int
     handle.ckv_score_select_after_update.argtypes = [ctypes.POINTER(LayerArgs), ctypes.POINTER(LayerArgs), _p]
     handle.ckv_score_select_after_update.restype = ctypes.c_int
+    handle.ckv_decode_step_after_update.argtypes = [ctypes.POINTER(LayerArgs), ctypes.POINTER(LayerArgs), _p]
+    handle.ckv_decode_step_after_update.restype = ctypes.c_int
     handle.ckv_batch_table_bytes.argtypes = [_i32]
     handle.ckv_batch_table_bytes.restype = ctypes.c_size_t
     handle.ckv_batch_prepare.argtypes = [ctypes.POINTER(LayerArgs), _i32, _p, _p]

@@ -125,6 +125,13 @@ class DecodeCall:
             ctypes.byref(self.layer_args()), None if pending is None else ctypes.byref(pending.layer_args()),
             ctypes.c_void_p(self._stream(stream))))
 
+    def decode_after(self, pending: "DecodeCall | None", stream=None) -> None:
+        """Selection + attention of this layer (its update left pending) plus
+        the deferred online update of ``pending`` in the same launches."""
+        nat.check(nat.lib().ckv_decode_step_after_update(
+            ctypes.byref(self.layer_args()), None if pending is None else ctypes.byref(pending.layer_args()),
+            ctypes.c_void_p(self._stream(stream))))
+
     def update(self, stream=None) -> None:
         nat.check(nat.lib().ckv_online_update(*self._args(self._stream(stream))))
 

@@ -17,6 +17,8 @@
 
 namespace {
 
+constexpr int64_t FUSED_MAX_WORKGROUPS = 256;  // compute units of the MI355X
+
 thread_local char g_error[512] = "";
 
 int fail(int code, const char* message) {
@@ -169,8 +171,14 @@ extern "C" int ckv_decode_layer(const ckv_kv_cache* kv, const ckv_graph_state* s
   if (rc) return rc;
   const ckv::DecodeArgs a = pack(kv, st, csr, dl, cfg, ws);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  rc = ckv::launch_score_select(a, s);
-  if (!rc) rc = ckv::launch_attention(a, s, false);
+  const int parts = ckv::fused_parts(a);
+  if (parts > 0) {
+    rc = ckv::launch_select_attend(a, s, nullptr, parts);
+    if (!rc) rc = ckv::launch_merge(a, s, parts);
+  } else {
+    rc = ckv::launch_score_select(a, s);
+    if (!rc) rc = ckv::launch_attention(a, s, false);
+  }
   if (!rc) rc = ckv::launch_update(a, s);
   return rc;
 }
@@ -196,6 +204,41 @@ extern "C" int ckv_score_select_after_update(const ckv_layer_args* layer, const 
   }
   rc = ckv::launch_score_select(a, s, &u);
   return rc ? rc : ckv::launch_sync_shared(u, s);
+}
+
+extern "C" int ckv_decode_step_after_update(const ckv_layer_args* layer, const ckv_layer_args* pending,
+                                            void* stream) {
+  if (!layer) return fail(CKV_E_INVALID, "null layer arguments");
+  int rc = validate(layer->kv, layer->state, layer->csr, layer->deltas, layer->config, layer->ws);
+  if (!rc) rc = validate_attention(layer->state, layer->deltas, layer->config, layer->ws);
+  if (rc) return rc;
+  const ckv::DecodeArgs a = pack(layer->kv, layer->state, layer->csr, layer->deltas, layer->config, layer->ws);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int parts = ckv::fused_parts(a);
+  if (parts == 0) {
+    rc = ckv_score_select_after_update(layer, pending, stream);
+    return rc ? rc : ckv::launch_attention(a, s, false);
+  }
+  ckv::DecodeArgs u;
+  const ckv::DecodeArgs* up = nullptr;
+  if (pending) {
+    rc = validate(pending->kv, pending->state, pending->csr, pending->deltas, pending->config, pending->ws);
+    if (!rc) rc = validate_attention(pending->state, pending->deltas, pending->config, pending->ws);
+    if (rc) return rc;
+    if (pending->state->centroids == layer->state->centroids || pending->ws->lse == layer->ws->lse)
+      return fail(CKV_E_INVALID, "the pending update must belong to another layer");
+    u = pack(pending->kv, pending->state, pending->csr, pending->deltas, pending->config, pending->ws);
+    if (u.st.centroid_dtype != a.st.centroid_dtype || u.kv.dtype != a.kv.dtype) {
+      rc = ckv::launch_update(u, s);  // different dtypes: a launch of its own, before this layer
+      if (rc) return rc;
+    } else {
+      up = &u;
+    }
+  }
+  rc = ckv::launch_select_attend(a, s, up, parts);
+  if (!rc && up) rc = ckv::launch_sync_shared(u, s);
+  if (!rc) rc = ckv::launch_merge(a, s, parts);
+  return rc;
 }
 
 extern "C" int ckv_online_update(const ckv_kv_cache* kv, const ckv_graph_state* st, const ckv_prefill_csr* csr,
@@ -306,8 +349,22 @@ extern "C" int ckv_batch_decode(const ckv_layer_args* items, int32_t count, cons
   const ckv::DecodeArgs* t = reinterpret_cast<const ckv::DecodeArgs*>(table);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const ckv::DecodeArgs& h = packed[0];
-  rc = ckv::launch_batch_select(h, t, count, max_nscore, max_lds, s);
-  if (!rc) rc = ckv::launch_batch_attention(h, t, count, s);
+  int parts = ckv::fused_parts(h);
+  size_t fused_lds = 0;
+  for (const ckv::DecodeArgs& it : packed) {
+    if (ckv::fused_parts(it) != parts) parts = 0;
+    fused_lds = std::max(fused_lds, ckv::fused_lds_bytes(it));
+  }
+  // Every fused workgroup repeats its head's selection: worth it only while
+  // the copies run side by side, one per compute unit.
+  if ((int64_t)count * h.st.retrieval_heads * parts > FUSED_MAX_WORKGROUPS) parts = 0;
+  if (parts > 0) {
+    rc = ckv::launch_batch_select_attend(h, t, count, max_nscore, fused_lds, parts, s);
+    if (!rc) rc = ckv::launch_batch_merge(h, t, count, parts, s);
+  } else {
+    rc = ckv::launch_batch_select(h, t, count, max_nscore, max_lds, s);
+    if (!rc) rc = ckv::launch_batch_attention(h, t, count, s);
+  }
   if (!rc && h.cfg.assignment != CKV_ASSIGN_NONE) rc = ckv::launch_batch_update(h, t, count, any_shared, s);
   return rc;
 }

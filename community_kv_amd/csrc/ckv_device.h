@@ -436,6 +436,13 @@ int launch_attention(const DecodeArgs& a, hipStream_t stream, bool partials_only
 int launch_update(const DecodeArgs& a, hipStream_t stream);
 size_t select_lds_bytes(int community_capacity, int descriptor_capacity, int max_selected);
 int attention_batch_splits(const DecodeArgs& a);  // 0 when the batched attention cannot serve `a`
+int fused_parts(const DecodeArgs& a);              // 0 when the fused selection + attention cannot serve `a`
+size_t fused_lds_bytes(const DecodeArgs& a);
+int launch_select_attend(const DecodeArgs& a, hipStream_t stream, const DecodeArgs* pending, int parts);
+int launch_batch_select_attend(const DecodeArgs& h, const DecodeArgs* table, int count, int max_nscore,
+                               size_t max_lds, int parts, hipStream_t stream);
+int launch_merge(const DecodeArgs& a, hipStream_t stream, int splits);
+int launch_batch_merge(const DecodeArgs& h, const DecodeArgs* table, int count, int splits, hipStream_t stream);
 int launch_batch_select(const DecodeArgs& h, const DecodeArgs* table, int count, int max_nscore, size_t max_lds,
                         hipStream_t stream);
 int launch_batch_attention(const DecodeArgs& h, const DecodeArgs* table, int count, hipStream_t stream,

@@ -25,6 +25,7 @@
 
 #include "ckv_device.h"
 #include "ckv_error.h"
+#include "ckv_tile.h"
 #include "ckv_update.h"
 
 namespace ckv {
@@ -39,6 +40,11 @@ int limit_error(const char* message) { return ckv_internal::set_error(CKV_E_LIMI
 constexpr int ROWS_PER_PASS = SELECT_THREADS / 8;          // centroid rows scored per pass
 constexpr int MAT_BATCH = 4;                               // 64-slot blocks per wave gathered together
 constexpr int DESC_ARRAYS = 7;                             // per-descriptor LDS arrays
+// Dynamic LDS the fused kernel may use (the selection's static arrays take
+// about 12 KB of the CU's 160 KB).
+constexpr size_t FUSED_LDS_LIMIT = 144 * 1024;
+// 64-slot tiles attended per workgroup of the fused path (parts per head = tiles / this).
+constexpr int FUSED_TILES = 2;
 }  // namespace
 
 // Centroid row fragment of one lane: 16 dims (e4m3: 16 bytes, f32: 64 bytes).
@@ -90,8 +96,16 @@ __device__ inline void decode_frag(const CentroidFrag<CT>& f, float* out) {
 // so that the per-community fields stay in registers.  Workgroups beyond
 // a.st.retrieval_heads run the pending online update of another layer `u`
 // (same dtypes, disjoint state) on otherwise idle CUs.
-template <int CT, int DT, int OWN>
-__device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh) {
+// LDS bytes of the fused path's slot table (16-byte aligned).
+__host__ __device__ inline size_t fused_slot_bytes(int slot_capacity) { return ((size_t)slot_capacity * 4 + 15) & ~(size_t)15; }
+
+// FUSED: `part` of `parts` workgroups of this head each run the whole
+// selection (they are latency-bound, so the copies cost no time), keep the
+// full slot table in LDS, and then attend their own part of it
+// (attend_part); only part 0 writes the selection's outputs.
+template <int CT, int DT, int OWN, bool FUSED = false>
+__device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, const int part = 0,
+                                            const int parts = 1) {
   constexpr int PB = CT == CKV_E4M3 ? 4 : 2;  // scoring passes whose loads are in flight together
   constexpr int WAVES = SELECT_THREADS / 64;
   constexpr int WIN_PER_THREAD = (CKV_MAX_WINDOW + SELECT_THREADS - 1) / SELECT_THREADS;
@@ -114,7 +128,11 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh) {
   __shared__ int sink_s[CKV_MAX_SINKS];
   __shared__ int s_bin, s_above, s_max_idx, s_sel_count, s_last_sel_pos, s_last_size, s_sink_max;
 
-  extern __shared__ __align__(16) unsigned char dyn[];
+  extern __shared__ __align__(16) unsigned char dyn_all[];
+  // fused: the slot table first, then the selection arrays (later the attention buffers)
+  int* slot_lds = reinterpret_cast<int*>(dyn_all);
+  unsigned char* dyn = dyn_all + (FUSED ? fused_slot_bytes(a.ws.slot_capacity) : 0);
+  const bool writer = !FUSED || part == 0;  // writes the selection's global outputs
   uint16_t* key16 = reinterpret_cast<uint16_t*>(dyn);  // masked fp16 score bits of every scored community
   const int dcap = a.ws.descriptor_capacity;
   int* desc_comm = reinterpret_cast<int*>(dyn + (size_t)((C + 7) & ~7) * 2);
@@ -601,12 +619,16 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh) {
       for (int q = 0; q < MAT_BATCH; ++q) {
         const int j = 64 * (b0 + q * WAVES) + lane;
         if (j < sel_count) {
-          slots[ns + j] = val[q];
+          if (FUSED) slot_lds[ns + j] = val[q];
+          if (writer) slots[ns + j] = val[q];
           if (j == sel_count - 1) s_last_sel_pos = val[q];
         }
       }
     }
-    if (tid < ns) slots[tid] = sink_s[tid];
+    if (tid < ns) {
+      if (FUSED) slot_lds[tid] = sink_s[tid];
+      if (writer) slots[tid] = sink_s[tid];
+    }
     __syncthreads();  // s_last_sel_pos
     CKV_STAMP(rh == 0, 4);
     // Window: positions cur-W .. cur-1 not already attended (sinks, or members
@@ -635,14 +657,22 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh) {
             }
           }
         }
-        slots[wbeg + i] = pos;
+        if (FUSED) slot_lds[wbeg + i] = pos;
+        if (writer) slots[wbeg + i] = pos;
       }
     }
-    if (inc && tid == 0) slots[wbeg + W] = cur;
-    for (int s = wbeg + W + inc + tid; s < slot_cap; s += SELECT_THREADS) slots[s] = -1;
+    if (inc && tid == 0) {
+      if (FUSED) slot_lds[wbeg + W] = cur;
+      if (writer) slots[wbeg + W] = cur;
+    }
+    for (int s = wbeg + W + inc + tid; s < slot_cap; s += SELECT_THREADS) {
+      if (FUSED) slot_lds[s] = -1;
+      if (writer) slots[s] = -1;
+    }
   }
 
   // ---- outputs that nothing in this kernel reads back --------------------------
+  if (writer) {
   if (tid == 0) {
     a.ws.descriptor_counts[rh] = n_desc;
     a.ws.selected_counts[rh] = sel_count;
@@ -675,7 +705,12 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh) {
     for (int w = 0; w < WAVES; ++w) m = near_s[w] < m ? near_s[w] : m;
     a.ws.nearest[rh] = (m == ~0ull) ? -1 : (int)(m & 0xffffffffu);
   }
+  }  // writer
   CKV_STAMP(rh == 0, 5);
+  if constexpr (FUSED) {
+    __syncthreads();  // slot table complete; the selection arrays are dead from here
+    attend_part<SELECT_THREADS / 64, FUSED_TILES>(a, rh, part, parts, slot_lds, dyn);
+  }
 }
 
 template <int CT, int DT, int OWN>
@@ -686,6 +721,28 @@ __global__ __launch_bounds__(SELECT_THREADS) void select_kernel(DecodeArgs a, De
     return;
   }
   select_body<CT, DT, OWN>(a, blockIdx.x);
+}
+
+// Fused selection + attention partials: `parts` workgroups per retrieval head
+// (workgroup w: head w / parts, part w % parts); workgroups beyond them run the
+// pending online update of another layer `u`.
+template <int CT, int DT, int OWN>
+__global__ __launch_bounds__(SELECT_THREADS) void select_attend_kernel(DecodeArgs a, DecodeArgs u, int parts) {
+  const int nsel = a.st.retrieval_heads * parts;
+  if ((int)blockIdx.x >= nsel) {
+    const int urh = (int)blockIdx.x - nsel;
+    owner_update<CT, DT>(u, urh, u.ws.lse[(int64_t)urh * u.cfg.group_size]);
+    return;
+  }
+  select_body<CT, DT, OWN, true>(a, blockIdx.x / parts, blockIdx.x % parts, parts);
+}
+
+template <int CT, int DT, int OWN>
+__global__ __launch_bounds__(SELECT_THREADS) void select_attend_batch_kernel(const DecodeArgs* __restrict__ table,
+                                                                            int heads, int parts) {
+  const int per_item = heads * parts;
+  const int r = blockIdx.x % per_item;
+  select_body<CT, DT, OWN, true>(table[blockIdx.x / per_item], r / parts, r % parts, parts);
 }
 
 // Batched selection: workgroup w serves item w / heads, head w % heads of the
@@ -742,6 +799,87 @@ int launch_score_select(const DecodeArgs& a, hipStream_t s, const DecodeArgs* pe
                   select_kernel<CKV_F32, CKV_BF16, OWN_MAX>);
   return by_own(select_kernel<CKV_F32, CKV_F32, 1>, select_kernel<CKV_F32, CKV_F32, 2>,
                 select_kernel<CKV_F32, CKV_F32, OWN_MAX>);
+}
+
+// Parts per head of the fused selection + attention path (64-slot tiles of
+// the slot table, eight per workgroup), or 0 when the path cannot serve `a`:
+// bf16 KV, a materialised slot table of at most 8192 slots held in LDS, and a
+// query group small enough for the wide split merge.
+int fused_parts(const DecodeArgs& a) {
+  if (a.kv.dtype != CKV_BF16 || a.csr.member_offsets == nullptr) return 0;
+  if (a.ws.slot_capacity > 8192 || a.cfg.group_size * D > 512) return 0;
+  const int tiles = a.ws.slot_capacity / TILE;
+  const int parts = (tiles + FUSED_TILES - 1) / FUSED_TILES;
+  const size_t lds = fused_slot_bytes(a.ws.slot_capacity) +
+                     std::max(select_lds_bytes(a.st.community_capacity, a.ws.descriptor_capacity, a.cfg.max_selected),
+                              attend_part_lds_bytes(SELECT_THREADS / 64));
+  return (parts <= 64 && lds <= FUSED_LDS_LIMIT) ? parts : 0;
+}
+
+size_t fused_lds_bytes(const DecodeArgs& a) {
+  return fused_slot_bytes(a.ws.slot_capacity) +
+         std::max(select_lds_bytes(a.st.community_capacity, a.ws.descriptor_capacity, a.cfg.max_selected),
+                  attend_part_lds_bytes(SELECT_THREADS / 64));
+}
+
+int launch_select_attend(const DecodeArgs& a, hipStream_t s, const DecodeArgs* pending, int parts) {
+  const size_t lds = fused_lds_bytes(a);
+  const int nscore = std::min(a.st.community_capacity, a.ws.score_blocks * SCORE_BLOCK);
+  const int own = (nscore + SELECT_THREADS - 1) / SELECT_THREADS;
+  auto launch = [&](auto kernel) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) {
+      (void)hipGetLastError();
+      return limit_error("fused selection + attention LDS exceeds the device limit");
+    }
+    DecodeArgs u;
+    memset(&u, 0, sizeof(u));
+    int extra = 0;
+    if (pending != nullptr && pending->cfg.assignment != CKV_ASSIGN_NONE) {
+      u = *pending;
+      extra = pending->st.retrieval_heads;
+    }
+    hipLaunchKernelGGL(kernel, dim3(a.st.retrieval_heads * parts + extra), dim3(SELECT_THREADS), lds, s, a, u,
+                       parts);
+    return launch_check("select_attend");
+  };
+  constexpr int OWN_MAX = CKV_MAX_COMMUNITIES / SELECT_THREADS;
+  if (a.st.centroid_dtype == CKV_E4M3) {
+    return own <= 1 ? launch(select_attend_kernel<CKV_E4M3, CKV_BF16, 1>)
+           : own <= 2 ? launch(select_attend_kernel<CKV_E4M3, CKV_BF16, 2>)
+           : own <= 4 ? launch(select_attend_kernel<CKV_E4M3, CKV_BF16, 4>)
+                      : launch(select_attend_kernel<CKV_E4M3, CKV_BF16, OWN_MAX>);
+  }
+  return own <= 1 ? launch(select_attend_kernel<CKV_F32, CKV_BF16, 1>)
+         : own <= 2 ? launch(select_attend_kernel<CKV_F32, CKV_BF16, 2>)
+                    : launch(select_attend_kernel<CKV_F32, CKV_BF16, OWN_MAX>);
+}
+
+int launch_batch_select_attend(const DecodeArgs& h, const DecodeArgs* table, int count, int max_nscore,
+                               size_t max_lds, int parts, hipStream_t s) {
+  const int own = (max_nscore + SELECT_THREADS - 1) / SELECT_THREADS;
+  auto launch = [&](auto kernel) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)max_lds);
+    if (e != hipSuccess) {
+      (void)hipGetLastError();
+      return limit_error("batched fused selection + attention LDS exceeds the device limit");
+    }
+    hipLaunchKernelGGL(kernel, dim3(count * h.st.retrieval_heads * parts), dim3(SELECT_THREADS), max_lds, s, table,
+                       h.st.retrieval_heads, parts);
+    return launch_check("select_attend_batch");
+  };
+  constexpr int OWN_MAX = CKV_MAX_COMMUNITIES / SELECT_THREADS;
+  if (h.st.centroid_dtype == CKV_E4M3) {
+    return own <= 1 ? launch(select_attend_batch_kernel<CKV_E4M3, CKV_BF16, 1>)
+           : own <= 2 ? launch(select_attend_batch_kernel<CKV_E4M3, CKV_BF16, 2>)
+           : own <= 4 ? launch(select_attend_batch_kernel<CKV_E4M3, CKV_BF16, 4>)
+                      : launch(select_attend_batch_kernel<CKV_E4M3, CKV_BF16, OWN_MAX>);
+  }
+  return own <= 1 ? launch(select_attend_batch_kernel<CKV_F32, CKV_BF16, 1>)
+         : own <= 2 ? launch(select_attend_batch_kernel<CKV_F32, CKV_BF16, 2>)
+                    : launch(select_attend_batch_kernel<CKV_F32, CKV_BF16, OWN_MAX>);
 }
 
 // Batched selection of `count` items (bf16 KV); `max_nscore`, `max_lds` are the

@@ -239,8 +239,7 @@ class DecodeRuntime:
                                     state=layer.converted.mutable, sink_positions=layer.sink_positions,
                                     current_position=layer.converted.current_position,
                                     softmax_scale=softmax_scale, lam=self.config.lam)
-        call.score_select_after(None if self._pending is None else self._pending[1])
-        call.attention()
+        call.decode_after(None if self._pending is None else self._pending[1])
         self._pending = (layer, call)
         return layer.workspace.attention.output.view(1, 1, query.shape[1], HEAD_DIM)
 

@@ -280,6 +280,18 @@ int ckv_batch_decode(const ckv_layer_args* items, int32_t count, const void* tab
 /* (diagnostics) the attention launch of ckv_batch_decode alone, writing split partials. */
 int ckv_batch_attention_partials(const ckv_layer_args* items, int32_t count, const void* table, void* stream);
 
+/* Scheduling variant, no counterpart in the reference: one layer's decode
+ * (selection + attention; its own online update is left pending) with, in the
+ * same launches, the deferred ckv_online_update of another layer `pending`
+ * (null: none).  Where the slot table fits in LDS (bf16 KV, at most 8192
+ * slots, group_size * 128 <= 512) the selection and the attention partials
+ * run in one launch: each retrieval head's slot table is split over several
+ * workgroups that each repeat the (latency-bound) selection and attend their
+ * own part, so no slot table round-trips through memory and no launch
+ * separates selection from attention; a split merge follows.  Otherwise it is
+ * ckv_score_select_after_update followed by ckv_segmented_attention. */
+int ckv_decode_step_after_update(const ckv_layer_args* layer, const ckv_layer_args* pending, void* stream);
+
 /* ckv_score_select, ckv_segmented_attention and ckv_online_update on one stream. */
 int ckv_decode_layer(const ckv_kv_cache* kv, const ckv_graph_state* state,
                      const ckv_prefill_csr* csr, const ckv_delta_chunks* deltas,

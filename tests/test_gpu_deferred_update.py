@@ -1,6 +1,7 @@
 """Deferred online update (carried by the next layer's selection launch) must
 leave every layer's output and graph state bit-identical to the serial
-select -> attend -> update order."""
+select -> attend -> update order, for the fused selection + attention launch
+and for separate selection and attention launches."""
 
 from __future__ import annotations
 
@@ -24,8 +25,9 @@ def _layer(fx, params, device):
     return dict(state=state, cur=cur, q=q, ws=ws, call=call)
 
 
+@pytest.mark.parametrize("fused", [True, False])
 @pytest.mark.parametrize("assignment", ["delta_q", "nearest_centroid"])
-def test_deferred_update_matches_serial(device, assignment):
+def test_deferred_update_matches_serial(device, assignment, fused):
     params = co.StepParams(group_size=4, num_sink=10, token_budget=512, local_window=64, assignment=assignment)
     fxs = [syn.build_layer(seed=31 + i, query_heads=16, kv_heads=4, seq_len=4096, communities=64, num_sink=10,
                            max_decode_tokens=16, aggregation=co.QUERY_GROUP) for i in range(3)]
@@ -35,11 +37,19 @@ def test_deferred_update_matches_serial(device, assignment):
     for step in range(8):
         print(f"step {step}", flush=True)
         for lay in serial:
-            lay["call"].decode()
+            if fused:
+                lay["call"].decode()  # fused selection + attention, merge, update
+            else:
+                lay["call"].score_select()
+                lay["call"].attention()
+                lay["call"].update()
         pending = None
         for lay in deferred:
-            lay["call"].score_select_after(pending)
-            lay["call"].attention()
+            if fused:
+                lay["call"].decode_after(pending)
+            else:
+                lay["call"].score_select_after(pending)
+                lay["call"].attention()
             pending = lay["call"]
         pending.update()
         torch.cuda.synchronize(device)
