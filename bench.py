@@ -9,10 +9,11 @@ Each layer owns its own KV cache and graph state (4.8 GB in total), so no layer
 finds another's data in the 256 MB Infinity Cache.  The whole step is captured
 in one HIP graph; inputs are resident in HBM before timing starts.
 
-Prints one JSON line: the benchmark contract's fields plus `roofline`
-(attention kernel: algorithmic bytes per launch over its graph-timed duration;
-`traffic` from the committed rocprofv3 counter summary when present) and
-`cpu_baseline` (the numpy oracle on one layer, one core).
+Prints one JSON line: the benchmark contract's fields plus `roofline` (the
+step's dominant kernel, the fused selection + attention launch: algorithmic
+bytes per launch over its graph-timed duration; `traffic` from the committed
+rocprofv3 counter summary when present) and `cpu_baseline` (the numpy oracle
+on one layer, one core).
 """
 
 from __future__ import annotations
@@ -163,9 +164,10 @@ def time_graph(graph, reps, device):
 
 
 def algorithmic_bytes(stack):
-    """Per-layer bytes: attention (K+V rows of valid slots, slot indices, q)
-    and whole step (+ centroid table, sizes, scores, update)."""
-    att, step = [], []
+    """Per-layer bytes: attention (K+V rows of valid slots, slot indices, q),
+    whole step (+ centroid table, sizes, scores, update) and the centroid
+    table (+ sizes, scores) alone."""
+    att, step, cent = [], [], []
     for entry in stack:
         sel = entry["layer"].workspace.selection
         slots = sel.slot_positions
@@ -177,14 +179,16 @@ def algorithmic_bytes(stack):
         s = a + c_bytes + HQ * D * 2 + (D * 2 + 256) * HKV
         att.append(a)
         step.append(s)
-    return float(np.mean(att)), float(np.mean(step)), float(np.mean([int((e["layer"].workspace.selection.slot_positions >= 0).sum()) / HKV for e in stack]))
+        cent.append(c_bytes)
+    tokens = float(np.mean([int((e["layer"].workspace.selection.slot_positions >= 0).sum()) / HKV for e in stack]))
+    return float(np.mean(att)), float(np.mean(step)), tokens, float(np.mean(cent))
 
 
 def profiled_traffic():
-    """HBM bytes per attention launch from the committed rocprofv3 counter
+    """HBM bytes per fused selection + attention launch from the committed rocprofv3 counter
     summary (FETCH_SIZE + WRITE_SIZE per dispatch, scaled by a plain copy of
     known size), or None when that summary is absent."""
-    path = os.path.join(ROOT, "profiles", "attend_mfma_config2_traffic.txt")
+    path = os.path.join(ROOT, "profiles", "select_attend_config2_traffic.txt")
     if not os.path.exists(path):
         return None
     with open(path) as f:
@@ -522,18 +526,15 @@ def main():
     serial_graph = capture(lambda: [e["call"].decode() for e in stack], device)
     serial_graph.replay()
     serial_ms = time_graph(serial_graph, max(5, args.steps // 2), device)
-    att_bytes, step_bytes, tokens_per_head = algorithmic_bytes(stack)
+    att_bytes, step_bytes, tokens_per_head, centroid_bytes = algorithmic_bytes(stack)
     overflow = sum(int(e["layer"].workspace.update.overflow.sum().item()) for e in stack)
 
-    # the attention as the step runs it (split-partials kernel + merge kernel),
-    # and the partials kernel alone (the kernel that moves the KV bytes: the
-    # roofline kernel), 36 launches per replay over the slots of the last step
-    att_graph = capture(lambda: [e["call"].attention() for e in stack], device)
-    att_graph.replay()
-    att_ms = time_graph(att_graph, max(10, args.steps), device) / len(stack)
-    part_graph = capture(lambda: [e["call"].attention_partials() for e in stack], device)
-    part_graph.replay()
-    part_ms = time_graph(part_graph, max(10, args.steps), device) / len(stack)
+    # the fused selection + attention-partials launch alone (the step's dominant
+    # kernel: it reads the centroids and gathers the KV rows), 36 launches per
+    # replay; the layers' states are left as the timed step left them
+    fused_graph = capture(lambda: [e["call"].select_attend_partials() for e in stack], device)
+    fused_graph.replay()
+    fused_ms = time_graph(fused_graph, max(10, args.steps), device) / len(stack)
 
     # dense bf16 decode over the same 32k caches (baseline)
     tiles = -(-SEQ // 64)
@@ -556,7 +557,8 @@ def main():
 
     us_layer = ms * 1e3 / len(stack)
     dense_us_layer = dense_ms * 1e3 / len(stack)
-    achieved = att_bytes / (part_ms * 1e-3) / 1e9
+    fused_bytes = att_bytes + centroid_bytes
+    achieved = fused_bytes / (fused_ms * 1e-3) / 1e9
     result = {
         "metric": "sparse_decode_tokens_per_s_32k_qwen3_8b_attention_stack",
         "value": 1e3 / ms,
@@ -578,15 +580,15 @@ def main():
         "us_per_step_layer_update_inline": serial_ms * 1e3 / len(stack),
         "dense_us_per_step_layer": dense_us_layer,
         "speedup_vs_dense": dense_us_layer / us_layer,
-        "attention_kernel_us": att_ms * 1e3,
-        "attention_partials_kernel_us": part_ms * 1e3,
+        "select_attend_kernel_us": fused_ms * 1e3,
         "attended_tokens_per_head": tokens_per_head,
         "step_algorithmic_bytes_per_layer": step_bytes,
         "step_hbm_frac": step_bytes / (us_layer * 1e-6) / 1e9 / HBM_PEAK_GBS,
         "overflow_flags": overflow,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": profiled_traffic(),
-                     "kernel": "attend_mfma_kernel<false> (gather + split partials)", "bytes_per_launch": att_bytes},
+                     "kernel": "select_attend_kernel (centroid scoring, selection, slot table in LDS, KV gather, "
+                               "split partials)", "bytes_per_launch": fused_bytes},
     }
     if args.copy_probe:
         src = torch.empty(64 << 20, dtype=torch.int32, device=device)

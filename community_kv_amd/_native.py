@@ -53,6 +53,7 @@ EXPORTED_SYMBOLS = (
     "ckv_online_update",
     "ckv_score_select_after_update",
     "ckv_decode_step_after_update",
+    "ckv_select_attend_partials",
     "ckv_batch_table_bytes",
     "ckv_batch_prepare",
     "ckv_batch_decode",
@@ -162,6 +163,8 @@ def lib() -> ctypes.CDLL:
     handle.ckv_score_select_after_update.restype = ctypes.c_int
     handle.ckv_decode_step_after_update.argtypes = [ctypes.POINTER(LayerArgs), ctypes.POINTER(LayerArgs), _p]
     handle.ckv_decode_step_after_update.restype = ctypes.c_int
+    handle.ckv_select_attend_partials.argtypes = [ctypes.POINTER(LayerArgs), _p]
+    handle.ckv_select_attend_partials.restype = ctypes.c_int
     handle.ckv_batch_table_bytes.argtypes = [_i32]
     handle.ckv_batch_table_bytes.restype = ctypes.c_size_t
     handle.ckv_batch_prepare.argtypes = [ctypes.POINTER(LayerArgs), _i32, _p, _p]

@@ -132,6 +132,11 @@ class DecodeCall:
             ctypes.byref(self.layer_args()), None if pending is None else ctypes.byref(pending.layer_args()),
             ctypes.c_void_p(self._stream(stream))))
 
+    def select_attend_partials(self, stream=None) -> None:
+        """The fused selection + attention-partials launch alone (profiling)."""
+        nat.check(nat.lib().ckv_select_attend_partials(ctypes.byref(self.layer_args()),
+                                                       ctypes.c_void_p(self._stream(stream))))
+
     def update(self, stream=None) -> None:
         nat.check(nat.lib().ckv_online_update(*self._args(self._stream(stream))))
 

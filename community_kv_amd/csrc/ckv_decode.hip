@@ -381,3 +381,14 @@ extern "C" int ckv_batch_attention_partials(const ckv_layer_args* items, int32_t
   return ckv::launch_batch_attention(packed[0], reinterpret_cast<const ckv::DecodeArgs*>(table), count,
                                      reinterpret_cast<hipStream_t>(stream), true);
 }
+
+extern "C" int ckv_select_attend_partials(const ckv_layer_args* layer, void* stream) {
+  if (!layer) return fail(CKV_E_INVALID, "null layer arguments");
+  int rc = validate(layer->kv, layer->state, layer->csr, layer->deltas, layer->config, layer->ws);
+  if (!rc) rc = validate_attention(layer->state, layer->deltas, layer->config, layer->ws);
+  if (rc) return rc;
+  const ckv::DecodeArgs a = pack(layer->kv, layer->state, layer->csr, layer->deltas, layer->config, layer->ws);
+  const int parts = ckv::fused_parts(a);
+  if (parts == 0) return fail(CKV_E_INVALID, "the fused selection + attention path cannot serve this layer");
+  return ckv::launch_select_attend(a, reinterpret_cast<hipStream_t>(stream), nullptr, parts);
+}

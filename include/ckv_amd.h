@@ -291,6 +291,9 @@ int ckv_batch_attention_partials(const ckv_layer_args* items, int32_t count, con
  * separates selection from attention; a split merge follows.  Otherwise it is
  * ckv_score_select_after_update followed by ckv_segmented_attention. */
 int ckv_decode_step_after_update(const ckv_layer_args* layer, const ckv_layer_args* pending, void* stream);
+/* (diagnostics) the fused selection + attention-partials launch of
+ * ckv_decode_step_after_update alone (no pending update, no merge). */
+int ckv_select_attend_partials(const ckv_layer_args* layer, void* stream);
 
 /* ckv_score_select, ckv_segmented_attention and ckv_online_update on one stream. */
 int ckv_decode_layer(const ckv_kv_cache* kv, const ckv_graph_state* state,
