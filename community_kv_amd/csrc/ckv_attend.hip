@@ -9,9 +9,6 @@
 namespace ckv {
 
 namespace {
-#ifdef CKV_PHASE_TIMING
-__device__ unsigned long long phase_stamp[32];
-#endif
 }  // namespace
 
 // ---------------------------------------------------------------------------
@@ -425,6 +422,7 @@ __device__ __forceinline__ void merge_wide_body(const DecodeArgs& a, const int r
   const int wave = tid >> 6;
   const int G = a.cfg.group_size;
   const int64_t base = (int64_t)rh * G * splits;
+  CKV_STAMP(rh == 0, 24);
   __shared__ float sc_s[MERGE_WIDE_THREADS / 64][PRE];
   __shared__ float den_s[MERGE_WIDE_THREADS / 64];
   const int i = min(tid, G * D - 1);
@@ -458,6 +456,7 @@ __device__ __forceinline__ void merge_wide_body(const DecodeArgs& a, const int r
     reinterpret_cast<uint16_t*>(a.ws.output)[((int64_t)rh * G + g) * D + (tid & (D - 1))] =
         ckv_f32_to_bf16_bits(acc / den_s[g]);
   }
+  CKV_STAMP(rh == 0, 25);
 }
 
 template <int PRE>

@@ -12,8 +12,11 @@ namespace ckv {
 
 // Phase timestamps (100 MHz wall clock) for latency-profiling builds compiled
 // with -DCKV_PHASE_TIMING; each kernel file then defines its own
-// `phase_stamp` array and a host getter.  Expands to nothing otherwise.
+// copy of the `phase_stamp` array and a host getter.  Expands to nothing otherwise.
 #ifdef CKV_PHASE_TIMING
+namespace {
+__device__ unsigned long long phase_stamp[32];  // one array per kernel file
+}  // namespace
 #define CKV_STAMP(cond, slot)                                         \
   do {                                                               \
     if ((cond) && threadIdx.x == 0) phase_stamp[(slot)] = wall_clock64(); \
@@ -205,6 +208,18 @@ __device__ inline float xor_f32(float v) {
   return ckv_u2f(xor_u32<X>(ckv_f2u(v)));
 }
 
+// v + v[lane ^ X] for X in {1, 2, 4}, written so that the compiler folds the
+// last lane move into the add (v_add_f32 with a DPP operand): every lane has a
+// source under these controls, so the bound-control zero never applies.
+template <int X>
+__device__ inline float add_xor_f32(float v) {
+  uint32_t u = ckv_f2u(v);
+  if constexpr (X == 4) u = dpp_u32<0x1B>(u);  // quad reverse, then the half-row mirror below
+  constexpr int CTRL = X == 1 ? 0xB1 : (X == 2 ? 0x4E : 0x141);
+  static_assert(X == 1 || X == 2 || X == 4, "xor distance");
+  return v + ckv_u2f((uint32_t)__builtin_amdgcn_update_dpp(0, (int)u, CTRL, 0xF, 0xF, true));
+}
+
 // v + v[lane ^ 16] (resp. 32) on every lane, as one swap and one add.
 __device__ inline float add_xor16(float v) {
   const auto r = __builtin_amdgcn_permlane16_swap(ckv_f2u(v), ckv_f2u(v), false, false);
@@ -241,9 +256,9 @@ __device__ inline float wave_sum_tree(float v) {
   v = add_xor32(v);
   v = add_xor16(v);
   v = v + xor_f32<8>(v);
-  v = v + xor_f32<4>(v);
-  v = v + xor_f32<2>(v);
-  return v + xor_f32<1>(v);
+  v = add_xor_f32<4>(v);
+  v = add_xor_f32<2>(v);
+  return add_xor_f32<1>(v);
 }
 
 template <int CTRL>

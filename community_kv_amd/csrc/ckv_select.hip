@@ -31,9 +31,6 @@
 namespace ckv {
 
 namespace {
-#ifdef CKV_PHASE_TIMING
-__device__ unsigned long long phase_stamp[32];
-#endif
 
 int limit_error(const char* message) { return ckv_internal::set_error(CKV_E_LIMIT, message); }
 
@@ -100,9 +97,9 @@ __device__ inline void decode_frag(const CentroidFrag<CT>& f, float* out) {
 __host__ __device__ inline size_t fused_slot_bytes(int slot_capacity) { return ((size_t)slot_capacity * 4 + 15) & ~(size_t)15; }
 
 // FUSED: `part` of `parts` workgroups of this head each run the whole
-// selection (they are latency-bound, so the copies cost no time), keep the
-// full slot table in LDS, and then attend their own part of it
-// (attend_part); only part 0 writes the selection's outputs.
+// selection (they are latency-bound, so the copies cost no time), resolve the
+// slots of their own tiles only, attend them (attend_part) and write that
+// part of the slot table; part 0 writes the selection's other outputs.
 template <int CT, int DT, int OWN, bool FUSED = false>
 __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, const int part = 0,
                                             const int parts = 1) {
@@ -118,7 +115,7 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
   const int ns = a.cfg.num_sink;
   const int W = a.cfg.local_window;
   const int cpg = a.dl.chunks_per_graph;
-  CKV_STAMP(rh == 0, 0);
+  CKV_STAMP(rh == 0 && part == 0, 0);
 
   __shared__ float q_s[CKV_MAX_GROUP * D];
   __shared__ float key_s[D];
@@ -129,7 +126,7 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
   __shared__ int s_bin, s_above, s_max_idx, s_sel_count, s_last_sel_pos, s_last_size, s_sink_max;
 
   extern __shared__ __align__(16) unsigned char dyn_all[];
-  // fused: the slot table first, then the selection arrays (later the attention buffers)
+  // fused: the window tokens' communities first, then the selection arrays (later the attention buffers)
   int* slot_lds = reinterpret_cast<int*>(dyn_all);
   unsigned char* dyn = dyn_all + (FUSED ? fused_slot_bytes(a.ws.slot_capacity) : 0);
   const bool writer = !FUSED || part == 0;  // writes the selection's global outputs
@@ -268,7 +265,7 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
   hist[tid & 255] = 0;
   if (tid == 0) s_max_idx = -1;
   __syncthreads();  // q_s, key_s, sink_s, hist
-  CKV_STAMP(rh == 0, 6);
+  CKV_STAMP(rh == 0 && part == 0, 6);
   if (tid < 64) {  // largest sink position: window tokens beyond it skip the sink test
     int m = -1;
     for (int i = tid; i < ns; i += 64) m = max(m, sink_s[i]);
@@ -320,12 +317,12 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
             a1 = a1 + qb[i] * cv[i];
           }
         }
-        a0 = a0 + xor_f32<4>(a0);
-        a1 = a1 + xor_f32<4>(a1);
-        a0 = a0 + xor_f32<2>(a0);
-        a1 = a1 + xor_f32<2>(a1);
-        a0 = a0 + xor_f32<1>(a0);
-        a1 = a1 + xor_f32<1>(a1);
+        a0 = add_xor_f32<4>(a0);
+        a1 = add_xor_f32<4>(a1);
+        a0 = add_xor_f32<2>(a0);
+        a1 = add_xor_f32<2>(a1);
+        a0 = add_xor_f32<1>(a0);
+        a1 = add_xor_f32<1>(a1);
         best[pb] = fmax_exact(best[pb], a0);
         if (g + 1 < G) best[pb] = fmax_exact(best[pb], a1);
       }
@@ -348,9 +345,9 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
           const float di = key_s[16 * lane8 + i] - cv[i];
           acc = acc + di * di;
         }
-        acc = acc + xor_f32<4>(acc);
-        acc = acc + xor_f32<2>(acc);
-        acc = acc + xor_f32<1>(acc);
+        acc = add_xor_f32<4>(acc);
+        acc = add_xor_f32<2>(acc);
+        acc = add_xor_f32<1>(acc);
         if (live) {
           const uint64_t cand = ((uint64_t)ckv_f2u(acc) << 32) | (uint32_t)c;
           best_nearest = cand < best_nearest ? cand : best_nearest;
@@ -365,13 +362,13 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
     score_batch(p0 + PB, 1);
     load_batch(p0 + 3 * PB, 1);
   }
-  CKV_STAMP(rh == 0, 7);
+  CKV_STAMP(rh == 0 && part == 0, 7);
   if (nearest_mode) {
     const uint64_t w = wave_min_u64(best_nearest);
     if ((tid & 63) == 0) near_s[tid >> 6] = w;
   }
   __syncthreads();  // key16, near_s
-  CKV_STAMP(rh == 0, 1);
+  CKV_STAMP(rh == 0 && part == 0, 1);
 
   // ---- exact weighted selection ---------------------------------------------
   const bool budget_mode = a.cfg.selection_mode == CKV_SELECT_BUDGET;
@@ -386,13 +383,13 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
     if (live) atomicAdd(hist + (o_key[k] >> 8), budget_mode ? o_size[k] : 1);
   }
   __syncthreads();
-  CKV_STAMP(rh == 0, 12);
+  CKV_STAMP(rh == 0 && part == 0, 12);
   // key16 is dead from here on; it becomes the community -> descriptor table.
   uint16_t* comm_desc = key16;
   for (int c = tid; c < nscore; c += SELECT_THREADS) comm_desc[c] = 0xffffu;
   if (tid < 64) find_threshold_bin(hist, target, &s_bin, &s_above);
   __syncthreads();
-  CKV_STAMP(rh == 0, 13);
+  CKV_STAMP(rh == 0 && part == 0, 13);
   const int hb = s_bin;
   int threshold;  // 16-bit key threshold; -1 selects every non-empty community
   if (hb < 0) {
@@ -413,7 +410,7 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
     __syncthreads();
     threshold = (hb << 8) | s_bin;
   }
-  CKV_STAMP(rh == 0, 2);
+  CKV_STAMP(rh == 0 && part == 0, 2);
 
   // Compaction, high keys first (id order), then threshold keys (id order): one
   // four-component block scan (high count/mass, threshold count/mass).
@@ -500,7 +497,7 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
   __syncthreads();  // descriptors, s_max_idx
   const int n_desc = s_max_idx + 1;
   const int sel_count = n_desc > 0 ? desc_end[n_desc - 1] : 0;
-  CKV_STAMP(rh == 0, 15);
+  CKV_STAMP(rh == 0 && part == 0, 15);
   const int nblk = (sel_count + 63) / 64;
   for (int b = tid; b <= nblk; b += SELECT_THREADS) {
     const int j = 64 * b;
@@ -523,154 +520,196 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
     }
   }
   if (tid == 0) s_last_sel_pos = -1;
-  CKV_STAMP(rh == 0, 3);
+  CKV_STAMP(rh == 0 && part == 0, 3);
 
   const int slot_cap = a.ws.slot_capacity;
   int32_t* slots = a.ws.slot_positions + (int64_t)rh * slot_cap;
   const int inc = a.cfg.include_current ? 1 : 0;
   const int wbeg = ns + sel_count;
+  int fused_pos = -1;  // FUSED: this lane's slot of its wave's tile
   if (materialise) {
-    __syncthreads();  // blk_first, comm_desc, s_last_size
-    CKV_STAMP(rh == 0, 16);
+    if constexpr (FUSED) {
+      // The window tokens' communities, for whichever wave resolves them (the
+      // slot table region is free: fused workgroups resolve only their own tiles).
+#pragma unroll
+      for (int h = 0; h < WIN_PER_THREAD; ++h) {
+        const int i = tid + h * SELECT_THREADS;
+        if (i < W) slot_lds[i] = wcomm[h];
+      }
+    }
+    __syncthreads();  // blk_first, comm_desc, s_last_size (and the window communities)
+    CKV_STAMP(rh == 0 && part == 0, 16);
     // ---- R3: slot materialisation ---------------------------------------------
     // Layout: sinks, selected members (newest first: decode deltas from the
     // tail chunk backwards, then the recency-descending CSR), window, current.
-    // Each wave resolves 64-slot blocks of the selection, lane = slot (coalesced
-    // gathers): a lane's descriptor is the block's first descriptor plus the
-    // number of descriptor ends at or before it, read off a wave-wide bit mask
-    // of the ends that fall inside the block (no search chains).
     const int32_t* members = a.csr.member_positions + (int64_t)graph * a.csr.member_stride;
     const int32_t* dpos = a.dl.positions + (int64_t)graph * a.dl.position_capacity;
     const int lane = tid & 63, wave = tid >> 6;
-    const int nblk_sel = (sel_count + 63) / 64;
-    for (int b0 = wave; b0 < nblk_sel; b0 += WAVES * MAT_BATCH) {
-      const int32_t* src[MAT_BATCH];
-      bool gathered[MAT_BATCH];
-      int slow_d[MAT_BATCH], slow_rem[MAT_BATCH];  // delta members beyond the tail chunk
+    // Source of selected member j (0 <= j < sel_count) of descriptor d: a
+    // decode-delta position of the tail chunk, a CSR member, or (slow_d >= 0) a
+    // delta member older than the tail chunk, resolved by walk_chain.
+    auto member_src = [&](int j, int d, const int32_t*& src, bool& gathered, int& slow_d, int& slow_rem) {
+      const int m = j - (d > 0 ? desc_end[d - 1] : 0);
+      const int dc = desc_dc[d];
+      if (m < dc) {
+        const int tn = desc_tn[d];
+        if (m < tn) {
+          const int p = desc_ts[d] + tn - 1 - m;
+          if (p >= 0 && p < a.dl.position_capacity) {
+            src = dpos + p;
+            gathered = true;
+          }
+        } else {
+          slow_d = d;
+          slow_rem = m - tn;
+        }
+      } else {
+        const int64_t idx = (int64_t)desc_lo[d] + (m - dc);
+        if (idx >= 0 && idx < a.csr.member_stride) {
+          src = members + idx;
+          gathered = true;
+        }
+      }
+    };
+    auto walk_chain = [&](int d, int rem, int& val) {
+      const int tail = desc_tl[d];
+      if (tail < 0 || tail >= cpg) return;
+      int ch = a.dl.chunk_previous[cb + tail];
+      for (int guard = 0; guard < 64 && ch >= 0 && ch < cpg; ++guard) {
+        const int cs = a.dl.chunk_size[cb + ch];
+        if (rem < cs) {
+          const int p = a.dl.chunk_start[cb + ch] + cs - 1 - rem;
+          if (p >= 0 && p < a.dl.position_capacity) val = dpos[p];
+          return;
+        }
+        rem -= cs;
+        ch = a.dl.chunk_previous[cb + ch];
+      }
+    };
+    // Window slot i (position cur-W+i), or -1 when that token is already
+    // attended (a sink, or a member of a selected community at or after the
+    // selection's oldest position); wc is the token's community.
+    auto window_pos = [&](int i, int wc, int last_pos) {
+      const int p = cur - W + i;
+      int pos = p < 0 ? -1 : p;
+      if (pos >= 0 && p <= s_sink_max) {
+        for (int k = 0; k < ns; ++k) {
+          if (sink_s[k] == p) pos = -1;
+        }
+      }
+      if (pos >= 0 && p < a.st.token_capacity && wc >= 0 && wc < count) {
+        const int found = comm_desc[wc] == 0xffffu ? -1 : (int)comm_desc[wc];
+        if (found >= 0) {
+          const int take = desc_end[found] - (found > 0 ? desc_end[found - 1] : 0);
+          const bool full = found < n_desc - 1 || take >= s_last_size;
+          if (full || p >= last_pos) pos = -1;
+        }
+      }
+      return pos;
+    };
+    if constexpr (FUSED) {
+      // Each wave below FUSED_TILES resolves the 64 slots of its own tile
+      // (lane = slot); wave FUSED_TILES resolves the last selected slot, whose
+      // position bounds the window, in the same gather round.
+      const int tile = part * FUSED_TILES + wave;
+      const bool mine = wave < FUSED_TILES && tile < slot_cap / TILE;
+      const int s = wave == FUSED_TILES ? wbeg - 1 : tile * TILE + lane;
+      const int j = s - ns;
+      const bool sel = (mine || (wave == FUSED_TILES && sel_count > 0)) && j >= 0 && j < sel_count;
+      const int32_t* src = a.st.community_counts + rh;  // in-bounds dummy address when nothing is gathered
+      bool gathered = false;
+      int slow_d = -1, slow_rem = 0;
+      if (sel) {
+        // first descriptor ending after j, between the first descriptors of j's block and the next
+        int lo = blk_first[j >> 6], hi = min(blk_first[(j >> 6) + 1], n_desc - 1);
+        while (lo < hi) {
+          const int mid = (lo + hi) >> 1;
+          if (desc_end[mid] <= j) lo = mid + 1; else hi = mid;
+        }
+        member_src(j, lo, src, gathered, slow_d, slow_rem);
+      }
+      CKV_STAMP(rh == 0 && part == 0, 17);
+      int val = gload_i32(src);
+      if (!gathered) val = -1;
+      if (slow_d >= 0) walk_chain(slow_d, slow_rem, val);
+      if (wave == FUSED_TILES && lane == 0 && sel) s_last_sel_pos = val;
+      __syncthreads();  // s_last_sel_pos
+      CKV_STAMP(rh == 0 && part == 0, 4);
+      if (mine) {
+        if (s < ns) {
+          fused_pos = sink_s[s];
+        } else if (sel) {
+          fused_pos = val;
+        } else if (s < wbeg + W) {
+          const int i = s - wbeg;
+          fused_pos = window_pos(i, slot_lds[i], s_last_sel_pos);
+        } else if (inc && s == wbeg + W) {
+          fused_pos = cur;
+        }
+      }
+    } else {
+      // Each wave resolves 64-slot blocks of the selection, lane = slot
+      // (coalesced gathers): a lane's descriptor is the block's first descriptor
+      // plus the number of descriptor ends at or before it, read off a wave-wide
+      // bit mask of the ends that fall inside the block (no search chains).
+      const int nblk_sel = (sel_count + 63) / 64;
+      for (int b0 = wave; b0 < nblk_sel; b0 += WAVES * MAT_BATCH) {
+        const int32_t* src[MAT_BATCH];
+        bool gathered[MAT_BATCH];
+        int slow_d[MAT_BATCH], slow_rem[MAT_BATCH];
 #pragma unroll
-      for (int q = 0; q < MAT_BATCH; ++q) {
-        const int b = b0 + q * WAVES;
-        src[q] = a.st.community_counts + rh;  // in-bounds dummy address when nothing is gathered
-        gathered[q] = false;
-        slow_d[q] = -1;
-        slow_rem[q] = 0;
-        if (b < nblk_sel) {  // wave-uniform
-          const int base = 64 * b;
-          const int j = base + lane;
-          const int d0 = blk_first[b];
-          const int e = d0 + lane < n_desc ? desc_end[d0 + lane] : 0x7fffffff;
-          const int off = e - base;
-          const uint64_t mask = wave_or_u64(off >= 1 && off <= 63 ? (1ull << off) : 0ull);
-          const uint64_t below = lane == 63 ? ~0ull : ((2ull << lane) - 1ull);
-          const int d = d0 + __popcll(mask & below);
+        for (int q = 0; q < MAT_BATCH; ++q) {
+          const int b = b0 + q * WAVES;
+          src[q] = a.st.community_counts + rh;  // in-bounds dummy address when nothing is gathered
+          gathered[q] = false;
+          slow_d[q] = -1;
+          slow_rem[q] = 0;
+          if (b < nblk_sel) {  // wave-uniform
+            const int base = 64 * b;
+            const int j = base + lane;
+            const int d0 = blk_first[b];
+            const int e = d0 + lane < n_desc ? desc_end[d0 + lane] : 0x7fffffff;
+            const int off = e - base;
+            const uint64_t mask = wave_or_u64(off >= 1 && off <= 63 ? (1ull << off) : 0ull);
+            const uint64_t below = lane == 63 ? ~0ull : ((2ull << lane) - 1ull);
+            const int d = d0 + __popcll(mask & below);
+            if (j < sel_count) member_src(j, d, src[q], gathered[q], slow_d[q], slow_rem[q]);
+          }
+        }
+        CKV_STAMP(rh == 0 && part == 0 && b0 == 0, 17);
+        int val[MAT_BATCH];
+#pragma unroll
+        for (int q = 0; q < MAT_BATCH; ++q) val[q] = gload_i32(src[q]);
+#pragma unroll
+        for (int q = 0; q < MAT_BATCH; ++q) {
+          if (!gathered[q]) val[q] = -1;
+        }
+#pragma unroll
+        for (int q = 0; q < MAT_BATCH; ++q) {
+          if (slow_d[q] >= 0) walk_chain(slow_d[q], slow_rem[q], val[q]);
+        }
+#pragma unroll
+        for (int q = 0; q < MAT_BATCH; ++q) {
+          const int j = 64 * (b0 + q * WAVES) + lane;
           if (j < sel_count) {
-            const int m = j - (d > 0 ? desc_end[d - 1] : 0);
-            const int dc = desc_dc[d];
-            if (m < dc) {
-              const int tn = desc_tn[d];
-              if (m < tn) {
-                const int p = desc_ts[d] + tn - 1 - m;
-                if (p >= 0 && p < a.dl.position_capacity) {
-                  src[q] = dpos + p;
-                  gathered[q] = true;
-                }
-              } else {
-                slow_d[q] = d;
-                slow_rem[q] = m - tn;
-              }
-            } else {
-              const int64_t idx = (int64_t)desc_lo[d] + (m - dc);
-              if (idx >= 0 && idx < a.csr.member_stride) {
-                src[q] = members + idx;
-                gathered[q] = true;
-              }
-            }
+            slots[ns + j] = val[q];
+            if (j == sel_count - 1) s_last_sel_pos = val[q];
           }
         }
       }
-      CKV_STAMP(rh == 0 && b0 == 0, 17);
-      int val[MAT_BATCH];
+      if (tid < ns) slots[tid] = sink_s[tid];
+      __syncthreads();  // s_last_sel_pos
+      CKV_STAMP(rh == 0 && part == 0, 4);
+      const int last_pos = s_last_sel_pos;
 #pragma unroll
-      for (int q = 0; q < MAT_BATCH; ++q) val[q] = gload_i32(src[q]);
-#pragma unroll
-      for (int q = 0; q < MAT_BATCH; ++q) {
-        if (!gathered[q]) val[q] = -1;
+      for (int h = 0; h < WIN_PER_THREAD; ++h) {
+        const int i = tid + h * SELECT_THREADS;
+        if (i < W) slots[wbeg + i] = window_pos(i, wcomm[h], last_pos);
       }
-      // Delta members older than the tail chunk: walk the chunk chain backwards.
-#pragma unroll
-      for (int q = 0; q < MAT_BATCH; ++q) {
-        if (slow_d[q] < 0) continue;
-        const int tail = desc_tl[slow_d[q]];
-        if (tail < 0 || tail >= cpg) continue;
-        int rem = slow_rem[q];
-        int ch = a.dl.chunk_previous[cb + tail];
-        for (int guard = 0; guard < 64 && ch >= 0 && ch < cpg; ++guard) {
-          const int cs = a.dl.chunk_size[cb + ch];
-          if (rem < cs) {
-            const int p = a.dl.chunk_start[cb + ch] + cs - 1 - rem;
-            if (p >= 0 && p < a.dl.position_capacity) val[q] = dpos[p];
-            break;
-          }
-          rem -= cs;
-          ch = a.dl.chunk_previous[cb + ch];
-        }
-      }
-#pragma unroll
-      for (int q = 0; q < MAT_BATCH; ++q) {
-        const int j = 64 * (b0 + q * WAVES) + lane;
-        if (j < sel_count) {
-          if (FUSED) slot_lds[ns + j] = val[q];
-          if (writer) slots[ns + j] = val[q];
-          if (j == sel_count - 1) s_last_sel_pos = val[q];
-        }
-      }
-    }
-    if (tid < ns) {
-      if (FUSED) slot_lds[tid] = sink_s[tid];
-      if (writer) slots[tid] = sink_s[tid];
-    }
-    __syncthreads();  // s_last_sel_pos
-    CKV_STAMP(rh == 0, 4);
-    // Window: positions cur-W .. cur-1 not already attended (sinks, or members
-    // of a selected community at or after the selection's oldest position).
-    const int last_pos = s_last_sel_pos;
-    const int sink_max = s_sink_max;
-#pragma unroll
-    for (int h = 0; h < WIN_PER_THREAD; ++h) {
-      const int i = tid + h * SELECT_THREADS;
-      if (i < W) {
-        const int p = cur - W + i;
-        int pos = p < 0 ? -1 : p;
-        if (pos >= 0 && p <= sink_max) {
-          for (int k = 0; k < ns; ++k) {
-            if (sink_s[k] == p) pos = -1;
-          }
-        }
-        if (pos >= 0 && p < a.st.token_capacity) {
-          const int c = wcomm[h];
-          if (c >= 0 && c < count) {
-            const int found = comm_desc[c] == 0xffffu ? -1 : (int)comm_desc[c];
-            if (found >= 0) {
-              const int take = desc_end[found] - (found > 0 ? desc_end[found - 1] : 0);
-              const bool full = found < n_desc - 1 || take >= s_last_size;
-              if (full || p >= last_pos) pos = -1;
-            }
-          }
-        }
-        if (FUSED) slot_lds[wbeg + i] = pos;
-        if (writer) slots[wbeg + i] = pos;
-      }
-    }
-    if (inc && tid == 0) {
-      if (FUSED) slot_lds[wbeg + W] = cur;
-      if (writer) slots[wbeg + W] = cur;
-    }
-    for (int s = wbeg + W + inc + tid; s < slot_cap; s += SELECT_THREADS) {
-      if (FUSED) slot_lds[s] = -1;
-      if (writer) slots[s] = -1;
+      if (inc && tid == 0) slots[wbeg + W] = cur;
+      for (int s = wbeg + W + inc + tid; s < slot_cap; s += SELECT_THREADS) slots[s] = -1;
     }
   }
-
   // ---- outputs that nothing in this kernel reads back --------------------------
   if (writer) {
   if (tid == 0) {
@@ -706,10 +745,10 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
     a.ws.nearest[rh] = (m == ~0ull) ? -1 : (int)(m & 0xffffffffu);
   }
   }  // writer
-  CKV_STAMP(rh == 0, 5);
+  CKV_STAMP(rh == 0 && part == 0, 5);
   if constexpr (FUSED) {
-    __syncthreads();  // slot table complete; the selection arrays are dead from here
-    attend_part<SELECT_THREADS / 64, FUSED_TILES>(a, rh, part, parts, slot_lds, dyn);
+    __syncthreads();  // the selection arrays are dead from here
+    attend_part<SELECT_THREADS / 64, FUSED_TILES>(a, rh, part, parts, fused_pos, dyn);
   }
 }
 

@@ -170,11 +170,12 @@ __device__ inline TileResult mfma_tile(const uint16_t* __restrict__ K, const uin
 }
 
 
-// Fused-path attention of one part of a retrieval head's slot table held in
-// LDS: the first TP of the workgroup's W waves take the part's 64-slot tiles
-// (tile = part * TP + wave), run mfma_tile, combine into split partial `part` of
-// `parts` (max, sum, unnormalised P.V per query) and write every slot's
-// query-0 score (the candidates of the online update's top-8).
+// Fused-path attention of one part of a retrieval head's slot table: the first
+// TP of the workgroup's W waves take the part's 64-slot tiles (tile = part * TP
+// + wave; `pos` = the KV position of this lane's slot, -1 for none), run
+// mfma_tile, combine into split partial `part` of `parts` (max, sum,
+// unnormalised P.V per query) and write every slot's position and query-0 score
+// (the candidates of the online update's top-8).
 // `lds` (16-byte aligned) holds attend_part_lds_bytes(W) bytes.
 constexpr size_t attend_part_lds_bytes(int waves) {
   return (size_t)waves * (V_HALF_ROWS * D * 2 + TILE * 4 + TILE * 4 + 2 * CKV_MAX_GROUP * 4);
@@ -182,7 +183,7 @@ constexpr size_t attend_part_lds_bytes(int waves) {
 
 template <int W, int TP>
 __device__ inline void attend_part(const DecodeArgs& a, const int rh, const int part, const int parts,
-                                   const int* slot_lds, unsigned char* lds) {
+                                   int pos, unsigned char* lds) {
   static_assert(TP <= W, "one tile per wave");
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -206,11 +207,12 @@ __device__ inline void attend_part(const DecodeArgs& a, const int rh, const int 
   const int tile = part * TP + wave;
   const int slot = tile * TILE + lane;
   const bool in_range = wave < TP && tile < tiles;
-  int pos = in_range ? slot_lds[slot] : -1;
+  const int raw_pos = in_range ? pos : -1;
   const bool valid = in_range && pos >= 0 && pos < a.kv.capacity;
   if (!valid) pos = -1;
   pos_s[lane] = pos;
   const bool any = __ballot(valid) != 0ull;
+  CKV_STAMP(rh == 0 && part == 0, 18);
   const uint4 zero = {0u, 0u, 0u, 0u};
   QOperand qop;
 #pragma unroll
@@ -227,6 +229,7 @@ __device__ inline void attend_part(const DecodeArgs& a, const int rh, const int 
     const TileResult r = mfma_tile<2>(K, V, kvh * a.kv.head_stride, a.kv.token_stride, pos_s, v_s,
                                       want_topk ? cand_s : nullptr, qop, a.cfg.softmax_scale, NEG_INF, o);
     wave_sync();
+    CKV_STAMP(rh == 0 && part == 0, 19);
     if (L == 0 && c16 < G) {
       wm_s[wave * CKV_MAX_GROUP + c16] = r.m;
       wl_s[wave * CKV_MAX_GROUP + c16] = r.l;
@@ -240,14 +243,17 @@ __device__ inline void attend_part(const DecodeArgs& a, const int rh, const int 
       }
     }
     if (want_topk && in_range) a.ws.slot_scores[(int64_t)rh * a.ws.slot_capacity + slot] = cand_s[lane];
+    if (in_range) a.ws.slot_positions[(int64_t)rh * a.ws.slot_capacity + slot] = raw_pos;
   } else {
     if (L == 0 && c16 < G) {
       wm_s[wave * CKV_MAX_GROUP + c16] = NEG_INF;
       wl_s[wave * CKV_MAX_GROUP + c16] = 0.0f;
     }
     if (want_topk && in_range) a.ws.slot_scores[(int64_t)rh * a.ws.slot_capacity + slot] = NEG_INF;
+    if (in_range) a.ws.slot_positions[(int64_t)rh * a.ws.slot_capacity + slot] = raw_pos;
   }
   __syncthreads();
+  CKV_STAMP(rh == 0 && part == 0, 20);
   // Combine the waves into this part's split partial.
   for (int i = tid; i < G * D; i += 64 * W) {
     const int g = i >> 7;
@@ -279,6 +285,8 @@ __device__ inline void attend_part(const DecodeArgs& a, const int rh, const int 
     a.ws.partial_max[((int64_t)rh * G + tid) * parts + part] = M;
     a.ws.partial_sum[((int64_t)rh * G + tid) * parts + part] = l;
   }
+  CKV_STAMP(rh == 0 && part == 0, 21);
+  CKV_STAMP_MAX(rh == 0, 22);
 }
 
 }  // namespace ckv
