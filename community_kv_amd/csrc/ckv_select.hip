@@ -355,9 +355,12 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
       }
     }
   };
-  for (int p0 = 0; p0 < passes; p0 += 2 * PB) {
+  // Passes past the live communities (score headroom for communities that
+  // have not formed yet) are skipped; their clamped prefetches are harmless.
+  const int live_passes = (count + ROWS_PER_PASS - 1) / ROWS_PER_PASS;
+  for (int p0 = 0; p0 < live_passes; p0 += 2 * PB) {
     score_batch(p0, 0);
-    if (p0 + PB >= passes) break;
+    if (p0 + PB >= live_passes) break;
     load_batch(p0 + 2 * PB, 0);
     score_batch(p0 + PB, 1);
     load_batch(p0 + 3 * PB, 1);
