@@ -159,16 +159,16 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
   // while the current one is scored.
   CentroidFrag<CT> frag[2][PB];
   int rsize[2][PB];
-  auto load_batch = [&](int p0, int buf) {
+  auto load_batch = [&](int p0, int buf, int last_row) {
 #pragma unroll
     for (int pb = 0; pb < PB; ++pb) {
-      const int row = min((p0 + pb) * ROWS_PER_PASS + sub, nscore - 1);
+      const int row = min((p0 + pb) * ROWS_PER_PASS + sub, last_row);
       load_frag<CT>(a.st.centroids, (int64_t)rh * C + row, 16 * lane8, frag[buf][pb]);
       rsize[buf][pb] = gload_i32(a.st.community_sizes + (int64_t)rh * C + row);
     }
   };
-  load_batch(0, 0);
-  load_batch(PB, 1);  // clamped rows: harmless when there is no second batch
+  load_batch(0, 0, nscore - 1);
+  load_batch(PB, 1, nscore - 1);  // clamped rows: harmless when there is no second batch
   // Query group: two elements per thread (G * 128 <= 2048 <= 4 * threads).
   float qv[4];
 #pragma unroll
@@ -356,14 +356,17 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
     }
   };
   // Passes past the live communities (score headroom for communities that
-  // have not formed yet) are skipped; their clamped prefetches are harmless.
+  // have not formed yet) are skipped.  Prefetches past them are clamped to the
+  // last live row (cache hits): the first use of any earlier load after the
+  // loop waits for every load issued in it.
   const int live_passes = (count + ROWS_PER_PASS - 1) / ROWS_PER_PASS;
+  const int last_live = max(count, 1) - 1;
   for (int p0 = 0; p0 < live_passes; p0 += 2 * PB) {
     score_batch(p0, 0);
     if (p0 + PB >= live_passes) break;
-    load_batch(p0 + 2 * PB, 0);
+    load_batch(p0 + 2 * PB, 0, last_live);
     score_batch(p0 + PB, 1);
-    load_batch(p0 + 3 * PB, 1);
+    load_batch(p0 + 3 * PB, 1, last_live);
   }
   CKV_STAMP(rh == 0 && part == 0, 7);
   if (nearest_mode) {
@@ -438,7 +441,9 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
 #pragma unroll
     for (int i = 0; i < 4; ++i) inc[i] = wave_inclusive_scan(v4[i]);
     if (lane == 63) *reinterpret_cast<int4*>(scan_s + 4 * wave) = int4{inc[0], inc[1], inc[2], inc[3]};
+    CKV_STAMP(rh == 0 && part == 0, 8);
     __syncthreads();
+    CKV_STAMP(rh == 0 && part == 0, 9);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       b4[i] = inc[i] - v4[i];
@@ -495,6 +500,7 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
         em += size;
       }
     }
+    CKV_STAMP(rh == 0 && part == 0, 10);
     if (my_max >= 0) atomicMax(&s_max_idx, my_max);
   }
   __syncthreads();  // descriptors, s_max_idx
@@ -714,6 +720,7 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
     }
   }
   // ---- outputs that nothing in this kernel reads back --------------------------
+  CKV_STAMP(rh == 0 && part == 0, 11);
   if (writer) {
   if (tid == 0) {
     a.ws.descriptor_counts[rh] = n_desc;

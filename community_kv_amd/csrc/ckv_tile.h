@@ -213,6 +213,7 @@ __device__ inline void attend_part(const DecodeArgs& a, const int rh, const int 
   pos_s[lane] = pos;
   const bool any = __ballot(valid) != 0ull;
   CKV_STAMP(rh == 0 && part == 0, 18);
+  CKV_STAMP(rh == 0 && part == 1, 23);
   const uint4 zero = {0u, 0u, 0u, 0u};
   QOperand qop;
 #pragma unroll
