@@ -18,7 +18,8 @@ PACKAGE_DIR = os.path.dirname(os.path.abspath(__file__))
 REPO_DIR = os.path.dirname(PACKAGE_DIR)
 LIB_PATH = os.path.join(PACKAGE_DIR, "libckv_amd.so")
 SOURCES = [os.path.join(PACKAGE_DIR, "csrc", name)
-           for name in ("ckv_decode.hip", "ckv_select.hip", "ckv_attend.hip", "ckv_prefill.hip", "ckv_diag.hip")]
+           for name in ("ckv_decode.hip", "ckv_select.hip", "ckv_attend.hip", "ckv_prefill.hip", "ckv_diag.hip",
+                                "ckv_state.hip")]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 HIP_FLAGS = [
     "--offload-arch=gfx950",
@@ -36,6 +37,7 @@ CKV_BF16, CKV_F32, CKV_E4M3 = 0, 1, 2
 CKV_SELECT_BUDGET, CKV_SELECT_TOPK = 0, 1
 CKV_ASSIGN_NONE, CKV_ASSIGN_DELTA_Q, CKV_ASSIGN_NEAREST = 0, 1, 2
 
+HEAD_DIM = 128
 TILE = 64
 KAPPA = 8
 SCORE_BLOCK = 64
@@ -60,6 +62,9 @@ EXPORTED_SYMBOLS = (
     "ckv_batch_attention_partials",
     "ckv_dense_decode",
     "ckv_prefill_attention_topk",
+    "ckv_state_workspace_bytes",
+    "ckv_label_counts",
+    "ckv_build_layer_state",
     "ckv_host_numerics",
     "ckv_device_numerics",
     "ckv_abi_version",
@@ -132,6 +137,16 @@ class PrefillArgs(ctypes.Structure):
                 ("softmax_scale", _f32), ("reserved", _f32)]
 
 
+class StateBuildArgs(ctypes.Structure):
+    _fields_ = [("labels", _p), ("keys", _p), ("head_stride", _i64), ("token_stride", _i64),
+                ("retrieval_to_graph", _p), ("retrieval_to_kv", _p), ("edge_src", _p), ("edge_dst", _p),
+                ("edge_weight", _p), ("edges", _i64), ("graphs", _i32), ("seq_len", _i32), ("num_sink", _i32),
+                ("retrieval_heads", _i32), ("kv_heads", _i32), ("key_dtype", _i32), ("centroid_dtype", _i32),
+                ("max_communities", _i32), ("community_capacity", _i32), ("token_capacity", _i32),
+                ("member_offsets", _p), ("member_positions", _p), ("centroids", _p), ("community_sizes", _p),
+                ("community_weight", _p), ("total_weight", _p), ("token_communities", _p), ("workspace", _p)]
+
+
 def build(verbose: bool = False) -> str:
     """Compiles libckv_amd.so for gfx950 in-tree (always recompiles)."""
     sources = [s for s in SOURCES if os.path.exists(s)]
@@ -178,6 +193,12 @@ def lib() -> ctypes.CDLL:
     if hasattr(handle, "ckv_prefill_attention_topk"):
         handle.ckv_prefill_attention_topk.argtypes = [ctypes.POINTER(PrefillArgs), _p]
         handle.ckv_prefill_attention_topk.restype = ctypes.c_int
+    handle.ckv_state_workspace_bytes.argtypes = [_i32, _i32, _i32, _i32]
+    handle.ckv_state_workspace_bytes.restype = ctypes.c_size_t
+    handle.ckv_label_counts.argtypes = [_p, _i32, _i32, _i32, _p, _p]
+    handle.ckv_label_counts.restype = ctypes.c_int
+    handle.ckv_build_layer_state.argtypes = [ctypes.POINTER(StateBuildArgs), _p]
+    handle.ckv_build_layer_state.restype = ctypes.c_int
     handle.ckv_host_numerics.argtypes = [ctypes.c_int, _p, _p, _i64]
     handle.ckv_host_numerics.restype = ctypes.c_int
     handle.ckv_device_numerics.argtypes = [ctypes.c_int, _p, _p, _i64, _p]

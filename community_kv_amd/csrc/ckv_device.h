@@ -242,6 +242,15 @@ __device__ inline float max_xor32(float v) {
 }
 
 // Wave-wide max (any pairing gives the same max), result on every lane.
+__device__ inline int wave_max_i32(int v) {
+  v = max(v, (int)xor_u32<1>((uint32_t)v));
+  v = max(v, (int)xor_u32<2>((uint32_t)v));
+  v = max(v, (int)xor_u32<4>((uint32_t)v));
+  v = max(v, (int)xor_u32<8>((uint32_t)v));
+  v = max(v, (int)xor_u32<16>((uint32_t)v));
+  return max(v, (int)xor_u32<32>((uint32_t)v));
+}
+
 __device__ inline float wave_max(float v) {
   v = fmax_exact(v, ckv_u2f(dpp_u32<0xB1>(ckv_f2u(v))));
   v = fmax_exact(v, ckv_u2f(dpp_u32<0x4E>(ckv_f2u(v))));

@@ -1,0 +1,396 @@
+// Prefill graph state assembled on the GPU from dense community labels: the
+// recency-descending membership CSR, FP8 (or f32) centroid tables with their
+// community sizes, the modularity weights of the prefill edges and the
+// per-token community table.  Restates the reference's state build after
+// Leiden (graph/partition.py:382-535, called from build_partitioned_layer
+// 538-618).
+//
+// Every integer output is exact, and the centroid means add each community's
+// keys in ascending position order (one wave per community row, lane = two
+// dims), so they are reproducible bit for bit.  The modularity weights add
+// edge weights with float atomics, like the reference's scatter_add_; their
+// summation order is not fixed.
+//
+// Launch sequence of ckv_build_layer_state (one stream):
+//   chunk_hist_kernel     per (graph, 2048-position chunk): community histogram
+//   csr_scan_kernel       per graph: CSR offsets and each chunk's first slot per community
+//   csr_scatter_kernel    per (graph, chunk): member positions, newest first
+//   centroid_kernel       per (retrieval head, 4 communities): means -> clamp -> E4M3 / f32
+//   token_table_kernel    labels -> token_communities (-1 past the prompt)
+//   weight_zero_kernel + edge_weight_kernel   modularity weights (when edges are given)
+#include <hip/hip_runtime.h>
+
+#include <stdint.h>
+
+#include "ckv_device.h"
+#include "ckv_error.h"
+
+namespace ckv {
+namespace {
+
+constexpr int STATE_CHUNK = 2048;        // positions per histogram / scatter chunk
+constexpr int COUNT_THREADS = 1024;
+constexpr int SCAN_THREADS = 1024;
+constexpr int HIST_THREADS = 256;
+constexpr int CENTROID_WAVES = 4;        // community rows per centroid workgroup
+constexpr int EDGE_THREADS = 256;
+
+inline int state_chunks(int seq_len, int num_sink) {
+  const int n = seq_len - num_sink;
+  return n <= 0 ? 0 : (n + STATE_CHUNK - 1) / STATE_CHUNK;
+}
+
+// community_counts[g] = 1 + the largest label of a non-sink position, 0 when
+// there is none, -1 when a non-sink label is negative.
+__global__ __launch_bounds__(COUNT_THREADS) void label_count_kernel(const int32_t* __restrict__ labels, int seq_len,
+                                                                    int num_sink, int32_t* __restrict__ counts) {
+  const int g = blockIdx.x;
+  const int32_t* row = labels + (int64_t)g * seq_len;
+  int mx = -1, mn = 0;
+  for (int p = num_sink + threadIdx.x; p < seq_len; p += COUNT_THREADS) {
+    const int v = row[p];
+    mx = max(mx, v);
+    mn = min(mn, v);
+  }
+  __shared__ int s_max[COUNT_THREADS / 64], s_min[COUNT_THREADS / 64];
+  mx = wave_max_i32(mx);
+  mn = -wave_max_i32(-mn);
+  if ((threadIdx.x & 63) == 0) {
+    s_max[threadIdx.x >> 6] = mx;
+    s_min[threadIdx.x >> 6] = mn;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 0; w < COUNT_THREADS / 64; ++w) {
+      mx = max(mx, s_max[w]);
+      mn = min(mn, s_min[w]);
+    }
+    counts[g] = mn < 0 ? -1 : mx + 1;
+  }
+}
+
+// hist[g][chunk][c]: members of community c among the chunk's positions.
+__global__ __launch_bounds__(HIST_THREADS) void chunk_hist_kernel(const int32_t* __restrict__ labels, int seq_len,
+                                                                  int num_sink, int maxc, int chunks,
+                                                                  int32_t* __restrict__ hist) {
+  extern __shared__ int h_s[];
+  const int chunk = blockIdx.x, g = blockIdx.y;
+  for (int c = threadIdx.x; c < maxc; c += HIST_THREADS) h_s[c] = 0;
+  __syncthreads();
+  const int32_t* row = labels + (int64_t)g * seq_len;
+  const int p0 = num_sink + chunk * STATE_CHUNK;
+  const int p1 = min(p0 + STATE_CHUNK, seq_len);
+  for (int p = p0 + threadIdx.x; p < p1; p += HIST_THREADS) {
+    const int c = row[p];
+    if (c >= 0 && c < maxc) atomicAdd(h_s + c, 1);
+  }
+  __syncthreads();
+  int32_t* out = hist + ((int64_t)g * chunks + chunk) * maxc;
+  for (int c = threadIdx.x; c < maxc; c += HIST_THREADS) out[c] = h_s[c];
+}
+
+// Per graph: offsets[c] = members of communities below c; then every chunk's
+// histogram entry becomes the CSR slot of that chunk's newest member of c
+// (later chunks first: the CSR is recency descending).
+__global__ __launch_bounds__(SCAN_THREADS) void csr_scan_kernel(int maxc, int chunks, int32_t* __restrict__ hist,
+                                                                int32_t* __restrict__ offsets) {
+  constexpr int PER = CKV_MAX_COMMUNITIES / SCAN_THREADS;
+  const int g = blockIdx.x;
+  const int tid = threadIdx.x;
+  int32_t* h = hist + (int64_t)g * chunks * maxc;
+  int tot[PER];
+  int local = 0;
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const int c = tid * PER + k;
+    int t = 0;
+    if (c < maxc) {
+      for (int i = 0; i < chunks; ++i) t += h[(int64_t)i * maxc + c];
+    }
+    tot[k] = t;
+    local += t;
+  }
+  // exclusive scan of the thread sums (thread order = community order)
+  __shared__ int s_wave[SCAN_THREADS / 64];
+  const int inc = wave_inclusive_scan(local);
+  if ((tid & 63) == 63) s_wave[tid >> 6] = inc;
+  __syncthreads();
+  int base = inc - local;
+  for (int w = 0; w < (tid >> 6); ++w) base += s_wave[w];
+  int32_t* off = offsets + (int64_t)g * (maxc + 1);
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const int c = tid * PER + k;
+    if (c < maxc) {
+      off[c] = base;
+      int run = base;
+      for (int i = chunks - 1; i >= 0; --i) {
+        const int64_t j = (int64_t)i * maxc + c;
+        const int n = h[j];
+        h[j] = run;
+        run += n;
+      }
+    } else if (c == maxc) {
+      off[c] = base;
+    }
+    base += tot[k];
+  }
+}
+
+// One wave per (graph, chunk): walks the chunk's positions from the newest
+// down, 64 at a time (lane l takes the l-th newest); lanes with equal labels
+// are ranked by lane (newer first) one distinct label per round, and an LDS
+// cursor per community advances by each round's members.
+__global__ __launch_bounds__(64) void csr_scatter_kernel(const int32_t* __restrict__ labels, int seq_len, int num_sink,
+                                                         int maxc, int chunks, const int32_t* __restrict__ hist,
+                                                         int32_t* __restrict__ member_positions) {
+  extern __shared__ int cur_s[];
+  const int chunk = blockIdx.x, g = blockIdx.y;
+  const int lane = threadIdx.x;
+  const int32_t* h = hist + ((int64_t)g * chunks + chunk) * maxc;
+  for (int c = lane; c < maxc; c += 64) cur_s[c] = h[c];
+  wave_sync();
+  const int32_t* row = labels + (int64_t)g * seq_len;
+  int32_t* out = member_positions + (int64_t)g * (seq_len - num_sink);
+  const int p0 = num_sink + chunk * STATE_CHUNK;
+  const int p1 = min(p0 + STATE_CHUNK, seq_len);
+  const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  for (int top = p1 - 1; top >= p0; top -= 64) {
+    const int p = top - lane;
+    const bool ok = p >= p0;
+    const int c = ok ? row[p] : -1;
+    const bool valid = ok && c >= 0 && c < maxc;
+    uint64_t todo = __ballot(valid);
+    while (todo) {
+      const int leader = __builtin_ctzll(todo);
+      const int lc = __builtin_amdgcn_readlane(c, leader);
+      const uint64_t m = __ballot(valid && c == lc);
+      const int base = cur_s[lc];
+      if (valid && c == lc) out[base + __popcll(m & below)] = p;
+      wave_sync();
+      if (lane == leader) cur_s[lc] = base + __popcll(m);
+      wave_sync();
+      todo &= ~m;
+    }
+  }
+}
+
+// One wave per (retrieval head, community row): mean of the community's keys
+// (ascending positions, f32, lane = dims 2l and 2l+1), clamped to +-448, then
+// E4M3 or f32.  Rows at or past maxc hold zeros.
+template <int KT, int CT>
+__global__ __launch_bounds__(64 * CENTROID_WAVES) void centroid_kernel(
+    const void* __restrict__ keys, int64_t head_stride, int64_t token_stride, const int32_t* __restrict__ to_graph,
+    const int32_t* __restrict__ to_kv, const int32_t* __restrict__ offsets, const int32_t* __restrict__ positions,
+    int seq_len, int num_sink, int maxc, int capacity, void* __restrict__ centroids, int32_t* __restrict__ sizes) {
+  const int r = blockIdx.y;
+  const int c = blockIdx.x * CENTROID_WAVES + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (c >= capacity) return;
+  const int g = to_graph[r];
+  const int kvh = to_kv[r];
+  int lo = 0, hi = 0;
+  if (c < maxc) {
+    lo = offsets[(int64_t)g * (maxc + 1) + c];
+    hi = offsets[(int64_t)g * (maxc + 1) + c + 1];
+  }
+  const int32_t* mem = positions + (int64_t)g * (seq_len - num_sink);
+  const int64_t kb = (int64_t)kvh * head_stride + 2 * lane;
+  float s0 = 0.0f, s1 = 0.0f;
+  // members hi-1, hi-2, ... are the oldest first (the CSR is newest first)
+  for (int b = hi - 1; b >= lo; b -= 64) {
+    const int n = min(64, b - lo + 1);
+    const int mine = mem[max(b - lane, lo)];
+    for (int j0 = 0; j0 < n; j0 += 8) {
+      float x0[8], x1[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int p = __builtin_amdgcn_readlane(mine, min(j0 + u, n - 1));
+        if constexpr (KT == CKV_BF16) {
+          const uint32_t w = (uint32_t)gload_i32(reinterpret_cast<const int32_t*>(
+              reinterpret_cast<const uint16_t*>(keys) + kb + (int64_t)p * token_stride));
+          x0[u] = ckv_u2f(w << 16);
+          x1[u] = ckv_u2f(w & 0xffff0000u);
+        } else {
+          const float* kp = reinterpret_cast<const float*>(keys) + kb + (int64_t)p * token_stride;
+          x0[u] = gload_f32(kp);
+          x1[u] = gload_f32(kp + 1);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        if (j0 + u < n) {
+          s0 = s0 + x0[u];
+          s1 = s1 + x1[u];
+        }
+      }
+    }
+  }
+  const int size = hi - lo;
+  if (c < maxc) {
+    const float den = (float)max(size, 1);
+    s0 = s0 / den;
+    s1 = s1 / den;
+  }
+  s0 = fminf(fmaxf(s0, -448.0f), 448.0f);
+  s1 = fminf(fmaxf(s1, -448.0f), 448.0f);
+  const int64_t row = (int64_t)r * capacity + c;
+  if constexpr (CT == CKV_E4M3) {
+    const uint16_t pair = (uint16_t)(ckv_f32_to_e4m3(s0) | ((uint16_t)ckv_f32_to_e4m3(s1) << 8));
+    reinterpret_cast<uint16_t*>(centroids)[row * (D / 2) + lane] = pair;
+  } else {
+    float* dst = reinterpret_cast<float*>(centroids) + row * D + 2 * lane;
+    dst[0] = s0;
+    dst[1] = s1;
+  }
+  if (lane == 0) sizes[row] = size;
+}
+
+__global__ void token_table_kernel(const int32_t* __restrict__ labels, int seq_len, int token_capacity, int graphs,
+                                   int32_t* __restrict__ tokens) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t total = (int64_t)graphs * token_capacity;
+  if (i >= total) return;
+  const int g = (int)(i / token_capacity);
+  const int t = (int)(i % token_capacity);
+  tokens[i] = t < seq_len ? labels[(int64_t)g * seq_len + t] : -1;
+}
+
+__global__ void weight_zero_kernel(float* __restrict__ weight, int64_t n, float* __restrict__ total, int graphs) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) weight[i] = 0.0f;
+  if (i < graphs) total[i] = 0.0f;
+}
+
+// Community degree weights and 2m: each edge (graph * seq_len + position
+// endpoints) adds its weight to both endpoint communities and twice to its
+// graph's total (one atomic per workgroup and graph run).
+__global__ __launch_bounds__(EDGE_THREADS) void edge_weight_kernel(
+    const int32_t* __restrict__ labels, int seq_len, int graphs, int capacity, const int32_t* __restrict__ src,
+    const int32_t* __restrict__ dst, const float* __restrict__ w, int64_t edges, float* __restrict__ weight,
+    float* __restrict__ total) {
+  const int64_t e = (int64_t)blockIdx.x * EDGE_THREADS + threadIdx.x;
+  float mine = 0.0f;
+  int g = -1;
+  if (e < edges) {
+    const int s = src[e], d = dst[e];
+    g = s / seq_len;
+    const float x = w[e];
+    if (g >= 0 && g < graphs && d / seq_len == g) {
+      const int sc = labels[(int64_t)g * seq_len + s % seq_len];
+      const int dc = labels[(int64_t)g * seq_len + d % seq_len];
+      if (sc >= 0 && sc < capacity) atomicAdd(weight + (int64_t)g * capacity + sc, x);
+      if (dc >= 0 && dc < capacity) atomicAdd(weight + (int64_t)g * capacity + dc, x);
+      mine = 2.0f * x;
+    } else {
+      g = -1;
+    }
+  }
+  // edges are grouped by graph (src-major): sum this workgroup's share per graph
+  __shared__ float s_sum[EDGE_THREADS];
+  __shared__ int s_g[EDGE_THREADS];
+  s_sum[threadIdx.x] = mine;
+  s_g[threadIdx.x] = g;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int cg = -1;
+    float acc = 0.0f;
+    for (int i = 0; i < EDGE_THREADS; ++i) {
+      if (s_g[i] != cg) {
+        if (cg >= 0) atomicAdd(total + cg, acc);
+        cg = s_g[i];
+        acc = 0.0f;
+      }
+      acc = acc + s_sum[i];
+    }
+    if (cg >= 0) atomicAdd(total + cg, acc);
+  }
+}
+
+int launch_check() {
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? 0 : ckv_internal::set_error(CKV_E_LAUNCH, hipGetErrorString(e));
+}
+
+}  // namespace
+}  // namespace ckv
+
+using namespace ckv;
+
+extern "C" size_t ckv_state_workspace_bytes(int32_t graphs, int32_t seq_len, int32_t num_sink,
+                                            int32_t max_communities) {
+  if (graphs <= 0 || seq_len <= 0 || max_communities <= 0) return 0;
+  return (size_t)graphs * state_chunks(seq_len, num_sink) * max_communities * sizeof(int32_t);
+}
+
+extern "C" int ckv_label_counts(const int32_t* labels, int32_t graphs, int32_t seq_len, int32_t num_sink,
+                                int32_t* community_counts, void* stream) {
+  if (!labels || !community_counts) return ckv_internal::set_error(CKV_E_INVALID, "null label-count argument");
+  if (graphs <= 0 || seq_len <= 0 || num_sink < 0)
+    return ckv_internal::set_error(CKV_E_INVALID, "graphs and seq_len must be positive, num_sink nonnegative");
+  hipLaunchKernelGGL(label_count_kernel, dim3(graphs), dim3(COUNT_THREADS), 0, (hipStream_t)stream, labels, seq_len,
+                     num_sink, community_counts);
+  return launch_check();
+}
+
+extern "C" int ckv_build_layer_state(const ckv_state_build_args* a, void* stream) {
+  if (!a) return ckv_internal::set_error(CKV_E_INVALID, "null state-build argument");
+  if (!a->labels || !a->keys || !a->retrieval_to_graph || !a->retrieval_to_kv || !a->member_offsets ||
+      !a->member_positions || !a->centroids || !a->community_sizes || !a->token_communities || !a->workspace)
+    return ckv_internal::set_error(CKV_E_INVALID, "null state-build pointer");
+  if (a->graphs <= 0 || a->seq_len <= 0 || a->num_sink < 0 || a->num_sink >= a->seq_len ||
+      a->retrieval_heads <= 0 || a->kv_heads <= 0)
+    return ckv_internal::set_error(CKV_E_INVALID, "bad graph, head or sequence sizes (num_sink < seq_len)");
+  if (a->max_communities <= 0 || a->max_communities > CKV_MAX_COMMUNITIES)
+    return ckv_internal::set_error(CKV_E_LIMIT, "max_communities must be in [1, 8192]");
+  if (a->community_capacity < a->max_communities)
+    return ckv_internal::set_error(CKV_E_INVALID, "community_capacity must cover max_communities");
+  if (a->token_capacity < a->seq_len) return ckv_internal::set_error(CKV_E_INVALID, "token_capacity < seq_len");
+  if (a->key_dtype != CKV_BF16 && a->key_dtype != CKV_F32)
+    return ckv_internal::set_error(CKV_E_INVALID, "key dtype must be bf16 or f32");
+  if (a->centroid_dtype != CKV_E4M3 && a->centroid_dtype != CKV_F32)
+    return ckv_internal::set_error(CKV_E_INVALID, "centroid dtype must be e4m3 or f32");
+  if (a->head_stride <= 0 || a->token_stride < CKV_HEAD_DIM)
+    return ckv_internal::set_error(CKV_E_INVALID, "bad key strides");
+  if (a->edges < 0 || (a->edges > 0 && (!a->edge_src || !a->edge_dst || !a->edge_weight)))
+    return ckv_internal::set_error(CKV_E_INVALID, "edges need src, dst and weight");
+  if (a->edges > 0 && (!a->community_weight || !a->total_weight))
+    return ckv_internal::set_error(CKV_E_INVALID, "edges need community_weight and total_weight outputs");
+  const hipStream_t s = (hipStream_t)stream;
+  const int maxc = a->max_communities;
+  const int chunks = state_chunks(a->seq_len, a->num_sink);
+  const size_t lds = (size_t)maxc * sizeof(int);
+  hipLaunchKernelGGL(chunk_hist_kernel, dim3(chunks, a->graphs), dim3(HIST_THREADS), lds, s, a->labels, a->seq_len,
+                     a->num_sink, maxc, chunks, a->workspace);
+  hipLaunchKernelGGL(csr_scan_kernel, dim3(a->graphs), dim3(SCAN_THREADS), 0, s, maxc, chunks, a->workspace,
+                     a->member_offsets);
+  hipLaunchKernelGGL(csr_scatter_kernel, dim3(chunks, a->graphs), dim3(64), lds, s, a->labels, a->seq_len,
+                     a->num_sink, maxc, chunks, (const int32_t*)a->workspace, a->member_positions);
+  const dim3 cgrid((a->community_capacity + CENTROID_WAVES - 1) / CENTROID_WAVES, a->retrieval_heads);
+  auto cent = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, cgrid, dim3(64 * CENTROID_WAVES), 0, s, a->keys, a->head_stride, a->token_stride,
+                       a->retrieval_to_graph, a->retrieval_to_kv, (const int32_t*)a->member_offsets,
+                       (const int32_t*)a->member_positions, a->seq_len, a->num_sink, maxc, a->community_capacity,
+                       a->centroids, a->community_sizes);
+  };
+  if (a->key_dtype == CKV_BF16) {
+    if (a->centroid_dtype == CKV_E4M3) cent(centroid_kernel<CKV_BF16, CKV_E4M3>); else cent(centroid_kernel<CKV_BF16, CKV_F32>);
+  } else {
+    if (a->centroid_dtype == CKV_E4M3) cent(centroid_kernel<CKV_F32, CKV_E4M3>); else cent(centroid_kernel<CKV_F32, CKV_F32>);
+  }
+  const int64_t ntok = (int64_t)a->graphs * a->token_capacity;
+  hipLaunchKernelGGL(token_table_kernel, dim3((unsigned)((ntok + 255) / 256)), dim3(256), 0, s, a->labels,
+                     a->seq_len, a->token_capacity, a->graphs, a->token_communities);
+  if (a->community_weight && a->total_weight) {
+    const int64_t nw = (int64_t)a->graphs * a->community_capacity;
+    const int64_t nz = nw > a->graphs ? nw : a->graphs;
+    hipLaunchKernelGGL(weight_zero_kernel, dim3((unsigned)((nz + 255) / 256)), dim3(256), 0, s, a->community_weight,
+                       nw, a->total_weight, a->graphs);
+    if (a->edges > 0) {
+      hipLaunchKernelGGL(edge_weight_kernel, dim3((unsigned)((a->edges + EDGE_THREADS - 1) / EDGE_THREADS)),
+                         dim3(EDGE_THREADS), 0, s, a->labels, a->seq_len, a->graphs, a->community_capacity,
+                         a->edge_src, a->edge_dst, a->edge_weight, a->edges, a->community_weight, a->total_weight);
+    }
+  }
+  return launch_check();
+}

@@ -189,6 +189,20 @@ def build_layer_from_labels(*, layer_idx: int, community_ids: torch.Tensor, keys
     to_graph, to_kv = aggregation_mappings(aggregation, query_heads=query_heads, kv_heads=kv_heads,
                                            device=keys.device)
     ids = community_ids.to(device=keys.device, dtype=torch.int32)
+    if keys.device.type == "cuda":
+        # HIP kernels (graph/kernels/state_build.py); the torch code below
+        # serves CPU tensors only
+        from community_kv_amd.graph.kernels.state_build import build_layer_state
+
+        st = build_layer_state(ids, keys, retrieval_to_graph=to_graph, retrieval_to_kv=to_kv, num_sink=num_sink,
+                               max_decode_tokens=max_decode_tokens, fp8=fp8, edges=edges)
+        return PartitionedLayer(layer_idx=layer_idx, prefill_seq_len=seq_len, aggregation=aggregation,
+                                query_heads=query_heads, kv_heads=kv_heads, retrieval_to_graph=to_graph,
+                                retrieval_to_kv=to_kv, member_offsets=st.member_offsets,
+                                member_positions=st.member_positions, community_counts=st.community_counts,
+                                centroids=st.centroids, community_sizes=st.community_sizes,
+                                community_weight=st.community_weight, total_weight=st.total_weight,
+                                token_communities=st.token_communities)
     counts = (ids[:, num_sink:].amax(dim=1) + 1).to(torch.int32)
     centroids, sizes = compute_centroids(ids, counts, keys, retrieval_to_graph=to_graph, retrieval_to_kv=to_kv,
                                          num_sink=num_sink, max_decode_tokens=max_decode_tokens, fp8=fp8)

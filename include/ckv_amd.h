@@ -27,6 +27,9 @@
  *   ckv_prefill_attention_topk
  *                           prefill_attention_topk()          attention/flash_attention.py:23-51
  *                           (patched FA3 op, third_party/flash_attention/community-kv.patch:31-120)
+ *   ckv_label_counts,       the state build of build_partitioned_layer() after Leiden
+ *   ckv_build_layer_state   (graph/partition.py:538-618): compute_centroids 382-454,
+ *                           build_member_csr 457-492, init_modularity_state 495-535
  */
 #ifndef CKV_AMD_H
 #define CKV_AMD_H
@@ -204,6 +207,67 @@ typedef struct ckv_prefill_args {
 } ckv_prefill_args;
 
 int ckv_prefill_attention_topk(const ckv_prefill_args* args, void* stream);
+
+/* Prefill graph state from dense community labels (reference: the state build
+ * of build_partitioned_layer, graph/partition.py:538-618).
+ *
+ * ckv_label_counts writes community_counts[g] = 1 + the largest label of graph
+ * g's non-sink positions (0 when there are none, -1 when one is negative);
+ * the caller reads them back to size the outputs (max_communities = their
+ * maximum), as the reference does with .item().
+ *
+ * ckv_build_layer_state then fills, for labels in [0, max_communities):
+ *   member_offsets    [graphs][max_communities + 1]   CSR over non-sink positions
+ *   member_positions  [graphs][seq_len - num_sink]    newest first within a community
+ *   centroids         [retrieval_heads][community_capacity][128]: mean of the
+ *                     community's non-sink keys of KV head retrieval_to_kv[r]
+ *                     (ascending-position f32 sum / size), clamped to +-448,
+ *                     E4M3 or f32; rows past max_communities are zero
+ *   community_sizes   [retrieval_heads][community_capacity]
+ *   token_communities [graphs][token_capacity]: the labels, -1 past seq_len
+ *   community_weight  [graphs][community_capacity], total_weight [graphs]
+ *                     (optional, both or neither): every edge adds its weight
+ *                     to both endpoint communities and twice to the total;
+ *                     float atomics, so the last bits depend on timing, as
+ *                     with the reference's scatter_add_
+ * Edge endpoints are graph * seq_len + position.  `workspace` holds
+ * ckv_state_workspace_bytes() bytes.  Integer outputs and centroids are
+ * deterministic. */
+typedef struct ckv_state_build_args {
+  const int32_t* labels;              /* [graphs][seq_len] */
+  const void* keys;                   /* keys[h*head_stride + t*token_stride + d], key_dtype */
+  int64_t head_stride;                /* elements */
+  int64_t token_stride;               /* elements */
+  const int32_t* retrieval_to_graph;  /* [retrieval_heads] */
+  const int32_t* retrieval_to_kv;     /* [retrieval_heads] */
+  const int32_t* edge_src;            /* [edges] */
+  const int32_t* edge_dst;            /* [edges] */
+  const float* edge_weight;           /* [edges] */
+  int64_t edges;
+  int32_t graphs;
+  int32_t seq_len;
+  int32_t num_sink;
+  int32_t retrieval_heads;
+  int32_t kv_heads;
+  int32_t key_dtype;                  /* CKV_BF16 or CKV_F32 */
+  int32_t centroid_dtype;             /* CKV_E4M3 or CKV_F32 */
+  int32_t max_communities;            /* <= CKV_MAX_COMMUNITIES */
+  int32_t community_capacity;         /* centroid rows (>= max_communities) */
+  int32_t token_capacity;             /* >= seq_len */
+  int32_t* member_offsets;
+  int32_t* member_positions;
+  void* centroids;
+  int32_t* community_sizes;
+  float* community_weight;            /* may be null (then total_weight too) */
+  float* total_weight;
+  int32_t* token_communities;
+  int32_t* workspace;
+} ckv_state_build_args;
+
+size_t ckv_state_workspace_bytes(int32_t graphs, int32_t seq_len, int32_t num_sink, int32_t max_communities);
+int ckv_label_counts(const int32_t* labels, int32_t graphs, int32_t seq_len, int32_t num_sink,
+                     int32_t* community_counts, void* stream);
+int ckv_build_layer_state(const ckv_state_build_args* args, void* stream);
 
 /* Score every retrieval head's centroids against its query group, select the
  * communities that fill the budget (reference order: strictly-above-threshold
