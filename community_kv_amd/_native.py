@@ -193,7 +193,7 @@ def lib() -> ctypes.CDLL:
     if hasattr(handle, "ckv_prefill_attention_topk"):
         handle.ckv_prefill_attention_topk.argtypes = [ctypes.POINTER(PrefillArgs), _p]
         handle.ckv_prefill_attention_topk.restype = ctypes.c_int
-    handle.ckv_state_workspace_bytes.argtypes = [_i32, _i32, _i32, _i32]
+    handle.ckv_state_workspace_bytes.argtypes = [_i32, _i32, _i32, _i32, _i32]
     handle.ckv_state_workspace_bytes.restype = ctypes.c_size_t
     handle.ckv_label_counts.argtypes = [_p, _i32, _i32, _i32, _p, _p]
     handle.ckv_label_counts.restype = ctypes.c_int

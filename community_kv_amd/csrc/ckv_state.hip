@@ -5,17 +5,22 @@
 // Leiden (graph/partition.py:382-535, called from build_partitioned_layer
 // 538-618).
 //
-// Every integer output is exact, and the centroid means add each community's
-// keys in ascending position order (one wave per community row, lane = two
-// dims), so they are reproducible bit for bit.  The modularity weights add
-// edge weights with float atomics, like the reference's scatter_add_; their
-// summation order is not fixed.
+// Every integer output is exact, and the centroid sums follow one fixed order
+// (a community's members in ascending position order, in blocks of 64: each
+// block summed in order by one wave, lane = two dims, then the block sums
+// added in order), so they are reproducible bit for bit; blocks spread a large
+// community over many waves.  The modularity weights add edge weights with
+// float atomics, like the reference's scatter_add_; their summation order is
+// not fixed.
 //
 // Launch sequence of ckv_build_layer_state (one stream):
-//   chunk_hist_kernel     per (graph, 2048-position chunk): community histogram
-//   csr_scan_kernel       per graph: CSR offsets and each chunk's first slot per community
+//   chunk_hist_kernel     per (graph, position chunk): community histogram
+//   csr_scan_kernel       per graph: CSR offsets, each chunk's first slot per
+//                         community, and the table of 64-member blocks
 //   csr_scatter_kernel    per (graph, chunk): member positions, newest first
-//   centroid_kernel       per (retrieval head, 4 communities): means -> clamp -> E4M3 / f32
+//   block_sum_kernel      per (retrieval head, block): in-order key sum of 64 members
+//   centroid_kernel       per (retrieval head, community): block sums in order,
+//                         mean -> clamp -> E4M3 / f32
 //   token_table_kernel    labels -> token_communities (-1 past the prompt)
 //   weight_zero_kernel + edge_weight_kernel   modularity weights (when edges are given)
 #include <hip/hip_runtime.h>
@@ -28,16 +33,60 @@
 namespace ckv {
 namespace {
 
-constexpr int STATE_CHUNK = 2048;        // positions per histogram / scatter chunk
+constexpr int MAX_CHUNKS = 64;           // position chunks per graph (histogram / scatter)
+constexpr int MIN_CHUNK = 512;
+constexpr int SUM_BLOCK = 64;            // members per centroid partial sum
 constexpr int COUNT_THREADS = 1024;
 constexpr int SCAN_THREADS = 1024;
 constexpr int HIST_THREADS = 256;
 constexpr int CENTROID_WAVES = 4;        // community rows per centroid workgroup
 constexpr int EDGE_THREADS = 256;
 
+// Positions per chunk: at least MIN_CHUNK, at most MAX_CHUNKS chunks, a multiple of 64.
+inline int state_chunk(int seq_len, int num_sink) {
+  const int n = seq_len - num_sink;
+  int c = (n + MAX_CHUNKS - 1) / MAX_CHUNKS;
+  c = (c + 63) / 64 * 64;
+  return c < MIN_CHUNK ? MIN_CHUNK : c;
+}
 inline int state_chunks(int seq_len, int num_sink) {
   const int n = seq_len - num_sink;
-  return n <= 0 ? 0 : (n + STATE_CHUNK - 1) / STATE_CHUNK;
+  return n <= 0 ? 0 : (n + state_chunk(seq_len, num_sink) - 1) / state_chunk(seq_len, num_sink);
+}
+// Upper bound of the 64-member blocks of one graph.
+inline int64_t state_max_blocks(int seq_len, int num_sink, int maxc) {
+  return (int64_t)(seq_len - num_sink + SUM_BLOCK - 1) / SUM_BLOCK + maxc;
+}
+
+// Workspace carve-up (int32 units): histograms, block starts, block communities, f32 partial sums.
+struct StateWorkspace {
+  int32_t* hist;       // [graphs][chunks][maxc]
+  int32_t* blk_first;  // [graphs][maxc + 1]
+  int32_t* blk_comm;   // [graphs][max_blocks]
+  float* partial;      // [retrieval_heads][max_blocks][128]
+};
+
+inline size_t state_ws_words(int graphs, int heads, int seq_len, int num_sink, int maxc, StateWorkspace* w,
+                             int32_t* base) {
+  const int64_t chunks = state_chunks(seq_len, num_sink);
+  const int64_t mb = state_max_blocks(seq_len, num_sink, maxc);
+  size_t off = 0;
+  auto take = [&](int64_t words) {
+    const size_t at = off;
+    off += (size_t)((words + 63) / 64 * 64);  // 256-byte aligned pieces
+    return at;
+  };
+  const size_t h = take((int64_t)graphs * chunks * maxc);
+  const size_t bf = take((int64_t)graphs * (maxc + 1));
+  const size_t bc = take((int64_t)graphs * mb);
+  const size_t pt = take((int64_t)heads * mb * D);
+  if (w && base) {
+    w->hist = base + h;
+    w->blk_first = base + bf;
+    w->blk_comm = base + bc;
+    w->partial = reinterpret_cast<float*>(base + pt);
+  }
+  return off;
 }
 
 // community_counts[g] = 1 + the largest label of a non-sink position, 0 when
@@ -71,15 +120,15 @@ __global__ __launch_bounds__(COUNT_THREADS) void label_count_kernel(const int32_
 
 // hist[g][chunk][c]: members of community c among the chunk's positions.
 __global__ __launch_bounds__(HIST_THREADS) void chunk_hist_kernel(const int32_t* __restrict__ labels, int seq_len,
-                                                                  int num_sink, int maxc, int chunks,
+                                                                  int num_sink, int maxc, int chunk_len, int chunks,
                                                                   int32_t* __restrict__ hist) {
   extern __shared__ int h_s[];
   const int chunk = blockIdx.x, g = blockIdx.y;
   for (int c = threadIdx.x; c < maxc; c += HIST_THREADS) h_s[c] = 0;
   __syncthreads();
   const int32_t* row = labels + (int64_t)g * seq_len;
-  const int p0 = num_sink + chunk * STATE_CHUNK;
-  const int p1 = min(p0 + STATE_CHUNK, seq_len);
+  const int p0 = num_sink + chunk * chunk_len;
+  const int p1 = min(p0 + chunk_len, seq_len);
   for (int p = p0 + threadIdx.x; p < p1; p += HIST_THREADS) {
     const int c = row[p];
     if (c >= 0 && c < maxc) atomicAdd(h_s + c, 1);
@@ -92,8 +141,11 @@ __global__ __launch_bounds__(HIST_THREADS) void chunk_hist_kernel(const int32_t*
 // Per graph: offsets[c] = members of communities below c; then every chunk's
 // histogram entry becomes the CSR slot of that chunk's newest member of c
 // (later chunks first: the CSR is recency descending).
-__global__ __launch_bounds__(SCAN_THREADS) void csr_scan_kernel(int maxc, int chunks, int32_t* __restrict__ hist,
-                                                                int32_t* __restrict__ offsets) {
+__global__ __launch_bounds__(SCAN_THREADS) void csr_scan_kernel(int maxc, int chunks, int64_t max_blocks,
+                                                                int32_t* __restrict__ hist,
+                                                                int32_t* __restrict__ offsets,
+                                                                int32_t* __restrict__ blk_first,
+                                                                int32_t* __restrict__ blk_comm) {
   constexpr int PER = CKV_MAX_COMMUNITIES / SCAN_THREADS;
   const int g = blockIdx.x;
   const int tid = threadIdx.x;
@@ -110,13 +162,38 @@ __global__ __launch_bounds__(SCAN_THREADS) void csr_scan_kernel(int maxc, int ch
     tot[k] = t;
     local += t;
   }
-  // exclusive scan of the thread sums (thread order = community order)
-  __shared__ int s_wave[SCAN_THREADS / 64];
+  // exclusive scans of the thread sums (thread order = community order): members and 64-member blocks
+  int lblk = 0;
+#pragma unroll
+  for (int k = 0; k < PER; ++k) lblk += (tot[k] + SUM_BLOCK - 1) / SUM_BLOCK;
+  __shared__ int s_wave[SCAN_THREADS / 64], s_wblk[SCAN_THREADS / 64];
   const int inc = wave_inclusive_scan(local);
-  if ((tid & 63) == 63) s_wave[tid >> 6] = inc;
+  const int incb = wave_inclusive_scan(lblk);
+  if ((tid & 63) == 63) {
+    s_wave[tid >> 6] = inc;
+    s_wblk[tid >> 6] = incb;
+  }
   __syncthreads();
   int base = inc - local;
-  for (int w = 0; w < (tid >> 6); ++w) base += s_wave[w];
+  int bbase = incb - lblk;
+  for (int w = 0; w < (tid >> 6); ++w) {
+    base += s_wave[w];
+    bbase += s_wblk[w];
+  }
+  int32_t* bf = blk_first + (int64_t)g * (maxc + 1);
+  int32_t* bc = blk_comm + (int64_t)g * max_blocks;
+  {
+    int b = bbase;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      const int c = tid * PER + k;
+      if (c < maxc) bf[c] = b;
+      const int nb = (tot[k] + SUM_BLOCK - 1) / SUM_BLOCK;
+      for (int j = 0; j < nb; ++j) bc[b + j] = c;
+      b += nb;
+      if (c == maxc - 1) bf[maxc] = b;
+    }
+  }
   int32_t* off = offsets + (int64_t)g * (maxc + 1);
 #pragma unroll
   for (int k = 0; k < PER; ++k) {
@@ -130,10 +207,9 @@ __global__ __launch_bounds__(SCAN_THREADS) void csr_scan_kernel(int maxc, int ch
         h[j] = run;
         run += n;
       }
-    } else if (c == maxc) {
-      off[c] = base;
     }
     base += tot[k];
+    if (c == maxc - 1) off[maxc] = base;
   }
 }
 
@@ -142,7 +218,8 @@ __global__ __launch_bounds__(SCAN_THREADS) void csr_scan_kernel(int maxc, int ch
 // are ranked by lane (newer first) one distinct label per round, and an LDS
 // cursor per community advances by each round's members.
 __global__ __launch_bounds__(64) void csr_scatter_kernel(const int32_t* __restrict__ labels, int seq_len, int num_sink,
-                                                         int maxc, int chunks, const int32_t* __restrict__ hist,
+                                                         int maxc, int chunk_len, int chunks,
+                                                         const int32_t* __restrict__ hist,
                                                          int32_t* __restrict__ member_positions) {
   extern __shared__ int cur_s[];
   const int chunk = blockIdx.x, g = blockIdx.y;
@@ -152,8 +229,8 @@ __global__ __launch_bounds__(64) void csr_scatter_kernel(const int32_t* __restri
   wave_sync();
   const int32_t* row = labels + (int64_t)g * seq_len;
   int32_t* out = member_positions + (int64_t)g * (seq_len - num_sink);
-  const int p0 = num_sink + chunk * STATE_CHUNK;
-  const int p1 = min(p0 + STATE_CHUNK, seq_len);
+  const int p0 = num_sink + chunk * chunk_len;
+  const int p1 = min(p0 + chunk_len, seq_len);
   const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   for (int top = p1 - 1; top >= p0; top -= 64) {
     const int p = top - lane;
@@ -175,58 +252,96 @@ __global__ __launch_bounds__(64) void csr_scatter_kernel(const int32_t* __restri
   }
 }
 
-// One wave per (retrieval head, community row): mean of the community's keys
-// (ascending positions, f32, lane = dims 2l and 2l+1), clamped to +-448, then
-// E4M3 or f32.  Rows at or past maxc hold zeros.
-template <int KT, int CT>
-__global__ __launch_bounds__(64 * CENTROID_WAVES) void centroid_kernel(
+// One wave per (retrieval head, 64-member block): members 64k .. 64k+63 of
+// community c in ascending position order (the CSR lists them newest first),
+// summed in order in f32, lane = dims 2l and 2l+1.  All 64 rows are loaded
+// before the sum, so a block costs one gather round.
+template <int KT>
+__global__ __launch_bounds__(64 * CENTROID_WAVES) void block_sum_kernel(
     const void* __restrict__ keys, int64_t head_stride, int64_t token_stride, const int32_t* __restrict__ to_graph,
     const int32_t* __restrict__ to_kv, const int32_t* __restrict__ offsets, const int32_t* __restrict__ positions,
-    int seq_len, int num_sink, int maxc, int capacity, void* __restrict__ centroids, int32_t* __restrict__ sizes) {
+    const int32_t* __restrict__ blk_first, const int32_t* __restrict__ blk_comm, int64_t max_blocks, int seq_len,
+    int num_sink, int maxc, float* __restrict__ partial) {
+  const int r = blockIdx.y;
+  const int64_t b = (int64_t)blockIdx.x * CENTROID_WAVES + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int g = to_graph[r];
+  const int kvh = to_kv[r];
+  if (b >= blk_first[(int64_t)g * (maxc + 1) + maxc]) return;  // past this graph's blocks
+  const int c = blk_comm[(int64_t)g * max_blocks + b];
+  const int k = (int)(b - blk_first[(int64_t)g * (maxc + 1) + c]);
+  const int lo = offsets[(int64_t)g * (maxc + 1) + c];
+  const int hi = offsets[(int64_t)g * (maxc + 1) + c + 1];
+  const int i0 = SUM_BLOCK * k;  // ascending member index of the block's first member
+  const int n = min(SUM_BLOCK, hi - lo - i0);
+  const int32_t* mem = positions + (int64_t)g * (seq_len - num_sink);
+  const int mine = mem[hi - 1 - (i0 + min(lane, n - 1))];
+  const int64_t kb = (int64_t)kvh * head_stride + 2 * lane;
+  float x0[SUM_BLOCK], x1[SUM_BLOCK];
+#pragma unroll
+  for (int u = 0; u < SUM_BLOCK; ++u) {
+    const int p = __builtin_amdgcn_readlane(mine, u);  // lanes past n repeat the last member
+    if constexpr (KT == CKV_BF16) {
+      const uint32_t w = (uint32_t)gload_i32(reinterpret_cast<const int32_t*>(
+          reinterpret_cast<const uint16_t*>(keys) + kb + (int64_t)p * token_stride));
+      x0[u] = ckv_u2f(w << 16);
+      x1[u] = ckv_u2f(w & 0xffff0000u);
+    } else {
+      const float* kp = reinterpret_cast<const float*>(keys) + kb + (int64_t)p * token_stride;
+      x0[u] = gload_f32(kp);
+      x1[u] = gload_f32(kp + 1);
+    }
+  }
+  float s0 = 0.0f, s1 = 0.0f;  // (+0 start: an all-negative-zero block sums to +0, as scatter_add_ does)
+#pragma unroll
+  for (int u = 0; u < SUM_BLOCK; ++u) {
+    if (u < n) {
+      s0 = s0 + x0[u];
+      s1 = s1 + x1[u];
+    }
+  }
+  float* dst = partial + ((int64_t)r * max_blocks + b) * D + 2 * lane;
+  dst[0] = s0;
+  dst[1] = s1;
+}
+
+// One wave per (retrieval head, community row): the community's block sums
+// added in order, divided by its size, clamped to +-448, then E4M3 or f32.
+// Rows at or past maxc hold zeros.
+template <int CT>
+__global__ __launch_bounds__(64 * CENTROID_WAVES) void centroid_kernel(
+    const int32_t* __restrict__ to_graph, const int32_t* __restrict__ offsets, const int32_t* __restrict__ blk_first,
+    const float* __restrict__ partial, int64_t max_blocks, int maxc, int capacity, void* __restrict__ centroids,
+    int32_t* __restrict__ sizes) {
   const int r = blockIdx.y;
   const int c = blockIdx.x * CENTROID_WAVES + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (c >= capacity) return;
   const int g = to_graph[r];
-  const int kvh = to_kv[r];
-  int lo = 0, hi = 0;
+  int size = 0, b0 = 0, nb = 0;
   if (c < maxc) {
-    lo = offsets[(int64_t)g * (maxc + 1) + c];
-    hi = offsets[(int64_t)g * (maxc + 1) + c + 1];
+    size = offsets[(int64_t)g * (maxc + 1) + c + 1] - offsets[(int64_t)g * (maxc + 1) + c];
+    b0 = blk_first[(int64_t)g * (maxc + 1) + c];
+    nb = blk_first[(int64_t)g * (maxc + 1) + c + 1] - b0;
   }
-  const int32_t* mem = positions + (int64_t)g * (seq_len - num_sink);
-  const int64_t kb = (int64_t)kvh * head_stride + 2 * lane;
+  const float* src = partial + ((int64_t)r * max_blocks + b0) * D + 2 * lane;
   float s0 = 0.0f, s1 = 0.0f;
-  // members hi-1, hi-2, ... are the oldest first (the CSR is newest first)
-  for (int b = hi - 1; b >= lo; b -= 64) {
-    const int n = min(64, b - lo + 1);
-    const int mine = mem[max(b - lane, lo)];
-    for (int j0 = 0; j0 < n; j0 += 8) {
-      float x0[8], x1[8];
+  for (int j0 = 0; j0 < nb; j0 += 16) {
+    float y0[16], y1[16];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int p = __builtin_amdgcn_readlane(mine, min(j0 + u, n - 1));
-        if constexpr (KT == CKV_BF16) {
-          const uint32_t w = (uint32_t)gload_i32(reinterpret_cast<const int32_t*>(
-              reinterpret_cast<const uint16_t*>(keys) + kb + (int64_t)p * token_stride));
-          x0[u] = ckv_u2f(w << 16);
-          x1[u] = ckv_u2f(w & 0xffff0000u);
-        } else {
-          const float* kp = reinterpret_cast<const float*>(keys) + kb + (int64_t)p * token_stride;
-          x0[u] = gload_f32(kp);
-          x1[u] = gload_f32(kp + 1);
-        }
-      }
+    for (int u = 0; u < 16; ++u) {
+      const float* q = src + (int64_t)min(j0 + u, nb - 1) * D;
+      y0[u] = gload_f32(q);
+      y1[u] = gload_f32(q + 1);
+    }
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        if (j0 + u < n) {
-          s0 = s0 + x0[u];
-          s1 = s1 + x1[u];
-        }
+    for (int u = 0; u < 16; ++u) {
+      if (j0 + u < nb) {
+        s0 = s0 + y0[u];
+        s1 = s1 + y1[u];
       }
     }
   }
-  const int size = hi - lo;
   if (c < maxc) {
     const float den = (float)max(size, 1);
     s0 = s0 / den;
@@ -317,10 +432,11 @@ int launch_check() {
 
 using namespace ckv;
 
-extern "C" size_t ckv_state_workspace_bytes(int32_t graphs, int32_t seq_len, int32_t num_sink,
-                                            int32_t max_communities) {
-  if (graphs <= 0 || seq_len <= 0 || max_communities <= 0) return 0;
-  return (size_t)graphs * state_chunks(seq_len, num_sink) * max_communities * sizeof(int32_t);
+extern "C" size_t ckv_state_workspace_bytes(int32_t graphs, int32_t retrieval_heads, int32_t seq_len,
+                                            int32_t num_sink, int32_t max_communities) {
+  if (graphs <= 0 || retrieval_heads <= 0 || seq_len <= num_sink || num_sink < 0 || max_communities <= 0) return 0;
+  return state_ws_words(graphs, retrieval_heads, seq_len, num_sink, max_communities, nullptr, nullptr) *
+         sizeof(int32_t);
 }
 
 extern "C" int ckv_label_counts(const int32_t* labels, int32_t graphs, int32_t seq_len, int32_t num_sink,
@@ -358,26 +474,33 @@ extern "C" int ckv_build_layer_state(const ckv_state_build_args* a, void* stream
     return ckv_internal::set_error(CKV_E_INVALID, "edges need community_weight and total_weight outputs");
   const hipStream_t s = (hipStream_t)stream;
   const int maxc = a->max_communities;
+  const int chunk_len = state_chunk(a->seq_len, a->num_sink);
   const int chunks = state_chunks(a->seq_len, a->num_sink);
+  const int64_t mb = state_max_blocks(a->seq_len, a->num_sink, maxc);
+  StateWorkspace w;
+  state_ws_words(a->graphs, a->retrieval_heads, a->seq_len, a->num_sink, maxc, &w, a->workspace);
   const size_t lds = (size_t)maxc * sizeof(int);
   hipLaunchKernelGGL(chunk_hist_kernel, dim3(chunks, a->graphs), dim3(HIST_THREADS), lds, s, a->labels, a->seq_len,
-                     a->num_sink, maxc, chunks, a->workspace);
-  hipLaunchKernelGGL(csr_scan_kernel, dim3(a->graphs), dim3(SCAN_THREADS), 0, s, maxc, chunks, a->workspace,
-                     a->member_offsets);
+                     a->num_sink, maxc, chunk_len, chunks, w.hist);
+  hipLaunchKernelGGL(csr_scan_kernel, dim3(a->graphs), dim3(SCAN_THREADS), 0, s, maxc, chunks, mb, w.hist,
+                     a->member_offsets, w.blk_first, w.blk_comm);
   hipLaunchKernelGGL(csr_scatter_kernel, dim3(chunks, a->graphs), dim3(64), lds, s, a->labels, a->seq_len,
-                     a->num_sink, maxc, chunks, (const int32_t*)a->workspace, a->member_positions);
+                     a->num_sink, maxc, chunk_len, chunks, (const int32_t*)w.hist, a->member_positions);
+  const dim3 bgrid((unsigned)((mb + CENTROID_WAVES - 1) / CENTROID_WAVES), a->retrieval_heads);
+  auto sums = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, bgrid, dim3(64 * CENTROID_WAVES), 0, s, a->keys, a->head_stride, a->token_stride,
+                       a->retrieval_to_graph, a->retrieval_to_kv, (const int32_t*)a->member_offsets,
+                       (const int32_t*)a->member_positions, (const int32_t*)w.blk_first,
+                       (const int32_t*)w.blk_comm, mb, a->seq_len, a->num_sink, maxc, w.partial);
+  };
+  if (a->key_dtype == CKV_BF16) sums(block_sum_kernel<CKV_BF16>); else sums(block_sum_kernel<CKV_F32>);
   const dim3 cgrid((a->community_capacity + CENTROID_WAVES - 1) / CENTROID_WAVES, a->retrieval_heads);
   auto cent = [&](auto kernel) {
-    hipLaunchKernelGGL(kernel, cgrid, dim3(64 * CENTROID_WAVES), 0, s, a->keys, a->head_stride, a->token_stride,
-                       a->retrieval_to_graph, a->retrieval_to_kv, (const int32_t*)a->member_offsets,
-                       (const int32_t*)a->member_positions, a->seq_len, a->num_sink, maxc, a->community_capacity,
-                       a->centroids, a->community_sizes);
+    hipLaunchKernelGGL(kernel, cgrid, dim3(64 * CENTROID_WAVES), 0, s, a->retrieval_to_graph,
+                       (const int32_t*)a->member_offsets, (const int32_t*)w.blk_first, (const float*)w.partial, mb,
+                       maxc, a->community_capacity, a->centroids, a->community_sizes);
   };
-  if (a->key_dtype == CKV_BF16) {
-    if (a->centroid_dtype == CKV_E4M3) cent(centroid_kernel<CKV_BF16, CKV_E4M3>); else cent(centroid_kernel<CKV_BF16, CKV_F32>);
-  } else {
-    if (a->centroid_dtype == CKV_E4M3) cent(centroid_kernel<CKV_F32, CKV_E4M3>); else cent(centroid_kernel<CKV_F32, CKV_F32>);
-  }
+  if (a->centroid_dtype == CKV_E4M3) cent(centroid_kernel<CKV_E4M3>); else cent(centroid_kernel<CKV_F32>);
   const int64_t ntok = (int64_t)a->graphs * a->token_capacity;
   hipLaunchKernelGGL(token_table_kernel, dim3((unsigned)((ntok + 255) / 256)), dim3(256), 0, s, a->labels,
                      a->seq_len, a->token_capacity, a->graphs, a->token_communities);

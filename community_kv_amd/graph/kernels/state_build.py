@@ -4,9 +4,10 @@
 Produces what the reference's ``build_partitioned_layer`` builds after Leiden
 (graph/partition.py:538-618): ``compute_centroids`` (382-454),
 ``build_member_csr`` (457-492), ``init_modularity_state`` (495-535) and the
-token-community table.  The CSR and the sizes are exact; the centroid means add
-keys in ascending position order (reproducible bit for bit); the modularity
-weights use float atomics like the reference's ``scatter_add_``.
+token-community table.  The CSR and the sizes are exact; the centroid sums add
+keys in ascending position order in blocks of 64 (reproducible bit for bit);
+the modularity weights use float atomics like the reference's
+``scatter_add_``.
 """
 
 from __future__ import annotations
@@ -70,7 +71,7 @@ def build_layer_state(community_ids: torch.Tensor, keys: torch.Tensor, *, retrie
     token_capacity = seq_len + max_decode_tokens if token_capacity is None else token_capacity
     heads = retrieval_to_graph.numel()
     lib = nat.lib()
-    ws_bytes = lib.ckv_state_workspace_bytes(graphs, seq_len, num_sink, maxc)
+    ws_bytes = lib.ckv_state_workspace_bytes(graphs, heads, seq_len, num_sink, maxc)
     i32 = dict(dtype=torch.int32, device=device)
     out = LayerStateTensors(
         community_counts=counts,

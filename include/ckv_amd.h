@@ -220,9 +220,12 @@ int ckv_prefill_attention_topk(const ckv_prefill_args* args, void* stream);
  *   member_offsets    [graphs][max_communities + 1]   CSR over non-sink positions
  *   member_positions  [graphs][seq_len - num_sink]    newest first within a community
  *   centroids         [retrieval_heads][community_capacity][128]: mean of the
- *                     community's non-sink keys of KV head retrieval_to_kv[r]
- *                     (ascending-position f32 sum / size), clamped to +-448,
- *                     E4M3 or f32; rows past max_communities are zero
+ *                     community's non-sink keys of KV head retrieval_to_kv[r],
+ *                     clamped to +-448, E4M3 or f32; rows past max_communities
+ *                     are zero.  The f32 sum runs over the members in
+ *                     ascending position order in blocks of 64 (each block
+ *                     summed in order, then the block sums in order) and is
+ *                     divided by the size
  *   community_sizes   [retrieval_heads][community_capacity]
  *   token_communities [graphs][token_capacity]: the labels, -1 past seq_len
  *   community_weight  [graphs][community_capacity], total_weight [graphs]
@@ -264,7 +267,8 @@ typedef struct ckv_state_build_args {
   int32_t* workspace;
 } ckv_state_build_args;
 
-size_t ckv_state_workspace_bytes(int32_t graphs, int32_t seq_len, int32_t num_sink, int32_t max_communities);
+size_t ckv_state_workspace_bytes(int32_t graphs, int32_t retrieval_heads, int32_t seq_len, int32_t num_sink,
+                                 int32_t max_communities);
 int ckv_label_counts(const int32_t* labels, int32_t graphs, int32_t seq_len, int32_t num_sink,
                      int32_t* community_counts, void* stream);
 int ckv_build_layer_state(const ckv_state_build_args* args, void* stream);

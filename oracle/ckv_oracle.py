@@ -59,12 +59,48 @@ def aggregation_mappings(aggregation: str, *, query_heads: int, kv_heads: int):
     return np.zeros_like(rh), rh
 
 
+CENTROID_SUM_BLOCK = 64
+
+
+def blocked_community_sums(ids, rows, capacity, block=CENTROID_SUM_BLOCK):
+    """f32 sum of ``rows`` per community ``ids`` in the state-build order:
+    members in ascending position (row) order, in blocks of ``block``; each
+    block summed in order from +0, then the block sums added in order from +0.
+    (The reference adds with ``scatter_add_``, whose GPU order is unspecified;
+    any fixed order is a valid restatement, and for communities of at most
+    ``block`` members this is the plain in-order sum.)"""
+    ids = np.asarray(ids, np.int64)
+    rows = np.asarray(rows, np.float32)
+    dim = rows.shape[-1]
+    out = np.zeros((capacity, dim), np.float32)
+    if ids.size == 0:
+        return out
+    order = np.argsort(ids, kind="stable")           # by community, ascending position within
+    sid = ids[order]
+    counts = np.bincount(sid, minlength=capacity)
+    starts = np.concatenate([[0], np.cumsum(counts)[:-1]])
+    rank = np.arange(sid.size) - starts[sid]
+    nblk = (counts + block - 1) // block
+    blk_first = np.concatenate([[0], np.cumsum(nblk)[:-1]])
+    bid = blk_first[sid] + rank // block
+    acc = np.zeros((int(nblk.sum()), dim), np.float32)
+    u = rank % block
+    for j in range(block):
+        sel = u == j
+        acc[bid[sel]] = (acc[bid[sel]] + rows[order[sel]]).astype(np.float32)
+    for k in range(int(nblk.max())):
+        has = nblk > k
+        out[has] = (out[has] + acc[blk_first[has] + k]).astype(np.float32)
+    return out
+
+
 def compute_centroids(community_ids, community_counts, keys, *, to_graph, to_kv,
                       num_sink, max_decode_tokens, fp8=True):
     """Restates ``compute_centroids`` (graph/partition.py:382-454).
 
     keys: float32 values ``[Hkv, S, D]``.  Returns (centroids, sizes) where
-    centroids are E4M3 codes (fp8=True) or float32 values.
+    centroids are E4M3 codes (fp8=True) or float32 values; the sums follow
+    ``blocked_community_sums``.
     """
     community_ids = np.asarray(community_ids)
     graphs, seq_len = community_ids.shape
@@ -77,8 +113,7 @@ def compute_centroids(community_ids, community_counts, keys, *, to_graph, to_kv,
     for r in range(rheads):
         ids = community_ids[to_graph[r], num_sink:].astype(np.int64)
         src = keys[to_kv[r], num_sink:].astype(np.float32)
-        # scatter_add_ in token order (float32 accumulation like torch's CPU scatter)
-        np.add.at(sums[r], ids, src)
+        sums[r] = blocked_community_sums(ids, src, capacity)
         np.add.at(sizes[r], ids, 1)
     cent = sums.copy()
     cent[:, :active_capacity] = (

@@ -86,6 +86,37 @@ def test_pinned_dot_is_exact_for_bf16_by_fp8_products():
     assert np.max(np.abs(got - ref)) < 1e-4
 
 
+def test_blocked_community_sums_order():
+    """Centroid sums: a scalar loop over each community's members (ascending
+    positions, blocks of 64 from +0, block sums in order from +0) agrees bit
+    for bit; communities of at most 64 members equal the plain in-order sum;
+    every sum is within fp32 rounding of the float64 sum."""
+    rng = np.random.default_rng(11)
+    n, cap = 3000, 12
+    w = 1.0 / np.arange(1, cap + 1) ** 1.5
+    ids = rng.choice(cap, size=n, p=w / w.sum())
+    ids[ids == 7] = 8  # an empty community
+    rows = (rng.standard_normal((n, 3)) * np.exp(2 * rng.standard_normal((n, 1)))).astype(np.float32)
+    got = co.blocked_community_sums(ids, rows, cap)
+    for c in range(cap):
+        mem = rows[ids == c]
+        total = np.zeros(3, np.float32)
+        for b0 in range(0, len(mem), 64):
+            blk = np.zeros(3, np.float32)
+            for x in mem[b0:b0 + 64]:
+                blk = (blk + x).astype(np.float32)
+            total = (total + blk).astype(np.float32)
+        assert np.array_equal(got[c], total), c
+        ref = mem.astype(np.float64).sum(0)
+        assert np.all(np.abs(got[c] - ref) <= 1e-5 * np.abs(mem).sum(0) + 1e-30)
+        if len(mem) <= 64:
+            seq = np.zeros((1, 3), np.float32)
+            np.add.at(seq, np.zeros(len(mem), np.int64), mem)  # scatter_add_'s in-order CPU sum
+            assert np.array_equal(got[c], seq[0])
+    assert not got[7].any()
+    assert (np.bincount(ids, minlength=cap) > 64).sum() >= 2  # the blocked path is exercised
+
+
 def test_attention_matches_torch_sdpa():
     rng = np.random.default_rng(5)
     q = rng.standard_normal((4, 128)).astype(np.float32)
