@@ -311,6 +311,100 @@ def run_prefill(args, device):
     print(json.dumps(result), flush=True)
 
 
+STATE_EDGES_PER_GRAPH = 1_500_000
+
+
+def run_state(args, device):
+    """GPU state assembly of one config-2 layer from labels (the 'next' row
+    after the decode path): 8 QUERY_GROUP graphs x 32,768 positions, 512
+    Zipf(1.1) communities, bf16 keys, 1.5M prefill edges per graph (sorted by
+    graph and source, as the coalesced adjacency is).  Times
+    ckv_build_layer_state (CSR, centroids, sizes, modularity weights, token
+    table) with inputs and outputs resident; the label-count read-back that
+    sizes the outputs is set-up."""
+    from community_kv_amd.graph.kernels.state_build import StateBuild
+
+    rng = np.random.default_rng(3)
+    gen = torch.Generator(device=device).manual_seed(3)
+    labels = torch.from_numpy(np.stack([zipf_labels(rng, SEQ, SINKS, COMMUNITIES) for _ in range(HKV)])).to(device)
+    keys = torch.randn(HKV, SEQ + 64, D, device=device, generator=gen).to(torch.bfloat16)[:, :SEQ]
+    n = STATE_EDGES_PER_GRAPH
+    g = torch.arange(HKV, device=device).repeat_interleave(n)
+    a = torch.randint(SINKS, SEQ, (HKV * n,), device=device, generator=gen)
+    b = torch.randint(SINKS, SEQ, (HKV * n,), device=device, generator=gen)
+    key = (g * SEQ + a) * SEQ + b
+    key = key.sort().values
+    src = (key // SEQ).to(torch.int32)
+    dst = (g * SEQ + key % SEQ).to(torch.int32)
+    w = torch.rand(HKV * n, device=device, generator=gen)
+    maps = torch.arange(HKV, dtype=torch.int32, device=device)
+    max_decode = 64
+    build = StateBuild(labels, keys, retrieval_to_graph=maps, retrieval_to_kv=maps, num_sink=SINKS,
+                       max_decode_tokens=max_decode, edges=(src, dst, w))
+    for _ in range(args.warmup):
+        build.run()
+    torch.cuda.synchronize(device)
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(args.steps):
+        build.run()
+    stop.record()
+    torch.cuda.synchronize(device)
+    ms = start.elapsed_time(stop) / args.steps
+    out = build.out
+    cap = out.community_sizes.shape[1]
+    edges = HKV * n
+    nsink = SEQ - SINKS
+    algorithmic = (HKV * SEQ * 4                      # labels
+                   + HKV * nsink * D * 2              # keys, each non-sink row once
+                   + edges * (4 + 4 + 4)              # edge src, dst, weight
+                   + edges * 2 * 4                    # the two endpoint labels
+                   + HKV * nsink * 4                  # member positions
+                   + out.member_offsets.numel() * 4
+                   + HKV * cap * (D + 4)              # centroids (e4m3) + sizes
+                   + out.token_communities.numel() * 4
+                   + HKV * (cap + 1) * 4)             # modularity weights
+    gbs = algorithmic / (ms * 1e-3) / 1e9
+    result = {
+        "metric": "state_build_us_32k_qwen3_8b_layer",
+        "value": ms * 1e3,
+        "unit": "us",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int32+bf16->e4m3",
+        "data": "synthetic (Zipf(1.1) labels, N(0,1) bf16 keys, uniform random edges)",
+        "config": {"workload": "GPU state assembly from labels, config-2 layer (8 graphs x 32768, 512 communities, "
+                               "1.5M edges per graph)", "graphs": HKV, "seq_len": SEQ, "communities": COMMUNITIES,
+                   "edges": edges},
+        "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": gbs / HBM_PEAK_GBS, "traffic": None,
+                     "kernel": "ckv_build_layer_state (7 launches, whole build)", "bytes_per_launch": algorithmic},
+    }
+    if not args.no_cpu:
+        from oracle import ckv_oracle as co
+
+        ids = labels.cpu().numpy()
+        counts = (ids[:, SINKS:].max(axis=1) + 1).astype(np.int32)
+        kn = keys.float().cpu().numpy()
+        sn, dn, wn = src.cpu().numpy(), dst.cpu().numpy(), w.cpu().numpy()
+        mp = np.arange(HKV, dtype=np.int32)
+        t0 = time.perf_counter()
+        co.build_member_csr(ids, counts, num_sink=SINKS)
+        co.compute_centroids(ids, counts, kn, to_graph=mp, to_kv=mp, num_sink=SINKS, max_decode_tokens=max_decode)
+        co.init_modularity_state(ids, sn, dn, wn, community_capacity=cap, seq_len=SEQ)
+        sec = time.perf_counter() - t0
+        result["cpu_baseline"] = {"value": sec * 1e6, "unit": "us", "cores": 1, "kind": "port",
+                                  "sample": "the whole layer build (numpy oracle: CSR, centroids, modularity "
+                                            "weights), once"}
+    print(json.dumps(result), flush=True)
+
+
 GEN_LAYERS = 36
 GEN_PROMPT = 65536
 GEN_STEPS = 128
@@ -480,9 +574,10 @@ def main():
     ap.add_argument("--layers", type=int, default=LAYERS)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
-    ap.add_argument("--workload", choices=["decode", "prefill", "generate", "batched"], default="decode",
+    ap.add_argument("--workload", choices=["decode", "prefill", "generate", "batched", "state"], default="decode",
                     help="decode: the 36-layer sparse decode step (default); prefill: config-5 edge export; "
-                         "generate: config-3 model decode loop; batched: config-4 ragged batch")
+                         "generate: config-3 model decode loop; batched: config-4 ragged batch; "
+                         "state: GPU state assembly of one config-2 layer from labels")
     ap.add_argument("--gen-layers", type=int, default=GEN_LAYERS)
     ap.add_argument("--gen-prompt", type=int, default=GEN_PROMPT)
     ap.add_argument("--gen-steps", type=int, default=GEN_STEPS)
@@ -500,6 +595,8 @@ def main():
     if args.workload == "generate":
         run_generate(args, device)
         return
+    if args.workload == "state":
+        return run_state(args, device)
     if args.workload == "batched":
         run_batched(args, device)
         return

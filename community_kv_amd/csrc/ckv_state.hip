@@ -146,70 +146,65 @@ __global__ __launch_bounds__(SCAN_THREADS) void csr_scan_kernel(int maxc, int ch
                                                                 int32_t* __restrict__ offsets,
                                                                 int32_t* __restrict__ blk_first,
                                                                 int32_t* __restrict__ blk_comm) {
-  constexpr int PER = CKV_MAX_COMMUNITIES / SCAN_THREADS;
+  // communities c = k * SCAN_THREADS + tid, one block-wide scan per round k
   const int g = blockIdx.x;
   const int tid = threadIdx.x;
   int32_t* h = hist + (int64_t)g * chunks * maxc;
-  int tot[PER];
-  int local = 0;
-#pragma unroll
-  for (int k = 0; k < PER; ++k) {
-    const int c = tid * PER + k;
-    int t = 0;
-    if (c < maxc) {
-      for (int i = 0; i < chunks; ++i) t += h[(int64_t)i * maxc + c];
-    }
-    tot[k] = t;
-    local += t;
-  }
-  // exclusive scans of the thread sums (thread order = community order): members and 64-member blocks
-  int lblk = 0;
-#pragma unroll
-  for (int k = 0; k < PER; ++k) lblk += (tot[k] + SUM_BLOCK - 1) / SUM_BLOCK;
-  __shared__ int s_wave[SCAN_THREADS / 64], s_wblk[SCAN_THREADS / 64];
-  const int inc = wave_inclusive_scan(local);
-  const int incb = wave_inclusive_scan(lblk);
-  if ((tid & 63) == 63) {
-    s_wave[tid >> 6] = inc;
-    s_wblk[tid >> 6] = incb;
-  }
-  __syncthreads();
-  int base = inc - local;
-  int bbase = incb - lblk;
-  for (int w = 0; w < (tid >> 6); ++w) {
-    base += s_wave[w];
-    bbase += s_wblk[w];
-  }
+  int32_t* off = offsets + (int64_t)g * (maxc + 1);
   int32_t* bf = blk_first + (int64_t)g * (maxc + 1);
   int32_t* bc = blk_comm + (int64_t)g * max_blocks;
-  {
-    int b = bbase;
-#pragma unroll
-    for (int k = 0; k < PER; ++k) {
-      const int c = tid * PER + k;
-      if (c < maxc) bf[c] = b;
-      const int nb = (tot[k] + SUM_BLOCK - 1) / SUM_BLOCK;
-      for (int j = 0; j < nb; ++j) bc[b + j] = c;
-      b += nb;
-      if (c == maxc - 1) bf[maxc] = b;
+  __shared__ int s_wave[SCAN_THREADS / 64], s_wblk[SCAN_THREADS / 64];
+  int carry = 0, bcarry = 0;
+  for (int c0 = 0; c0 < maxc; c0 += SCAN_THREADS) {
+    const int c = c0 + tid;
+    int t = 0;
+    if (c < maxc) {
+#pragma unroll 8
+      for (int i = 0; i < chunks; ++i) t += h[(int64_t)i * maxc + c];
     }
-  }
-  int32_t* off = offsets + (int64_t)g * (maxc + 1);
-#pragma unroll
-  for (int k = 0; k < PER; ++k) {
-    const int c = tid * PER + k;
+    const int nb = (t + SUM_BLOCK - 1) / SUM_BLOCK;
+    const int inc = wave_inclusive_scan(t);
+    const int incb = wave_inclusive_scan(nb);
+    if ((tid & 63) == 63) {
+      s_wave[tid >> 6] = inc;
+      s_wblk[tid >> 6] = incb;
+    }
+    __syncthreads();
+    int base = carry + inc - t, bbase = bcarry + incb - nb;
+    int round = 0, bround = 0;
+    for (int wv = 0; wv < SCAN_THREADS / 64; ++wv) {
+      if (wv < (tid >> 6)) {
+        base += s_wave[wv];
+        bbase += s_wblk[wv];
+      }
+      round += s_wave[wv];
+      bround += s_wblk[wv];
+    }
+    __syncthreads();  // s_wave reused next round
     if (c < maxc) {
       off[c] = base;
+      bf[c] = bbase;
+      for (int j = 0; j < nb; ++j) bc[bbase + j] = c;
       int run = base;
-      for (int i = chunks - 1; i >= 0; --i) {
-        const int64_t j = (int64_t)i * maxc + c;
-        const int n = h[j];
-        h[j] = run;
-        run += n;
+      for (int i0 = chunks - 1; i0 >= 0; i0 -= 8) {  // eight loads in flight, then their stores
+        int n[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) n[u] = i0 - u >= 0 ? h[(int64_t)(i0 - u) * maxc + c] : 0;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          if (i0 - u >= 0) {
+            h[(int64_t)(i0 - u) * maxc + c] = run;
+            run += n[u];
+          }
+        }
       }
     }
-    base += tot[k];
-    if (c == maxc - 1) off[maxc] = base;
+    carry += round;
+    bcarry += bround;
+  }
+  if (tid == 0) {
+    off[maxc] = carry;
+    bf[maxc] = bcarry;
   }
 }
 
@@ -379,46 +374,54 @@ __global__ void weight_zero_kernel(float* __restrict__ weight, int64_t n, float*
 
 // Community degree weights and 2m: each edge (graph * seq_len + position
 // endpoints) adds its weight to both endpoint communities and twice to its
-// graph's total (one atomic per workgroup and graph run).
+// graph's total.  A workgroup takes EDGES_PER_WG consecutive edges (the list
+// is grouped by graph): the weights of the graph of its first edge gather in
+// LDS and leave with one global atomic per touched community; edges of other
+// graphs (at most a boundary's worth) add straight to global memory.
+constexpr int EDGES_PER_WG = 8192;
+
 __global__ __launch_bounds__(EDGE_THREADS) void edge_weight_kernel(
     const int32_t* __restrict__ labels, int seq_len, int graphs, int capacity, const int32_t* __restrict__ src,
     const int32_t* __restrict__ dst, const float* __restrict__ w, int64_t edges, float* __restrict__ weight,
     float* __restrict__ total) {
-  const int64_t e = (int64_t)blockIdx.x * EDGE_THREADS + threadIdx.x;
+  extern __shared__ float w_s[];
+  const int64_t e0 = (int64_t)blockIdx.x * EDGES_PER_WG;
+  const int64_t e1 = min(edges, e0 + EDGES_PER_WG);
+  const int g0 = src[e0] / seq_len;
+  for (int c = threadIdx.x; c < capacity; c += EDGE_THREADS) w_s[c] = 0.0f;
+  __syncthreads();
   float mine = 0.0f;
-  int g = -1;
-  if (e < edges) {
+  for (int64_t e = e0 + threadIdx.x; e < e1; e += EDGE_THREADS) {
     const int s = src[e], d = dst[e];
-    g = s / seq_len;
+    const int g = s / seq_len;
+    if (g < 0 || g >= graphs || d / seq_len != g) continue;
     const float x = w[e];
-    if (g >= 0 && g < graphs && d / seq_len == g) {
-      const int sc = labels[(int64_t)g * seq_len + s % seq_len];
-      const int dc = labels[(int64_t)g * seq_len + d % seq_len];
+    const int sc = labels[(int64_t)g * seq_len + s % seq_len];
+    const int dc = labels[(int64_t)g * seq_len + d % seq_len];
+    if (g == g0) {
+      if (sc >= 0 && sc < capacity) atomicAdd(w_s + sc, x);
+      if (dc >= 0 && dc < capacity) atomicAdd(w_s + dc, x);
+      mine = mine + 2.0f * x;
+    } else {
       if (sc >= 0 && sc < capacity) atomicAdd(weight + (int64_t)g * capacity + sc, x);
       if (dc >= 0 && dc < capacity) atomicAdd(weight + (int64_t)g * capacity + dc, x);
-      mine = 2.0f * x;
-    } else {
-      g = -1;
+      atomicAdd(total + g, 2.0f * x);
     }
   }
-  // edges are grouped by graph (src-major): sum this workgroup's share per graph
-  __shared__ float s_sum[EDGE_THREADS];
-  __shared__ int s_g[EDGE_THREADS];
-  s_sum[threadIdx.x] = mine;
-  s_g[threadIdx.x] = g;
+  __shared__ float s_part[EDGE_THREADS / 64];
+  mine = wave_sum_tree(mine);
+  if ((threadIdx.x & 63) == 0) s_part[threadIdx.x >> 6] = mine;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    int cg = -1;
-    float acc = 0.0f;
-    for (int i = 0; i < EDGE_THREADS; ++i) {
-      if (s_g[i] != cg) {
-        if (cg >= 0) atomicAdd(total + cg, acc);
-        cg = s_g[i];
-        acc = 0.0f;
-      }
-      acc = acc + s_sum[i];
+  if (g0 >= 0 && g0 < graphs) {
+    for (int c = threadIdx.x; c < capacity; c += EDGE_THREADS) {
+      const float v = w_s[c];
+      if (v != 0.0f) atomicAdd(weight + (int64_t)g0 * capacity + c, v);
     }
-    if (cg >= 0) atomicAdd(total + cg, acc);
+    if (threadIdx.x == 0) {
+      float t = 0.0f;
+      for (int i = 0; i < EDGE_THREADS / 64; ++i) t = t + s_part[i];
+      atomicAdd(total + g0, t);
+    }
   }
 }
 
@@ -510,8 +513,8 @@ extern "C" int ckv_build_layer_state(const ckv_state_build_args* a, void* stream
     hipLaunchKernelGGL(weight_zero_kernel, dim3((unsigned)((nz + 255) / 256)), dim3(256), 0, s, a->community_weight,
                        nw, a->total_weight, a->graphs);
     if (a->edges > 0) {
-      hipLaunchKernelGGL(edge_weight_kernel, dim3((unsigned)((a->edges + EDGE_THREADS - 1) / EDGE_THREADS)),
-                         dim3(EDGE_THREADS), 0, s, a->labels, a->seq_len, a->graphs, a->community_capacity,
+      hipLaunchKernelGGL(edge_weight_kernel, dim3((unsigned)((a->edges + EDGES_PER_WG - 1) / EDGES_PER_WG)),
+                         dim3(EDGE_THREADS), (size_t)a->community_capacity * sizeof(float), s, a->labels, a->seq_len, a->graphs, a->community_capacity,
                          a->edge_src, a->edge_dst, a->edge_weight, a->edges, a->community_weight, a->total_weight);
     }
   }

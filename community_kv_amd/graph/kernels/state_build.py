@@ -43,6 +43,84 @@ def label_counts(community_ids: torch.Tensor, *, num_sink: int) -> torch.Tensor:
     return counts
 
 
+class StateBuild:
+    """One layer's state build, set up once: reads the community counts back,
+    allocates the outputs and the workspace, and packs the launch arguments;
+    ``run()`` queues ``ckv_build_layer_state`` on the current stream (it may be
+    replayed, e.g. for timing)."""
+
+    def __init__(self, community_ids: torch.Tensor, keys: torch.Tensor, *, retrieval_to_graph: torch.Tensor,
+                 retrieval_to_kv: torch.Tensor, num_sink: int, max_decode_tokens: int, fp8: bool = True,
+                 edges: tuple[torch.Tensor, torch.Tensor, torch.Tensor] | None = None,
+                 token_capacity: int | None = None):
+        device = nat.require_device(community_ids, keys, retrieval_to_graph, retrieval_to_kv)
+        if keys.ndim != 3 or keys.shape[-1] != nat.HEAD_DIM or keys.stride(-1) != 1:
+            raise ValueError("keys must be [KV heads, sequence, 128] with unit dim stride")
+        graphs, seq_len = community_ids.shape
+        if keys.shape[1] < seq_len:
+            raise ValueError("keys must cover the labelled sequence")
+        if not 0 <= num_sink < seq_len:
+            raise ValueError("num_sink must be below the sequence length")
+        if retrieval_to_graph.dtype != torch.int32 or retrieval_to_kv.dtype != torch.int32:
+            raise TypeError("aggregation mappings must be int32")
+        self.device = device
+        self.ids = community_ids.to(torch.int32).contiguous()
+        counts = label_counts(self.ids, num_sink=num_sink)
+        host_counts = counts.cpu()
+        if int(host_counts.min()) < 0:
+            raise ValueError("community labels of non-sink positions must be nonnegative")
+        maxc = int(host_counts.max())
+        if maxc <= 0:
+            raise ValueError("no labelled non-sink positions")
+        if maxc > nat.MAX_COMMUNITIES:
+            raise ValueError(f"more than {nat.MAX_COMMUNITIES} communities per graph are not supported")
+        capacity = maxc + max_decode_tokens
+        token_capacity = seq_len + max_decode_tokens if token_capacity is None else token_capacity
+        heads = retrieval_to_graph.numel()
+        lib = nat.lib()
+        ws_bytes = lib.ckv_state_workspace_bytes(graphs, heads, seq_len, num_sink, maxc)
+        i32 = dict(dtype=torch.int32, device=device)
+        self.out = LayerStateTensors(
+            community_counts=counts,
+            member_offsets=torch.empty((graphs, maxc + 1), **i32),
+            member_positions=torch.empty((graphs, seq_len - num_sink), **i32),
+            centroids=torch.empty((heads, capacity, nat.HEAD_DIM),
+                                  dtype=torch.float8_e4m3fn if fp8 else torch.float32, device=device),
+            community_sizes=torch.empty((heads, capacity), **i32),
+            community_weight=torch.empty((graphs, capacity), dtype=torch.float32, device=device),
+            total_weight=torch.empty((graphs,), dtype=torch.float32, device=device),
+            token_communities=torch.empty((graphs, token_capacity), **i32),
+        )
+        self.workspace = torch.empty(max(ws_bytes // 4, 1), **i32)
+        self.keys = keys
+        self.edges = None
+        n_edges = 0
+        if edges is not None and edges[0].numel():
+            self.edges = (edges[0].to(device=device, dtype=torch.int32).contiguous(),
+                          edges[1].to(device=device, dtype=torch.int32).contiguous(),
+                          edges[2].to(device=device, dtype=torch.float32).contiguous())
+            n_edges = self.edges[0].numel()
+        src, dst, w = self.edges if self.edges is not None else (None, None, None)
+        self.maps = (retrieval_to_graph.contiguous(), retrieval_to_kv.contiguous())
+        o = self.out
+        self.args = nat.StateBuildArgs(
+            labels=nat.ptr(self.ids), keys=nat.ptr(keys), head_stride=keys.stride(0),
+            token_stride=keys.stride(1), retrieval_to_graph=nat.ptr(self.maps[0]),
+            retrieval_to_kv=nat.ptr(self.maps[1]), edge_src=nat.ptr(src), edge_dst=nat.ptr(dst),
+            edge_weight=nat.ptr(w), edges=n_edges, graphs=graphs, seq_len=seq_len, num_sink=num_sink,
+            retrieval_heads=heads, kv_heads=keys.shape[0], key_dtype=nat.dtype_code(keys.dtype),
+            centroid_dtype=nat.CKV_E4M3 if fp8 else nat.CKV_F32, max_communities=maxc,
+            community_capacity=capacity, token_capacity=token_capacity,
+            member_offsets=nat.ptr(o.member_offsets), member_positions=nat.ptr(o.member_positions),
+            centroids=nat.ptr(o.centroids), community_sizes=nat.ptr(o.community_sizes),
+            community_weight=nat.ptr(o.community_weight), total_weight=nat.ptr(o.total_weight),
+            token_communities=nat.ptr(o.token_communities), workspace=nat.ptr(self.workspace))
+
+    def run(self) -> LayerStateTensors:
+        nat.check(nat.lib().ckv_build_layer_state(self.args, nat.stream_handle(self.device)))
+        return self.out
+
+
 def build_layer_state(community_ids: torch.Tensor, keys: torch.Tensor, *, retrieval_to_graph: torch.Tensor,
                       retrieval_to_kv: torch.Tensor, num_sink: int, max_decode_tokens: int, fp8: bool = True,
                       edges: tuple[torch.Tensor, torch.Tensor, torch.Tensor] | None = None,
@@ -50,65 +128,12 @@ def build_layer_state(community_ids: torch.Tensor, keys: torch.Tensor, *, retrie
     """Every prefill state tensor of one layer from labels ``[graphs, S]`` and
     keys ``[Hkv, S, 128]`` (bf16 or f32, token stride may exceed 128).  Reads
     the community counts back once to size the outputs, as the reference
-    does with ``.item()``."""
-    device = nat.require_device(community_ids, keys, retrieval_to_graph, retrieval_to_kv)
-    if keys.ndim != 3 or keys.shape[-1] != nat.HEAD_DIM or keys.stride(-1) != 1:
-        raise ValueError("keys must be [KV heads, sequence, 128] with unit dim stride")
-    graphs, seq_len = community_ids.shape
-    if keys.shape[1] < seq_len:
-        raise ValueError("keys must cover the labelled sequence")
-    if retrieval_to_graph.dtype != torch.int32 or retrieval_to_kv.dtype != torch.int32:
-        raise TypeError("aggregation mappings must be int32")
-    ids = community_ids.to(torch.int32).contiguous()
-    counts = label_counts(ids, num_sink=num_sink)
-    host_counts = counts.cpu()
-    if int(host_counts.min()) < 0:
-        raise ValueError("community labels of non-sink positions must be nonnegative")
-    maxc = int(host_counts.max())
-    if maxc <= 0:
-        raise ValueError("no labelled non-sink positions")
-    capacity = maxc + max_decode_tokens
-    token_capacity = seq_len + max_decode_tokens if token_capacity is None else token_capacity
-    heads = retrieval_to_graph.numel()
-    lib = nat.lib()
-    ws_bytes = lib.ckv_state_workspace_bytes(graphs, heads, seq_len, num_sink, maxc)
-    i32 = dict(dtype=torch.int32, device=device)
-    out = LayerStateTensors(
-        community_counts=counts,
-        member_offsets=torch.empty((graphs, maxc + 1), **i32),
-        member_positions=torch.empty((graphs, seq_len - num_sink), **i32),
-        centroids=torch.empty((heads, capacity, nat.HEAD_DIM),
-                              dtype=torch.float8_e4m3fn if fp8 else torch.float32, device=device),
-        community_sizes=torch.empty((heads, capacity), **i32),
-        community_weight=torch.empty((graphs, capacity), dtype=torch.float32, device=device),
-        total_weight=torch.empty((graphs,), dtype=torch.float32, device=device),
-        token_communities=torch.empty((graphs, token_capacity), **i32),
-    )
-    workspace = torch.empty(max(ws_bytes // 4, 1), **i32)
-    src = dst = w = None
-    n_edges = 0
-    if edges is not None and edges[0].numel():
-        src = edges[0].to(device=device, dtype=torch.int32).contiguous()
-        dst = edges[1].to(device=device, dtype=torch.int32).contiguous()
-        w = edges[2].to(device=device, dtype=torch.float32).contiguous()
-        n_edges = src.numel()
-    to_graph = retrieval_to_graph.contiguous()
-    to_kv = retrieval_to_kv.contiguous()
-    args = nat.StateBuildArgs(
-        labels=nat.ptr(ids), keys=nat.ptr(keys), head_stride=keys.stride(0), token_stride=keys.stride(1),
-        retrieval_to_graph=nat.ptr(to_graph), retrieval_to_kv=nat.ptr(to_kv), edge_src=nat.ptr(src),
-        edge_dst=nat.ptr(dst), edge_weight=nat.ptr(w), edges=n_edges, graphs=graphs, seq_len=seq_len,
-        num_sink=num_sink, retrieval_heads=heads, kv_heads=keys.shape[0], key_dtype=nat.dtype_code(keys.dtype),
-        centroid_dtype=nat.CKV_E4M3 if fp8 else nat.CKV_F32, max_communities=maxc, community_capacity=capacity,
-        token_capacity=token_capacity, member_offsets=nat.ptr(out.member_offsets),
-        member_positions=nat.ptr(out.member_positions), centroids=nat.ptr(out.centroids),
-        community_sizes=nat.ptr(out.community_sizes), community_weight=nat.ptr(out.community_weight),
-        total_weight=nat.ptr(out.total_weight), token_communities=nat.ptr(out.token_communities),
-        workspace=nat.ptr(workspace))
-    # (the workspace and edge copies are freed to the caching allocator on this
-    # stream, so later work on it cannot overwrite them before the launches run)
-    nat.check(lib.ckv_build_layer_state(args, nat.stream_handle(device)))
-    return out
+    does with ``.item()``.  (The workspace and edge copies return to the
+    caching allocator on this stream, so later work on it cannot overwrite
+    them before the launches run.)"""
+    return StateBuild(community_ids, keys, retrieval_to_graph=retrieval_to_graph, retrieval_to_kv=retrieval_to_kv,
+                      num_sink=num_sink, max_decode_tokens=max_decode_tokens, fp8=fp8, edges=edges,
+                      token_capacity=token_capacity).run()
 
 
-__all__ = ["LayerStateTensors", "build_layer_state", "label_counts"]
+__all__ = ["LayerStateTensors", "StateBuild", "build_layer_state", "label_counts"]
