@@ -258,6 +258,66 @@ class DecodeRuntime:
             raise RuntimeError(f"decode state overflow: {failures}")
 
 
+class _DecodeStepGraph:
+    """Replaces ``model.forward`` during ``CommunityKVRuntime.generate``: every
+    single-token step after the first (which completes the prefill hand-off
+    and moves the cache cursor to the device) replays one HIP graph of the
+    whole model forward -- projections, norms, RoPE, cache writes, the sparse
+    decode of every layer with the previous layer's deferred update, and the
+    LM head -- instead of launching each kernel from Python.  The step's
+    inputs are copied into the graph's fixed buffers; the returned output
+    holds the graph's fixed logits buffer (the caller copies what it keeps, as
+    ``generate`` does).  Other calls (prefill, first step) run eagerly."""
+
+    def __init__(self, model: Any, runtime: "CommunityKVRuntime") -> None:
+        self.model = model
+        self.runtime = runtime
+        self.forward = model.forward
+        self.graph: torch.cuda.CUDAGraph | None = None
+        self.static: dict[str, torch.Tensor] = {}
+        self.output: Any = None
+        self.replays = 0
+
+    # per-step tensors copied into fixed buffers (when the caller passes them;
+    # otherwise the model derives positions from the cache's device cursor)
+    STEP_TENSORS = ("input_ids", "position_ids", "cache_position")
+
+    def __call__(self, *args: Any, **kwargs: Any) -> Any:
+        ids = kwargs.get("input_ids")
+        if (args or ids is None or ids.ndim != 2 or ids.shape[-1] != 1 or kwargs.get("inputs_embeds") is not None
+                or not self.runtime._ready):
+            return self.forward(*args, **kwargs)
+        if self.graph is None:
+            self._capture(kwargs)
+        for name in self.STEP_TENSORS:
+            if name in self.static:
+                self.static[name].copy_(kwargs[name])
+        self.graph.replay()
+        self.replays += 1
+        return self.output
+
+    def _capture(self, kwargs: dict[str, Any]) -> None:
+        device = kwargs["input_ids"].device
+        self.static = {name: kwargs[name].clone() for name in self.STEP_TENSORS
+                       if isinstance(kwargs.get(name), torch.Tensor)}
+        call = {k: v for k, v in kwargs.items() if k not in self.STEP_TENSORS and k != "attention_mask"}
+        call.update(self.static)
+        # the community_kv attention reads no mask, and a 2-D mask grows every step
+        call["attention_mask"] = None
+        graph = torch.cuda.CUDAGraph()
+        stream = torch.cuda.Stream(device)
+        stream.wait_stream(torch.cuda.current_stream(device))
+        with torch.cuda.graph(graph, stream=stream):
+            self.output = self.forward(**call)
+        torch.cuda.current_stream(device).wait_stream(stream)
+        self.graph = graph
+
+    def release(self) -> None:
+        self.graph = None
+        self.output = None
+        self.static = {}
+
+
 class CommunityKVRuntime:
     """Request runtime spanning prefill, partition hand-off and decode (runtime.py:402-614)."""
 
@@ -329,7 +389,11 @@ class CommunityKVRuntime:
 
     def generate(self, model: Any, inputs: torch.Tensor | None = None, *,
                  resolutions: Mapping[int, float] | Sequence[float] | None = None, **kwargs: Any) -> Any:
-        """Generates one sequence with runtime-managed request state and cache (runtime.py:510-608)."""
+        """Generates one sequence with runtime-managed request state and cache (runtime.py:510-608).
+
+        ``graph_decode`` (default True, not a Hugging Face option) replays the
+        model's single-token forward from one HIP graph after the first decode
+        step (see ``_DecodeStepGraph``); False launches every step eagerly."""
         if inputs is not None and "input_ids" in kwargs:
             raise ValueError("pass input_ids either positionally or by keyword")
         input_ids = kwargs.get("input_ids", inputs)
@@ -375,16 +439,24 @@ class CommunityKVRuntime:
             raise RuntimeError("CommunityKV runtime is already generating")
         self.start_request(resolutions=resolutions, max_decode_tokens=max(1, max_new_tokens - 1))
         generate_kwargs = dict(kwargs)
+        generate_kwargs.pop("graph_decode", None)
         generate_kwargs.update(past_key_values=cache, do_sample=False, num_beams=1, num_return_sequences=1)
         if hasattr(generation_config, "disable_compile"):
             generate_kwargs["disable_compile"] = True
         self._generation_cache = cache
+        step_graph = _DecodeStepGraph(model, self) if kwargs.get("graph_decode", True) else None
+        if step_graph is not None:
+            model.forward = step_graph
         try:
             output = model.generate(**generate_kwargs) if inputs is None else model.generate(inputs, **generate_kwargs)
             self.finish_prefill()
             self.assert_no_overflow()
+            self.last_graph_replays = 0 if step_graph is None else step_graph.replays
             return output
         finally:
+            if step_graph is not None:
+                del model.forward  # back to the class's forward
+                step_graph.release()
             self._generation_cache = None
 
     def close(self) -> None:

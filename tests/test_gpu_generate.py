@@ -5,7 +5,9 @@ With every community selected (``selection="topk"`` over all communities) the
 sparse decode attends the whole context, so every step's logits must match a
 dense eager forward over the generated sequence up to bf16 rounding; that pins the
 plumbing (prefill kernel, edge hand-off, state install, static cache with a
-device cursor, deferred online updates) without a reference run."""
+device cursor, deferred online updates, the HIP-graph replay of the
+single-token forward, checked on every replayed step) without a reference
+run."""
 
 from __future__ import annotations
 
@@ -39,12 +41,12 @@ def _labels(layer_idx, keys, topk_indices, topk_scores):
     return lab
 
 
-@pytest.mark.parametrize("assignment", ["delta_q", "nearest_centroid"])
-def test_generate_full_selection_matches_dense(device, assignment):
+@pytest.mark.parametrize("assignment,graph", [("delta_q", True), ("nearest_centroid", True), ("delta_q", False)])
+def test_generate_full_selection_matches_dense(device, assignment, graph):
     from community_kv_amd import CommunityKVAttention, CommunityKVConfig, CommunityKVRuntime, GraphAggregation
     from community_kv_amd.config import PartitionConfig
 
-    print(f"generate e2e assignment={assignment}", flush=True)
+    print(f"generate e2e assignment={assignment} graph={graph}", flush=True)
     model = _model(device)
     prompt = torch.randint(0, 512, (1, 300), generator=torch.Generator().manual_seed(1)).to(device)
     new = 8
@@ -57,8 +59,10 @@ def test_generate_full_selection_matches_dense(device, assignment):
         model.set_attn_implementation("community_kv")
         with torch.inference_mode():
             out = runtime.generate(model, prompt, max_new_tokens=new, output_logits=True,
-                                   return_dict_in_generate=True)
+                                   return_dict_in_generate=True, graph_decode=graph)
         torch.cuda.synchronize()
+        # prefill + one eager decode step, then one graph replay per further token
+        assert runtime.last_graph_replays == (new - 2 if graph else 0)
         # every decoded token joined a community of every graph
         for layer in runtime.decode_runtime.layers.values():
             cur = layer.converted.current_position.cpu()
