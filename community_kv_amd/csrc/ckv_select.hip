@@ -99,7 +99,8 @@ __host__ __device__ inline size_t fused_slot_bytes(int slot_capacity) { return (
 // FUSED: `part` of `parts` workgroups of this head each run the whole
 // selection (they are latency-bound, so the copies cost no time), resolve the
 // slots of their own tiles only, attend them (attend_part) and write that
-// part of the slot table; part 0 writes the selection's other outputs.
+// part of the slot table; the selection's other outputs are split over the
+// parts.
 template <int CT, int DT, int OWN, bool FUSED = false>
 __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, const int part = 0,
                                             const int parts = 1) {
@@ -129,7 +130,6 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
   // fused: the window tokens' communities first, then the selection arrays (later the attention buffers)
   int* slot_lds = reinterpret_cast<int*>(dyn_all);
   unsigned char* dyn = dyn_all + (FUSED ? fused_slot_bytes(a.ws.slot_capacity) : 0);
-  const bool writer = !FUSED || part == 0;  // writes the selection's global outputs
   uint16_t* key16 = reinterpret_cast<uint16_t*>(dyn);  // masked fp16 score bits of every scored community
   const int dcap = a.ws.descriptor_capacity;
   int* desc_comm = reinterpret_cast<int*>(dyn + (size_t)((C + 7) & ~7) * 2);
@@ -720,41 +720,47 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
     }
   }
   // ---- outputs that nothing in this kernel reads back --------------------------
+  // (fused: split over the head's parts, so no part carries them all)
   CKV_STAMP(rh == 0 && part == 0, 11);
-  if (writer) {
-  if (tid == 0) {
-    a.ws.descriptor_counts[rh] = n_desc;
-    a.ws.selected_counts[rh] = sel_count;
-  }
-  for (int i = tid; i < n_desc; i += SELECT_THREADS) {
-    a.ws.communities[(int64_t)rh * dcap + i] = desc_comm[i];
-    a.ws.cumulative_ends[(int64_t)rh * dcap + i] = desc_end[i];
-  }
-  for (int t = tid; t < a.ws.budget_tiles; t += SELECT_THREADS) {
-    const int off = max(t * TILE - ns, 0);
-    int lo = 0, hi = n_desc;
-    while (lo < hi) {
-      const int mid = (lo + hi) >> 1;
-      if (desc_end[mid] <= off) lo = mid + 1; else hi = mid;
+  {
+    const int wp = FUSED ? part : 0, wn = FUSED ? parts : 1;
+    const int stride = wn * SELECT_THREADS;
+    if (tid == 0 && wp == 0) {
+      a.ws.descriptor_counts[rh] = n_desc;
+      a.ws.selected_counts[rh] = sel_count;
     }
-    a.ws.tile_descriptors[(int64_t)rh * a.ws.budget_tiles + t] = max(0, min(lo, n_desc - 1));
-  }
+    for (int i = wp * SELECT_THREADS + tid; i < n_desc; i += stride) {
+      a.ws.communities[(int64_t)rh * dcap + i] = desc_comm[i];
+      a.ws.cumulative_ends[(int64_t)rh * dcap + i] = desc_end[i];
+    }
+    for (int t = wp * SELECT_THREADS + tid; t < a.ws.budget_tiles; t += stride) {
+      const int off = max(t * TILE - ns, 0);
+      int lo = 0, hi = n_desc;
+      while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (desc_end[mid] <= off) lo = mid + 1; else hi = mid;
+      }
+      a.ws.tile_descriptors[(int64_t)rh * a.ws.budget_tiles + t] = max(0, min(lo, n_desc - 1));
+    }
+    if (tid % wn == wp) {
 #pragma unroll
-  for (int k = 0; k < OWN; ++k) {
-    const int c = c0 + k;
-    if (c < nscore) {
-      const bool live = c < count && o_size[k] > 0;
-      const uint32_t key = o_key[k];
-      const uint16_t bits = live ? (uint16_t)((key & 0x8000u) ? (key ^ 0x8000u) : (key ^ 0xffffu)) : (uint16_t)0xfc00u;
-      a.ws.scores[(int64_t)rh * C + c] = bits;
+      for (int k = 0; k < OWN; ++k) {
+        const int c = c0 + k;
+        if (c < nscore) {
+          const bool live = c < count && o_size[k] > 0;
+          const uint32_t key = o_key[k];
+          const uint16_t bits =
+              live ? (uint16_t)((key & 0x8000u) ? (key ^ 0x8000u) : (key ^ 0xffffu)) : (uint16_t)0xfc00u;
+          a.ws.scores[(int64_t)rh * C + c] = bits;
+        }
+      }
+    }
+    if (nearest_mode && tid == 0 && wp == wn - 1) {
+      uint64_t m = ~0ull;
+      for (int w = 0; w < WAVES; ++w) m = near_s[w] < m ? near_s[w] : m;
+      a.ws.nearest[rh] = (m == ~0ull) ? -1 : (int)(m & 0xffffffffu);
     }
   }
-  if (nearest_mode && tid == 0) {
-    uint64_t m = ~0ull;
-    for (int w = 0; w < WAVES; ++w) m = near_s[w] < m ? near_s[w] : m;
-    a.ws.nearest[rh] = (m == ~0ull) ? -1 : (int)(m & 0xffffffffu);
-  }
-  }  // writer
   CKV_STAMP(rh == 0 && part == 0, 5);
   if constexpr (FUSED) {
     __syncthreads();  // the selection arrays are dead from here
