@@ -255,16 +255,16 @@ __device__ inline void attend_part(const DecodeArgs& a, const int rh, const int 
   }
   __syncthreads();
   CKV_STAMP(rh == 0 && part == 0, 20);
-  // Combine the waves into this part's split partial.
+  // Combine the tile waves into this part's split partial (the other waves hold no tile).
   for (int i = tid; i < G * D; i += 64 * W) {
     const int g = i >> 7;
     const int d = i & (D - 1);
     float M = NEG_INF;
 #pragma unroll
-    for (int w = 0; w < W; ++w) M = fmax_exact(M, wm_s[w * CKV_MAX_GROUP + g]);
+    for (int w = 0; w < TP; ++w) M = fmax_exact(M, wm_s[w * CKV_MAX_GROUP + g]);
     float acc = 0.0f;
 #pragma unroll
-    for (int w = 0; w < W; ++w) {
+    for (int w = 0; w < TP; ++w) {
       const float mw = wm_s[w * CKV_MAX_GROUP + g];
       if (mw != NEG_INF) {
         const float* ow = reinterpret_cast<const float*>(v_all + w * (V_HALF_ROWS * D));
@@ -276,10 +276,10 @@ __device__ inline void attend_part(const DecodeArgs& a, const int rh, const int 
   if (tid < G) {
     float M = NEG_INF;
 #pragma unroll
-    for (int w = 0; w < W; ++w) M = fmax_exact(M, wm_s[w * CKV_MAX_GROUP + tid]);
+    for (int w = 0; w < TP; ++w) M = fmax_exact(M, wm_s[w * CKV_MAX_GROUP + tid]);
     float l = 0.0f;
 #pragma unroll
-    for (int w = 0; w < W; ++w) {
+    for (int w = 0; w < TP; ++w) {
       const float mw = wm_s[w * CKV_MAX_GROUP + tid];
       if (mw != NEG_INF) l = l + wl_s[w * CKV_MAX_GROUP + tid] * __expf(mw - M);
     }
