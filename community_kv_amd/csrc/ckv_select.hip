@@ -219,39 +219,6 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
     key_v = load_elem<DT>(a.kv.key, kvh * a.kv.head_stride + cp * a.kv.token_stride + (tid & (D - 1)));
   }
 
-  // ---- R2: tail-chunk fields; communities of the window tokens ---------------
-  int wcomm[WIN_PER_THREAD];
-#pragma unroll
-  for (int h = 0; h < WIN_PER_THREAD; ++h) wcomm[h] = -1;
-  if (materialise) {
-    if (cpg > 0) {
-#pragma unroll
-      for (int k = 0; k < OWN; ++k) {
-        const int t = min(max(o_tl[k], 0), cpg - 1);
-        o_ts[k] = gload_i32(a.dl.chunk_start + cb + t);
-        o_tn[k] = gload_i32(a.dl.chunk_size + cb + t);
-      }
-    }
-    if (W > 0) {
-      const int32_t* tcomm = a.st.token_communities + (int64_t)graph * a.st.token_capacity;
-#pragma unroll
-      for (int h = 0; h < WIN_PER_THREAD; ++h) {
-        const int64_t p = (int64_t)cur - W + tid + h * SELECT_THREADS;
-        wcomm[h] = gload_i32(tcomm + (p < 0 ? 0 : (p >= a.st.token_capacity ? a.st.token_capacity - 1 : p)));
-      }
-    }
-  }
-  // masks of the R0/R1 fields (R2 fields stay raw until used: masking them here would wait for R2)
-#pragma unroll
-  for (int k = 0; k < OWN; ++k) {
-    const int c = c0 + k;
-    if (c >= nscore) o_size[k] = 0;
-    if (c >= count) {
-      o_lo[k] = 0;
-      o_dc[k] = 0;
-      o_tl[k] = -1;
-    }
-  }
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const int e = 2 * (tid + h * SELECT_THREADS);
@@ -261,7 +228,7 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
     }
   }
   if (tid < ns) sink_s[tid] = sink_v;
-  if (tid < D) key_s[tid] = (cur >= 0 && cur < a.kv.capacity) ? key_v : 0.0f;
+  if (nearest_mode && tid < D) key_s[tid] = (cur >= 0 && cur < a.kv.capacity) ? key_v : 0.0f;
   hist[tid & 255] = 0;
   if (tid == 0) s_max_idx = -1;
   __syncthreads();  // q_s, key_s, sink_s, hist
@@ -376,6 +343,46 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
   __syncthreads();  // key16, near_s
   CKV_STAMP(rh == 0 && part == 0, 1);
 
+  // ---- R2: tail-chunk fields; communities of the window tokens ---------------
+  // Issued after the scoring: their addresses need the R1 fields and the
+  // current position, and nothing before the compaction reads them, so the
+  // scoring starts as soon as the R0 data is in.  Every earlier load has
+  // landed by now (the R1 fields long ago, the last prefetches are cache
+  // hits); waiting for them here keeps the waits for older loads after the
+  // conditional R2 issue from also waiting for R2.
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  int wcomm[WIN_PER_THREAD];
+#pragma unroll
+  for (int h = 0; h < WIN_PER_THREAD; ++h) wcomm[h] = -1;
+  if (materialise) {
+    if (cpg > 0) {
+#pragma unroll
+      for (int k = 0; k < OWN; ++k) {
+        const int t = min(max(o_tl[k], 0), cpg - 1);
+        o_ts[k] = gload_i32(a.dl.chunk_start + cb + t);
+        o_tn[k] = gload_i32(a.dl.chunk_size + cb + t);
+      }
+    }
+    if (W > 0) {
+      const int32_t* tcomm = a.st.token_communities + (int64_t)graph * a.st.token_capacity;
+#pragma unroll
+      for (int h = 0; h < WIN_PER_THREAD; ++h) {
+        const int64_t p = (int64_t)cur - W + tid + h * SELECT_THREADS;
+        wcomm[h] = gload_i32(tcomm + (p < 0 ? 0 : (p >= a.st.token_capacity ? a.st.token_capacity - 1 : p)));
+      }
+    }
+  }
+  // masks of the R0/R1 fields (R2 fields stay raw until used: masking them here would wait for R2)
+#pragma unroll
+  for (int k = 0; k < OWN; ++k) {
+    const int c = c0 + k;
+    if (c >= nscore) o_size[k] = 0;
+    if (c >= count) {
+      o_lo[k] = 0;
+      o_dc[k] = 0;
+      o_tl[k] = -1;
+    }
+  }
   // ---- exact weighted selection ---------------------------------------------
   const bool budget_mode = a.cfg.selection_mode == CKV_SELECT_BUDGET;
   const int sel_slots = a.cfg.max_selected;
