@@ -144,7 +144,9 @@ class StateBuildArgs(ctypes.Structure):
                 ("retrieval_heads", _i32), ("kv_heads", _i32), ("key_dtype", _i32), ("centroid_dtype", _i32),
                 ("max_communities", _i32), ("community_capacity", _i32), ("token_capacity", _i32),
                 ("member_offsets", _p), ("member_positions", _p), ("centroids", _p), ("community_sizes", _p),
-                ("community_weight", _p), ("total_weight", _p), ("token_communities", _p), ("workspace", _p)]
+                ("community_weight", _p), ("total_weight", _p), ("token_communities", _p), ("workspace", _p),
+                ("topk_indices", _p), ("topk_scores", _p), ("topk_heads", _i32), ("topk_rows", _i32),
+                ("topk_kappa", _i32), ("topk_group", _i32), ("topk_row0", _i32), ("lam", _f32)]
 
 
 def build(verbose: bool = False) -> str:

@@ -22,7 +22,8 @@
 //   centroid_kernel       per (retrieval head, community): block sums in order,
 //                         mean -> clamp -> E4M3 / f32
 //   token_table_kernel    labels -> token_communities (-1 past the prompt)
-//   weight_zero_kernel + edge_weight_kernel   modularity weights (when edges are given)
+//   weight_zero_kernel + edge_weight_kernel   modularity weights from an edge list, or
+//   weight_zero_kernel + topk_weight_kernel   the same weights from the prefill top-k edges
 #include <hip/hip_runtime.h>
 
 #include <stdint.h>
@@ -381,14 +382,14 @@ __global__ void weight_zero_kernel(float* __restrict__ weight, int64_t n, float*
 constexpr int EDGES_PER_WG = 8192;
 
 __global__ __launch_bounds__(EDGE_THREADS) void edge_weight_kernel(
-    const int32_t* __restrict__ labels, int seq_len, int graphs, int capacity, const int32_t* __restrict__ src,
-    const int32_t* __restrict__ dst, const float* __restrict__ w, int64_t edges, float* __restrict__ weight,
-    float* __restrict__ total) {
-  extern __shared__ float w_s[];
+    const int32_t* __restrict__ labels, int seq_len, int graphs, int capacity, int lds_n,
+    const int32_t* __restrict__ src, const int32_t* __restrict__ dst, const float* __restrict__ w, int64_t edges,
+    float* __restrict__ weight, float* __restrict__ total) {
+  extern __shared__ float w_s[];  // communities [0, lds_n) of the first edge's graph
   const int64_t e0 = (int64_t)blockIdx.x * EDGES_PER_WG;
   const int64_t e1 = min(edges, e0 + EDGES_PER_WG);
   const int g0 = src[e0] / seq_len;
-  for (int c = threadIdx.x; c < capacity; c += EDGE_THREADS) w_s[c] = 0.0f;
+  for (int c = threadIdx.x; c < lds_n; c += EDGE_THREADS) w_s[c] = 0.0f;
   __syncthreads();
   float mine = 0.0f;
   for (int64_t e = e0 + threadIdx.x; e < e1; e += EDGE_THREADS) {
@@ -399,8 +400,10 @@ __global__ __launch_bounds__(EDGE_THREADS) void edge_weight_kernel(
     const int sc = labels[(int64_t)g * seq_len + s % seq_len];
     const int dc = labels[(int64_t)g * seq_len + d % seq_len];
     if (g == g0) {
-      if (sc >= 0 && sc < capacity) atomicAdd(w_s + sc, x);
-      if (dc >= 0 && dc < capacity) atomicAdd(w_s + dc, x);
+      if (sc >= 0 && sc < lds_n) atomicAdd(w_s + sc, x);
+      else if (sc >= lds_n && sc < capacity) atomicAdd(weight + (int64_t)g * capacity + sc, x);
+      if (dc >= 0 && dc < lds_n) atomicAdd(w_s + dc, x);
+      else if (dc >= lds_n && dc < capacity) atomicAdd(weight + (int64_t)g * capacity + dc, x);
       mine = mine + 2.0f * x;
     } else {
       if (sc >= 0 && sc < capacity) atomicAdd(weight + (int64_t)g * capacity + sc, x);
@@ -413,7 +416,7 @@ __global__ __launch_bounds__(EDGE_THREADS) void edge_weight_kernel(
   if ((threadIdx.x & 63) == 0) s_part[threadIdx.x >> 6] = mine;
   __syncthreads();
   if (g0 >= 0 && g0 < graphs) {
-    for (int c = threadIdx.x; c < capacity; c += EDGE_THREADS) {
+    for (int c = threadIdx.x; c < lds_n; c += EDGE_THREADS) {
       const float v = w_s[c];
       if (v != 0.0f) atomicAdd(weight + (int64_t)g0 * capacity + c, v);
     }
@@ -422,6 +425,79 @@ __global__ __launch_bounds__(EDGE_THREADS) void edge_weight_kernel(
       for (int i = 0; i < EDGE_THREADS / 64; ++i) t = t + s_part[i];
       atomicAdd(total + g0, t);
     }
+  }
+}
+
+// Modularity weights straight from the prefill top-k edges: one thread per
+// (query head, row).  With the row's valid columns k (score p_k), S = sum p_k:
+// the direct edges (position, column k) weigh lam/2 p_k, the co-occurrence
+// edges (k, l), k <= l, weigh (1 - lam) p_k p_l.  Column k's community gains
+// lam/2 p_k + (1 - lam) p_k (S + p_k) (its own pair k = k counts at both
+// ends), the row position's community gains lam/2 S, and the graph's total
+// 2 x (edge weights) = lam S + (1 - lam) (S^2 + sum p_k^2).  A workgroup's
+// rows share one head, hence one graph: weights gather in LDS first.
+constexpr int TOPK_ROWS_PER_WG = 256;
+
+__global__ __launch_bounds__(TOPK_ROWS_PER_WG) void topk_weight_kernel(
+    const int32_t* __restrict__ labels, int seq_len, int capacity, int lds_n, const int32_t* __restrict__ idx,
+    const float* __restrict__ sc, int rows, int kappa, int group, int row0, float lam, float* __restrict__ weight,
+    float* __restrict__ total) {
+  extern __shared__ float w_s[];  // communities [0, lds_n)
+  const int h = blockIdx.y;
+  const int g = h / group;
+  for (int c = threadIdx.x; c < lds_n; c += TOPK_ROWS_PER_WG) w_s[c] = 0.0f;
+  __syncthreads();
+  const int r = blockIdx.x * TOPK_ROWS_PER_WG + threadIdx.x;
+  const int32_t* lab = labels + (int64_t)g * seq_len;
+  float mine = 0.0f;
+  if (r < rows) {
+    const int32_t* ir = idx + ((int64_t)h * rows + r) * kappa;
+    const float* sr = sc + ((int64_t)h * rows + r) * kappa;
+    int col[16];
+    float p[16];
+    float s = 0.0f, s2 = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      col[k] = k < kappa ? ir[k] : -1;
+      p[k] = k < kappa ? sr[k] : 0.0f;
+    }
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      if (col[k] >= 0 && col[k] < seq_len) {
+        s = s + p[k];
+        s2 = s2 + p[k] * p[k];
+      }
+    }
+    const float half = 0.5f * lam, co = 1.0f - lam;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      if (col[k] >= 0 && col[k] < seq_len) {
+        const int c = lab[col[k]];
+        const float v = half * p[k] + co * (p[k] * (s + p[k]));
+        if (c >= 0 && c < lds_n) atomicAdd(w_s + c, v);
+        else if (c >= lds_n && c < capacity) atomicAdd(weight + (int64_t)g * capacity + c, v);
+      }
+    }
+    const int pos = row0 + r;
+    if (pos >= 0 && pos < seq_len) {
+      const int c = lab[pos];
+      if (c >= 0 && c < lds_n) atomicAdd(w_s + c, half * s);
+      else if (c >= lds_n && c < capacity) atomicAdd(weight + (int64_t)g * capacity + c, half * s);
+    }
+    mine = lam * s + co * (s * s + s2);
+  }
+  __shared__ float s_part[TOPK_ROWS_PER_WG / 64];
+  mine = wave_sum_tree(mine);
+  if ((threadIdx.x & 63) == 0) s_part[threadIdx.x >> 6] = mine;
+  __syncthreads();
+  for (int c = threadIdx.x; c < lds_n; c += TOPK_ROWS_PER_WG) {
+    const float v = w_s[c];
+    if (v != 0.0f) atomicAdd(weight + (int64_t)g * capacity + c, v);
+  }
+  if (threadIdx.x == 0) {
+    float t = 0.0f;
+    for (int i = 0; i < TOPK_ROWS_PER_WG / 64; ++i) t = t + s_part[i];
+    atomicAdd(total + g, t);
   }
 }
 
@@ -475,6 +551,14 @@ extern "C" int ckv_build_layer_state(const ckv_state_build_args* a, void* stream
     return ckv_internal::set_error(CKV_E_INVALID, "edges need src, dst and weight");
   if (a->edges > 0 && (!a->community_weight || !a->total_weight))
     return ckv_internal::set_error(CKV_E_INVALID, "edges need community_weight and total_weight outputs");
+  if (a->topk_indices) {
+    if (a->edges > 0) return ckv_internal::set_error(CKV_E_INVALID, "give either an edge list or top-k edges");
+    if (!a->topk_scores || !a->community_weight || !a->total_weight)
+      return ckv_internal::set_error(CKV_E_INVALID, "top-k edges need scores and the weight outputs");
+    if (a->topk_kappa < 1 || a->topk_kappa > 16 || a->topk_heads <= 0 || a->topk_rows < 0 || a->topk_group <= 0 ||
+        a->topk_heads > a->topk_group * a->graphs)
+      return ckv_internal::set_error(CKV_E_INVALID, "bad top-k edge shape (kappa 1..16, heads <= group * graphs)");
+  }
   const hipStream_t s = (hipStream_t)stream;
   const int maxc = a->max_communities;
   const int chunk_len = state_chunk(a->seq_len, a->num_sink);
@@ -512,10 +596,17 @@ extern "C" int ckv_build_layer_state(const ckv_state_build_args* a, void* stream
     const int64_t nz = nw > a->graphs ? nw : a->graphs;
     hipLaunchKernelGGL(weight_zero_kernel, dim3((unsigned)((nz + 255) / 256)), dim3(256), 0, s, a->community_weight,
                        nw, a->total_weight, a->graphs);
+    if (a->topk_indices && a->topk_rows > 0) {
+      hipLaunchKernelGGL(topk_weight_kernel,
+                         dim3((a->topk_rows + TOPK_ROWS_PER_WG - 1) / TOPK_ROWS_PER_WG, a->topk_heads),
+                         dim3(TOPK_ROWS_PER_WG), (size_t)maxc * sizeof(float), s, a->labels,
+                         a->seq_len, a->community_capacity, maxc, a->topk_indices, a->topk_scores, a->topk_rows,
+                         a->topk_kappa, a->topk_group, a->topk_row0, a->lam, a->community_weight, a->total_weight);
+    }
     if (a->edges > 0) {
       hipLaunchKernelGGL(edge_weight_kernel, dim3((unsigned)((a->edges + EDGES_PER_WG - 1) / EDGES_PER_WG)),
-                         dim3(EDGE_THREADS), (size_t)a->community_capacity * sizeof(float), s, a->labels, a->seq_len, a->graphs, a->community_capacity,
-                         a->edge_src, a->edge_dst, a->edge_weight, a->edges, a->community_weight, a->total_weight);
+                         dim3(EDGE_THREADS), (size_t)maxc * sizeof(float), s, a->labels, a->seq_len, a->graphs,
+                         a->community_capacity, maxc, a->edge_src, a->edge_dst, a->edge_weight, a->edges, a->community_weight, a->total_weight);
     }
   }
   return launch_check();

@@ -20,6 +20,20 @@ from community_kv_amd import _native as nat
 
 
 @dataclass
+class TopkEdges:
+    """Prefill top-k edges as the partitioner receives them: ``indices`` /
+    ``scores`` ``[heads, rows, kappa]`` with heads grouped by graph (``group``
+    query heads per graph); row r is position ``row0 + r``.  The state build
+    derives the modularity weights of the reference's ``build_adjacency``
+    graph (partition.py:168-249, weight ``lam``) from them directly."""
+    indices: torch.Tensor
+    scores: torch.Tensor
+    row0: int
+    group: int
+    lam: float
+
+
+@dataclass
 class LayerStateTensors:
     community_counts: torch.Tensor   # int32 [graphs]
     member_offsets: torch.Tensor     # int32 [graphs, maxc + 1]
@@ -52,8 +66,10 @@ class StateBuild:
     def __init__(self, community_ids: torch.Tensor, keys: torch.Tensor, *, retrieval_to_graph: torch.Tensor,
                  retrieval_to_kv: torch.Tensor, num_sink: int, max_decode_tokens: int, fp8: bool = True,
                  edges: tuple[torch.Tensor, torch.Tensor, torch.Tensor] | None = None,
-                 token_capacity: int | None = None):
+                 token_capacity: int | None = None, topk_edges: "TopkEdges | None" = None):
         device = nat.require_device(community_ids, keys, retrieval_to_graph, retrieval_to_kv)
+        if edges is not None and topk_edges is not None:
+            raise ValueError("give either an edge list or top-k edges")
         if keys.ndim != 3 or keys.shape[-1] != nat.HEAD_DIM or keys.stride(-1) != 1:
             raise ValueError("keys must be [KV heads, sequence, 128] with unit dim stride")
         graphs, seq_len = community_ids.shape
@@ -101,6 +117,20 @@ class StateBuild:
                           edges[2].to(device=device, dtype=torch.float32).contiguous())
             n_edges = self.edges[0].numel()
         src, dst, w = self.edges if self.edges is not None else (None, None, None)
+        self.topk = None
+        tk = dict(topk_indices=None, topk_scores=None, topk_heads=0, topk_rows=0, topk_kappa=0, topk_group=1,
+                  topk_row0=0, lam=0.0)
+        if topk_edges is not None:
+            ti = topk_edges.indices.to(device=device, dtype=torch.int32).contiguous()
+            ts = topk_edges.scores.to(device=device, dtype=torch.float32).contiguous()
+            if ti.ndim != 3 or ts.shape != ti.shape or ti.shape[-1] > 16:
+                raise ValueError("top-k edges must be [heads, rows, kappa <= 16] indices with matching scores")
+            if ti.shape[0] % graphs or ti.shape[0] // graphs != topk_edges.group:
+                raise ValueError("top-k heads must be graphs x group, grouped by graph")
+            self.topk = (ti, ts)
+            tk = dict(topk_indices=nat.ptr(ti), topk_scores=nat.ptr(ts), topk_heads=ti.shape[0],
+                      topk_rows=ti.shape[1], topk_kappa=ti.shape[2], topk_group=topk_edges.group,
+                      topk_row0=topk_edges.row0, lam=float(topk_edges.lam))
         self.maps = (retrieval_to_graph.contiguous(), retrieval_to_kv.contiguous())
         o = self.out
         self.args = nat.StateBuildArgs(
@@ -114,7 +144,7 @@ class StateBuild:
             member_offsets=nat.ptr(o.member_offsets), member_positions=nat.ptr(o.member_positions),
             centroids=nat.ptr(o.centroids), community_sizes=nat.ptr(o.community_sizes),
             community_weight=nat.ptr(o.community_weight), total_weight=nat.ptr(o.total_weight),
-            token_communities=nat.ptr(o.token_communities), workspace=nat.ptr(self.workspace))
+            token_communities=nat.ptr(o.token_communities), workspace=nat.ptr(self.workspace), **tk)
 
     def run(self) -> LayerStateTensors:
         nat.check(nat.lib().ckv_build_layer_state(self.args, nat.stream_handle(self.device)))
@@ -124,7 +154,7 @@ class StateBuild:
 def build_layer_state(community_ids: torch.Tensor, keys: torch.Tensor, *, retrieval_to_graph: torch.Tensor,
                       retrieval_to_kv: torch.Tensor, num_sink: int, max_decode_tokens: int, fp8: bool = True,
                       edges: tuple[torch.Tensor, torch.Tensor, torch.Tensor] | None = None,
-                      token_capacity: int | None = None) -> LayerStateTensors:
+                      token_capacity: int | None = None, topk_edges: "TopkEdges | None" = None) -> LayerStateTensors:
     """Every prefill state tensor of one layer from labels ``[graphs, S]`` and
     keys ``[Hkv, S, 128]`` (bf16 or f32, token stride may exceed 128).  Reads
     the community counts back once to size the outputs, as the reference
@@ -133,7 +163,7 @@ def build_layer_state(community_ids: torch.Tensor, keys: torch.Tensor, *, retrie
     them before the launches run.)"""
     return StateBuild(community_ids, keys, retrieval_to_graph=retrieval_to_graph, retrieval_to_kv=retrieval_to_kv,
                       num_sink=num_sink, max_decode_tokens=max_decode_tokens, fp8=fp8, edges=edges,
-                      token_capacity=token_capacity).run()
+                      token_capacity=token_capacity, topk_edges=topk_edges).run()
 
 
-__all__ = ["LayerStateTensors", "StateBuild", "build_layer_state", "label_counts"]
+__all__ = ["LayerStateTensors", "StateBuild", "TopkEdges", "build_layer_state", "label_counts"]

@@ -11,6 +11,8 @@ label provider.
 
 from __future__ import annotations
 
+from typing import Any
+
 import math
 from dataclasses import dataclass, fields, replace
 
@@ -179,9 +181,12 @@ def build_layer_from_labels(*, layer_idx: int, community_ids: torch.Tensor, keys
                             num_sink: int, max_decode_tokens: int, query_heads: int,
                             aggregation: GraphAggregation = GraphAggregation.PER_QUERY_HEAD,
                             edges: tuple[torch.Tensor, torch.Tensor, torch.Tensor] | None = None,
-                            fp8: bool = True) -> PartitionedLayer:
+                            fp8: bool = True, topk_edges: Any = None) -> PartitionedLayer:
     """Everything ``build_partitioned_layer`` (partition.py:538-618) produces
-    after Leiden, from given dense labels ``community_ids [graphs, S]``."""
+    after Leiden, from given dense labels ``community_ids [graphs, S]``.  The
+    modularity weights come from ``edges`` (a coalesced edge list) or from
+    ``topk_edges`` (a ``graph.kernels.state_build.TopkEdges``: the prefill
+    top-k edges, device tensors only), or are zero."""
     if max_decode_tokens <= 0:
         raise ValueError("max_decode_tokens must be positive")
     kv_heads, seq_len, _ = keys.shape
@@ -195,7 +200,7 @@ def build_layer_from_labels(*, layer_idx: int, community_ids: torch.Tensor, keys
         from community_kv_amd.graph.kernels.state_build import build_layer_state
 
         st = build_layer_state(ids, keys, retrieval_to_graph=to_graph, retrieval_to_kv=to_kv, num_sink=num_sink,
-                               max_decode_tokens=max_decode_tokens, fp8=fp8, edges=edges)
+                               max_decode_tokens=max_decode_tokens, fp8=fp8, edges=edges, topk_edges=topk_edges)
         return PartitionedLayer(layer_idx=layer_idx, prefill_seq_len=seq_len, aggregation=aggregation,
                                 query_heads=query_heads, kv_heads=kv_heads, retrieval_to_graph=to_graph,
                                 retrieval_to_kv=to_kv, member_offsets=st.member_offsets,
@@ -203,6 +208,8 @@ def build_layer_from_labels(*, layer_idx: int, community_ids: torch.Tensor, keys
                                 centroids=st.centroids, community_sizes=st.community_sizes,
                                 community_weight=st.community_weight, total_weight=st.total_weight,
                                 token_communities=st.token_communities)
+    if topk_edges is not None:
+        raise ValueError("top-k edges are taken by the device state build only; pass a coalesced edge list")
     counts = (ids[:, num_sink:].amax(dim=1) + 1).to(torch.int32)
     centroids, sizes = compute_centroids(ids, counts, keys, retrieval_to_graph=to_graph, retrieval_to_kv=to_kv,
                                          num_sink=num_sink, max_decode_tokens=max_decode_tokens, fp8=fp8)

@@ -17,6 +17,7 @@ from typing import Any, Callable
 import torch
 
 from community_kv_amd.config import CommunityKVConfig, GraphAggregation, PartitionConfig
+from community_kv_amd.graph.kernels.state_build import TopkEdges
 from community_kv_amd.graph.partition import PartitionedLayer, build_adjacency, build_layer_from_labels
 
 
@@ -48,24 +49,28 @@ class PartitionRuntime:
         cfg = self.algorithm
         aggregation = GraphAggregation(cfg.aggregation)
         labels = self.label_provider(layer_idx, keys, topk_indices, topk_scores)
-        edges = None
+        edges = topk_edges = None
         if topk_indices is not None and topk_indices.numel():
             seq_len = keys.shape[1]
             heads, rows, kappa = topk_indices.shape
-            kv_heads = keys.shape[0]
             graphs = labels.shape[0]
             group = heads // graphs
-            base = torch.arange(kappa - 1 + cfg.num_sink, kappa - 1 + cfg.num_sink + rows,
-                                device=topk_indices.device)
-            idx = topk_indices.reshape(graphs, group * rows, kappa)
-            sc = topk_scores.reshape(graphs, group * rows, kappa)
-            pos = base.repeat(group).unsqueeze(0).expand(graphs, -1)
-            edges = build_adjacency(idx, sc, pos, seq_len=seq_len, lam=cfg.lam)
-            del kv_heads
+            row0 = kappa - 1 + cfg.num_sink
+            if keys.device.type == "cuda":
+                # the device state build takes the top-k edges as they are (no
+                # edge list to build, sort and coalesce: Leiden is not run here)
+                topk_edges = TopkEdges(indices=topk_indices, scores=topk_scores, row0=row0, group=group,
+                                       lam=cfg.lam)
+            else:
+                base = torch.arange(row0, row0 + rows, device=topk_indices.device)
+                idx = topk_indices.reshape(graphs, group * rows, kappa)
+                sc = topk_scores.reshape(graphs, group * rows, kappa)
+                pos = base.repeat(group).unsqueeze(0).expand(graphs, -1)
+                edges = build_adjacency(idx, sc, pos, seq_len=seq_len, lam=cfg.lam)
         self._results[layer_idx] = build_layer_from_labels(
             layer_idx=layer_idx, community_ids=labels, keys=keys, num_sink=cfg.num_sink,
             max_decode_tokens=max_decode_tokens, query_heads=topk_indices.shape[0], aggregation=aggregation,
-            edges=edges)
+            edges=edges, topk_edges=topk_edges)
 
     def wait(self, callback: Callable[[PartitionedLayer], Any]) -> None:
         for idx in sorted(self._results):

@@ -265,6 +265,22 @@ typedef struct ckv_state_build_args {
   float* total_weight;
   int32_t* token_communities;
   int32_t* workspace;
+  /* Instead of an edge list (then edges == 0): the prefill top-k edges
+   * themselves.  Row r of query head h is position topk_row0 + r of graph
+   * h / topk_group.  The weights equal those of the reference's
+   * build_adjacency (graph/partition.py:168-249: direct edges lam/2 * p,
+   * co-occurrence edges (1 - lam) * p_k * p_l for columns k <= l, columns
+   * outside [0, seq_len) dropped) followed by init_modularity_state; each row
+   * adds its share in closed form, so no edge list is built, sorted or
+   * coalesced.  topk_indices == NULL disables this. */
+  const int32_t* topk_indices;        /* [topk_heads][topk_rows][topk_kappa] */
+  const float* topk_scores;           /* same shape */
+  int32_t topk_heads;
+  int32_t topk_rows;
+  int32_t topk_kappa;                 /* <= 16 */
+  int32_t topk_group;                 /* query heads per graph */
+  int32_t topk_row0;
+  float lam;
 } ckv_state_build_args;
 
 size_t ckv_state_workspace_bytes(int32_t graphs, int32_t retrieval_heads, int32_t seq_len, int32_t num_sink,

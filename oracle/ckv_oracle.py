@@ -145,6 +145,40 @@ def build_member_csr(community_ids, community_counts, *, num_sink):
     return offsets, positions
 
 
+def build_adjacency(topk_indices, topk_scores, query_positions, *, seq_len, lam):
+    """Restates ``build_adjacency`` (graph/partition.py:168-249).
+
+    ``topk_indices`` / ``topk_scores`` ``[graphs, rows, kappa]``; row r of graph
+    g is position ``query_positions[g, r]``.  Direct edges (position, column)
+    for columns in [0, seq_len), weighted ``score * (lam / 2)``; when lam < 1,
+    co-occurrence edges between columns k <= l of a row (both valid) weighted
+    ``(score_k * score_l) * (1 - lam)``.  Endpoints are graph * seq_len +
+    position, stored as (min, max), coalesced (weights summed in edge order)
+    and sorted by (src, dst).  Returns (src, dst, weight) int32/int32/f32."""
+    idx = np.asarray(topk_indices, np.int64)
+    sc = np.asarray(topk_scores, np.float32)
+    graphs, rows, kappa = idx.shape
+    total = graphs * seq_len
+    off = (np.arange(graphs, dtype=np.int64) * seq_len)[:, None]
+    src = np.broadcast_to((np.asarray(query_positions, np.int64) + off)[..., None], idx.shape)
+    dst = idx + off[..., None]
+    ok = (idx >= 0) & (idx < seq_len)
+    srcs, dsts, ws = [src[ok]], [dst[ok]], [(sc[ok] * F32(lam / 2.0)).astype(np.float32)]
+    if lam < 1.0:
+        r, c = np.triu_indices(kappa)
+        ci, cj = idx[..., r], idx[..., c]
+        ok2 = (ci >= 0) & (ci < seq_len) & (cj >= 0) & (cj < seq_len)
+        srcs.append((ci + off[..., None])[ok2])
+        dsts.append((cj + off[..., None])[ok2])
+        ws.append(((sc[..., r] * sc[..., c]).astype(np.float32)[ok2] * F32(1.0 - lam)).astype(np.float32))
+    s_all, d_all = np.concatenate(srcs), np.concatenate(dsts)
+    keys = np.minimum(s_all, d_all) * total + np.maximum(s_all, d_all)
+    uniq, inv = np.unique(keys, return_inverse=True)
+    w = np.zeros(len(uniq), np.float32)
+    np.add.at(w, inv.reshape(-1), np.concatenate(ws))
+    return (uniq // total).astype(np.int32), (uniq % total).astype(np.int32), w
+
+
 def init_modularity_state(community_ids, edge_src, edge_dst, edge_weight, *,
                           community_capacity, seq_len):
     """Restates ``init_modularity_state`` (graph/partition.py:495-535)."""

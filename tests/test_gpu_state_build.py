@@ -106,3 +106,42 @@ def test_label_counts_flags_negative_labels(device):
     tg = torch.arange(2, dtype=torch.int32, device=device)
     with pytest.raises(ValueError, match="nonnegative"):
         build_layer_state(ids, keys, retrieval_to_graph=tg, retrieval_to_kv=tg, num_sink=1, max_decode_tokens=4)
+
+
+@pytest.mark.parametrize("lam,kappa", [(0.5, 8), (1.0, 8), (0.3, 16)])
+def test_state_build_topk_edges_match_coalesced_graph(device, lam, kappa):
+    """Modularity weights from the prefill top-k edges directly must equal
+    those of the reference's graph (build_adjacency + init_modularity_state)."""
+    from community_kv_amd.graph.kernels.state_build import TopkEdges
+
+    print(f"state build top-k edges lam={lam} kappa={kappa}", flush=True)
+    rng = np.random.default_rng(int(lam * 10) + kappa)
+    graphs, group, seq_len, num_sink, maxc = 2, 4, 3000, 10, 120
+    ids = _labels(rng, graphs, seq_len, maxc, num_sink)
+    row0 = num_sink + kappa - 1
+    rows = seq_len - row0
+    heads = graphs * group
+    idx = rng.integers(num_sink, seq_len, size=(heads, rows, kappa)).astype(np.int32)
+    idx[rng.random(idx.shape) < 0.05] = -1                 # dropped columns
+    idx[rng.random(idx.shape) < 0.02] = seq_len + 3        # outside the sequence
+    sc = rng.random((heads, rows, kappa)).astype(np.float32)
+    keys = torch.randn(graphs, seq_len, 128, generator=torch.Generator().manual_seed(5)).to(torch.bfloat16)
+    tg = torch.arange(graphs, dtype=torch.int32, device=device)
+    st = build_layer_state(torch.from_numpy(ids).to(device), keys.to(device), retrieval_to_graph=tg,
+                           retrieval_to_kv=tg, num_sink=num_sink, max_decode_tokens=8,
+                           topk_edges=TopkEdges(indices=torch.from_numpy(idx).to(device),
+                                                scores=torch.from_numpy(sc).to(device), row0=row0, group=group,
+                                                lam=lam))
+    torch.cuda.synchronize()
+    pos = np.tile(np.arange(row0, row0 + rows), group)[None].repeat(graphs, 0)
+    src, dst, w = co.build_adjacency(idx.reshape(graphs, group * rows, kappa), sc.reshape(graphs, group * rows, kappa),
+                                     pos, seq_len=seq_len, lam=lam)
+    cw, tw = co.init_modularity_state(ids, src, dst, w, community_capacity=st.community_weight.shape[1],
+                                      seq_len=seq_len)
+    np.testing.assert_allclose(st.community_weight.cpu().numpy(), cw, rtol=1e-4, atol=1e-3)
+    # the totals add ~10^5-10^6 edge weights: the device's (per-row closed
+    # form, per-workgroup partial sums) sits within 1e-5 of the float64 sum;
+    # the oracle's one long float32 chain drifts further (checked loosely)
+    tw64 = np.array([2.0 * w[src // seq_len == g].astype(np.float64).sum() for g in range(graphs)])
+    np.testing.assert_allclose(st.total_weight.cpu().numpy(), tw64, rtol=1e-5)
+    np.testing.assert_allclose(tw, tw64, rtol=1e-3)

@@ -311,3 +311,12 @@ def test_effective_token_budget():
         assert co.effective_token_budget(budget, seq, sink) == expected
     with pytest.raises(ValueError):
         co.effective_token_budget(4096, 10, 10)
+
+
+@pytest.mark.parametrize("name", ["adjacency_coalesces", "adjacency_discards_outside"])
+def test_adjacency_known_answers(name):
+    case = GOLDEN[name]
+    src, dst, w = co.build_adjacency(np.asarray(case["indices"]), np.asarray(case["scores"], np.float32),
+                                     np.asarray(case["query_positions"]), seq_len=case["seq_len"], lam=case["lam"])
+    got = {(int(a), int(b)): float(x) for a, b, x in zip(src, dst, w)}
+    assert got == {(a, b): x for a, b, x in case["pairs"]}
