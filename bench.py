@@ -311,36 +311,33 @@ def run_prefill(args, device):
     print(json.dumps(result), flush=True)
 
 
-STATE_EDGES_PER_GRAPH = 1_500_000
+STATE_KAPPA = 8  # the prefill edge width the runtime requests
 
 
 def run_state(args, device):
-    """GPU state assembly of one config-2 layer from labels (the 'next' row
-    after the decode path): 8 QUERY_GROUP graphs x 32,768 positions, 512
-    Zipf(1.1) communities, bf16 keys, 1.5M prefill edges per graph (sorted by
-    graph and source, as the coalesced adjacency is).  Times
-    ckv_build_layer_state (CSR, centroids, sizes, modularity weights, token
-    table) with inputs and outputs resident; the label-count read-back that
-    sizes the outputs is set-up."""
-    from community_kv_amd.graph.kernels.state_build import StateBuild
+    """GPU state assembly of one config-2 layer from labels and the prefill's
+    top-k edges (the first 'next' row after the decode path): 8 QUERY_GROUP
+    graphs x 32,768 positions, 512 Zipf(1.1) communities, bf16 keys, top-8
+    edges of every row of all 32 query heads.  Times ckv_build_layer_state
+    (CSR, centroids, sizes, modularity weights, token table) with inputs and
+    outputs resident; the label-count read-back that sizes the outputs is
+    set-up."""
+    from community_kv_amd.graph.kernels.state_build import StateBuild, TopkEdges
 
     rng = np.random.default_rng(3)
     gen = torch.Generator(device=device).manual_seed(3)
     labels = torch.from_numpy(np.stack([zipf_labels(rng, SEQ, SINKS, COMMUNITIES) for _ in range(HKV)])).to(device)
     keys = torch.randn(HKV, SEQ + 64, D, device=device, generator=gen).to(torch.bfloat16)[:, :SEQ]
-    n = STATE_EDGES_PER_GRAPH
-    g = torch.arange(HKV, device=device).repeat_interleave(n)
-    a = torch.randint(SINKS, SEQ, (HKV * n,), device=device, generator=gen)
-    b = torch.randint(SINKS, SEQ, (HKV * n,), device=device, generator=gen)
-    key = (g * SEQ + a) * SEQ + b
-    key = key.sort().values
-    src = (key // SEQ).to(torch.int32)
-    dst = (g * SEQ + key % SEQ).to(torch.int32)
-    w = torch.rand(HKV * n, device=device, generator=gen)
+    row0 = SINKS + STATE_KAPPA - 1
+    rows = SEQ - row0
+    tk_idx = torch.randint(SINKS, SEQ, (HQ, rows, STATE_KAPPA), device=device, generator=gen, dtype=torch.int32)
+    tk_sc = torch.rand(HQ, rows, STATE_KAPPA, device=device, generator=gen)
     maps = torch.arange(HKV, dtype=torch.int32, device=device)
     max_decode = 64
+    lam = 0.5
     build = StateBuild(labels, keys, retrieval_to_graph=maps, retrieval_to_kv=maps, num_sink=SINKS,
-                       max_decode_tokens=max_decode, edges=(src, dst, w))
+                       max_decode_tokens=max_decode,
+                       topk_edges=TopkEdges(indices=tk_idx, scores=tk_sc, row0=row0, group=HQ // HKV, lam=lam))
     for _ in range(args.warmup):
         build.run()
     torch.cuda.synchronize(device)
@@ -354,12 +351,12 @@ def run_state(args, device):
     ms = start.elapsed_time(stop) / args.steps
     out = build.out
     cap = out.community_sizes.shape[1]
-    edges = HKV * n
     nsink = SEQ - SINKS
+    entries = HQ * rows * STATE_KAPPA
     algorithmic = (HKV * SEQ * 4                      # labels
                    + HKV * nsink * D * 2              # keys, each non-sink row once
-                   + edges * (4 + 4 + 4)              # edge src, dst, weight
-                   + edges * 2 * 4                    # the two endpoint labels
+                   + entries * (4 + 4)                # top-k indices and scores
+                   + entries * 4 + HQ * rows * 4      # the column and row labels
                    + HKV * nsink * 4                  # member positions
                    + out.member_offsets.numel() * 4
                    + HKV * cap * (D + 4)              # centroids (e4m3) + sizes
@@ -378,13 +375,13 @@ def run_state(args, device):
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int32+bf16->e4m3",
-        "data": "synthetic (Zipf(1.1) labels, N(0,1) bf16 keys, uniform random edges)",
-        "config": {"workload": "GPU state assembly from labels, config-2 layer (8 graphs x 32768, 512 communities, "
-                               "1.5M edges per graph)", "graphs": HKV, "seq_len": SEQ, "communities": COMMUNITIES,
-                   "edges": edges},
+        "data": "synthetic (Zipf(1.1) labels, N(0,1) bf16 keys, uniform random top-8 columns and scores)",
+        "config": {"workload": "GPU state assembly from labels and prefill top-8 edges, config-2 layer (8 graphs "
+                               "x 32768, 512 communities, 32 query heads)", "graphs": HKV, "seq_len": SEQ,
+                   "communities": COMMUNITIES, "kappa": STATE_KAPPA, "lam": lam},
         "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": gbs / HBM_PEAK_GBS, "traffic": None,
-                     "kernel": "ckv_build_layer_state (7 launches, whole build)", "bytes_per_launch": algorithmic},
+                     "kernel": "ckv_build_layer_state (8 launches, whole build)", "bytes_per_launch": algorithmic},
     }
     if not args.no_cpu:
         from oracle import ckv_oracle as co
@@ -392,16 +389,20 @@ def run_state(args, device):
         ids = labels.cpu().numpy()
         counts = (ids[:, SINKS:].max(axis=1) + 1).astype(np.int32)
         kn = keys.float().cpu().numpy()
-        sn, dn, wn = src.cpu().numpy(), dst.cpu().numpy(), w.cpu().numpy()
+        group = HQ // HKV
+        ti = tk_idx.cpu().numpy().reshape(HKV, group * rows, STATE_KAPPA)
+        ts = tk_sc.cpu().numpy().reshape(HKV, group * rows, STATE_KAPPA)
+        pos = np.tile(np.arange(row0, row0 + rows), group)[None].repeat(HKV, 0)
         mp = np.arange(HKV, dtype=np.int32)
         t0 = time.perf_counter()
         co.build_member_csr(ids, counts, num_sink=SINKS)
         co.compute_centroids(ids, counts, kn, to_graph=mp, to_kv=mp, num_sink=SINKS, max_decode_tokens=max_decode)
+        sn, dn, wn = co.build_adjacency(ti, ts, pos, seq_len=SEQ, lam=lam)
         co.init_modularity_state(ids, sn, dn, wn, community_capacity=cap, seq_len=SEQ)
         sec = time.perf_counter() - t0
         result["cpu_baseline"] = {"value": sec * 1e6, "unit": "us", "cores": 1, "kind": "port",
-                                  "sample": "the whole layer build (numpy oracle: CSR, centroids, modularity "
-                                            "weights), once"}
+                                  "sample": "the whole layer build (numpy oracle: CSR, centroids, coalesced "
+                                            "adjacency, modularity weights), once"}
     print(json.dumps(result), flush=True)
 
 
