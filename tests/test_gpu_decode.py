@@ -96,6 +96,13 @@ CASES = {
                                    max_decode_tokens=12, aggregation=co.QUERY_GROUP),
                               dict(group_size=4, num_sink=10, token_budget=4096, mode="topk", topk_communities=6,
                                    max_selected=4096, assignment="nearest_centroid")),
+    # no sinks and no window; a query group of 4 (fused path) and of 8 (selection and attention launches)
+    "no_sinks_no_window_bf16": (dict(query_heads=8, kv_heads=2, seq_len=2048, communities=30, num_sink=0,
+                                     max_decode_tokens=16, aggregation=co.QUERY_GROUP),
+                                dict(group_size=4, num_sink=0, token_budget=256, local_window=0)),
+    "group8_bf16": (dict(query_heads=16, kv_heads=2, seq_len=2048, communities=30, num_sink=10,
+                         max_decode_tokens=16, aggregation=co.QUERY_GROUP),
+                    dict(group_size=8, num_sink=10, token_budget=320, local_window=64)),
 }
 STEPS = {"communities_1500_bf16": 4, "communities_2600_nearest": 4, "deep_delta_chains_bf16": 36,
          "topk_all_nearest_bf16": 12}
