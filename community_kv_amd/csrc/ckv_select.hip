@@ -88,6 +88,46 @@ __device__ inline void decode_frag(const CentroidFrag<CT>& f, float* out) {
   }
 }
 
+// One 8-lane group's share of a centroid row's dots with two queries, in the
+// pinned order: each lane sums its 16 dims in order (bf16 x e4m3 products have
+// at most 12 significant bits, so they are exact in f32 and a fused
+// multiply-add equals the pinned multiply-then-add), then the butterfly xor 4,
+// 2, 1 adds the lanes.  Shared by the selection's scoring and the prescoring
+// kernel so that both give the same bits.
+template <int CT, int DT>
+__device__ __forceinline__ void dot16_pair(const float* qa, const float* qb, const float* cv, float& a0, float& a1) {
+  a0 = qa[0] * cv[0];
+  a1 = qb[0] * cv[0];
+#pragma unroll
+  for (int i = 1; i < 16; ++i) {
+    if constexpr (CT == CKV_E4M3 && DT == CKV_BF16) {
+      a0 = __builtin_fmaf(qa[i], cv[i], a0);
+      a1 = __builtin_fmaf(qb[i], cv[i], a1);
+    } else {
+      a0 = a0 + qa[i] * cv[i];
+      a1 = a1 + qb[i] * cv[i];
+    }
+  }
+  a0 = add_xor_f32<4>(a0);
+  a1 = add_xor_f32<4>(a1);
+  a0 = add_xor_f32<2>(a0);
+  a1 = add_xor_f32<2>(a1);
+  a0 = add_xor_f32<1>(a0);
+  a1 = add_xor_f32<1>(a1);
+}
+
+// Query slice (dims 16*lane8 .. +15) of queries g and g+1 from the LDS copy.
+__device__ __forceinline__ void load_q_pair(const float* q_s, int g, int lane8, float* qa, float* qb) {
+  const float4* pa = reinterpret_cast<const float4*>(q_s + g * D + 16 * lane8);
+  const float4* pq = reinterpret_cast<const float4*>(q_s + (g + 1) * D + 16 * lane8);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float4 x = pa[i], y = pq[i];
+    qa[4 * i] = x.x; qa[4 * i + 1] = x.y; qa[4 * i + 2] = x.z; qa[4 * i + 3] = x.w;
+    qb[4 * i] = y.x; qb[4 * i + 1] = y.y; qb[4 * i + 2] = y.z; qb[4 * i + 3] = y.w;
+  }
+}
+
 // OWN: communities owned per thread (thread t owns [t*OWN, (t+1)*OWN), so id
 // order is thread order then k order), chosen from the scored community count
 // so that the per-community fields stay in registers.  Workgroups beyond
@@ -101,7 +141,9 @@ __host__ __device__ inline size_t fused_slot_bytes(int slot_capacity) { return (
 // slots of their own tiles only, attend them (attend_part) and write that
 // part of the slot table; the selection's other outputs are split over the
 // parts.
-template <int CT, int DT, int OWN, bool FUSED = false>
+// PRE: the scores were written to a.ws.scores by score_rows_kernel (no
+// nearest-centroid search then); the workgroup loads them instead of scoring.
+template <int CT, int DT, int OWN, bool FUSED = false, bool PRE = false>
 __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, const int part = 0,
                                             const int parts = 1) {
   constexpr int PB = CT == CKV_E4M3 ? 4 : 2;  // scoring passes whose loads are in flight together
@@ -167,12 +209,22 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
       rsize[buf][pb] = gload_i32(a.st.community_sizes + (int64_t)rh * C + row);
     }
   };
-  load_batch(0, 0, nscore - 1);
-  load_batch(PB, 1, nscore - 1);  // clamped rows: harmless when there is no second batch
+  if constexpr (!PRE) {
+    load_batch(0, 0, nscore - 1);
+    load_batch(PB, 1, nscore - 1);  // clamped rows: harmless when there is no second batch
+  }
   // Query group: two elements per thread (G * 128 <= 2048 <= 4 * threads).
-  float qv[4];
+  float qv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  // prescored: the scores of this head's rows t, t + threads, ...
+  uint16_t pre_key[OWN];
+  if constexpr (PRE) {
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
+    for (int k = 0; k < OWN; ++k)
+      pre_key[k] = reinterpret_cast<const uint16_t*>(a.ws.scores)[(int64_t)rh * C +
+                                                                    min(tid + k * SELECT_THREADS, nscore - 1)];
+  }
+#pragma unroll
+  for (int h = 0; h < (PRE ? 0 : 2); ++h) {
     const int qe = min(2 * (tid + h * SELECT_THREADS), G * D - 2);
     if constexpr (DT == CKV_BF16) {
       const uint32_t w = (uint32_t)gload_i32(reinterpret_cast<const int32_t*>(
@@ -257,39 +309,13 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
 #pragma unroll 1
     for (int g = 0; g < G; g += 2) {
       float qa[16], qb[16];
-      {
-        const float4* pa = reinterpret_cast<const float4*>(q_s + g * D + 16 * lane8);
-        const float4* pq = reinterpret_cast<const float4*>(q_s + (g + 1) * D + 16 * lane8);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float4 x = pa[i], y = pq[i];
-          qa[4 * i] = x.x; qa[4 * i + 1] = x.y; qa[4 * i + 2] = x.z; qa[4 * i + 3] = x.w;
-          qb[4 * i] = y.x; qb[4 * i + 1] = y.y; qb[4 * i + 2] = y.z; qb[4 * i + 3] = y.w;
-        }
-      }
+      load_q_pair(q_s, g, lane8, qa, qb);
 #pragma unroll
       for (int pb = 0; pb < PB; ++pb) {
         float cv[16];
         decode_frag<CT>(frag[buf][pb], cv);
-        // bf16 x e4m3 products have at most 12 significant bits, so they are
-        // exact in f32 and a fused multiply-add equals the pinned multiply-then-add.
-        float a0 = qa[0] * cv[0], a1 = qb[0] * cv[0];
-#pragma unroll
-        for (int i = 1; i < 16; ++i) {
-          if constexpr (CT == CKV_E4M3 && DT == CKV_BF16) {
-            a0 = __builtin_fmaf(qa[i], cv[i], a0);
-            a1 = __builtin_fmaf(qb[i], cv[i], a1);
-          } else {
-            a0 = a0 + qa[i] * cv[i];
-            a1 = a1 + qb[i] * cv[i];
-          }
-        }
-        a0 = add_xor_f32<4>(a0);
-        a1 = add_xor_f32<4>(a1);
-        a0 = add_xor_f32<2>(a0);
-        a1 = add_xor_f32<2>(a1);
-        a0 = add_xor_f32<1>(a0);
-        a1 = add_xor_f32<1>(a1);
+        float a0, a1;
+        dot16_pair<CT, DT>(qa, qb, cv, a0, a1);
         best[pb] = fmax_exact(best[pb], a0);
         if (g + 1 < G) best[pb] = fmax_exact(best[pb], a1);
       }
@@ -328,12 +354,20 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
   // loop waits for every load issued in it.
   const int live_passes = (count + ROWS_PER_PASS - 1) / ROWS_PER_PASS;
   const int last_live = max(count, 1) - 1;
-  for (int p0 = 0; p0 < live_passes; p0 += 2 * PB) {
-    score_batch(p0, 0);
-    if (p0 + PB >= live_passes) break;
-    load_batch(p0 + 2 * PB, 0, last_live);
-    score_batch(p0 + PB, 1);
-    load_batch(p0 + 3 * PB, 1, last_live);
+  if constexpr (PRE) {
+#pragma unroll
+    for (int k = 0; k < OWN; ++k) {
+      const int c = tid + k * SELECT_THREADS;
+      if (c < count) key16[c] = pre_key[k];
+    }
+  } else {
+    for (int p0 = 0; p0 < live_passes; p0 += 2 * PB) {
+      score_batch(p0, 0);
+      if (p0 + PB >= live_passes) break;
+      load_batch(p0 + 2 * PB, 0, last_live);
+      score_batch(p0 + PB, 1);
+      load_batch(p0 + 3 * PB, 1, last_live);
+    }
   }
   CKV_STAMP(rh == 0 && part == 0, 7);
   if (nearest_mode) {
@@ -807,6 +841,54 @@ __global__ __launch_bounds__(SELECT_THREADS) void select_attend_batch_kernel(con
   select_body<CT, DT, OWN, true>(table[blockIdx.x / per_item], r / parts, r % parts, parts);
 }
 
+// Scores of 64 centroid rows of one (item, head) per workgroup, written to
+// a.ws.scores as fp16 bits (-inf for empty or inactive rows), in exactly the
+// selection's scoring arithmetic (dot16_pair); workgroups past the head's
+// live rows exit.  Lets a batch with many communities per head score on every
+// compute unit before the one-workgroup-per-head selection.
+template <int CT, int DT>
+__global__ __launch_bounds__(SELECT_THREADS) void score_rows_batch_kernel(const DecodeArgs* __restrict__ table,
+                                                                         int heads) {
+  __shared__ float q_s[CKV_MAX_GROUP * D];
+  const DecodeArgs& a = table[blockIdx.y / heads];
+  const int rh = blockIdx.y % heads;
+  const int tid = threadIdx.x;
+  const int C = a.st.community_capacity;
+  const int nscore = min(C, a.ws.score_blocks * SCORE_BLOCK);
+  int count = a.st.community_counts[rh];
+  count = count < 0 ? 0 : (count > nscore ? nscore : count);
+  const int r0 = blockIdx.x * ROWS_PER_PASS;
+  if (r0 >= count) return;
+  const int G = a.cfg.group_size;
+  const int sub = tid >> 3, lane8 = tid & 7;
+  const int row = min(r0 + sub, count - 1);
+  CentroidFrag<CT> frag;
+  load_frag<CT>(a.st.centroids, (int64_t)rh * C + row, 16 * lane8, frag);
+  const int size = gload_i32(a.st.community_sizes + (int64_t)rh * C + row);
+  for (int e = tid; e < G * D; e += SELECT_THREADS) q_s[e] = load_elem<DT>(a.kv.query, (int64_t)rh * G * D + e);
+  __syncthreads();
+  float cv[16];
+  decode_frag<CT>(frag, cv);
+  float best = NEG_INF;
+  for (int g = 0; g < G; g += 2) {
+    float qa[16], qb[16];
+    load_q_pair(q_s, g, lane8, qa, qb);
+    float a0, a1;
+    dot16_pair<CT, DT>(qa, qb, cv, a0, a1);
+    best = fmax_exact(best, a0);
+    if (g + 1 < G) best = fmax_exact(best, a1);
+  }
+  const int c = r0 + sub;
+  if (lane8 == 0 && c < count)
+    reinterpret_cast<uint16_t*>(a.ws.scores)[(int64_t)rh * C + c] = f16_bits_hw(size > 0 ? best : NEG_INF);
+}
+
+template <int CT, int DT, int OWN>
+__global__ __launch_bounds__(SELECT_THREADS) void select_prescored_batch_kernel(const DecodeArgs* __restrict__ table,
+                                                                               int heads) {
+  select_body<CT, DT, OWN, false, true>(table[blockIdx.x / heads], blockIdx.x % heads);
+}
+
 // Batched selection: workgroup w serves item w / heads, head w % heads of the
 // device table.
 template <int CT, int DT, int OWN>
@@ -946,9 +1028,27 @@ int launch_batch_select_attend(const DecodeArgs& h, const DecodeArgs* table, int
 
 // Batched selection of `count` items (bf16 KV); `max_nscore`, `max_lds` are the
 // maxima over the items.
+// With more than PRESCORE_MIN_ROWS scored rows per head (and no nearest-centroid
+// search, which the prescoring does not do) the rows are scored first by
+// score_rows_batch_kernel on every compute unit; the selection then loads the
+// scores.
+constexpr int PRESCORE_MIN_ROWS = 2 * SELECT_THREADS;
+
 int launch_batch_select(const DecodeArgs& h, const DecodeArgs* table, int count, int max_nscore, size_t max_lds,
                         hipStream_t s) {
   const int own = (max_nscore + SELECT_THREADS - 1) / SELECT_THREADS;
+  const bool pre = max_nscore > PRESCORE_MIN_ROWS && h.cfg.assignment != CKV_ASSIGN_NEAREST;
+  if (pre) {
+    const dim3 grid((max_nscore + ROWS_PER_PASS - 1) / ROWS_PER_PASS, count * h.st.retrieval_heads);
+    if (h.st.centroid_dtype == CKV_E4M3)
+      hipLaunchKernelGGL((score_rows_batch_kernel<CKV_E4M3, CKV_BF16>), grid, dim3(SELECT_THREADS), 0, s, table,
+                         h.st.retrieval_heads);
+    else
+      hipLaunchKernelGGL((score_rows_batch_kernel<CKV_F32, CKV_BF16>), grid, dim3(SELECT_THREADS), 0, s, table,
+                         h.st.retrieval_heads);
+    const int rc = launch_check("score_rows_batch");
+    if (rc) return rc;
+  }
   auto launch = [&](auto kernel) {
     if (max_lds > 48 * 1024) {
       const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
@@ -963,6 +1063,14 @@ int launch_batch_select(const DecodeArgs& h, const DecodeArgs* table, int count,
     return launch_check("select_batch");
   };
   constexpr int OWN_MAX = CKV_MAX_COMMUNITIES / SELECT_THREADS;
+  if (pre) {
+    if (h.st.centroid_dtype == CKV_E4M3) {
+      return own <= 4 ? launch(select_prescored_batch_kernel<CKV_E4M3, CKV_BF16, 4>)
+                      : launch(select_prescored_batch_kernel<CKV_E4M3, CKV_BF16, OWN_MAX>);
+    }
+    return own <= 4 ? launch(select_prescored_batch_kernel<CKV_F32, CKV_BF16, 4>)
+                    : launch(select_prescored_batch_kernel<CKV_F32, CKV_BF16, OWN_MAX>);
+  }
   if (h.st.centroid_dtype == CKV_E4M3) {
     return own <= 1 ? launch(select_batch_kernel<CKV_E4M3, CKV_BF16, 1>)
            : own <= 2 ? launch(select_batch_kernel<CKV_E4M3, CKV_BF16, 2>)

@@ -32,14 +32,24 @@ def _item(fx, params, device):
     return dict(state=state, cur=cur, q=q, ws=ws, call=call)
 
 
-@pytest.mark.parametrize("aggregation,assignment,group", [
-    (co.QUERY_GROUP, "delta_q", 4), (co.QUERY_GROUP, "nearest_centroid", 4), (co.LAYER_WISE, "delta_q", 2)])
-def test_batch_decode_matches_single_items(device, aggregation, assignment, group):
-    print(f"batch decode {aggregation} {assignment}", flush=True)
+# more than 1024 scored rows per head: the batch scores them first on every
+# compute unit (score_rows_batch_kernel), the selection loads the scores
+ITEMS_LARGE = [
+    dict(seq_len=16384, communities=1500),
+    dict(seq_len=6000, communities=300),
+    dict(seq_len=12000, communities=1100),
+]
+
+
+@pytest.mark.parametrize("aggregation,assignment,group,items", [
+    (co.QUERY_GROUP, "delta_q", 4, ITEMS), (co.QUERY_GROUP, "nearest_centroid", 4, ITEMS),
+    (co.LAYER_WISE, "delta_q", 2, ITEMS), (co.QUERY_GROUP, "delta_q", 4, ITEMS_LARGE)])
+def test_batch_decode_matches_single_items(device, aggregation, assignment, group, items):
+    print(f"batch decode {aggregation} {assignment} communities={[kw['communities'] for kw in items]}", flush=True)
     params = co.StepParams(group_size=group, num_sink=10, token_budget=512, local_window=64, assignment=assignment)
     qh = 4 * group
     fxs = [syn.build_layer(seed=50 + i, query_heads=qh, kv_heads=4, num_sink=10, max_decode_tokens=16,
-                           aggregation=aggregation, **kw) for i, kw in enumerate(ITEMS)]
+                           aggregation=aggregation, **kw) for i, kw in enumerate(items)]
     single = [_item(fx, params, device) for fx in fxs]
     batched = [_item(fx, params, device) for fx in fxs]
     batch = BatchDecode([b["call"] for b in batched])
