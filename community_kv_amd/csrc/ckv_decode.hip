@@ -3,9 +3,14 @@
 // (scoring + selection + slot table), ckv_attend.hip (attention, split merge,
 // online update, dense baseline) and ckv_prefill.hip (prefill edge export).
 //
-// Each decode-layer transition is two stream-ordered launches (three with a
-// layer-wise shared graph): score_select_kernel, then the attention kernel
-// whose last tile per retrieval head merges the splits and runs the update.
+// ckv_decode_layer is three stream-ordered launches when the layer fits the
+// fused path (bf16 KV with prefill membership, slot table <= 8192, group
+// <= 4): select_attend_kernel (selection + attention partials), the split
+// merge, and the online update (callers that defer it fold it into the next
+// layer's launch: ckv_decode_step_after_update).  Otherwise: select_kernel,
+// the attention partials kernel, the merge and the update.  A layer-wise shared
+// graph adds the centroid sync after the update.  ckv_state.hip builds the
+// prefill state from labels.
 #include <stdio.h>
 #include <string.h>
 

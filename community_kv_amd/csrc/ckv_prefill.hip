@@ -7,7 +7,7 @@
 // merges four lanes, an approximation), kappa is a parameter (<= 16) and the
 // stored value can be the reference probability or the dequantised raw score.
 //
-// prefill_mfma_kernel: one workgroup = 4 waves = 128 packed rows
+// prefill_mfma_kernel: one workgroup = 8 waves = 256 packed rows
 // (row r <-> position r / G, query head kv_head * G + r % G, PackGQA), so every
 // K/V tile staged in LDS serves all G query heads of the KV head.  Each wave
 // owns 32 packed rows and computes S^T = K Q^T with v_mfma_f32_32x32x16_bf16:

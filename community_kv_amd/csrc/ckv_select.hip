@@ -1,20 +1,30 @@
-// Centroid scoring + exact community selection + slot materialisation.
+// Centroid scoring + exact community selection + slot materialisation, and
+// the fused selection + attention launch.
 //
-// select_kernel: one 512-thread workgroup per retrieval head.  Every decode
-// layer-step is a chain of dependent memory round trips, so the kernel is laid
+// select_body: one 512-thread workgroup per retrieval head.  Every decode
+// layer-step is a chain of dependent memory round trips, so the body is laid
 // out to need as few of them as possible:
 //   R0  head mapping, query group, centroid rows, community sizes, sinks
 //   R1  graph-indexed fields of every scored community: CSR start, decode-delta
-//       member count and tail chunk; the current position
-//   R2  tail-chunk start and fill of every community with decode deltas (and,
-//       for nearest-centroid assignment, the current key row)
-//   --  scoring and the exact weighted selection run while R2 is in flight
-//   R3  one gather round for every attended slot (CSR member, delta member,
-//       sink, window community)
+//       member count and tail chunk (in flight during the scoring)
+//   --  scoring as soon as R0 has landed
+//   R2  tail-chunk start and fill of every community with decode deltas, and
+//       the communities of the window tokens (issued after the scoring, in
+//       flight during the selection)
+//   --  exact weighted selection and descriptors
+//   R3  one gather round for the attended slots (CSR member, delta member)
 // Scoring: 8 lanes per centroid row (16 dims each), pinned fp32 summation order
 // (each lane sums its 16 products in order, then a butterfly over the 8 lanes),
 // fp16 round-to-nearest-even key.  Selection: two 8-bit radix passes over
 // order-preserving fp16 keys in LDS, descriptors in the reference order.
+//
+// Kernels: select_kernel (the selection alone: writes the slot table for the
+// attention kernels), select_attend_kernel (FUSED: parts workgroups per head
+// each run the selection, resolve only their own two tiles' slots and attend
+// them into split partials), their batched variants over a device table of
+// items, and select_prescored_batch_kernel (scores computed beforehand by
+// score_rows_batch_kernel on every compute unit).  Workgroups past the heads
+// run the deferred online update of another layer.
 //
 // Reference: attention/kernels/centroid_selection.py:32-188 (scoring),
 // attention/kernels/_csrc/descriptor_selection.cu:164-487 (selection),
