@@ -416,7 +416,8 @@ __device__ inline void merge_group(const DecodeArgs& a, const int rh, const int 
 constexpr int MERGE_WIDE_THREADS = 512;
 
 template <int PRE>
-__device__ __forceinline__ void merge_wide_body(const DecodeArgs& a, const int rh, const int splits) {
+// Returns the merged lse of the head's first query (every thread).
+__device__ __forceinline__ float merge_wide_body(const DecodeArgs& a, const int rh, const int splits) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -425,6 +426,7 @@ __device__ __forceinline__ void merge_wide_body(const DecodeArgs& a, const int r
   CKV_STAMP(rh == 0, 24);
   __shared__ float sc_s[MERGE_WIDE_THREADS / 64][PRE];
   __shared__ float den_s[MERGE_WIDE_THREADS / 64];
+  __shared__ float lse0_s;
   const int i = min(tid, G * D - 1);
   const float* src = a.ws.partial_acc + (base + (int64_t)(i >> 7) * splits) * D + (i & (D - 1));
   float v[PRE];
@@ -441,7 +443,9 @@ __device__ __forceinline__ void merge_wide_body(const DecodeArgs& a, const int r
     if (lane < PRE) sc_s[wave][lane] = sc;
     if (lane == 0) {
       den_s[wave] = den;
-      a.ws.lse[(int64_t)rh * G + wave] = M + ckv_logf(den);
+      const float lse = M + ckv_logf(den);
+      a.ws.lse[(int64_t)rh * G + wave] = lse;
+      if (wave == 0) lse0_s = lse;
     }
   }
   __syncthreads();
@@ -457,6 +461,7 @@ __device__ __forceinline__ void merge_wide_body(const DecodeArgs& a, const int r
         ckv_f32_to_bf16_bits(acc / den_s[g]);
   }
   CKV_STAMP(rh == 0, 25);
+  return lse0_s;
 }
 
 template <int PRE>
@@ -468,6 +473,18 @@ template <int PRE>
 __global__ __launch_bounds__(MERGE_WIDE_THREADS) void merge_wide_batch_kernel(const DecodeArgs* __restrict__ table,
                                                                               int heads, int splits) {
   merge_wide_body<PRE>(table[blockIdx.x / heads], blockIdx.x % heads, splits);
+}
+
+// Split merge and then, in the same workgroup, the head's online update (it
+// needs the merged lse of the first query and the slots' candidate scores):
+// one kernel boundary fewer than merge + update launches.
+template <int PRE, int CT, int DT>
+__global__ __launch_bounds__(MERGE_WIDE_THREADS) void merge_update_batch_kernel(
+    const DecodeArgs* __restrict__ table, int heads, int splits) {
+  const DecodeArgs& a = table[blockIdx.x / heads];
+  const int rh = blockIdx.x % heads;
+  const float lse0 = merge_wide_body<PRE>(a, rh, splits);
+  owner_update<CT, DT>(a, rh, lse0);
 }
 
 // Split merge of the bf16 path: one workgroup per retrieval head.  A kernel of
@@ -784,6 +801,31 @@ int launch_batch_attention(const DecodeArgs& h, const DecodeArgs* table, int cou
   int r = launch_check("attend_mfma_batch");
   if (r || partials_only) return r;
   return launch_batch_merge(h, table, count, splits, s);
+}
+
+int launch_batch_merge_update(const DecodeArgs& h, const DecodeArgs* table, int count, int splits,
+                              bool any_shared, hipStream_t s) {
+  const int heads = h.st.retrieval_heads;
+  const dim3 g(count * heads);
+  auto go = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, g, dim3(MERGE_WIDE_THREADS), 0, s, table, heads, splits);
+  };
+  if (h.st.centroid_dtype == CKV_E4M3) {
+    if (splits <= 8) go(merge_update_batch_kernel<8, CKV_E4M3, CKV_BF16>);
+    else if (splits <= 16) go(merge_update_batch_kernel<16, CKV_E4M3, CKV_BF16>);
+    else if (splits <= 32) go(merge_update_batch_kernel<32, CKV_E4M3, CKV_BF16>);
+    else go(merge_update_batch_kernel<64, CKV_E4M3, CKV_BF16>);
+  } else {
+    if (splits <= 8) go(merge_update_batch_kernel<8, CKV_F32, CKV_BF16>);
+    else if (splits <= 16) go(merge_update_batch_kernel<16, CKV_F32, CKV_BF16>);
+    else if (splits <= 32) go(merge_update_batch_kernel<32, CKV_F32, CKV_BF16>);
+    else go(merge_update_batch_kernel<64, CKV_F32, CKV_BF16>);
+  }
+  int r = launch_check("merge_update_batch");
+  if (r || !any_shared) return r;
+  if (h.st.centroid_dtype == CKV_E4M3) hipLaunchKernelGGL((sync_shared_batch_kernel<CKV_E4M3, CKV_BF16>), g, dim3(REDUCE_THREADS), 0, s, table, heads);
+  else hipLaunchKernelGGL((sync_shared_batch_kernel<CKV_F32, CKV_BF16>), g, dim3(REDUCE_THREADS), 0, s, table, heads);
+  return launch_check("sync_shared_batch");
 }
 
 int launch_batch_update(const DecodeArgs& h, const DecodeArgs* table, int count, bool any_shared, hipStream_t s) {

@@ -363,15 +363,17 @@ extern "C" int ckv_batch_decode(const ckv_layer_args* items, int32_t count, cons
   // Every fused workgroup repeats its head's selection: worth it only while
   // the copies run side by side, one per compute unit.
   if ((int64_t)count * h.st.retrieval_heads * parts > FUSED_MAX_WORKGROUPS) parts = 0;
+  int splits = parts;
   if (parts > 0) {
     rc = ckv::launch_batch_select_attend(h, t, count, max_nscore, fused_lds, parts, s);
-    if (!rc) rc = ckv::launch_batch_merge(h, t, count, parts, s);
   } else {
     rc = ckv::launch_batch_select(h, t, count, max_nscore, max_lds, s);
-    if (!rc) rc = ckv::launch_batch_attention(h, t, count, s);
+    if (!rc) rc = ckv::launch_batch_attention(h, t, count, s, true);
+    splits = ckv::attention_batch_splits(h);
   }
-  if (!rc && h.cfg.assignment != CKV_ASSIGN_NONE) rc = ckv::launch_batch_update(h, t, count, any_shared, s);
-  return rc;
+  if (rc) return rc;
+  if (h.cfg.assignment == CKV_ASSIGN_NONE) return ckv::launch_batch_merge(h, t, count, splits, s);
+  return ckv::launch_batch_merge_update(h, t, count, splits, any_shared, s);
 }
 
 extern "C" int ckv_batch_attention_partials(const ckv_layer_args* items, int32_t count, const void* table,

@@ -472,6 +472,9 @@ int launch_batch_select(const DecodeArgs& h, const DecodeArgs* table, int count,
 int launch_batch_attention(const DecodeArgs& h, const DecodeArgs* table, int count, hipStream_t stream,
                            bool partials_only = false);
 int launch_batch_update(const DecodeArgs& h, const DecodeArgs* table, int count, bool any_shared, hipStream_t stream);
+// Merge of `splits` partials and the online update in one launch (+ the shared-graph sync).
+int launch_batch_merge_update(const DecodeArgs& h, const DecodeArgs* table, int count, int splits, bool any_shared,
+                              hipStream_t stream);
 int launch_dense(const DecodeArgs& a, int seq_len, int group, hipStream_t stream);
 int launch_check(const char* what);
 
