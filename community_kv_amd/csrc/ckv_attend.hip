@@ -475,6 +475,12 @@ __global__ __launch_bounds__(MERGE_WIDE_THREADS) void merge_wide_batch_kernel(co
   merge_wide_body<PRE>(table[blockIdx.x / heads], blockIdx.x % heads, splits);
 }
 
+template <int PRE, int CT, int DT>
+__global__ __launch_bounds__(MERGE_WIDE_THREADS) void merge_update_kernel(DecodeArgs a, int splits) {
+  const float lse0 = merge_wide_body<PRE>(a, blockIdx.x, splits);
+  owner_update<CT, DT>(a, blockIdx.x, lse0);
+}
+
 // Split merge and then, in the same workgroup, the head's online update (it
 // needs the merged lse of the first query and the slots' candidate scores):
 // one kernel boundary fewer than merge + update launches.
@@ -755,6 +761,27 @@ int launch_attention(const DecodeArgs& a, hipStream_t s, bool partials_only) {
   if (r || partials_only) return r;
   hipLaunchKernelGGL(reduce_kernel<CKV_F32>, dim3(a.st.retrieval_heads), dim3(REDUCE_THREADS), 0, s, a);
   return launch_check("reduce");
+}
+
+// Merge of `splits` bf16 partials (group * 128 <= 512) and the online update
+// in one launch, then the shared-graph sync.
+int launch_merge_update(const DecodeArgs& a, hipStream_t s, int splits) {
+  if (a.cfg.assignment == CKV_ASSIGN_NONE) return launch_merge(a, s, splits);
+  const dim3 g(a.st.retrieval_heads);
+  auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, g, dim3(MERGE_WIDE_THREADS), 0, s, a, splits); };
+  if (a.st.centroid_dtype == CKV_E4M3) {
+    if (splits <= 8) go(merge_update_kernel<8, CKV_E4M3, CKV_BF16>);
+    else if (splits <= 16) go(merge_update_kernel<16, CKV_E4M3, CKV_BF16>);
+    else if (splits <= 32) go(merge_update_kernel<32, CKV_E4M3, CKV_BF16>);
+    else go(merge_update_kernel<64, CKV_E4M3, CKV_BF16>);
+  } else {
+    if (splits <= 8) go(merge_update_kernel<8, CKV_F32, CKV_BF16>);
+    else if (splits <= 16) go(merge_update_kernel<16, CKV_F32, CKV_BF16>);
+    else if (splits <= 32) go(merge_update_kernel<32, CKV_F32, CKV_BF16>);
+    else go(merge_update_kernel<64, CKV_F32, CKV_BF16>);
+  }
+  const int r = launch_check("merge_update");
+  return r ? r : launch_sync_shared(a, s);
 }
 
 int launch_update(const DecodeArgs& a, hipStream_t s) {

@@ -179,11 +179,10 @@ extern "C" int ckv_decode_layer(const ckv_kv_cache* kv, const ckv_graph_state* s
   const int parts = ckv::fused_parts(a);
   if (parts > 0) {
     rc = ckv::launch_select_attend(a, s, nullptr, parts);
-    if (!rc) rc = ckv::launch_merge(a, s, parts);
-  } else {
-    rc = ckv::launch_score_select(a, s);
-    if (!rc) rc = ckv::launch_attention(a, s, false);
+    return rc ? rc : ckv::launch_merge_update(a, s, parts);
   }
+  rc = ckv::launch_score_select(a, s);
+  if (!rc) rc = ckv::launch_attention(a, s, false);
   if (!rc) rc = ckv::launch_update(a, s);
   return rc;
 }

@@ -458,6 +458,8 @@ int launch_score_select(const DecodeArgs& a, hipStream_t stream, const DecodeArg
 int launch_sync_shared(const DecodeArgs& a, hipStream_t stream);
 int launch_attention(const DecodeArgs& a, hipStream_t stream, bool partials_only);
 int launch_update(const DecodeArgs& a, hipStream_t stream);
+// Merge of `splits` bf16 partials (group * 128 <= 512, splits <= 64) + online update in one launch.
+int launch_merge_update(const DecodeArgs& a, hipStream_t stream, int splits);
 size_t select_lds_bytes(int community_capacity, int descriptor_capacity, int max_selected);
 int attention_batch_splits(const DecodeArgs& a);  // 0 when the batched attention cannot serve `a`
 int fused_parts(const DecodeArgs& a);              // 0 when the fused selection + attention cannot serve `a`
