@@ -81,3 +81,27 @@ def test_generate_full_selection_matches_dense(device, assignment, graph):
         print(f"step {step}: max |logit diff| {err:.4f} (max |logit| {scale:.3f})", flush=True)
         assert err < 0.02 * scale + 0.01, step
         assert int(seq[0, 300 + step]) == int(a[0].argmax())
+
+
+def test_generate_twice_repeats_itself(device):
+    """A second request on the same runtime (state reset, new cache, the step
+    graph captured again) reproduces the first one token for token."""
+    from community_kv_amd import CommunityKVAttention, CommunityKVConfig, CommunityKVRuntime, GraphAggregation
+    from community_kv_amd.config import PartitionConfig
+
+    print("generate twice", flush=True)
+    model = _model(device)
+    prompt = torch.randint(0, 512, (1, 260), generator=torch.Generator().manual_seed(3)).to(device)
+    new = 6
+    cfg = CommunityKVConfig(token_budget=128, num_sink=10, aggregation=GraphAggregation.QUERY_GROUP,
+                            local_window=32, assignment="delta_q")
+    with CommunityKVRuntime(config=cfg, partition=PartitionConfig(), num_layers=LAYERS, max_decode_tokens=new,
+                            label_provider=_labels) as runtime:
+        CommunityKVAttention(runtime).register()
+        model.set_attn_implementation("community_kv")
+        with torch.inference_mode():
+            a = runtime.generate(model, prompt, max_new_tokens=new)
+            b = runtime.generate(model, prompt, max_new_tokens=new)
+        torch.cuda.synchronize()
+        assert runtime.last_graph_replays == new - 2
+    assert torch.equal(a, b)
