@@ -11,10 +11,11 @@ namespace ckv {
 // candidates, assignment, running-mean centroid, delta append, overflow.
 // s_lse0 is the merged lse of the head's first query.  Block size 128..512.
 //
-// Dependent memory rounds: (1) candidates + cursor/count/total, (2) candidate
-// communities + current key row, (3) per-candidate weight/size/delta tail and
-// centroid rows (slot KAPPA holds the community a new token would open, or the
-// nearest centroid), (4) the assigned community's tail-chunk state.
+// Dependent memory rounds: (1) candidates + cursor/count/total and the free
+// lists, (2) candidate communities + current key row, (3) per-candidate
+// weight/size/delta tail and centroid rows (slot KAPPA holds the community a
+// new token would open, or the nearest centroid), (4) every candidate's
+// tail-chunk state, in flight during the assignment; then the stores.
 template <int CT, int DT>
 __device__ void owner_update(const DecodeArgs& a, const int rh, const float s_lse0) {
   const int tid = threadIdx.x;
@@ -35,6 +36,21 @@ __device__ void owner_update(const DecodeArgs& a, const int rh, const float s_ls
   __shared__ float s_key[D];
   __shared__ float s_cent[NS][D];
   __shared__ int s_assigned, s_slot, s_comm_ov;
+
+  // Cursor state and the allocator's free lists, loaded now (in flight with
+  // round 1) and published after it.
+  int cur_r = 0, active_r = 0, nearest_r = -1, free_chunk_r = 0, free_pos_r = 0;
+  float total_r = 0.0f;
+  if (tid == 64) {
+    cur_r = a.st.current_position[graph];
+    active_r = a.st.community_counts[rh];
+    total_r = a.st.total_weight[graph];
+    nearest_r = delta_q ? -1 : a.ws.nearest[rh];
+  }
+  if (tid == 0) {
+    free_chunk_r = a.dl.next_free_chunk[graph];
+    free_pos_r = a.dl.next_free_position[graph];
+  }
 
   // ---- round 1: exact top-8 over every attended non-sink slot (score desc,
   // position asc); cursor state (one thread of wave 1).  Each thread keeps a
@@ -91,10 +107,10 @@ __device__ void owner_update(const DecodeArgs& a, const int rh, const float s_ls
     }
   }
   if (tid == 64) {
-    s_cur = a.st.current_position[graph];
-    s_active = a.st.community_counts[rh];
-    s_total = a.st.total_weight[graph];
-    s_nearest = delta_q ? -1 : a.ws.nearest[rh];
+    s_cur = cur_r;
+    s_active = active_r;
+    s_total = total_r;
+    s_nearest = nearest_r;
   }
   __syncthreads();
   const int cur = s_cur;
@@ -141,6 +157,18 @@ __device__ void owner_update(const DecodeArgs& a, const int rh, const float s_ls
     s_cent[k][d] = (comm >= 0 && comm < C) ? load_centroid1<CT>(a.st.centroids, ((int64_t)rh * C + comm) * D + d) : 0.0f;
   }
   __syncthreads();
+
+  // Tail-chunk fields of every candidate's community, loaded now (in flight
+  // during the assignment) for round 4, which needs only the assigned one's.
+  const int64_t cb = (int64_t)graph * a.dl.chunks_per_graph;
+  int t_cs = 0, t_cc = 0, t_st = 0;
+  if (tid < NS && a.dl.chunks_per_graph > 0) {
+    const int t = s_tail[tid];
+    const int tt = min(max(t, 0), a.dl.chunks_per_graph - 1);
+    t_cs = gload_i32(a.dl.chunk_size + cb + tt);
+    t_cc = gload_i32(a.dl.chunk_capacity + cb + tt);
+    t_st = gload_i32(a.dl.chunk_start + cb + tt);
+  }
 
   // ---- assignment (lanes 0..7 of wave 0) ------------------------------------
   if (tid < 64) {
@@ -239,19 +267,26 @@ __device__ void owner_update(const DecodeArgs& a, const int rh, const float s_ls
       store_centroid1<CT>(a.st.centroids, ((int64_t)rh * C + asg) * D + d, upd);
     }
   }
-  // ---- round 4: decode-delta append ----------------------------------------
+  // ---- round 4: decode-delta append (the assigned community's tail-chunk
+  // fields were prefetched by lane `slot` of wave 0) -------------------------
+  int slot_cs = 0, slot_cc = 0, slot_st = 0;
+  if (tid < 64) {
+    slot_cs = __shfl(t_cs, slot, 64);
+    slot_cc = __shfl(t_cc, slot, 64);
+    slot_st = __shfl(t_st, slot, 64);
+  }
   if (tid == 0) {
     bool chunk_ov = false, pos_ov = false;
     if (!comm_ov) {
       const int64_t tb = (int64_t)graph * C + asg;
-      const int64_t cb = (int64_t)graph * a.dl.chunks_per_graph;
       const int delta_size = s_dsize[slot];
       const int old_tail = s_tail[slot];
-      const int old_cs = old_tail >= 0 ? a.dl.chunk_size[cb + old_tail] : 0;
-      const int old_cc = old_tail >= 0 ? a.dl.chunk_capacity[cb + old_tail] : 0;
-      const int old_start = old_tail >= 0 ? a.dl.chunk_start[cb + old_tail] : 0;
-      const int free_chunk = a.dl.next_free_chunk[graph];
-      const int free_pos = a.dl.next_free_position[graph];
+      const bool tail_ok = old_tail >= 0 && old_tail < a.dl.chunks_per_graph;
+      const int old_cs = tail_ok ? slot_cs : 0;
+      const int old_cc = tail_ok ? slot_cc : 0;
+      const int old_start = tail_ok ? slot_st : 0;
+      const int free_chunk = free_chunk_r;
+      const int free_pos = free_pos_r;
       const bool allocate = old_tail < 0 || old_cs >= old_cc;
       const int new_cap = old_tail < 0 ? 1 : old_cc * 2;
       chunk_ov = allocate && free_chunk >= a.dl.chunks_per_graph;
