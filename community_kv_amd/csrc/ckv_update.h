@@ -22,6 +22,7 @@ __device__ void owner_update(const DecodeArgs& a, const int rh, const float s_ls
   const int graph = a.st.retrieval_to_graph[rh];
   if (a.cfg.assignment == CKV_ASSIGN_NONE || rh != graph) return;
   __syncthreads();
+  CKV_STAMP(rh == 0, 26);
 
   constexpr int NS = KAPPA + 1;  // candidate slots
   const int C = a.st.community_capacity;
@@ -53,18 +54,29 @@ __device__ void owner_update(const DecodeArgs& a, const int rh, const float s_ls
   }
 
   // ---- round 1: exact top-8 over every attended non-sink slot (score desc,
-  // position asc); cursor state (one thread of wave 1).  Each thread keeps a
-  // sorted top-8 of its strided share (loaded 8 at a time, one round per
-  // chunk), each wave merges its lanes' lists in 8 rounds of a wave-wide max,
-  // and wave 0 sorts the waves' survivors.
+  // position asc, as one packed 64-bit key each).  Each thread keeps a sorted
+  // top-8 of its strided share (loaded 8 at a time, one round per chunk;
+  // sorted by a 19-comparator network, merged into the running list).  The
+  // eighth largest of the threads' maxima, T8, bounds the answer from below:
+  // every global top-8 key is at least T8, and only the (at most 8) threads
+  // whose maximum reaches T8 hold such keys, so at most 64 candidates remain;
+  // wave 0 sorts them.
   {
     constexpr int CH = 8;
     __shared__ uint64_t wtop[8 * KAPPA];
+    __shared__ uint64_t cand_s[64];
+    __shared__ uint64_t s_t8;
+    __shared__ int s_ncand;
     const int nt = blockDim.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int scap = a.ws.slot_capacity;
     const float* scs = a.ws.slot_scores + (int64_t)rh * scap;
     const int32_t* sps = a.ws.slot_positions + (int64_t)rh * scap;
+    auto cas = [](uint64_t& x, uint64_t& y) {  // x = max, y = min
+      const uint64_t hi = x > y ? x : y;
+      y = x > y ? y : x;
+      x = hi;
+    };
     uint64_t loc[KAPPA];
 #pragma unroll
     for (int k = 0; k < KAPPA; ++k) loc[k] = 0ull;
@@ -77,32 +89,59 @@ __device__ void owner_update(const DecodeArgs& a, const int rh, const float s_ls
         sv[c] = gload_f32(scs + s);
         pv[c] = gload_i32(sps + s);
       }
+      uint64_t v[CH];
 #pragma unroll
       for (int c = 0; c < CH; ++c) {
         const int s = s0 + c * nt + tid;
         const bool ok = s < scap && s >= a.cfg.num_sink && pv[c] >= 0 && pv[c] < a.kv.capacity;
-        uint64_t v = ok ? pack_candidate(sv[c], pv[c]) : 0ull;
+        v[c] = ok ? pack_candidate(sv[c], pv[c]) : 0ull;
+      }
+      cas(v[0], v[2]); cas(v[1], v[3]); cas(v[4], v[6]); cas(v[5], v[7]);
+      cas(v[0], v[4]); cas(v[1], v[5]); cas(v[2], v[6]); cas(v[3], v[7]);
+      cas(v[0], v[1]); cas(v[2], v[3]); cas(v[4], v[5]); cas(v[6], v[7]);
+      cas(v[2], v[4]); cas(v[3], v[5]);
+      cas(v[1], v[4]); cas(v[3], v[6]);
+      cas(v[1], v[2]); cas(v[3], v[4]); cas(v[5], v[6]);
+      if (s0 == 0) {
 #pragma unroll
-        for (int k = 0; k < KAPPA; ++k) {
-          const uint64_t hi = v > loc[k] ? v : loc[k];
-          v = v > loc[k] ? loc[k] : v;
-          loc[k] = hi;
-        }
+        for (int k = 0; k < KAPPA; ++k) loc[k] = v[k];
+      } else {
+        // top 8 of two sorted lists: pairwise max against the reversed list
+        // gives a bitonic sequence of the 8 largest; sort it
+#pragma unroll
+        for (int k = 0; k < KAPPA; ++k) loc[k] = loc[k] > v[KAPPA - 1 - k] ? loc[k] : v[KAPPA - 1 - k];
+        cas(loc[0], loc[4]); cas(loc[1], loc[5]); cas(loc[2], loc[6]); cas(loc[3], loc[7]);
+        cas(loc[0], loc[2]); cas(loc[1], loc[3]); cas(loc[4], loc[6]); cas(loc[5], loc[7]);
+        cas(loc[0], loc[1]); cas(loc[2], loc[3]); cas(loc[4], loc[5]); cas(loc[6], loc[7]);
       }
     }
+    uint64_t tmax = loc[0];
     for (int r = 0; r < KAPPA; ++r) {
-      const uint64_t best = wave_max_u64(loc[0]);
+      const uint64_t best = wave_max_u64(tmax);
       if (lane == 0) wtop[wave * KAPPA + r] = best;
-      if (best != 0ull && loc[0] == best) {
-#pragma unroll
-        for (int k = 0; k < KAPPA - 1; ++k) loc[k] = loc[k + 1];
-        loc[KAPPA - 1] = 0ull;
-      }
+      if (tmax == best) tmax = 0ull;  // keys are unique (they hold the position)
     }
     __syncthreads();
     if (wave == 0) {
       const int n = (nt >> 6) * KAPPA;  // at most 64 (blocks of at most 512 threads)
-      const uint64_t v = wave_sort_desc_u64(lane < n ? wtop[lane] : 0ull);
+      const uint64_t srt = wave_sort_desc_u64(lane < n ? wtop[lane] : 0ull);
+      const uint64_t t8 = ((uint64_t)__builtin_amdgcn_readlane((uint32_t)(srt >> 32), KAPPA - 1) << 32) |
+                          (uint32_t)__builtin_amdgcn_readlane((uint32_t)(srt & 0xffffffffu), KAPPA - 1);
+      if (lane == 0) {
+        s_t8 = t8;
+        s_ncand = 0;
+      }
+    }
+    __syncthreads();
+    const uint64_t t8 = s_t8;
+#pragma unroll
+    for (int k = 0; k < KAPPA; ++k) {
+      if (loc[k] != 0ull && loc[k] >= t8) cand_s[atomicAdd(&s_ncand, 1)] = loc[k];
+    }
+    __syncthreads();
+    if (wave == 0) {
+      const int n = s_ncand;
+      const uint64_t v = wave_sort_desc_u64(lane < n ? cand_s[lane] : 0ull);
       if (lane < KAPPA) top[lane] = v;
     }
   }
@@ -113,6 +152,7 @@ __device__ void owner_update(const DecodeArgs& a, const int rh, const float s_ls
     s_nearest = nearest_r;
   }
   __syncthreads();
+  CKV_STAMP(rh == 0, 27);
   const int cur = s_cur;
   const int active = s_active;
   const bool valid_pos = cur >= 0 && cur < tc_cap;
@@ -141,6 +181,7 @@ __device__ void owner_update(const DecodeArgs& a, const int rh, const float s_ls
     s_key[d] = valid_pos ? load_elem<DT>(a.kv.key, kvh * a.kv.head_stride + (int64_t)cur * a.kv.token_stride + d) : 0.0f;
   }
   __syncthreads();
+  CKV_STAMP(rh == 0, 28);
 
   // ---- round 3: per-candidate state and centroid rows ----------------------
   if (tid < NS) {
@@ -157,6 +198,7 @@ __device__ void owner_update(const DecodeArgs& a, const int rh, const float s_ls
     s_cent[k][d] = (comm >= 0 && comm < C) ? load_centroid1<CT>(a.st.centroids, ((int64_t)rh * C + comm) * D + d) : 0.0f;
   }
   __syncthreads();
+  CKV_STAMP(rh == 0, 29);
 
   // Tail-chunk fields of every candidate's community, loaded now (in flight
   // during the assignment) for round 4, which needs only the assigned one's.
@@ -255,6 +297,7 @@ __device__ void owner_update(const DecodeArgs& a, const int rh, const float s_ls
     }
   }
   __syncthreads();
+  CKV_STAMP(rh == 0, 30);
   const int slot = s_slot;
   const int asg = s_assigned;
   const bool comm_ov = s_comm_ov != 0;
@@ -319,6 +362,7 @@ __device__ void owner_update(const DecodeArgs& a, const int rh, const float s_ls
     a.ws.overflow[graph] = overflow;
     if (overflow == 0) a.st.current_position[graph] = cur + 1;
   }
+  CKV_STAMP(rh == 0, 31);
 }
 
 }  // namespace ckv
