@@ -415,9 +415,20 @@ __device__ inline void merge_group(const DecodeArgs& a, const int rh, const int 
 // the denominator with lane = split.
 constexpr int MERGE_WIDE_THREADS = 512;
 
-template <int PRE>
-// Returns the merged lse of the head's first query (every thread).
-__device__ __forceinline__ float merge_wide_body(const DecodeArgs& a, const int rh, const int splits) {
+// Merged output of one thread (bf16 bits of element tid, tid < G * 128) and
+// of lane 0 of waves < G (that query's lse), stored by merge_store: callers
+// that load more afterwards store last, so that those loads' completion
+// waits do not cover the stores.
+struct MergeOut {
+  uint16_t bits;
+  float lse;
+};
+
+// Returns the merged lse of the head's first query (every thread); with
+// DEFER the outputs are left in `mo` for merge_store.
+template <int PRE, bool DEFER = false>
+__device__ __forceinline__ float merge_wide_body(const DecodeArgs& a, const int rh, const int splits,
+                                                 MergeOut* mo = nullptr) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -444,7 +455,7 @@ __device__ __forceinline__ float merge_wide_body(const DecodeArgs& a, const int 
     if (lane == 0) {
       den_s[wave] = den;
       const float lse = M + ckv_logf(den);
-      a.ws.lse[(int64_t)rh * G + wave] = lse;
+      if constexpr (DEFER) mo->lse = lse; else a.ws.lse[(int64_t)rh * G + wave] = lse;
       if (wave == 0) lse0_s = lse;
     }
   }
@@ -457,11 +468,20 @@ __device__ __forceinline__ float merge_wide_body(const DecodeArgs& a, const int 
       const float sc = sc_s[g][k];
       if (k < splits) acc = acc + (sc != 0.0f ? v[k] * sc : 0.0f);
     }
-    reinterpret_cast<uint16_t*>(a.ws.output)[((int64_t)rh * G + g) * D + (tid & (D - 1))] =
-        ckv_f32_to_bf16_bits(acc / den_s[g]);
+    const uint16_t bits = ckv_f32_to_bf16_bits(acc / den_s[g]);
+    if constexpr (DEFER) mo->bits = bits;
+    else reinterpret_cast<uint16_t*>(a.ws.output)[((int64_t)rh * G + g) * D + (tid & (D - 1))] = bits;
   }
   CKV_STAMP(rh == 0, 25);
   return lse0_s;
+}
+
+__device__ __forceinline__ void merge_store(const DecodeArgs& a, const int rh, const MergeOut& mo) {
+  const int tid = threadIdx.x;
+  const int G = a.cfg.group_size;
+  if (tid < G * D) reinterpret_cast<uint16_t*>(a.ws.output)[(int64_t)rh * G * D + tid] = mo.bits;
+  const int wave = tid >> 6;
+  if ((tid & 63) == 0 && wave < G) a.ws.lse[(int64_t)rh * G + wave] = mo.lse;
 }
 
 template <int PRE>
@@ -477,8 +497,10 @@ __global__ __launch_bounds__(MERGE_WIDE_THREADS) void merge_wide_batch_kernel(co
 
 template <int PRE, int CT, int DT>
 __global__ __launch_bounds__(MERGE_WIDE_THREADS) void merge_update_kernel(DecodeArgs a, int splits) {
-  const float lse0 = merge_wide_body<PRE>(a, blockIdx.x, splits);
+  MergeOut mo;
+  const float lse0 = merge_wide_body<PRE, true>(a, blockIdx.x, splits, &mo);
   owner_update<CT, DT>(a, blockIdx.x, lse0);
+  merge_store(a, blockIdx.x, mo);
 }
 
 // Split merge and then, in the same workgroup, the head's online update (it
@@ -489,8 +511,10 @@ __global__ __launch_bounds__(MERGE_WIDE_THREADS) void merge_update_batch_kernel(
     const DecodeArgs* __restrict__ table, int heads, int splits) {
   const DecodeArgs& a = table[blockIdx.x / heads];
   const int rh = blockIdx.x % heads;
-  const float lse0 = merge_wide_body<PRE>(a, rh, splits);
+  MergeOut mo;
+  const float lse0 = merge_wide_body<PRE, true>(a, rh, splits, &mo);
   owner_update<CT, DT>(a, rh, lse0);
+  merge_store(a, rh, mo);
 }
 
 // Split merge of the bf16 path: one workgroup per retrieval head.  A kernel of

@@ -167,9 +167,8 @@ __device__ void owner_update(const DecodeArgs& a, const int rh, const float s_ls
         sc = unordered_f32((uint32_t)(v >> 32));
         pos = (int)(0xffffffffu - (uint32_t)(v & 0xffffffffu));
       }
-      s_sc[tid] = sc;
-      a.ws.topk_scores[(int64_t)rh * KAPPA + tid] = sc;
-      a.ws.topk_positions[(int64_t)rh * KAPPA + tid] = pos;
+      s_sc[tid] = sc;  // (the top-8 outputs are stored at the end: a store here would make
+                       // the next loads' completion waits cover it)
       if (delta_q && pos >= 0 && pos < tc_cap) comm = a.st.token_communities[(int64_t)graph * a.st.token_capacity + pos];
     } else {
       comm = (!delta_q && s_nearest >= 0) ? s_nearest : active;  // community a new token would open
@@ -361,6 +360,10 @@ __device__ void owner_update(const DecodeArgs& a, const int rh, const float s_ls
     const int overflow = (comm_ov ? 1 : 0) | (chunk_ov ? 2 : 0) | (pos_ov ? 4 : 0) | (valid_pos ? 0 : 8);
     a.ws.overflow[graph] = overflow;
     if (overflow == 0) a.st.current_position[graph] = cur + 1;
+  }
+  if (tid < KAPPA) {
+    a.ws.topk_scores[(int64_t)rh * KAPPA + tid] = s_sc[tid];
+    a.ws.topk_positions[(int64_t)rh * KAPPA + tid] = s_pos[tid];
   }
   CKV_STAMP(rh == 0, 31);
 }
