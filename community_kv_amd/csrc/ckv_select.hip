@@ -780,11 +780,12 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
       a.ws.descriptor_counts[rh] = n_desc;
       a.ws.selected_counts[rh] = sel_count;
     }
-    for (int i = wp * SELECT_THREADS + tid; i < n_desc; i += stride) {
+    // item i goes to part i % wn (each part writes a strided share)
+    for (int i = wp + wn * tid; i < n_desc; i += stride) {
       a.ws.communities[(int64_t)rh * dcap + i] = desc_comm[i];
       a.ws.cumulative_ends[(int64_t)rh * dcap + i] = desc_end[i];
     }
-    for (int t = wp * SELECT_THREADS + tid; t < a.ws.budget_tiles; t += stride) {
+    for (int t = wp + wn * tid; t < a.ws.budget_tiles; t += stride) {
       const int off = max(t * TILE - ns, 0);
       int lo = 0, hi = n_desc;
       while (lo < hi) {
