@@ -191,7 +191,7 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
   int* desc_tl = desc_dc + dcap;     // tail chunk id
   int* desc_ts = desc_tl + dcap;     // tail chunk start
   int* desc_tn = desc_ts + dcap;     // tail chunk fill
-  int* blk_first = desc_tn + dcap;   // first descriptor reaching each 64-slot block of the selection
+  int* blk_first = desc_tn + dcap;   // descriptor holding the first slot of each 64-slot block of the selection
 
   // Every prefetch load below is unconditional (indices clamped, results
   // masked afterwards) and no global store is issued before the last gather:
@@ -512,9 +512,12 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
     }
   }
   const int high_count = t4[0], high_mass = t4[1];
-  auto store_desc = [&](int idx, int c, int end, int k) {
+  // Also marks idx as the first descriptor of every 64-slot block whose first
+  // slot falls in [start, end) (the ranges partition the selection).
+  auto store_desc = [&](int idx, int c, int start, int end, int k) {
     desc_comm[idx] = c;
     desc_end[idx] = end;
+    for (int b = (start + 63) >> 6; (b << 6) < end; ++b) blk_first[b] = idx;
     desc_lo[idx] = o_lo[k];
     desc_dc[idx] = o_dc[k];
     desc_tl[idx] = o_tl[k];
@@ -534,7 +537,7 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
       const bool eq = ok && threshold >= 0 && (int)o_key[k] == threshold;
       if (high) {
         if (hm < cap_tokens && hc < dcap) {
-          store_desc(hc, c, min(cap_tokens, hm + size), k);
+          store_desc(hc, c, hm, min(cap_tokens, hm + size), k);
           my_max = max(my_max, hc);  // (a later high-key community has a smaller index than an earlier threshold one)
         }
         hc += 1;
@@ -544,7 +547,7 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
         const bool within = budget_mode ? (st0 < sel_slots) : (ec < a.cfg.topk_communities - high_count);
         const int idx = high_count + ec;
         if (within && st0 < cap_tokens && idx < dcap) {
-          store_desc(idx, c, min(cap_tokens, st0 + size), k);
+          store_desc(idx, c, st0, min(cap_tokens, st0 + size), k);
           my_max = max(my_max, idx);
         }
         ec += 1;
@@ -558,16 +561,7 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
   const int n_desc = s_max_idx + 1;
   const int sel_count = n_desc > 0 ? desc_end[n_desc - 1] : 0;
   CKV_STAMP(rh == 0 && part == 0, 15);
-  const int nblk = (sel_count + 63) / 64;
-  for (int b = tid; b <= nblk; b += SELECT_THREADS) {
-    const int j = 64 * b;
-    int lo = 0, hi = n_desc;
-    while (lo < hi) {
-      const int mid = (lo + hi) >> 1;
-      if (desc_end[mid] <= j) lo = mid + 1; else hi = mid;
-    }
-    blk_first[b] = lo;
-  }
+  if (tid == 0) blk_first[(sel_count + 63) / 64] = n_desc;  // (blocks below were marked by store_desc)
   for (int d = tid; d < n_desc; d += SELECT_THREADS) comm_desc[desc_comm[d]] = (uint16_t)d;
   // Only the last descriptor can be truncated; remember its community size.
   if (n_desc > 0) {
