@@ -780,11 +780,17 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
       a.ws.cumulative_ends[(int64_t)rh * dcap + i] = desc_end[i];
     }
     for (int t = wp + wn * tid; t < a.ws.budget_tiles; t += stride) {
+      // first descriptor ending after the tile's first selected slot (searched
+      // between the first descriptors of its 64-slot block and the next)
       const int off = max(t * TILE - ns, 0);
-      int lo = 0, hi = n_desc;
-      while (lo < hi) {
-        const int mid = (lo + hi) >> 1;
-        if (desc_end[mid] <= off) lo = mid + 1; else hi = mid;
+      int lo = n_desc - 1;
+      if (off < sel_count) {
+        lo = blk_first[off >> 6];
+        int hi = min(blk_first[(off >> 6) + 1], n_desc - 1);
+        while (lo < hi) {
+          const int mid = (lo + hi) >> 1;
+          if (desc_end[mid] <= off) lo = mid + 1; else hi = mid;
+        }
       }
       a.ws.tile_descriptors[(int64_t)rh * a.ws.budget_tiles + t] = max(0, min(lo, n_desc - 1));
     }
