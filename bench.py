@@ -660,6 +660,22 @@ def main():
     dense_graph.replay()
     dense_ms = time_graph(dense_graph, max(5, args.steps // 5), device)
 
+    # torch-ROCm SDPA decode over the same caches (second dense baseline)
+    sdpa_q = [e["query"].view(1, HQ, 1, D) for e in stack]
+    sdpa_kv = [(e["key"][:, :SEQ].unsqueeze(0), e["value"][:, :SEQ].unsqueeze(0)) for e in stack]
+
+    def sdpa_step():
+        for q, (k, v) in zip(sdpa_q, sdpa_kv):
+            torch.nn.functional.scaled_dot_product_attention(q, k, v, enable_gqa=True)
+
+    sdpa_us_layer = None
+    try:
+        sdpa_graph = capture(sdpa_step, device)
+        sdpa_graph.replay()
+        sdpa_us_layer = time_graph(sdpa_graph, max(5, args.steps // 5), device) * 1e3 / len(stack)
+    except RuntimeError as err:  # reported, not fatal: it is a baseline
+        print(f"torch SDPA baseline unavailable: {err}", file=sys.stderr)
+
     us_layer = ms * 1e3 / len(stack)
     dense_us_layer = dense_ms * 1e3 / len(stack)
     fused_bytes = att_bytes + centroid_bytes
@@ -684,6 +700,7 @@ def main():
         "us_per_step_layer": us_layer,
         "us_per_step_layer_update_inline": serial_ms * 1e3 / len(stack),
         "dense_us_per_step_layer": dense_us_layer,
+        "torch_sdpa_us_per_step_layer": sdpa_us_layer,
         "speedup_vs_dense": dense_us_layer / us_layer,
         "select_attend_kernel_us": fused_ms * 1e3,
         "attended_tokens_per_head": tokens_per_head,
