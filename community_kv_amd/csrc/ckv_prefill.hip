@@ -224,6 +224,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_mfma_kernel(ckv_pref
     }
   };
   uint32_t q_min = 0u;
+  uint32_t row_thr = 0u;  // a lower bound of the row's QN-th best key (both halves)
   float m = NEG_INF;  // reference max of the raw score (scale > 0)
   float l = 0.0f;     // this half's share of the softmax denominator
 
@@ -341,9 +342,10 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_mfma_kernel(ckv_pref
     // Top-kappa candidates of this lane's 32 columns, inspected by group
     // against the larger of the two halves' worst kept keys.  Placed after the
     // PV^T MFMAs are issued: the rare branch runs while they drain.
-    uint32_t thr = max(q_min, swap32_u32(q_min));
+    uint32_t thr = max(max(q_min, swap32_u32(q_min)), row_thr);
     float tf = prefilter(thr);
-    if (lmax >= tf) {
+    const bool inspect = lmax >= tf;
+    if (inspect) {
       uint32_t qk[QN];
       load_queue(qk);
 #pragma unroll
@@ -369,6 +371,18 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_mfma_kernel(ckv_pref
 #pragma unroll
       for (int j = 0; j < QN / 4; ++j) q_lds[j * 64 * PF_WAVES] = uint4{qk[4 * j], qk[4 * j + 1], qk[4 * j + 2], qk[4 * j + 3]};
       q_min = qk[QN - 1];
+    }
+    // After an inspection anywhere in the wave: the QN-th best key of the row
+    // over both halves' queues (the minimum of the bitonic top-QN of their
+    // union).  No later candidate below it can reach the row's top QN, so it
+    // is the tighter threshold for both halves.
+    if (__builtin_amdgcn_ballot_w64(inspect)) {
+      uint32_t mine[QN];
+      load_queue(mine);
+      uint32_t rt = 0xffffffffu;
+#pragma unroll
+      for (int i = 0; i < QN; ++i) rt = min(rt, max(mine[i], swap32_u32(mine[QN - 1 - i])));
+      row_thr = rt;
     }
 
     sacc[0] = snext[0];
