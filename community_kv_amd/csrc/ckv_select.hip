@@ -45,7 +45,7 @@ namespace {
 int limit_error(const char* message) { return ckv_internal::set_error(CKV_E_LIMIT, message); }
 
 constexpr int ROWS_PER_PASS = SELECT_THREADS / 8;          // centroid rows scored per pass
-constexpr int MAT_BATCH = 4;                               // 64-slot blocks per wave gathered together
+constexpr int MAT_BATCH = 8;                               // 64-slot blocks per wave gathered together
 constexpr int DESC_ARRAYS = 7;                             // per-descriptor LDS arrays
 // Dynamic LDS the fused kernel may use (the selection's static arrays take
 // about 12 KB of the CU's 160 KB).
