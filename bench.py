@@ -408,6 +408,78 @@ def run_state(args, device):
     print(json.dumps(result), flush=True)
 
 
+def run_partition(args, device):
+    """Prefill partition of one config-2 layer (the second 'next' row): the
+    top-8 edges of all 32 query heads from the prefill kernel on planted
+    config-5 style inputs (32,768 tokens, 256 clusters), grouped into 8
+    QUERY_GROUP graphs, then ``partition_graphs``: build_adjacency (device
+    torch ops), native multi-level Leiden (ckv_batched_leiden /
+    ckv_aggregate_coo / ckv_densify_*), isolated fill and dense remap.  The
+    timed region is the whole partition; the Leiden part is timed alone too."""
+    from community_kv_amd.attention.flash_attention import prefill_attention_topk
+    from community_kv_amd.graph import partition as P
+    from community_kv_amd.graph.leiden import run_leiden
+
+    q, k, v = planted_prefill_inputs(device, seq=args.prefill_seq)
+    S = q.shape[1]
+    out = prefill_attention_topk(q, k, v, softmax_scale=D ** -0.5, num_sink=SINKS, kappa=STATE_KAPPA)
+    idx, val = out[5][0].contiguous(), out[4][0].contiguous()
+    del q, k, v, out
+    kw = dict(aggregation="query_group", num_kv_heads=HKV, prefill_seq_len=S, num_sink=SINKS, lam=0.5,
+              leiden_resolution=1.0, leiden_seed=0)
+    run = lambda: P.partition_graphs(idx, val, **kw)
+    g_idx, g_val, pos = P._reshape_by_aggregation(idx, val, aggregation="query_group", num_kv_heads=HKV,
+                                                  num_sink=SINKS)
+    src, dst, w = P.build_adjacency(g_idx, g_val, pos, seq_len=S, lam=0.5)
+    iters = P.leiden_max_iterations(S)
+    leiden = lambda: run_leiden(src, dst, w, G=HKV, seq_len=S, max_inner_iter=iters, seed=0)
+    for _ in range(args.warmup):
+        res = run()
+    torch.cuda.synchronize(device)
+
+    def timed(fn):
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            fn()
+        torch.cuda.synchronize(device)
+        return (time.perf_counter() - t0) / args.steps * 1e3
+
+    ms = timed(run)
+    leiden_ms = timed(leiden)
+    counts = res.community_counts.cpu().tolist()
+    result = {
+        "metric": "partition_ms_32k_qwen3_8b_layer",
+        "value": ms,
+        "unit": "ms",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int32+f32 (f64 gains)",
+        "data": "synthetic (prefill top-8 edges of planted config-5 style q/k/v, 256 clusters, cosine 0.6)",
+        "config": {"workload": "prefill partition of a config-2 layer: 8 QUERY_GROUP graphs x 32768 tokens, "
+                               "top-8 edges of 32 query heads, lam 0.5, resolution 1, "
+                               f"{iters} sweeps per phase", "graphs": HKV, "seq_len": S,
+                   "edges": int(src.numel()), "communities_per_graph": counts,
+                   "modularity": res.modularity, "leiden_only_ms": leiden_ms},
+        "roofline": None,
+    }
+    if not args.no_cpu:
+        from oracle import leiden as L
+
+        one = (src.long() // S) == 0  # graph 0 alone, scaled by the graph count
+        s0, d0, w0 = (t[one].cpu().numpy() for t in (src, dst, w))
+        t0 = time.perf_counter()
+        L.partition_labels(s0, d0, w0, graphs=1, seq_len=S, resolution=1.0, max_inner_iter=iters, seed=0)
+        sec = time.perf_counter() - t0
+        result["cpu_baseline"] = {"value": sec * 1e3 * HKV, "unit": "ms", "cores": 1, "kind": "port",
+                                  "sample": "numpy oracle Leiden + relabel of graph 0 of 8, scaled by 8"}
+    print(json.dumps(result), flush=True)
+
+
 GEN_LAYERS = 36
 GEN_PROMPT = 65536
 GEN_STEPS = 128
@@ -577,7 +649,7 @@ def main():
     ap.add_argument("--layers", type=int, default=LAYERS)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
-    ap.add_argument("--workload", choices=["decode", "prefill", "generate", "batched", "state"], default="decode",
+    ap.add_argument("--workload", choices=["decode", "prefill", "generate", "batched", "state", "partition"], default="decode",
                     help="decode: the 36-layer sparse decode step (default); prefill: config-5 edge export; "
                          "generate: config-3 model decode loop; batched: config-4 ragged batch; "
                          "state: GPU state assembly of one config-2 layer from labels")
@@ -598,6 +670,8 @@ def main():
     if args.workload == "generate":
         run_generate(args, device)
         return
+    if args.workload == "partition":
+        return run_partition(args, device)
     if args.workload == "state":
         return run_state(args, device)
     if args.workload == "batched":

@@ -19,7 +19,7 @@ REPO_DIR = os.path.dirname(PACKAGE_DIR)
 LIB_PATH = os.path.join(PACKAGE_DIR, "libckv_amd.so")
 SOURCES = [os.path.join(PACKAGE_DIR, "csrc", name)
            for name in ("ckv_decode.hip", "ckv_select.hip", "ckv_attend.hip", "ckv_prefill.hip", "ckv_diag.hip",
-                                "ckv_state.hip")]
+                                "ckv_state.hip", "ckv_leiden.hip")]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 HIP_FLAGS = [
     "--offload-arch=gfx950",
@@ -65,6 +65,13 @@ EXPORTED_SYMBOLS = (
     "ckv_state_workspace_bytes",
     "ckv_label_counts",
     "ckv_build_layer_state",
+    "ckv_leiden_workspace_bytes",
+    "ckv_batched_leiden",
+    "ckv_aggregate_coo_workspace_bytes",
+    "ckv_aggregate_coo",
+    "ckv_densify_workspace_bytes",
+    "ckv_densify_count",
+    "ckv_densify_apply",
     "ckv_host_numerics",
     "ckv_device_numerics",
     "ckv_abi_version",
@@ -201,6 +208,21 @@ def lib() -> ctypes.CDLL:
     handle.ckv_label_counts.restype = ctypes.c_int
     handle.ckv_build_layer_state.argtypes = [ctypes.POINTER(StateBuildArgs), _p]
     handle.ckv_build_layer_state.restype = ctypes.c_int
+    handle.ckv_leiden_workspace_bytes.argtypes = [_i64, _i32, _i32]
+    handle.ckv_leiden_workspace_bytes.restype = ctypes.c_size_t
+    handle.ckv_batched_leiden.argtypes = [_p, _p, _p, _i64, _i32, _i32, _f32, _f32, _i32, _i32, _i32, _p, _p, _p,
+                                          _p]
+    handle.ckv_batched_leiden.restype = ctypes.c_int
+    handle.ckv_aggregate_coo_workspace_bytes.argtypes = [_i64]
+    handle.ckv_aggregate_coo_workspace_bytes.restype = ctypes.c_size_t
+    handle.ckv_aggregate_coo.argtypes = [_p, _p, _p, _i64, _p, _i32, _p, _p, _p, _p, _p, _p]
+    handle.ckv_aggregate_coo.restype = ctypes.c_int
+    handle.ckv_densify_workspace_bytes.argtypes = [_i32, _i32]
+    handle.ckv_densify_workspace_bytes.restype = ctypes.c_size_t
+    handle.ckv_densify_count.argtypes = [_p, _i32, _i32, _p, _p, _p]
+    handle.ckv_densify_count.restype = ctypes.c_int
+    handle.ckv_densify_apply.argtypes = [_p, _i32, _i32, _i32, _p, _p, _p]
+    handle.ckv_densify_apply.restype = ctypes.c_int
     handle.ckv_host_numerics.argtypes = [ctypes.c_int, _p, _p, _i64]
     handle.ckv_host_numerics.restype = ctypes.c_int
     handle.ckv_device_numerics.argtypes = [ctypes.c_int, _p, _p, _i64, _p]

@@ -1,0 +1,814 @@
+// Batched Leiden over G vertex-disjoint graphs, one level per call, plus the
+// two helpers of the multi-level driver (COO aggregation, per-graph label
+// densification).  Restates the reference's graph/leiden/_csrc (leiden.cu
+// 43-205, local_moving.cu 69-210, refinement.cu 71-300, csr.cu 20-271,
+// aggregate.cu 24-184, helpers.cu 9-122) for MI355X:
+//
+//   * one wave64 per vertex; the vertex's neighbour communities are gathered
+//     into a per-wave LDS table by a leader loop (a chunk of 64 row entries at
+//     a time, ballot per distinct community, fp64 butterfly sum), so sums are
+//     formed in one fixed order and a low-degree vertex touches only its row;
+//   * the sweep loops run without host round trips: every sweep's kernels
+//     are queued up front and read a device control word (moved count,
+//     up/down direction, stall count, done flag) that a one-wave control
+//     kernel advances after each sweep, so converged sweeps exit at once;
+//   * the symmetric CSR is one stable radix sort of (src, dst) keys, rows
+//     ordered by neighbour id.
+//
+// Move rules follow the reference: synchronous moves on a snapshot, gain
+//   dQ = (k_v,new - k_v,old)/m + gamma k_v (Sigma_old - k_v - Sigma_new)/(2 m^2),
+// neighbour-community weights rounded to float, the per-vertex jitter and the
+// per-sweep rank of the reference's PCG hash (rng.cuh), the up/down gate in
+// local moving, the well-connectedness gate and the independent-set commit in
+// refinement.  Equal float scores are broken by the order in which the
+// reference's 1024-slot table scan prefers a community's home slot, then by
+// smaller id.  A vertex keeps at most TABLE_CAP distinct neighbour
+// communities (the reference's table size), in order of first appearance.
+//
+// Launch sequence of ckv_batched_leiden (one stream, no host sync):
+//   mirror_kernel, radix sort, row_ptr_kernel, col_kernel, degree_kernel, init_kernel
+//   local moving x max_inner_iter: sigma_zero, sigma_scatter, local_moving_kernel, lm_control_kernel
+//   refine_init_kernel, parent sigma
+//   refinement x max_inner_iter: sigma_zero, sigma_scatter, refine_propose_kernel,
+//                                refine_commit_kernel, refine_control_kernel
+//   sigma of the result, modularity_kernel, finish_kernel (labels, -1 for isolated)
+#include <hip/hip_runtime.h>
+#include <hipcub/hipcub.hpp>
+
+#include <stdint.h>
+
+#include "ckv_amd.h"
+#include "ckv_error.h"
+
+namespace ckv {
+namespace {
+
+constexpr int LWAVES = 4;        // vertices (waves) per workgroup
+constexpr int LTHREADS = 64 * LWAVES;
+constexpr int TABLE_CAP = 1024;  // distinct neighbour communities per vertex
+constexpr int ETHREADS = 256;
+
+enum { CTL_MOVED = 0, CTL_UPDOWN = 1, CTL_STALE = 2, CTL_DONE = 3, CTL_WORDS = 8 };
+
+// ----------------------------------------------------------------- hashing (rng.cuh)
+__device__ __host__ inline uint32_t pcg_hash(uint32_t x) {
+  const uint32_t state = x * 747796405u + 2891336453u;
+  const uint32_t word = ((state >> ((state >> 28u) + 4u)) ^ state) * 277803737u;
+  return (word >> 22u) ^ word;
+}
+__device__ inline uint32_t mix4(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  uint32_t h = pcg_hash(a);
+  h = pcg_hash(h ^ b);
+  h = pcg_hash(h ^ c);
+  return pcg_hash(h ^ d);
+}
+__device__ inline float unit_float(uint32_t h) { return (float)(h >> 8) * (1.0f / 16777216.0f); }
+__device__ inline float rand_uniform(uint32_t g, uint32_t v, uint32_t level, uint32_t sweep, uint32_t seed) {
+  return unit_float(mix4(g, v, (level << 16) | sweep, seed));
+}
+__device__ inline float rand_uniform_pair(uint32_t g, uint32_t v, uint32_t c, uint32_t level, uint32_t sweep,
+                                          uint32_t seed) {
+  const uint32_t s = pcg_hash((sweep << 16) ^ c);
+  return unit_float(mix4(g, v, (level << 16) | (s & 0xFFFFu), seed));
+}
+__device__ inline float gumbel(float u) {
+  u = fmaxf(u, 1.0e-7f);
+  u = fminf(u, 1.0f - 1.0e-7f);
+  return -logf(-logf(u));
+}
+
+// Tie preference among equal scores (larger wins): the reference scans home
+// slot s = pcg_hash(c) & 1023 with thread s & 127 (slice index s >> 7, first
+// strict maximum kept) and reduces lanes, then warps, with 32-lane
+// shuffle-down trees that keep their own value on ties; then the smaller id.
+__device__ inline uint32_t bitrev5(uint32_t x) { return __builtin_bitreverse32(x) >> 27; }
+__device__ inline uint32_t cand_pref(int32_t c) {
+  const uint32_t s = pcg_hash((uint32_t)c) & 1023u;
+  const uint32_t key = (bitrev5((s >> 5) & 3u) << 8) | (bitrev5(s & 31u) << 3) | (s >> 7);
+  return ((8191u - key) << 18) | (0x3FFFFu - ((uint32_t)c & 0x3FFFFu));
+}
+constexpr uint32_t STAY_PREF = 0xFFFFFFFFu;  // staying wins every tie
+__device__ inline uint32_t ordered(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ inline uint64_t pack(float score, uint32_t pref) { return ((uint64_t)ordered(score) << 32) | pref; }
+
+// ----------------------------------------------------------------- wave helpers
+__device__ inline int lane() { return (int)__lane_id(); }
+__device__ inline double wave_sum_f64(double x) {
+  for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o);
+  return x;
+}
+__device__ inline uint64_t wave_max_u64(uint64_t x) {
+  for (int o = 32; o >= 1; o >>= 1) {
+    const uint64_t y = (uint64_t)__shfl_xor((long long)x, o);
+    x = y > x ? y : x;
+  }
+  return x;
+}
+__device__ inline int first_lane(uint64_t m) { return __ffsll((long long)m) - 1; }
+
+// Neighbour-community table of vertex v over its row [a, b): self loops
+// skipped; with `parent`, only neighbours u with parent[u] == pv.  Returns the
+// number of entries (wave-uniform); *e_sum gets the summed weight of the
+// admitted entries (every lane).
+__device__ int build_table(int32_t* tc, double* ts, const int32_t* __restrict__ col,
+                           const float* __restrict__ wt, const int32_t* __restrict__ lab,
+                           const int32_t* __restrict__ parent, int32_t pv, int32_t v, int32_t a, int32_t b,
+                           double* e_sum) {
+  const int ln = lane();
+  int n = 0;
+  double e_acc = 0.0;
+  for (int32_t e0 = a; e0 < b; e0 += 64) {
+    const int32_t e = e0 + ln;
+    bool ok = e < b;
+    const int32_t u = ok ? col[e] : v;
+    ok = ok && u != v;
+    const float w = ok ? wt[e] : 0.0f;
+    if (parent) ok = ok && parent[u] == pv;
+    const int32_t c = ok ? lab[u] : -1;
+    if (ok) e_acc += (double)w;
+    uint64_t active = __ballot(ok);
+    while (active) {
+      const int32_t c0 = __shfl(c, first_lane(active));
+      const uint64_t m = __ballot(ok && c == c0);
+      const double s = wave_sum_f64(((m >> ln) & 1) ? (double)w : 0.0);
+      int idx = -1;
+      for (int j0 = 0; j0 < n; j0 += 64) {
+        const int j = j0 + ln;
+        const uint64_t hit = __ballot(j < n && tc[j] == c0);
+        if (hit) {
+          idx = j0 + first_lane(hit);
+          break;
+        }
+      }
+      if (idx < 0 && n < TABLE_CAP) {
+        idx = n++;
+        if (ln == 0) {
+          tc[idx] = c0;
+          ts[idx] = 0.0;
+        }
+      }
+      if (idx >= 0 && ln == 0) ts[idx] += s;
+      __builtin_amdgcn_wave_barrier();
+      active &= ~m;
+    }
+  }
+  *e_sum = wave_sum_f64(e_acc);
+  return n;
+}
+
+__device__ float table_lookup(const int32_t* tc, const double* ts, int n, int32_t c) {
+  for (int j0 = 0; j0 < n; j0 += 64) {
+    const int j = j0 + lane();
+    const uint64_t hit = __ballot(j < n && tc[j] == c);
+    if (hit) return (float)ts[j0 + first_lane(hit)];
+  }
+  return 0.0f;
+}
+
+// ----------------------------------------------------------------- CSR build
+__global__ void mirror_kernel(const int32_t* __restrict__ src, const int32_t* __restrict__ dst,
+                              const float* __restrict__ w, int64_t E, int32_t V, int bits,
+                              uint64_t* __restrict__ keys, float* __restrict__ vals) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= E) return;
+  const int32_t u = src[i], t = dst[i];
+  const float wi = w[i];
+  const uint64_t sentinel = (uint64_t)V << bits;
+  const bool ok = u >= 0 && u < V && t >= 0 && t < V;  // out-of-range edges are dropped
+  keys[2 * i] = ok ? ((uint64_t)u << bits) | (uint64_t)t : sentinel;
+  vals[2 * i] = u == t ? 2.0f * wi : wi;
+  keys[2 * i + 1] = (ok && u != t) ? ((uint64_t)t << bits) | (uint64_t)u : sentinel;
+  vals[2 * i + 1] = wi;
+}
+
+__global__ void row_ptr_kernel(const uint64_t* __restrict__ keys, int64_t n, int32_t V, int bits,
+                               int32_t* __restrict__ row_ptr) {
+  const int32_t v = blockIdx.x * blockDim.x + threadIdx.x;
+  if (v > V) return;
+  const uint64_t target = (uint64_t)v << bits;
+  int64_t lo = 0, hi = n;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    if (keys[mid] < target) lo = mid + 1;
+    else hi = mid;
+  }
+  row_ptr[v] = (int32_t)lo;
+}
+
+__global__ void col_kernel(const uint64_t* __restrict__ keys, int64_t n, int bits, int32_t* __restrict__ col) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) col[i] = (int32_t)(keys[i] & (((uint64_t)1 << bits) - 1));
+}
+
+__global__ void zero_kernel(double* __restrict__ two_m, int32_t G, double* __restrict__ modularity,
+                            int32_t* __restrict__ ctl) {
+  const int i = threadIdx.x;
+  for (int g = i; g < G; g += blockDim.x) {
+    two_m[g] = 0.0;
+    modularity[g] = 0.0;
+  }
+  if (i < CTL_WORDS) ctl[i] = i == CTL_UPDOWN ? 1 : 0;  // local moving starts with upward moves
+}
+
+__global__ __launch_bounds__(LTHREADS) void degree_kernel(const int32_t* __restrict__ row_ptr,
+                                                          const float* __restrict__ wt, int32_t V, int32_t S,
+                                                          double* __restrict__ k_v, double* __restrict__ two_m) {
+  const int32_t v = blockIdx.x * LWAVES + (threadIdx.x >> 6);
+  if (v >= V) return;
+  const int32_t a = row_ptr[v], b = row_ptr[v + 1];
+  double s = 0.0;
+  for (int32_t e = a + lane(); e < b; e += 64) s += (double)wt[e];
+  s = wave_sum_f64(s);
+  if (lane() == 0) {
+    k_v[v] = s;
+    if (s != 0.0) atomicAdd(two_m + v / S, s);
+  }
+}
+
+__global__ void identity_kernel(int32_t V, int32_t* __restrict__ labels) {
+  const int32_t v = blockIdx.x * blockDim.x + threadIdx.x;
+  if (v < V) labels[v] = v;
+}
+
+// ----------------------------------------------------------------- sweeps
+__global__ void sigma_zero_kernel(double* __restrict__ sigma, int32_t V, const int32_t* __restrict__ ctl) {
+  if (ctl && ctl[CTL_DONE]) return;
+  const int32_t v = blockIdx.x * blockDim.x + threadIdx.x;
+  if (v < V) sigma[v] = 0.0;
+}
+
+__global__ void sigma_scatter_kernel(const int32_t* __restrict__ labels, const double* __restrict__ k_v, int32_t V,
+                                     double* __restrict__ sigma, const int32_t* __restrict__ ctl) {
+  if (ctl && ctl[CTL_DONE]) return;
+  const int32_t v = blockIdx.x * blockDim.x + threadIdx.x;
+  if (v >= V) return;
+  const int32_t c = labels[v];
+  const double k = k_v[v];
+  if (c >= 0 && k != 0.0) atomicAdd(sigma + c, k);
+}
+
+struct Graph {
+  const int32_t* row_ptr;
+  const int32_t* col;
+  const float* wt;
+  const double* k_v;
+  const double* two_m;
+  int32_t V;
+  int32_t S;
+};
+
+__global__ __launch_bounds__(LTHREADS) void local_moving_kernel(Graph gr, const double* __restrict__ sigma,
+                                                                const int32_t* __restrict__ lin,
+                                                                int32_t* __restrict__ lout,
+                                                                int32_t* __restrict__ ctl, float resolution,
+                                                                uint32_t level, uint32_t sweep, uint32_t seed) {
+  __shared__ int32_t tab_c[LWAVES][TABLE_CAP];
+  __shared__ double tab_s[LWAVES][TABLE_CAP];
+  const int wv = threadIdx.x >> 6;
+  const int32_t v = blockIdx.x * LWAVES + wv;
+  if (v >= gr.V) return;
+  const int32_t old = lin[v];
+  const bool done = ctl[CTL_DONE] != 0;
+  const int32_t a = gr.row_ptr[v], b = gr.row_ptr[v + 1];
+  const int32_t g = v / gr.S;
+  const double tm = gr.two_m[g];
+  if (done || a == b || !(tm > 0.0)) {
+    if (lane() == 0) lout[v] = old;
+    return;
+  }
+  const int up_down = ctl[CTL_UPDOWN];
+  double e_sum;
+  const int n = build_table(tab_c[wv], tab_s[wv], gr.col, gr.wt, lin, nullptr, 0, v, a, b, &e_sum);
+  const float k_old = table_lookup(tab_c[wv], tab_s[wv], n, old);
+  const double kv = gr.k_v[v];
+  const double m_g = 0.5 * tm;
+  const double inv_m = 1.0 / m_g;
+  const double inv_2m2 = 1.0 / (2.0 * m_g * m_g);
+  const double sig_old_excl = sigma[old] - kv;
+  const float jitter = (rand_uniform((uint32_t)g, (uint32_t)v, level, sweep, seed) - 0.5f) * 1e-9f;
+  uint64_t mine = 0;
+  int32_t mine_c = old;
+  for (int j = lane(); j < n; j += 64) {
+    const int32_t c = tab_c[wv][j];
+    if (c == old || (c > old ? 1 : 0) != up_down) continue;
+    const float kn = (float)tab_s[wv][j];
+    const double dq = ((double)kn - (double)k_old) * inv_m
+                      + (double)resolution * kv * (sig_old_excl - sigma[c]) * inv_2m2;
+    const float dqf = (float)dq + jitter;
+    const uint64_t p = pack(dqf, cand_pref(c));
+    if (p > mine) {
+      mine = p;
+      mine_c = c;
+    }
+  }
+  const uint64_t best = wave_max_u64(mine);
+  int32_t choice = old;
+  if (best > pack(0.0f, STAY_PREF)) choice = __shfl(mine_c, first_lane(__ballot(mine == best)));
+  if (lane() == 0) {
+    lout[v] = choice;
+    if (choice != old) atomicAdd(ctl + CTL_MOVED, 1);
+  }
+}
+
+// After a local-moving sweep: a stalled sweep flips the direction, two in a
+// row end local moving (leiden.cu:113-135).
+__global__ void lm_control_kernel(int32_t* __restrict__ ctl) {
+  if (threadIdx.x != 0) return;
+  if (!ctl[CTL_DONE]) {
+    if (ctl[CTL_MOVED] == 0) {
+      ctl[CTL_UPDOWN] ^= 1;
+      if (++ctl[CTL_STALE] >= 2) ctl[CTL_DONE] = 1;
+    } else {
+      ctl[CTL_STALE] = 0;
+    }
+  }
+  ctl[CTL_MOVED] = 0;
+}
+
+__global__ void refine_init_kernel(const int32_t* __restrict__ lm, int32_t V, int32_t* __restrict__ parent,
+                                   int32_t* __restrict__ labels, int32_t* __restrict__ ctl) {
+  const int32_t v = blockIdx.x * blockDim.x + threadIdx.x;
+  if (v < V) {
+    parent[v] = lm[v];
+    labels[v] = v;
+  }
+  if (v < CTL_WORDS) ctl[v] = 0;
+}
+
+__global__ __launch_bounds__(LTHREADS) void refine_propose_kernel(
+    Graph gr, const int32_t* __restrict__ parent, const double* __restrict__ sigma,
+    const double* __restrict__ parent_sigma, const int32_t* __restrict__ lin, int32_t* __restrict__ prop,
+    uint32_t* __restrict__ rank, const int32_t* __restrict__ ctl, float resolution, float inv_theta,
+    int boltzmann, uint32_t level, uint32_t sweep, uint32_t seed) {
+  __shared__ int32_t tab_c[LWAVES][TABLE_CAP];
+  __shared__ double tab_s[LWAVES][TABLE_CAP];
+  const int wv = threadIdx.x >> 6;
+  const int32_t v = blockIdx.x * LWAVES + wv;
+  if (v >= gr.V || ctl[CTL_DONE]) return;
+  const int32_t g = v / gr.S;
+  if (lane() == 0) rank[v] = mix4((uint32_t)g, (uint32_t)v, (level << 16) | sweep, seed);
+  const int32_t old = lin[v];
+  const int32_t a = gr.row_ptr[v], b = gr.row_ptr[v + 1];
+  const double tm = gr.two_m[g];
+  if (a == b || !(tm > 0.0)) {
+    if (lane() == 0) prop[v] = old;
+    return;
+  }
+  const int32_t pv = parent[v];
+  double e_sum;
+  const int n = build_table(tab_c[wv], tab_s[wv], gr.col, gr.wt, lin, parent, pv, v, a, b, &e_sum);
+  const double kv = gr.k_v[v];
+  double vol_minus = parent_sigma[pv] - kv;
+  if (vol_minus < 0.0) vol_minus = 0.0;
+  const double bound = (double)resolution * kv * vol_minus / tm;
+  if ((double)(float)e_sum < bound) {  // {v} is not well connected to its parent community
+    if (lane() == 0) prop[v] = old;
+    return;
+  }
+  const float k_old = table_lookup(tab_c[wv], tab_s[wv], n, old);
+  const double m_g = 0.5 * tm;
+  const double inv_m = 1.0 / m_g;
+  const double inv_2m2 = 1.0 / (2.0 * m_g * m_g);
+  const double sig_old_excl = sigma[old] - kv;
+  uint64_t mine = 0;
+  int32_t mine_c = old;
+  for (int j = lane(); j < n; j += 64) {
+    const int32_t c = tab_c[wv][j];
+    if (c == old) continue;
+    const float kn = (float)tab_s[wv][j];
+    const double dq = ((double)kn - (double)k_old) * inv_m
+                      + (double)resolution * kv * (sig_old_excl - sigma[c]) * inv_2m2;
+    if (dq < 0.0) continue;
+    const float score = boltzmann
+        ? (float)(dq * (double)inv_theta)
+              + gumbel(rand_uniform_pair((uint32_t)g, (uint32_t)v, (uint32_t)c, level, sweep, seed))
+        : (float)dq;
+    const uint64_t p = pack(score, cand_pref(c));
+    if (p > mine) {
+      mine = p;
+      mine_c = c;
+    }
+  }
+  const uint64_t best = wave_max_u64(mine);
+  const float stay = boltzmann
+      ? gumbel(rand_uniform_pair((uint32_t)g, (uint32_t)v, (uint32_t)old, level, sweep, seed))
+      : 0.0f;
+  int32_t choice = old;
+  if (best > pack(stay, STAY_PREF)) choice = __shfl(mine_c, first_lane(__ballot(mine == best)));
+  if (lane() == 0) prop[v] = choice;
+}
+
+// Commit an independent set of the proposals: a mover commits unless a
+// moving neighbour in its parent community outranks it on (rank, id)
+// (refinement.cu:263-300).
+__global__ __launch_bounds__(LTHREADS) void refine_commit_kernel(
+    Graph gr, const int32_t* __restrict__ parent, const int32_t* __restrict__ lin,
+    const int32_t* __restrict__ prop, const uint32_t* __restrict__ rank, int32_t* __restrict__ lout,
+    int32_t* __restrict__ ctl) {
+  const int32_t v = blockIdx.x * LWAVES + (threadIdx.x >> 6);
+  if (v >= gr.V) return;
+  const int32_t old = lin[v];
+  if (ctl[CTL_DONE]) {
+    if (lane() == 0) lout[v] = old;
+    return;
+  }
+  const int32_t p = prop[v];
+  if (p == old) {
+    if (lane() == 0) lout[v] = old;
+    return;
+  }
+  const int32_t pv = parent[v];
+  const uint32_t rv = rank[v];
+  const int32_t a = gr.row_ptr[v], b = gr.row_ptr[v + 1];
+  bool lost = false;
+  for (int32_t e = a + lane(); e < b; e += 64) {
+    const int32_t u = gr.col[e];
+    if (u == v || parent[u] != pv || prop[u] == lin[u]) continue;
+    const uint32_t ru = rank[u];
+    lost = lost || ru > rv || (ru == rv && u > v);
+  }
+  const bool any_lost = __ballot(lost) != 0;
+  if (lane() == 0) {
+    lout[v] = any_lost ? old : p;
+    if (!any_lost) atomicAdd(ctl + CTL_MOVED, 1);
+  }
+}
+
+__global__ void refine_control_kernel(int32_t* __restrict__ ctl) {
+  if (threadIdx.x != 0) return;
+  if (!ctl[CTL_DONE] && ctl[CTL_MOVED] == 0) ctl[CTL_DONE] = 1;
+  ctl[CTL_MOVED] = 0;
+}
+
+// Q_g = sum_v [in(v) / 2m - gamma k_v Sigma[c_v] / (4 m^2)] (helpers.cu:41-78).
+__global__ __launch_bounds__(LTHREADS) void modularity_kernel(Graph gr, const int32_t* __restrict__ labels,
+                                                              const double* __restrict__ sigma, float resolution,
+                                                              double* __restrict__ modularity) {
+  const int32_t v = blockIdx.x * LWAVES + (threadIdx.x >> 6);
+  if (v >= gr.V) return;
+  const int32_t g = v / gr.S;
+  const double tm = gr.two_m[g];
+  if (!(tm > 0.0)) return;
+  const int32_t cv = labels[v];
+  const int32_t a = gr.row_ptr[v], b = gr.row_ptr[v + 1];
+  double in_sum = 0.0;
+  for (int32_t e = a + lane(); e < b; e += 64)
+    if (labels[gr.col[e]] == cv) in_sum += (double)gr.wt[e];
+  in_sum = wave_sum_f64(in_sum);
+  if (lane() == 0) {
+    const double m_g = 0.5 * tm;
+    const double q = in_sum / tm - (double)resolution * (gr.k_v[v] * sigma[cv]) / (4.0 * m_g * m_g);
+    if (q != 0.0) atomicAdd(modularity + g, q);
+  }
+}
+
+__global__ void finish_kernel(const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ result, int32_t V,
+                              int32_t* __restrict__ labels) {
+  const int32_t v = blockIdx.x * blockDim.x + threadIdx.x;
+  if (v < V) labels[v] = row_ptr[v] == row_ptr[v + 1] ? -1 : result[v];
+}
+
+// ----------------------------------------------------------------- aggregation / densify
+__global__ void remap_kernel(const int32_t* __restrict__ src, const int32_t* __restrict__ dst,
+                             const float* __restrict__ w, const int32_t* __restrict__ labels, int64_t E,
+                             int32_t Vs, int bits, uint64_t* __restrict__ keys, float* __restrict__ vals) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= E) return;
+  int32_t s = labels[src[i]], t = labels[dst[i]];
+  const int32_t lo = s < t ? s : t, hi = s < t ? t : s;
+  const bool ok = lo >= 0 && hi < Vs;
+  keys[i] = ok ? ((uint64_t)lo << bits) | (uint64_t)hi : ((uint64_t)Vs << bits);
+  vals[i] = ok ? w[i] : 0.0f;
+}
+
+__global__ void unpack_kernel(const uint64_t* __restrict__ keys, int64_t E, int bits,
+                              const int64_t* __restrict__ count, int32_t* __restrict__ out_src,
+                              int32_t* __restrict__ out_dst) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= *count) return;
+  const uint64_t k = keys[i];
+  out_src[i] = (int32_t)(k >> bits);
+  out_dst[i] = (int32_t)(k & (((uint64_t)1 << bits) - 1));
+}
+
+// Edges with an endpoint label outside [0, Vs) carry the sentinel key, which
+// sorts last: drop that run from the count.
+__global__ void count_fix_kernel(const uint64_t* __restrict__ keys, int32_t Vs, int bits, int64_t* __restrict__ count) {
+  if (threadIdx.x != 0) return;
+  const int64_t n = *count;
+  if (n > 0 && (keys[n - 1] >> bits) >= (uint64_t)Vs) *count = n - 1;
+}
+
+__global__ void flag_zero_kernel(int32_t* __restrict__ flags, int32_t V) {
+  const int32_t v = blockIdx.x * blockDim.x + threadIdx.x;
+  if (v < V) flags[v] = 0;
+}
+
+// Labels below zero stand for the vertex itself; labels outside the vertex's
+// graph are ignored (their vertices get rank -1 in the apply step).
+__device__ inline int32_t own_label(const int32_t* labels, int32_t v, int32_t S) {
+  const int32_t l = labels[v] < 0 ? v : labels[v];
+  return (l / S == v / S) ? l : -1;
+}
+
+__global__ void flag_mark_kernel(const int32_t* __restrict__ labels, int32_t V, int32_t S,
+                                 int32_t* __restrict__ flags) {
+  const int32_t v = blockIdx.x * blockDim.x + threadIdx.x;
+  if (v >= V) return;
+  const int32_t l = own_label(labels, v, S);
+  if (l >= 0) flags[l] = 1;
+}
+
+__global__ void densify_count_kernel(const int32_t* __restrict__ flags, const int32_t* __restrict__ scan, int32_t G,
+                                     int32_t S, int32_t* __restrict__ counts) {
+  const int32_t g = blockIdx.x * blockDim.x + threadIdx.x;
+  if (g < G) {
+    const int32_t last = (g + 1) * S - 1;
+    counts[g] = scan[last] + flags[last] - scan[g * S];
+  }
+}
+
+__global__ void densify_apply_kernel(const int32_t* __restrict__ labels, const int32_t* __restrict__ scan, int32_t V,
+                                     int32_t S, int32_t new_S, int32_t* __restrict__ dense) {
+  const int32_t v = blockIdx.x * blockDim.x + threadIdx.x;
+  if (v >= V) return;
+  const int32_t g = v / S;
+  const int32_t l = own_label(labels, v, S);
+  dense[v] = l < 0 ? -1 : scan[l] - scan[g * S] + g * new_S;
+}
+
+// ----------------------------------------------------------------- host side
+inline int bits_for(uint64_t x) {  // bits needed to hold values 0..x
+  int b = 1;
+  while (b < 63 && (x >> b) != 0) ++b;
+  return b;
+}
+inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+inline unsigned blocks(int64_t n, int t) { return (unsigned)((n + t - 1) / t); }
+
+int launch_check() {
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? 0 : ckv_internal::set_error(CKV_E_LAUNCH, hipGetErrorString(e));
+}
+
+struct LeidenLayout {
+  size_t keys_a, keys_b, vals_a, vals_b, temp, temp_bytes, row_ptr, col, k_v, two_m, sigma, psigma, lab_a, lab_b,
+      parent, prop, rank, ctl, total;
+};
+
+LeidenLayout leiden_layout(int64_t E, int32_t G, int32_t S) {
+  LeidenLayout L{};
+  const int64_t n = 2 * E;
+  const int64_t V = (int64_t)G * S;
+  size_t temp_bytes = 0;
+  if (n > 0)
+    (void)hipcub::DeviceRadixSort::SortPairs(nullptr, temp_bytes, (uint64_t*)nullptr, (uint64_t*)nullptr,
+                                       (float*)nullptr, (float*)nullptr, (int)n, 0, 64, (hipStream_t)0);
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = off;
+    off += align256(bytes);
+    return at;
+  };
+  L.keys_a = take(n * 8);
+  L.keys_b = take(n * 8);
+  L.vals_a = take(n * 4);
+  L.vals_b = take(n * 4);
+  L.temp_bytes = temp_bytes;
+  L.temp = take(temp_bytes);
+  L.row_ptr = take((V + 1) * 4);
+  L.col = take(n * 4);
+  L.k_v = take(V * 8);
+  L.two_m = take(G * 8);
+  L.sigma = take(V * 8);
+  L.psigma = take(V * 8);
+  L.lab_a = take(V * 4);
+  L.lab_b = take(V * 4);
+  L.parent = take(V * 4);
+  L.prop = take(V * 4);
+  L.rank = take(V * 4);
+  L.ctl = take(CTL_WORDS * 4);
+  L.total = off;
+  return L;
+}
+
+struct AggLayout {
+  size_t keys_a, keys_b, vals_a, uniq, temp, temp_bytes, total;
+};
+
+AggLayout agg_layout(int64_t E) {
+  AggLayout L{};
+  size_t sort_bytes = 0, red_bytes = 0;
+  if (E > 0) {
+    (void)hipcub::DeviceRadixSort::SortPairs(nullptr, sort_bytes, (uint64_t*)nullptr, (uint64_t*)nullptr, (float*)nullptr,
+                                       (float*)nullptr, (int)E, 0, 64, (hipStream_t)0);
+    (void)hipcub::DeviceReduce::ReduceByKey(nullptr, red_bytes, (uint64_t*)nullptr, (uint64_t*)nullptr, (float*)nullptr,
+                                      (float*)nullptr, (int64_t*)nullptr, hipcub::Sum(), (int)E, (hipStream_t)0);
+  }
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = off;
+    off += align256(bytes);
+    return at;
+  };
+  L.keys_a = take(E * 8);
+  L.keys_b = take(E * 8);
+  L.vals_a = take(E * 4 * 2);  // values in, sorted values
+  L.uniq = take(E * 8);
+  L.temp_bytes = sort_bytes > red_bytes ? sort_bytes : red_bytes;
+  L.temp = take(L.temp_bytes);
+  L.total = off;
+  return L;
+}
+
+size_t densify_temp_bytes(int64_t V) {
+  size_t bytes = 0;
+  (void)hipcub::DeviceScan::ExclusiveSum(nullptr, bytes, (int32_t*)nullptr, (int32_t*)nullptr, (int)V, (hipStream_t)0);
+  return bytes;
+}
+
+}  // namespace
+}  // namespace ckv
+
+using namespace ckv;
+
+extern "C" size_t ckv_leiden_workspace_bytes(int64_t edges, int32_t graphs, int32_t seq_len) {
+  if (edges < 0 || graphs <= 0 || seq_len <= 0) return 0;
+  return leiden_layout(edges, graphs, seq_len).total;
+}
+
+extern "C" int ckv_batched_leiden(const int32_t* edge_src, const int32_t* edge_dst, const float* edge_weight,
+                                  int64_t edges, int32_t graphs, int32_t seq_len, float resolution, float theta,
+                                  int32_t max_inner_iter, int32_t seed, int32_t use_boltzmann, int32_t* labels,
+                                  double* modularity, void* workspace, void* stream) {
+  if (graphs <= 0 || seq_len <= 0) return ckv_internal::set_error(CKV_E_INVALID, "graphs and seq_len must be positive");
+  if (!labels || !modularity) return ckv_internal::set_error(CKV_E_INVALID, "null Leiden output");
+  if (edges < 0 || (edges > 0 && (!edge_src || !edge_dst || !edge_weight || !workspace)))
+    return ckv_internal::set_error(CKV_E_INVALID, "Leiden edges need src, dst, weight and a workspace");
+  const int64_t V64 = (int64_t)graphs * seq_len;
+  if (V64 >= (int64_t)1 << 30 || 2 * edges >= ((int64_t)1 << 31) - 1)
+    return ckv_internal::set_error(CKV_E_LIMIT, "Leiden graph too large (vertices < 2^30, 2 * edges < 2^31)");
+  if (max_inner_iter < 0) return ckv_internal::set_error(CKV_E_INVALID, "max_inner_iter must be nonnegative");
+  hipStream_t st = (hipStream_t)stream;
+  const int32_t V = (int32_t)V64;
+  if (edges == 0) {
+    // leiden.cu:68-76: every vertex isolated, modularity 0
+    if (hipMemsetAsync(labels, 0xFF, (size_t)V * 4, st) != hipSuccess ||
+        hipMemsetAsync(modularity, 0, (size_t)graphs * 8, st) != hipSuccess)
+      return launch_check();
+    return 0;
+  }
+  const LeidenLayout L = leiden_layout(edges, graphs, seq_len);
+  char* ws = (char*)workspace;
+  uint64_t* keys_a = (uint64_t*)(ws + L.keys_a);
+  uint64_t* keys_b = (uint64_t*)(ws + L.keys_b);
+  float* vals_a = (float*)(ws + L.vals_a);
+  float* vals_b = (float*)(ws + L.vals_b);
+  int32_t* row_ptr = (int32_t*)(ws + L.row_ptr);
+  int32_t* col = (int32_t*)(ws + L.col);
+  double* k_v = (double*)(ws + L.k_v);
+  double* two_m = (double*)(ws + L.two_m);
+  double* sigma = (double*)(ws + L.sigma);
+  double* psigma = (double*)(ws + L.psigma);
+  int32_t* lab[2] = {(int32_t*)(ws + L.lab_a), (int32_t*)(ws + L.lab_b)};
+  int32_t* parent = (int32_t*)(ws + L.parent);
+  int32_t* prop = (int32_t*)(ws + L.prop);
+  uint32_t* rank = (uint32_t*)(ws + L.rank);
+  int32_t* ctl = (int32_t*)(ws + L.ctl);
+
+  const int bits = bits_for((uint64_t)V - 1);
+  const int end_bit = bits + bits_for((uint64_t)V);
+  const int64_t n = 2 * edges;
+  mirror_kernel<<<blocks(edges, ETHREADS), ETHREADS, 0, st>>>(edge_src, edge_dst, edge_weight, edges, V, bits, keys_a,
+                                                             vals_a);
+  size_t temp_bytes = L.temp_bytes;
+  if (hipcub::DeviceRadixSort::SortPairs(ws + L.temp, temp_bytes, keys_a, keys_b, vals_a, vals_b, (int)n, 0, end_bit,
+                                         st) != hipSuccess)
+    return ckv_internal::set_error(CKV_E_LAUNCH, "Leiden CSR sort failed");
+  row_ptr_kernel<<<blocks(V + 1, ETHREADS), ETHREADS, 0, st>>>(keys_b, n, V, bits, row_ptr);
+  col_kernel<<<blocks(n, ETHREADS), ETHREADS, 0, st>>>(keys_b, n, bits, col);
+  zero_kernel<<<1, 256, 0, st>>>(two_m, graphs, modularity, ctl);
+  const unsigned vgrid = blocks(V, LWAVES);
+  degree_kernel<<<vgrid, LTHREADS, 0, st>>>(row_ptr, vals_b, V, seq_len, k_v, two_m);
+  identity_kernel<<<blocks(V, ETHREADS), ETHREADS, 0, st>>>(V, lab[0]);
+  const Graph gr{row_ptr, col, vals_b, k_v, two_m, V, seq_len};
+
+  const unsigned egrid = blocks(V, ETHREADS);
+  int cur = 0;
+  for (int sweep = 0; sweep < max_inner_iter; ++sweep) {
+    sigma_zero_kernel<<<egrid, ETHREADS, 0, st>>>(sigma, V, ctl);
+    sigma_scatter_kernel<<<egrid, ETHREADS, 0, st>>>(lab[cur], k_v, V, sigma, ctl);
+    local_moving_kernel<<<vgrid, LTHREADS, 0, st>>>(gr, sigma, lab[cur], lab[cur ^ 1], ctl, resolution, 0u,
+                                                    (uint32_t)sweep, (uint32_t)seed);
+    lm_control_kernel<<<1, 64, 0, st>>>(ctl);
+    cur ^= 1;
+  }
+  // refinement from singletons inside the local-moving communities
+  refine_init_kernel<<<egrid, ETHREADS, 0, st>>>(lab[cur], V, parent, lab[cur ^ 1], ctl);
+  cur ^= 1;
+  sigma_zero_kernel<<<egrid, ETHREADS, 0, st>>>(psigma, V, nullptr);
+  sigma_scatter_kernel<<<egrid, ETHREADS, 0, st>>>(parent, k_v, V, psigma, nullptr);
+  const float t = theta > 0.0f ? theta : 1.0e-3f;
+  const float inv_theta = 1.0f / t;
+  for (int sweep = 0; sweep < max_inner_iter; ++sweep) {
+    sigma_zero_kernel<<<egrid, ETHREADS, 0, st>>>(sigma, V, ctl);
+    sigma_scatter_kernel<<<egrid, ETHREADS, 0, st>>>(lab[cur], k_v, V, sigma, ctl);
+    refine_propose_kernel<<<vgrid, LTHREADS, 0, st>>>(gr, parent, sigma, psigma, lab[cur], prop, rank, ctl,
+                                                      resolution, inv_theta, use_boltzmann ? 1 : 0, 1u,
+                                                      (uint32_t)sweep, (uint32_t)seed);
+    refine_commit_kernel<<<vgrid, LTHREADS, 0, st>>>(gr, parent, lab[cur], prop, rank, lab[cur ^ 1], ctl);
+    refine_control_kernel<<<1, 64, 0, st>>>(ctl);
+    cur ^= 1;
+  }
+  sigma_zero_kernel<<<egrid, ETHREADS, 0, st>>>(sigma, V, nullptr);
+  sigma_scatter_kernel<<<egrid, ETHREADS, 0, st>>>(lab[cur], k_v, V, sigma, nullptr);
+  modularity_kernel<<<vgrid, LTHREADS, 0, st>>>(gr, lab[cur], sigma, resolution, modularity);
+  finish_kernel<<<egrid, ETHREADS, 0, st>>>(row_ptr, lab[cur], V, labels);
+  return launch_check();
+}
+
+extern "C" size_t ckv_aggregate_coo_workspace_bytes(int64_t edges) {
+  return edges <= 0 ? 0 : agg_layout(edges).total;
+}
+
+extern "C" int ckv_aggregate_coo(const int32_t* edge_src, const int32_t* edge_dst, const float* edge_weight,
+                                 int64_t edges, const int32_t* labels, int32_t super_vertices, int32_t* out_src,
+                                 int32_t* out_dst, float* out_weight, int64_t* out_count, void* workspace,
+                                 void* stream) {
+  if (edges < 0 || super_vertices <= 0 || !out_count)
+    return ckv_internal::set_error(CKV_E_INVALID, "bad aggregation sizes");
+  hipStream_t st = (hipStream_t)stream;
+  if (edges == 0) {
+    if (hipMemsetAsync(out_count, 0, 8, st) != hipSuccess) return launch_check();
+    return 0;
+  }
+  if (!edge_src || !edge_dst || !edge_weight || !labels || !out_src || !out_dst || !out_weight || !workspace)
+    return ckv_internal::set_error(CKV_E_INVALID, "null aggregation pointer");
+  if (edges >= ((int64_t)1 << 31) - 1 || super_vertices >= (1 << 30))
+    return ckv_internal::set_error(CKV_E_LIMIT, "aggregation too large");
+  const AggLayout L = agg_layout(edges);
+  char* ws = (char*)workspace;
+  uint64_t* keys_a = (uint64_t*)(ws + L.keys_a);
+  uint64_t* keys_b = (uint64_t*)(ws + L.keys_b);
+  float* vals_in = (float*)(ws + L.vals_a);
+  float* vals_sorted = vals_in + edges;
+  uint64_t* uniq = (uint64_t*)(ws + L.uniq);
+  const int bits = bits_for((uint64_t)super_vertices - 1);
+  const int end_bit = bits + bits_for((uint64_t)super_vertices);
+  remap_kernel<<<blocks(edges, ETHREADS), ETHREADS, 0, st>>>(edge_src, edge_dst, edge_weight, labels, edges,
+                                                             super_vertices, bits, keys_a, vals_in);
+  size_t temp_bytes = L.temp_bytes;
+  if (hipcub::DeviceRadixSort::SortPairs(ws + L.temp, temp_bytes, keys_a, keys_b, vals_in, vals_sorted, (int)edges, 0,
+                                         end_bit, st) != hipSuccess)
+    return ckv_internal::set_error(CKV_E_LAUNCH, "aggregation sort failed");
+  temp_bytes = L.temp_bytes;
+  if (hipcub::DeviceReduce::ReduceByKey(ws + L.temp, temp_bytes, keys_b, uniq, vals_sorted, out_weight, out_count,
+                                        hipcub::Sum(), (int)edges, st) != hipSuccess)
+    return ckv_internal::set_error(CKV_E_LAUNCH, "aggregation reduce failed");
+  count_fix_kernel<<<1, 64, 0, st>>>(uniq, super_vertices, bits, out_count);
+  unpack_kernel<<<blocks(edges, ETHREADS), ETHREADS, 0, st>>>(uniq, edges, bits, out_count, out_src, out_dst);
+  return launch_check();
+}
+
+extern "C" size_t ckv_densify_workspace_bytes(int32_t graphs, int32_t seq_len) {
+  if (graphs <= 0 || seq_len <= 0) return 0;
+  const int64_t V = (int64_t)graphs * seq_len;
+  return 2 * align256((size_t)V * 4) + align256(densify_temp_bytes(V));
+}
+
+extern "C" int ckv_densify_count(const int32_t* labels, int32_t graphs, int32_t seq_len, int32_t* counts,
+                                 void* workspace, void* stream) {
+  if (!labels || !counts || !workspace || graphs <= 0 || seq_len <= 0)
+    return ckv_internal::set_error(CKV_E_INVALID, "bad densify arguments");
+  const int64_t V64 = (int64_t)graphs * seq_len;
+  if (V64 >= (int64_t)1 << 30) return ckv_internal::set_error(CKV_E_LIMIT, "densify: too many vertices");
+  const int32_t V = (int32_t)V64;
+  hipStream_t st = (hipStream_t)stream;
+  int32_t* flags = (int32_t*)workspace;
+  int32_t* scan = (int32_t*)((char*)workspace + align256((size_t)V * 4));
+  void* temp = (char*)workspace + 2 * align256((size_t)V * 4);
+  size_t temp_bytes = densify_temp_bytes(V);
+  flag_zero_kernel<<<blocks(V, ETHREADS), ETHREADS, 0, st>>>(flags, V);
+  flag_mark_kernel<<<blocks(V, ETHREADS), ETHREADS, 0, st>>>(labels, V, seq_len, flags);
+  if (hipcub::DeviceScan::ExclusiveSum(temp, temp_bytes, flags, scan, V, st) != hipSuccess)
+    return ckv_internal::set_error(CKV_E_LAUNCH, "densify scan failed");
+  densify_count_kernel<<<blocks(graphs, ETHREADS), ETHREADS, 0, st>>>(flags, scan, graphs, seq_len, counts);
+  return launch_check();
+}
+
+extern "C" int ckv_densify_apply(const int32_t* labels, int32_t graphs, int32_t seq_len, int32_t new_seq_len,
+                                 int32_t* dense, const void* workspace, void* stream) {
+  if (!labels || !dense || !workspace || graphs <= 0 || seq_len <= 0 || new_seq_len <= 0)
+    return ckv_internal::set_error(CKV_E_INVALID, "bad densify arguments");
+  const int64_t V64 = (int64_t)graphs * seq_len;
+  if (V64 >= (int64_t)1 << 30 || (int64_t)graphs * new_seq_len >= (int64_t)1 << 30)
+    return ckv_internal::set_error(CKV_E_LIMIT, "densify: too many vertices");
+  const int32_t V = (int32_t)V64;
+  const int32_t* scan = (const int32_t*)((const char*)workspace + align256((size_t)V * 4));
+  densify_apply_kernel<<<blocks(V, ETHREADS), ETHREADS, 0, (hipStream_t)stream>>>(labels, scan, V, seq_len,
+                                                                                   new_seq_len, dense);
+  return launch_check();
+}

@@ -66,7 +66,8 @@ class StateBuild:
     def __init__(self, community_ids: torch.Tensor, keys: torch.Tensor, *, retrieval_to_graph: torch.Tensor,
                  retrieval_to_kv: torch.Tensor, num_sink: int, max_decode_tokens: int, fp8: bool = True,
                  edges: tuple[torch.Tensor, torch.Tensor, torch.Tensor] | None = None,
-                 token_capacity: int | None = None, topk_edges: "TopkEdges | None" = None):
+                 token_capacity: int | None = None, topk_edges: "TopkEdges | None" = None,
+                 count_sink_labels: bool = False):
         device = nat.require_device(community_ids, keys, retrieval_to_graph, retrieval_to_kv)
         if edges is not None and topk_edges is not None:
             raise ValueError("give either an edge list or top-k edges")
@@ -81,7 +82,7 @@ class StateBuild:
             raise TypeError("aggregation mappings must be int32")
         self.device = device
         self.ids = community_ids.to(torch.int32).contiguous()
-        counts = label_counts(self.ids, num_sink=num_sink)
+        counts = label_counts(self.ids, num_sink=0 if count_sink_labels else num_sink)
         host_counts = counts.cpu()
         if int(host_counts.min()) < 0:
             raise ValueError("community labels of non-sink positions must be nonnegative")
@@ -154,16 +155,19 @@ class StateBuild:
 def build_layer_state(community_ids: torch.Tensor, keys: torch.Tensor, *, retrieval_to_graph: torch.Tensor,
                       retrieval_to_kv: torch.Tensor, num_sink: int, max_decode_tokens: int, fp8: bool = True,
                       edges: tuple[torch.Tensor, torch.Tensor, torch.Tensor] | None = None,
-                      token_capacity: int | None = None, topk_edges: "TopkEdges | None" = None) -> LayerStateTensors:
+                      token_capacity: int | None = None, topk_edges: "TopkEdges | None" = None,
+                      count_sink_labels: bool = False) -> LayerStateTensors:
     """Every prefill state tensor of one layer from labels ``[graphs, S]`` and
     keys ``[Hkv, S, 128]`` (bf16 or f32, token stride may exceed 128).  Reads
     the community counts back once to size the outputs, as the reference
-    does with ``.item()``.  (The workspace and edge copies return to the
+    does with ``.item()``.  ``count_sink_labels`` counts communities over all
+    positions (sinks included) instead of the non-sink ones.  (The workspace and edge copies return to the
     caching allocator on this stream, so later work on it cannot overwrite
     them before the launches run.)"""
     return StateBuild(community_ids, keys, retrieval_to_graph=retrieval_to_graph, retrieval_to_kv=retrieval_to_kv,
                       num_sink=num_sink, max_decode_tokens=max_decode_tokens, fp8=fp8, edges=edges,
-                      token_capacity=token_capacity, topk_edges=topk_edges).run()
+                      token_capacity=token_capacity, topk_edges=topk_edges,
+                      count_sink_labels=count_sink_labels).run()
 
 
 __all__ = ["LayerStateTensors", "StateBuild", "TopkEdges", "build_layer_state", "label_counts"]

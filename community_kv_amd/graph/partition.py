@@ -4,9 +4,10 @@ These builders run once per request (not per token).  They turn per-token
 community labels and the prefill keys into the tensors the decode kernels use:
 FP8 centroids with decode headroom, the recency-descending member CSR, and the
 modularity weights.  ``build_adjacency`` restates the reference's top-k edge
-graph.  Leiden itself (``partition_graphs``) is outside this build: callers
-supply labels through ``build_layer_from_labels`` or a ``PartitionRuntime``
-label provider.
+graph; ``partition_graphs`` runs the native batched Leiden on it
+(``graph.leiden``) and ``build_partitioned_layer`` chains the two with the
+state build.  Callers may also supply labels directly through
+``build_layer_from_labels`` or a ``PartitionRuntime`` label provider.
 """
 
 from __future__ import annotations
@@ -181,12 +182,16 @@ def build_layer_from_labels(*, layer_idx: int, community_ids: torch.Tensor, keys
                             num_sink: int, max_decode_tokens: int, query_heads: int,
                             aggregation: GraphAggregation = GraphAggregation.PER_QUERY_HEAD,
                             edges: tuple[torch.Tensor, torch.Tensor, torch.Tensor] | None = None,
-                            fp8: bool = True, topk_edges: Any = None) -> PartitionedLayer:
+                            fp8: bool = True, topk_edges: Any = None,
+                            count_sink_labels: bool = False) -> PartitionedLayer:
     """Everything ``build_partitioned_layer`` (partition.py:538-618) produces
     after Leiden, from given dense labels ``community_ids [graphs, S]``.  The
     modularity weights come from ``edges`` (a coalesced edge list) or from
     ``topk_edges`` (a ``graph.kernels.state_build.TopkEdges``: the prefill
-    top-k edges, device tensors only), or are zero."""
+    top-k edges, device tensors only), or are zero.  The community count is
+    1 + the largest non-sink label, or, with ``count_sink_labels``, 1 + the
+    largest label of any position (the reference's count after Leiden, whose
+    sink singletons may carry the largest ids)."""
     if max_decode_tokens <= 0:
         raise ValueError("max_decode_tokens must be positive")
     kv_heads, seq_len, _ = keys.shape
@@ -200,7 +205,8 @@ def build_layer_from_labels(*, layer_idx: int, community_ids: torch.Tensor, keys
         from community_kv_amd.graph.kernels.state_build import build_layer_state
 
         st = build_layer_state(ids, keys, retrieval_to_graph=to_graph, retrieval_to_kv=to_kv, num_sink=num_sink,
-                               max_decode_tokens=max_decode_tokens, fp8=fp8, edges=edges, topk_edges=topk_edges)
+                               max_decode_tokens=max_decode_tokens, fp8=fp8, edges=edges, topk_edges=topk_edges,
+                               count_sink_labels=count_sink_labels)
         return PartitionedLayer(layer_idx=layer_idx, prefill_seq_len=seq_len, aggregation=aggregation,
                                 query_heads=query_heads, kv_heads=kv_heads, retrieval_to_graph=to_graph,
                                 retrieval_to_kv=to_kv, member_offsets=st.member_offsets,
@@ -210,7 +216,7 @@ def build_layer_from_labels(*, layer_idx: int, community_ids: torch.Tensor, keys
                                 token_communities=st.token_communities)
     if topk_edges is not None:
         raise ValueError("top-k edges are taken by the device state build only; pass a coalesced edge list")
-    counts = (ids[:, num_sink:].amax(dim=1) + 1).to(torch.int32)
+    counts = (ids[:, 0 if count_sink_labels else num_sink:].amax(dim=1) + 1).to(torch.int32)
     centroids, sizes = compute_centroids(ids, counts, keys, retrieval_to_graph=to_graph, retrieval_to_kv=to_kv,
                                          num_sink=num_sink, max_decode_tokens=max_decode_tokens, fp8=fp8)
     offsets, positions = build_member_csr(ids, counts, num_sink=num_sink)
@@ -227,20 +233,121 @@ def build_layer_from_labels(*, layer_idx: int, community_ids: torch.Tensor, keys
                             community_weight=weight, total_weight=total, token_communities=tokens)
 
 
-def partition_graphs(*args, **kwargs) -> PartitionResult:
-    """Leiden partitioning (partition.py:289-353) is not part of this build."""
-    raise NotImplementedError(
-        "Leiden partitioning is outside the MI355X decode build; supply community labels "
-        "(build_layer_from_labels or a PartitionRuntime label provider)")
+def _reshape_by_aggregation(topk_indices: torch.Tensor, topk_scores: torch.Tensor, *,
+                            aggregation: GraphAggregation, num_kv_heads: int,
+                            num_sink: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Top-k rows grouped into graphs (partition.py:97-147): per query head,
+    per KV-head group, or one graph; row r is position kappa - 1 + num_sink + r."""
+    if topk_indices.ndim != 3 or topk_scores.shape != topk_indices.shape:
+        raise ValueError("top-k tensors must have shape [query heads, rows, kappa]")
+    query_heads, rows, kappa = topk_indices.shape
+    if num_kv_heads <= 0 or query_heads % num_kv_heads:
+        raise ValueError("query heads must divide evenly into KV-head groups")
+    group = query_heads // num_kv_heads
+    if not 1 <= group <= 16:
+        raise ValueError("GQA group size must be in [1, 16]")
+    base = torch.arange(kappa - 1 + num_sink, kappa - 1 + num_sink + rows, dtype=torch.int64,
+                        device=topk_indices.device)
+    aggregation = GraphAggregation(aggregation)
+    if aggregation is GraphAggregation.PER_QUERY_HEAD:
+        return topk_indices, topk_scores, base.unsqueeze(0).expand(query_heads, -1)
+    if aggregation is GraphAggregation.QUERY_GROUP:
+        shape = (num_kv_heads, group * rows, kappa)
+        return (topk_indices.reshape(shape), topk_scores.reshape(shape),
+                base.repeat(group).unsqueeze(0).expand(num_kv_heads, -1))
+    return (topk_indices.reshape(1, query_heads * rows, kappa), topk_scores.reshape(1, query_heads * rows, kappa),
+            base.repeat(query_heads).unsqueeze(0))
 
 
-def partition_query_groups(*args, **kwargs) -> PartitionResult:
+def _scatter_membership(vertex: torch.Tensor, labels: torch.Tensor, *, graph_count: int,
+                        seq_len: int) -> torch.Tensor:
+    """partition.py:252-266: Leiden labels into a [graphs, S] table, -1 elsewhere."""
+    membership = torch.full((graph_count * seq_len,), -1, dtype=torch.int32, device=vertex.device)
+    membership[vertex] = labels
+    return membership.view(graph_count, seq_len)
+
+
+def _fill_isolated_vertices(membership: torch.Tensor) -> torch.Tensor:
+    """partition.py:269-273: vertices without edges become singletons numbered
+    after the graph's largest label, in position order."""
+    missing = membership == -1
+    next_ids = membership.amax(dim=1) + 1
+    offsets = missing.to(torch.int32).cumsum(dim=1) - 1
+    return torch.where(missing, next_ids.unsqueeze(1) + offsets, membership)
+
+
+def _dense_remap(membership: torch.Tensor) -> torch.Tensor:
+    """partition.py:276-286: per graph, each label becomes its rank among the
+    graph's distinct labels."""
+    sorted_values, order = membership.sort(dim=-1)
+    transitions = torch.ones_like(sorted_values, dtype=torch.int32)
+    if sorted_values.shape[-1] > 1:
+        transitions[:, 1:] = (sorted_values[:, 1:] != sorted_values[:, :-1]).to(torch.int32)
+    dense = torch.empty_like(membership, dtype=torch.int32)
+    dense.scatter_(1, order, (transitions.cumsum(dim=-1) - 1).to(torch.int32))
+    return dense
+
+
+def partition_graphs(topk_indices: torch.Tensor, topk_scores: torch.Tensor, *, aggregation: GraphAggregation,
+                     num_kv_heads: int, prefill_seq_len: int, num_sink: int, lam: float, leiden_resolution: float,
+                     leiden_seed: int) -> PartitionResult:
+    """Top-k edges -> coalesced graph -> native batched Leiden -> dense
+    per-graph community ids (partition.py:289-353).  Device tensors only."""
+    from community_kv_amd.graph.leiden import run_leiden
+
+    grouped_idx, grouped_scores, positions = _reshape_by_aggregation(
+        topk_indices, topk_scores, aggregation=aggregation, num_kv_heads=num_kv_heads, num_sink=num_sink)
+    graph_count = grouped_idx.shape[0]
+    src, dst, weight = build_adjacency(grouped_idx, grouped_scores, positions, seq_len=prefill_seq_len, lam=lam)
+    if src.numel():
+        vertex, labels, modularity = run_leiden(src, dst, weight, G=graph_count, seq_len=prefill_seq_len,
+                                                resolution=leiden_resolution,
+                                                max_inner_iter=leiden_max_iterations(prefill_seq_len),
+                                                seed=leiden_seed)
+        membership = _scatter_membership(vertex, labels, graph_count=graph_count, seq_len=prefill_seq_len)
+    else:
+        modularity = 0.0
+        membership = torch.full((graph_count, prefill_seq_len), -1, dtype=torch.int32, device=topk_indices.device)
+    community_ids = _dense_remap(_fill_isolated_vertices(membership))
+    community_counts = (community_ids.amax(dim=1) + 1).to(torch.int32)
+    return PartitionResult(community_ids=community_ids, community_counts=community_counts, modularity=modularity,
+                           edge_src=src, edge_dst=dst, edge_weight=weight)
+
+
+def partition_query_groups(topk_indices: torch.Tensor, topk_scores: torch.Tensor, *, num_kv_heads: int,
+                           prefill_seq_len: int, num_sink: int, lam: float, leiden_resolution: float,
+                           leiden_seed: int) -> PartitionResult:
     """Query-group wrapper of :func:`partition_graphs` (partition.py:356-379)."""
-    return partition_graphs(*args, **kwargs)
+    return partition_graphs(topk_indices, topk_scores, aggregation=GraphAggregation.QUERY_GROUP,
+                            num_kv_heads=num_kv_heads, prefill_seq_len=prefill_seq_len, num_sink=num_sink, lam=lam,
+                            leiden_resolution=leiden_resolution, leiden_seed=leiden_seed)
+
+
+def build_partitioned_layer(*, layer_idx: int, topk_indices: torch.Tensor, topk_scores: torch.Tensor,
+                            keys: torch.Tensor, num_sink: int, lam: float, leiden_resolution: float,
+                            leiden_seed: int, max_decode_tokens: int,
+                            aggregation: GraphAggregation = GraphAggregation.PER_QUERY_HEAD) -> PartitionedLayer:
+    """Full prefill partition of one layer and its decode state
+    (partition.py:538-618): Leiden on the top-k graph, then the state build
+    with the community count over all positions, sinks included, as the
+    reference counts them."""
+    if max_decode_tokens <= 0:
+        raise ValueError("max_decode_tokens must be positive")
+    kv_heads, seq_len, _ = keys.shape
+    aggregation = GraphAggregation(aggregation)
+    result = partition_graphs(topk_indices, topk_scores, aggregation=aggregation, num_kv_heads=kv_heads,
+                              prefill_seq_len=seq_len, num_sink=num_sink, lam=lam,
+                              leiden_resolution=leiden_resolution, leiden_seed=leiden_seed)
+    edges = (result.edge_src, result.edge_dst, result.edge_weight) if result.edge_src.numel() else None
+    return build_layer_from_labels(layer_idx=layer_idx, community_ids=result.community_ids, keys=keys,
+                                   num_sink=num_sink, max_decode_tokens=max_decode_tokens,
+                                   query_heads=topk_indices.shape[0], aggregation=aggregation, edges=edges,
+                                   count_sink_labels=True)
 
 
 __all__ = [
     "PartitionResult", "PartitionedLayer", "aggregation_mappings", "build_adjacency", "build_layer_from_labels",
+    "build_partitioned_layer",
     "build_member_csr", "compute_centroids", "init_modularity_state", "leiden_max_iterations",
     "partition_graphs", "partition_query_groups",
 ]

@@ -1,13 +1,12 @@
 """Prefill partition hand-off (reference: community_kv/graph/runtime.py:29-176).
 
-The reference runs Leiden on worker threads, one job per layer.  Leiden is
-outside this build, so jobs are resolved by a *label provider*: a callable
+The reference runs Leiden on worker threads, one job per layer.  Here a job
+runs ``build_partitioned_layer`` (top-k graph, native batched Leiden, state
+build) synchronously on the submitting stream after the completion event, so
+no extra threads or streams are created.  A *label provider*, a callable
 ``provider(layer_idx, keys, topk_indices, topk_scores) -> community_ids
-[graphs, S]`` whose labels are turned into decode state by
-``build_layer_from_labels`` (the reference's build_partitioned_layer after its
-Leiden call).  The top-k prefill edges become the modularity state through
-``build_adjacency``.  Jobs run synchronously on the submitting stream after the
-completion event, so no extra threads or streams are created.
+[graphs, S]``, may replace Leiden; its labels are turned into decode state by
+``build_layer_from_labels`` with the modularity state of the top-k edges.
 """
 
 from __future__ import annotations
@@ -18,7 +17,8 @@ import torch
 
 from community_kv_amd.config import CommunityKVConfig, GraphAggregation, PartitionConfig
 from community_kv_amd.graph.kernels.state_build import TopkEdges
-from community_kv_amd.graph.partition import PartitionedLayer, build_adjacency, build_layer_from_labels
+from community_kv_amd.graph.partition import (PartitionedLayer, build_adjacency, build_layer_from_labels,
+                                              build_partitioned_layer)
 
 
 class PartitionRuntime:
@@ -41,13 +41,16 @@ class PartitionRuntime:
             raise ValueError(f"layer {layer_idx} was already submitted")
         if not 0 <= layer_idx < self.max_layers:
             raise ValueError("layer index out of range")
-        if self.label_provider is None:
-            raise NotImplementedError(
-                "Leiden partitioning is outside the MI355X decode build; pass a label_provider")
         if completion_event is not None and hasattr(completion_event, "synchronize"):
             completion_event.synchronize()
         cfg = self.algorithm
         aggregation = GraphAggregation(cfg.aggregation)
+        if self.label_provider is None:
+            self._results[layer_idx] = build_partitioned_layer(
+                layer_idx=layer_idx, topk_indices=topk_indices, topk_scores=topk_scores, keys=keys,
+                num_sink=cfg.num_sink, lam=cfg.lam, leiden_resolution=resolution, leiden_seed=cfg.leiden_seed,
+                max_decode_tokens=max_decode_tokens, aggregation=aggregation)
+            return
         labels = self.label_provider(layer_idx, keys, topk_indices, topk_scores)
         edges = topk_edges = None
         if topk_indices is not None and topk_indices.numel():

@@ -30,6 +30,13 @@
  *   ckv_label_counts,       the state build of build_partitioned_layer() after Leiden
  *   ckv_build_layer_state   (graph/partition.py:538-618): compute_centroids 382-454,
  *                           build_member_csr 457-492, init_modularity_state 495-535
+ *   ckv_batched_leiden      batched_leiden() of the Leiden extension (graph/leiden/_csrc/bindings.cpp:40-103,
+ *                           launch_batched_leiden in leiden.cu:43-205), called by run_leiden()
+ *                           (graph/leiden/algorithm.py:51-161)
+ *   ckv_aggregate_coo       aggregate_coo() of the same extension (bindings.cpp:118-170,
+ *                           aggregate_upper_coo in aggregate.cu:88-184)
+ *   ckv_densify_count,      _densify_per_graph() (graph/leiden/algorithm.py:30-48), as two calls
+ *   ckv_densify_apply       so that the caller reads the per-graph counts in between
  */
 #ifndef CKV_AMD_H
 #define CKV_AMD_H
@@ -288,6 +295,42 @@ size_t ckv_state_workspace_bytes(int32_t graphs, int32_t retrieval_heads, int32_
 int ckv_label_counts(const int32_t* labels, int32_t graphs, int32_t seq_len, int32_t num_sink,
                      int32_t* community_counts, void* stream);
 int ckv_build_layer_state(const ckv_state_build_args* args, void* stream);
+
+/* One Leiden level over `graphs` vertex-disjoint graphs of seq_len vertices
+ * each (vertex ids g * seq_len + i).  Edges: upper-triangular COO (self loops
+ * allowed), int32 src/dst, f32 weight, device memory; out-of-range edges are
+ * dropped.  Outputs: labels [graphs * seq_len] (a vertex id within the same
+ * graph naming the community; -1 for vertices without edges) and
+ * modularity [graphs] (f64).  Local moving (up/down gated, up to
+ * max_inner_iter sweeps, ends after a stalled sweep in each direction), then
+ * refinement inside each local-moving community (greedy, or Gumbel-max at
+ * temperature theta when use_boltzmann).  No host synchronisation; workspace
+ * of ckv_leiden_workspace_bytes(edges, graphs, seq_len) bytes. */
+size_t ckv_leiden_workspace_bytes(int64_t edges, int32_t graphs, int32_t seq_len);
+int ckv_batched_leiden(const int32_t* edge_src, const int32_t* edge_dst, const float* edge_weight, int64_t edges,
+                       int32_t graphs, int32_t seq_len, float resolution, float theta, int32_t max_inner_iter,
+                       int32_t seed, int32_t use_boltzmann, int32_t* labels, double* modularity,
+                       void* workspace, void* stream);
+
+/* Contract an upper-triangular COO by `labels` (super-vertex per vertex, in
+ * [0, super_vertices)): both ends relabelled, (min, max) order, duplicates
+ * summed, sorted by (src, dst).  Outputs have room for `edges` entries;
+ * *out_count (device int64) receives the number written. */
+size_t ckv_aggregate_coo_workspace_bytes(int64_t edges);
+int ckv_aggregate_coo(const int32_t* edge_src, const int32_t* edge_dst, const float* edge_weight, int64_t edges,
+                      const int32_t* labels, int32_t super_vertices, int32_t* out_src, int32_t* out_dst,
+                      float* out_weight, int64_t* out_count, void* workspace, void* stream);
+
+/* Per-graph dense relabelling: a vertex's label (its own id when negative)
+ * becomes its rank among the distinct labels of its graph, plus
+ * g * new_seq_len.  ckv_densify_count writes the distinct count per graph
+ * (device int32 [graphs]); ckv_densify_apply, with the same workspace and
+ * new_seq_len >= every count, writes the dense labels. */
+size_t ckv_densify_workspace_bytes(int32_t graphs, int32_t seq_len);
+int ckv_densify_count(const int32_t* labels, int32_t graphs, int32_t seq_len, int32_t* counts, void* workspace,
+                      void* stream);
+int ckv_densify_apply(const int32_t* labels, int32_t graphs, int32_t seq_len, int32_t new_seq_len, int32_t* dense,
+                      const void* workspace, void* stream);
 
 /* Score every retrieval head's centroids against its query group, select the
  * communities that fill the budget (reference order: strictly-above-threshold

@@ -1,0 +1,90 @@
+"""Host logic of the multi-level Leiden driver (community_kv_amd.graph.leiden.
+algorithm) with the native module replaced, as the reference's own tests do
+(tests/community_kv/graph/leiden/test_algorithm.py:36-105).  CPU only."""
+
+from __future__ import annotations
+
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from community_kv_amd.graph.leiden import algorithm
+from oracle import leiden as L
+
+GOLDEN = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "reference_known_answers.json")))
+
+
+def _cpu_densify(labels, G, seq_len):
+    dense, width = L.densify_per_graph(labels.numpy(), G, seq_len)
+    return torch.from_numpy(dense), width
+
+
+def _install(monkeypatch, labels):
+    calls = []
+
+    class _Module:
+        @staticmethod
+        def batched_leiden(*args):
+            calls.append(args)
+            return torch.tensor(labels, dtype=torch.int32), torch.zeros(1, dtype=torch.float64)
+
+        @staticmethod
+        def aggregate_coo(*args):
+            raise AssertionError("single-level run must not aggregate")
+
+    monkeypatch.setattr(algorithm, "_load_module", lambda: _Module)
+    monkeypatch.setattr(algorithm, "_densify_per_graph", _cpu_densify)
+    return calls
+
+
+def test_run_leiden_handles_isolates_and_explicit_parameters(monkeypatch):
+    ka = GOLDEN["leiden_isolates"]
+    calls = _install(monkeypatch, ka["native_labels"])
+    vertex, partition, modularity = algorithm.run_leiden(
+        torch.tensor([0], dtype=torch.int32), torch.tensor([1], dtype=torch.int32), torch.ones(1), G=ka["G"],
+        seq_len=ka["seq_len"], max_level=ka["max_level"], theta=ka["theta"], max_inner_iter=ka["max_inner_iter"],
+        use_boltzmann=ka["use_boltzmann"])
+    assert vertex.tolist() == ka["vertex"] and partition.tolist() == ka["partition"]
+    assert math.isfinite(modularity)
+    assert calls[0][7] == ka["theta"] and calls[0][8] == ka["max_inner_iter"] and calls[0][10] is True
+
+
+def test_run_leiden_applies_environment_overrides(monkeypatch):
+    ka = GOLDEN["leiden_env_overrides"]
+    calls = _install(monkeypatch, [0, 0])
+    for k, v in ka["env"].items():
+        monkeypatch.setenv(k, v)
+    algorithm.run_leiden(torch.tensor([0], dtype=torch.int32), torch.tensor([1], dtype=torch.int32), torch.ones(1),
+                         G=1, seq_len=2, max_level=1)
+    assert calls[0][7] == ka["theta"] and calls[0][8] == ka["max_inner_iter"] and calls[0][10] is True
+
+
+def test_disjoint_modularity_known_answer():
+    ka = GOLDEN["leiden_two_component_modularity"]
+    q = algorithm._compute_disjoint_modularity(torch.tensor(ka["src"], dtype=torch.int32),
+                                               torch.tensor(ka["dst"], dtype=torch.int32),
+                                               torch.tensor(ka["weight"]), torch.tensor(ka["labels"]),
+                                               ka["resolution"])
+    assert q == pytest.approx(ka["modularity"], abs=1e-9)
+
+
+def test_native_densify_requires_device_tensors():
+    with pytest.raises((RuntimeError, ValueError, TypeError)):
+        algorithm._densify_per_graph(torch.tensor(GOLDEN["leiden_densify"]["labels"], dtype=torch.int32), 2, 3)
+
+
+def test_partition_helpers_match_oracle():
+    from community_kv_amd.graph import partition as P
+
+    m = torch.tensor([[5, -1, 5, 2, -1], [-1, -1, 0, 0, 7]], dtype=torch.int32)
+    filled = P._fill_isolated_vertices(m)
+    assert filled.tolist() == L.fill_isolated(m.numpy()).tolist()
+    assert P._dense_remap(filled).tolist() == L.dense_remap(filled.numpy()).tolist()
+    idx = torch.arange(4 * 3 * 2, dtype=torch.int32).reshape(4, 3, 2)
+    g_idx, _, pos = P._reshape_by_aggregation(idx, idx.float(), aggregation="query_group", num_kv_heads=2,
+                                              num_sink=1)
+    assert g_idx.shape == (2, 6, 2) and pos[0].tolist() == [2, 3, 4, 2, 3, 4]
