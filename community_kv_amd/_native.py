@@ -72,6 +72,8 @@ EXPORTED_SYMBOLS = (
     "ckv_densify_workspace_bytes",
     "ckv_densify_count",
     "ckv_densify_apply",
+    "ckv_partition_modularity_workspace_bytes",
+    "ckv_partition_modularity",
     "ckv_host_numerics",
     "ckv_device_numerics",
     "ckv_abi_version",
@@ -223,6 +225,10 @@ def lib() -> ctypes.CDLL:
     handle.ckv_densify_count.restype = ctypes.c_int
     handle.ckv_densify_apply.argtypes = [_p, _i32, _i32, _i32, _p, _p, _p]
     handle.ckv_densify_apply.restype = ctypes.c_int
+    handle.ckv_partition_modularity_workspace_bytes.argtypes = [_i32]
+    handle.ckv_partition_modularity_workspace_bytes.restype = ctypes.c_size_t
+    handle.ckv_partition_modularity.argtypes = [_p, _p, _p, _i64, _p, _i32, _f32, _p, _p, _p]
+    handle.ckv_partition_modularity.restype = ctypes.c_int
     handle.ckv_host_numerics.argtypes = [ctypes.c_int, _p, _p, _i64]
     handle.ckv_host_numerics.restype = ctypes.c_int
     handle.ckv_device_numerics.argtypes = [ctypes.c_int, _p, _p, _i64, _p]

@@ -26,12 +26,14 @@
 // communities (the reference's table size), in order of first appearance.
 //
 // Launch sequence of ckv_batched_leiden (one stream, no host sync):
-//   mirror_kernel, radix sort, row_ptr_kernel, col_kernel, degree_kernel, init_kernel
-//   local moving x max_inner_iter: sigma_zero, sigma_scatter, local_moving_kernel, lm_control_kernel
+//   mirror_kernel, radix sort, row_ptr_kernel, col_kernel, zero_kernel, hub_list_kernel, degree_kernel,
+//   graph_sum_kernel (2m), identity_kernel
+//   local moving x max_inner_iter: sigma_zero, sigma_scatter, local_moving_kernel (small rows, then
+//                                  hubs), lm_control_kernel
 //   refine_init_kernel, parent sigma
-//   refinement x max_inner_iter: sigma_zero, sigma_scatter, refine_propose_kernel,
+//   refinement x max_inner_iter: sigma_zero, sigma_scatter, refine_propose_kernel (small, hubs),
 //                                refine_commit_kernel, refine_control_kernel
-//   sigma of the result, modularity_kernel, finish_kernel (labels, -1 for isolated)
+//   sigma of the result, modularity_kernel, graph_sum_kernel, finish_kernel (labels, -1 for isolated)
 #include <hip/hip_runtime.h>
 #include <hipcub/hipcub.hpp>
 
@@ -48,7 +50,8 @@ constexpr int LTHREADS = 64 * LWAVES;
 constexpr int TABLE_CAP = 1024;  // distinct neighbour communities per vertex
 constexpr int ETHREADS = 256;
 
-enum { CTL_MOVED = 0, CTL_UPDOWN = 1, CTL_STALE = 2, CTL_DONE = 3, CTL_WORDS = 8 };
+enum { CTL_MOVED = 0,  // nonzero once a vertex moved in the current sweep
+       CTL_UPDOWN = 1, CTL_STALE = 2, CTL_DONE = 3, CTL_WORDS = 8 };
 
 // ----------------------------------------------------------------- hashing (rng.cuh)
 __device__ __host__ inline uint32_t pcg_hash(uint32_t x) {
@@ -109,17 +112,67 @@ __device__ inline uint64_t wave_max_u64(uint64_t x) {
 }
 __device__ inline int first_lane(uint64_t m) { return __ffsll((long long)m) - 1; }
 
+// The control kernels only test the moved word for zero: set it once per
+// sweep (read first, so that later movers do not queue writes to one line).
+__device__ inline void mark_moved(int32_t* ctl) {
+  if (__hip_atomic_load(ctl + CTL_MOVED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0)
+    __hip_atomic_store(ctl + CTL_MOVED, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Neighbour-community table of vertex v over its row [a, b): self loops
 // skipped; with `parent`, only neighbours u with parent[u] == pv.  Returns the
-// number of entries (wave-uniform); *e_sum gets the summed weight of the
-// admitted entries (every lane).
+// number of table slots to scan (wave-uniform; empty slots hold -1); *e_sum
+// gets the summed weight of the admitted entries (every lane).
+//
+// Rows of at most CAP / 2 entries (nearly all): every lane inserts its
+// neighbour's community into an open-addressing table of 2 x degree slots
+// (LDS compare-and-swap) and adds its weight with an LDS f64 atomic.  Longer
+// rows (hubs, where the TABLE_CAP limit can bite): a leader loop over the
+// chunk's distinct communities, entries in order of first appearance along
+// the row, later ones dropped once TABLE_CAP are held.
+template <int CAP>
 __device__ int build_table(int32_t* tc, double* ts, const int32_t* __restrict__ col,
                            const float* __restrict__ wt, const int32_t* __restrict__ lab,
                            const int32_t* __restrict__ parent, int32_t pv, int32_t v, int32_t a, int32_t b,
                            double* e_sum) {
   const int ln = lane();
-  int n = 0;
   double e_acc = 0.0;
+  if (b - a <= CAP / 2) {
+    int size = 64;
+    while (size < 2 * (b - a)) size <<= 1;
+    for (int j = ln; j < size; j += 64) {
+      tc[j] = -1;
+      ts[j] = 0.0;
+    }
+    __builtin_amdgcn_wave_barrier();
+    for (int32_t e0 = a; e0 < b; e0 += 64) {
+      const int32_t e = e0 + ln;
+      bool ok = e < b;
+      const int32_t u = ok ? col[e] : v;
+      ok = ok && u != v;
+      if (parent) ok = ok && parent[u] == pv;
+      if (ok) {
+        const float w = wt[e];
+        const int32_t c = lab[u];
+        e_acc += (double)w;
+        uint32_t h = pcg_hash((uint32_t)c) & (uint32_t)(size - 1);
+        while (true) {
+          const int32_t cur = __hip_atomic_load(tc + h, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+          if (cur == c) break;
+          if (cur == -1) {
+            const int32_t prev = atomicCAS(tc + h, -1, c);
+            if (prev == -1 || prev == c) break;
+          }
+          h = (h + 1) & (uint32_t)(size - 1);
+        }
+        unsafeAtomicAdd(ts + h, (double)w);
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+    *e_sum = wave_sum_f64(e_acc);
+    return size;
+  }
+  int n = 0;
   for (int32_t e0 = a; e0 < b; e0 += 64) {
     const int32_t e = e0 + ln;
     bool ok = e < b;
@@ -143,7 +196,7 @@ __device__ int build_table(int32_t* tc, double* ts, const int32_t* __restrict__ 
           break;
         }
       }
-      if (idx < 0 && n < TABLE_CAP) {
+      if (idx < 0 && n < CAP) {
         idx = n++;
         if (ln == 0) {
           tc[idx] = c0;
@@ -162,7 +215,7 @@ __device__ int build_table(int32_t* tc, double* ts, const int32_t* __restrict__ 
 __device__ float table_lookup(const int32_t* tc, const double* ts, int n, int32_t c) {
   for (int j0 = 0; j0 < n; j0 += 64) {
     const int j = j0 + lane();
-    const uint64_t hit = __ballot(j < n && tc[j] == c);
+    const uint64_t hit = __ballot(j < n && tc[j] == c && c >= 0);
     if (hit) return (float)ts[j0 + first_lane(hit)];
   }
   return 0.0f;
@@ -204,28 +257,43 @@ __global__ void col_kernel(const uint64_t* __restrict__ keys, int64_t n, int bit
 }
 
 __global__ void zero_kernel(double* __restrict__ two_m, int32_t G, double* __restrict__ modularity,
-                            int32_t* __restrict__ ctl) {
+                            int32_t* __restrict__ ctl, int32_t* __restrict__ hub_count) {
   const int i = threadIdx.x;
   for (int g = i; g < G; g += blockDim.x) {
     two_m[g] = 0.0;
     modularity[g] = 0.0;
   }
   if (i < CTL_WORDS) ctl[i] = i == CTL_UPDOWN ? 1 : 0;  // local moving starts with upward moves
+  if (i == 0) *hub_count = 0;
 }
 
 __global__ __launch_bounds__(LTHREADS) void degree_kernel(const int32_t* __restrict__ row_ptr,
                                                           const float* __restrict__ wt, int32_t V, int32_t S,
-                                                          double* __restrict__ k_v, double* __restrict__ two_m) {
+                                                          double* __restrict__ k_v) {
   const int32_t v = blockIdx.x * LWAVES + (threadIdx.x >> 6);
   if (v >= V) return;
   const int32_t a = row_ptr[v], b = row_ptr[v + 1];
   double s = 0.0;
   for (int32_t e = a + lane(); e < b; e += 64) s += (double)wt[e];
   s = wave_sum_f64(s);
-  if (lane() == 0) {
-    k_v[v] = s;
-    if (s != 0.0) atomicAdd(two_m + v / S, s);
+  if (lane() == 0) k_v[v] = s;
+}
+
+// out[g] = sum of x over graph g's S vertices (one workgroup per graph, fixed
+// order: strided per-thread sums, then a tree over the threads).
+__global__ __launch_bounds__(256) void graph_sum_kernel(const double* __restrict__ x, int32_t S,
+                                                        double* __restrict__ out) {
+  __shared__ double part[256];
+  const int32_t g = blockIdx.x;
+  double s = 0.0;
+  for (int32_t i = threadIdx.x; i < S; i += 256) s += x[(int64_t)g * S + i];
+  part[threadIdx.x] = s;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if ((int)threadIdx.x < o) part[threadIdx.x] += part[threadIdx.x + o];
+    __syncthreads();
   }
+  if (threadIdx.x == 0) out[g] = part[0];
 }
 
 __global__ void identity_kernel(int32_t V, int32_t* __restrict__ labels) {
@@ -247,7 +315,7 @@ __global__ void sigma_scatter_kernel(const int32_t* __restrict__ labels, const d
   if (v >= V) return;
   const int32_t c = labels[v];
   const double k = k_v[v];
-  if (c >= 0 && k != 0.0) atomicAdd(sigma + c, k);
+  if (c >= 0 && k != 0.0) unsafeAtomicAdd(sigma + c, k);
 }
 
 struct Graph {
@@ -260,16 +328,11 @@ struct Graph {
   int32_t S;
 };
 
-__global__ __launch_bounds__(LTHREADS) void local_moving_kernel(Graph gr, const double* __restrict__ sigma,
-                                                                const int32_t* __restrict__ lin,
-                                                                int32_t* __restrict__ lout,
-                                                                int32_t* __restrict__ ctl, float resolution,
-                                                                uint32_t level, uint32_t sweep, uint32_t seed) {
-  __shared__ int32_t tab_c[LWAVES][TABLE_CAP];
-  __shared__ double tab_s[LWAVES][TABLE_CAP];
-  const int wv = threadIdx.x >> 6;
-  const int32_t v = blockIdx.x * LWAVES + wv;
-  if (v >= gr.V) return;
+template <int CAP>
+__device__ void local_moving_vertex(const Graph& gr, const double* __restrict__ sigma, const int32_t* __restrict__ lin,
+                                    int32_t* __restrict__ lout, int32_t* __restrict__ ctl, float resolution,
+                                    uint32_t level, uint32_t sweep, uint32_t seed, int32_t v, int32_t* tc,
+                                    double* ts) {
   const int32_t old = lin[v];
   const bool done = ctl[CTL_DONE] != 0;
   const int32_t a = gr.row_ptr[v], b = gr.row_ptr[v + 1];
@@ -281,8 +344,8 @@ __global__ __launch_bounds__(LTHREADS) void local_moving_kernel(Graph gr, const 
   }
   const int up_down = ctl[CTL_UPDOWN];
   double e_sum;
-  const int n = build_table(tab_c[wv], tab_s[wv], gr.col, gr.wt, lin, nullptr, 0, v, a, b, &e_sum);
-  const float k_old = table_lookup(tab_c[wv], tab_s[wv], n, old);
+  const int n = build_table<CAP>(tc, ts, gr.col, gr.wt, lin, nullptr, 0, v, a, b, &e_sum);
+  const float k_old = table_lookup(tc, ts, n, old);
   const double kv = gr.k_v[v];
   const double m_g = 0.5 * tm;
   const double inv_m = 1.0 / m_g;
@@ -292,9 +355,9 @@ __global__ __launch_bounds__(LTHREADS) void local_moving_kernel(Graph gr, const 
   uint64_t mine = 0;
   int32_t mine_c = old;
   for (int j = lane(); j < n; j += 64) {
-    const int32_t c = tab_c[wv][j];
-    if (c == old || (c > old ? 1 : 0) != up_down) continue;
-    const float kn = (float)tab_s[wv][j];
+    const int32_t c = tc[j];
+    if (c < 0 || c == old || (c > old ? 1 : 0) != up_down) continue;
+    const float kn = (float)ts[j];
     const double dq = ((double)kn - (double)k_old) * inv_m
                       + (double)resolution * kv * (sig_old_excl - sigma[c]) * inv_2m2;
     const float dqf = (float)dq + jitter;
@@ -309,7 +372,7 @@ __global__ __launch_bounds__(LTHREADS) void local_moving_kernel(Graph gr, const 
   if (best > pack(0.0f, STAY_PREF)) choice = __shfl(mine_c, first_lane(__ballot(mine == best)));
   if (lane() == 0) {
     lout[v] = choice;
-    if (choice != old) atomicAdd(ctl + CTL_MOVED, 1);
+    if (choice != old) mark_moved(ctl);
   }
 }
 
@@ -338,16 +401,13 @@ __global__ void refine_init_kernel(const int32_t* __restrict__ lm, int32_t V, in
   if (v < CTL_WORDS) ctl[v] = 0;
 }
 
-__global__ __launch_bounds__(LTHREADS) void refine_propose_kernel(
-    Graph gr, const int32_t* __restrict__ parent, const double* __restrict__ sigma,
-    const double* __restrict__ parent_sigma, const int32_t* __restrict__ lin, int32_t* __restrict__ prop,
-    uint32_t* __restrict__ rank, const int32_t* __restrict__ ctl, float resolution, float inv_theta,
-    int boltzmann, uint32_t level, uint32_t sweep, uint32_t seed) {
-  __shared__ int32_t tab_c[LWAVES][TABLE_CAP];
-  __shared__ double tab_s[LWAVES][TABLE_CAP];
-  const int wv = threadIdx.x >> 6;
-  const int32_t v = blockIdx.x * LWAVES + wv;
-  if (v >= gr.V || ctl[CTL_DONE]) return;
+template <int CAP>
+__device__ void refine_propose_vertex(const Graph& gr, const int32_t* __restrict__ parent,
+                                      const double* __restrict__ sigma, const double* __restrict__ parent_sigma,
+                                      const int32_t* __restrict__ lin, int32_t* __restrict__ prop,
+                                      uint32_t* __restrict__ rank, float resolution, float inv_theta, int boltzmann,
+                                      uint32_t level, uint32_t sweep, uint32_t seed, int32_t v, int32_t* tc,
+                                      double* ts) {
   const int32_t g = v / gr.S;
   if (lane() == 0) rank[v] = mix4((uint32_t)g, (uint32_t)v, (level << 16) | sweep, seed);
   const int32_t old = lin[v];
@@ -359,7 +419,7 @@ __global__ __launch_bounds__(LTHREADS) void refine_propose_kernel(
   }
   const int32_t pv = parent[v];
   double e_sum;
-  const int n = build_table(tab_c[wv], tab_s[wv], gr.col, gr.wt, lin, parent, pv, v, a, b, &e_sum);
+  const int n = build_table<CAP>(tc, ts, gr.col, gr.wt, lin, parent, pv, v, a, b, &e_sum);
   const double kv = gr.k_v[v];
   double vol_minus = parent_sigma[pv] - kv;
   if (vol_minus < 0.0) vol_minus = 0.0;
@@ -368,7 +428,7 @@ __global__ __launch_bounds__(LTHREADS) void refine_propose_kernel(
     if (lane() == 0) prop[v] = old;
     return;
   }
-  const float k_old = table_lookup(tab_c[wv], tab_s[wv], n, old);
+  const float k_old = table_lookup(tc, ts, n, old);
   const double m_g = 0.5 * tm;
   const double inv_m = 1.0 / m_g;
   const double inv_2m2 = 1.0 / (2.0 * m_g * m_g);
@@ -376,9 +436,9 @@ __global__ __launch_bounds__(LTHREADS) void refine_propose_kernel(
   uint64_t mine = 0;
   int32_t mine_c = old;
   for (int j = lane(); j < n; j += 64) {
-    const int32_t c = tab_c[wv][j];
-    if (c == old) continue;
-    const float kn = (float)tab_s[wv][j];
+    const int32_t c = tc[j];
+    if (c < 0 || c == old) continue;
+    const float kn = (float)ts[j];
     const double dq = ((double)kn - (double)k_old) * inv_m
                       + (double)resolution * kv * (sig_old_excl - sigma[c]) * inv_2m2;
     if (dq < 0.0) continue;
@@ -399,6 +459,68 @@ __global__ __launch_bounds__(LTHREADS) void refine_propose_kernel(
   int32_t choice = old;
   if (best > pack(stay, STAY_PREF)) choice = __shfl(mine_c, first_lane(__ballot(mine == best)));
   if (lane() == 0) prop[v] = choice;
+}
+
+// Vertices with at most SMALL_CAP / 2 row entries (nearly all) run with a
+// small LDS table and 8 waves per workgroup; the rest (hubs, listed once per
+// call by hub_list_kernel) run with the full TABLE_CAP table, grid-striding
+// over the list.
+constexpr int SMALL_CAP = 256;
+constexpr int SWAVES = 8;
+constexpr int HUB_BLOCKS = 512;
+
+__global__ void hub_list_kernel(const int32_t* __restrict__ row_ptr, int32_t V, int32_t* __restrict__ hubs,
+                                int32_t* __restrict__ hub_count) {
+  const int32_t v = blockIdx.x * blockDim.x + threadIdx.x;
+  if (v < V && row_ptr[v + 1] - row_ptr[v] > SMALL_CAP / 2) hubs[atomicAdd(hub_count, 1)] = v;
+}
+
+template <bool HUB>
+__global__ __launch_bounds__(HUB ? LTHREADS : 64 * SWAVES) void local_moving_kernel(
+    Graph gr, const double* __restrict__ sigma, const int32_t* __restrict__ lin, int32_t* __restrict__ lout,
+    int32_t* __restrict__ ctl, const int32_t* __restrict__ hubs, const int32_t* __restrict__ hub_count,
+    float resolution, uint32_t level, uint32_t sweep, uint32_t seed) {
+  constexpr int W = HUB ? LWAVES : SWAVES;
+  constexpr int CAP = HUB ? TABLE_CAP : SMALL_CAP;
+  __shared__ int32_t tab_c[W][CAP];
+  __shared__ double tab_s[W][CAP];
+  const int wv = threadIdx.x >> 6;
+  if (HUB) {
+    const int32_t n = *hub_count;
+    for (int32_t i = blockIdx.x * W + wv; i < n; i += gridDim.x * W)
+      local_moving_vertex<CAP>(gr, sigma, lin, lout, ctl, resolution, level, sweep, seed, hubs[i], tab_c[wv],
+                               tab_s[wv]);
+  } else {
+    const int32_t v = blockIdx.x * W + wv;
+    if (v >= gr.V || gr.row_ptr[v + 1] - gr.row_ptr[v] > CAP / 2) return;
+    local_moving_vertex<CAP>(gr, sigma, lin, lout, ctl, resolution, level, sweep, seed, v, tab_c[wv], tab_s[wv]);
+  }
+}
+
+template <bool HUB>
+__global__ __launch_bounds__(HUB ? LTHREADS : 64 * SWAVES) void refine_propose_kernel(
+    Graph gr, const int32_t* __restrict__ parent, const double* __restrict__ sigma,
+    const double* __restrict__ parent_sigma, const int32_t* __restrict__ lin, int32_t* __restrict__ prop,
+    uint32_t* __restrict__ rank, const int32_t* __restrict__ ctl, const int32_t* __restrict__ hubs,
+    const int32_t* __restrict__ hub_count, float resolution, float inv_theta, int boltzmann, uint32_t level,
+    uint32_t sweep, uint32_t seed) {
+  constexpr int W = HUB ? LWAVES : SWAVES;
+  constexpr int CAP = HUB ? TABLE_CAP : SMALL_CAP;
+  __shared__ int32_t tab_c[W][CAP];
+  __shared__ double tab_s[W][CAP];
+  if (ctl[CTL_DONE]) return;
+  const int wv = threadIdx.x >> 6;
+  if (HUB) {
+    const int32_t n = *hub_count;
+    for (int32_t i = blockIdx.x * W + wv; i < n; i += gridDim.x * W)
+      refine_propose_vertex<CAP>(gr, parent, sigma, parent_sigma, lin, prop, rank, resolution, inv_theta,
+                                 boltzmann, level, sweep, seed, hubs[i], tab_c[wv], tab_s[wv]);
+  } else {
+    const int32_t v = blockIdx.x * W + wv;
+    if (v >= gr.V || gr.row_ptr[v + 1] - gr.row_ptr[v] > CAP / 2) return;
+    refine_propose_vertex<CAP>(gr, parent, sigma, parent_sigma, lin, prop, rank, resolution, inv_theta, boltzmann,
+                               level, sweep, seed, v, tab_c[wv], tab_s[wv]);
+  }
 }
 
 // Commit an independent set of the proposals: a mover commits unless a
@@ -433,7 +555,7 @@ __global__ __launch_bounds__(LTHREADS) void refine_commit_kernel(
   const bool any_lost = __ballot(lost) != 0;
   if (lane() == 0) {
     lout[v] = any_lost ? old : p;
-    if (!any_lost) atomicAdd(ctl + CTL_MOVED, 1);
+    if (!any_lost) mark_moved(ctl);
   }
 }
 
@@ -443,15 +565,19 @@ __global__ void refine_control_kernel(int32_t* __restrict__ ctl) {
   ctl[CTL_MOVED] = 0;
 }
 
-// Q_g = sum_v [in(v) / 2m - gamma k_v Sigma[c_v] / (4 m^2)] (helpers.cu:41-78).
+// q_v = in(v) / 2m - gamma k_v Sigma[c_v] / (4 m^2); Q_g is their sum over
+// the graph (helpers.cu:41-78).
 __global__ __launch_bounds__(LTHREADS) void modularity_kernel(Graph gr, const int32_t* __restrict__ labels,
                                                               const double* __restrict__ sigma, float resolution,
-                                                              double* __restrict__ modularity) {
+                                                              double* __restrict__ q_v) {
   const int32_t v = blockIdx.x * LWAVES + (threadIdx.x >> 6);
   if (v >= gr.V) return;
   const int32_t g = v / gr.S;
   const double tm = gr.two_m[g];
-  if (!(tm > 0.0)) return;
+  if (!(tm > 0.0)) {
+    if (lane() == 0) q_v[v] = 0.0;
+    return;
+  }
   const int32_t cv = labels[v];
   const int32_t a = gr.row_ptr[v], b = gr.row_ptr[v + 1];
   double in_sum = 0.0;
@@ -460,8 +586,7 @@ __global__ __launch_bounds__(LTHREADS) void modularity_kernel(Graph gr, const in
   in_sum = wave_sum_f64(in_sum);
   if (lane() == 0) {
     const double m_g = 0.5 * tm;
-    const double q = in_sum / tm - (double)resolution * (gr.k_v[v] * sigma[cv]) / (4.0 * m_g * m_g);
-    if (q != 0.0) atomicAdd(modularity + g, q);
+    q_v[v] = in_sum / tm - (double)resolution * (gr.k_v[v] * sigma[cv]) / (4.0 * m_g * m_g);
   }
 }
 
@@ -540,6 +665,74 @@ __global__ void densify_apply_kernel(const int32_t* __restrict__ labels, const i
   dense[v] = l < 0 ? -1 : scan[l] - scan[g * S] + g * new_S;
 }
 
+// ----------------------------------------------------------------- modularity of a labelled edge list
+__device__ inline double block_sum_f64(double x, double* part) {  // 256 threads
+  x = wave_sum_f64(x);
+  if (lane() == 0) part[threadIdx.x >> 6] = x;
+  __syncthreads();
+  return part[0] + part[1] + part[2] + part[3];
+}
+
+__global__ void mod_zero_kernel(double* __restrict__ k, double* __restrict__ sig, int32_t V,
+                                double* __restrict__ acc) {
+  const int32_t v = blockIdx.x * blockDim.x + threadIdx.x;
+  if (v < V) {
+    k[v] = 0.0;
+    sig[v] = 0.0;
+  }
+  if (v < 4) acc[v] = 0.0;
+}
+
+__global__ __launch_bounds__(256) void mod_edge_kernel(const int32_t* __restrict__ src,
+                                                       const int32_t* __restrict__ dst, const float* __restrict__ w,
+                                                       int64_t E, const int32_t* __restrict__ labels, int32_t V,
+                                                       double* __restrict__ k, double* __restrict__ acc) {
+  __shared__ double part[4];
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  double in = 0.0;
+  if (i < E) {
+    const int32_t a = src[i], b = dst[i];
+    if (a >= 0 && a < V && b >= 0 && b < V) {
+      const double x = (double)w[i];
+      unsafeAtomicAdd(k + a, x);
+      unsafeAtomicAdd(k + b, x);
+      if (labels[a] == labels[b]) in = x;
+    }
+  }
+  in = block_sum_f64(in, part);
+  if (threadIdx.x == 0 && in != 0.0) unsafeAtomicAdd(acc, in);
+}
+
+__global__ __launch_bounds__(256) void mod_sigma_kernel(const int32_t* __restrict__ labels,
+                                                        const double* __restrict__ k, int32_t V,
+                                                        double* __restrict__ sig, double* __restrict__ acc) {
+  __shared__ double part[4];
+  const int32_t v = blockIdx.x * blockDim.x + threadIdx.x;
+  double kv = 0.0;
+  if (v < V) {
+    kv = k[v];
+    const int32_t l = labels[v];
+    if (l >= 0 && l < V && kv != 0.0) unsafeAtomicAdd(sig + l, kv);
+  }
+  kv = block_sum_f64(kv, part);
+  if (threadIdx.x == 0 && kv != 0.0) unsafeAtomicAdd(acc + 1, kv);
+}
+
+__global__ __launch_bounds__(256) void mod_square_kernel(const double* __restrict__ sig, int32_t V,
+                                                         double* __restrict__ acc) {
+  __shared__ double part[4];
+  const int32_t v = blockIdx.x * blockDim.x + threadIdx.x;
+  double x = v < V ? sig[v] * sig[v] : 0.0;
+  x = block_sum_f64(x, part);
+  if (threadIdx.x == 0 && x != 0.0) unsafeAtomicAdd(acc + 2, x);
+}
+
+__global__ void mod_final_kernel(const double* __restrict__ acc, float resolution, double* __restrict__ out) {
+  if (threadIdx.x != 0) return;
+  const double two_m = acc[1];
+  *out = two_m > 0.0 ? 2.0 * acc[0] / two_m - (double)resolution * acc[2] / (two_m * two_m) : 0.0;
+}
+
 // ----------------------------------------------------------------- host side
 inline int bits_for(uint64_t x) {  // bits needed to hold values 0..x
   int b = 1;
@@ -556,7 +749,7 @@ int launch_check() {
 
 struct LeidenLayout {
   size_t keys_a, keys_b, vals_a, vals_b, temp, temp_bytes, row_ptr, col, k_v, two_m, sigma, psigma, lab_a, lab_b,
-      parent, prop, rank, ctl, total;
+      parent, prop, rank, ctl, hubs, hub_count, total;
 };
 
 LeidenLayout leiden_layout(int64_t E, int32_t G, int32_t S) {
@@ -591,6 +784,8 @@ LeidenLayout leiden_layout(int64_t E, int32_t G, int32_t S) {
   L.prop = take(V * 4);
   L.rank = take(V * 4);
   L.ctl = take(CTL_WORDS * 4);
+  L.hubs = take(V * 4);
+  L.hub_count = take(4);
   L.total = off;
   return L;
 }
@@ -678,6 +873,8 @@ extern "C" int ckv_batched_leiden(const int32_t* edge_src, const int32_t* edge_d
   int32_t* prop = (int32_t*)(ws + L.prop);
   uint32_t* rank = (uint32_t*)(ws + L.rank);
   int32_t* ctl = (int32_t*)(ws + L.ctl);
+  int32_t* hubs = (int32_t*)(ws + L.hubs);
+  int32_t* hub_count = (int32_t*)(ws + L.hub_count);
 
   const int bits = bits_for((uint64_t)V - 1);
   const int end_bit = bits + bits_for((uint64_t)V);
@@ -690,9 +887,11 @@ extern "C" int ckv_batched_leiden(const int32_t* edge_src, const int32_t* edge_d
     return ckv_internal::set_error(CKV_E_LAUNCH, "Leiden CSR sort failed");
   row_ptr_kernel<<<blocks(V + 1, ETHREADS), ETHREADS, 0, st>>>(keys_b, n, V, bits, row_ptr);
   col_kernel<<<blocks(n, ETHREADS), ETHREADS, 0, st>>>(keys_b, n, bits, col);
-  zero_kernel<<<1, 256, 0, st>>>(two_m, graphs, modularity, ctl);
+  zero_kernel<<<1, 256, 0, st>>>(two_m, graphs, modularity, ctl, hub_count);
+  hub_list_kernel<<<blocks(V, ETHREADS), ETHREADS, 0, st>>>(row_ptr, V, hubs, hub_count);
   const unsigned vgrid = blocks(V, LWAVES);
-  degree_kernel<<<vgrid, LTHREADS, 0, st>>>(row_ptr, vals_b, V, seq_len, k_v, two_m);
+  degree_kernel<<<vgrid, LTHREADS, 0, st>>>(row_ptr, vals_b, V, seq_len, k_v);
+  graph_sum_kernel<<<graphs, 256, 0, st>>>(k_v, seq_len, two_m);
   identity_kernel<<<blocks(V, ETHREADS), ETHREADS, 0, st>>>(V, lab[0]);
   const Graph gr{row_ptr, col, vals_b, k_v, two_m, V, seq_len};
 
@@ -701,8 +900,11 @@ extern "C" int ckv_batched_leiden(const int32_t* edge_src, const int32_t* edge_d
   for (int sweep = 0; sweep < max_inner_iter; ++sweep) {
     sigma_zero_kernel<<<egrid, ETHREADS, 0, st>>>(sigma, V, ctl);
     sigma_scatter_kernel<<<egrid, ETHREADS, 0, st>>>(lab[cur], k_v, V, sigma, ctl);
-    local_moving_kernel<<<vgrid, LTHREADS, 0, st>>>(gr, sigma, lab[cur], lab[cur ^ 1], ctl, resolution, 0u,
-                                                    (uint32_t)sweep, (uint32_t)seed);
+    local_moving_kernel<false><<<blocks(V, SWAVES), 64 * SWAVES, 0, st>>>(
+        gr, sigma, lab[cur], lab[cur ^ 1], ctl, hubs, hub_count, resolution, 0u, (uint32_t)sweep, (uint32_t)seed);
+    local_moving_kernel<true><<<HUB_BLOCKS, LTHREADS, 0, st>>>(gr, sigma, lab[cur], lab[cur ^ 1], ctl, hubs,
+                                                              hub_count, resolution, 0u, (uint32_t)sweep,
+                                                              (uint32_t)seed);
     lm_control_kernel<<<1, 64, 0, st>>>(ctl);
     cur ^= 1;
   }
@@ -716,16 +918,20 @@ extern "C" int ckv_batched_leiden(const int32_t* edge_src, const int32_t* edge_d
   for (int sweep = 0; sweep < max_inner_iter; ++sweep) {
     sigma_zero_kernel<<<egrid, ETHREADS, 0, st>>>(sigma, V, ctl);
     sigma_scatter_kernel<<<egrid, ETHREADS, 0, st>>>(lab[cur], k_v, V, sigma, ctl);
-    refine_propose_kernel<<<vgrid, LTHREADS, 0, st>>>(gr, parent, sigma, psigma, lab[cur], prop, rank, ctl,
-                                                      resolution, inv_theta, use_boltzmann ? 1 : 0, 1u,
-                                                      (uint32_t)sweep, (uint32_t)seed);
+    refine_propose_kernel<false><<<blocks(V, SWAVES), 64 * SWAVES, 0, st>>>(
+        gr, parent, sigma, psigma, lab[cur], prop, rank, ctl, hubs, hub_count, resolution, inv_theta,
+        use_boltzmann ? 1 : 0, 1u, (uint32_t)sweep, (uint32_t)seed);
+    refine_propose_kernel<true><<<HUB_BLOCKS, LTHREADS, 0, st>>>(
+        gr, parent, sigma, psigma, lab[cur], prop, rank, ctl, hubs, hub_count, resolution, inv_theta,
+        use_boltzmann ? 1 : 0, 1u, (uint32_t)sweep, (uint32_t)seed);
     refine_commit_kernel<<<vgrid, LTHREADS, 0, st>>>(gr, parent, lab[cur], prop, rank, lab[cur ^ 1], ctl);
     refine_control_kernel<<<1, 64, 0, st>>>(ctl);
     cur ^= 1;
   }
   sigma_zero_kernel<<<egrid, ETHREADS, 0, st>>>(sigma, V, nullptr);
   sigma_scatter_kernel<<<egrid, ETHREADS, 0, st>>>(lab[cur], k_v, V, sigma, nullptr);
-  modularity_kernel<<<vgrid, LTHREADS, 0, st>>>(gr, lab[cur], sigma, resolution, modularity);
+  modularity_kernel<<<vgrid, LTHREADS, 0, st>>>(gr, lab[cur], sigma, resolution, psigma);
+  graph_sum_kernel<<<graphs, 256, 0, st>>>(psigma, seq_len, modularity);
   finish_kernel<<<egrid, ETHREADS, 0, st>>>(row_ptr, lab[cur], V, labels);
   return launch_check();
 }
@@ -810,5 +1016,29 @@ extern "C" int ckv_densify_apply(const int32_t* labels, int32_t graphs, int32_t 
   const int32_t* scan = (const int32_t*)((const char*)workspace + align256((size_t)V * 4));
   densify_apply_kernel<<<blocks(V, ETHREADS), ETHREADS, 0, (hipStream_t)stream>>>(labels, scan, V, seq_len,
                                                                                    new_seq_len, dense);
+  return launch_check();
+}
+
+extern "C" size_t ckv_partition_modularity_workspace_bytes(int32_t vertices) {
+  return vertices <= 0 ? 0 : 2 * align256((size_t)vertices * 8) + 256;
+}
+
+extern "C" int ckv_partition_modularity(const int32_t* edge_src, const int32_t* edge_dst, const float* edge_weight,
+                                        int64_t edges, const int32_t* labels, int32_t vertices, float resolution,
+                                        double* modularity, void* workspace, void* stream) {
+  if (vertices <= 0 || edges < 0 || !labels || !modularity || !workspace ||
+      (edges > 0 && (!edge_src || !edge_dst || !edge_weight)))
+    return ckv_internal::set_error(CKV_E_INVALID, "bad modularity arguments");
+  hipStream_t st = (hipStream_t)stream;
+  double* k = (double*)workspace;
+  double* sig = (double*)((char*)workspace + align256((size_t)vertices * 8));
+  double* acc = (double*)((char*)workspace + 2 * align256((size_t)vertices * 8));
+  mod_zero_kernel<<<blocks(vertices, ETHREADS), ETHREADS, 0, st>>>(k, sig, vertices, acc);
+  if (edges > 0)
+    mod_edge_kernel<<<blocks(edges, 256), 256, 0, st>>>(edge_src, edge_dst, edge_weight, edges, labels, vertices, k,
+                                                        acc);
+  mod_sigma_kernel<<<blocks(vertices, 256), 256, 0, st>>>(labels, k, vertices, sig, acc);
+  mod_square_kernel<<<blocks(vertices, 256), 256, 0, st>>>(sig, vertices, acc);
+  mod_final_kernel<<<1, 64, 0, st>>>(acc, resolution, modularity);
   return launch_check();
 }

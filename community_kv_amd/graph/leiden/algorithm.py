@@ -168,25 +168,39 @@ def run_leiden(edge_src: torch.Tensor, edge_dst: torch.Tensor, edge_weight: torc
 def _compute_disjoint_modularity(edge_src: torch.Tensor, edge_dst: torch.Tensor, edge_weight: torch.Tensor,
                                  labels: torch.Tensor, resolution: float) -> float:
     """Newman modularity of the disjoint union of the G graphs
-    (algorithm.py:166-199), float64 device reductions."""
+    (algorithm.py:166-199): ``ckv_partition_modularity`` on device tensors
+    (f64 sums), the same formula in float64 torch ops on host tensors."""
     if edge_src.numel() == 0:
         return 0.0
+    if labels.device.type == "cuda":
+        device = nat.require_device(edge_src, edge_dst, edge_weight, labels)
+        lib = nat.lib()
+        lab = labels.to(torch.int32).contiguous()
+        V = lab.numel()
+        ws = torch.empty(max(1, (lib.ckv_partition_modularity_workspace_bytes(V) + 7) // 8), dtype=torch.int64,
+                         device=device)
+        out = torch.empty(1, dtype=torch.float64, device=device)
+        nat.check(lib.ckv_partition_modularity(nat.ptr(edge_src.contiguous()), nat.ptr(edge_dst.contiguous()),
+                                               nat.ptr(edge_weight.contiguous()), edge_src.numel(), nat.ptr(lab), V,
+                                               float(resolution), nat.ptr(out), nat.ptr(ws),
+                                               nat.stream_handle(device)))
+        return float(out.item())
     V = labels.numel()
     src = edge_src.long()
     dst = edge_dst.long()
     w64 = edge_weight.to(torch.float64)
-    k = torch.zeros(V, dtype=torch.float64, device=labels.device)
+    k = torch.zeros(V, dtype=torch.float64)
     k.scatter_add_(0, src, w64)
     k.scatter_add_(0, dst, w64)
-    two_m = float(k.sum().item())
+    two_m = float(k.sum())
     if two_m <= 0.0:
         return 0.0
     lab = labels.long()
-    in_total = 2.0 * float(w64[lab[src] == lab[dst]].sum().item())
+    in_total = 2.0 * float(w64[lab[src] == lab[dst]].sum())
     _, inverse = torch.unique(lab, return_inverse=True)
-    sigma = torch.zeros(int(inverse.max().item()) + 1, dtype=torch.float64, device=labels.device)
+    sigma = torch.zeros(int(inverse.max()) + 1, dtype=torch.float64)
     sigma.scatter_add_(0, inverse, k)
-    return in_total / two_m - resolution * float((sigma * sigma).sum().item()) / (two_m * two_m)
+    return in_total / two_m - resolution * float((sigma * sigma).sum()) / (two_m * two_m)
 
 
 __all__ = ["run_leiden"]

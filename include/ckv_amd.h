@@ -321,6 +321,16 @@ int ckv_aggregate_coo(const int32_t* edge_src, const int32_t* edge_dst, const fl
                       const int32_t* labels, int32_t super_vertices, int32_t* out_src, int32_t* out_dst,
                       float* out_weight, int64_t* out_count, void* workspace, void* stream);
 
+/* Newman modularity of a labelled edge list taken as one graph (the disjoint
+ * union of the per-graph edge lists), labels in [0, vertices): sum of the
+ * weights inside communities over m minus resolution * sum of squared
+ * community degrees over (2m)^2 (graph/leiden/algorithm.py:166-199, the
+ * final modularity of run_leiden()).  *modularity is device f64. */
+size_t ckv_partition_modularity_workspace_bytes(int32_t vertices);
+int ckv_partition_modularity(const int32_t* edge_src, const int32_t* edge_dst, const float* edge_weight,
+                             int64_t edges, const int32_t* labels, int32_t vertices, float resolution,
+                             double* modularity, void* workspace, void* stream);
+
 /* Per-graph dense relabelling: a vertex's label (its own id when negative)
  * becomes its rank among the distinct labels of its graph, plus
  * g * new_seq_len.  ckv_densify_count writes the distinct count per graph
