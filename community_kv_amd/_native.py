@@ -74,6 +74,9 @@ EXPORTED_SYMBOLS = (
     "ckv_densify_apply",
     "ckv_partition_modularity_workspace_bytes",
     "ckv_partition_modularity",
+    "ckv_adjacency_workspace_bytes",
+    "ckv_adjacency_capacity",
+    "ckv_build_adjacency",
     "ckv_host_numerics",
     "ckv_device_numerics",
     "ckv_abi_version",
@@ -229,6 +232,12 @@ def lib() -> ctypes.CDLL:
     handle.ckv_partition_modularity_workspace_bytes.restype = ctypes.c_size_t
     handle.ckv_partition_modularity.argtypes = [_p, _p, _p, _i64, _p, _i32, _f32, _p, _p, _p]
     handle.ckv_partition_modularity.restype = ctypes.c_int
+    handle.ckv_adjacency_workspace_bytes.argtypes = [_i32, _i32, _i32, _f32]
+    handle.ckv_adjacency_workspace_bytes.restype = ctypes.c_size_t
+    handle.ckv_adjacency_capacity.argtypes = [_i32, _i32, _i32, _f32]
+    handle.ckv_adjacency_capacity.restype = ctypes.c_int64
+    handle.ckv_build_adjacency.argtypes = [_p, _p, _p, _i32, _i32, _i32, _i32, _f32, _p, _p, _p, _p, _p, _p]
+    handle.ckv_build_adjacency.restype = ctypes.c_int
     handle.ckv_host_numerics.argtypes = [ctypes.c_int, _p, _p, _i64]
     handle.ckv_host_numerics.restype = ctypes.c_int
     handle.ckv_device_numerics.argtypes = [ctypes.c_int, _p, _p, _i64, _p]

@@ -825,6 +825,81 @@ size_t densify_temp_bytes(int64_t V) {
   return bytes;
 }
 
+// Sort the (key, weight) pairs in keys_a / vals_a of an AggLayout, sum equal
+// keys, drop the sentinel run and unpack (src, dst).
+int coalesce(const AggLayout& L, char* ws, int64_t n, int32_t vertices, int bits, int end_bit, int32_t* out_src,
+             int32_t* out_dst, float* out_weight, int64_t* out_count, hipStream_t st) {
+  uint64_t* keys_a = (uint64_t*)(ws + L.keys_a);
+  uint64_t* keys_b = (uint64_t*)(ws + L.keys_b);
+  float* vals_in = (float*)(ws + L.vals_a);
+  float* vals_sorted = vals_in + n;
+  uint64_t* uniq = (uint64_t*)(ws + L.uniq);
+  size_t temp_bytes = L.temp_bytes;
+  if (hipcub::DeviceRadixSort::SortPairs(ws + L.temp, temp_bytes, keys_a, keys_b, vals_in, vals_sorted, (int)n, 0,
+                                         end_bit, st) != hipSuccess)
+    return ckv_internal::set_error(CKV_E_LAUNCH, "edge sort failed");
+  temp_bytes = L.temp_bytes;
+  if (hipcub::DeviceReduce::ReduceByKey(ws + L.temp, temp_bytes, keys_b, uniq, vals_sorted, out_weight, out_count,
+                                        hipcub::Sum(), (int)n, st) != hipSuccess)
+    return ckv_internal::set_error(CKV_E_LAUNCH, "edge reduce failed");
+  count_fix_kernel<<<1, 64, 0, st>>>(uniq, vertices, bits, out_count);
+  unpack_kernel<<<blocks(n, ETHREADS), ETHREADS, 0, st>>>(uniq, n, bits, out_count, out_src, out_dst);
+  return launch_check();
+}
+
+// Entries of the top-k graph (partition.py:168-249): per row of graph g at
+// position p, kappa direct edges (p, col) of weight score * lam / 2 and, when
+// lam < 1, kappa (kappa + 1) / 2 co-occurrence pairs (col_i, col_j), i <= j,
+// of weight score_i * score_j * (1 - lam); columns outside [0, S) drop the
+// entry (sentinel key).  Ends in (min, max) order, global ids g * S + i.
+__global__ void adjacency_expand_kernel(const int32_t* __restrict__ idx, const float* __restrict__ sc,
+                                        const int64_t* __restrict__ positions, int32_t G, int32_t R, int32_t kappa,
+                                        int32_t S, float half_lam, float co_lam, int32_t per_row, int bits,
+                                        uint64_t* __restrict__ keys, float* __restrict__ vals) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t n = (int64_t)G * R * per_row;
+  if (i >= n) return;
+  const int64_t row = i / per_row;
+  int t = (int)(i - row * per_row);
+  const int32_t g = (int32_t)(row / R);
+  const int32_t* ri = idx + row * kappa;
+  const float* rs = sc + row * kappa;
+  const uint64_t sentinel = (uint64_t)((int64_t)G * S) << bits;
+  const int64_t base = (int64_t)g * S;
+  int64_t a, b;
+  float w;
+  bool ok;
+  if (t < kappa) {
+    const int32_t c = ri[t];
+    const int64_t p = positions[row];
+    ok = c >= 0 && c < S && p >= 0 && p < S;
+    a = base + p;
+    b = base + c;
+    w = rs[t] * half_lam;
+  } else {
+    t -= kappa;  // pair t of the upper triangle (diagonal included), row-major
+    int r0 = 0;
+    while (t >= kappa - r0) {
+      t -= kappa - r0;
+      ++r0;
+    }
+    const int r1 = r0 + t;
+    const int32_t c0 = ri[r0], c1 = ri[r1];
+    ok = c0 >= 0 && c0 < S && c1 >= 0 && c1 < S;
+    a = base + c0;
+    b = base + c1;
+    w = (rs[r0] * rs[r1]) * co_lam;
+  }
+  const int64_t lo = a < b ? a : b, hi = a < b ? b : a;
+  keys[i] = ok ? ((uint64_t)lo << bits) | (uint64_t)hi : sentinel;
+  vals[i] = ok ? w : 0.0f;
+}
+
+inline int64_t adjacency_entries(int32_t graphs, int32_t rows, int32_t kappa, float lam) {
+  const int per_row = kappa + (lam < 1.0f ? kappa * (kappa + 1) / 2 : 0);
+  return (int64_t)graphs * rows * per_row;
+}
+
 }  // namespace
 }  // namespace ckv
 
@@ -958,25 +1033,12 @@ extern "C" int ckv_aggregate_coo(const int32_t* edge_src, const int32_t* edge_ds
   const AggLayout L = agg_layout(edges);
   char* ws = (char*)workspace;
   uint64_t* keys_a = (uint64_t*)(ws + L.keys_a);
-  uint64_t* keys_b = (uint64_t*)(ws + L.keys_b);
   float* vals_in = (float*)(ws + L.vals_a);
-  float* vals_sorted = vals_in + edges;
-  uint64_t* uniq = (uint64_t*)(ws + L.uniq);
   const int bits = bits_for((uint64_t)super_vertices - 1);
   const int end_bit = bits + bits_for((uint64_t)super_vertices);
   remap_kernel<<<blocks(edges, ETHREADS), ETHREADS, 0, st>>>(edge_src, edge_dst, edge_weight, labels, edges,
                                                              super_vertices, bits, keys_a, vals_in);
-  size_t temp_bytes = L.temp_bytes;
-  if (hipcub::DeviceRadixSort::SortPairs(ws + L.temp, temp_bytes, keys_a, keys_b, vals_in, vals_sorted, (int)edges, 0,
-                                         end_bit, st) != hipSuccess)
-    return ckv_internal::set_error(CKV_E_LAUNCH, "aggregation sort failed");
-  temp_bytes = L.temp_bytes;
-  if (hipcub::DeviceReduce::ReduceByKey(ws + L.temp, temp_bytes, keys_b, uniq, vals_sorted, out_weight, out_count,
-                                        hipcub::Sum(), (int)edges, st) != hipSuccess)
-    return ckv_internal::set_error(CKV_E_LAUNCH, "aggregation reduce failed");
-  count_fix_kernel<<<1, 64, 0, st>>>(uniq, super_vertices, bits, out_count);
-  unpack_kernel<<<blocks(edges, ETHREADS), ETHREADS, 0, st>>>(uniq, edges, bits, out_count, out_src, out_dst);
-  return launch_check();
+  return coalesce(L, ws, edges, super_vertices, bits, end_bit, out_src, out_dst, out_weight, out_count, st);
 }
 
 extern "C" size_t ckv_densify_workspace_bytes(int32_t graphs, int32_t seq_len) {
@@ -1041,4 +1103,43 @@ extern "C" int ckv_partition_modularity(const int32_t* edge_src, const int32_t* 
   mod_square_kernel<<<blocks(vertices, 256), 256, 0, st>>>(sig, vertices, acc);
   mod_final_kernel<<<1, 64, 0, st>>>(acc, resolution, modularity);
   return launch_check();
+}
+
+extern "C" size_t ckv_adjacency_workspace_bytes(int32_t graphs, int32_t rows, int32_t kappa, float lam) {
+  if (graphs <= 0 || rows < 0 || kappa <= 0) return 0;
+  const int64_t n = adjacency_entries(graphs, rows, kappa, lam);
+  return n == 0 ? 0 : agg_layout(n).total;
+}
+
+extern "C" int64_t ckv_adjacency_capacity(int32_t graphs, int32_t rows, int32_t kappa, float lam) {
+  if (graphs <= 0 || rows < 0 || kappa <= 0) return 0;
+  return adjacency_entries(graphs, rows, kappa, lam);
+}
+
+extern "C" int ckv_build_adjacency(const int32_t* topk_indices, const float* topk_scores,
+                                   const int64_t* query_positions, int32_t graphs, int32_t rows, int32_t kappa,
+                                   int32_t seq_len, float lam, int32_t* out_src, int32_t* out_dst, float* out_weight,
+                                   int64_t* out_count, void* workspace, void* stream) {
+  if (graphs <= 0 || rows < 0 || kappa <= 0 || kappa > 64 || seq_len <= 0 || !out_count || !(lam >= 0.0f && lam <= 1.0f))
+    return ckv_internal::set_error(CKV_E_INVALID, "bad adjacency sizes (kappa <= 64, lam in [0, 1])");
+  hipStream_t st = (hipStream_t)stream;
+  const int64_t n = adjacency_entries(graphs, rows, kappa, lam);
+  if (n == 0) {
+    if (hipMemsetAsync(out_count, 0, 8, st) != hipSuccess) return launch_check();
+    return 0;
+  }
+  if (!topk_indices || !topk_scores || !query_positions || !out_src || !out_dst || !out_weight || !workspace)
+    return ckv_internal::set_error(CKV_E_INVALID, "null adjacency pointer");
+  const int64_t V = (int64_t)graphs * seq_len;
+  if (n >= ((int64_t)1 << 31) - 1 || V >= (int64_t)1 << 30)
+    return ckv_internal::set_error(CKV_E_LIMIT, "adjacency too large");
+  const AggLayout L = agg_layout(n);
+  char* ws = (char*)workspace;
+  const int bits = bits_for((uint64_t)V - 1);
+  const int end_bit = bits + bits_for((uint64_t)V);
+  const int per_row = (int)(n / ((int64_t)graphs * rows));
+  adjacency_expand_kernel<<<blocks(n, ETHREADS), ETHREADS, 0, st>>>(
+      topk_indices, topk_scores, query_positions, graphs, rows, kappa, seq_len, lam / 2.0f, 1.0f - lam, per_row, bits,
+      (uint64_t*)(ws + L.keys_a), (float*)(ws + L.vals_a));
+  return coalesce(L, ws, n, (int32_t)V, bits, end_bit, out_src, out_dst, out_weight, out_count, st);
 }

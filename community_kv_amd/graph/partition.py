@@ -83,7 +83,11 @@ def aggregation_mappings(aggregation: GraphAggregation, *, query_heads: int, kv_
 def build_adjacency(topk_indices: torch.Tensor, topk_scores: torch.Tensor, query_positions: torch.Tensor,
                     *, seq_len: int, lam: float) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """Coalesced disjoint batched token graph from top-k edges (partition.py:168-249):
-    direct edges weighted lam/2 * p, co-occurrence edges (1 - lam) * p_i * p_j."""
+    direct edges weighted lam/2 * p, co-occurrence edges (1 - lam) * p_i * p_j.
+    Device tensors run ``ckv_build_adjacency`` (one radix sort of the edge
+    keys, equal pairs summed); the torch ops below serve host tensors."""
+    if topk_indices.device.type == "cuda":
+        return _native_adjacency(topk_indices, topk_scores, query_positions, seq_len=seq_len, lam=lam)
     graphs, _, kappa = topk_indices.shape
     device = topk_indices.device
     total = graphs * seq_len
@@ -107,6 +111,30 @@ def build_adjacency(topk_indices: torch.Tensor, topk_scores: torch.Tensor, query
     weight = torch.zeros(unique.shape[0], dtype=torch.float32, device=device)
     weight.scatter_add_(0, inverse, torch.cat(a_w))
     return (unique // total).to(torch.int32), (unique % total).to(torch.int32), weight
+
+
+def _native_adjacency(topk_indices: torch.Tensor, topk_scores: torch.Tensor, query_positions: torch.Tensor, *,
+                      seq_len: int, lam: float) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    from community_kv_amd import _native as nat
+
+    device = nat.require_device(topk_indices, topk_scores, query_positions)
+    graphs, rows, kappa = topk_indices.shape
+    idx = topk_indices.to(torch.int32).contiguous()
+    sc = topk_scores.to(torch.float32).contiguous()
+    pos = query_positions.to(torch.int64).expand(graphs, rows).contiguous()
+    lib = nat.lib()
+    cap = lib.ckv_adjacency_capacity(graphs, rows, kappa, float(lam))
+    out_src = torch.empty(max(cap, 1), dtype=torch.int32, device=device)
+    out_dst = torch.empty(max(cap, 1), dtype=torch.int32, device=device)
+    out_w = torch.empty(max(cap, 1), dtype=torch.float32, device=device)
+    count = torch.zeros(1, dtype=torch.int64, device=device)
+    ws = torch.empty(max(1, (lib.ckv_adjacency_workspace_bytes(graphs, rows, kappa, float(lam)) + 7) // 8),
+                     dtype=torch.int64, device=device)
+    nat.check(lib.ckv_build_adjacency(nat.ptr(idx), nat.ptr(sc), nat.ptr(pos), graphs, rows, kappa, seq_len,
+                                      float(lam), nat.ptr(out_src), nat.ptr(out_dst), nat.ptr(out_w), nat.ptr(count),
+                                      nat.ptr(ws), nat.stream_handle(device)))
+    n = int(count.item())
+    return out_src[:n], out_dst[:n], out_w[:n]
 
 
 def compute_centroids(community_ids: torch.Tensor, community_counts: torch.Tensor, keys: torch.Tensor, *,

@@ -30,6 +30,7 @@
  *   ckv_label_counts,       the state build of build_partitioned_layer() after Leiden
  *   ckv_build_layer_state   (graph/partition.py:538-618): compute_centroids 382-454,
  *                           build_member_csr 457-492, init_modularity_state 495-535
+ *   ckv_build_adjacency     build_adjacency()                 graph/partition.py:168-249
  *   ckv_batched_leiden      batched_leiden() of the Leiden extension (graph/leiden/_csrc/bindings.cpp:40-103,
  *                           launch_batched_leiden in leiden.cu:43-205), called by run_leiden()
  *                           (graph/leiden/algorithm.py:51-161)
@@ -320,6 +321,21 @@ size_t ckv_aggregate_coo_workspace_bytes(int64_t edges);
 int ckv_aggregate_coo(const int32_t* edge_src, const int32_t* edge_dst, const float* edge_weight, int64_t edges,
                       const int32_t* labels, int32_t super_vertices, int32_t* out_src, int32_t* out_dst,
                       float* out_weight, int64_t* out_count, void* workspace, void* stream);
+
+/* The coalesced top-k graph of build_adjacency() (graph/partition.py:168-249):
+ * topk_indices / topk_scores [graphs][rows][kappa] (int32 / f32), row r of
+ * graph g at position query_positions[g][r] (int64).  Direct edges
+ * (position, column) weigh score * lam / 2; when lam < 1, every pair i <= j
+ * of a row's columns adds score_i * score_j * (1 - lam).  Columns outside
+ * [0, seq_len) are dropped.  Output: upper-triangular COO over global ids
+ * g * seq_len + i, sorted by (src, dst), equal pairs summed; room for
+ * ckv_adjacency_capacity() entries, *out_count (device int64) = entries
+ * written. */
+size_t ckv_adjacency_workspace_bytes(int32_t graphs, int32_t rows, int32_t kappa, float lam);
+int64_t ckv_adjacency_capacity(int32_t graphs, int32_t rows, int32_t kappa, float lam);
+int ckv_build_adjacency(const int32_t* topk_indices, const float* topk_scores, const int64_t* query_positions,
+                        int32_t graphs, int32_t rows, int32_t kappa, int32_t seq_len, float lam, int32_t* out_src,
+                        int32_t* out_dst, float* out_weight, int64_t* out_count, void* workspace, void* stream);
 
 /* Newman modularity of a labelled edge list taken as one graph (the disjoint
  * union of the per-graph edge lists), labels in [0, vertices): sum of the

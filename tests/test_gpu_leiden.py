@@ -157,3 +157,44 @@ def test_partition_graphs_matches_oracle_pipeline(device):
     np.testing.assert_array_equal(res.community_ids.cpu().numpy(), ids)
     assert res.community_counts.cpu().tolist() == (ids.max(axis=1) + 1).tolist()
     assert res.modularity == pytest.approx(q, abs=1e-9)
+
+
+def test_build_adjacency_known_answers(device):
+    """The reference tests' coalescing / discard cases (test_partition.py:212-250) through ckv_build_adjacency."""
+    import json
+    import os
+
+    from community_kv_amd.graph.partition import build_adjacency
+
+    golden = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "reference_known_answers.json")))
+    for name in ("adjacency_coalesces", "adjacency_discards_outside"):
+        ka = golden[name]
+        src, dst, w = build_adjacency(torch.tensor(ka["indices"], dtype=torch.int32, device=device),
+                                      torch.tensor(ka["scores"], dtype=torch.float32, device=device),
+                                      torch.tensor(ka["query_positions"], dtype=torch.int64, device=device),
+                                      seq_len=ka["seq_len"], lam=ka["lam"])
+        got = sorted(zip(src.tolist(), dst.tolist(), w.tolist()))
+        assert got == sorted(tuple(p) for p in ka["pairs"]), name
+
+
+@pytest.mark.parametrize("lam,dyadic", [(0.5, True), (1.0, False), (0.0, True), (0.3, False)])
+def test_build_adjacency_matches_oracle(device, lam, dyadic):
+    from community_kv_amd.graph.partition import build_adjacency
+    from oracle import ckv_oracle as co
+
+    rng = np.random.default_rng(int(lam * 10) + dyadic)
+    G, R, kappa, S = 3, 2000, 8, 1500
+    idx = rng.integers(0, S, (G, R, kappa)).astype(np.int32)
+    idx[rng.random(idx.shape) < 0.05] = -1
+    idx[rng.random(idx.shape) < 0.02] = S + 5
+    sc = (rng.integers(1, 32, idx.shape) / 32.0 if dyadic else rng.random(idx.shape)).astype(np.float32)
+    pos = rng.integers(0, S, (G, R)).astype(np.int64)
+    print(f"build_adjacency lam={lam} dyadic={dyadic}", flush=True)
+    s, d, w = build_adjacency(*_dev(device, idx, sc, pos), seq_len=S, lam=lam)
+    rs, rd, rw = co.build_adjacency(idx, sc, pos, seq_len=S, lam=lam)
+    np.testing.assert_array_equal(s.cpu().numpy(), rs)
+    np.testing.assert_array_equal(d.cpu().numpy(), rd)
+    if dyadic:
+        np.testing.assert_array_equal(w.cpu().numpy(), rw)
+    else:
+        np.testing.assert_allclose(w.cpu().numpy(), rw, rtol=2e-6)
