@@ -41,20 +41,23 @@ def _labels(layer_idx, keys, topk_indices, topk_scores):
     return lab
 
 
-@pytest.mark.parametrize("assignment,graph", [("delta_q", True), ("nearest_centroid", True), ("delta_q", False)])
-def test_generate_full_selection_matches_dense(device, assignment, graph):
+@pytest.mark.parametrize("assignment,graph,leiden", [("delta_q", True, False), ("nearest_centroid", True, False),
+                                                     ("delta_q", False, False), ("delta_q", True, True)])
+def test_generate_full_selection_matches_dense(device, assignment, graph, leiden):
+    """``leiden``: no label provider, every prefill layer is partitioned by the
+    native Leiden on its top-k edges (build_partitioned_layer)."""
     from community_kv_amd import CommunityKVAttention, CommunityKVConfig, CommunityKVRuntime, GraphAggregation
     from community_kv_amd.config import PartitionConfig
 
-    print(f"generate e2e assignment={assignment} graph={graph}", flush=True)
+    print(f"generate e2e assignment={assignment} graph={graph} leiden={leiden}", flush=True)
     model = _model(device)
     prompt = torch.randint(0, 512, (1, 300), generator=torch.Generator().manual_seed(1)).to(device)
     new = 8
     cfg = CommunityKVConfig(token_budget=4096, num_sink=10, aggregation=GraphAggregation.QUERY_GROUP,
-                            selection="topk", topk_communities=COMMUNITIES, max_selected=4096,
-                            assignment=assignment)
+                            selection="topk", topk_communities=8192 if leiden else COMMUNITIES,
+                            max_selected=4096, assignment=assignment)
     with CommunityKVRuntime(config=cfg, partition=PartitionConfig(), num_layers=LAYERS, max_decode_tokens=new,
-                            label_provider=_labels) as runtime:
+                            label_provider=None if leiden else _labels) as runtime:
         CommunityKVAttention(runtime).register()
         model.set_attn_implementation("community_kv")
         with torch.inference_mode():
@@ -67,6 +70,8 @@ def test_generate_full_selection_matches_dense(device, assignment, graph):
         for layer in runtime.decode_runtime.layers.values():
             cur = layer.converted.current_position.cpu()
             assert bool((cur == 300 + new - 1).all()), cur
+            if leiden:  # Leiden found several communities in every graph
+                assert min(layer.converted.initial_community_counts) > 1
     # teacher-forced dense reference over the generated sequence (greedy near-ties
     # cannot make the two runs diverge)
     seq = out.sequences
