@@ -523,7 +523,7 @@ def run_generate(args, device):
     cfg = CommunityKVConfig(token_budget=BUDGET, num_sink=SINKS, aggregation=GraphAggregation.QUERY_GROUP,
                             local_window=WINDOW, assignment="nearest_centroid")
     with CommunityKVRuntime(config=cfg, partition=PartitionConfig(), num_layers=layers, max_decode_tokens=steps,
-                            label_provider=labels) as runtime:
+                            label_provider=None if args.leiden else labels) as runtime:
         CommunityKVAttention(runtime).register()
         model.set_attn_implementation("community_kv")
 
@@ -553,7 +553,9 @@ def run_generate(args, device):
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (uniform random prompt ids, random-init weights, Zipf(1.1) labels over ~1024 communities)",
+        "data": ("synthetic (uniform random prompt ids, random-init weights, "
+                 + ("communities from the native Leiden on each layer's prefill top-8 edges)" if args.leiden
+                    else "Zipf(1.1) labels over ~1024 communities)")),
         "config": {"workload": "BASELINE config 3: random-init Qwen3-8B architecture, greedy decode through "
                                "CommunityKVRuntime.generate, nearest-centroid assignment",
                    "layers": layers, "prompt_tokens": prompt_len, "decode_steps": steps, "token_budget": BUDGET,
@@ -649,6 +651,8 @@ def main():
     ap.add_argument("--layers", type=int, default=LAYERS)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--leiden", action="store_true",
+                    help="generate: partition every prompt layer with the native Leiden instead of synthetic labels")
     ap.add_argument("--workload", choices=["decode", "prefill", "generate", "batched", "state", "partition"], default="decode",
                     help="decode: the 36-layer sparse decode step (default); prefill: config-5 edge export; "
                          "generate: config-3 model decode loop; batched: config-4 ragged batch; "
