@@ -467,7 +467,7 @@ __device__ void refine_propose_vertex(const Graph& gr, const int32_t* __restrict
 // over the list.
 constexpr int SMALL_CAP = 256;
 constexpr int SWAVES = 8;
-constexpr int HUB_BLOCKS = 512;
+constexpr int HUB_BLOCKS = 768;  // three 48 KB workgroups per CU
 
 __global__ void hub_list_kernel(const int32_t* __restrict__ row_ptr, int32_t V, int32_t* __restrict__ hubs,
                                 int32_t* __restrict__ hub_count) {

@@ -122,6 +122,12 @@ def run_leiden(edge_src: torch.Tensor, edge_dst: torch.Tensor, edge_weight: torc
     edge_weight = edge_weight.contiguous()
     V_orig = G * seq_len
     device = edge_src.device
+    if edge_src.numel():
+        # every edge inside one graph: the per-graph relabelling depends on it
+        lo = torch.minimum(edge_src, edge_dst)
+        bad = (lo < 0) | (torch.maximum(edge_src, edge_dst) >= V_orig) | (edge_src // seq_len != edge_dst // seq_len)
+        if bool(bad.any()):
+            raise ValueError("edges must join two vertices of the same graph, ids in [0, G * seq_len)")
 
     theta_env = os.environ.get("COMMUNITY_KV_LEIDEN_THETA")
     if theta_env is not None:

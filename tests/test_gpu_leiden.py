@@ -198,3 +198,9 @@ def test_build_adjacency_matches_oracle(device, lam, dyadic):
         np.testing.assert_array_equal(w.cpu().numpy(), rw)
     else:
         np.testing.assert_allclose(w.cpu().numpy(), rw, rtol=2e-6)
+
+
+def test_run_leiden_rejects_edges_across_graphs(device):
+    s, d, w = _dev(device, np.array([0, 3], np.int32), np.array([1, 5], np.int32), np.ones(2, np.float32))
+    with pytest.raises(ValueError, match="same graph"):
+        algorithm.run_leiden(s, d, w, G=2, seq_len=4)
