@@ -127,10 +127,13 @@ def test_ring_of_cliques_end_to_end(device):
     assert (by_clique == by_clique[..., :1]).all() and np.unique(by_clique[..., 0]).size == 12
 
 
-def test_partition_graphs_matches_oracle_pipeline(device):
+@pytest.mark.parametrize("aggregation", ["query_group", "per_query_head", "layer_wise"])
+def test_partition_graphs_matches_oracle_pipeline(device, aggregation):
     """Top-k prefill edges -> build_adjacency -> Leiden -> dense community ids
-    (partition.py:289-353), against the oracle's composition."""
-    from community_kv_amd.graph.partition import partition_graphs
+    (partition.py:289-353), against the oracle's composition; then
+    build_partitioned_layer (538-618) on the same edges: community count over
+    all positions (sink singletons included) and the token table."""
+    from community_kv_amd.graph import partition as P
     from oracle import ckv_oracle as co
 
     rng = np.random.default_rng(17)
@@ -145,18 +148,25 @@ def test_partition_graphs_matches_oracle_pipeline(device):
         for h in range(Hq):
             idx[h, r] = rng.choice(pool, kappa, replace=False)
     sc = (rng.integers(1, 32, idx.shape) / 32.0).astype(np.float32)
-    print("partition_graphs pipeline", flush=True)
-    res = partition_graphs(torch.from_numpy(idx).to(device), torch.from_numpy(sc).to(device),
-                           aggregation="query_group", num_kv_heads=Hkv, prefill_seq_len=S, num_sink=sinks, lam=0.5,
-                           leiden_resolution=1.0, leiden_seed=0)
-    group = Hq // Hkv
-    pos = np.tile(np.arange(sinks + kappa - 1, sinks + kappa - 1 + rows), group)[None].repeat(Hkv, 0)
-    src, dst, w = co.build_adjacency(idx.reshape(Hkv, group * rows, kappa), sc.reshape(Hkv, group * rows, kappa),
-                                     pos, seq_len=S, lam=0.5)
-    ids, q = L.partition_labels(src, dst, w, graphs=Hkv, seq_len=S, resolution=1.0, max_inner_iter=3, seed=0)
+    print(f"partition_graphs pipeline {aggregation}", flush=True)
+    ti, ts = torch.from_numpy(idx).to(device), torch.from_numpy(sc).to(device)
+    res = P.partition_graphs(ti, ts, aggregation=aggregation, num_kv_heads=Hkv, prefill_seq_len=S, num_sink=sinks,
+                             lam=0.5, leiden_resolution=1.0, leiden_seed=0)
+    gi, gs, pos = P._reshape_by_aggregation(torch.from_numpy(idx), torch.from_numpy(sc), aggregation=aggregation,
+                                            num_kv_heads=Hkv, num_sink=sinks)
+    graphs = gi.shape[0]
+    src, dst, w = co.build_adjacency(gi.numpy(), gs.numpy(), pos.numpy(), seq_len=S, lam=0.5)
+    ids, q = L.partition_labels(src, dst, w, graphs=graphs, seq_len=S, resolution=1.0, max_inner_iter=3, seed=0)
     np.testing.assert_array_equal(res.community_ids.cpu().numpy(), ids)
     assert res.community_counts.cpu().tolist() == (ids.max(axis=1) + 1).tolist()
     assert res.modularity == pytest.approx(q, abs=1e-9)
+    keys = torch.randn(Hkv, S, 128, generator=torch.Generator().manual_seed(2)).to(torch.bfloat16).to(device)
+    layer = P.build_partitioned_layer(layer_idx=0, topk_indices=ti, topk_scores=ts, keys=keys, num_sink=sinks,
+                                      lam=0.5, leiden_resolution=1.0, leiden_seed=0, max_decode_tokens=4,
+                                      aggregation=aggregation)
+    assert layer.community_counts.cpu().tolist() == (ids.max(axis=1) + 1).tolist()
+    np.testing.assert_array_equal(layer.token_communities[:, :S].cpu().numpy(), ids)
+    assert (layer.token_communities[:, S:] == -1).all()
 
 
 def test_build_adjacency_known_answers(device):
