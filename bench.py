@@ -522,7 +522,8 @@ def run_generate(args, device):
 
     cfg = CommunityKVConfig(token_budget=BUDGET, num_sink=SINKS, aggregation=GraphAggregation.QUERY_GROUP,
                             local_window=WINDOW, assignment="nearest_centroid")
-    with CommunityKVRuntime(config=cfg, partition=PartitionConfig(), num_layers=layers, max_decode_tokens=steps,
+    with CommunityKVRuntime(config=cfg, partition=PartitionConfig(overlap=not args.partition_inline),
+                            num_layers=layers, max_decode_tokens=steps,
                             label_provider=None if args.leiden else labels) as runtime:
         CommunityKVAttention(runtime).register()
         model.set_attn_implementation("community_kv")
@@ -653,6 +654,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--leiden", action="store_true",
                     help="generate: partition every prompt layer with the native Leiden instead of synthetic labels")
+    ap.add_argument("--partition-inline", action="store_true",
+                    help="generate --leiden: partition each layer inline instead of on the overlapping worker")
     ap.add_argument("--workload", choices=["decode", "prefill", "generate", "batched", "state", "partition"], default="decode",
                     help="decode: the 36-layer sparse decode step (default); prefill: config-5 edge export; "
                          "generate: config-3 model decode loop; batched: config-4 ragged batch; "

@@ -84,10 +84,15 @@ class CommunityKVConfig:
 
 @dataclass(frozen=True, slots=True)
 class PartitionConfig:
-    """Dedicated-GPU prefill partition scheduling configuration."""
+    """Prefill partition scheduling (reference config.py:61-70).  ``devices``
+    names GPUs for partition offload (only the model's own GPU is supported
+    here); ``overlap`` (this build's switch) runs each layer's partition on a
+    worker thread and its own stream so that it overlaps the prefill of later
+    layers, as the reference's worker pool does; ``False`` runs it inline."""
 
     devices: tuple[str, ...] = ()
     workers_per_device: int = 2
+    overlap: bool = True
 
     def __post_init__(self) -> None:
         if self.workers_per_device <= 0:

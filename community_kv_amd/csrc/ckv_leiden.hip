@@ -29,9 +29,10 @@
 //   mirror_kernel, radix sort, row_ptr_kernel, col_kernel, zero_kernel, hub_list_kernel, degree_kernel,
 //   graph_sum_kernel (2m), identity_kernel
 //   local moving x max_inner_iter: sigma_zero, sigma_scatter, local_moving_kernel (small rows, then
-//                                  hubs), lm_control_kernel
+//                                  hubs), local_moving_giant_kernel, lm_control_kernel
 //   refine_init_kernel, parent sigma
 //   refinement x max_inner_iter: sigma_zero, sigma_scatter, refine_propose_kernel (small, hubs),
+//                                refine_propose_giant_kernel,
 //                                refine_commit_kernel, refine_control_kernel
 //   sigma of the result, modularity_kernel, graph_sum_kernel, finish_kernel (labels, -1 for isolated)
 #include <hip/hip_runtime.h>
@@ -124,12 +125,12 @@ __device__ inline void mark_moved(int32_t* ctl) {
 // number of table slots to scan (wave-uniform; empty slots hold -1); *e_sum
 // gets the summed weight of the admitted entries (every lane).
 //
-// Rows of at most CAP / 2 entries (nearly all): every lane inserts its
-// neighbour's community into an open-addressing table of 2 x degree slots
-// (LDS compare-and-swap) and adds its weight with an LDS f64 atomic.  Longer
-// rows (hubs, where the TABLE_CAP limit can bite): a leader loop over the
-// chunk's distinct communities, entries in order of first appearance along
-// the row, later ones dropped once TABLE_CAP are held.
+// Rows of at most CAP entries (all rows the per-wave kernels take): every
+// lane inserts its neighbour's community into an open-addressing table of
+// min(2 x degree, CAP) slots (LDS compare-and-swap) and adds its weight with an
+// LDS f64 atomic.  Longer rows (the workgroup kernels' fallback): a leader
+// loop over the chunk's distinct communities, entries in order of first
+// appearance along the row, later ones dropped once CAP are held.
 template <int CAP>
 __device__ int build_table(int32_t* tc, double* ts, const int32_t* __restrict__ col,
                            const float* __restrict__ wt, const int32_t* __restrict__ lab,
@@ -137,9 +138,9 @@ __device__ int build_table(int32_t* tc, double* ts, const int32_t* __restrict__ 
                            double* e_sum) {
   const int ln = lane();
   double e_acc = 0.0;
-  if (b - a <= CAP / 2) {
+  if (b - a <= CAP) {  // at most CAP distinct communities: no capacity rule to apply
     int size = 64;
-    while (size < 2 * (b - a)) size <<= 1;
+    while (size < 2 * (b - a) && size < CAP) size <<= 1;
     for (int j = ln; j < size; j += 64) {
       tc[j] = -1;
       ts[j] = 0.0;
@@ -257,14 +258,18 @@ __global__ void col_kernel(const uint64_t* __restrict__ keys, int64_t n, int bit
 }
 
 __global__ void zero_kernel(double* __restrict__ two_m, int32_t G, double* __restrict__ modularity,
-                            int32_t* __restrict__ ctl, int32_t* __restrict__ hub_count) {
+                            int32_t* __restrict__ ctl, int32_t* __restrict__ hub_count,
+                            int32_t* __restrict__ giant_count) {
   const int i = threadIdx.x;
   for (int g = i; g < G; g += blockDim.x) {
     two_m[g] = 0.0;
     modularity[g] = 0.0;
   }
   if (i < CTL_WORDS) ctl[i] = i == CTL_UPDOWN ? 1 : 0;  // local moving starts with upward moves
-  if (i == 0) *hub_count = 0;
+  if (i == 0) {
+    *hub_count = 0;
+    *giant_count = 0;
+  }
 }
 
 __global__ __launch_bounds__(LTHREADS) void degree_kernel(const int32_t* __restrict__ row_ptr,
@@ -469,10 +474,171 @@ constexpr int SMALL_CAP = 256;
 constexpr int SWAVES = 8;
 constexpr int HUB_BLOCKS = 768;  // three 48 KB workgroups per CU
 
+constexpr int GIANT_MIN = TABLE_CAP;  // rows longer than this take a whole workgroup
+constexpr int GIANT_SLOTS = 4096;
+constexpr int GIANT_THREADS = 1024;
+constexpr int GIANT_BLOCKS = 512;  // two 65 KB workgroups per CU
+
 __global__ void hub_list_kernel(const int32_t* __restrict__ row_ptr, int32_t V, int32_t* __restrict__ hubs,
-                                int32_t* __restrict__ hub_count) {
+                                int32_t* __restrict__ hub_count, int32_t* __restrict__ giants,
+                                int32_t* __restrict__ giant_count) {
   const int32_t v = blockIdx.x * blockDim.x + threadIdx.x;
-  if (v < V && row_ptr[v + 1] - row_ptr[v] > SMALL_CAP / 2) hubs[atomicAdd(hub_count, 1)] = v;
+  const int32_t d = v < V ? row_ptr[v + 1] - row_ptr[v] : 0;
+  const bool giant = d > GIANT_MIN, hub = !giant && d > SMALL_CAP / 2;
+  const uint64_t mg = __ballot(giant), mh = __ballot(hub);  // one atomic per wave and list
+  const uint64_t below = (((uint64_t)1) << lane()) - 1;
+  int32_t bg = 0, bh = 0;
+  if (lane() == 0) {
+    if (mg) bg = atomicAdd(giant_count, __popcll(mg));
+    if (mh) bh = atomicAdd(hub_count, __popcll(mh));
+  }
+  bg = __shfl(bg, 0);
+  bh = __shfl(bh, 0);
+  if (giant) giants[bg + __popcll(mg & below)] = v;
+  if (hub) hubs[bh + __popcll(mh & below)] = v;
+}
+
+// Rows longer than GIANT_MIN: one 1024-thread workgroup per vertex.  All
+// threads insert the row's neighbour communities into a GIANT_SLOTS-slot LDS
+// table (sum of weights in f64, first row position by atomic min); when more
+// than TABLE_CAP communities appear, a binary search on the first positions
+// keeps exactly the TABLE_CAP that appear first along the row (the rule of
+// the per-wave tables).  The row is walked in position order, GIANT_THREADS
+// entries at a time, and no community is inserted once TABLE_CAP are held, so
+// the table never holds more than 2 x TABLE_CAP - 1.  The candidates are
+// scored across the workgroup.
+struct GiantShared {
+  int32_t c[GIANT_SLOTS];
+  double s[GIANT_SLOTS];
+  int32_t first[GIANT_SLOTS];
+  uint64_t best[GIANT_THREADS / 64];
+  int32_t best_c[GIANT_THREADS / 64];
+  double red[GIANT_THREADS / 64];
+  int32_t n, overflow, count, k_old_slot;
+};
+
+__device__ inline double block_sum_giant(double x, GiantShared& sh) {
+  x = wave_sum_f64(x);
+  if (lane() == 0) sh.red[threadIdx.x >> 6] = x;
+  __syncthreads();
+  double t = 0.0;
+  for (int i = 0; i < GIANT_THREADS / 64; ++i) t += sh.red[i];
+  __syncthreads();
+  return t;
+}
+
+// Returns false when the table overflowed (caller falls back); on success
+// *thr bounds the kept first positions and *e_sum is the admitted weight.
+template <bool REFINE>
+__device__ bool giant_table(const Graph& gr, const int32_t* __restrict__ parent, const int32_t* __restrict__ lin,
+                            int32_t v, int32_t pv, int32_t a, int32_t b, GiantShared& sh, int32_t* thr,
+                            double* e_sum) {
+  const int tid = threadIdx.x;
+  for (int j = tid; j < GIANT_SLOTS; j += GIANT_THREADS) {
+    sh.c[j] = -1;
+    sh.s[j] = 0.0;
+    sh.first[j] = 0x7FFFFFFF;
+  }
+  if (tid == 0) {
+    sh.n = 0;
+    sh.overflow = 0;
+  }
+  __syncthreads();
+  double e_acc = 0.0;
+  bool capped = false;  // TABLE_CAP communities held: later ones cannot be among the first TABLE_CAP
+  for (int32_t e0 = a; e0 < b; e0 += GIANT_THREADS) {
+    const int32_t e = e0 + tid;
+    if (e < b) {
+      const int32_t u = gr.col[e];
+      const bool ok = u != v && (!REFINE || parent[u] == pv);
+      if (ok) {
+        const float w = gr.wt[e];
+        const int32_t c = lin[u];
+        e_acc += (double)w;
+        uint32_t h = pcg_hash((uint32_t)c) & (GIANT_SLOTS - 1);
+        int probes = 0;
+        bool placed = false;
+        while (probes++ < GIANT_SLOTS) {
+          const int32_t cur = __hip_atomic_load(sh.c + h, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+          if (cur == c) {
+            placed = true;
+            break;
+          }
+          if (cur == -1) {
+            if (capped) break;  // not held: appears after the first TABLE_CAP communities
+            const int32_t prev = atomicCAS(sh.c + h, -1, c);
+            if (prev == -1) atomicAdd(&sh.n, 1);
+            if (prev == -1 || prev == c) {
+              placed = true;
+              break;
+            }
+          }
+          h = (h + 1) & (GIANT_SLOTS - 1);
+        }
+        if (placed) {
+          unsafeAtomicAdd(sh.s + h, (double)w);
+          atomicMin(sh.first + h, e);
+        } else if (!capped) {
+          sh.overflow = 1;  // unreachable: at most 2 x TABLE_CAP - 1 entries are ever inserted
+        }
+      }
+    }
+    __syncthreads();
+    capped = sh.n >= TABLE_CAP;
+    __syncthreads();
+  }
+  __syncthreads();
+  *e_sum = block_sum_giant(e_acc, sh);
+  if (sh.overflow) return false;
+  int32_t t = 0x7FFFFFFF;
+  if (sh.n > TABLE_CAP) {  // smallest t with TABLE_CAP first positions below it
+    int32_t lo = a, hi = b;
+    while (lo < hi) {
+      const int32_t mid = lo + (hi - lo) / 2;
+      if (tid == 0) sh.count = 0;
+      __syncthreads();
+      int cnt = 0;
+      for (int j = tid; j < GIANT_SLOTS; j += GIANT_THREADS) cnt += sh.first[j] < mid + 1;
+      if (cnt) atomicAdd(&sh.count, cnt);
+      __syncthreads();
+      if (sh.count >= TABLE_CAP) hi = mid;
+      else lo = mid + 1;
+      __syncthreads();
+    }
+    t = lo + 1;
+  }
+  *thr = t;
+  return true;
+}
+
+// Block-wide max of packed candidates; every thread gets the winner.
+__device__ inline int32_t giant_pick(uint64_t mine, int32_t mine_c, uint64_t stay, int32_t old, GiantShared& sh) {
+  const uint64_t wbest = wave_max_u64(mine);
+  const int32_t wc = __shfl(mine_c, first_lane(__ballot(mine == wbest)));
+  if (lane() == 0) {
+    sh.best[threadIdx.x >> 6] = wbest;
+    sh.best_c[threadIdx.x >> 6] = wc;
+  }
+  __syncthreads();
+  uint64_t best = 0;
+  int32_t c = old;
+  for (int i = 0; i < GIANT_THREADS / 64; ++i)
+    if (sh.best[i] > best) {
+      best = sh.best[i];
+      c = sh.best_c[i];
+    }
+  __syncthreads();
+  return best > stay ? c : old;
+}
+
+__device__ float giant_k_old(GiantShared& sh, int32_t old, int32_t thr) {
+  if (threadIdx.x == 0) sh.k_old_slot = -1;
+  __syncthreads();
+  for (int j = threadIdx.x; j < GIANT_SLOTS; j += GIANT_THREADS)
+    if (sh.c[j] == old && sh.first[j] < thr) sh.k_old_slot = j;
+  __syncthreads();
+  const int32_t slot = sh.k_old_slot;
+  return slot >= 0 ? (float)sh.s[slot] : 0.0f;
 }
 
 template <bool HUB>
@@ -520,6 +686,135 @@ __global__ __launch_bounds__(HUB ? LTHREADS : 64 * SWAVES) void refine_propose_k
     if (v >= gr.V || gr.row_ptr[v + 1] - gr.row_ptr[v] > CAP / 2) return;
     refine_propose_vertex<CAP>(gr, parent, sigma, parent_sigma, lin, prop, rank, resolution, inv_theta, boltzmann,
                                level, sweep, seed, v, tab_c[wv], tab_s[wv]);
+  }
+}
+
+__global__ __launch_bounds__(GIANT_THREADS) void local_moving_giant_kernel(
+    Graph gr, const double* __restrict__ sigma, const int32_t* __restrict__ lin, int32_t* __restrict__ lout,
+    int32_t* __restrict__ ctl, const int32_t* __restrict__ giants, const int32_t* __restrict__ giant_count,
+    float resolution, uint32_t level, uint32_t sweep, uint32_t seed) {
+  __shared__ GiantShared sh;
+  const int32_t count = *giant_count;
+  const bool done = ctl[CTL_DONE] != 0;
+  const int up_down = ctl[CTL_UPDOWN];
+  for (int32_t i = blockIdx.x; i < count; i += gridDim.x) {
+    const int32_t v = giants[i];
+    const int32_t old = lin[v];
+    const int32_t g = v / gr.S;
+    const double tm = gr.two_m[g];
+    if (done || !(tm > 0.0)) {
+      if (threadIdx.x == 0) lout[v] = old;
+      continue;
+    }
+    const int32_t a = gr.row_ptr[v], b = gr.row_ptr[v + 1];
+    int32_t thr;
+    double e_sum;
+    if (!giant_table<false>(gr, nullptr, lin, v, 0, a, b, sh, &thr, &e_sum)) {
+      __syncthreads();
+      if (threadIdx.x < 64)
+        local_moving_vertex<TABLE_CAP>(gr, sigma, lin, lout, ctl, resolution, level, sweep, seed, v, sh.c, sh.s);
+      __syncthreads();
+      continue;
+    }
+    const float k_old = giant_k_old(sh, old, thr);
+    const double kv = gr.k_v[v];
+    const double m_g = 0.5 * tm;
+    const double inv_m = 1.0 / m_g;
+    const double inv_2m2 = 1.0 / (2.0 * m_g * m_g);
+    const double sig_old_excl = sigma[old] - kv;
+    const float jitter = (rand_uniform((uint32_t)g, (uint32_t)v, level, sweep, seed) - 0.5f) * 1e-9f;
+    uint64_t mine = 0;
+    int32_t mine_c = old;
+    for (int j = threadIdx.x; j < GIANT_SLOTS; j += GIANT_THREADS) {
+      const int32_t c = sh.c[j];
+      if (c < 0 || sh.first[j] >= thr || c == old || (c > old ? 1 : 0) != up_down) continue;
+      const float kn = (float)sh.s[j];
+      const double dq = ((double)kn - (double)k_old) * inv_m
+                        + (double)resolution * kv * (sig_old_excl - sigma[c]) * inv_2m2;
+      const float dqf = (float)dq + jitter;
+      const uint64_t p = pack(dqf, cand_pref(c));
+      if (p > mine) {
+        mine = p;
+        mine_c = c;
+      }
+    }
+    const int32_t choice = giant_pick(mine, mine_c, pack(0.0f, STAY_PREF), old, sh);
+    if (threadIdx.x == 0) {
+      lout[v] = choice;
+      if (choice != old) mark_moved(ctl);
+    }
+  }
+}
+
+__global__ __launch_bounds__(GIANT_THREADS) void refine_propose_giant_kernel(
+    Graph gr, const int32_t* __restrict__ parent, const double* __restrict__ sigma,
+    const double* __restrict__ parent_sigma, const int32_t* __restrict__ lin, int32_t* __restrict__ prop,
+    uint32_t* __restrict__ rank, const int32_t* __restrict__ ctl, const int32_t* __restrict__ giants,
+    const int32_t* __restrict__ giant_count, float resolution, float inv_theta, int boltzmann, uint32_t level,
+    uint32_t sweep, uint32_t seed) {
+  __shared__ GiantShared sh;
+  if (ctl[CTL_DONE]) return;
+  const int32_t count = *giant_count;
+  for (int32_t i = blockIdx.x; i < count; i += gridDim.x) {
+    const int32_t v = giants[i];
+    const int32_t g = v / gr.S;
+    if (threadIdx.x == 0) rank[v] = mix4((uint32_t)g, (uint32_t)v, (level << 16) | sweep, seed);
+    const int32_t old = lin[v];
+    const double tm = gr.two_m[g];
+    if (!(tm > 0.0)) {
+      if (threadIdx.x == 0) prop[v] = old;
+      continue;
+    }
+    const int32_t a = gr.row_ptr[v], b = gr.row_ptr[v + 1];
+    const int32_t pv = parent[v];
+    int32_t thr;
+    double e_sum;
+    if (!giant_table<true>(gr, parent, lin, v, pv, a, b, sh, &thr, &e_sum)) {
+      __syncthreads();
+      if (threadIdx.x < 64)
+        refine_propose_vertex<TABLE_CAP>(gr, parent, sigma, parent_sigma, lin, prop, rank, resolution, inv_theta,
+                                         boltzmann, level, sweep, seed, v, sh.c, sh.s);
+      __syncthreads();
+      continue;
+    }
+    const double kv = gr.k_v[v];
+    double vol_minus = parent_sigma[pv] - kv;
+    if (vol_minus < 0.0) vol_minus = 0.0;
+    const double bound = (double)resolution * kv * vol_minus / tm;
+    if ((double)(float)e_sum < bound) {  // {v} is not well connected to its parent community
+      if (threadIdx.x == 0) prop[v] = old;
+      __syncthreads();
+      continue;
+    }
+    const float k_old = giant_k_old(sh, old, thr);
+    const double m_g = 0.5 * tm;
+    const double inv_m = 1.0 / m_g;
+    const double inv_2m2 = 1.0 / (2.0 * m_g * m_g);
+    const double sig_old_excl = sigma[old] - kv;
+    uint64_t mine = 0;
+    int32_t mine_c = old;
+    for (int j = threadIdx.x; j < GIANT_SLOTS; j += GIANT_THREADS) {
+      const int32_t c = sh.c[j];
+      if (c < 0 || sh.first[j] >= thr || c == old) continue;
+      const float kn = (float)sh.s[j];
+      const double dq = ((double)kn - (double)k_old) * inv_m
+                        + (double)resolution * kv * (sig_old_excl - sigma[c]) * inv_2m2;
+      if (dq < 0.0) continue;
+      const float score = boltzmann
+          ? (float)(dq * (double)inv_theta)
+                + gumbel(rand_uniform_pair((uint32_t)g, (uint32_t)v, (uint32_t)c, level, sweep, seed))
+          : (float)dq;
+      const uint64_t p = pack(score, cand_pref(c));
+      if (p > mine) {
+        mine = p;
+        mine_c = c;
+      }
+    }
+    const float stay = boltzmann
+        ? gumbel(rand_uniform_pair((uint32_t)g, (uint32_t)v, (uint32_t)old, level, sweep, seed))
+        : 0.0f;
+    const int32_t choice = giant_pick(mine, mine_c, pack(stay, STAY_PREF), old, sh);
+    if (threadIdx.x == 0) prop[v] = choice;
   }
 }
 
@@ -749,7 +1044,7 @@ int launch_check() {
 
 struct LeidenLayout {
   size_t keys_a, keys_b, vals_a, vals_b, temp, temp_bytes, row_ptr, col, k_v, two_m, sigma, psigma, lab_a, lab_b,
-      parent, prop, rank, ctl, hubs, hub_count, total;
+      parent, prop, rank, ctl, hubs, hub_count, giants, giant_count, total;
 };
 
 LeidenLayout leiden_layout(int64_t E, int32_t G, int32_t S) {
@@ -786,6 +1081,8 @@ LeidenLayout leiden_layout(int64_t E, int32_t G, int32_t S) {
   L.ctl = take(CTL_WORDS * 4);
   L.hubs = take(V * 4);
   L.hub_count = take(4);
+  L.giants = take(V * 4);
+  L.giant_count = take(4);
   L.total = off;
   return L;
 }
@@ -950,6 +1247,8 @@ extern "C" int ckv_batched_leiden(const int32_t* edge_src, const int32_t* edge_d
   int32_t* ctl = (int32_t*)(ws + L.ctl);
   int32_t* hubs = (int32_t*)(ws + L.hubs);
   int32_t* hub_count = (int32_t*)(ws + L.hub_count);
+  int32_t* giants = (int32_t*)(ws + L.giants);
+  int32_t* giant_count = (int32_t*)(ws + L.giant_count);
 
   const int bits = bits_for((uint64_t)V - 1);
   const int end_bit = bits + bits_for((uint64_t)V);
@@ -962,8 +1261,8 @@ extern "C" int ckv_batched_leiden(const int32_t* edge_src, const int32_t* edge_d
     return ckv_internal::set_error(CKV_E_LAUNCH, "Leiden CSR sort failed");
   row_ptr_kernel<<<blocks(V + 1, ETHREADS), ETHREADS, 0, st>>>(keys_b, n, V, bits, row_ptr);
   col_kernel<<<blocks(n, ETHREADS), ETHREADS, 0, st>>>(keys_b, n, bits, col);
-  zero_kernel<<<1, 256, 0, st>>>(two_m, graphs, modularity, ctl, hub_count);
-  hub_list_kernel<<<blocks(V, ETHREADS), ETHREADS, 0, st>>>(row_ptr, V, hubs, hub_count);
+  zero_kernel<<<1, 256, 0, st>>>(two_m, graphs, modularity, ctl, hub_count, giant_count);
+  hub_list_kernel<<<blocks(V, ETHREADS), ETHREADS, 0, st>>>(row_ptr, V, hubs, hub_count, giants, giant_count);
   const unsigned vgrid = blocks(V, LWAVES);
   degree_kernel<<<vgrid, LTHREADS, 0, st>>>(row_ptr, vals_b, V, seq_len, k_v);
   graph_sum_kernel<<<graphs, 256, 0, st>>>(k_v, seq_len, two_m);
@@ -980,6 +1279,9 @@ extern "C" int ckv_batched_leiden(const int32_t* edge_src, const int32_t* edge_d
     local_moving_kernel<true><<<HUB_BLOCKS, LTHREADS, 0, st>>>(gr, sigma, lab[cur], lab[cur ^ 1], ctl, hubs,
                                                               hub_count, resolution, 0u, (uint32_t)sweep,
                                                               (uint32_t)seed);
+    local_moving_giant_kernel<<<GIANT_BLOCKS, GIANT_THREADS, 0, st>>>(gr, sigma, lab[cur], lab[cur ^ 1], ctl, giants,
+                                                                     giant_count, resolution, 0u, (uint32_t)sweep,
+                                                                     (uint32_t)seed);
     lm_control_kernel<<<1, 64, 0, st>>>(ctl);
     cur ^= 1;
   }
@@ -998,6 +1300,9 @@ extern "C" int ckv_batched_leiden(const int32_t* edge_src, const int32_t* edge_d
         use_boltzmann ? 1 : 0, 1u, (uint32_t)sweep, (uint32_t)seed);
     refine_propose_kernel<true><<<HUB_BLOCKS, LTHREADS, 0, st>>>(
         gr, parent, sigma, psigma, lab[cur], prop, rank, ctl, hubs, hub_count, resolution, inv_theta,
+        use_boltzmann ? 1 : 0, 1u, (uint32_t)sweep, (uint32_t)seed);
+    refine_propose_giant_kernel<<<GIANT_BLOCKS, GIANT_THREADS, 0, st>>>(
+        gr, parent, sigma, psigma, lab[cur], prop, rank, ctl, giants, giant_count, resolution, inv_theta,
         use_boltzmann ? 1 : 0, 1u, (uint32_t)sweep, (uint32_t)seed);
     refine_commit_kernel<<<vgrid, LTHREADS, 0, st>>>(gr, parent, lab[cur], prop, rank, lab[cur ^ 1], ctl);
     refine_control_kernel<<<1, 64, 0, st>>>(ctl);

@@ -1,9 +1,14 @@
 """Prefill partition hand-off (reference: community_kv/graph/runtime.py:29-176).
 
-The reference runs Leiden on worker threads, one job per layer.  Here a job
-runs ``build_partitioned_layer`` (top-k graph, native batched Leiden, state
-build) synchronously on the submitting stream after the completion event, so
-no extra threads or streams are created.  A *label provider*, a callable
+The reference runs Leiden on worker threads, one job per layer, each job on
+its own stream after the layer's completion event.  Here a job runs
+``build_partitioned_layer`` (top-k graph, native batched Leiden, state build)
+the same way on the model's GPU: one worker thread per GPU
+(``PartitionConfig.workers_per_device`` caps it), a stream of default priority
+per job that waits on the completion event, the stream synchronised before the
+result is handed over, so the partition of layer i overlaps the prefill of
+layers i+1, ...; with ``PartitionConfig(overlap=False)`` jobs run inline on the
+submitting stream.  A *label provider*, a callable
 ``provider(layer_idx, keys, topk_indices, topk_scores) -> community_ids
 [graphs, S]``, may replace Leiden; its labels are turned into decode state by
 ``build_layer_from_labels`` with the modularity state of the top-k edges.
@@ -11,6 +16,8 @@ no extra threads or streams are created.  A *label provider*, a callable
 
 from __future__ import annotations
 
+import dataclasses
+from concurrent.futures import Future, ThreadPoolExecutor
 from typing import Any, Callable
 
 import torch
@@ -31,16 +38,49 @@ class PartitionRuntime:
         self.max_layers = max_layers
         self.label_provider = label_provider
         self._results: dict[int, PartitionedLayer] = {}
+        self._futures: dict[int, Future] = {}
+        self._executor: ThreadPoolExecutor | None = None
 
     def reset(self) -> None:
+        for future in self._futures.values():
+            future.result()
+        self._futures.clear()
         self._results.clear()
+
+    def _pool(self) -> ThreadPoolExecutor:
+        if self._executor is None:
+            self._executor = ThreadPoolExecutor(max_workers=1, thread_name_prefix="ckv-partition")
+        return self._executor
+
+    def _run_job(self, *, layer_idx: int, topk_indices: torch.Tensor, topk_scores: torch.Tensor,
+                 keys: torch.Tensor, completion_event: Any, resolution: float,
+                 max_decode_tokens: int) -> PartitionedLayer:
+        cfg = self.algorithm
+        with torch.cuda.device(keys.device):
+            stream = torch.cuda.Stream(device=keys.device)
+            if completion_event is not None:
+                stream.wait_event(completion_event)
+            with torch.cuda.stream(stream):
+                layer = build_partitioned_layer(
+                    layer_idx=layer_idx, topk_indices=topk_indices, topk_scores=topk_scores, keys=keys,
+                    num_sink=cfg.num_sink, lam=cfg.lam, leiden_resolution=resolution, leiden_seed=cfg.leiden_seed,
+                    max_decode_tokens=max_decode_tokens, aggregation=GraphAggregation(cfg.aggregation))
+            stream.synchronize()
+        return layer
 
     def submit(self, *, layer_idx: int, topk_indices: torch.Tensor, topk_scores: torch.Tensor, keys: torch.Tensor,
                completion_event: Any, resolution: float, max_decode_tokens: int) -> None:
-        if layer_idx in self._results:
+        if layer_idx in self._results or layer_idx in self._futures:
             raise ValueError(f"layer {layer_idx} was already submitted")
         if not 0 <= layer_idx < self.max_layers:
             raise ValueError("layer index out of range")
+        if any(torch.device(d) != keys.device for d in self.scheduling.devices):
+            raise NotImplementedError("partition offload to another GPU is not part of this build")
+        if self.label_provider is None and self.scheduling.overlap and keys.device.type == "cuda":
+            self._futures[layer_idx] = self._pool().submit(
+                self._run_job, layer_idx=layer_idx, topk_indices=topk_indices, topk_scores=topk_scores, keys=keys,
+                completion_event=completion_event, resolution=resolution, max_decode_tokens=max_decode_tokens)
+            return
         if completion_event is not None and hasattr(completion_event, "synchronize"):
             completion_event.synchronize()
         cfg = self.algorithm
@@ -76,12 +116,28 @@ class PartitionRuntime:
             edges=edges, topk_edges=topk_edges)
 
     def wait(self, callback: Callable[[PartitionedLayer], Any]) -> None:
+        for idx, future in sorted(self._futures.items()):
+            layer = future.result()
+            # made on the job's stream, used from now on by the current one
+            consumer = torch.cuda.current_stream(layer.centroids.device)
+            for value in vars_of(layer):
+                if isinstance(value, torch.Tensor) and value.is_cuda:
+                    value.record_stream(consumer)
+            self._results[idx] = layer
+        self._futures.clear()
         for idx in sorted(self._results):
             callback(self._results[idx])
         self._results.clear()
 
     def shutdown(self) -> None:
-        self._results.clear()
+        self.reset()
+        if self._executor is not None:
+            self._executor.shutdown(wait=True)
+            self._executor = None
+
+
+def vars_of(layer: PartitionedLayer) -> list[Any]:
+    return [getattr(layer, f.name) for f in dataclasses.fields(layer)]
 
 
 __all__ = ["PartitionRuntime"]

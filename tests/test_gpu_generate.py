@@ -41,11 +41,13 @@ def _labels(layer_idx, keys, topk_indices, topk_scores):
     return lab
 
 
-@pytest.mark.parametrize("assignment,graph,leiden", [("delta_q", True, False), ("nearest_centroid", True, False),
-                                                     ("delta_q", False, False), ("delta_q", True, True)])
+@pytest.mark.parametrize("assignment,graph,leiden", [("delta_q", True, ""), ("nearest_centroid", True, ""),
+                                                     ("delta_q", False, ""), ("delta_q", True, "overlap"),
+                                                     ("nearest_centroid", True, "inline")])
 def test_generate_full_selection_matches_dense(device, assignment, graph, leiden):
     """``leiden``: no label provider, every prefill layer is partitioned by the
-    native Leiden on its top-k edges (build_partitioned_layer)."""
+    native Leiden on its top-k edges (build_partitioned_layer), on a worker
+    thread and stream overlapping the next layers ("overlap") or inline."""
     from community_kv_amd import CommunityKVAttention, CommunityKVConfig, CommunityKVRuntime, GraphAggregation
     from community_kv_amd.config import PartitionConfig
 
@@ -56,8 +58,8 @@ def test_generate_full_selection_matches_dense(device, assignment, graph, leiden
     cfg = CommunityKVConfig(token_budget=4096, num_sink=10, aggregation=GraphAggregation.QUERY_GROUP,
                             selection="topk", topk_communities=8192 if leiden else COMMUNITIES,
                             max_selected=4096, assignment=assignment)
-    with CommunityKVRuntime(config=cfg, partition=PartitionConfig(), num_layers=LAYERS, max_decode_tokens=new,
-                            label_provider=None if leiden else _labels) as runtime:
+    with CommunityKVRuntime(config=cfg, partition=PartitionConfig(overlap=leiden != "inline"), num_layers=LAYERS,
+                            max_decode_tokens=new, label_provider=None if leiden else _labels) as runtime:
         CommunityKVAttention(runtime).register()
         model.set_attn_implementation("community_kv")
         with torch.inference_mode():

@@ -52,10 +52,12 @@ def test_batched_leiden_level_matches_oracle(device, seed, G, S, k, gkw, lkw):
     np.testing.assert_allclose(q, q_ref, rtol=1e-9, atol=1e-12)
 
 
-@pytest.mark.parametrize("leaves", [1500, 300, 100])
+@pytest.mark.parametrize("leaves", [3000, 1500, 1100, 300, 100])
 def test_hub_vertex_over_table_capacity(device, leaves):
-    """Degree 1500 (leader-loop table, capacity reached at the first sweep),
-    300 (hub kernel, hashed table) and 100 (small-row kernel)."""
+    """Degree 3000 (workgroup table overflows at the first sweep: single-wave
+    leader loop), 1500 and 1100 (workgroup table, the first 1024 communities
+    along the row kept), 300 (hub kernel, hashed table) and 100 (small-row
+    kernel)."""
     src, dst, w, S = lg.hub(4, leaves, 40)
     print(f"leiden hub S={S} edges={src.size}", flush=True)
     got, _ = _native_level(device, src, dst, w, 1, S)
