@@ -3,8 +3,8 @@
 The reference runs Leiden on worker threads, one job per layer, each job on
 its own stream after the layer's completion event.  Here a job runs
 ``build_partitioned_layer`` (top-k graph, native batched Leiden, state build)
-the same way on the model's GPU: one worker thread per GPU
-(``PartitionConfig.workers_per_device`` caps it), a stream of default priority
+the same way on the model's GPU: ``PartitionConfig.workers_per_device`` worker
+threads (jobs of different layers run concurrently), a stream of default priority
 per job that waits on the completion event, the stream synchronised before the
 result is handed over, so the partition of layer i overlaps the prefill of
 layers i+1, ...; with ``PartitionConfig(overlap=False)`` jobs run inline on the
@@ -49,7 +49,8 @@ class PartitionRuntime:
 
     def _pool(self) -> ThreadPoolExecutor:
         if self._executor is None:
-            self._executor = ThreadPoolExecutor(max_workers=1, thread_name_prefix="ckv-partition")
+            workers = max(1, min(self.max_layers, self.scheduling.workers_per_device))
+            self._executor = ThreadPoolExecutor(max_workers=workers, thread_name_prefix="ckv-partition")
         return self._executor
 
     def _run_job(self, *, layer_idx: int, topk_indices: torch.Tensor, topk_scores: torch.Tensor,
