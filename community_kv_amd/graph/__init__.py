@@ -7,6 +7,7 @@ from community_kv_amd.graph.partition import (
     build_adjacency,
     build_layer_from_labels,
     build_member_csr,
+    build_partitioned_layer,
     compute_centroids,
     init_modularity_state,
     leiden_max_iterations,
@@ -27,6 +28,7 @@ __all__ = [
     "build_adjacency",
     "build_layer_from_labels",
     "build_member_csr",
+    "build_partitioned_layer",
     "compute_centroids",
     "init_modularity_state",
     "leiden_max_iterations",
