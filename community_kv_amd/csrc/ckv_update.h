@@ -39,7 +39,7 @@ __device__ void owner_update(const DecodeArgs& a, const int rh, const float s_ls
   __shared__ int s_assigned, s_slot, s_comm_ov;
 
   // Cursor state and the allocator's free lists, loaded now (in flight with
-  // round 1) and published after it.
+  // stage 1) and published after it.
   int cur_r = 0, active_r = 0, nearest_r = -1, free_chunk_r = 0, free_pos_r = 0;
   float total_r = 0.0f;
   if (tid == 64) {
@@ -53,7 +53,7 @@ __device__ void owner_update(const DecodeArgs& a, const int rh, const float s_ls
     free_pos_r = a.dl.next_free_position[graph];
   }
 
-  // ---- round 1: exact top-8 over every attended non-sink slot (score desc,
+  // ---- stage 1: exact top-8 over every attended non-sink slot (score desc,
   // position asc, as one packed 64-bit key each).  Each thread keeps a sorted
   // top-8 of its strided share (loaded 8 at a time, one round per chunk;
   // sorted by a 19-comparator network, merged into the running list).  The
@@ -157,7 +157,7 @@ __device__ void owner_update(const DecodeArgs& a, const int rh, const float s_ls
   const int active = s_active;
   const bool valid_pos = cur >= 0 && cur < tc_cap;
 
-  // ---- round 2: candidate communities; the current key row ----------------
+  // ---- stage 2: candidate communities; the current key row ----------------
   if (tid < NS) {
     int pos = -1, comm = -1;
     if (tid < KAPPA) {
@@ -182,7 +182,7 @@ __device__ void owner_update(const DecodeArgs& a, const int rh, const float s_ls
   __syncthreads();
   CKV_STAMP(rh == 0, 28);
 
-  // ---- round 3: per-candidate state and centroid rows ----------------------
+  // ---- stage 3: per-candidate state and centroid rows ----------------------
   if (tid < NS) {
     const int comm = s_comm[tid];
     const bool ok = comm >= 0 && comm < C;
@@ -200,7 +200,7 @@ __device__ void owner_update(const DecodeArgs& a, const int rh, const float s_ls
   CKV_STAMP(rh == 0, 29);
 
   // Tail-chunk fields of every candidate's community, loaded now (in flight
-  // during the assignment) for round 4, which needs only the assigned one's.
+  // during the assignment) for stage 4, which needs only the assigned one's.
   const int64_t cb = (int64_t)graph * a.dl.chunks_per_graph;
   int t_cs = 0, t_cc = 0, t_st = 0;
   if (tid < NS && a.dl.chunks_per_graph > 0) {
@@ -309,7 +309,7 @@ __device__ void owner_update(const DecodeArgs& a, const int rh, const float s_ls
       store_centroid1<CT>(a.st.centroids, ((int64_t)rh * C + asg) * D + d, upd);
     }
   }
-  // ---- round 4: decode-delta append (the assigned community's tail-chunk
+  // ---- stage 4: decode-delta append (the assigned community's tail-chunk
   // fields were prefetched by lane `slot` of wave 0) -------------------------
   int slot_cs = 0, slot_cc = 0, slot_st = 0;
   if (tid < 64) {
