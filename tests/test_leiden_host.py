@@ -88,3 +88,29 @@ def test_partition_helpers_match_oracle():
     g_idx, _, pos = P._reshape_by_aggregation(idx, idx.float(), aggregation="query_group", num_kv_heads=2,
                                               num_sink=1)
     assert g_idx.shape == (2, 6, 2) and pos[0].tolist() == [2, 3, 4, 2, 3, 4]
+
+
+def test_partition_runtime_guards():
+    """PartitionRuntime (graph/runtime.py:29-176): one job per layer, layer
+    range, and offload to another GPU is refused (not part of this build)."""
+    from community_kv_amd.config import CommunityKVConfig, PartitionConfig
+    from community_kv_amd.graph.runtime import PartitionRuntime
+
+    labels = lambda layer, keys, idx, sc: torch.zeros(1, keys.shape[1], dtype=torch.int32)
+    keys = torch.zeros(1, 40, 128)
+    idx = torch.zeros(1, 31, 8, dtype=torch.int32)
+    sc = torch.ones(1, 31, 8)
+    kw = dict(topk_indices=idx, topk_scores=sc, keys=keys, completion_event=None, resolution=1.0,
+              max_decode_tokens=2)
+    rt = PartitionRuntime(algorithm=CommunityKVConfig(num_sink=2, token_budget=64), scheduling=PartitionConfig(),
+                          max_layers=2, label_provider=labels)
+    with pytest.raises(ValueError, match="out of range"):
+        rt.submit(layer_idx=2, **kw)
+    off = PartitionRuntime(algorithm=CommunityKVConfig(), scheduling=PartitionConfig(devices=("cuda:1",)),
+                           max_layers=1)
+    with pytest.raises(NotImplementedError, match="another GPU"):
+        off.submit(layer_idx=0, **kw)
+    with pytest.raises(ValueError):
+        PartitionRuntime(algorithm=CommunityKVConfig(), scheduling=PartitionConfig(), max_layers=0)
+    rt.shutdown()
+    off.shutdown()
