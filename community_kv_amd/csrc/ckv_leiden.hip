@@ -984,16 +984,33 @@ __global__ __launch_bounds__(256) void mod_edge_kernel(const int32_t* __restrict
                                                        double* __restrict__ k, double* __restrict__ acc) {
   __shared__ double part[4];
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  double in = 0.0;
+  double in = 0.0, xs = 0.0;
+  int32_t a = -1;
   if (i < E) {
-    const int32_t a = src[i], b = dst[i];
-    if (a >= 0 && a < V && b >= 0 && b < V) {
+    const int32_t s0 = src[i], b = dst[i];
+    if (s0 >= 0 && s0 < V && b >= 0 && b < V) {
       const double x = (double)w[i];
-      unsafeAtomicAdd(k + a, x);
+      a = s0;
+      xs = x;
       unsafeAtomicAdd(k + b, x);
-      if (labels[a] == labels[b]) in = x;
+      if (labels[s0] == labels[b]) in = x;
     }
   }
+  // Source ends: sum runs of equal source within the wave (edge lists come
+  // sorted by source, so a hub's edges arrive together), one atomic per run.
+  const int ln = lane();
+  const int32_t prev_a = __shfl_up(a, 1);
+  const int32_t next_a = __shfl_down(a, 1);
+  bool h = ln == 0 || prev_a != a;  // a run starts here
+  for (int o = 1; o < 64; o <<= 1) {
+    const double y = __shfl_up(xs, o);
+    const bool hy = __shfl_up(h ? 1 : 0, o) != 0;
+    if (ln >= o) {
+      if (!h) xs += y;
+      h = h || hy;
+    }
+  }
+  if (a >= 0 && (ln == 63 || next_a != a)) unsafeAtomicAdd(k + a, xs);
   in = block_sum_f64(in, part);
   if (threadIdx.x == 0 && in != 0.0) unsafeAtomicAdd(acc, in);
 }
