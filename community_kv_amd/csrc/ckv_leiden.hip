@@ -359,12 +359,26 @@ __device__ void local_moving_vertex(const Graph& gr, const double* __restrict__ 
   const float jitter = (rand_uniform((uint32_t)g, (uint32_t)v, level, sweep, seed) - 0.5f) * 1e-9f;
   uint64_t mine = 0;
   int32_t mine_c = old;
-  for (int j = lane(); j < n; j += 64) {
-    const int32_t c = tc[j];
-    if (c < 0 || c == old || (c > old ? 1 : 0) != up_down) continue;
-    const float kn = (float)ts[j];
+  // every slot's community total is loaded before any is used, so a lane's
+  // gathers are in flight together
+  constexpr int PER = CAP / 64;
+  int32_t cs[PER];
+  double sg[PER];
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const int j = lane() + 64 * k;
+    const int32_t c = j < n ? tc[j] : -1;
+    cs[k] = (c < 0 || c == old || (c > old ? 1 : 0) != up_down) ? -1 : c;
+  }
+#pragma unroll
+  for (int k = 0; k < PER; ++k) sg[k] = cs[k] >= 0 ? sigma[cs[k]] : 0.0;
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const int32_t c = cs[k];
+    if (c < 0) continue;
+    const float kn = (float)ts[lane() + 64 * k];
     const double dq = ((double)kn - (double)k_old) * inv_m
-                      + (double)resolution * kv * (sig_old_excl - sigma[c]) * inv_2m2;
+                      + (double)resolution * kv * (sig_old_excl - sg[k]) * inv_2m2;
     const float dqf = (float)dq + jitter;
     const uint64_t p = pack(dqf, cand_pref(c));
     if (p > mine) {
@@ -440,12 +454,24 @@ __device__ void refine_propose_vertex(const Graph& gr, const int32_t* __restrict
   const double sig_old_excl = sigma[old] - kv;
   uint64_t mine = 0;
   int32_t mine_c = old;
-  for (int j = lane(); j < n; j += 64) {
-    const int32_t c = tc[j];
-    if (c < 0 || c == old) continue;
-    const float kn = (float)ts[j];
+  constexpr int PER = CAP / 64;  // community totals gathered together, as in local moving
+  int32_t cs[PER];
+  double sg[PER];
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const int j = lane() + 64 * k;
+    const int32_t c = j < n ? tc[j] : -1;
+    cs[k] = (c < 0 || c == old) ? -1 : c;
+  }
+#pragma unroll
+  for (int k = 0; k < PER; ++k) sg[k] = cs[k] >= 0 ? sigma[cs[k]] : 0.0;
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const int32_t c = cs[k];
+    if (c < 0) continue;
+    const float kn = (float)ts[lane() + 64 * k];
     const double dq = ((double)kn - (double)k_old) * inv_m
-                      + (double)resolution * kv * (sig_old_excl - sigma[c]) * inv_2m2;
+                      + (double)resolution * kv * (sig_old_excl - sg[k]) * inv_2m2;
     if (dq < 0.0) continue;
     const float score = boltzmann
         ? (float)(dq * (double)inv_theta)
@@ -506,7 +532,8 @@ __global__ void hub_list_kernel(const int32_t* __restrict__ row_ptr, int32_t V, 
 // the per-wave tables).  The row is walked in position order, GIANT_THREADS
 // entries at a time, and no community is inserted once TABLE_CAP are held, so
 // the table never holds more than 2 x TABLE_CAP - 1.  The candidates are
-// scored across the workgroup.
+// scored across the workgroup.  (giant_table reports an overflow only if the
+// table bound above were broken; the vertex then stays where it is.)
 struct GiantShared {
   int32_t c[GIANT_SLOTS];
   double s[GIANT_SLOTS];
@@ -709,10 +736,8 @@ __global__ __launch_bounds__(GIANT_THREADS) void local_moving_giant_kernel(
     const int32_t a = gr.row_ptr[v], b = gr.row_ptr[v + 1];
     int32_t thr;
     double e_sum;
-    if (!giant_table<false>(gr, nullptr, lin, v, 0, a, b, sh, &thr, &e_sum)) {
-      __syncthreads();
-      if (threadIdx.x < 64)
-        local_moving_vertex<TABLE_CAP>(gr, sigma, lin, lout, ctl, resolution, level, sweep, seed, v, sh.c, sh.s);
+    if (!giant_table<false>(gr, nullptr, lin, v, 0, a, b, sh, &thr, &e_sum)) {  // cannot happen: stay
+      if (threadIdx.x == 0) lout[v] = old;
       __syncthreads();
       continue;
     }
@@ -769,11 +794,8 @@ __global__ __launch_bounds__(GIANT_THREADS) void refine_propose_giant_kernel(
     const int32_t pv = parent[v];
     int32_t thr;
     double e_sum;
-    if (!giant_table<true>(gr, parent, lin, v, pv, a, b, sh, &thr, &e_sum)) {
-      __syncthreads();
-      if (threadIdx.x < 64)
-        refine_propose_vertex<TABLE_CAP>(gr, parent, sigma, parent_sigma, lin, prop, rank, resolution, inv_theta,
-                                         boltzmann, level, sweep, seed, v, sh.c, sh.s);
+    if (!giant_table<true>(gr, parent, lin, v, pv, a, b, sh, &thr, &e_sum)) {  // cannot happen: stay
+      if (threadIdx.x == 0) prop[v] = old;
       __syncthreads();
       continue;
     }
