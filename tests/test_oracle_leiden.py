@@ -151,3 +151,34 @@ def test_fill_and_dense_remap():
     filled = L.fill_isolated(m)
     assert filled.tolist() == [[5, 6, 5, 2, 7], [8, 9, 0, 0, 7]]
     assert L.dense_remap(filled).tolist() == [[1, 2, 1, 0, 3], [2, 3, 0, 0, 1]]
+
+
+def test_boltzmann_refinement_samples_softmax_of_gains():
+    """Gumbel-max (refinement.cu:195-245): over independent draws the chosen
+    target follows P(c) ∝ exp(dQ_c / theta) over the non-negative-gain
+    candidates and staying (dQ = 0)."""
+    # vertex 0 joined to triangle {1,2,3} (edges 1) by two edges of 1 and to
+    # triangle {4,5,6} (edges 0.5) by two edges of 0.8; a separate triangle
+    # {7,8,9}; one parent community; vertices 1..9 already grouped
+    src = np.array([0, 0, 1, 1, 2, 0, 0, 4, 4, 5, 7, 8, 7])
+    dst = np.array([1, 2, 2, 3, 3, 4, 5, 5, 6, 6, 8, 9, 9])
+    w = np.array([1, 1, 1, 1, 1, 0.8, 0.8, 0.5, 0.5, 0.5, 1, 1, 1], np.float32)
+    csr = L.build_csr(src, dst, w, 1, 10)
+    labels = np.array([0, 1, 1, 1, 4, 4, 4, 7, 7, 7], np.int32)
+    parent = np.zeros(10, np.int32)
+    sig = L.sigma_tot(csr, labels)
+    v, c, dq = L.move_gains(csr, labels, sig, 1.0)
+    gains = {int(cc): float(d) for vv, cc, d in zip(v, c, dq) if vv == 0}
+    assert gains[1] > 0 and gains[4] > 0 and set(gains) == {1, 4}
+    theta = 0.02
+    counts = {0: 0, 1: 0, 4: 0}
+    draws = 4000
+    for sweep in range(draws):
+        prop, _ = L.refine_propose(csr, parent, labels, sig, L.sigma_tot(csr, parent), resolution=1.0,
+                                   theta=theta, boltzmann=True, level=1, sweep=sweep % 65536, seed=sweep // 65536)
+        counts[int(prop[0])] += 1
+    logits = np.array([0.0, gains[1], gains[4]]) / theta
+    p = np.exp(logits - logits.max())
+    p /= p.sum()
+    freq = np.array([counts[0], counts[1], counts[4]]) / draws
+    np.testing.assert_allclose(freq, p, atol=0.03)
