@@ -31,7 +31,7 @@ HIP_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 CKV_BF16, CKV_F32, CKV_E4M3 = 0, 1, 2
 CKV_SELECT_BUDGET, CKV_SELECT_TOPK = 0, 1
@@ -125,7 +125,7 @@ class DecodeConfig(ctypes.Structure):
 class DecodeWorkspace(ctypes.Structure):
     _fields_ = [("scores", _p), ("communities", _p), ("cumulative_ends", _p),
                 ("descriptor_counts", _p), ("tile_descriptors", _p), ("selected_counts", _p),
-                ("slot_positions", _p), ("nearest_partial", _p), ("nearest", _p),
+                ("slot_positions", _p), ("exchange", _p), ("nearest", _p),
                 ("block_counters", _p), ("partial_max", _p), ("partial_sum", _p),
                 ("partial_acc", _p), ("slot_scores", _p), ("output", _p), ("lse", _p),
                 ("topk_scores", _p), ("topk_positions", _p), ("assigned", _p), ("overflow", _p),
@@ -162,15 +162,35 @@ class StateBuildArgs(ctypes.Structure):
 
 
 def build(verbose: bool = False) -> str:
-    """Compiles libckv_amd.so for gfx950 in-tree (always recompiles)."""
+    """Compiles libckv_amd.so for gfx950 in-tree (always recompiles): one
+    hipcc process per source file in parallel, then one link."""
+    import tempfile
+    from concurrent.futures import ThreadPoolExecutor
+
     sources = [s for s in SOURCES if os.path.exists(s)]
-    cmd = [HIPCC, *HIP_FLAGS, "-I", os.path.join(REPO_DIR, "include"), "-o", LIB_PATH + ".tmp", *sources]
-    proc = subprocess.run(cmd, capture_output=True, text=True)
-    if proc.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{proc.stderr[-4000:]}")
+    include = ["-I", os.path.join(REPO_DIR, "include")]
+    compile_flags = [f for f in HIP_FLAGS if f != "-shared"]
+    with tempfile.TemporaryDirectory(prefix="ckv_build_") as tmp:
+        objects = [os.path.join(tmp, os.path.basename(src) + ".o") for src in sources]
+        cmds = [[HIPCC, *compile_flags, *include, "-c", "-o", obj, src] for src, obj in zip(sources, objects)]
+
+        def run(cmd):
+            return subprocess.run(cmd, capture_output=True, text=True)
+
+        workers = max(1, min(len(cmds), os.cpu_count() or 1, 16))
+        with ThreadPoolExecutor(max_workers=workers) as pool:
+            procs = list(pool.map(run, cmds))
+        for cmd, proc in zip(cmds, procs):
+            if proc.returncode != 0:
+                raise RuntimeError(f"hipcc failed ({proc.returncode}) on {cmd[-1]}:\n{proc.stderr[-4000:]}")
+        link = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", LIB_PATH + ".tmp", *objects]
+        proc = run(link)
+        if proc.returncode != 0:
+            raise RuntimeError(f"hipcc link failed ({proc.returncode}):\n{proc.stderr[-4000:]}")
     os.replace(LIB_PATH + ".tmp", LIB_PATH)
     if verbose:
-        print(" ".join(cmd))
+        for cmd in cmds + [link]:
+            print(" ".join(cmd))
     lib.cache_clear()
     return LIB_PATH
 

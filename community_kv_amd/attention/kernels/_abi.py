@@ -71,7 +71,7 @@ def workspace_struct(selection, attention, update) -> nat.DecodeWorkspace:
     return nat.DecodeWorkspace(
         p(selection.scores), p(selection.communities), p(selection.cumulative_ends),
         p(selection.descriptor_counts), p(selection.tile_descriptors), p(selection.selected_counts),
-        p(selection.slot_positions), p(selection.nearest_partial), p(selection.nearest),
+        p(selection.slot_positions), p(selection.exchange), p(selection.nearest),
         p(selection.block_counters),
         p(attention.partial_max) if attention else None, p(attention.partial_sum) if attention else None,
         p(attention.partial_acc) if attention else None, p(attention.slot_scores) if attention else None,

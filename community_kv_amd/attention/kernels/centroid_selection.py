@@ -36,9 +36,9 @@ class CentroidSelectionWorkspace:
     tile_descriptors: torch.Tensor  # [R, token_budget / 64] int32
     selected_counts: torch.Tensor   # [R] int32
     slot_positions: torch.Tensor    # [R, slot capacity] int32
-    nearest_partial: torch.Tensor   # [R, score blocks] uint64
+    exchange: torch.Tensor          # [R, C + 512] uint64 (zeros): scores handed between a fused launch's workgroups
     nearest: torch.Tensor           # [R] int32
-    block_counters: torch.Tensor    # [2R] int32 arrival counters (zero; the kernels leave them zero)
+    block_counters: torch.Tensor    # [4R] int32 arrival counters and epochs (zeros; kernel-maintained)
     token_budget: int
     num_sink: int
     score_coverage: int
@@ -95,7 +95,6 @@ class CentroidSelectionWorkspace:
             raise ValueError(f"descriptor capacity above {nat.MAX_DESCRIPTORS} is not supported")
         slots = num_sink + selected + local_window + inc
         slots = -(-slots // ATTENTION_TILE) * ATTENTION_TILE
-        score_blocks = -(-coverage // SCORE_BLOCK_N)
 
         def i32(shape, value=0):
             return torch.full(shape, value, dtype=torch.int32, device=device)
@@ -109,9 +108,9 @@ class CentroidSelectionWorkspace:
             tile_descriptors=i32((kv_heads, token_budget // ATTENTION_TILE)),
             selected_counts=i32((kv_heads,)),
             slot_positions=i32((kv_heads, slots), -1),
-            nearest_partial=torch.zeros((kv_heads, score_blocks), dtype=torch.uint64, device=device),
+            exchange=torch.zeros((kv_heads, community_capacity + 512), dtype=torch.uint64, device=device),
             nearest=i32((kv_heads,), -1),
-            block_counters=i32((2 * kv_heads,)),
+            block_counters=i32((4 * kv_heads,)),
             token_budget=token_budget,
             num_sink=num_sink,
             score_coverage=coverage,
@@ -150,7 +149,7 @@ class CentroidSelectionWorkspace:
 
     @property
     def score_blocks(self) -> int:
-        return self.nearest_partial.shape[1]
+        return -(-self.score_coverage // SCORE_BLOCK_N)
 
     def packed_segments(self) -> PackedSegments:
         return PackedSegments(

@@ -177,8 +177,12 @@ extern "C" int ckv_decode_layer(const ckv_kv_cache* kv, const ckv_graph_state* s
   const ckv::DecodeArgs a = pack(kv, st, csr, dl, cfg, ws);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const int parts = ckv::fused_parts(a);
+  if (ckv::coop_parts(a) > 0) {  // merged inside the launch; the update follows
+    rc = ckv::launch_select_attend(a, s, nullptr, parts, true);
+    return rc ? rc : ckv::launch_update(a, s);
+  }
   if (parts > 0) {
-    rc = ckv::launch_select_attend(a, s, nullptr, parts);
+    rc = ckv::launch_select_attend(a, s, nullptr, parts, false);
     return rc ? rc : ckv::launch_merge_update(a, s, parts);
   }
   rc = ckv::launch_score_select(a, s);
@@ -239,9 +243,10 @@ extern "C" int ckv_decode_step_after_update(const ckv_layer_args* layer, const c
       up = &u;
     }
   }
-  rc = ckv::launch_select_attend(a, s, up, parts);
+  const bool coop = ckv::coop_parts(a) > 0;
+  rc = ckv::launch_select_attend(a, s, up, parts, coop);
   if (!rc && up) rc = ckv::launch_sync_shared(u, s);
-  if (!rc) rc = ckv::launch_merge(a, s, parts);
+  if (!rc && !coop) rc = ckv::launch_merge(a, s, parts);
   return rc;
 }
 
@@ -396,5 +401,5 @@ extern "C" int ckv_select_attend_partials(const ckv_layer_args* layer, void* str
   const ckv::DecodeArgs a = pack(layer->kv, layer->state, layer->csr, layer->deltas, layer->config, layer->ws);
   const int parts = ckv::fused_parts(a);
   if (parts == 0) return fail(CKV_E_INVALID, "the fused selection + attention path cannot serve this layer");
-  return ckv::launch_select_attend(a, reinterpret_cast<hipStream_t>(stream), nullptr, parts);
+  return ckv::launch_select_attend(a, reinterpret_cast<hipStream_t>(stream), nullptr, parts, false);
 }

@@ -25,7 +25,22 @@ __device__ unsigned long long phase_stamp[32];  // one array per kernel file
   do {                                                                                       \
     if ((cond) && threadIdx.x == 0) atomicMax(&phase_stamp[(slot)], (unsigned long long)wall_clock64()); \
   } while (0)
+// Register-held stamps (no store until the flush, so no memory wait covers them).
+#define CKV_TS_DECL unsigned long long ckv_ts[32] = {}
+#define CKV_TS_ARG , unsigned long long* ckv_ts
+#define CKV_TS_PASS , ckv_ts
+#define CKV_TS(slot) (ckv_ts[(slot)] = wall_clock64())
+#define CKV_TS_FLUSH(cond)                                                        \
+  do {                                                                            \
+    if ((cond) && threadIdx.x == 0)                                               \
+      for (int i_ = 0; i_ < 32; ++i_) if (ckv_ts[i_]) phase_stamp[i_] = ckv_ts[i_]; \
+  } while (0)
 #else
+#define CKV_TS_DECL do {} while (0)
+#define CKV_TS_ARG
+#define CKV_TS_PASS
+#define CKV_TS(slot) do {} while (0)
+#define CKV_TS_FLUSH(cond) do {} while (0)
 #define CKV_STAMP(cond, slot) \
   do {                        \
   } while (0)
@@ -159,6 +174,32 @@ __device__ inline float gload_f32(const float* p) {
   typedef const __attribute__((address_space(1))) float* global_f32_ptr;
   return *(global_f32_ptr)(p);
 }
+
+// Loads and stores for data that workgroups of one launch hand to each other.
+// Each XCD's L2 caches device memory without coherence with the other XCDs;
+// agent-scope relaxed atomics compile to global_load/global_store with sc1,
+// which bypass those copies, so a value stored this way (and waited for) is
+// seen by such a load on any compute unit.
+__device__ inline uint64_t ld_agent_u64(const uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline uint32_t ld_agent_u32(const uint32_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline float ld_agent_f32(const float* p) {
+  return __uint_as_float(ld_agent_u32(reinterpret_cast<const uint32_t*>(p)));
+}
+__device__ inline void st_agent_u64(uint64_t* p, uint64_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline void st_agent_u32(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline void st_agent_f32(float* p, float v) {
+  st_agent_u32(reinterpret_cast<uint32_t*>(p), __float_as_uint(v));
+}
+// Waits until every global load and store this thread issued has completed.
+__device__ inline void wait_vm() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 
 // ---------------------------------------------------------------------------
@@ -464,7 +505,10 @@ size_t select_lds_bytes(int community_capacity, int descriptor_capacity, int max
 int attention_batch_splits(const DecodeArgs& a);  // 0 when the batched attention cannot serve `a`
 int fused_parts(const DecodeArgs& a);              // 0 when the fused selection + attention cannot serve `a`
 size_t fused_lds_bytes(const DecodeArgs& a);
-int launch_select_attend(const DecodeArgs& a, hipStream_t stream, const DecodeArgs* pending, int parts);
+// coop: the cooperative variant (scoring shared between a head's workgroups,
+// the split merge inside the launch); coop_parts(a) must equal `parts`.
+int launch_select_attend(const DecodeArgs& a, hipStream_t stream, const DecodeArgs* pending, int parts, bool coop);
+int coop_parts(const DecodeArgs& a);  // parts of the cooperative fused launch, 0 when it cannot serve `a`
 int launch_batch_select_attend(const DecodeArgs& h, const DecodeArgs* table, int count, int max_nscore,
                                size_t max_lds, int parts, hipStream_t stream);
 int launch_merge(const DecodeArgs& a, hipStream_t stream, int splits);

@@ -37,6 +37,7 @@
 #include "ckv_error.h"
 #include "ckv_tile.h"
 #include "ckv_update.h"
+#include "ckv_score.h"
 
 namespace ckv {
 
@@ -52,90 +53,91 @@ constexpr int DESC_ARRAYS = 7;                             // per-descriptor LDS
 constexpr size_t FUSED_LDS_LIMIT = 144 * 1024;
 // 64-slot tiles attended per workgroup of the fused path (parts per head = tiles / this).
 constexpr int FUSED_TILES = 2;
+// Cooperative fused launch: polling rounds (each a memory round trip plus a
+// short sleep, about 1 us) before a part scores the missing communities
+// itself; at most 64 parts per head.
+constexpr int COOP_POLLS = 48;
+constexpr int COOP_MAX_PARTS = 64;
+constexpr int COOP_WAVES = SELECT_THREADS / 64;
 }  // namespace
 
-// Centroid row fragment of one lane: 16 dims (e4m3: 16 bytes, f32: 64 bytes).
-template <int CT>
-struct CentroidFrag {
-  static constexpr int N = CT == CKV_E4M3 ? 1 : 4;
-  uint4 v[N];
-};
-
-template <int CT>
-__device__ inline void load_frag(const void* base, int64_t row, int d0, CentroidFrag<CT>& f) {
-  if constexpr (CT == CKV_E4M3) {
-    f.v[0] = gload16(reinterpret_cast<const uint8_t*>(base) + row * D + d0);
-  } else {
-    const float* p = reinterpret_cast<const float*>(base) + row * D + d0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) f.v[i] = gload16(p + 4 * i);
-  }
+// Exchange row of one retrieval head: the tagged scores, then one
+// nearest-centroid minimum per wave of each of at most 64 parts.
+__host__ __device__ inline int64_t exchange_stride(int community_capacity) {
+  return (int64_t)community_capacity + COOP_MAX_PARTS * COOP_WAVES;
 }
 
-template <int CT>
-__device__ inline void decode_frag(const CentroidFrag<CT>& f, float* out) {
-  if constexpr (CT == CKV_E4M3) {
-    // Hardware OCP e4m3 -> f32 (exact: every e4m3 value is an f32), two bytes per instruction.
-    typedef float f32x2_t __attribute__((ext_vector_type(2)));
-    const uint32_t w[4] = {f.v[0].x, f.v[0].y, f.v[0].z, f.v[0].w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const f32x2_t lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[i], false);
-      const f32x2_t hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[i], true);
-      out[4 * i] = lo[0];
-      out[4 * i + 1] = lo[1];
-      out[4 * i + 2] = hi[0];
-      out[4 * i + 3] = hi[1];
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      out[4 * i] = ckv_u2f(f.v[i].x);
-      out[4 * i + 1] = ckv_u2f(f.v[i].y);
-      out[4 * i + 2] = ckv_u2f(f.v[i].z);
-      out[4 * i + 3] = ckv_u2f(f.v[i].w);
-    }
-  }
-}
 
-// One 8-lane group's share of a centroid row's dots with two queries, in the
-// pinned order: each lane sums its 16 dims in order (bf16 x e4m3 products have
-// at most 12 significant bits, so they are exact in f32 and a fused
-// multiply-add equals the pinned multiply-then-add), then the butterfly xor 4,
-// 2, 1 adds the lanes.  Shared by the selection's scoring and the prescoring
-// kernel so that both give the same bits.
-template <int CT, int DT>
-__device__ __forceinline__ void dot16_pair(const float* qa, const float* qb, const float* cv, float& a0, float& a1) {
-  a0 = qa[0] * cv[0];
-  a1 = qb[0] * cv[0];
+// Arrival of one part of head rh.  The last part to arrive merges the head's
+// split partials into output and lse (the arithmetic of merge_wide_body, so
+// the results equal the separate merge kernel's), reduces the parts'
+// nearest-centroid minima into a.ws.nearest, then resets the arrival counter
+// and advances the head's epoch for the next launch.  Nothing here waits on
+// another workgroup.
+template <int PMAX>
+__device__ __forceinline__ void coop_finish(const DecodeArgs& a, const int rh, const int parts, const uint32_t epoch,
+                                   const bool nearest_mode, const uint64_t* xrow) {
+  __shared__ int s_last;
+  __shared__ float sc_s[CKV_MAX_GROUP][PMAX];
+  __shared__ float den_s[CKV_MAX_GROUP];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  uint32_t* counter = a.ws.block_counters + rh;
+  wait_vm();
+  __syncthreads();  // every store of the part has completed
+  if (tid == 0)
+    s_last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(parts - 1);
+  __syncthreads();
+  if (!s_last) return;
+  CKV_STAMP(rh == 0, 24);
+  const int G = a.cfg.group_size;
+  const int C = a.st.community_capacity;
+  const int64_t base = (int64_t)rh * G * parts;
+  const int i = min(tid, G * D - 1);
+  const float* src = a.ws.partial_acc + (base + (int64_t)(i >> 7) * parts) * D + (i & (D - 1));
+  float v[PMAX];
 #pragma unroll
-  for (int i = 1; i < 16; ++i) {
-    if constexpr (CT == CKV_E4M3 && DT == CKV_BF16) {
-      a0 = __builtin_fmaf(qa[i], cv[i], a0);
-      a1 = __builtin_fmaf(qb[i], cv[i], a1);
-    } else {
-      a0 = a0 + qa[i] * cv[i];
-      a1 = a1 + qb[i] * cv[i];
+  for (int k = 0; k < PMAX; ++k) v[k] = ld_agent_f32(src + (int64_t)min(k, parts - 1) * D);
+  if (wave < G) {
+    const bool ok = lane < parts;
+    const int64_t j = base + (int64_t)wave * parts + (ok ? lane : 0);
+    const float mt = ok ? ld_agent_f32(a.ws.partial_max + j) : NEG_INF;
+    const float lt = ok ? ld_agent_f32(a.ws.partial_sum + j) : 0.0f;
+    const float M = wave_max(mt);
+    const float sc = mt == NEG_INF ? 0.0f : ckv_expf(mt - M);
+    const float den = wave_sum_tree(sc != 0.0f ? lt * sc : 0.0f);
+    if (lane < PMAX) sc_s[wave][lane] = sc;
+    if (lane == 0) {
+      den_s[wave] = den;
+      a.ws.lse[(int64_t)rh * G + wave] = M + ckv_logf(den);
     }
+  } else if (nearest_mode && wave == COOP_WAVES - 1) {
+    uint64_t m = ~0ull;
+    for (int e = lane; e < parts * COOP_WAVES; e += 64) {
+      const uint64_t x = ld_agent_u64(xrow + C + e);
+      m = x < m ? x : m;
+    }
+    m = wave_min_u64(m);
+    if (lane == 0) a.ws.nearest[rh] = (m == ~0ull) ? -1 : (int)(m & 0xffffffffu);
   }
-  a0 = add_xor_f32<4>(a0);
-  a1 = add_xor_f32<4>(a1);
-  a0 = add_xor_f32<2>(a0);
-  a1 = add_xor_f32<2>(a1);
-  a0 = add_xor_f32<1>(a0);
-  a1 = add_xor_f32<1>(a1);
-}
-
-// Query slice (dims 16*lane8 .. +15) of queries g and g+1 from the LDS copy.
-__device__ __forceinline__ void load_q_pair(const float* q_s, int g, int lane8, float* qa, float* qb) {
-  const float4* pa = reinterpret_cast<const float4*>(q_s + g * D + 16 * lane8);
-  const float4* pq = reinterpret_cast<const float4*>(q_s + (g + 1) * D + 16 * lane8);
+  __syncthreads();
+  if (tid < G * D) {
+    const int g = tid >> 7;
+    float acc = 0.0f;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const float4 x = pa[i], y = pq[i];
-    qa[4 * i] = x.x; qa[4 * i + 1] = x.y; qa[4 * i + 2] = x.z; qa[4 * i + 3] = x.w;
-    qb[4 * i] = y.x; qb[4 * i + 1] = y.y; qb[4 * i + 2] = y.z; qb[4 * i + 3] = y.w;
+    for (int k = 0; k < PMAX; ++k) {
+      const float sc = sc_s[g][k];
+      if (k < parts) acc = acc + (sc != 0.0f ? v[k] * sc : 0.0f);
+    }
+    reinterpret_cast<uint16_t*>(a.ws.output)[((int64_t)rh * G + g) * D + (tid & (D - 1))] =
+        ckv_f32_to_bf16_bits(acc / den_s[g]);
   }
+  if (tid == 0) {
+    st_agent_u32(counter, 0u);
+    st_agent_u32(a.ws.block_counters + 2 * a.st.retrieval_heads + rh, epoch + 1u);
+  }
+  CKV_STAMP(rh == 0, 25);
 }
 
 // OWN: communities owned per thread (thread t owns [t*OWN, (t+1)*OWN), so id
@@ -145,6 +147,13 @@ __device__ __forceinline__ void load_q_pair(const float* q_s, int g, int lane8, 
 // (same dtypes, disjoint state) on otherwise idle CUs.
 // LDS bytes of the fused path's slot table (16-byte aligned).
 __host__ __device__ inline size_t fused_slot_bytes(int slot_capacity) { return ((size_t)slot_capacity * 4 + 15) & ~(size_t)15; }
+// LDS bytes of the selection arrays in the fused path (16-byte aligned); the
+// attention buffers follow them.
+__host__ __device__ inline size_t fused_select_bytes(int community_capacity, int descriptor_capacity,
+                                                     int max_selected) {
+  return ((size_t)((community_capacity + 7) & ~7) * 2 + (size_t)descriptor_capacity * 7 * 4 +
+          (size_t)((max_selected + 63) / 64 + 2) * 4 + 15) & ~(size_t)15;
+}
 
 // FUSED: `part` of `parts` workgroups of this head each run the whole
 // selection (they are latency-bound, so the copies cost no time), resolve the
@@ -153,7 +162,13 @@ __host__ __device__ inline size_t fused_slot_bytes(int slot_capacity) { return (
 // parts.
 // PRE: the scores were written to a.ws.scores by score_rows_kernel (no
 // nearest-centroid search then); the workgroup loads them instead of scoring.
-template <int CT, int DT, int OWN, bool FUSED = false, bool PRE = false>
+// COOP (with FUSED): each part scores only its share of the live communities
+// and publishes it, epoch-tagged, in a.ws.exchange; the parts read the other
+// shares from there (bounded polling: a part that does not see them all
+// within COOP_POLLS rounds scores every community itself, so no part waits
+// on another indefinitely).  The last part to finish merges the head's split
+// partials (coop_finish).
+template <int CT, int DT, int OWN, bool FUSED = false, bool PRE = false, bool COOP = false, int PMAX = 32>
 __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, const int part = 0,
                                             const int parts = 1) {
   constexpr int PB = CT == CKV_E4M3 ? 4 : 2;  // scoring passes whose loads are in flight together
@@ -219,10 +234,25 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
       rsize[buf][pb] = gload_i32(a.st.community_sizes + (int64_t)rh * C + row);
     }
   };
-  if constexpr (!PRE) {
+  if constexpr (!PRE && !COOP) {
     load_batch(0, 0, nscore - 1);
     load_batch(PB, 1, nscore - 1);  // clamped rows: harmless when there is no second batch
   }
+  // COOP: this part's share [sh0, sh1) of the live communities (one 64-row
+  // pass when the share fits), the head's epoch and the exchange row.
+  const int share = (count + parts - 1) / max(parts, 1);
+  const int sh0 = min(part * share, count), sh1 = min(sh0 + share, count);
+  uint64_t* xrow = COOP ? a.ws.exchange + (int64_t)rh * exchange_stride(C) : nullptr;
+  uint32_t epoch = 0;
+  CentroidFrag<CT> cfrag;
+  int csize = 0;
+  if constexpr (COOP) {
+    epoch = ld_agent_u32(a.ws.block_counters + 2 * a.st.retrieval_heads + rh);
+    const int row = min(sh0 + sub, max(sh1, 1) - 1);
+    load_frag<CT>(a.st.centroids, (int64_t)rh * C + row, 16 * lane8, cfrag);
+    csize = gload_i32(a.st.community_sizes + (int64_t)rh * C + row);
+  }
+  const uint64_t tag = (uint64_t)(epoch + 1u) << 32;
   // Query group: two elements per thread (G * 128 <= 2048 <= 4 * threads).
   float qv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   // prescored: the scores of this head's rows t, t + threads, ...
@@ -364,13 +394,93 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
   // loop waits for every load issued in it.
   const int live_passes = (count + ROWS_PER_PASS - 1) / ROWS_PER_PASS;
   const int last_live = max(count, 1) - 1;
+  bool score_all = !PRE;
+  if constexpr (COOP) {
+    // This part's share, published as (epoch + 1) << 32 | fp16 bits.
+    uint64_t best_share = ~0ull;
+    for (int r0 = sh0; r0 < sh1; r0 += ROWS_PER_PASS) {
+      if (r0 != sh0) {
+        const int row = min(r0 + sub, sh1 - 1);
+        load_frag<CT>(a.st.centroids, (int64_t)rh * C + row, 16 * lane8, cfrag);
+        csize = gload_i32(a.st.community_sizes + (int64_t)rh * C + row);
+      }
+      float cv[16];
+      decode_frag<CT>(cfrag, cv);
+      float best = NEG_INF;
+#pragma unroll 1
+      for (int g = 0; g < G; g += 2) {
+        float qa[16], qb[16];
+        load_q_pair(q_s, g, lane8, qa, qb);
+        float a0, a1;
+        dot16_pair<CT, DT>(qa, qb, cv, a0, a1);
+        best = fmax_exact(best, a0);
+        if (g + 1 < G) best = fmax_exact(best, a1);
+      }
+      const int c = r0 + sub;
+      const bool in = c < sh1;
+      const bool live = in && csize > 0;
+      const uint16_t bits = f16_bits_hw(live ? best : NEG_INF);
+      if (lane8 == 0 && in) {
+        key16[c] = bits;
+        st_agent_u64(xrow + c, tag | bits);
+      }
+      if (nearest_mode) {
+        float acc;
+        {
+          const float d0 = key_s[16 * lane8] - cv[0];
+          acc = d0 * d0;
+        }
+#pragma unroll
+        for (int i = 1; i < 16; ++i) {
+          const float di = key_s[16 * lane8 + i] - cv[i];
+          acc = acc + di * di;
+        }
+        acc = add_xor_f32<4>(acc);
+        acc = add_xor_f32<2>(acc);
+        acc = add_xor_f32<1>(acc);
+        if (live) {
+          const uint64_t cand = ((uint64_t)ckv_f2u(acc) << 32) | (uint32_t)c;
+          best_share = cand < best_share ? cand : best_share;
+        }
+      }
+    }
+    if (nearest_mode) {  // every wave of every part publishes its minimum (~0 when it has none)
+      const uint64_t w = wave_min_u64(best_share);
+      if ((tid & 63) == 0) st_agent_u64(xrow + C + part * WAVES + (tid >> 6), w);
+    }
+    // The other parts' shares of this thread's communities.
+    uint32_t need = 0;
+#pragma unroll
+    for (int k = 0; k < OWN; ++k) {
+      const int c = c0 + k;
+      if (c < count && (c < sh0 || c >= sh1)) need |= 1u << k;
+    }
+    for (int poll = 0; need != 0 && poll < COOP_POLLS; ++poll) {
+      uint64_t v[OWN];
+#pragma unroll
+      for (int k = 0; k < OWN; ++k) v[k] = ld_agent_u64(xrow + min(c0 + k, C - 1));
+#pragma unroll
+      for (int k = 0; k < OWN; ++k) {
+        if (((need >> k) & 1u) && (v[k] & 0xffffffff00000000ull) == tag) {
+          key16[c0 + k] = (uint16_t)v[k];
+          need &= ~(1u << k);
+        }
+      }
+      if (need != 0) __builtin_amdgcn_s_sleep(8);
+    }
+    score_all = __syncthreads_or(need != 0);
+  }
   if constexpr (PRE) {
 #pragma unroll
     for (int k = 0; k < OWN; ++k) {
       const int c = tid + k * SELECT_THREADS;
       if (c < count) key16[c] = pre_key[k];
     }
-  } else {
+  } else if (score_all) {
+    if constexpr (COOP) {  // fallback: every community scored here
+      load_batch(0, 0, nscore - 1);
+      load_batch(PB, 1, nscore - 1);
+    }
     for (int p0 = 0; p0 < live_passes; p0 += 2 * PB) {
       score_batch(p0, 0);
       if (p0 + PB >= live_passes) break;
@@ -765,21 +875,24 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
     }
   }
   // ---- outputs that nothing in this kernel reads back --------------------------
-  // (fused: split over the head's parts, so no part carries them all)
+  // (fused: split over the head's parts, so no part carries them all, and
+  // written by the waves that attend no tile: their attention buffers lie
+  // past the selection arrays, so the tile waves start attending at once)
   CKV_STAMP(rh == 0 && part == 0, 11);
   {
     const int wp = FUSED ? part : 0, wn = FUSED ? parts : 1;
-    const int stride = wn * SELECT_THREADS;
-    if (tid == 0 && wp == 0) {
+    const int ot = FUSED ? tid - 64 * FUSED_TILES : tid;  // index among the writing threads (< 0: none)
+    const int stride = wn * (FUSED ? SELECT_THREADS - 64 * FUSED_TILES : SELECT_THREADS);
+    if (ot == 0 && wp == 0) {
       a.ws.descriptor_counts[rh] = n_desc;
       a.ws.selected_counts[rh] = sel_count;
     }
     // item i goes to part i % wn (each part writes a strided share)
-    for (int i = wp + wn * tid; i < n_desc; i += stride) {
+    for (int i = wp + wn * ot; ot >= 0 && i < n_desc; i += stride) {
       a.ws.communities[(int64_t)rh * dcap + i] = desc_comm[i];
       a.ws.cumulative_ends[(int64_t)rh * dcap + i] = desc_end[i];
     }
-    for (int t = wp + wn * tid; t < a.ws.budget_tiles; t += stride) {
+    for (int t = wp + wn * ot; ot >= 0 && t < a.ws.budget_tiles; t += stride) {
       // first descriptor ending after the tile's first selected slot (searched
       // between the first descriptors of its 64-slot block and the next)
       const int off = max(t * TILE - ns, 0);
@@ -807,7 +920,7 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
         }
       }
     }
-    if (nearest_mode && tid == 0 && wp == wn - 1) {
+    if (nearest_mode && !COOP && tid == 0 && wp == wn - 1) {
       uint64_t m = ~0ull;
       for (int w = 0; w < WAVES; ++w) m = near_s[w] < m ? near_s[w] : m;
       a.ws.nearest[rh] = (m == ~0ull) ? -1 : (int)(m & 0xffffffffu);
@@ -815,9 +928,10 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
   }
   CKV_STAMP(rh == 0 && part == 0, 5);
   if constexpr (FUSED) {
-    __syncthreads();  // the selection arrays are dead from here
-    attend_part<SELECT_THREADS / 64, FUSED_TILES>(a, rh, part, parts, fused_pos, dyn);
+    attend_part<SELECT_THREADS / 64, FUSED_TILES, COOP>(
+        a, rh, part, parts, fused_pos, dyn + fused_select_bytes(C, dcap, a.cfg.max_selected));
   }
+  if constexpr (COOP) coop_finish<PMAX>(a, rh, parts, epoch, nearest_mode, xrow);
 }
 
 template <int CT, int DT, int OWN>
@@ -833,7 +947,12 @@ __global__ __launch_bounds__(SELECT_THREADS) void select_kernel(DecodeArgs a, De
 // Fused selection + attention partials: `parts` workgroups per retrieval head
 // (workgroup w: head w / parts, part w % parts); workgroups beyond them run the
 // pending online update of another layer `u`.
-template <int CT, int DT, int OWN>
+// PMAX > 0: cooperative scoring and the in-launch split merge (parts <= PMAX).
+// Cooperative parts of a head are interleaved (head = block % heads): the
+// dispatcher deals blocks to the XCDs round robin, so with 8 heads every
+// part of a head shares one XCD's L2, and each head's parts span the whole
+// dispatch order instead of its tail.
+template <int CT, int DT, int OWN, int PMAX = 0>
 __global__ __launch_bounds__(SELECT_THREADS) void select_attend_kernel(DecodeArgs a, DecodeArgs u, int parts) {
   const int nsel = a.st.retrieval_heads * parts;
   if ((int)blockIdx.x >= nsel) {
@@ -841,7 +960,11 @@ __global__ __launch_bounds__(SELECT_THREADS) void select_attend_kernel(DecodeArg
     owner_update<CT, DT>(u, urh, u.ws.lse[(int64_t)urh * u.cfg.group_size]);
     return;
   }
-  select_body<CT, DT, OWN, true>(a, blockIdx.x / parts, blockIdx.x % parts, parts);
+  if constexpr (PMAX > 0)
+    select_body<CT, DT, OWN, true, false, true, PMAX>(a, blockIdx.x % a.st.retrieval_heads,
+                                                       blockIdx.x / a.st.retrieval_heads, parts);
+  else
+    select_body<CT, DT, OWN, true>(a, blockIdx.x / parts, blockIdx.x % parts, parts);
 }
 
 template <int CT, int DT, int OWN>
@@ -965,19 +1088,23 @@ int fused_parts(const DecodeArgs& a) {
   if (a.ws.slot_capacity > 8192 || a.cfg.group_size * D > 512) return 0;
   const int tiles = a.ws.slot_capacity / TILE;
   const int parts = (tiles + FUSED_TILES - 1) / FUSED_TILES;
-  const size_t lds = fused_slot_bytes(a.ws.slot_capacity) +
-                     std::max(select_lds_bytes(a.st.community_capacity, a.ws.descriptor_capacity, a.cfg.max_selected),
-                              attend_part_lds_bytes(SELECT_THREADS / 64));
+  const size_t lds = fused_lds_bytes(a);
   return (parts <= 64 && lds <= FUSED_LDS_LIMIT) ? parts : 0;
 }
 
 size_t fused_lds_bytes(const DecodeArgs& a) {
   return fused_slot_bytes(a.ws.slot_capacity) +
-         std::max(select_lds_bytes(a.st.community_capacity, a.ws.descriptor_capacity, a.cfg.max_selected),
-                  attend_part_lds_bytes(SELECT_THREADS / 64));
+         fused_select_bytes(a.st.community_capacity, a.ws.descriptor_capacity, a.cfg.max_selected) +
+         attend_part_lds_bytes(SELECT_THREADS / 64);
 }
 
-int launch_select_attend(const DecodeArgs& a, hipStream_t s, const DecodeArgs* pending, int parts) {
+int coop_parts(const DecodeArgs& a) {
+  const int parts = fused_parts(a);
+  if (parts == 0 || parts > COOP_MAX_PARTS || a.ws.exchange == nullptr || a.st.centroid_dtype != CKV_E4M3) return 0;
+  return a.st.community_capacity <= 4 * SELECT_THREADS ? parts : 0;
+}
+
+int launch_select_attend(const DecodeArgs& a, hipStream_t s, const DecodeArgs* pending, int parts, bool coop) {
   const size_t lds = fused_lds_bytes(a);
   const int nscore = std::min(a.st.community_capacity, a.ws.score_blocks * SCORE_BLOCK);
   const int own = (nscore + SELECT_THREADS - 1) / SELECT_THREADS;
@@ -1000,6 +1127,17 @@ int launch_select_attend(const DecodeArgs& a, hipStream_t s, const DecodeArgs* p
     return launch_check("select_attend");
   };
   constexpr int OWN_MAX = CKV_MAX_COMMUNITIES / SELECT_THREADS;
+  if (coop) {
+    if (coop_parts(a) != parts) return limit_error("the cooperative fused launch cannot serve this layer");
+    if (parts <= 32) {
+      return own <= 1 ? launch(select_attend_kernel<CKV_E4M3, CKV_BF16, 1, 32>)
+             : own <= 2 ? launch(select_attend_kernel<CKV_E4M3, CKV_BF16, 2, 32>)
+                        : launch(select_attend_kernel<CKV_E4M3, CKV_BF16, 4, 32>);
+    }
+    return own <= 1 ? launch(select_attend_kernel<CKV_E4M3, CKV_BF16, 1, 64>)
+           : own <= 2 ? launch(select_attend_kernel<CKV_E4M3, CKV_BF16, 2, 64>)
+                      : launch(select_attend_kernel<CKV_E4M3, CKV_BF16, 4, 64>);
+  }
   if (a.st.centroid_dtype == CKV_E4M3) {
     return own <= 1 ? launch(select_attend_kernel<CKV_E4M3, CKV_BF16, 1>)
            : own <= 2 ? launch(select_attend_kernel<CKV_E4M3, CKV_BF16, 2>)

@@ -181,7 +181,9 @@ constexpr size_t attend_part_lds_bytes(int waves) {
   return (size_t)waves * (V_HALF_ROWS * D * 2 + TILE * 4 + TILE * 4 + 2 * CKV_MAX_GROUP * 4);
 }
 
-template <int W, int TP>
+// AGENT: the split partials are stored with st_agent_f32 (another workgroup
+// of the launch merges them).
+template <int W, int TP, bool AGENT = false>
 __device__ inline void attend_part(const DecodeArgs& a, const int rh, const int part, const int parts,
                                    int pos, unsigned char* lds) {
   static_assert(TP <= W, "one tile per wave");
@@ -271,7 +273,8 @@ __device__ inline void attend_part(const DecodeArgs& a, const int rh, const int 
         acc = acc + ow[g * D + d] * __expf(mw - M);
       }
     }
-    a.ws.partial_acc[(((int64_t)rh * G + g) * parts + part) * D + d] = acc;
+    float* dst = a.ws.partial_acc + (((int64_t)rh * G + g) * parts + part) * D + d;
+    if constexpr (AGENT) st_agent_f32(dst, acc); else *dst = acc;
   }
   if (tid < G) {
     float M = NEG_INF;
@@ -283,8 +286,15 @@ __device__ inline void attend_part(const DecodeArgs& a, const int rh, const int 
       const float mw = wm_s[w * CKV_MAX_GROUP + tid];
       if (mw != NEG_INF) l = l + wl_s[w * CKV_MAX_GROUP + tid] * __expf(mw - M);
     }
-    a.ws.partial_max[((int64_t)rh * G + tid) * parts + part] = M;
-    a.ws.partial_sum[((int64_t)rh * G + tid) * parts + part] = l;
+    float* pm = a.ws.partial_max + ((int64_t)rh * G + tid) * parts + part;
+    float* pl = a.ws.partial_sum + ((int64_t)rh * G + tid) * parts + part;
+    if constexpr (AGENT) {
+      st_agent_f32(pm, M);
+      st_agent_f32(pl, l);
+    } else {
+      *pm = M;
+      *pl = l;
+    }
   }
   CKV_STAMP(rh == 0 && part == 0, 21);
   CKV_STAMP_MAX(rh == 0, 22);

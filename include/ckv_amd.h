@@ -49,7 +49,7 @@
 extern "C" {
 #endif
 
-#define CKV_ABI_VERSION 2
+#define CKV_ABI_VERSION 3
 #define CKV_HEAD_DIM 128
 #define CKV_TILE 64
 #define CKV_KAPPA 8
@@ -156,9 +156,12 @@ typedef struct ckv_decode_workspace {
   int32_t* tile_descriptors;   /* [retrieval_heads][budget_tiles] */
   int32_t* selected_counts;    /* [retrieval_heads] */
   int32_t* slot_positions;     /* [retrieval_heads][slot_capacity] KV position per attended slot, -1 = none */
-  uint64_t* nearest_partial;   /* reserved (may be null): the selection kernel reduces in LDS */
+  uint64_t* exchange;          /* [retrieval_heads][community_capacity + 512], zero before first use, or null:
+                                  the fused launch's workgroups of a head hand each other their share of the
+                                  centroid scores (epoch-tagged) and nearest-centroid minima through it */
   int32_t* nearest;            /* [retrieval_heads] */
-  uint32_t* block_counters;    /* [2 * retrieval_heads], zero before first use; kernels leave it zero */
+  uint32_t* block_counters;    /* [4 * retrieval_heads], zero before first use: arrival counters (the kernels
+                                  leave them zero) and, at [2R, 3R), the fused launch's epoch per head */
   float* partial_max;          /* [query_heads][slot_tiles] */
   float* partial_sum;          /* [query_heads][slot_tiles] */
   float* partial_acc;          /* [query_heads][slot_tiles][128] */
