@@ -39,6 +39,9 @@
 #include "ckv_update.h"
 #include "ckv_score.h"
 
+#ifndef CKV_R2_LATE
+#define CKV_R2_LATE 0
+#endif
 namespace ckv {
 
 namespace {
@@ -147,12 +150,20 @@ __device__ __forceinline__ void coop_finish(const DecodeArgs& a, const int rh, c
 // (same dtypes, disjoint state) on otherwise idle CUs.
 // LDS bytes of the fused path's slot table (16-byte aligned).
 __host__ __device__ inline size_t fused_slot_bytes(int slot_capacity) { return ((size_t)slot_capacity * 4 + 15) & ~(size_t)15; }
-// LDS bytes of the selection arrays in the fused path (16-byte aligned); the
-// attention buffers follow them.
-__host__ __device__ inline size_t fused_select_bytes(int community_capacity, int descriptor_capacity,
-                                                     int max_selected) {
-  return ((size_t)((community_capacity + 7) & ~7) * 2 + (size_t)descriptor_capacity * 7 * 4 +
-          (size_t)((max_selected + 63) / 64 + 2) * 4 + 15) & ~(size_t)15;
+// LDS of the fused path's selection (16-byte aligned), after the window
+// communities: fp16 keys, seven per-community int arrays (selection start,
+// size, CSR start, delta count, tail chunk, its start and fill) and the tile
+// marks; the attention buffers follow.
+__host__ __device__ inline size_t fused_select_bytes(int community_capacity, int budget_tiles, int parts) {
+  const size_t cp = (size_t)((community_capacity + 7) & ~7);
+  const size_t td = (size_t)((budget_tiles + parts - 1) / parts);
+  return (cp * 2 + cp * 8 * 4 + ((size_t)FUSED_TILES * TILE + td) * 4 + 15) & ~(size_t)15;
+}
+__device__ inline int* fused_fields(unsigned char* dyn, int community_capacity) {
+  return reinterpret_cast<int*>(dyn + (size_t)((community_capacity + 7) & ~7) * 2);
+}
+__device__ inline int* fused_marks(unsigned char* dyn, int community_capacity) {
+  return fused_fields(dyn, community_capacity) + 8 * ((community_capacity + 7) & ~7);
 }
 
 // FUSED: `part` of `parts` workgroups of this head each run the whole
@@ -183,7 +194,8 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
   const int ns = a.cfg.num_sink;
   const int W = a.cfg.local_window;
   const int cpg = a.dl.chunks_per_graph;
-  CKV_STAMP(rh == 0 && part == 0, 0);
+  CKV_TS_DECL;
+  CKV_TS(0);
 
   __shared__ float q_s[CKV_MAX_GROUP * D];
   __shared__ float key_s[D];
@@ -322,9 +334,42 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
   if (tid < ns) sink_s[tid] = sink_v;
   if (nearest_mode && tid < D) key_s[tid] = (cur >= 0 && cur < a.kv.capacity) ? key_v : 0.0f;
   hist[tid & 255] = 0;
-  if (tid == 0) s_max_idx = -1;
+  if (tid == 0) {
+    s_max_idx = -1;
+    s_sel_count = 0;
+  }
+  if constexpr (FUSED) {  // tile marks (see the fused slot resolution)
+    if (tid < FUSED_TILES * TILE) fused_marks(dyn, C)[tid] = -1;
+  }
+  // R2 issue (tail-chunk start and fill of every owned community with decode
+  // deltas, the communities of the window tokens).  The cooperative path
+  // issues it right after R0 lands (its scoring share was loaded before, and
+  // the polls after it take as long), the others after the scoring.
+  int wcomm[WIN_PER_THREAD];
+#pragma unroll
+  for (int h = 0; h < WIN_PER_THREAD; ++h) wcomm[h] = -1;
+  auto issue_r2 = [&]() {
+    if (!materialise) return;
+    if (cpg > 0) {
+#pragma unroll
+      for (int k = 0; k < OWN; ++k) {
+        const int t = min(max(o_tl[k], 0), cpg - 1);
+        o_ts[k] = gload_i32(a.dl.chunk_start + cb + t);
+        o_tn[k] = gload_i32(a.dl.chunk_size + cb + t);
+      }
+    }
+    if (W > 0) {
+      const int32_t* tcomm = a.st.token_communities + (int64_t)graph * a.st.token_capacity;
+#pragma unroll
+      for (int h = 0; h < WIN_PER_THREAD; ++h) {
+        const int64_t p = (int64_t)cur - W + tid + h * SELECT_THREADS;
+        wcomm[h] = gload_i32(tcomm + (p < 0 ? 0 : (p >= a.st.token_capacity ? a.st.token_capacity - 1 : p)));
+      }
+    }
+  };
   __syncthreads();  // q_s, key_s, sink_s, hist
-  CKV_STAMP(rh == 0 && part == 0, 6);
+  if constexpr (COOP && !CKV_R2_LATE) issue_r2();
+  CKV_TS(6);
   if (tid < 64) {  // largest sink position: window tokens beyond it skip the sink test
     int m = -1;
     for (int i = tid; i < ns; i += 64) m = max(m, sink_s[i]);
@@ -489,13 +534,13 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
       load_batch(p0 + 3 * PB, 1, last_live);
     }
   }
-  CKV_STAMP(rh == 0 && part == 0, 7);
+  CKV_TS(7);
   if (nearest_mode) {
     const uint64_t w = wave_min_u64(best_nearest);
     if ((tid & 63) == 0) near_s[tid >> 6] = w;
   }
   __syncthreads();  // key16, near_s
-  CKV_STAMP(rh == 0 && part == 0, 1);
+  CKV_TS(1);
 
   // ---- R2: tail-chunk fields; communities of the window tokens ---------------
   // Issued after the scoring: their addresses need the R1 fields and the
@@ -504,27 +549,9 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
   // landed by now (the R1 fields long ago, the last prefetches are cache
   // hits); waiting for them here keeps the waits for older loads after the
   // conditional R2 issue from also waiting for R2.
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-  int wcomm[WIN_PER_THREAD];
-#pragma unroll
-  for (int h = 0; h < WIN_PER_THREAD; ++h) wcomm[h] = -1;
-  if (materialise) {
-    if (cpg > 0) {
-#pragma unroll
-      for (int k = 0; k < OWN; ++k) {
-        const int t = min(max(o_tl[k], 0), cpg - 1);
-        o_ts[k] = gload_i32(a.dl.chunk_start + cb + t);
-        o_tn[k] = gload_i32(a.dl.chunk_size + cb + t);
-      }
-    }
-    if (W > 0) {
-      const int32_t* tcomm = a.st.token_communities + (int64_t)graph * a.st.token_capacity;
-#pragma unroll
-      for (int h = 0; h < WIN_PER_THREAD; ++h) {
-        const int64_t p = (int64_t)cur - W + tid + h * SELECT_THREADS;
-        wcomm[h] = gload_i32(tcomm + (p < 0 ? 0 : (p >= a.st.token_capacity ? a.st.token_capacity - 1 : p)));
-      }
-    }
+  if constexpr (!COOP || CKV_R2_LATE) {
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    issue_r2();
   }
   // masks of the R0/R1 fields (R2 fields stay raw until used: masking them here would wait for R2)
 #pragma unroll
@@ -550,13 +577,15 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
     if (live) atomicAdd(hist + (o_key[k] >> 8), budget_mode ? o_size[k] : 1);
   }
   __syncthreads();
-  CKV_STAMP(rh == 0 && part == 0, 12);
-  // key16 is dead from here on; it becomes the community -> descriptor table.
+  CKV_TS(12);
+  // key16 is dead from here on (unfused); it becomes the community -> descriptor table.
   uint16_t* comm_desc = key16;
-  for (int c = tid; c < nscore; c += SELECT_THREADS) comm_desc[c] = 0xffffu;
+  if constexpr (!FUSED) {
+    for (int c = tid; c < nscore; c += SELECT_THREADS) comm_desc[c] = 0xffffu;
+  }
   if (tid < 64) find_threshold_bin(hist, target, &s_bin, &s_above);
   __syncthreads();
-  CKV_STAMP(rh == 0 && part == 0, 13);
+  CKV_TS(13);
   const int hb = s_bin;
   int threshold;  // 16-bit key threshold; -1 selects every non-empty community
   if (hb < 0) {
@@ -577,7 +606,7 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
     __syncthreads();
     threshold = (hb << 8) | s_bin;
   }
-  CKV_STAMP(rh == 0 && part == 0, 2);
+  CKV_TS(2);
 
   // Compaction, high keys first (id order), then threshold keys (id order): one
   // four-component block scan (high count/mass, threshold count/mass).
@@ -602,9 +631,9 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
 #pragma unroll
     for (int i = 0; i < 4; ++i) inc[i] = wave_inclusive_scan(v4[i]);
     if (lane == 63) *reinterpret_cast<int4*>(scan_s + 4 * wave) = int4{inc[0], inc[1], inc[2], inc[3]};
-    CKV_STAMP(rh == 0 && part == 0, 8);
+    CKV_TS(8);
     __syncthreads();
-    CKV_STAMP(rh == 0 && part == 0, 9);
+    CKV_TS(9);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       b4[i] = inc[i] - v4[i];
@@ -622,22 +651,32 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
     }
   }
   const int high_count = t4[0], high_mass = t4[1];
-  // Also marks idx as the first descriptor of every 64-slot block whose first
-  // slot falls in [start, end) (the ranges partition the selection).
-  auto store_desc = [&](int idx, int c, int start, int end, int k) {
-    desc_comm[idx] = c;
-    desc_end[idx] = end;
-    for (int b = (start + 63) >> 6; (b << 6) < end; ++b) blk_first[b] = idx;
-    desc_lo[idx] = o_lo[k];
-    desc_dc[idx] = o_dc[k];
-    desc_tl[idx] = o_tl[k];
-    const bool has = o_dc[k] > 0 && o_tl[k] >= 0 && o_tl[k] < cpg;
-    desc_ts[idx] = has ? o_ts[k] : 0;
-    desc_tn[idx] = has ? o_tn[k] : 0;
-  };
-  {
+  const int cap_sel = sel_slots;
+  int fused_pos = -1;  // FUSED: this lane's slot of its wave's tile
+  if constexpr (FUSED) {
+    // ---- fused slot resolution --------------------------------------------
+    // Each owner thread places its selected community: its selection start
+    // and membership fields go to LDS by community id, and a mark at the
+    // first slot it covers in each of this part's tiles, so a tile lane finds
+    // its community with one ballot (no descriptor search), and it writes its
+    // own descriptor and tile-descriptor outputs.  The window slots look their
+    // token's community up by id; the truncated last community's oldest
+    // attended member is gathered by the window lanes that need it, in the
+    // same round as the members (no workgroup barrier in between).
+    const int cp = (C + 7) & ~7;
+    int* f_st = fused_fields(dyn, C);  // selection start of each community, -1 when not selected
+    int* f_size = f_st + cp;
+    int* f_lo = f_size + cp;
+    int* f_dc = f_lo + cp;
+    int* f_tl = f_dc + cp;
+    int* f_ts = f_tl + cp;
+    int* f_tn = f_ts + cp;
+    int* f_idx = f_tn + cp;  // descriptor index of each selected community
+    int* marks = fused_marks(dyn, C);
+    int* td_s = marks + FUSED_TILES * TILE;  // this part's tile descriptors (tiles part, part + parts, ...)
+    const int dcap_ = a.ws.descriptor_capacity;
     int hc = b4[0], hm = b4[1], ec = b4[2], em = b4[3];
-    int my_max = -1;
+    int my_max = -1, my_end = 0;
 #pragma unroll
     for (int k = 0; k < OWN; ++k) {
       const int c = c0 + k;
@@ -645,292 +684,465 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
       const bool ok = c < count && size > 0;
       const bool high = ok && (int)o_key[k] > threshold;
       const bool eq = ok && threshold >= 0 && (int)o_key[k] == threshold;
+      int st = -1, en = 0, idx = -1;
       if (high) {
-        if (hm < cap_tokens && hc < dcap) {
-          store_desc(hc, c, hm, min(cap_tokens, hm + size), k);
-          my_max = max(my_max, hc);  // (a later high-key community has a smaller index than an earlier threshold one)
+        if (hm < cap_sel && hc < dcap_) {
+          st = hm;
+          en = min(cap_sel, hm + size);
+          idx = hc;
         }
         hc += 1;
         hm += size;
       } else if (eq) {
         const int st0 = high_mass + em;
         const bool within = budget_mode ? (st0 < sel_slots) : (ec < a.cfg.topk_communities - high_count);
-        const int idx = high_count + ec;
-        if (within && st0 < cap_tokens && idx < dcap) {
-          store_desc(idx, c, st0, min(cap_tokens, st0 + size), k);
-          my_max = max(my_max, idx);
+        const int i2 = high_count + ec;
+        if (within && st0 < cap_sel && i2 < dcap_) {
+          st = st0;
+          en = min(cap_sel, st0 + size);
+          idx = i2;
         }
         ec += 1;
         em += size;
       }
-    }
-    CKV_STAMP(rh == 0 && part == 0, 10);
-    if (my_max >= 0) atomicMax(&s_max_idx, my_max);
-  }
-  __syncthreads();  // descriptors, s_max_idx
-  const int n_desc = s_max_idx + 1;
-  const int sel_count = n_desc > 0 ? desc_end[n_desc - 1] : 0;
-  CKV_STAMP(rh == 0 && part == 0, 15);
-  if (tid == 0) blk_first[(sel_count + 63) / 64] = n_desc;  // (blocks below were marked by store_desc)
-  for (int d = tid; d < n_desc; d += SELECT_THREADS) comm_desc[desc_comm[d]] = (uint16_t)d;
-  // Only the last descriptor can be truncated; remember its community size.
-  if (n_desc > 0) {
-    const int last_c = desc_comm[n_desc - 1];
-    if (last_c / OWN == tid) {
+      if (c < cp) f_st[c] = st;
+      if (st >= 0) {
+        f_idx[c] = idx;
+        f_size[c] = size;
+        f_lo[c] = o_lo[k];
+        f_dc[c] = o_dc[k];
+        f_tl[c] = o_tl[k];
+        const bool has = o_dc[k] > 0 && o_tl[k] >= 0 && o_tl[k] < cpg;
+        f_ts[c] = has ? o_ts[k] : 0;
+        f_tn[c] = has ? o_tn[k] : 0;
 #pragma unroll
-      for (int k = 0; k < OWN; ++k) {
-        if (c0 + k == last_c) s_last_size = o_size[k];
+        for (int w = 0; w < FUSED_TILES; ++w) {
+          const int t0 = (part * FUSED_TILES + w) * TILE - ns;
+          if (st < t0 + TILE && en > t0) marks[w * TILE + max(st, t0) - t0] = c;
+        }
+        my_max = max(my_max, idx);
+        my_end = max(my_end, en);
+        // this part's tile descriptors whose first selected slot lies here
+        // (LDS only: a global store here would make the tile waves' later
+        // memory waits cover it)
+        for (int t = part, q = 0; t < a.ws.budget_tiles; t += parts, ++q) {
+          const int off = max(t * TILE - ns, 0);
+          if (st <= off && off < en) td_s[q] = idx;
+        }
       }
     }
-  }
-  if (tid == 0) s_last_sel_pos = -1;
-  CKV_STAMP(rh == 0 && part == 0, 3);
-
-  const int slot_cap = a.ws.slot_capacity;
-  int32_t* slots = a.ws.slot_positions + (int64_t)rh * slot_cap;
-  const int inc = a.cfg.include_current ? 1 : 0;
-  const int wbeg = ns + sel_count;
-  int fused_pos = -1;  // FUSED: this lane's slot of its wave's tile
-  if (materialise) {
-    if constexpr (FUSED) {
-      // The window tokens' communities, for whichever wave resolves them (the
-      // slot table region is free: fused workgroups resolve only their own tiles).
-#pragma unroll
-      for (int h = 0; h < WIN_PER_THREAD; ++h) {
-        const int i = tid + h * SELECT_THREADS;
-        if (i < W) slot_lds[i] = wcomm[h];
+    {  // totals: one DPP maximum per wave, then one LDS atomic per wave
+      const int wmax = wave_max_i32(my_max);
+      const int wend = wave_max_i32(my_end);
+      if ((tid & 63) == 0 && wmax >= 0) {
+        atomicMax(&s_max_idx, wmax);
+        atomicMax(&s_sel_count, wend);
       }
     }
-    __syncthreads();  // blk_first, comm_desc, s_last_size (and the window communities)
-    CKV_STAMP(rh == 0 && part == 0, 16);
-    // ---- R3: slot materialisation ---------------------------------------------
-    // Layout: sinks, selected members (newest first: decode deltas from the
-    // tail chunk backwards, then the recency-descending CSR), window, current.
-    const int32_t* members = a.csr.member_positions + (int64_t)graph * a.csr.member_stride;
-    const int32_t* dpos = a.dl.positions + (int64_t)graph * a.dl.position_capacity;
+#pragma unroll
+    for (int h = 0; h < WIN_PER_THREAD; ++h) {
+      const int i = tid + h * SELECT_THREADS;
+      if (i < W) slot_lds[i] = wcomm[h];
+    }
+    CKV_TS(10);
+    __syncthreads();  // fields, marks, totals, window communities
+    CKV_TS(3);
+    const int n_desc = s_max_idx + 1;
+    const int sel_count = s_sel_count;
     const int lane = tid & 63, wave = tid >> 6;
-    // Source of selected member j (0 <= j < sel_count) of descriptor d: a
-    // decode-delta position of the tail chunk, a CSR member, or (slow_d >= 0) a
-    // delta member older than the tail chunk, resolved by walk_chain.
-    auto member_src = [&](int j, int d, const int32_t*& src, bool& gathered, int& slow_d, int& slow_rem) {
-      const int m = j - (d > 0 ? desc_end[d - 1] : 0);
-      const int dc = desc_dc[d];
-      if (m < dc) {
-        const int tn = desc_tn[d];
-        if (m < tn) {
-          const int p = desc_ts[d] + tn - 1 - m;
-          if (p >= 0 && p < a.dl.position_capacity) {
-            src = dpos + p;
-            gathered = true;
-          }
-        } else {
-          slow_d = d;
-          slow_rem = m - tn;
-        }
-      } else {
-        const int64_t idx = (int64_t)desc_lo[d] + (m - dc);
-        if (idx >= 0 && idx < a.csr.member_stride) {
-          src = members + idx;
-          gathered = true;
-        }
-      }
-    };
-    auto walk_chain = [&](int d, int rem, int& val) {
-      const int tail = desc_tl[d];
-      if (tail < 0 || tail >= cpg) return;
-      int ch = a.dl.chunk_previous[cb + tail];
-      for (int guard = 0; guard < 64 && ch >= 0 && ch < cpg; ++guard) {
-        const int cs = a.dl.chunk_size[cb + ch];
-        if (rem < cs) {
-          const int p = a.dl.chunk_start[cb + ch] + cs - 1 - rem;
-          if (p >= 0 && p < a.dl.position_capacity) val = dpos[p];
-          return;
-        }
-        rem -= cs;
-        ch = a.dl.chunk_previous[cb + ch];
-      }
-    };
-    // Window slot i (position cur-W+i), or -1 when that token is already
-    // attended (a sink, or a member of a selected community at or after the
-    // selection's oldest position); wc is the token's community.
-    auto window_pos = [&](int i, int wc, int last_pos) {
-      const int p = cur - W + i;
-      int pos = p < 0 ? -1 : p;
-      if (pos >= 0 && p <= s_sink_max) {
-        for (int k = 0; k < ns; ++k) {
-          if (sink_s[k] == p) pos = -1;
-        }
-      }
-      if (pos >= 0 && p < a.st.token_capacity && wc >= 0 && wc < count) {
-        const int found = comm_desc[wc] == 0xffffu ? -1 : (int)comm_desc[wc];
-        if (found >= 0) {
-          const int take = desc_end[found] - (found > 0 ? desc_end[found - 1] : 0);
-          const bool full = found < n_desc - 1 || take >= s_last_size;
-          if (full || p >= last_pos) pos = -1;
-        }
-      }
-      return pos;
-    };
-    if constexpr (FUSED) {
-      // Each wave below FUSED_TILES resolves the 64 slots of its own tile
-      // (lane = slot); wave FUSED_TILES resolves the last selected slot, whose
-      // position bounds the window, in the same gather round.
+    if (wave < FUSED_TILES) {
+      const int slot_cap = a.ws.slot_capacity;
       const int tile = part * FUSED_TILES + wave;
-      const bool mine = wave < FUSED_TILES && tile < slot_cap / TILE;
-      const int s = wave == FUSED_TILES ? wbeg - 1 : tile * TILE + lane;
+      const int s = tile * TILE + lane;
       const int j = s - ns;
-      const bool sel = (mine || (wave == FUSED_TILES && sel_count > 0)) && j >= 0 && j < sel_count;
+      const int wbeg = ns + sel_count;
+      const int inc = a.cfg.include_current ? 1 : 0;
+      const int32_t* members = a.csr.member_positions + (int64_t)graph * a.csr.member_stride;
+      const int32_t* dpos = a.dl.positions + (int64_t)graph * a.dl.position_capacity;
+      const int mk = marks[wave * TILE + lane];
+      const uint64_t mm = __ballot(mk >= 0);
       const int32_t* src = a.st.community_counts + rh;  // in-bounds dummy address when nothing is gathered
       bool gathered = false;
-      int slow_d = -1, slow_rem = 0;
-      if (sel) {
-        // first descriptor ending after j, between the first descriptors of j's block and the next
-        int lo = blk_first[j >> 6], hi = min(blk_first[(j >> 6) + 1], n_desc - 1);
-        while (lo < hi) {
-          const int mid = (lo + hi) >> 1;
-          if (desc_end[mid] <= j) lo = mid + 1; else hi = mid;
+      int slow_c = -1, slow_rem = 0;
+      // member m (newest first) of community c: a tail-chunk delta, a CSR
+      // member, or (slow_c >= 0) a delta member older than the tail chunk
+      auto member_src_c = [&](int c, int m) {
+        const int dc = f_dc[c];
+        if (m < dc) {
+          const int tn = f_tn[c];
+          if (m < tn) {
+            const int p = f_ts[c] + tn - 1 - m;
+            if (p >= 0 && p < a.dl.position_capacity) {
+              src = dpos + p;
+              gathered = true;
+            }
+          } else {
+            slow_c = c;
+            slow_rem = m - tn;
+          }
+        } else {
+          const int64_t idx = (int64_t)f_lo[c] + (m - dc);
+          if (idx >= 0 && idx < a.csr.member_stride) {
+            src = members + idx;
+            gathered = true;
+          }
         }
-        member_src(j, lo, src, gathered, slow_d, slow_rem);
+      };
+      int kind = 0;  // 1 sink, 2 selected member, 3 window, 4 current
+      int wpos = -1;
+      bool need_last = false;
+      if (tile < slot_cap / TILE) {
+        if (s < ns) {
+          kind = 1;
+        } else if (j < sel_count) {
+          kind = 2;
+          const uint64_t upto = mm & (lane == 63 ? ~0ull : ((2ull << lane) - 1ull));
+          if (upto != 0) {  // always: the community covering a selected slot marks it or an earlier one
+            const int c = marks[wave * TILE + 63 - __builtin_clzll(upto)];
+            member_src_c(c, j - f_st[c]);
+          }
+        } else if (s < wbeg + W) {
+          kind = 3;
+          const int i = s - wbeg;
+          const int p = cur - W + i;
+          wpos = p < 0 ? -1 : p;
+          if (wpos >= 0 && p <= s_sink_max) {
+            for (int q = 0; q < ns; ++q) {
+              if (sink_s[q] == p) wpos = -1;
+            }
+          }
+          const int wc = slot_lds[i];
+          if (wpos >= 0 && p < a.st.token_capacity && wc >= 0 && wc < count && f_st[wc] >= 0) {
+            const int take = min(f_size[wc], cap_sel - f_st[wc]);
+            if (take >= f_size[wc]) {
+              wpos = -1;  // the whole community is attended already
+            } else {
+              // the truncated last community: attended already when at or
+              // after its oldest attended member
+              need_last = true;
+              member_src_c(wc, take - 1);
+            }
+          }
+        } else if (inc && s == wbeg + W) {
+          kind = 4;
+        }
       }
-      CKV_STAMP(rh == 0 && part == 0, 17);
+      CKV_TS(17);
       int val = gload_i32(src);
       if (!gathered) val = -1;
-      if (slow_d >= 0) walk_chain(slow_d, slow_rem, val);
-      if (wave == FUSED_TILES && lane == 0 && sel) s_last_sel_pos = val;
-      __syncthreads();  // s_last_sel_pos
-      CKV_STAMP(rh == 0 && part == 0, 4);
-      if (mine) {
-        if (s < ns) {
-          fused_pos = sink_s[s];
-        } else if (sel) {
-          fused_pos = val;
-        } else if (s < wbeg + W) {
-          const int i = s - wbeg;
-          fused_pos = window_pos(i, slot_lds[i], s_last_sel_pos);
-        } else if (inc && s == wbeg + W) {
-          fused_pos = cur;
+      if (slow_c >= 0) {
+        val = -1;
+        const int tail = f_tl[slow_c];
+        if (tail >= 0 && tail < cpg) {
+          int rem = slow_rem;
+          int ch = a.dl.chunk_previous[cb + tail];
+          for (int guard = 0; guard < 64 && ch >= 0 && ch < cpg; ++guard) {
+            const int cs = a.dl.chunk_size[cb + ch];
+            if (rem < cs) {
+              const int p = a.dl.chunk_start[cb + ch] + cs - 1 - rem;
+              if (p >= 0 && p < a.dl.position_capacity) val = dpos[p];
+              break;
+            }
+            rem -= cs;
+            ch = a.dl.chunk_previous[cb + ch];
+          }
         }
       }
+      if (kind == 1) fused_pos = sink_s[s];
+      else if (kind == 2) fused_pos = val;
+      else if (kind == 3) fused_pos = (need_last && wpos >= val) ? -1 : wpos;
+      else if (kind == 4) fused_pos = cur;
+      CKV_TS(4);
     } else {
-      // Each wave resolves 64-slot blocks of the selection, lane = slot
-      // (coalesced gathers): a lane's descriptor is the block's first descriptor
-      // plus the number of descriptor ends at or before it, read off a wave-wide
-      // bit mask of the ends that fall inside the block (no search chains).
-      const int nblk_sel = (sel_count + 63) / 64;
-      for (int b0 = wave; b0 < nblk_sel; b0 += WAVES * MAT_BATCH) {
-        const int32_t* src[MAT_BATCH];
-        bool gathered[MAT_BATCH];
-        int slow_d[MAT_BATCH], slow_rem[MAT_BATCH];
-#pragma unroll
-        for (int q = 0; q < MAT_BATCH; ++q) {
-          const int b = b0 + q * WAVES;
-          src[q] = a.st.community_counts + rh;  // in-bounds dummy address when nothing is gathered
-          gathered[q] = false;
-          slow_d[q] = -1;
-          slow_rem[q] = 0;
-          if (b < nblk_sel) {  // wave-uniform
-            const int base = 64 * b;
-            const int j = base + lane;
-            const int d0 = blk_first[b];
-            const int e = d0 + lane < n_desc ? desc_end[d0 + lane] : 0x7fffffff;
-            const int off = e - base;
-            const uint64_t mask = wave_or_u64(off >= 1 && off <= 63 ? (1ull << off) : 0ull);
-            const uint64_t below = lane == 63 ? ~0ull : ((2ull << lane) - 1ull);
-            const int d = d0 + __popcll(mask & below);
-            if (j < sel_count) member_src(j, d, src[q], gathered[q], slow_d[q], slow_rem[q]);
-          }
-        }
-        CKV_STAMP(rh == 0 && part == 0 && b0 == 0, 17);
-        int val[MAT_BATCH];
-#pragma unroll
-        for (int q = 0; q < MAT_BATCH; ++q) val[q] = gload_i32(src[q]);
-#pragma unroll
-        for (int q = 0; q < MAT_BATCH; ++q) {
-          if (!gathered[q]) val[q] = -1;
-        }
-#pragma unroll
-        for (int q = 0; q < MAT_BATCH; ++q) {
-          if (slow_d[q] >= 0) walk_chain(slow_d[q], slow_rem[q], val[q]);
-        }
-#pragma unroll
-        for (int q = 0; q < MAT_BATCH; ++q) {
-          const int j = 64 * (b0 + q * WAVES) + lane;
-          if (j < sel_count) {
-            slots[ns + j] = val[q];
-            if (j == sel_count - 1) s_last_sel_pos = val[q];
-          }
-        }
+      // ---- this part's share of the selection outputs (waves without a tile) ----
+      const int ot = tid - FUSED_TILES * 64;
+      const int on = SELECT_THREADS - FUSED_TILES * 64;
+      if (part == 0 && ot == 0) {
+        a.ws.descriptor_counts[rh] = n_desc;
+        a.ws.selected_counts[rh] = sel_count;
       }
-      if (tid < ns) slots[tid] = sink_s[tid];
-      __syncthreads();  // s_last_sel_pos
-      CKV_STAMP(rh == 0 && part == 0, 4);
-      const int last_pos = s_last_sel_pos;
-#pragma unroll
-      for (int h = 0; h < WIN_PER_THREAD; ++h) {
-        const int i = tid + h * SELECT_THREADS;
-        if (i < W) slots[wbeg + i] = window_pos(i, wcomm[h], last_pos);
-      }
-      if (inc && tid == 0) slots[wbeg + W] = cur;
-      for (int s = wbeg + W + inc + tid; s < slot_cap; s += SELECT_THREADS) slots[s] = -1;
-    }
-  }
-  // ---- outputs that nothing in this kernel reads back --------------------------
-  // (fused: split over the head's parts, so no part carries them all, and
-  // written by the waves that attend no tile: their attention buffers lie
-  // past the selection arrays, so the tile waves start attending at once)
-  CKV_STAMP(rh == 0 && part == 0, 11);
-  {
-    const int wp = FUSED ? part : 0, wn = FUSED ? parts : 1;
-    const int ot = FUSED ? tid - 64 * FUSED_TILES : tid;  // index among the writing threads (< 0: none)
-    const int stride = wn * (FUSED ? SELECT_THREADS - 64 * FUSED_TILES : SELECT_THREADS);
-    if (ot == 0 && wp == 0) {
-      a.ws.descriptor_counts[rh] = n_desc;
-      a.ws.selected_counts[rh] = sel_count;
-    }
-    // item i goes to part i % wn (each part writes a strided share)
-    for (int i = wp + wn * ot; ot >= 0 && i < n_desc; i += stride) {
-      a.ws.communities[(int64_t)rh * dcap + i] = desc_comm[i];
-      a.ws.cumulative_ends[(int64_t)rh * dcap + i] = desc_end[i];
-    }
-    for (int t = wp + wn * ot; ot >= 0 && t < a.ws.budget_tiles; t += stride) {
-      // first descriptor ending after the tile's first selected slot (searched
-      // between the first descriptors of its 64-slot block and the next)
-      const int off = max(t * TILE - ns, 0);
-      int lo = n_desc - 1;
-      if (off < sel_count) {
-        lo = blk_first[off >> 6];
-        int hi = min(blk_first[(off >> 6) + 1], n_desc - 1);
-        while (lo < hi) {
-          const int mid = (lo + hi) >> 1;
-          if (desc_end[mid] <= off) lo = mid + 1; else hi = mid;
+      for (int c = part + parts * ot; c < nscore; c += parts * on) {
+        const int st = c < count ? f_st[c] : -1;
+        if (st >= 0) {
+          const int idx = f_idx[c];
+          a.ws.communities[(int64_t)rh * dcap_ + idx] = c;
+          a.ws.cumulative_ends[(int64_t)rh * dcap_ + idx] = min(cap_sel, st + f_size[c]);
         }
+        a.ws.scores[(int64_t)rh * C + c] = c < count ? key16[c] : (uint16_t)0xfc00u;
       }
-      a.ws.tile_descriptors[(int64_t)rh * a.ws.budget_tiles + t] = max(0, min(lo, n_desc - 1));
+      for (int t = part + parts * ot, q = ot; t < a.ws.budget_tiles; t += parts * on, q += on) {
+        const int off = max(t * TILE - ns, 0);
+        a.ws.tile_descriptors[(int64_t)rh * a.ws.budget_tiles + t] = off < sel_count ? td_s[q] : max(0, n_desc - 1);
+      }
+      if (nearest_mode && !COOP && tid == FUSED_TILES * 64 && part == parts - 1) {
+        uint64_t m = ~0ull;
+        for (int w = 0; w < WAVES; ++w) m = near_s[w] < m ? near_s[w] : m;
+        a.ws.nearest[rh] = (m == ~0ull) ? -1 : (int)(m & 0xffffffffu);
+      }
     }
-    if (tid % wn == wp) {
-#pragma unroll
+  } else {
+  // Also marks idx as the first descriptor of every 64-slot block whose first
+    // slot falls in [start, end) (the ranges partition the selection).
+    auto store_desc = [&](int idx, int c, int start, int end, int k) {
+      desc_comm[idx] = c;
+      desc_end[idx] = end;
+      for (int b = (start + 63) >> 6; (b << 6) < end; ++b) blk_first[b] = idx;
+      desc_lo[idx] = o_lo[k];
+      desc_dc[idx] = o_dc[k];
+      desc_tl[idx] = o_tl[k];
+      const bool has = o_dc[k] > 0 && o_tl[k] >= 0 && o_tl[k] < cpg;
+      desc_ts[idx] = has ? o_ts[k] : 0;
+      desc_tn[idx] = has ? o_tn[k] : 0;
+    };
+    {
+      int hc = b4[0], hm = b4[1], ec = b4[2], em = b4[3];
+      int my_max = -1;
+  #pragma unroll
       for (int k = 0; k < OWN; ++k) {
         const int c = c0 + k;
-        if (c < nscore) {
-          const bool live = c < count && o_size[k] > 0;
-          const uint32_t key = o_key[k];
-          const uint16_t bits =
-              live ? (uint16_t)((key & 0x8000u) ? (key ^ 0x8000u) : (key ^ 0xffffu)) : (uint16_t)0xfc00u;
-          a.ws.scores[(int64_t)rh * C + c] = bits;
+        const int size = o_size[k];
+        const bool ok = c < count && size > 0;
+        const bool high = ok && (int)o_key[k] > threshold;
+        const bool eq = ok && threshold >= 0 && (int)o_key[k] == threshold;
+        if (high) {
+          if (hm < cap_tokens && hc < dcap) {
+            store_desc(hc, c, hm, min(cap_tokens, hm + size), k);
+            my_max = max(my_max, hc);  // (a later high-key community has a smaller index than an earlier threshold one)
+          }
+          hc += 1;
+          hm += size;
+        } else if (eq) {
+          const int st0 = high_mass + em;
+          const bool within = budget_mode ? (st0 < sel_slots) : (ec < a.cfg.topk_communities - high_count);
+          const int idx = high_count + ec;
+          if (within && st0 < cap_tokens && idx < dcap) {
+            store_desc(idx, c, st0, min(cap_tokens, st0 + size), k);
+            my_max = max(my_max, idx);
+          }
+          ec += 1;
+          em += size;
+        }
+      }
+      CKV_TS(10);
+      const int wmax = wave_max_i32(my_max);  // one LDS atomic per wave
+      if ((tid & 63) == 0 && wmax >= 0) atomicMax(&s_max_idx, wmax);
+    }
+    __syncthreads();  // descriptors, s_max_idx
+    const int n_desc = s_max_idx + 1;
+    const int sel_count = n_desc > 0 ? desc_end[n_desc - 1] : 0;
+    CKV_TS(15);
+    if (tid == 0) blk_first[(sel_count + 63) / 64] = n_desc;  // (blocks below were marked by store_desc)
+    for (int d = tid; d < n_desc; d += SELECT_THREADS) comm_desc[desc_comm[d]] = (uint16_t)d;
+    // Only the last descriptor can be truncated; remember its community size.
+    if (n_desc > 0) {
+      const int last_c = desc_comm[n_desc - 1];
+      if (last_c / OWN == tid) {
+  #pragma unroll
+        for (int k = 0; k < OWN; ++k) {
+          if (c0 + k == last_c) s_last_size = o_size[k];
         }
       }
     }
-    if (nearest_mode && !COOP && tid == 0 && wp == wn - 1) {
-      uint64_t m = ~0ull;
-      for (int w = 0; w < WAVES; ++w) m = near_s[w] < m ? near_s[w] : m;
-      a.ws.nearest[rh] = (m == ~0ull) ? -1 : (int)(m & 0xffffffffu);
+    if (tid == 0) s_last_sel_pos = -1;
+    CKV_TS(3);
+  
+    const int slot_cap = a.ws.slot_capacity;
+    int32_t* slots = a.ws.slot_positions + (int64_t)rh * slot_cap;
+    const int inc = a.cfg.include_current ? 1 : 0;
+    const int wbeg = ns + sel_count;
+    if (materialise) {
+      __syncthreads();  // blk_first, comm_desc, s_last_size
+      CKV_TS(16);
+      // ---- R3: slot materialisation ---------------------------------------------
+      // Layout: sinks, selected members (newest first: decode deltas from the
+      // tail chunk backwards, then the recency-descending CSR), window, current.
+      const int32_t* members = a.csr.member_positions + (int64_t)graph * a.csr.member_stride;
+      const int32_t* dpos = a.dl.positions + (int64_t)graph * a.dl.position_capacity;
+      const int lane = tid & 63, wave = tid >> 6;
+      // Source of selected member j (0 <= j < sel_count) of descriptor d: a
+      // decode-delta position of the tail chunk, a CSR member, or (slow_d >= 0) a
+      // delta member older than the tail chunk, resolved by walk_chain.
+      auto member_src = [&](int j, int d, const int32_t*& src, bool& gathered, int& slow_d, int& slow_rem) {
+        const int m = j - (d > 0 ? desc_end[d - 1] : 0);
+        const int dc = desc_dc[d];
+        if (m < dc) {
+          const int tn = desc_tn[d];
+          if (m < tn) {
+            const int p = desc_ts[d] + tn - 1 - m;
+            if (p >= 0 && p < a.dl.position_capacity) {
+              src = dpos + p;
+              gathered = true;
+            }
+          } else {
+            slow_d = d;
+            slow_rem = m - tn;
+          }
+        } else {
+          const int64_t idx = (int64_t)desc_lo[d] + (m - dc);
+          if (idx >= 0 && idx < a.csr.member_stride) {
+            src = members + idx;
+            gathered = true;
+          }
+        }
+      };
+      auto walk_chain = [&](int d, int rem, int& val) {
+        const int tail = desc_tl[d];
+        if (tail < 0 || tail >= cpg) return;
+        int ch = a.dl.chunk_previous[cb + tail];
+        for (int guard = 0; guard < 64 && ch >= 0 && ch < cpg; ++guard) {
+          const int cs = a.dl.chunk_size[cb + ch];
+          if (rem < cs) {
+            const int p = a.dl.chunk_start[cb + ch] + cs - 1 - rem;
+            if (p >= 0 && p < a.dl.position_capacity) val = dpos[p];
+            return;
+          }
+          rem -= cs;
+          ch = a.dl.chunk_previous[cb + ch];
+        }
+      };
+      // Window slot i (position cur-W+i), or -1 when that token is already
+      // attended (a sink, or a member of a selected community at or after the
+      // selection's oldest position); wc is the token's community.
+      auto window_pos = [&](int i, int wc, int last_pos) {
+        const int p = cur - W + i;
+        int pos = p < 0 ? -1 : p;
+        if (pos >= 0 && p <= s_sink_max) {
+          for (int k = 0; k < ns; ++k) {
+            if (sink_s[k] == p) pos = -1;
+          }
+        }
+        if (pos >= 0 && p < a.st.token_capacity && wc >= 0 && wc < count) {
+          const int found = comm_desc[wc] == 0xffffu ? -1 : (int)comm_desc[wc];
+          if (found >= 0) {
+            const int take = desc_end[found] - (found > 0 ? desc_end[found - 1] : 0);
+            const bool full = found < n_desc - 1 || take >= s_last_size;
+            if (full || p >= last_pos) pos = -1;
+          }
+        }
+        return pos;
+      };
+      {
+        // Each wave resolves 64-slot blocks of the selection, lane = slot
+        // (coalesced gathers): a lane's descriptor is the block's first descriptor
+        // plus the number of descriptor ends at or before it, read off a wave-wide
+        // bit mask of the ends that fall inside the block (no search chains).
+        const int nblk_sel = (sel_count + 63) / 64;
+        for (int b0 = wave; b0 < nblk_sel; b0 += WAVES * MAT_BATCH) {
+          const int32_t* src[MAT_BATCH];
+          bool gathered[MAT_BATCH];
+          int slow_d[MAT_BATCH], slow_rem[MAT_BATCH];
+  #pragma unroll
+          for (int q = 0; q < MAT_BATCH; ++q) {
+            const int b = b0 + q * WAVES;
+            src[q] = a.st.community_counts + rh;  // in-bounds dummy address when nothing is gathered
+            gathered[q] = false;
+            slow_d[q] = -1;
+            slow_rem[q] = 0;
+            if (b < nblk_sel) {  // wave-uniform
+              const int base = 64 * b;
+              const int j = base + lane;
+              const int d0 = blk_first[b];
+              const int e = d0 + lane < n_desc ? desc_end[d0 + lane] : 0x7fffffff;
+              const int off = e - base;
+              const uint64_t mask = wave_or_u64(off >= 1 && off <= 63 ? (1ull << off) : 0ull);
+              const uint64_t below = lane == 63 ? ~0ull : ((2ull << lane) - 1ull);
+              const int d = d0 + __popcll(mask & below);
+              if (j < sel_count) member_src(j, d, src[q], gathered[q], slow_d[q], slow_rem[q]);
+            }
+          }
+          CKV_TS(17);
+          int val[MAT_BATCH];
+  #pragma unroll
+          for (int q = 0; q < MAT_BATCH; ++q) val[q] = gload_i32(src[q]);
+  #pragma unroll
+          for (int q = 0; q < MAT_BATCH; ++q) {
+            if (!gathered[q]) val[q] = -1;
+          }
+  #pragma unroll
+          for (int q = 0; q < MAT_BATCH; ++q) {
+            if (slow_d[q] >= 0) walk_chain(slow_d[q], slow_rem[q], val[q]);
+          }
+  #pragma unroll
+          for (int q = 0; q < MAT_BATCH; ++q) {
+            const int j = 64 * (b0 + q * WAVES) + lane;
+            if (j < sel_count) {
+              slots[ns + j] = val[q];
+              if (j == sel_count - 1) s_last_sel_pos = val[q];
+            }
+          }
+        }
+        if (tid < ns) slots[tid] = sink_s[tid];
+        __syncthreads();  // s_last_sel_pos
+        CKV_TS(4);
+        const int last_pos = s_last_sel_pos;
+  #pragma unroll
+        for (int h = 0; h < WIN_PER_THREAD; ++h) {
+          const int i = tid + h * SELECT_THREADS;
+          if (i < W) slots[wbeg + i] = window_pos(i, wcomm[h], last_pos);
+        }
+        if (inc && tid == 0) slots[wbeg + W] = cur;
+        for (int s = wbeg + W + inc + tid; s < slot_cap; s += SELECT_THREADS) slots[s] = -1;
+      }
     }
-  }
-  CKV_STAMP(rh == 0 && part == 0, 5);
+    // ---- outputs that nothing in this kernel reads back --------------------------
+    // (fused: split over the head's parts, so no part carries them all, and
+    // written by the waves that attend no tile: their attention buffers lie
+    // past the selection arrays, so the tile waves start attending at once)
+    CKV_TS(11);
+    {
+      const int wp = 0, wn = 1;
+      const int ot = tid;
+      const int stride = SELECT_THREADS;
+      if (ot == 0 && wp == 0) {
+        a.ws.descriptor_counts[rh] = n_desc;
+        a.ws.selected_counts[rh] = sel_count;
+      }
+      // item i goes to part i % wn (each part writes a strided share)
+      for (int i = wp + wn * ot; ot >= 0 && i < n_desc; i += stride) {
+        a.ws.communities[(int64_t)rh * dcap + i] = desc_comm[i];
+        a.ws.cumulative_ends[(int64_t)rh * dcap + i] = desc_end[i];
+      }
+      for (int t = wp + wn * ot; ot >= 0 && t < a.ws.budget_tiles; t += stride) {
+        // first descriptor ending after the tile's first selected slot (searched
+        // between the first descriptors of its 64-slot block and the next)
+        const int off = max(t * TILE - ns, 0);
+        int lo = n_desc - 1;
+        if (off < sel_count) {
+          lo = blk_first[off >> 6];
+          int hi = min(blk_first[(off >> 6) + 1], n_desc - 1);
+          while (lo < hi) {
+            const int mid = (lo + hi) >> 1;
+            if (desc_end[mid] <= off) lo = mid + 1; else hi = mid;
+          }
+        }
+        a.ws.tile_descriptors[(int64_t)rh * a.ws.budget_tiles + t] = max(0, min(lo, n_desc - 1));
+      }
+      if (tid % wn == wp) {
+  #pragma unroll
+        for (int k = 0; k < OWN; ++k) {
+          const int c = c0 + k;
+          if (c < nscore) {
+            const bool live = c < count && o_size[k] > 0;
+            const uint32_t key = o_key[k];
+            const uint16_t bits =
+                live ? (uint16_t)((key & 0x8000u) ? (key ^ 0x8000u) : (key ^ 0xffffu)) : (uint16_t)0xfc00u;
+            a.ws.scores[(int64_t)rh * C + c] = bits;
+          }
+        }
+      }
+      if (nearest_mode && !COOP && tid == 0 && wp == wn - 1) {
+        uint64_t m = ~0ull;
+        for (int w = 0; w < WAVES; ++w) m = near_s[w] < m ? near_s[w] : m;
+        a.ws.nearest[rh] = (m == ~0ull) ? -1 : (int)(m & 0xffffffffu);
+      }
+    }
+}
+  CKV_TS(5);
   if constexpr (FUSED) {
     attend_part<SELECT_THREADS / 64, FUSED_TILES, COOP>(
-        a, rh, part, parts, fused_pos, dyn + fused_select_bytes(C, dcap, a.cfg.max_selected));
+        a, rh, part, parts, fused_pos, dyn + fused_select_bytes(C, a.ws.budget_tiles, parts) CKV_TS_PASS);
   }
+  CKV_TS_FLUSH(rh == 0 && part == 0);
   if constexpr (COOP) coop_finish<PMAX>(a, rh, parts, epoch, nearest_mode, xrow);
 }
 
@@ -1093,8 +1305,8 @@ int fused_parts(const DecodeArgs& a) {
 }
 
 size_t fused_lds_bytes(const DecodeArgs& a) {
-  return fused_slot_bytes(a.ws.slot_capacity) +
-         fused_select_bytes(a.st.community_capacity, a.ws.descriptor_capacity, a.cfg.max_selected) +
+  const int parts = (a.ws.slot_capacity / TILE + FUSED_TILES - 1) / FUSED_TILES;
+  return fused_slot_bytes(a.ws.slot_capacity) + fused_select_bytes(a.st.community_capacity, a.ws.budget_tiles, parts) +
          attend_part_lds_bytes(SELECT_THREADS / 64);
 }
 

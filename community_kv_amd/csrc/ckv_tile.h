@@ -185,7 +185,7 @@ constexpr size_t attend_part_lds_bytes(int waves) {
 // of the launch merges them).
 template <int W, int TP, bool AGENT = false>
 __device__ inline void attend_part(const DecodeArgs& a, const int rh, const int part, const int parts,
-                                   int pos, unsigned char* lds) {
+                                   int pos, unsigned char* lds CKV_TS_ARG) {
   static_assert(TP <= W, "one tile per wave");
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -214,8 +214,7 @@ __device__ inline void attend_part(const DecodeArgs& a, const int rh, const int 
   if (!valid) pos = -1;
   pos_s[lane] = pos;
   const bool any = __ballot(valid) != 0ull;
-  CKV_STAMP(rh == 0 && part == 0, 18);
-  CKV_STAMP(rh == 0 && part == 1, 23);
+  CKV_TS(18);
   const uint4 zero = {0u, 0u, 0u, 0u};
   QOperand qop;
 #pragma unroll
@@ -232,7 +231,7 @@ __device__ inline void attend_part(const DecodeArgs& a, const int rh, const int 
     const TileResult r = mfma_tile<2>(K, V, kvh * a.kv.head_stride, a.kv.token_stride, pos_s, v_s,
                                       want_topk ? cand_s : nullptr, qop, a.cfg.softmax_scale, NEG_INF, o);
     wave_sync();
-    CKV_STAMP(rh == 0 && part == 0, 19);
+    CKV_TS(19);
     if (L == 0 && c16 < G) {
       wm_s[wave * CKV_MAX_GROUP + c16] = r.m;
       wl_s[wave * CKV_MAX_GROUP + c16] = r.l;
@@ -256,7 +255,7 @@ __device__ inline void attend_part(const DecodeArgs& a, const int rh, const int 
     if (in_range) a.ws.slot_positions[(int64_t)rh * a.ws.slot_capacity + slot] = raw_pos;
   }
   __syncthreads();
-  CKV_STAMP(rh == 0 && part == 0, 20);
+  CKV_TS(20);
   // Combine the tile waves into this part's split partial (the other waves hold no tile).
   for (int i = tid; i < G * D; i += 64 * W) {
     const int g = i >> 7;
@@ -296,8 +295,7 @@ __device__ inline void attend_part(const DecodeArgs& a, const int rh, const int 
       *pl = l;
     }
   }
-  CKV_STAMP(rh == 0 && part == 0, 21);
-  CKV_STAMP_MAX(rh == 0, 22);
+  CKV_TS(21);
 }
 
 }  // namespace ckv
