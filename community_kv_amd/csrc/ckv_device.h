@@ -494,6 +494,37 @@ __device__ inline void find_threshold_bin(const int* hist, int target, int* out_
   }
 }
 
+// find_threshold_bin's rule with the result on every lane of the calling
+// wave (every wave of a workgroup may run it on the same histogram, so no
+// barrier is needed to share the result).
+__device__ inline void wave_find_bin(const int* hist, int target, int& out_bin, int& out_above) {
+  const int lane = threadIdx.x & 63;
+  const int b0 = 4 * lane;
+  const int4 h = *reinterpret_cast<const int4*>(hist + b0);
+  const int hs[4] = {h.x, h.y, h.z, h.w};
+  const int prefix = wave_inclusive_scan(h.x + h.y + h.z + h.w);
+  const int total = __builtin_amdgcn_readlane(prefix, 63);
+  int above = total - prefix;
+  int bin = -1, bin_above = 0;
+#pragma unroll
+  for (int i = 3; i >= 0; --i) {
+    if (bin < 0 && above < target && above + hs[i] >= target) {
+      bin = b0 + i;
+      bin_above = above;
+    }
+    above += hs[i];
+  }
+  const uint64_t hit = __ballot(bin >= 0);
+  if (hit == 0) {
+    out_bin = -1;
+    out_above = 0;
+    return;
+  }
+  const int owner = __ffsll((unsigned long long)hit) - 1;
+  out_bin = __builtin_amdgcn_readlane(bin, owner);
+  out_above = __builtin_amdgcn_readlane(bin_above, owner);
+}
+
 // Host-side launchers (one per translation unit), called after validation.
 int launch_score_select(const DecodeArgs& a, hipStream_t stream, const DecodeArgs* pending_update = nullptr);
 int launch_sync_shared(const DecodeArgs& a, hipStream_t stream);

@@ -199,11 +199,12 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
 
   __shared__ float q_s[CKV_MAX_GROUP * D];
   __shared__ float key_s[D];
-  __shared__ int hist[256];
+  __shared__ __align__(16) int hist[256];
+  __shared__ __align__(16) int hist2[256];  // second radix pass (no clearing barrier in between)
   __shared__ __align__(16) int scan_s[4 * WAVES];
   __shared__ uint64_t near_s[WAVES];
   __shared__ int sink_s[CKV_MAX_SINKS];
-  __shared__ int s_bin, s_above, s_max_idx, s_sel_count, s_last_sel_pos, s_last_size, s_sink_max;
+  __shared__ int s_max_idx, s_sel_count, s_last_sel_pos, s_last_size, s_sink_max;
 
   extern __shared__ __align__(16) unsigned char dyn_all[];
   // fused: the window tokens' communities first, then the selection arrays (later the attention buffers)
@@ -334,6 +335,7 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
   if (tid < ns) sink_s[tid] = sink_v;
   if (nearest_mode && tid < D) key_s[tid] = (cur >= 0 && cur < a.kv.capacity) ? key_v : 0.0f;
   hist[tid & 255] = 0;
+  hist2[tid & 255] = 0;
   if (tid == 0) {
     s_max_idx = -1;
     s_sel_count = 0;
@@ -583,28 +585,25 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
   if constexpr (!FUSED) {
     for (int c = tid; c < nscore; c += SELECT_THREADS) comm_desc[c] = 0xffffu;
   }
-  if (tid < 64) find_threshold_bin(hist, target, &s_bin, &s_above);
-  __syncthreads();
+  // Every wave finds the bins itself (same histogram, same result): no
+  // barrier to broadcast them.
+  int hb, above_hb;
+  wave_find_bin(hist, target, hb, above_hb);
   CKV_TS(13);
-  const int hb = s_bin;
   int threshold;  // 16-bit key threshold; -1 selects every non-empty community
   if (hb < 0) {
     threshold = -1;
   } else {
-    const int above_hb = s_above;
-    __syncthreads();
-    hist[tid & 255] = 0;
-    __syncthreads();
 #pragma unroll
     for (int k = 0; k < OWN; ++k) {
       const int c = c0 + k;
       const bool live = c < count && o_size[k] > 0;
-      if (live && (int)(o_key[k] >> 8) == hb) atomicAdd(hist + (o_key[k] & 0xff), budget_mode ? o_size[k] : 1);
+      if (live && (int)(o_key[k] >> 8) == hb) atomicAdd(hist2 + (o_key[k] & 0xff), budget_mode ? o_size[k] : 1);
     }
     __syncthreads();
-    if (tid < 64) find_threshold_bin(hist, target - above_hb, &s_bin, &s_above);
-    __syncthreads();
-    threshold = (hb << 8) | s_bin;
+    int lb, above_lb;
+    wave_find_bin(hist2, target - above_hb, lb, above_lb);
+    threshold = (hb << 8) | lb;
   }
   CKV_TS(2);
 
