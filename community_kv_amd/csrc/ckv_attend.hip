@@ -449,12 +449,12 @@ __device__ __forceinline__ float merge_wide_body(const DecodeArgs& a, const int 
     const float mt = ok ? gload_f32(a.ws.partial_max + j) : NEG_INF;
     const float lt = ok ? gload_f32(a.ws.partial_sum + j) : 0.0f;
     const float M = wave_max(mt);
-    const float sc = mt == NEG_INF ? 0.0f : ckv_expf(mt - M);
+    const float sc = mt == NEG_INF ? 0.0f : __expf(mt - M);
     const float den = wave_sum_tree(sc != 0.0f ? lt * sc : 0.0f);
     if (lane < PRE) sc_s[wave][lane] = sc;
     if (lane == 0) {
       den_s[wave] = den;
-      const float lse = M + ckv_logf(den);
+      const float lse = M + __logf(den);
       if constexpr (DEFER) mo->lse = lse; else a.ws.lse[(int64_t)rh * G + wave] = lse;
       if (wave == 0) lse0_s = lse;
     }

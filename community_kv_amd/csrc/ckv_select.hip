@@ -99,21 +99,24 @@ __device__ __forceinline__ void coop_finish(const DecodeArgs& a, const int rh, c
   const int64_t base = (int64_t)rh * G * parts;
   const int i = min(tid, G * D - 1);
   const float* src = a.ws.partial_acc + (base + (int64_t)(i >> 7) * parts) * D + (i & (D - 1));
+  // the maxima and sums first: their reduction runs while the accumulators arrive
+  const bool ok = wave < G && lane < parts;
+  const int64_t j = base + (int64_t)min(wave, G - 1) * parts + (ok ? lane : 0);
+  const float mt0 = ld_agent_f32(a.ws.partial_max + j);
+  const float lt0 = ld_agent_f32(a.ws.partial_sum + j);
   float v[PMAX];
 #pragma unroll
   for (int k = 0; k < PMAX; ++k) v[k] = ld_agent_f32(src + (int64_t)min(k, parts - 1) * D);
   if (wave < G) {
-    const bool ok = lane < parts;
-    const int64_t j = base + (int64_t)wave * parts + (ok ? lane : 0);
-    const float mt = ok ? ld_agent_f32(a.ws.partial_max + j) : NEG_INF;
-    const float lt = ok ? ld_agent_f32(a.ws.partial_sum + j) : 0.0f;
+    const float mt = ok ? mt0 : NEG_INF;
+    const float lt = ok ? lt0 : 0.0f;
     const float M = wave_max(mt);
-    const float sc = mt == NEG_INF ? 0.0f : ckv_expf(mt - M);
+    const float sc = mt == NEG_INF ? 0.0f : __expf(mt - M);
     const float den = wave_sum_tree(sc != 0.0f ? lt * sc : 0.0f);
     if (lane < PMAX) sc_s[wave][lane] = sc;
     if (lane == 0) {
       den_s[wave] = den;
-      a.ws.lse[(int64_t)rh * G + wave] = M + ckv_logf(den);
+      a.ws.lse[(int64_t)rh * G + wave] = M + __logf(den);
     }
   } else if (nearest_mode && wave == COOP_WAVES - 1) {
     uint64_t m = ~0ull;
@@ -1340,14 +1343,16 @@ int launch_select_attend(const DecodeArgs& a, hipStream_t s, const DecodeArgs* p
   constexpr int OWN_MAX = CKV_MAX_COMMUNITIES / SELECT_THREADS;
   if (coop) {
     if (coop_parts(a) != parts) return limit_error("the cooperative fused launch cannot serve this layer");
-    if (parts <= 32) {
-      return own <= 1 ? launch(select_attend_kernel<CKV_E4M3, CKV_BF16, 1, 32>)
-             : own <= 2 ? launch(select_attend_kernel<CKV_E4M3, CKV_BF16, 2, 32>)
-                        : launch(select_attend_kernel<CKV_E4M3, CKV_BF16, 4, 32>);
-    }
-    return own <= 1 ? launch(select_attend_kernel<CKV_E4M3, CKV_BF16, 1, 64>)
-           : own <= 2 ? launch(select_attend_kernel<CKV_E4M3, CKV_BF16, 2, 64>)
-                      : launch(select_attend_kernel<CKV_E4M3, CKV_BF16, 4, 64>);
+    // the merge loads PMAX accumulators per output element (clamped to the parts)
+    auto by_own = [&](auto k1, auto k2, auto k4) { return own <= 1 ? launch(k1) : own <= 2 ? launch(k2) : launch(k4); };
+    if (parts <= 24)
+      return by_own(select_attend_kernel<CKV_E4M3, CKV_BF16, 1, 24>, select_attend_kernel<CKV_E4M3, CKV_BF16, 2, 24>,
+                    select_attend_kernel<CKV_E4M3, CKV_BF16, 4, 24>);
+    if (parts <= 40)
+      return by_own(select_attend_kernel<CKV_E4M3, CKV_BF16, 1, 40>, select_attend_kernel<CKV_E4M3, CKV_BF16, 2, 40>,
+                    select_attend_kernel<CKV_E4M3, CKV_BF16, 4, 40>);
+    return by_own(select_attend_kernel<CKV_E4M3, CKV_BF16, 1, 64>, select_attend_kernel<CKV_E4M3, CKV_BF16, 2, 64>,
+                  select_attend_kernel<CKV_E4M3, CKV_BF16, 4, 64>);
   }
   if (a.st.centroid_dtype == CKV_E4M3) {
     return own <= 1 ? launch(select_attend_kernel<CKV_E4M3, CKV_BF16, 1>)

@@ -170,23 +170,43 @@ __device__ inline TileResult mfma_tile(const uint16_t* __restrict__ K, const uin
 }
 
 
-// Fused-path attention of one part of a retrieval head's slot table: the first
-// TP of the workgroup's W waves take the part's 64-slot tiles (tile = part * TP
-// + wave; `pos` = the KV position of this lane's slot, -1 for none), run
-// mfma_tile, combine into split partial `part` of `parts` (max, sum,
-// unnormalised P.V per query) and write every slot's position and query-0 score
-// (the candidates of the online update's top-8).
-// `lds` (16-byte aligned) holds attend_part_lds_bytes(W) bytes.
-constexpr size_t attend_part_lds_bytes(int waves) {
-  return (size_t)waves * (V_HALF_ROWS * D * 2 + TILE * 4 + TILE * 4 + 2 * CKV_MAX_GROUP * 4);
-}
-
+// Fused-path attention of one part of a retrieval head's slot table.  The
+// part's TP 64-slot tiles (tile = part * TP + w; `pos` = the KV position of
+// lane l's slot in tile w on the waves w < TP, -1 for none) are spread over
+// all W waves of the workgroup, QROWS = 16 slots each, so that every wave's
+// dependent chain is short: it gathers its 16 K and V rows, computes Q K^T
+// with v_mfma_f32_16x16x32_bf16 (four 32-dim steps; A = K rows, B = Q^T, the
+// accumulator holds query lane % 16 for slots 4 * (lane / 16) + i), the
+// softmax numerators rounded to bf16 (as the reference rounds P before its
+// dot), and P.V with v_mfma_f32_16x16x16_bf16 (A = P straight from that
+// accumulator layout, B = V^T by one transposing LDS read per 16-dim block).
+// The workgroup then combines its W wave partials into split partial `part`
+// (max, sum, unnormalised P.V per query) and writes every slot's position and
+// query-0 score (the candidates of the online update's top-8).
 // AGENT: the split partials are stored with st_agent_f32 (another workgroup
 // of the launch merges them).
+constexpr int QROWS = 16;  // slots per wave in attend_part
+
+// LDS index of element (row, dim) of a 16 x 128 bf16 block whose 16-byte
+// chunks are XOR-swizzled by the row: the transposing reads (four rows of one
+// chunk per lane group) and the row writes are both free of bank conflicts.
+__device__ inline int vq_idx(int row, int dim) { return row * D + ((((dim >> 3) ^ row) & 15) << 3) + (dim & 7); }
+
+__device__ inline f32x4_t mfma_bf16_k16(uint2 a, uint2 b, f32x4_t c) {
+  typedef short s16x4_t __attribute__((ext_vector_type(4)));
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4_t, a), __builtin_bit_cast(s16x4_t, b), c,
+                                                   0, 0, 0);
+}
+
+// `lds` (16-byte aligned) holds attend_part_lds_bytes(W) bytes.
+constexpr size_t attend_part_lds_bytes(int waves) {
+  return (size_t)waves * (QROWS * D * 2 + QROWS * 4 + QROWS * 4 + 2 * CKV_MAX_GROUP * 4);
+}
+
 template <int W, int TP, bool AGENT = false>
 __device__ inline void attend_part(const DecodeArgs& a, const int rh, const int part, const int parts,
                                    int pos, unsigned char* lds CKV_TS_ARG) {
-  static_assert(TP <= W, "one tile per wave");
+  static_assert(W * QROWS == TP * TILE, "the part's tiles are spread over all waves, 16 slots each");
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
@@ -194,27 +214,27 @@ __device__ inline void attend_part(const DecodeArgs& a, const int rh, const int 
   const int c16 = lane & 15;
   const int tiles = a.ws.slot_capacity / TILE;
   const int G = a.cfg.group_size;
-  const int kvh = a.st.retrieval_to_kv[rh];
+  const int64_t kb = (int64_t)a.st.retrieval_to_kv[rh] * a.kv.head_stride;
+  const int64_t ts = a.kv.token_stride;
   const uint16_t* K = reinterpret_cast<const uint16_t*>(a.kv.key);
   const uint16_t* V = reinterpret_cast<const uint16_t*>(a.kv.value);
   const uint16_t* Q = reinterpret_cast<const uint16_t*>(a.kv.query);
-  uint16_t* v_all = reinterpret_cast<uint16_t*>(lds);
-  uint16_t* v_s = v_all + wave * (V_HALF_ROWS * D);
-  float* o_s = reinterpret_cast<float*>(v_s);  // this wave's P.V rows after its tile
-  int* pos_s = reinterpret_cast<int*>(lds + (size_t)W * V_HALF_ROWS * D * 2) + wave * TILE;
-  float* cand_s = reinterpret_cast<float*>(lds + (size_t)W * (V_HALF_ROWS * D * 2 + TILE * 4)) + wave * TILE;
-  float* wm_s = reinterpret_cast<float*>(lds + (size_t)W * (V_HALF_ROWS * D * 2 + 2 * TILE * 4));
+  uint16_t* v_s = reinterpret_cast<uint16_t*>(lds) + wave * (QROWS * D);
+  float* o_s = reinterpret_cast<float*>(v_s);  // this wave's P.V rows after its slots
+  int* pos_all = reinterpret_cast<int*>(lds + (size_t)W * QROWS * D * 2);  // [W * 16]: the part's slots
+  float* cand_all = reinterpret_cast<float*>(pos_all + W * QROWS);
+  float* wm_s = cand_all + W * QROWS;
   float* wl_s = wm_s + W * CKV_MAX_GROUP;
+  const bool want_topk = a.cfg.assignment != CKV_ASSIGN_NONE;
 
-  const int tile = part * TP + wave;
-  const int slot = tile * TILE + lane;
-  const bool in_range = wave < TP && tile < tiles;
-  const int raw_pos = in_range ? pos : -1;
-  const bool valid = in_range && pos >= 0 && pos < a.kv.capacity;
-  if (!valid) pos = -1;
-  pos_s[lane] = pos;
-  const bool any = __ballot(valid) != 0ull;
-  CKV_TS(18);
+  // the tile waves publish their slots' positions (and the slot table)
+  if (wave < TP) {
+    const int tile = part * TP + wave;
+    const bool in_range = tile < tiles;
+    const bool valid = in_range && pos >= 0 && pos < a.kv.capacity;
+    pos_all[wave * TILE + lane] = valid ? pos : -1;
+    if (in_range) a.ws.slot_positions[(int64_t)rh * a.ws.slot_capacity + tile * TILE + lane] = pos;
+  }
   const uint4 zero = {0u, 0u, 0u, 0u};
   QOperand qop;
 #pragma unroll
@@ -222,53 +242,92 @@ __device__ inline void attend_part(const DecodeArgs& a, const int rh, const int 
     const uint4 v = gload16(Q + ((int64_t)rh * G + min(c16, G - 1)) * D + 32 * s + 8 * L);
     qop.s[s] = c16 < G ? v : zero;
   }
+  __syncthreads();
+  CKV_TS(18);
+  // ---- this wave's 16 slots: part slots 16 * wave + r ----
+  const int* pq = pos_all + QROWS * wave;
+  uint4 kreg[4], vreg[4];
+  {
+    const int prow = max(pq[c16], 0);  // masked slots read row 0 and are masked out of the softmax
+#pragma unroll
+    for (int s = 0; s < 4; ++s) kreg[s] = gload16(K + kb + (int64_t)prow * ts + 32 * s + 8 * L);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) vreg[i] = gload16(V + kb + (int64_t)max(pq[4 * i + L], 0) * ts + 8 * c16);
+  }
+  bool ok[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) ok[i] = pq[4 * L + i] >= 0;
+  f32x4_t sacc = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int s = 0; s < 4; ++s) sacc = mfma_bf16(kreg[s], qop.s[s], sacc);
+  const float scale = a.cfg.softmax_scale;
+  float sc[4];
+  float m = NEG_INF;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    sc[i] = ok[i] ? sacc[i] * scale : NEG_INF;
+    m = fmax_exact(m, sc[i]);
+  }
+  if (want_topk && c16 == 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) cand_all[QROWS * wave + 4 * L + i] = sc[i];
+  }
+  m = max_xor16(m);
+  m = max_xor32(m);
+  float p[4];
+  float l = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    p[i] = sc[i] == NEG_INF ? 0.0f : __expf(sc[i] - m);
+    l = l + p[i];
+  }
+  l = add_xor16(l);
+  l = add_xor32(l);
+  const uint2 aop = {pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3])};
+  // V rows to LDS (row 4i + L, dims 8 * c16 .. +7), then P.V per 16-dim block
+#pragma unroll
+  for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(v_s + vq_idx(4 * i + L, 8 * c16)) = vreg[i];
   wave_sync();
-  const bool want_topk = a.cfg.assignment != CKV_ASSIGN_NONE;
-  if (any) {
-    f32x4_t o[8];
+  f32x4_t o[8];
 #pragma unroll
-    for (int nb = 0; nb < 8; ++nb) o[nb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    const TileResult r = mfma_tile<2>(K, V, kvh * a.kv.head_stride, a.kv.token_stride, pos_s, v_s,
-                                      want_topk ? cand_s : nullptr, qop, a.cfg.softmax_scale, NEG_INF, o);
-    wave_sync();
-    CKV_TS(19);
-    if (L == 0 && c16 < G) {
-      wm_s[wave * CKV_MAX_GROUP + c16] = r.m;
-      wl_s[wave * CKV_MAX_GROUP + c16] = r.l;
-    }
+  for (int nb = 0; nb < 8; ++nb) {
+    // lane (L, c16) receives V[4L .. 4L+3][16 nb + c16]
+    const uint2 bop = lds_read_tr16(v_s + vq_idx(4 * L + (c16 >> 2), 16 * nb + 4 * (c16 & 3)));
+    o[nb] = mfma_bf16_k16(aop, bop, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f});
+  }
+  wave_sync();  // every lane's V reads are done before the P.V rows reuse the buffer
+  CKV_TS(19);
+  if (L == 0 && c16 < G) {
+    wm_s[wave * CKV_MAX_GROUP + c16] = m;
+    wl_s[wave * CKV_MAX_GROUP + c16] = l;
+  }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int g = 4 * L + i;
-      if (g < G) {
+  for (int i = 0; i < 4; ++i) {
+    const int g = 4 * L + i;
+    if (g < G) {
 #pragma unroll
-        for (int nb = 0; nb < 8; ++nb) o_s[g * D + 16 * nb + c16] = o[nb][i];
-      }
+      for (int nb = 0; nb < 8; ++nb) o_s[g * D + 16 * nb + c16] = o[nb][i];
     }
-    if (want_topk && in_range) a.ws.slot_scores[(int64_t)rh * a.ws.slot_capacity + slot] = cand_s[lane];
-    if (in_range) a.ws.slot_positions[(int64_t)rh * a.ws.slot_capacity + slot] = raw_pos;
-  } else {
-    if (L == 0 && c16 < G) {
-      wm_s[wave * CKV_MAX_GROUP + c16] = NEG_INF;
-      wl_s[wave * CKV_MAX_GROUP + c16] = 0.0f;
-    }
-    if (want_topk && in_range) a.ws.slot_scores[(int64_t)rh * a.ws.slot_capacity + slot] = NEG_INF;
-    if (in_range) a.ws.slot_positions[(int64_t)rh * a.ws.slot_capacity + slot] = raw_pos;
   }
   __syncthreads();
   CKV_TS(20);
-  // Combine the tile waves into this part's split partial (the other waves hold no tile).
+  if (want_topk && wave < TP) {
+    const int tile = part * TP + wave;
+    if (tile < tiles) a.ws.slot_scores[(int64_t)rh * a.ws.slot_capacity + tile * TILE + lane] = cand_all[wave * TILE + lane];
+  }
+  // Combine the W wave partials into this part's split partial.
   for (int i = tid; i < G * D; i += 64 * W) {
     const int g = i >> 7;
     const int d = i & (D - 1);
     float M = NEG_INF;
 #pragma unroll
-    for (int w = 0; w < TP; ++w) M = fmax_exact(M, wm_s[w * CKV_MAX_GROUP + g]);
+    for (int w = 0; w < W; ++w) M = fmax_exact(M, wm_s[w * CKV_MAX_GROUP + g]);
     float acc = 0.0f;
 #pragma unroll
-    for (int w = 0; w < TP; ++w) {
+    for (int w = 0; w < W; ++w) {
       const float mw = wm_s[w * CKV_MAX_GROUP + g];
       if (mw != NEG_INF) {
-        const float* ow = reinterpret_cast<const float*>(v_all + w * (V_HALF_ROWS * D));
+        const float* ow = reinterpret_cast<const float*>(reinterpret_cast<uint16_t*>(lds) + w * (QROWS * D));
         acc = acc + ow[g * D + d] * __expf(mw - M);
       }
     }
@@ -278,21 +337,21 @@ __device__ inline void attend_part(const DecodeArgs& a, const int rh, const int 
   if (tid < G) {
     float M = NEG_INF;
 #pragma unroll
-    for (int w = 0; w < TP; ++w) M = fmax_exact(M, wm_s[w * CKV_MAX_GROUP + tid]);
-    float l = 0.0f;
+    for (int w = 0; w < W; ++w) M = fmax_exact(M, wm_s[w * CKV_MAX_GROUP + tid]);
+    float lsum = 0.0f;
 #pragma unroll
-    for (int w = 0; w < TP; ++w) {
+    for (int w = 0; w < W; ++w) {
       const float mw = wm_s[w * CKV_MAX_GROUP + tid];
-      if (mw != NEG_INF) l = l + wl_s[w * CKV_MAX_GROUP + tid] * __expf(mw - M);
+      if (mw != NEG_INF) lsum = lsum + wl_s[w * CKV_MAX_GROUP + tid] * __expf(mw - M);
     }
     float* pm = a.ws.partial_max + ((int64_t)rh * G + tid) * parts + part;
     float* pl = a.ws.partial_sum + ((int64_t)rh * G + tid) * parts + part;
     if constexpr (AGENT) {
       st_agent_f32(pm, M);
-      st_agent_f32(pl, l);
+      st_agent_f32(pl, lsum);
     } else {
       *pm = M;
-      *pl = l;
+      *pl = lsum;
     }
   }
   CKV_TS(21);
