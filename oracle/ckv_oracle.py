@@ -19,7 +19,12 @@ Pinning (see tests/test_oracle_*.py):
   * numerics: numpy / torch conversions and numpy.exp / numpy.log;
   * attention: closed-form softmax in float64 (textbook definition) and a
     dense torch SDPA cross-check;
-  * partition fixture builders: reference test known answers.
+  * partition fixture builders: reference test known answers;
+  * scoring (group max, -inf masking, fp16 rounding), nearest-centroid
+    assignment, top-k selection, slot materialisation with the window union
+    and the layer-wise centroid sync: tests/test_oracle_pins.py (exact
+    rational / float64 brute force, brute-force set construction, the
+    reference's materialisation answer, hand-computed sync answers).
 """
 
 from __future__ import annotations
