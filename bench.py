@@ -5,17 +5,20 @@ A step is one decode token through 36 independent Qwen3-8B-shaped attention
 layers (32 query / 8 KV heads, head_dim 128, bf16 KV, 32,768-token context,
 QUERY_GROUP graphs with 512 Zipf(1.1) communities per KV head, 2,048-token
 budget + 128-token recent window, 10 sinks, modularity-gain online update).
-Each layer owns its own KV cache and graph state (4.8 GB in total), so no layer
-finds another's data in the 256 MB Infinity Cache.  The whole step is captured
-in one HIP graph (each layer's online update rides in the next layer's launch,
-the last layer's in the next step's first launch); inputs are resident in HBM
-before timing starts.
+Each layer owns its own KV cache and graph state (4.8 GB in total).  A step is
+captured in a HIP graph (each layer's online update rides in the next layer's
+launch, the last layer's in the next step's first launch); four such graphs
+whose layers read different queries are replayed in rotation, so a layer's
+gathered rows recur only after more than 1 GB of other traffic (the Infinity
+Cache holds 256 MB).  Inputs are resident in HBM before timing starts.
 
-Prints one JSON line: the benchmark contract's fields plus `roofline` (the
-step's dominant kernel, the fused selection + attention launch: algorithmic
-bytes per launch over its graph-timed duration; `traffic` from the committed
-rocprofv3 counter summary when present) and `cpu_baseline` (the numpy oracle
-on one layer, one core).
+Prints one JSON line: the benchmark contract's fields (value = tokens/s over
+the K timed steps), the median and 10th/90th percentile of the per-step event
+times, `roofline` (the step's dominant kernel, the cooperative selection +
+attention + merge launch: algorithmic bytes per launch over its graph-timed
+duration; `traffic` from the committed rocprofv3 counter summary when
+present) and `cpu_baseline` (the numpy oracle on copies of one layer, one
+process per host core).
 """
 
 from __future__ import annotations
@@ -102,10 +105,16 @@ def planted_prefill_inputs(device, seq=PREFILL_SEQ, hq=HQ, hkv=HKV, clusters=PRE
     return q, k, v
 
 
-def build_stack(device, layers, max_decode, seed=0, seq_lens=None, communities=None, budget=BUDGET, window=WINDOW):
+QUERY_SETS = 4  # query variants per layer, replayed in rotation by the timed step
+
+
+def build_stack(device, layers, max_decode, seed=0, seq_lens=None, communities=None, budget=BUDGET, window=WINDOW,
+                query_sets=1):
     """`layers` independent layer states (config 2 by default).  With
     `seq_lens` / `communities` (one entry per layer) the entries are the
-    sequences of a ragged batch instead (config 4)."""
+    sequences of a ragged batch instead (config 4).  Each entry carries
+    `query_sets` decode calls that share the layer's state and workspace but
+    read different queries (each near another random community centre)."""
     cfg = CommunityKVConfig(token_budget=budget, num_sink=SINKS, lam=0.5, aggregation=GraphAggregation.QUERY_GROUP,
                             local_window=window)
     runtime = DecodeRuntime(cfg)
@@ -132,14 +141,18 @@ def build_stack(device, layers, max_decode, seed=0, seq_lens=None, communities=N
         part.community_weight.uniform_(0.5, 2.0, generator=gen)
         part.total_weight.fill_(float(part.community_weight[0].sum()))
         layer = runtime.prepare_partitioned_layer(part)
-        pick = torch.randint(0, comms, (HKV,), device=device, generator=gen)
-        query = (centers[torch.arange(HKV, device=device), pick].repeat_interleave(HQ // HKV, 0)
-                 + 0.5 * torch.randn(HQ, D, device=device, generator=gen)).to(torch.bfloat16).contiguous()
         conv = layer.converted
-        call = layer.workspace.call(query=query, key=key, value=value, csr=conv.csr, state=conv.mutable,
-                                    sink_positions=layer.sink_positions, current_position=conv.current_position,
-                                    softmax_scale=D ** -0.5, lam=cfg.lam)
-        stack.append(dict(layer=layer, query=query, key=key, value=value, call=call, seq=seq))
+        queries, calls = [], []
+        for _ in range(query_sets):
+            pick = torch.randint(0, comms, (HKV,), device=device, generator=gen)
+            query = (centers[torch.arange(HKV, device=device), pick].repeat_interleave(HQ // HKV, 0)
+                     + 0.5 * torch.randn(HQ, D, device=device, generator=gen)).to(torch.bfloat16).contiguous()
+            queries.append(query)
+            calls.append(layer.workspace.call(query=query, key=key, value=value, csr=conv.csr, state=conv.mutable,
+                                              sink_positions=layer.sink_positions,
+                                              current_position=conv.current_position, softmax_scale=D ** -0.5,
+                                              lam=cfg.lam))
+        stack.append(dict(layer=layer, query=queries[0], key=key, value=value, call=calls[0], calls=calls, seq=seq))
     return runtime, stack
 
 
@@ -163,6 +176,22 @@ def time_graph(graph, reps, device):
     stop.record()
     torch.cuda.synchronize(device)
     return start.elapsed_time(stop) / reps  # ms
+
+
+def time_rotation(graphs, steps, device):
+    """Replays graphs[i % len(graphs)] for i < steps between two device
+    synchronisations; returns (mean ms per step over the whole timed region,
+    per-step ms from events around each replay)."""
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    stops = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    torch.cuda.synchronize(device)
+    for i in range(steps):
+        starts[i].record()
+        graphs[i % len(graphs)].replay()
+        stops[i].record()
+    torch.cuda.synchronize(device)
+    per = [a.elapsed_time(b) for a, b in zip(starts, stops)]
+    return starts[0].elapsed_time(stops[-1]) / steps, per
 
 
 def algorithmic_bytes(stack):
@@ -200,73 +229,84 @@ def profiled_traffic():
     return None
 
 
+def cpu_workers():
+    """Host cores the CPU baselines use: the box's CPU share (OMP_NUM_THREADS
+    there), at most os.cpu_count() and at most 16."""
+    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
+    return max(1, min(share, os.cpu_count() or 1, 16))
+
+
+def run_cpu_workers(kind, arrays, seconds):
+    """Runs `kind` of oracle/cpu_bench.py in cpu_workers() single-threaded child
+    processes (numpy + the oracle only; they never touch the GPU) on the
+    arrays saved to a temporary .npz; returns (per-worker results, workers,
+    wall seconds)."""
+    import subprocess
+    import tempfile
+
+    workers = cpu_workers()
+    env = dict(os.environ, OMP_NUM_THREADS="1", OPENBLAS_NUM_THREADS="1", MKL_NUM_THREADS="1",
+               PYTHONPATH=ROOT + os.pathsep + os.environ.get("PYTHONPATH", ""))
+    with tempfile.TemporaryDirectory(prefix="ckv_cpu_") as tmp:
+        path = os.path.join(tmp, "inputs.npz")
+        np.savez(path, **arrays)
+        t0 = time.perf_counter()
+        procs = [subprocess.Popen([sys.executable, "-m", "oracle.cpu_bench", kind, path, str(seconds), str(i),
+                                   str(workers)], stdout=subprocess.PIPE, stderr=subprocess.PIPE, env=env, cwd=ROOT)
+                 for i in range(workers)]
+        outs = []
+        for pr in procs:
+            out, err = pr.communicate(timeout=seconds * 4 + 300)
+            if pr.returncode != 0:
+                raise RuntimeError(f"cpu baseline worker failed: {err.decode()[-2000:]}")
+            outs.append(json.loads(out.decode().strip().splitlines()[-1]))
+        wall = time.perf_counter() - t0
+    return outs, workers, wall
+
+
 def cpu_baseline(entry, seconds=20.0):
-    """Oracle decode step (numpy port of the reference semantics) on one layer's
-    state, single-threaded, for a bounded number of steps."""
-    from threadpoolctl import threadpool_limits
-
-    from oracle import ckv_oracle as co
-
+    """Oracle decode layer-steps (numpy restatement of the reference semantics)
+    on copies of one layer's state, one per host core, for a bounded time."""
     layer = entry["layer"]
     conv = layer.converted
     m = conv.mutable
-    d = m.deltas
     npy = lambda t: t.detach().cpu().numpy().copy()
-    deltas = co.DeltaChunks(*(npy(t) for t in d.tensors()))
-    st = co.LayerState(
-        centroids=npy(m.centroids.view(torch.uint8)), community_sizes=npy(m.community_sizes),
-        community_counts=npy(m.community_counts), community_weight=npy(m.community_weight),
-        total_weight=npy(m.total_weight), token_communities=npy(m.token_communities), deltas=deltas,
-        to_graph=npy(m.retrieval_to_graph), to_kv=npy(m.retrieval_to_kv), member_offsets=npy(conv.csr.member_offsets),
-        member_positions=npy(conv.csr.member_positions), current_position=npy(conv.current_position), fp8=True)
-    q = entry["query"].float().cpu().numpy()
-    k = entry["key"].float().cpu().numpy()
-    v = entry["value"].float().cpu().numpy()
-    params = co.StepParams(group_size=HQ // HKV, num_sink=SINKS, token_budget=BUDGET, local_window=WINDOW)
-    steps = 0
-    t0 = time.perf_counter()
-    with threadpool_limits(limits=1):
-        while True:
-            co.decode_step(st, q, k, v, params)
-            steps += 1
-            el = time.perf_counter() - t0
-            if el >= seconds or steps >= 50:
-                break
-    per_layer_step = el / steps
-    return {"value": 1.0 / (LAYERS * per_layer_step), "unit": "tokens/s", "cores": 1, "kind": "port",
-            "sample": f"{steps} decode layer-steps of one config-2 layer through the numpy oracle "
-                      f"({per_layer_step * 1e3:.1f} ms per layer-step), scaled to 36 layers"}
+    arrays = dict(centroids=npy(m.centroids.view(torch.uint8)), community_sizes=npy(m.community_sizes),
+                  community_counts=npy(m.community_counts), community_weight=npy(m.community_weight),
+                  total_weight=npy(m.total_weight), token_communities=npy(m.token_communities),
+                  to_graph=npy(m.retrieval_to_graph), to_kv=npy(m.retrieval_to_kv),
+                  member_offsets=npy(conv.csr.member_offsets), member_positions=npy(conv.csr.member_positions),
+                  current_position=npy(conv.current_position),
+                  q=entry["query"].float().cpu().numpy(), k=entry["key"].float().cpu().numpy(),
+                  v=entry["value"].float().cpu().numpy(),
+                  params=np.array([HQ // HKV, SINKS, BUDGET, WINDOW, 50], np.int64))
+    for i, t in enumerate(m.deltas.tensors()):
+        arrays[f"d{i}"] = npy(t)
+    outs, workers, wall = run_cpu_workers("decode", arrays, seconds)
+    steps = sum(o["steps"] for o in outs)
+    rate = sum(o["steps"] / o["seconds"] for o in outs)  # layer-steps per second over all cores
+    return {"value": rate / LAYERS, "unit": "tokens/s", "cores": workers, "kind": "port",
+            "sample": f"{steps} decode layer-steps of one config-2 layer through the numpy oracle on {workers} "
+                      f"host cores ({workers / rate * 1e3:.1f} ms per layer-step per core), scaled to 36 layers"}
 
 
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 
 
 def prefill_cpu_baseline(q, k, v, scale, sinks, kappa, seconds):
-    """Oracle prefill rows (numpy, one core) at evenly spaced positions of the
-    same inputs, scaled to the whole prefill by each row's causal length."""
-    from threadpoolctl import threadpool_limits
-
-    from oracle import prefill as op
-
+    """Oracle prefill rows (numpy) at random positions of the same inputs, one
+    worker per host core, scaled to the whole prefill by each row's causal
+    length."""
+    arrays = dict(q=q[0].float().cpu().numpy(), k=k[0].float().cpu().numpy(), v=v[0].float().cpu().numpy(),
+                  params=np.array([scale, sinks, kappa], np.float64))
+    outs, workers, wall = run_cpu_workers("prefill", arrays, seconds)
     S, Hq = q.shape[1], q.shape[2]
-    qn = q[0].float().cpu().numpy()
-    kn = k[0].float().cpu().numpy()
-    vn = v[0].float().cpu().numpy()
-    rng = np.random.default_rng(1)
-    done_cols, n, t0 = 0, 0, time.perf_counter()
-    with threadpool_limits(limits=1):
-        while time.perf_counter() - t0 < seconds and n < 4096:
-            r = int(rng.integers(0, S))
-            h = int(rng.integers(0, Hq))
-            op.prefill_rows(qn, kn, vn, [r], [h], softmax_scale=scale, num_sink=sinks, kappa=kappa)
-            done_cols += r + 1
-            n += 1
-    el = time.perf_counter() - t0
+    cols_per_s = sum(o["cols"] / o["seconds"] for o in outs)
+    rows = sum(o["rows"] for o in outs)
     total_cols = Hq * S * (S + 1) / 2
-    seconds_full = el * total_cols / done_cols
-    return {"value": 1.0 / seconds_full, "unit": "prefills/s", "cores": 1, "kind": "port",
-            "sample": f"{n} random (row, head) pairs of the config-5 prefill through the numpy oracle "
-                      f"({done_cols} score columns in {el:.1f} s), scaled by causal columns to the whole prefill"}
+    return {"value": cols_per_s / total_cols, "unit": "prefills/s", "cores": workers, "kind": "port",
+            "sample": f"{rows} random (row, head) pairs of the config-5 prefill through the numpy oracle on "
+                      f"{workers} host cores, scaled by causal columns to the whole prefill"}
 
 
 def run_prefill(args, device):
@@ -386,25 +426,17 @@ def run_state(args, device):
                      "kernel": "ckv_build_layer_state (8 launches, whole build)", "bytes_per_launch": algorithmic},
     }
     if not args.no_cpu:
-        from oracle import ckv_oracle as co
-
-        ids = labels.cpu().numpy()
-        counts = (ids[:, SINKS:].max(axis=1) + 1).astype(np.int32)
-        kn = keys.float().cpu().numpy()
         group = HQ // HKV
-        ti = tk_idx.cpu().numpy().reshape(HKV, group * rows, STATE_KAPPA)
-        ts = tk_sc.cpu().numpy().reshape(HKV, group * rows, STATE_KAPPA)
         pos = np.tile(np.arange(row0, row0 + rows), group)[None].repeat(HKV, 0)
-        mp = np.arange(HKV, dtype=np.int32)
-        t0 = time.perf_counter()
-        co.build_member_csr(ids, counts, num_sink=SINKS)
-        co.compute_centroids(ids, counts, kn, to_graph=mp, to_kv=mp, num_sink=SINKS, max_decode_tokens=max_decode)
-        sn, dn, wn = co.build_adjacency(ti, ts, pos, seq_len=SEQ, lam=lam)
-        co.init_modularity_state(ids, sn, dn, wn, community_capacity=cap, seq_len=SEQ)
-        sec = time.perf_counter() - t0
-        result["cpu_baseline"] = {"value": sec * 1e6, "unit": "us", "cores": 1, "kind": "port",
-                                  "sample": "the whole layer build (numpy oracle: CSR, centroids, coalesced "
-                                            "adjacency, modularity weights), once"}
+        arrays = dict(ids=labels.cpu().numpy(), keys=keys.float().cpu().numpy(),
+                      tk_idx=tk_idx.cpu().numpy().reshape(HKV, group * rows, STATE_KAPPA),
+                      tk_sc=tk_sc.cpu().numpy().reshape(HKV, group * rows, STATE_KAPPA), pos=pos,
+                      params=np.array([SINKS, max_decode, SEQ, cap], np.int64), lam=np.array([lam], np.float64))
+        outs, workers, wall = run_cpu_workers("state", arrays, 0.0)
+        result["cpu_baseline"] = {"value": wall * 1e6, "unit": "us", "cores": workers, "kind": "port",
+                                  "sample": f"the whole layer build (numpy oracle: CSR, centroids, coalesced adjacency, "
+                                            f"modularity weights), graphs split over {workers} host cores, wall time "
+                                            f"including worker start-up"}
     print(json.dumps(result), flush=True)
 
 
@@ -468,15 +500,12 @@ def run_partition(args, device):
         "roofline": None,
     }
     if not args.no_cpu:
-        from oracle import leiden as L
-
-        one = (src.long() // S) == 0  # graph 0 alone, scaled by the graph count
-        s0, d0, w0 = (t[one].cpu().numpy() for t in (src, dst, w))
-        t0 = time.perf_counter()
-        L.partition_labels(s0, d0, w0, graphs=1, seq_len=S, resolution=1.0, max_inner_iter=iters, seed=0)
-        sec = time.perf_counter() - t0
-        result["cpu_baseline"] = {"value": sec * 1e3 * HKV, "unit": "ms", "cores": 1, "kind": "port",
-                                  "sample": "numpy oracle Leiden + relabel of graph 0 of 8, scaled by 8"}
+        arrays = dict(src=src.long().cpu().numpy(), dst=dst.long().cpu().numpy(), w=w.cpu().numpy(),
+                      params=np.array([S, HKV, iters], np.int64))
+        outs, workers, wall = run_cpu_workers("partition", arrays, 0.0)
+        result["cpu_baseline"] = {"value": wall * 1e3, "unit": "ms", "cores": workers, "kind": "port",
+                                  "sample": f"numpy oracle Leiden + relabel of the 8 graphs, split over {workers} host "
+                                            f"cores, wall time including worker start-up"}
     print(json.dumps(result), flush=True)
 
 
@@ -685,7 +714,7 @@ def main():
         run_batched(args, device)
         return
     max_decode = args.warmup + args.steps + max(5, args.steps // 2) + 17  # every full step appends one token
-    runtime, stack = build_stack(device, args.layers, max_decode)
+    runtime, stack = build_stack(device, args.layers, max_decode, query_sets=QUERY_SETS)
     torch.cuda.synchronize(device)
 
     # whole step: 36 layer transitions in one graph.  Each layer's online update
@@ -696,18 +725,23 @@ def main():
     # step's last, this step's first 35), each before its layer's next
     # selection.  An eager step before the capture leaves the first pending
     # update; the last one is flushed after the timing.
-    def step_carry(pending):
+    # The timed steps rotate over QUERY_SETS captured graphs whose layers read
+    # different queries, so a (layer, query) pair recurs only every
+    # QUERY_SETS steps: 36 x 4 x ~9.4 MB > 1 GB of gathered rows in between,
+    # well beyond the 256 MB Infinity Cache.
+    def step_carry(pending, qs):
         for e in stack:
-            e["call"].decode_after(pending)
-            pending = e["call"]
+            c = e["calls"][qs]
+            c.decode_after(pending)
+            pending = c
         return pending
 
-    carried = step_carry(None)
-    step_graph = capture(lambda: step_carry(carried), device)
-    for _ in range(args.warmup):
-        step_graph.replay()
+    carried = step_carry(None, 0)
+    step_graphs = [capture(lambda qs=qs: step_carry(carried, qs), device) for qs in range(QUERY_SETS)]
+    for i in range(args.warmup):
+        step_graphs[i % QUERY_SETS].replay()
     torch.cuda.synchronize(device)
-    ms = time_graph(step_graph, args.steps, device)
+    ms, step_ms = time_rotation(step_graphs, args.steps, device)
     stack[-1]["call"].update()
     serial_graph = capture(lambda: [e["call"].decode() for e in stack], device)
     serial_graph.replay()
@@ -715,12 +749,14 @@ def main():
     att_bytes, step_bytes, tokens_per_head, centroid_bytes = algorithmic_bytes(stack)
     overflow = sum(int(e["layer"].workspace.update.overflow.sum().item()) for e in stack)
 
-    # the fused selection + attention-partials launch alone (the step's dominant
-    # kernel: it reads the centroids and gathers the KV rows), 36 launches per
-    # replay; the layers' states are left as the timed step left them
-    fused_graph = capture(lambda: [e["call"].select_attend_partials() for e in stack], device)
-    fused_graph.replay()
-    fused_ms = time_graph(fused_graph, max(10, args.steps), device) / len(stack)
+    # the step's dominant kernel alone: the cooperative selection + attention +
+    # merge launch without a pending update, 36 launches per replay, rotating
+    # over the query sets; the layers' states are left as the timed step left them
+    fused_graphs = [capture(lambda qs=qs: [e["calls"][qs].decode_after(None) for e in stack], device)
+                    for qs in range(QUERY_SETS)]
+    for g in fused_graphs:
+        g.replay()
+    fused_ms = time_rotation(fused_graphs, max(12, args.steps), device)[0] / len(stack)
 
     # dense bf16 decode over the same 32k caches (baseline)
     tiles = -(-SEQ // 64)
@@ -779,6 +815,10 @@ def main():
                    "layers": len(stack), "query_heads": HQ, "kv_heads": HKV, "head_dim": D, "context": SEQ,
                    "token_budget": BUDGET, "local_window": WINDOW, "num_sink": SINKS},
         "us_per_step_layer": us_layer,
+        "us_per_step_layer_median": float(np.median(step_ms)) * 1e3 / len(stack),
+        "us_per_step_layer_p10_p90": [float(np.percentile(step_ms, 10)) * 1e3 / len(stack),
+                                      float(np.percentile(step_ms, 90)) * 1e3 / len(stack)],
+        "query_sets": QUERY_SETS,
         "us_per_step_layer_update_inline": serial_ms * 1e3 / len(stack),
         "dense_us_per_step_layer": dense_us_layer,
         "torch_sdpa_us_per_step_layer": sdpa_us_layer,
@@ -790,8 +830,9 @@ def main():
         "overflow_flags": overflow,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": profiled_traffic(),
-                     "kernel": "select_attend_kernel (centroid scoring, selection, slot table in LDS, KV gather, "
-                               "split partials)", "bytes_per_launch": fused_bytes},
+                     "kernel": "select_attend_kernel<2, 0, 1, 24> (cooperative: shared centroid scoring, exact "
+                               "selection, slot resolution, KV gather + MFMA attention, in-launch split merge)",
+                     "bytes_per_launch": fused_bytes},
     }
     if args.copy_probe:
         src = torch.empty(64 << 20, dtype=torch.int32, device=device)

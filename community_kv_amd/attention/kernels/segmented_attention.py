@@ -28,7 +28,8 @@ class SegmentedAttentionWorkspace:
     partial_max: torch.Tensor          # [Hq, tiles] float32
     partial_sum: torch.Tensor          # [Hq, tiles] float32
     partial_acc: torch.Tensor          # [Hq, tiles, 128] float32
-    partial_topk_packed: torch.Tensor  # [R, tiles, 8] uint64 (reference layout, kept for interface parity)
+    partial_topk_packed: torch.Tensor  # [R, tiles, 8] uint64: the reference's shape, as a zero-stride view (no
+                                       # memory): the kernels take the top-8 from slot_scores instead
     slot_scores: torch.Tensor          # [R, slot capacity] float32: first query's score per slot (top-8 candidates)
     output: torch.Tensor               # [Hq, 128]
     lse: torch.Tensor                  # [Hq] float32
@@ -56,7 +57,7 @@ class SegmentedAttentionWorkspace:
             partial_max=torch.empty((heads, tiles), dtype=torch.float32, device=device),
             partial_sum=torch.empty((heads, tiles), dtype=torch.float32, device=device),
             partial_acc=torch.empty((heads, tiles, HEAD_DIM), dtype=torch.float32, device=device),
-            partial_topk_packed=torch.empty((kv_heads, tiles, KAPPA), dtype=torch.uint64, device=device),
+            partial_topk_packed=torch.zeros((), dtype=torch.uint64, device=device).expand(kv_heads, tiles, KAPPA),
             slot_scores=torch.empty((kv_heads, slots), dtype=torch.float32, device=device),
             output=torch.empty((heads, HEAD_DIM), dtype=dtype, device=device),
             lse=torch.empty((heads,), dtype=torch.float32, device=device),
@@ -72,7 +73,7 @@ def segmented_attention(*, query: torch.Tensor, key: torch.Tensor, value: torch.
     """Attention over the slots chosen by the preceding ``score_and_select``
     (which must have been given the same graph state), then the fused update.
     Returns (output, lse, topk_scores, topk_positions)."""
-    retrieval_heads = workspace.partial_topk_packed.shape[0]
+    retrieval_heads = workspace.topk_scores.shape[0]
     if query.shape != (retrieval_heads * workspace.group_size, HEAD_DIM):
         raise ValueError(f"query must have {workspace.group_size} [128] heads per retrieval head")
     if key.ndim != 3 or value.shape != key.shape or key.shape[-1] != HEAD_DIM:

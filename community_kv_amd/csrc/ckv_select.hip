@@ -204,7 +204,7 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
   __shared__ float key_s[D];
   __shared__ __align__(16) int hist[256];
   __shared__ __align__(16) int hist2[256];  // second radix pass (no clearing barrier in between)
-  __shared__ __align__(16) int scan_s[4 * WAVES];
+  __shared__ __align__(16) int scan_s[4 * WAVES * OWN];
   __shared__ uint64_t near_s[WAVES];
   __shared__ int sink_s[CKV_MAX_SINKS];
   __shared__ int s_max_idx, s_sel_count, s_last_sel_pos, s_last_size, s_sink_max;
@@ -294,10 +294,11 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
     }
   }
   const int sink_v = (materialise && ns > 0) ? gload_i32(a.cfg.sink_positions + min(tid, ns - 1)) : -1;
-  const int c0 = tid * OWN;  // first owned community
+  // thread t owns communities t, t + SELECT_THREADS, ...: id order is k, then thread
+  auto cid = [&](int k) { return tid + k * SELECT_THREADS; };
   int o_size[OWN];
 #pragma unroll
-  for (int k = 0; k < OWN; ++k) o_size[k] = gload_i32(a.st.community_sizes + (int64_t)rh * C + min(c0 + k, nscore - 1));
+  for (int k = 0; k < OWN; ++k) o_size[k] = gload_i32(a.st.community_sizes + (int64_t)rh * C + min(cid(k), nscore - 1));
 
   // ---- R1 -------------------------------------------------------------------
   const int cur = a.st.current_position[graph];
@@ -315,7 +316,7 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
   if (materialise) {
 #pragma unroll
     for (int k = 0; k < OWN; ++k) {
-      const int c = min(c0 + k, C - 1);
+      const int c = min(cid(k), C - 1);
       o_lo[k] = gload_i32(a.csr.member_offsets + (int64_t)graph * (C + 1) + c);
       o_dc[k] = gload_i32(a.dl.community_sizes + tbl + c);
       o_tl[k] = gload_i32(a.dl.community_tail + tbl + c);
@@ -502,17 +503,17 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
     uint32_t need = 0;
 #pragma unroll
     for (int k = 0; k < OWN; ++k) {
-      const int c = c0 + k;
+      const int c = cid(k);
       if (c < count && (c < sh0 || c >= sh1)) need |= 1u << k;
     }
     for (int poll = 0; need != 0 && poll < COOP_POLLS; ++poll) {
       uint64_t v[OWN];
 #pragma unroll
-      for (int k = 0; k < OWN; ++k) v[k] = ld_agent_u64(xrow + min(c0 + k, C - 1));
+      for (int k = 0; k < OWN; ++k) v[k] = ld_agent_u64(xrow + min(cid(k), C - 1));
 #pragma unroll
       for (int k = 0; k < OWN; ++k) {
         if (((need >> k) & 1u) && (v[k] & 0xffffffff00000000ull) == tag) {
-          key16[c0 + k] = (uint16_t)v[k];
+          key16[cid(k)] = (uint16_t)v[k];
           need &= ~(1u << k);
         }
       }
@@ -561,7 +562,7 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
   // masks of the R0/R1 fields (R2 fields stay raw until used: masking them here would wait for R2)
 #pragma unroll
   for (int k = 0; k < OWN; ++k) {
-    const int c = c0 + k;
+    const int c = cid(k);
     if (c >= nscore) o_size[k] = 0;
     if (c >= count) {
       o_lo[k] = 0;
@@ -576,7 +577,7 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
   uint32_t o_key[OWN];
 #pragma unroll
   for (int k = 0; k < OWN; ++k) {
-    const int c = c0 + k;
+    const int c = cid(k);
     const bool live = c < count && o_size[k] > 0;
     o_key[k] = live ? ckv_ordered_key16(key16[c]) : 0u;
     if (live) atomicAdd(hist + (o_key[k] >> 8), budget_mode ? o_size[k] : 1);
@@ -599,7 +600,7 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
   } else {
 #pragma unroll
     for (int k = 0; k < OWN; ++k) {
-      const int c = c0 + k;
+      const int c = cid(k);
       const bool live = c < count && o_size[k] > 0;
       if (live && (int)(o_key[k] >> 8) == hb) atomicAdd(hist2 + (o_key[k] & 0xff), budget_mode ? o_size[k] : 1);
     }
@@ -613,42 +614,49 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
   // Compaction, high keys first (id order), then threshold keys (id order): one
   // four-component block scan (high count/mass, threshold count/mass).
   const int cap_tokens = sel_slots;
-  int v4[4] = {0, 0, 0, 0};
-#pragma unroll
-  for (int k = 0; k < OWN; ++k) {
-    const int c = c0 + k;
-    const int size = o_size[k];
-    const bool ok = c < count && size > 0;
-    const bool high = ok && (int)o_key[k] > threshold;
-    const bool eq = ok && threshold >= 0 && (int)o_key[k] == threshold;
-    v4[0] += high ? 1 : 0;
-    v4[1] += high ? size : 0;
-    v4[2] += eq ? 1 : 0;
-    v4[3] += eq ? size : 0;
-  }
-  int b4[4], t4[4];
+  // One scan per ownership round k (the rounds are consecutive id ranges).
+  int b4k[OWN][4], t4[4] = {0, 0, 0, 0};
   {
     const int lane = tid & 63, wave = tid >> 6;
-    int inc[4];
+    int v4[OWN][4], inc[OWN][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) inc[i] = wave_inclusive_scan(v4[i]);
-    if (lane == 63) *reinterpret_cast<int4*>(scan_s + 4 * wave) = int4{inc[0], inc[1], inc[2], inc[3]};
+    for (int k = 0; k < OWN; ++k) {
+      const int c = cid(k);
+      const int size = o_size[k];
+      const bool ok = c < count && size > 0;
+      const bool high = ok && (int)o_key[k] > threshold;
+      const bool eq = ok && threshold >= 0 && (int)o_key[k] == threshold;
+      v4[k][0] = high ? 1 : 0;
+      v4[k][1] = high ? size : 0;
+      v4[k][2] = eq ? 1 : 0;
+      v4[k][3] = eq ? size : 0;
+      if (k > 0 && k * SELECT_THREADS >= count) {  // a round without live communities (uniform)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) inc[k][i] = 0;
+        continue;
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) inc[k][i] = wave_inclusive_scan(v4[k][i]);
+      if (lane == 63)
+        *reinterpret_cast<int4*>(scan_s + 4 * (k * WAVES + wave)) = int4{inc[k][0], inc[k][1], inc[k][2], inc[k][3]};
+    }
     CKV_TS(8);
     __syncthreads();
     CKV_TS(9);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      b4[i] = inc[i] - v4[i];
-      t4[i] = 0;
-    }
+    for (int k = 0; k < OWN; ++k) {
 #pragma unroll
-    for (int w = 0; w < WAVES; ++w) {
-      const int4 x = *reinterpret_cast<const int4*>(scan_s + 4 * w);
-      const int xs[4] = {x.x, x.y, x.z, x.w};
+      for (int i = 0; i < 4; ++i) b4k[k][i] = inc[k][i] - v4[k][i] + t4[i];
+      if (k > 0 && k * SELECT_THREADS >= count) continue;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        if (w < wave) b4[i] += xs[i];
-        t4[i] += xs[i];
+      for (int w = 0; w < WAVES; ++w) {
+        const int4 x = *reinterpret_cast<const int4*>(scan_s + 4 * (k * WAVES + w));
+        const int xs[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if (w < wave) b4k[k][i] += xs[i];
+          t4[i] += xs[i];
+        }
       }
     }
   }
@@ -677,11 +685,11 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
     int* marks = fused_marks(dyn, C);
     int* td_s = marks + FUSED_TILES * TILE;  // this part's tile descriptors (tiles part, part + parts, ...)
     const int dcap_ = a.ws.descriptor_capacity;
-    int hc = b4[0], hm = b4[1], ec = b4[2], em = b4[3];
     int my_max = -1, my_end = 0;
 #pragma unroll
     for (int k = 0; k < OWN; ++k) {
-      const int c = c0 + k;
+      const int c = cid(k);
+      int hc = b4k[k][0], hm = b4k[k][1], ec = b4k[k][2], em = b4k[k][3];
       const int size = o_size[k];
       const bool ok = c < count && size > 0;
       const bool high = ok && (int)o_key[k] > threshold;
@@ -897,11 +905,11 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
       desc_tn[idx] = has ? o_tn[k] : 0;
     };
     {
-      int hc = b4[0], hm = b4[1], ec = b4[2], em = b4[3];
-      int my_max = -1;
+        int my_max = -1;
   #pragma unroll
       for (int k = 0; k < OWN; ++k) {
-        const int c = c0 + k;
+        const int c = cid(k);
+        int hc = b4k[k][0], hm = b4k[k][1], ec = b4k[k][2], em = b4k[k][3];
         const int size = o_size[k];
         const bool ok = c < count && size > 0;
         const bool high = ok && (int)o_key[k] > threshold;
@@ -938,10 +946,10 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
     // Only the last descriptor can be truncated; remember its community size.
     if (n_desc > 0) {
       const int last_c = desc_comm[n_desc - 1];
-      if (last_c / OWN == tid) {
+      if (last_c % SELECT_THREADS == tid) {
   #pragma unroll
         for (int k = 0; k < OWN; ++k) {
-          if (c0 + k == last_c) s_last_size = o_size[k];
+          if (cid(k) == last_c) s_last_size = o_size[k];
         }
       }
     }
@@ -1122,7 +1130,7 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
       if (tid % wn == wp) {
   #pragma unroll
         for (int k = 0; k < OWN; ++k) {
-          const int c = c0 + k;
+          const int c = cid(k);
           if (c < nscore) {
             const bool live = c < count && o_size[k] > 0;
             const uint32_t key = o_key[k];
