@@ -1,52 +1,69 @@
-"""Decode-time graph state layouts (reference: community_kv/graph/state.py:15-349).
+"""Decode-time graph state (reference data contract: community_kv/graph/state.py:15-349).
 
-The field names, dtypes and shapes are the reference's data contract: the HIP
-kernels read and mutate exactly these tensors in place.  ``validate`` runs once
-when a layer is prepared, never inside the decode step (the reference validated
-on every step, with device-to-host syncs: graph/state.py:319-324).
+The field names, dtypes and shapes are the reference's: the partitioner
+produces these tensors and the HIP kernels read and mutate them in place.
+Each class states its layout once, as a table of (field, dtypes, dimension
+names); ``validate`` checks every field against the table, binding each
+dimension name to the first extent it meets, so two fields that share a name
+must agree.  Validation runs once when a layer is prepared, never inside the
+decode step.
 """
 
 from __future__ import annotations
 
-from dataclasses import dataclass
+from dataclasses import dataclass, fields
 
 import torch
 
+I32 = (torch.int32,)
+F32 = (torch.float32,)
 
-def _require_int32(name: str, value: torch.Tensor) -> None:
-    if value.dtype != torch.int32:
-        raise TypeError(f"{name} must use torch.int32")
+
+def _check_layout(obj, layout, dims: dict[str, int] | None = None) -> dict[str, int]:
+    """Checks each (field, dtypes, dimension names) of ``layout`` on ``obj``;
+    returns the bound extents.  A None entry in the names skips that dimension."""
+    dims = {} if dims is None else dims
+    kind = type(obj).__name__
+    for name, dtypes, names in layout:
+        t = getattr(obj, name)
+        if t.dtype not in dtypes:
+            raise TypeError(f"{kind}.{name} has dtype {t.dtype}; expected {' or '.join(map(str, dtypes))}")
+        if t.ndim != len(names):
+            raise ValueError(f"{kind}.{name} has rank {t.ndim}; expected {len(names)} ({', '.join(map(str, names))})")
+        for axis, dim in enumerate(names):
+            if dim is None:
+                continue
+            extent = int(t.shape[axis])
+            if dims.setdefault(dim, extent) != extent:
+                raise ValueError(f"{kind}.{name} dimension {axis} is {extent}, but {dim} is {dims[dim]} elsewhere")
+    return dims
 
 
 @dataclass(slots=True)
 class PrefillCSR:
-    """Immutable community -> prefill-position index, newest position first."""
+    """Immutable community -> prefill positions index (each row newest first)."""
 
     member_offsets: torch.Tensor     # [graphs, community_capacity + 1]
     member_positions: torch.Tensor   # [graphs, members]
     community_counts: torch.Tensor   # [graphs]
 
+    LAYOUT = (("member_offsets", I32, ("graphs", "offsets")),
+              ("member_positions", I32, ("graphs", "members")),
+              ("community_counts", I32, ("graphs",)))
+
     def validate(self) -> None:
-        _require_int32("member_offsets", self.member_offsets)
-        _require_int32("member_positions", self.member_positions)
-        _require_int32("community_counts", self.community_counts)
-        if self.member_offsets.ndim != 2 or self.member_positions.ndim != 2:
-            raise ValueError("member offsets and positions must be rank two")
-        if self.community_counts.shape != (self.member_offsets.shape[0],):
-            raise ValueError("community_counts must have one entry per graph")
-        if self.member_positions.shape[0] != self.member_offsets.shape[0]:
-            raise ValueError("member_positions must have one row per graph")
-        offsets = self.member_offsets.to(device="cpu", dtype=torch.int64)
-        counts = self.community_counts.to(device="cpu", dtype=torch.int64)
-        for graph in range(offsets.shape[0]):
-            count = int(counts[graph])
-            if count < 0 or count + 1 > offsets.shape[1]:
-                raise ValueError("community count exceeds offset capacity")
-            row = offsets[graph, : count + 1]
-            if int(row[0]) != 0 or bool(torch.any(row[1:] < row[:-1])):
-                raise ValueError("active CSR offsets must start at zero and be monotonic")
-            if int(row[-1]) > self.member_positions.shape[1]:
-                raise ValueError("CSR offsets exceed member-position capacity")
+        dims = _check_layout(self, self.LAYOUT)
+        offsets = self.member_offsets.to("cpu", torch.int64)
+        counts = self.community_counts.to("cpu", torch.int64).tolist()
+        for graph, count in enumerate(counts):
+            if not 0 <= count < dims["offsets"]:
+                raise ValueError(f"graph {graph}: {count} active communities do not fit {dims['offsets'] - 1} offsets")
+            active = offsets[graph, : count + 1]
+            steps = active[1:] - active[:-1]
+            if int(active[0]) != 0 or bool((steps < 0).any()):
+                raise ValueError(f"graph {graph}: active CSR offsets must start at 0 and never decrease")
+            if int(active[-1]) > dims["members"]:
+                raise ValueError(f"graph {graph}: CSR offsets reach {int(active[-1])} of {dims['members']} members")
 
     @property
     def graph_count(self) -> int:
@@ -57,28 +74,22 @@ class PrefillCSR:
         return self.member_offsets.shape[1] - 1
 
     def members(self, graph: int, community: int) -> torch.Tensor:
-        if graph < 0 or graph >= self.graph_count:
+        """Prefill members of one active community, newest first."""
+        if not 0 <= graph < self.graph_count:
             raise IndexError("graph is outside the CSR")
-        count = int(self.community_counts[graph])
-        if community < 0 or community >= count:
+        if not 0 <= community < int(self.community_counts[graph]):
             raise IndexError("community is outside the active CSR")
-        start = int(self.member_offsets[graph, community])
-        end = int(self.member_offsets[graph, community + 1])
-        return self.member_positions[graph, start:end]
-
-
-_DELTA_FIELDS = (
-    "positions", "chunk_start", "chunk_capacity", "chunk_size", "chunk_next", "chunk_previous",
-    "community_head", "community_tail", "community_sizes", "next_free_chunk", "next_free_position",
-)
+        lo, hi = (int(x) for x in self.member_offsets[graph, community:community + 2])
+        return self.member_positions[graph, lo:hi]
 
 
 @dataclass(slots=True)
 class DecodeDeltaChunks:
-    """Single-writer geometric chunk chains of decode-assigned positions.
+    """Per-graph pools of decode-assigned positions, chained per community.
 
-    Chunk capacities of one community double (1, 2, 4, ...), so a community with
-    n decode members has at most log2(n) + 1 chunks.
+    A community's chunks double in capacity (1, 2, 4, ...), so n decode members
+    take at most log2(n) + 1 chunks; every append touches only its own
+    community's tail chunk (one writer per graph: the graph's owner head).
     """
 
     positions: torch.Tensor          # [graphs, 2 * max_decode_tokens]
@@ -93,30 +104,28 @@ class DecodeDeltaChunks:
     next_free_chunk: torch.Tensor    # [graphs]
     next_free_position: torch.Tensor
 
+    LAYOUT = (("positions", I32, ("graphs", "position_pool")),
+              *((name, I32, ("graphs", "chunks")) for name in
+                ("chunk_start", "chunk_capacity", "chunk_size", "chunk_next", "chunk_previous")),
+              *((name, I32, ("graphs", "communities")) for name in
+                ("community_head", "community_tail", "community_sizes")),
+              ("next_free_chunk", I32, ("graphs",)),
+              ("next_free_position", I32, ("graphs",)))
+
     @classmethod
     def allocate(cls, *, graph_count: int, community_capacity: int, max_decode_tokens: int,
                  device: torch.device | str = "cpu") -> "DecodeDeltaChunks":
         if min(graph_count, community_capacity, max_decode_tokens) <= 0:
-            raise ValueError("all capacities must be positive")
-        chunks = (graph_count, max_decode_tokens)
-        table = (graph_count, community_capacity)
-
-        def full(shape, value):
-            return torch.full(shape, value, dtype=torch.int32, device=device)
-
-        return cls(
-            positions=full((graph_count, 2 * max_decode_tokens), -1),
-            chunk_start=full(chunks, -1),
-            chunk_capacity=full(chunks, 0),
-            chunk_size=full(chunks, 0),
-            chunk_next=full(chunks, -1),
-            chunk_previous=full(chunks, -1),
-            community_head=full(table, -1),
-            community_tail=full(table, -1),
-            community_sizes=full(table, 0),
-            next_free_chunk=full((graph_count,), 0),
-            next_free_position=full((graph_count,), 0),
-        )
+            raise ValueError("graph count, community capacity and decode tokens must all be positive")
+        extent = {"position_pool": 2 * max_decode_tokens, "chunks": max_decode_tokens,
+                  "communities": community_capacity}
+        unset = {"positions": -1, "chunk_start": -1, "chunk_next": -1, "chunk_previous": -1,
+                 "community_head": -1, "community_tail": -1}
+        made = {}
+        for name, _, names in cls.LAYOUT:
+            shape = tuple(graph_count if d == "graphs" else extent[d] for d in names)
+            made[name] = torch.full(shape, unset.get(name, 0), dtype=torch.int32, device=device)
+        return cls(**made)
 
     @property
     def graph_count(self) -> int:
@@ -135,87 +144,69 @@ class DecodeDeltaChunks:
         return self.community_head.shape[1]
 
     def tensors(self) -> tuple[torch.Tensor, ...]:
-        return tuple(getattr(self, name) for name in _DELTA_FIELDS)
+        """The fields in declaration order (the C ABI's order)."""
+        return tuple(getattr(self, f.name) for f in fields(self))
 
     def validate(self) -> None:
-        for name in _DELTA_FIELDS:
-            _require_int32(name, getattr(self, name))
-            if not getattr(self, name).is_contiguous():
-                raise ValueError(f"{name} must be contiguous")
-        if self.positions.ndim != 2 or self.chunk_start.ndim != 2:
-            raise ValueError("delta position and chunk pools must be rank two")
-        graphs = self.positions.shape[0]
-        if self.chunk_start.shape[0] != graphs or min(self.positions.shape[1:]) <= 0:
-            raise ValueError("delta pool capacities must be positive")
-        for value in (self.chunk_capacity, self.chunk_size, self.chunk_next, self.chunk_previous):
-            if value.shape != self.chunk_start.shape:
-                raise ValueError("chunk metadata shapes must match")
-        if self.community_head.ndim != 2:
-            raise ValueError("community chunk tables must be rank two")
-        if self.community_head.shape != self.community_tail.shape:
-            raise ValueError("community head and tail tables must match")
-        if self.community_head.shape != self.community_sizes.shape:
-            raise ValueError("community chunk tables and sizes must match")
-        if self.community_head.shape[0] != graphs:
-            raise ValueError("community chunk tables must match graph count")
-        if self.next_free_chunk.shape != (graphs,):
-            raise ValueError("next_free_chunk must have one entry per graph")
-        if self.next_free_position.shape != (graphs,):
-            raise ValueError("next_free_position must have one entry per graph")
+        dims = _check_layout(self, self.LAYOUT)
+        if min(dims["position_pool"], dims["chunks"]) <= 0:
+            raise ValueError("the delta position and chunk pools must not be empty")
+        loose = [f.name for f in fields(self) if not getattr(self, f.name).is_contiguous()]
+        if loose:
+            raise ValueError(f"delta fields must be contiguous: {loose}")
+
+    def _open_chunk(self, graph: int, community: int, after: int, capacity: int) -> int:
+        """Takes the graph's next free chunk (and `capacity` pool slots) and
+        links it behind chunk `after` (-1: the community's first)."""
+        chunk = int(self.next_free_chunk[graph])
+        start = int(self.next_free_position[graph])
+        if chunk >= self.chunk_capacity_per_graph:
+            raise RuntimeError(f"graph {graph}: all {self.chunk_capacity_per_graph} decode-delta chunks are in use")
+        if start + capacity > self.position_capacity:
+            raise RuntimeError(f"graph {graph}: the decode-delta position pool is full")
+        self.next_free_chunk[graph] = chunk + 1
+        self.next_free_position[graph] = start + capacity
+        self.chunk_start[graph, chunk] = start
+        self.chunk_capacity[graph, chunk] = capacity
+        self.chunk_previous[graph, chunk] = after
+        (self.community_head if after < 0 else self.chunk_next)[graph, community if after < 0 else after] = chunk
+        self.community_tail[graph, community] = chunk
+        return chunk
 
     def append(self, graph: int, community: int, position: int) -> None:
-        """Host-side append (one writer per graph); the device update kernel
-        performs the same transition."""
-        if graph < 0 or graph >= self.graph_count:
-            raise IndexError("graph is outside the delta store")
-        if community < 0 or community >= self.community_capacity:
-            raise IndexError("community is outside the delta store")
+        """Host-side append; the device update kernel makes the same transition."""
+        if not 0 <= graph < self.graph_count:
+            raise IndexError(f"graph {graph} is outside the delta store")
+        if not 0 <= community < self.community_capacity:
+            raise IndexError(f"community {community} is outside the delta store")
         tail = int(self.community_tail[graph, community])
-        size = int(self.chunk_size[graph, tail]) if tail >= 0 else 0
-        cap = int(self.chunk_capacity[graph, tail]) if tail >= 0 else 0
-        if tail < 0 or size == cap:
-            chunk = int(self.next_free_chunk[graph])
-            new_cap = 1 if tail < 0 else 2 * cap
-            start = int(self.next_free_position[graph])
-            if chunk >= self.chunk_capacity_per_graph:
-                raise RuntimeError("decode-delta chunk capacity exhausted")
-            if start + new_cap > self.position_capacity:
-                raise RuntimeError("decode-delta position capacity exhausted")
-            self.next_free_chunk[graph] = chunk + 1
-            self.next_free_position[graph] = start + new_cap
-            self.chunk_start[graph, chunk] = start
-            self.chunk_capacity[graph, chunk] = new_cap
-            self.chunk_previous[graph, chunk] = tail
-            if tail < 0:
-                self.community_head[graph, community] = chunk
-            else:
-                self.chunk_next[graph, tail] = chunk
-            self.community_tail[graph, community] = chunk
-            tail, size = chunk, 0
-        self.positions[graph, int(self.chunk_start[graph, tail]) + size] = position
-        self.chunk_size[graph, tail] = size + 1
+        if tail < 0:
+            tail = self._open_chunk(graph, community, -1, 1)
+        elif int(self.chunk_size[graph, tail]) == int(self.chunk_capacity[graph, tail]):
+            tail = self._open_chunk(graph, community, tail, 2 * int(self.chunk_capacity[graph, tail]))
+        fill = int(self.chunk_size[graph, tail])
+        self.positions[graph, int(self.chunk_start[graph, tail]) + fill] = position
+        self.chunk_size[graph, tail] = fill + 1
         self.community_sizes[graph, community] += 1
 
     def members(self, graph: int, community: int) -> torch.Tensor:
-        """Decode members of a community, oldest first."""
-        size = int(self.community_sizes[graph, community])
-        out = torch.empty((size,), dtype=torch.int32, device=self.positions.device)
+        """Decode members of a community in append order (oldest first)."""
+        parts = []
         chunk = int(self.community_head[graph, community])
-        cursor = 0
-        while chunk >= 0 and cursor < size:
-            n = int(self.chunk_size[graph, chunk])
+        while chunk >= 0:
             start = int(self.chunk_start[graph, chunk])
-            out[cursor:cursor + n] = self.positions[graph, start:start + n]
-            cursor += n
+            parts.append(self.positions[graph, start:start + int(self.chunk_size[graph, chunk])])
             chunk = int(self.chunk_next[graph, chunk])
-        if cursor != size:
-            raise RuntimeError("decode-delta chunk chain ended early")
+        out = torch.cat(parts) if parts else self.positions.new_empty((0,))
+        if out.numel() != int(self.community_sizes[graph, community]):
+            raise RuntimeError(f"graph {graph}, community {community}: the chunk chain holds {out.numel()} of "
+                               f"{int(self.community_sizes[graph, community])} members")
         return out
 
 
 @dataclass(slots=True)
 class MutableGraphState:
-    """Graph and centroid state mutated once per layer and decode token."""
+    """Graph and centroid state that every decode token updates."""
 
     centroids: torch.Tensor           # [retrieval heads, C, 128] float8_e4m3fn (or float32)
     community_sizes: torch.Tensor     # [retrieval heads, C] int32
@@ -226,6 +217,15 @@ class MutableGraphState:
     deltas: DecodeDeltaChunks
     retrieval_to_graph: torch.Tensor  # [retrieval heads] int32
     retrieval_to_kv: torch.Tensor     # [retrieval heads] int32
+
+    LAYOUT = (("centroids", (torch.float8_e4m3fn, torch.float32), ("heads", "communities", None)),
+              ("community_sizes", I32, ("heads", "communities")),
+              ("community_counts", I32, ("heads",)),
+              ("community_weight", F32, ("graphs", "communities")),
+              ("total_weight", F32, ("graphs",)),
+              ("token_communities", I32, ("graphs", None)),
+              ("retrieval_to_graph", I32, ("heads",)),
+              ("retrieval_to_kv", I32, ("heads",)))
 
     @property
     def graph_count(self) -> int:
@@ -243,53 +243,24 @@ class MutableGraphState:
     def head_dim(self) -> int:
         return self.centroids.shape[2]
 
+    def _tensors(self) -> list[torch.Tensor]:
+        return [getattr(self, name) for name, _, _ in self.LAYOUT] + list(self.deltas.tensors())
+
     def validate(self) -> None:
-        if self.centroids.ndim != 3:
-            raise ValueError("centroids must have shape [graphs, communities, dim]")
-        if self.centroids.dtype not in (torch.float8_e4m3fn, torch.float32):
-            raise TypeError("centroids must use FP8 E4M3 (or float32)")
-        heads, capacity, _ = self.centroids.shape
-        graphs = self.graph_count
-        if self.community_sizes.shape != (heads, capacity):
-            raise ValueError("community_sizes must match centroid rows")
-        _require_int32("community_sizes", self.community_sizes)
-        if self.community_counts.shape != (heads,):
-            raise ValueError("community_counts must have one entry per retrieval head")
-        _require_int32("community_counts", self.community_counts)
-        if self.community_weight.shape != (graphs, capacity):
-            raise ValueError("community_weight must have one row per graph")
-        if self.community_weight.dtype != torch.float32:
-            raise TypeError("community_weight must use float32")
-        if self.total_weight.shape != (graphs,):
-            raise ValueError("total_weight must have one entry per graph")
-        if self.total_weight.dtype != torch.float32:
-            raise TypeError("total_weight must use float32")
-        if self.token_communities.ndim != 2 or self.token_communities.shape[0] != graphs:
-            raise ValueError("token_communities must have one row per graph")
-        _require_int32("token_communities", self.token_communities)
+        dims = _check_layout(self, self.LAYOUT)
         self.deltas.validate()
-        if self.deltas.graph_count != graphs:
-            raise ValueError("delta pages must match graph count")
-        if self.deltas.community_capacity != capacity:
-            raise ValueError("delta pages must match community capacity")
-        for name in ("retrieval_to_graph", "retrieval_to_kv"):
-            mapping = getattr(self, name)
-            _require_int32(name, mapping)
-            if mapping.shape != (heads,):
-                raise ValueError(f"{name} must have one entry per retrieval head")
-        to_graph = self.retrieval_to_graph.cpu()
-        if int(to_graph.min()) < 0 or int(to_graph.max()) >= graphs or int(self.retrieval_to_kv.min()) < 0:
-            raise ValueError("retrieval mapping index is out of bounds")
-        for r in range(heads):
-            g = int(to_graph[r])
-            if int(to_graph[g]) != g:
-                raise ValueError("every graph must be owned by the retrieval head with its index")
-        device = self.centroids.device
-        tensors = (self.community_sizes, self.community_counts, self.community_weight, self.total_weight,
-                   self.token_communities, self.retrieval_to_graph, self.retrieval_to_kv, *self.deltas.tensors())
-        if any(t.device != device for t in tensors):
-            raise ValueError("all mutable graph tensors must share one device")
-        if any(not t.is_contiguous() for t in (self.centroids, *tensors)):
+        # the delta store is indexed by graph and community like the tables above
+        _check_layout(self.deltas, (("community_sizes", I32, ("graphs", "communities")),), dims)
+        to_graph = self.retrieval_to_graph.cpu().tolist()
+        if any(not 0 <= g < dims["graphs"] for g in to_graph) or int(self.retrieval_to_kv.min()) < 0:
+            raise ValueError(f"retrieval head mappings point outside the {dims['graphs']} graphs / KV heads")
+        owners = [g for g in to_graph if to_graph[g] != g]
+        if owners:
+            raise ValueError(f"graph {owners[0]} is not owned by the retrieval head of the same index")
+        tensors = self._tensors()
+        if len({t.device for t in tensors}) != 1:
+            raise ValueError("the graph state spans several devices")
+        if not all(t.is_contiguous() for t in tensors):
             raise ValueError("graph state tensors must be contiguous")
 
 

@@ -26,12 +26,16 @@ ATTENTION_TILE = 64
 
 
 def _effective_token_budget(*, configured_budget: int, prefill_seq_len: int, num_sink: int) -> int:
-    """Largest whole-tile budget the prefill can fill exactly (runtime.py:22-34)."""
-    available = ((prefill_seq_len + 1) // ATTENTION_TILE) * ATTENTION_TILE
-    effective = min(configured_budget, available)
-    if effective <= num_sink + 1:
-        raise ValueError("prefill sequence is too short for the fixed 64-token decode kernel")
-    return effective
+    """The decode budget a prompt can fill exactly (reference runtime.py:22-34):
+    the configured budget, capped at the whole 64-slot tiles that the prompt
+    plus the current token cover.  Raises when no selected slot would remain
+    after the sinks and the current token."""
+    whole_tiles = (prefill_seq_len + 1) // ATTENTION_TILE
+    budget = min(configured_budget, whole_tiles * ATTENTION_TILE)
+    if budget - num_sink - 1 <= 0:
+        raise ValueError(f"a {prefill_seq_len}-token prefill is too short for the fixed 64-token decode kernel "
+                         f"with {num_sink} sinks (budget {budget})")
+    return budget
 
 
 @dataclass(slots=True)
@@ -55,18 +59,19 @@ class DecodeLayerState:
     sink_positions: torch.Tensor
 
 
-def _pad_member_offsets(member_offsets: torch.Tensor, *, community_capacity: int) -> torch.Tensor:
-    if member_offsets.dtype != torch.int32 or member_offsets.ndim != 2:
-        raise TypeError("member_offsets must be a rank-two int32 tensor")
-    width = community_capacity + 1
-    if member_offsets.shape[1] > width:
-        raise ValueError("member offsets exceed centroid community capacity")
-    if member_offsets.shape[1] == width:
+def _offsets_for_capacity(member_offsets: torch.Tensor, community_capacity: int) -> torch.Tensor:
+    """CSR offsets widened to community_capacity + 1 columns: communities that
+    decode creates later start empty, at the last prefill offset."""
+    if member_offsets.ndim != 2 or member_offsets.dtype != torch.int32:
+        raise TypeError(f"member_offsets must be an int32 [graphs, communities + 1] tensor, got "
+                        f"{member_offsets.dtype} of rank {member_offsets.ndim}")
+    extra = community_capacity + 1 - member_offsets.shape[1]
+    if extra < 0:
+        raise ValueError(f"member_offsets has {member_offsets.shape[1] - 1} communities, more than the "
+                         f"{community_capacity} centroid rows")
+    if extra == 0:
         return member_offsets.contiguous()
-    padded = torch.empty((member_offsets.shape[0], width), dtype=torch.int32, device=member_offsets.device)
-    padded[:, :member_offsets.shape[1]].copy_(member_offsets)
-    padded[:, member_offsets.shape[1]:].copy_(member_offsets[:, -1:])
-    return padded
+    return torch.cat([member_offsets, member_offsets[:, -1:].expand(-1, extra)], dim=1).contiguous()
 
 
 def convert_prefill_tensors(*, member_offsets: torch.Tensor, member_positions: torch.Tensor,
@@ -77,82 +82,64 @@ def convert_prefill_tensors(*, member_offsets: torch.Tensor, member_positions: t
                             max_decode_tokens: int, group_size: int = 4,
                             aggregation: GraphAggregation = GraphAggregation.PER_QUERY_HEAD,
                             query_heads: int | None = None, kv_heads: int | None = None) -> ConvertedPrefillState:
-    """Validates explicit prefill tensors and allocates decode-delta pages (runtime.py:85-234)."""
-    if centroids.ndim != 3 or centroids.shape[-1] != HEAD_DIM:
-        raise ValueError("centroids must have shape [retrieval heads, communities, 128]")
-    if centroids.dtype not in (torch.float8_e4m3fn, torch.float32):
-        raise TypeError("centroids must use FP8 E4M3")
-    heads, capacity, _ = centroids.shape
-    graphs = member_offsets.shape[0]
-    if min(heads, graphs, capacity) <= 0:
-        raise ValueError("prefill state must contain active graphs and centroids")
-    if member_positions.dtype != torch.int32 or member_positions.ndim != 2:
-        raise TypeError("member_positions must be a rank-two int32 tensor")
-    if member_positions.shape[0] != graphs:
-        raise ValueError("member positions must contain one row per graph")
-    if num_communities.dtype != torch.int32:
-        raise TypeError("num_communities must use int32")
-    if num_communities.shape != (graphs,):
-        raise ValueError("num_communities must contain one value per graph")
-    if community_sizes.shape != centroids.shape[:2]:
-        raise ValueError("community_sizes must match centroids")
-    if community_sizes.dtype != torch.int32:
-        raise TypeError("community_sizes must use int32")
-    if community_weight.shape != (graphs, capacity):
-        raise ValueError("community_weight must have one row per graph")
-    if community_weight.dtype != torch.float32:
-        raise TypeError("community_weight must use float32")
-    if total_weight.shape != (graphs,) or total_weight.dtype != torch.float32:
-        raise TypeError("total_weight must be one float32 value per graph")
-    if token_communities.dtype != torch.int32 or token_communities.ndim != 2:
-        raise TypeError("token_communities must be a rank-two int32 tensor")
-    if token_communities.shape[0] != graphs:
-        raise ValueError("token_communities must contain one row per graph")
+    """Checks explicit prefill tensors and builds the decode state with empty
+    decode-delta pools (reference runtime.py:85-234).
+
+    The layouts are checked by ``PrefillCSR.validate`` and
+    ``MutableGraphState.validate`` (dtypes, ranks and shared extents); this
+    function adds what only the conversion knows: the head geometry, the
+    decode headroom of the token table and the active community counts."""
     if prefill_seq_len <= 0 or max_decode_tokens <= 0:
-        raise ValueError("prefill and decode capacities must be positive")
+        raise ValueError(f"prefill_seq_len ({prefill_seq_len}) and max_decode_tokens ({max_decode_tokens}) "
+                         "must be positive")
     if not 1 <= group_size <= 16:
-        raise ValueError("group_size must be in [1, 16]")
-    aggregation = GraphAggregation(aggregation)
-    if retrieval_to_graph is None or retrieval_to_kv is None:
-        if heads != graphs:
-            raise ValueError("aggregation mappings are required for non-identity state")
-        retrieval_to_graph = torch.arange(heads, dtype=torch.int32, device=centroids.device)
-        retrieval_to_kv = retrieval_to_graph
-    if (retrieval_to_graph.dtype != torch.int32 or retrieval_to_graph.shape != (heads,)
-            or retrieval_to_kv.dtype != torch.int32 or retrieval_to_kv.shape != (heads,)):
-        raise TypeError("aggregation mappings must be int32 retrieval-head vectors")
-    inferred = heads * group_size
-    query_heads = inferred if query_heads is None else query_heads
-    max_kv = int(retrieval_to_kv.max().item())
-    kv_heads = max_kv + 1 if kv_heads is None else kv_heads
-    if query_heads != inferred:
-        raise ValueError("query-head count does not match retrieval-head geometry")
-    if kv_heads <= 0 or max_kv >= kv_heads:
-        raise ValueError("KV-head count does not cover retrieval mappings")
-    if token_communities.shape[1] < prefill_seq_len + max_decode_tokens:
-        raise ValueError("token_communities lacks requested decode headroom")
-    tensors = (member_offsets, member_positions, num_communities, community_sizes, community_weight,
-               total_weight, token_communities, retrieval_to_graph, retrieval_to_kv)
-    if any(t.device != centroids.device for t in tensors):
-        raise ValueError("all converted tensors must share one device")
-    head_counts = num_communities[retrieval_to_graph.long()].contiguous()
-    initial = tuple(int(v) for v in head_counts.cpu().tolist())
-    if any(c <= 0 or c > capacity for c in initial):
-        raise ValueError("active community counts must fit centroid capacity")
-    csr = PrefillCSR(_pad_member_offsets(member_offsets, community_capacity=capacity),
-                     member_positions.contiguous(), num_communities.clone())
+        raise ValueError(f"group_size must be in [1, 16], got {group_size}")
+    if centroids.ndim != 3 or centroids.shape[-1] != HEAD_DIM or 0 in centroids.shape:
+        raise ValueError(f"centroids must be a non-empty [retrieval heads, communities, {HEAD_DIM}] tensor")
+    heads, capacity = centroids.shape[0], centroids.shape[1]
+    device = centroids.device
+    if (retrieval_to_graph is None) != (retrieval_to_kv is None):
+        raise ValueError("pass both aggregation mappings or neither")
+    if retrieval_to_graph is None:
+        if heads != member_offsets.shape[0]:
+            raise ValueError("without aggregation mappings every retrieval head needs a graph of its own")
+        retrieval_to_graph = retrieval_to_kv = torch.arange(heads, dtype=torch.int32, device=device)
+    csr = PrefillCSR(_offsets_for_capacity(member_offsets, capacity), member_positions.contiguous(),
+                     num_communities.clone())
+    graphs = csr.graph_count
+    for name, t in (("retrieval_to_graph", retrieval_to_graph), ("retrieval_to_kv", retrieval_to_kv)):
+        if t.dtype != torch.int32 or t.shape != (heads,):
+            raise TypeError(f"{name} must be an int32 vector with one entry per retrieval head ({heads})")
+    head_counts = num_communities[retrieval_to_graph.long()] if num_communities.shape == (graphs,) else None
     mutable = MutableGraphState(
         centroids=centroids.contiguous(), community_sizes=community_sizes.contiguous(),
-        community_counts=head_counts.clone(), community_weight=community_weight.contiguous(),
-        total_weight=total_weight.contiguous(), token_communities=token_communities.contiguous(),
+        community_counts=(head_counts if head_counts is not None else num_communities).contiguous().clone(),
+        community_weight=community_weight.contiguous(), total_weight=total_weight.contiguous(),
+        token_communities=token_communities.contiguous(),
         deltas=DecodeDeltaChunks.allocate(graph_count=graphs, community_capacity=capacity,
-                                          max_decode_tokens=max_decode_tokens, device=centroids.device),
+                                          max_decode_tokens=max_decode_tokens, device=device),
         retrieval_to_graph=retrieval_to_graph.contiguous(), retrieval_to_kv=retrieval_to_kv.contiguous())
-    current = torch.full((graphs,), prefill_seq_len, dtype=torch.int32, device=centroids.device)
     csr.validate()
     mutable.validate()
+    if len({t.device for t in (member_offsets, member_positions, num_communities, centroids)}) != 1:
+        raise ValueError("the CSR and the graph state must live on one device")
+    if token_communities.shape[1] < prefill_seq_len + max_decode_tokens:
+        raise ValueError(f"token_communities holds {token_communities.shape[1]} positions; the prefill and the "
+                         f"decode headroom need {prefill_seq_len + max_decode_tokens}")
+    # head geometry: query heads = retrieval heads x group; KV heads cover the mapping
+    highest_kv = int(retrieval_to_kv.max().item())
+    query_heads = heads * group_size if query_heads is None else query_heads
+    kv_heads = highest_kv + 1 if kv_heads is None else kv_heads
+    if query_heads != heads * group_size:
+        raise ValueError(f"{query_heads} query heads do not match {heads} retrieval heads x group {group_size}")
+    if not 0 <= highest_kv < kv_heads:
+        raise ValueError(f"the retrieval heads map to KV head {highest_kv}, beyond the {kv_heads} KV heads")
+    initial = tuple(int(c) for c in mutable.community_counts.cpu().tolist())
+    if not all(0 < c <= capacity for c in initial):
+        raise ValueError(f"active community counts {initial} must lie in [1, {capacity}]")
+    current = torch.full((graphs,), prefill_seq_len, dtype=torch.int32, device=device)
     return ConvertedPrefillState(csr, mutable, current, initial, prefill_seq_len, max_decode_tokens, group_size,
-                                 aggregation, query_heads, kv_heads)
+                                 GraphAggregation(aggregation), query_heads, kv_heads)
 
 
 class DecodeRuntime:
