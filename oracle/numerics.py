@@ -48,14 +48,16 @@ def ordered_fp16_key(bits) -> np.ndarray:
 
 def f32_to_bf16(x) -> np.ndarray:
     """fp32 -> bf16 (returned as fp32 values), round-to-nearest-even, NaN kept."""
-    x = np.asarray(x, dtype=np.float32)
-    bits = x.view(np.uint32).astype(np.uint64)
-    lsb = (bits >> np.uint64(16)) & np.uint64(1)
-    rounded = (bits + np.uint64(0x7FFF) + lsb) & np.uint64(0xFFFF0000)
-    out = rounded.astype(np.uint32)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    bits = x.view(np.uint32)
+    # round half to even on the 16 dropped bits; only NaN bit patterns can wrap
+    # around 2^32 here, and they are replaced below
+    with np.errstate(over="ignore"):
+        rounded = (bits + (np.uint32(0x7FFF) + ((bits >> np.uint32(16)) & np.uint32(1)))) & np.uint32(0xFFFF0000)
     nan = np.isnan(x)
-    out = np.where(nan, (x.view(np.uint32) | np.uint32(0x00400000)) & np.uint32(0xFFFF0000), out)
-    return out.astype(np.uint32).view(np.float32)
+    if nan.any():
+        rounded = np.where(nan, (bits | np.uint32(0x00400000)) & np.uint32(0xFFFF0000), rounded)
+    return rounded.astype(np.uint32).view(np.float32)
 
 
 def bf16_bits(x) -> np.ndarray:
