@@ -52,7 +52,9 @@ constexpr int TABLE_CAP = 1024;  // distinct neighbour communities per vertex
 constexpr int ETHREADS = 256;
 
 enum { CTL_MOVED = 0,  // nonzero once a vertex moved in the current sweep
-       CTL_UPDOWN = 1, CTL_STALE = 2, CTL_DONE = 3, CTL_WORDS = 8 };
+       CTL_UPDOWN = 1, CTL_STALE = 2, CTL_DONE = 3,
+       CTL_OVERFLOW = 4,  // nonzero when a workgroup table overflowed (a broken table bound)
+       CTL_WORDS = 8 };
 
 // ----------------------------------------------------------------- hashing (rng.cuh)
 __device__ __host__ inline uint32_t pcg_hash(uint32_t x) {
@@ -736,8 +738,11 @@ __global__ __launch_bounds__(GIANT_THREADS) void local_moving_giant_kernel(
     const int32_t a = gr.row_ptr[v], b = gr.row_ptr[v + 1];
     int32_t thr;
     double e_sum;
-    if (!giant_table<false>(gr, nullptr, lin, v, 0, a, b, sh, &thr, &e_sum)) {  // cannot happen: stay
-      if (threadIdx.x == 0) lout[v] = old;
+    if (!giant_table<false>(gr, nullptr, lin, v, 0, a, b, sh, &thr, &e_sum)) {  // cannot happen: stay, flagged
+      if (threadIdx.x == 0) {
+        lout[v] = old;
+        ctl[CTL_OVERFLOW] = 1;
+      }
       __syncthreads();
       continue;
     }
@@ -774,7 +779,7 @@ __global__ __launch_bounds__(GIANT_THREADS) void local_moving_giant_kernel(
 __global__ __launch_bounds__(GIANT_THREADS) void refine_propose_giant_kernel(
     Graph gr, const int32_t* __restrict__ parent, const double* __restrict__ sigma,
     const double* __restrict__ parent_sigma, const int32_t* __restrict__ lin, int32_t* __restrict__ prop,
-    uint32_t* __restrict__ rank, const int32_t* __restrict__ ctl, const int32_t* __restrict__ giants,
+    uint32_t* __restrict__ rank, int32_t* __restrict__ ctl, const int32_t* __restrict__ giants,
     const int32_t* __restrict__ giant_count, float resolution, float inv_theta, int boltzmann, uint32_t level,
     uint32_t sweep, uint32_t seed) {
   __shared__ GiantShared sh;
@@ -794,8 +799,11 @@ __global__ __launch_bounds__(GIANT_THREADS) void refine_propose_giant_kernel(
     const int32_t pv = parent[v];
     int32_t thr;
     double e_sum;
-    if (!giant_table<true>(gr, parent, lin, v, pv, a, b, sh, &thr, &e_sum)) {  // cannot happen: stay
-      if (threadIdx.x == 0) prop[v] = old;
+    if (!giant_table<true>(gr, parent, lin, v, pv, a, b, sh, &thr, &e_sum)) {  // cannot happen: stay, flagged
+      if (threadIdx.x == 0) {
+        prop[v] = old;
+        ctl[CTL_OVERFLOW] = 1;
+      }
       __syncthreads();
       continue;
     }
@@ -905,6 +913,13 @@ __global__ __launch_bounds__(LTHREADS) void modularity_kernel(Graph gr, const in
     const double m_g = 0.5 * tm;
     q_v[v] = in_sum / tm - (double)resolution * (gr.k_v[v] * sigma[cv]) / (4.0 * m_g * m_g);
   }
+}
+
+// A flagged table overflow turns every graph's modularity into NaN, which the
+// host checks: the labels of such a call are not to be trusted.
+__global__ void overflow_mark_kernel(const int32_t* __restrict__ ctl, int32_t G, double* __restrict__ modularity) {
+  const int32_t g = blockIdx.x * blockDim.x + threadIdx.x;
+  if (g < G && ctl[CTL_OVERFLOW] != 0) modularity[g] = __builtin_nan("");
 }
 
 __global__ void finish_kernel(const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ result, int32_t V,
@@ -1351,6 +1366,7 @@ extern "C" int ckv_batched_leiden(const int32_t* edge_src, const int32_t* edge_d
   sigma_scatter_kernel<<<egrid, ETHREADS, 0, st>>>(lab[cur], k_v, V, sigma, nullptr);
   modularity_kernel<<<vgrid, LTHREADS, 0, st>>>(gr, lab[cur], sigma, resolution, psigma);
   graph_sum_kernel<<<graphs, 256, 0, st>>>(psigma, seq_len, modularity);
+  overflow_mark_kernel<<<blocks(graphs, ETHREADS), ETHREADS, 0, st>>>(ctl, graphs, modularity);
   finish_kernel<<<egrid, ETHREADS, 0, st>>>(row_ptr, lab[cur], V, labels);
   return launch_check();
 }

@@ -139,8 +139,10 @@ def run_leiden(edge_src: torch.Tensor, edge_dst: torch.Tensor, edge_weight: torc
     if boltzmann_env is not None:
         use_boltzmann = boltzmann_env not in ("", "0", "false", "False")
 
-    labels0, _ = module.batched_leiden(edge_src, edge_dst, edge_weight, G, seq_len, max_level, float(resolution),
+    level_modularity = []
+    labels0, mod0 = module.batched_leiden(edge_src, edge_dst, edge_weight, G, seq_len, max_level, float(resolution),
                                        float(theta), max_inner_iter, seed, use_boltzmann)
+    level_modularity.append(mod0)
     is_isolated = labels0 == -1
     arange_v = torch.arange(V_orig, dtype=torch.int32, device=device)
     cur_labels = torch.where(is_isolated, arange_v, labels0)
@@ -155,8 +157,10 @@ def run_leiden(edge_src: torch.Tensor, edge_dst: torch.Tensor, edge_weight: torc
         cur_src, cur_dst, cur_w = module.aggregate_coo(cur_src, cur_dst, cur_w, dense_for_agg, G * cur_seq_len)
         if cur_src.numel() == 0:
             break
-        labels_k, _ = module.batched_leiden(cur_src, cur_dst, cur_w, G, cur_seq_len, max_level, float(resolution),
-                                            float(theta), max_inner_iter, seed + level, use_boltzmann)
+        labels_k, mod_k = module.batched_leiden(cur_src, cur_dst, cur_w, G, cur_seq_len, max_level,
+                                                float(resolution), float(theta), max_inner_iter, seed + level,
+                                                use_boltzmann)
+        level_modularity.append(mod_k)
         arange_super = torch.arange(G * cur_seq_len, dtype=torch.int32, device=device)
         labels_k = torch.where(labels_k == -1, arange_super, labels_k)
         dense_k, next_seq_len = _densify_per_graph(labels_k, G, cur_seq_len)
@@ -165,6 +169,10 @@ def run_leiden(edge_src: torch.Tensor, edge_dst: torch.Tensor, edge_weight: torc
         cur_seq_len = next_seq_len
         dense_for_agg = dense_k
 
+    # the native sweeps mark every graph's modularity NaN when a neighbour
+    # table overflowed (a broken table bound): fail instead of returning labels
+    if bool(torch.isnan(torch.cat(level_modularity)).any()):
+        raise RuntimeError("Leiden: a neighbour-community table overflowed; the labels are not valid")
     modularity = _compute_disjoint_modularity(edge_src, edge_dst, edge_weight, chain, float(resolution))
     keep = ~is_isolated
     vertex = torch.nonzero(keep, as_tuple=False).squeeze(-1).long()

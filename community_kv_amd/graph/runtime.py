@@ -42,10 +42,19 @@ class PartitionRuntime:
         self._executor: ThreadPoolExecutor | None = None
 
     def reset(self) -> None:
-        for future in self._futures.values():
-            future.result()
+        """Drops every pending and finished job.  Waits for the running ones;
+        the first job error is raised once, after the runtime is empty again,
+        so a later request starts clean."""
+        futures = list(self._futures.values())
         self._futures.clear()
         self._results.clear()
+        error = None
+        for future in futures:
+            exc = future.exception()
+            if exc is not None and error is None:
+                error = exc
+        if error is not None:
+            raise error
 
     def _pool(self) -> ThreadPoolExecutor:
         if self._executor is None:
@@ -75,7 +84,7 @@ class PartitionRuntime:
             raise ValueError(f"layer {layer_idx} was already submitted")
         if not 0 <= layer_idx < self.max_layers:
             raise ValueError("layer index out of range")
-        if any(torch.device(d) != keys.device for d in self.scheduling.devices):
+        if not all(_same_device(d, keys.device) for d in self.scheduling.devices):
             raise NotImplementedError("partition offload to another GPU is not part of this build")
         if self.label_provider is None and self.scheduling.overlap and keys.device.type == "cuda":
             self._futures[layer_idx] = self._pool().submit(
@@ -135,6 +144,18 @@ class PartitionRuntime:
         if self._executor is not None:
             self._executor.shutdown(wait=True)
             self._executor = None
+
+
+def _same_device(name: Any, device: torch.device) -> bool:
+    """Whether the configured device `name` is `device`; a CUDA device
+    without an index means the current one."""
+    d = torch.device(name)
+    if d.type != device.type:
+        return False
+    if d.type == "cuda":
+        current = torch.cuda.current_device() if torch.cuda.is_available() else 0
+        return (current if d.index is None else d.index) == (current if device.index is None else device.index)
+    return True
 
 
 def vars_of(layer: PartitionedLayer) -> list[Any]:

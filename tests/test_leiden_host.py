@@ -114,3 +114,46 @@ def test_partition_runtime_guards():
         PartitionRuntime(algorithm=CommunityKVConfig(), scheduling=PartitionConfig(), max_layers=0)
     rt.shutdown()
     off.shutdown()
+
+
+def test_partition_runtime_device_names_and_failed_job_recovery():
+    """A device name without an index means the current GPU; a failed job is
+    raised once by reset(), after which the runtime serves new requests."""
+    from concurrent.futures import Future
+
+    from community_kv_amd.config import CommunityKVConfig, PartitionConfig
+    from community_kv_amd.graph import runtime as grt
+
+    cuda0 = torch.device("cuda", 0)
+    assert grt._same_device("cuda", cuda0) == (not torch.cuda.is_available() or torch.cuda.current_device() == 0)
+    assert grt._same_device("cuda:0", cuda0)
+    assert not grt._same_device("cuda:1", cuda0)
+    assert not grt._same_device("cpu", cuda0)
+    assert grt._same_device("cpu", torch.device("cpu"))
+
+    rt = grt.PartitionRuntime(algorithm=CommunityKVConfig(), scheduling=PartitionConfig(), max_layers=2)
+    failed: Future = Future()
+    failed.set_exception(RuntimeError("job failed"))
+    done: Future = Future()
+    done.set_result(None)
+    rt._futures = {0: failed, 1: done}
+    with pytest.raises(RuntimeError, match="job failed"):
+        rt.reset()
+    assert not rt._futures and not rt._results
+    rt.reset()  # nothing left to raise
+    rt.shutdown()
+
+
+def test_run_leiden_raises_on_flagged_table_overflow(monkeypatch):
+    """The native sweeps mark modularity NaN when a neighbour table overflowed."""
+
+    class _Module:
+        @staticmethod
+        def batched_leiden(*args):
+            return torch.tensor([0, 0], dtype=torch.int32), torch.full((1,), float("nan"), dtype=torch.float64)
+
+    monkeypatch.setattr(algorithm, "_load_module", lambda: _Module)
+    monkeypatch.setattr(algorithm, "_densify_per_graph", _cpu_densify)
+    with pytest.raises(RuntimeError, match="overflowed"):
+        algorithm.run_leiden(torch.tensor([0], dtype=torch.int32), torch.tensor([1], dtype=torch.int32),
+                             torch.ones(1), G=1, seq_len=2, max_level=1)
