@@ -19,7 +19,7 @@ REPO_DIR = os.path.dirname(PACKAGE_DIR)
 LIB_PATH = os.path.join(PACKAGE_DIR, "libckv_amd.so")
 SOURCES = [os.path.join(PACKAGE_DIR, "csrc", name)
            for name in ("ckv_decode.hip", "ckv_select.hip", "ckv_attend.hip", "ckv_prefill.hip", "ckv_diag.hip",
-                                "ckv_state.hip", "ckv_leiden.hip")]
+                                "ckv_state.hip", "ckv_leiden.hip", "ckv_noalloc.hip")]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 HIP_FLAGS = [
     "--offload-arch=gfx950",
@@ -52,6 +52,9 @@ EXPORTED_SYMBOLS = (
     "ckv_segmented_attention",
     "ckv_attention_partials",
     "ckv_decode_layer",
+    "ckv_decode_layer_static",
+    "ckv_decode_static_scratch_bytes",
+    "ckv_decode_static_scratch_limit",
     "ckv_online_update",
     "ckv_score_select_after_update",
     "ckv_decode_step_after_update",
@@ -208,6 +211,15 @@ def lib() -> ctypes.CDLL:
                        ctypes.POINTER(DeltaChunks), ctypes.POINTER(DecodeConfig),
                        ctypes.POINTER(DecodeWorkspace), _p]
         fn.restype = ctypes.c_int
+    handle.ckv_decode_layer_static.argtypes = [ctypes.POINTER(KvCache), ctypes.POINTER(GraphState),
+                                               ctypes.POINTER(PrefillCsr), ctypes.POINTER(DeltaChunks),
+                                               ctypes.POINTER(DecodeConfig), _p, _p, _p, _p, _p, _p, _p]
+    handle.ckv_decode_layer_static.restype = ctypes.c_int
+    handle.ckv_decode_static_scratch_bytes.argtypes = [ctypes.POINTER(GraphState), ctypes.POINTER(DecodeConfig),
+                                                       _i32]
+    handle.ckv_decode_static_scratch_bytes.restype = ctypes.c_size_t
+    handle.ckv_decode_static_scratch_limit.argtypes = []
+    handle.ckv_decode_static_scratch_limit.restype = ctypes.c_size_t
     handle.ckv_score_select_after_update.argtypes = [ctypes.POINTER(LayerArgs), ctypes.POINTER(LayerArgs), _p]
     handle.ckv_score_select_after_update.restype = ctypes.c_int
     handle.ckv_decode_step_after_update.argtypes = [ctypes.POINTER(LayerArgs), ctypes.POINTER(LayerArgs), _p]

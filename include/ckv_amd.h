@@ -457,6 +457,29 @@ int ckv_decode_layer(const ckv_kv_cache* kv, const ckv_graph_state* state,
                      const ckv_decode_config* config, ckv_decode_workspace* ws,
                      void* stream);
 
+/* Allocation-free variant of ckv_decode_layer, no counterpart in the reference:
+ * for callers that cannot allocate device memory (code under graph capture,
+ * serving loops that forbid hipMalloc).  The caller passes the state, the KV
+ * cache and the outputs (output [query_heads][128] in the kv dtype, lse
+ * [query_heads], topk_scores / topk_positions [retrieval_heads][8], assigned /
+ * overflow [graph_count]); every other workspace array (scores, descriptors,
+ * slot table, exchange row and counters, split partials, per-slot scores)
+ * lives in one static device array of ckv_decode_static_scratch_limit() bytes
+ * (16 MiB) per GPU, held until the process ends.  Workspace capacities are the
+ * ones the Python workspace would allocate for `config` (descriptors
+ * min(max_selected or topk_communities, community_capacity), slot capacity
+ * ceil((num_sink + max_selected + local_window + include_current) / 64) * 64).
+ * A layer needing more scratch than the limit (ckv_decode_static_scratch_bytes)
+ * fails with CKV_E_LIMIT.  Calls on one GPU share the array and must not
+ * overlap (another stream or host thread): they race.  Calls no allocator. */
+int ckv_decode_layer_static(const ckv_kv_cache* kv, const ckv_graph_state* state,
+                            const ckv_prefill_csr* csr, const ckv_delta_chunks* deltas,
+                            const ckv_decode_config* config, void* output, float* lse, float* topk_scores,
+                            int32_t* topk_positions, int32_t* assigned, int32_t* overflow, void* stream);
+size_t ckv_decode_static_scratch_bytes(const ckv_graph_state* state, const ckv_decode_config* config,
+                                       int32_t query_heads);
+size_t ckv_decode_static_scratch_limit(void);
+
 /* Dense decode baseline: every query head attends positions [0, seq_len) of its
  * KV head (query head h uses KV head h / (query_heads / kv_heads)).  partial_*
  * hold [query_heads][ceil(seq_len/64)] splits. */
