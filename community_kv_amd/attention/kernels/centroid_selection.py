@@ -24,6 +24,13 @@ HEAD_DIM = 128
 SCORE_BLOCK_N = nat.SCORE_BLOCK
 
 
+def exchange_words(community_capacity: int) -> int:
+    """uint64 words per retrieval head of the fused launch's exchange row:
+    tagged scores, then tagged nearest-centroid minima and done words (8 waves
+    x 64 parts each) (ckv_exchange_words in csrc/ckv_device.h)."""
+    return community_capacity + 2 * 64 * 8
+
+
 @dataclass(slots=True)
 class CentroidSelectionWorkspace:
     """Preallocated scoring/selection outputs and slot table."""
@@ -36,7 +43,8 @@ class CentroidSelectionWorkspace:
     tile_descriptors: torch.Tensor  # [R, token_budget / 64] int32
     selected_counts: torch.Tensor   # [R] int32
     slot_positions: torch.Tensor    # [R, slot capacity] int32
-    exchange: torch.Tensor          # [R, C + 512] uint64 (zeros): scores handed between a fused launch's workgroups
+    exchange: torch.Tensor          # [R, exchange_words(C)] uint64 (zeros): a fused launch's workgroups hand each
+                                    # other centroid scores, done words and nearest-centroid minima through it
     nearest: torch.Tensor           # [R] int32
     block_counters: torch.Tensor    # [4R] int32 arrival counters and epochs (zeros; kernel-maintained)
     token_budget: int
@@ -108,7 +116,8 @@ class CentroidSelectionWorkspace:
             tile_descriptors=i32((kv_heads, token_budget // ATTENTION_TILE)),
             selected_counts=i32((kv_heads,)),
             slot_positions=i32((kv_heads, slots), -1),
-            exchange=torch.zeros((kv_heads, community_capacity + 512), dtype=torch.uint64, device=device),
+            exchange=torch.zeros((kv_heads, exchange_words(community_capacity)), dtype=torch.uint64,
+                                 device=device),
             nearest=i32((kv_heads,), -1),
             block_counters=i32((4 * kv_heads,)),
             token_budget=token_budget,

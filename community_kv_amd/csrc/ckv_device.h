@@ -25,6 +25,10 @@ __device__ unsigned long long phase_stamp[32];  // one array per kernel file
   do {                                                                                       \
     if ((cond) && threadIdx.x == 0) atomicMax(&phase_stamp[(slot)], (unsigned long long)wall_clock64()); \
   } while (0)
+#define CKV_STAMP_AT(cond, slot)                 \
+  do {                                           \
+    if (cond) phase_stamp[(slot)] = wall_clock64(); \
+  } while (0)
 // Register-held stamps (no store until the flush, so no memory wait covers them).
 #define CKV_TS_DECL unsigned long long ckv_ts[32] = {}
 #define CKV_TS_ARG , unsigned long long* ckv_ts
@@ -47,6 +51,9 @@ __device__ unsigned long long phase_stamp[32];  // one array per kernel file
 #define CKV_STAMP_MAX(cond, slot) \
   do {                            \
   } while (0)
+#define CKV_STAMP_AT(cond, slot) \
+  do {                           \
+  } while (0)
 #endif
 
 constexpr int D = CKV_HEAD_DIM;
@@ -56,6 +63,14 @@ constexpr int SCORE_BLOCK = CKV_SCORE_BLOCK;
 constexpr int SELECT_THREADS = 512;  // one selection workgroup per retrieval head
 constexpr int REDUCE_THREADS = 128;
 constexpr float NEG_INF = -__builtin_huge_valf();
+
+// Words (uint64) of one retrieval head's row of the fused launch's exchange
+// buffer: the epoch-tagged centroid scores (one per community), then the
+// tagged nearest-centroid minima and the scoring waves' done words (eight
+// waves of at most 64 parts each).
+__host__ __device__ inline int64_t ckv_exchange_words(int community_capacity) {
+  return (int64_t)community_capacity + 2 * 64 * 8;
+}
 
 // Every decode kernel receives the full argument set by value.
 struct DecodeArgs {
@@ -197,6 +212,15 @@ __device__ inline void st_agent_u32(uint32_t* p, uint32_t v) {
 }
 __device__ inline void st_agent_f32(float* p, float v) {
   st_agent_u32(reinterpret_cast<uint32_t*>(p), __float_as_uint(v));
+}
+// A store that stays in this XCD's L2 (workgroup scope: L1 is write-through,
+// nothing is written through to memory).  Another workgroup on the same XCD
+// sees it with ld_agent_* (which bypasses L1 and hits that L2) after about a
+// quarter of a microsecond; one on another XCD does not see it before the
+// kernel ends, so data handed over this way carries a tag that the reader
+// checks, with a fallback when it never shows.
+__device__ inline void st_xcd_u64(uint64_t* p, uint64_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 // Waits until every global load and store this thread issued has completed.
 __device__ inline void wait_vm() { __builtin_amdgcn_s_waitcnt(0x0F70); }

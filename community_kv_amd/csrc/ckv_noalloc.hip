@@ -31,7 +31,7 @@ std::mutex g_mutex;
 unsigned char* g_ptr[MAX_DEVICES] = {};   // device address of `scratch` per GPU
 struct ExchangeLayout {  // where the last call on a GPU kept its exchange row and counters
   int32_t heads, capacity;
-  size_t offset;
+  size_t offset, end;
 };
 ExchangeLayout g_layout[MAX_DEVICES] = {};
 
@@ -71,7 +71,7 @@ Layout layout_of(const ckv_graph_state* st, const ckv_decode_config* cfg, int qu
       (size_t)R * std::max(l.budget_tiles, 1) * 4,  // tile descriptors
       (size_t)R * 4,                              // selected counts
       (size_t)R * l.slot_cap * 4,                 // slot positions
-      (size_t)R * (C + 512) * 8,                  // exchange
+      (size_t)R * ckv::ckv_exchange_words(C) * 8,  // exchange
       (size_t)R * 4,                              // nearest
       (size_t)R * 4 * 4,                          // block counters
       (size_t)query_heads * l.tiles * 4,          // partial max
@@ -132,9 +132,9 @@ extern "C" int ckv_decode_layer_static(const ckv_kv_cache* kv, const ckv_graph_s
       g_ptr[dev] = static_cast<unsigned char*>(p);
     }
     base = g_ptr[dev];
-    const ExchangeLayout now{st->retrieval_heads, st->community_capacity, l.off[7]};
+    const ExchangeLayout now{st->retrieval_heads, st->community_capacity, l.off[7], l.off[10]};
     const ExchangeLayout& was = g_layout[dev];
-    clear = was.heads != now.heads || was.capacity != now.capacity || was.offset != now.offset;
+    clear = was.heads != now.heads || was.capacity != now.capacity || was.offset != now.offset || was.end != now.end;
     g_layout[dev] = now;
   }
   ckv_decode_workspace ws;

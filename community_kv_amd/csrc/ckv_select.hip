@@ -59,17 +59,22 @@ constexpr int FUSED_TILES = 2;
 // Cooperative fused launch: polling rounds (each a memory round trip plus a
 // short sleep, about 1 us) before a part scores the missing communities
 // itself; at most 64 parts per head.
-constexpr int COOP_POLLS = 48;
+constexpr int COOP_POLLS = 64;
+constexpr int COOP_PRE = 2;  // passes of the cooperative scoring share loaded with the first round
+constexpr int COOP_SCORE_WAVES = 6;  // waves that score and poll; the others walk the graph-indexed chain
 constexpr int COOP_MAX_PARTS = 64;
 constexpr int COOP_WAVES = SELECT_THREADS / 64;
+// Exchange row layout after the C tagged scores: the nearest-centroid minima
+// (part * COOP_WAVES + wave), then the scoring waves' done words (same indexing).
+constexpr int COOP_NEAR_OFF = 0;
+constexpr int COOP_FLAGS_OFF = COOP_MAX_PARTS * COOP_WAVES;
 }  // namespace
 
-// Exchange row of one retrieval head: the tagged scores, then one
-// nearest-centroid minimum per wave of each of at most 64 parts.
 __host__ __device__ inline int64_t exchange_stride(int community_capacity) {
-  return (int64_t)community_capacity + COOP_MAX_PARTS * COOP_WAVES;
+  return ckv_exchange_words(community_capacity);
 }
-
+// Low 16 bits of a launch's tag, carried by the nearest-centroid minima.
+__device__ inline uint64_t near_tag16(uint32_t epoch) { return (uint64_t)((epoch + 1u) & 0xffffu); }
 
 // Arrival of one part of head rh.  The last part to arrive merges the head's
 // split partials into output and lse (the arithmetic of merge_wide_body, so
@@ -79,7 +84,7 @@ __host__ __device__ inline int64_t exchange_stride(int community_capacity) {
 // another workgroup.
 template <int PMAX>
 __device__ __forceinline__ void coop_finish(const DecodeArgs& a, const int rh, const int parts, const uint32_t epoch,
-                                   const bool nearest_mode, const uint64_t* xrow) {
+                                            const bool nearest_mode, const uint64_t* xrow) {
   __shared__ int s_last;
   __shared__ float sc_s[CKV_MAX_GROUP][PMAX];
   __shared__ float den_s[CKV_MAX_GROUP];
@@ -87,6 +92,7 @@ __device__ __forceinline__ void coop_finish(const DecodeArgs& a, const int rh, c
   const int lane = tid & 63;
   const int wave = tid >> 6;
   uint32_t* counter = a.ws.block_counters + rh;
+  CKV_STAMP_MAX(rh == 0, 29);
   wait_vm();
   __syncthreads();  // every store of the part has completed
   if (tid == 0)
@@ -119,13 +125,14 @@ __device__ __forceinline__ void coop_finish(const DecodeArgs& a, const int rh, c
       a.ws.lse[(int64_t)rh * G + wave] = M + __logf(den);
     }
   } else if (nearest_mode && wave == COOP_WAVES - 1) {
+    // distance bits << 32 | row << 16 | tag; every part's stores have landed
     uint64_t m = ~0ull;
     for (int e = lane; e < parts * COOP_WAVES; e += 64) {
-      const uint64_t x = ld_agent_u64(xrow + C + e);
+      const uint64_t x = ld_agent_u64(xrow + C + COOP_NEAR_OFF + e);
       m = x < m ? x : m;
     }
     m = wave_min_u64(m);
-    if (lane == 0) a.ws.nearest[rh] = (m == ~0ull) ? -1 : (int)(m & 0xffffffffu);
+    if (lane == 0) a.ws.nearest[rh] = (m >> 32) == 0xffffffffull ? -1 : (int)((m >> 16) & 0xffffu);
   }
   __syncthreads();
   if (tid < G * D) {
@@ -199,6 +206,7 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
   const int cpg = a.dl.chunks_per_graph;
   CKV_TS_DECL;
   CKV_TS(0);
+  CKV_STAMP_MAX(FUSED && rh == 0, 26);
 
   __shared__ float q_s[CKV_MAX_GROUP * D];
   __shared__ float key_s[D];
@@ -207,7 +215,7 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
   __shared__ __align__(16) int scan_s[4 * WAVES * OWN];
   __shared__ uint64_t near_s[WAVES];
   __shared__ int sink_s[CKV_MAX_SINKS];
-  __shared__ int s_max_idx, s_sel_count, s_last_sel_pos, s_last_size, s_sink_max;
+  __shared__ int s_max_idx, s_sel_count, s_last_sel_pos, s_last_size, s_sink_max, s_cur;
 
   extern __shared__ __align__(16) unsigned char dyn_all[];
   // fused: the window tokens' communities first, then the selection arrays (later the attention buffers)
@@ -254,19 +262,60 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
     load_batch(0, 0, nscore - 1);
     load_batch(PB, 1, nscore - 1);  // clamped rows: harmless when there is no second batch
   }
-  // COOP: this part's share [sh0, sh1) of the live communities (one 64-row
-  // pass when the share fits), the head's epoch and the exchange row.
-  const int share = (count + parts - 1) / max(parts, 1);
-  const int sh0 = min(part * share, count), sh1 = min(sh0 + share, count);
+  // COOP: waves 0 .. COOP_SCORE_WAVES - 1 score this part's share of the rows
+  // and poll for the other parts' shares; the remaining waves walk the
+  // graph-indexed chain (CSR offsets, decode-delta fields, tail chunks, window
+  // communities, sinks, current key) into LDS, so that the scoring waves' memory
+  // waits never cover those dependent rounds.  The share is interleaved (rows
+  // part, part + parts, ...), so its addresses do not wait for the community
+  // count, and up to COOP_PRE passes of fragments are loaded with the first
+  // round.  Each row's 8-lane group is replicated over `qps` query-pair groups
+  // (thread bits 3..), which split the query pairs of the group between them.
   uint64_t* xrow = COOP ? a.ws.exchange + (int64_t)rh * exchange_stride(C) : nullptr;
   uint32_t epoch = 0;
-  CentroidFrag<CT> cfrag;
-  int csize = 0;
+  const bool chain_wave = COOP && (tid >> 6) >= COOP_SCORE_WAVES;
+  // Blocks go to the eight XCDs round robin and the parts of head rh are blocks
+  // rh + R * part, so with R a multiple of 8 they share one XCD: scores and
+  // done words then stay in its L2 (st_xcd_u64), else they are written through.
+  const bool xcd_local = (a.st.retrieval_heads & 7) == 0;
+  const int npairs = (G + 1) >> 1;
+  const int rpp = (nscore + max(parts, 1) - 1) / max(parts, 1);  // rows per part
+  int qps_log = 0;
+  if constexpr (COOP) {
+    const int pairs_log = npairs <= 1 ? 0 : 1;  // the fused path serves groups of at most four queries
+    for (int l = pairs_log; l > 0; --l) {
+      if (((COOP_SCORE_WAVES * 64) >> (3 + l)) >= rpp) {
+        qps_log = l;
+        break;
+      }
+    }
+  }
+  const int qp = (tid >> 3) & ((1 << qps_log) - 1);
+  const int ri = tid >> (3 + qps_log);  // row of this thread within a pass
+  const int rows_pass = (COOP_SCORE_WAVES * 64) >> (3 + qps_log);
+  CentroidFrag<CT> cfrag[COOP_PRE];
+  int csize[COOP_PRE];
+  uint4 qraw[2][2][2];  // [pair][query of the pair][dims 0-7, 8-15 of this lane's slice], bf16
   if constexpr (COOP) {
     epoch = ld_agent_u32(a.ws.block_counters + 2 * a.st.retrieval_heads + rh);
-    const int row = min(sh0 + sub, max(sh1, 1) - 1);
-    load_frag<CT>(a.st.centroids, (int64_t)rh * C + row, 16 * lane8, cfrag);
-    csize = gload_i32(a.st.community_sizes + (int64_t)rh * C + row);
+    if (!chain_wave) {
+#pragma unroll
+      for (int ps = 0; ps < COOP_PRE; ++ps) {
+        const int row = min(part + parts * min(ri + ps * rows_pass, rpp - 1), nscore - 1);
+        load_frag<CT>(a.st.centroids, (int64_t)rh * C + row, 16 * lane8, cfrag[ps]);
+        csize[ps] = gload_i32(a.st.community_sizes + (int64_t)rh * C + row);
+      }
+      const uint16_t* qbase = reinterpret_cast<const uint16_t*>(a.kv.query) + (int64_t)rh * G * D + 16 * lane8;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int g = min(2 * qp + (2 << qps_log) * j + u, G - 1);
+          qraw[j][u][0] = gload16(qbase + (int64_t)g * D);
+          qraw[j][u][1] = gload16(qbase + (int64_t)g * D + 8);
+        }
+      }
+    }
   }
   const uint64_t tag = (uint64_t)(epoch + 1u) << 32;
   // Query group: two elements per thread (G * 128 <= 2048 <= 4 * threads).
@@ -280,7 +329,7 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
                                                                     min(tid + k * SELECT_THREADS, nscore - 1)];
   }
 #pragma unroll
-  for (int h = 0; h < (PRE ? 0 : 2); ++h) {
+  for (int h = 0; h < ((PRE || COOP) ? 0 : 2); ++h) {
     const int qe = min(2 * (tid + h * SELECT_THREADS), G * D - 2);
     if constexpr (DT == CKV_BF16) {
       const uint32_t w = (uint32_t)gload_i32(reinterpret_cast<const int32_t*>(
@@ -293,7 +342,7 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
       qv[2 * h + 1] = gload_f32(qp + 1);
     }
   }
-  const int sink_v = (materialise && ns > 0) ? gload_i32(a.cfg.sink_positions + min(tid, ns - 1)) : -1;
+  const int sink_v = (!COOP && materialise && ns > 0) ? gload_i32(a.cfg.sink_positions + min(tid, ns - 1)) : -1;
   // thread t owns communities t, t + SELECT_THREADS, ...: id order is k, then thread
   auto cid = [&](int k) { return tid + k * SELECT_THREADS; };
   int o_size[OWN];
@@ -301,7 +350,7 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
   for (int k = 0; k < OWN; ++k) o_size[k] = gload_i32(a.st.community_sizes + (int64_t)rh * C + min(cid(k), nscore - 1));
 
   // ---- R1 -------------------------------------------------------------------
-  const int cur = a.st.current_position[graph];
+  int cur = COOP ? 0 : a.st.current_position[graph];  // COOP: from LDS after the polls
   const int64_t tbl = (int64_t)graph * C;
   const int64_t cb = (int64_t)graph * cpg;
   int o_lo[OWN], o_dc[OWN], o_tl[OWN], o_ts[OWN], o_tn[OWN];
@@ -313,7 +362,7 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
     o_ts[k] = 0;
     o_tn[k] = 0;
   }
-  if (materialise) {
+  if (!COOP && materialise) {
 #pragma unroll
     for (int k = 0; k < OWN; ++k) {
       const int c = min(cid(k), C - 1);
@@ -323,29 +372,31 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
     }
   }
   float key_v = 0.0f;
-  if (nearest_mode) {
+  if (!COOP && nearest_mode) {
     const int64_t cp = cur < 0 ? 0 : (cur >= a.kv.capacity ? a.kv.capacity - 1 : cur);
     key_v = load_elem<DT>(a.kv.key, kvh * a.kv.head_stride + cp * a.kv.token_stride + (tid & (D - 1)));
   }
 
+  if constexpr (!COOP) {  // (COOP: the chain waves set these up)
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int e = 2 * (tid + h * SELECT_THREADS);
-    if (e < G * D) {
-      q_s[e] = qv[2 * h];
-      q_s[e + 1] = qv[2 * h + 1];
+    for (int h = 0; h < 2; ++h) {
+      const int e = 2 * (tid + h * SELECT_THREADS);
+      if (e < G * D) {
+        q_s[e] = qv[2 * h];
+        q_s[e + 1] = qv[2 * h + 1];
+      }
     }
-  }
-  if (tid < ns) sink_s[tid] = sink_v;
-  if (nearest_mode && tid < D) key_s[tid] = (cur >= 0 && cur < a.kv.capacity) ? key_v : 0.0f;
-  hist[tid & 255] = 0;
-  hist2[tid & 255] = 0;
-  if (tid == 0) {
-    s_max_idx = -1;
-    s_sel_count = 0;
-  }
-  if constexpr (FUSED) {  // tile marks (see the fused slot resolution)
-    if (tid < FUSED_TILES * TILE) fused_marks(dyn, C)[tid] = -1;
+    if (tid < ns) sink_s[tid] = sink_v;
+    if (nearest_mode && tid < D) key_s[tid] = (cur >= 0 && cur < a.kv.capacity) ? key_v : 0.0f;
+    hist[tid & 255] = 0;
+    hist2[tid & 255] = 0;
+    if (tid == 0) {
+      s_max_idx = -1;
+      s_sel_count = 0;
+    }
+    if constexpr (FUSED) {  // tile marks (see the fused slot resolution)
+      if (tid < FUSED_TILES * TILE) fused_marks(dyn, C)[tid] = -1;
+    }
   }
   // R2 issue (tail-chunk start and fill of every owned community with decode
   // deltas, the communities of the window tokens).  The cooperative path
@@ -373,10 +424,9 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
       }
     }
   };
-  __syncthreads();  // q_s, key_s, sink_s, hist
-  if constexpr (COOP && !CKV_R2_LATE) issue_r2();
-  CKV_TS(6);
-  if (tid < 64) {  // largest sink position: window tokens beyond it skip the sink test
+  if constexpr (!COOP) __syncthreads();  // q_s, key_s, sink_s, hist
+  if constexpr (!COOP) CKV_TS(6);
+  if (!COOP && tid < 64) {  // largest sink position: window tokens beyond it skip the sink test
     int m = -1;
     for (int i = tid; i < ns; i += 64) m = max(m, sink_s[i]);
     m = max(m, (int)dpp_u32<0xB1>((uint32_t)m));
@@ -447,79 +497,307 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
   const int last_live = max(count, 1) - 1;
   bool score_all = !PRE;
   if constexpr (COOP) {
-    // This part's share, published as (epoch + 1) << 32 | fp16 bits.
-    uint64_t best_share = ~0ull;
-    for (int r0 = sh0; r0 < sh1; r0 += ROWS_PER_PASS) {
-      if (r0 != sh0) {
-        const int row = min(r0 + sub, sh1 - 1);
-        load_frag<CT>(a.st.centroids, (int64_t)rh * C + row, 16 * lane8, cfrag);
-        csize = gload_i32(a.st.community_sizes + (int64_t)rh * C + row);
-      }
-      float cv[16];
-      decode_frag<CT>(cfrag, cv);
-      float best = NEG_INF;
-#pragma unroll 1
-      for (int g = 0; g < G; g += 2) {
-        float qa[16], qb[16];
-        load_q_pair(q_s, g, lane8, qa, qb);
-        float a0, a1;
-        dot16_pair<CT, DT>(qa, qb, cv, a0, a1);
-        best = fmax_exact(best, a0);
-        if (g + 1 < G) best = fmax_exact(best, a1);
-      }
-      const int c = r0 + sub;
-      const bool in = c < sh1;
-      const bool live = in && csize > 0;
-      const uint16_t bits = f16_bits_hw(live ? best : NEG_INF);
-      if (lane8 == 0 && in) {
-        key16[c] = bits;
-        st_agent_u64(xrow + c, tag | bits);
-      }
-      if (nearest_mode) {
-        float acc;
-        {
-          const float d0 = key_s[16 * lane8] - cv[0];
-          acc = d0 * d0;
-        }
-#pragma unroll
-        for (int i = 1; i < 16; ++i) {
-          const float di = key_s[16 * lane8 + i] - cv[i];
-          acc = acc + di * di;
-        }
-        acc = add_xor_f32<4>(acc);
-        acc = add_xor_f32<2>(acc);
-        acc = add_xor_f32<1>(acc);
-        if (live) {
-          const uint64_t cand = ((uint64_t)ckv_f2u(acc) << 32) | (uint32_t)c;
-          best_share = cand < best_share ? cand : best_share;
-        }
-      }
-    }
-    if (nearest_mode) {  // every wave of every part publishes its minimum (~0 when it has none)
-      const uint64_t w = wave_min_u64(best_share);
-      if ((tid & 63) == 0) st_agent_u64(xrow + C + part * WAVES + (tid >> 6), w);
-    }
-    // The other parts' shares of this thread's communities.
     uint32_t need = 0;
+    if (chain_wave) {
+      // ---- graph-indexed chain into LDS (no barrier until the polls end) ----
+      const int ct = tid - COOP_SCORE_WAVES * 64;
+      constexpr int CN = SELECT_THREADS - COOP_SCORE_WAVES * 64;
+      const int cp = (C + 7) & ~7;
+      int* f_lo = fused_fields(dyn, C) + 2 * cp;
+      int* f_dc = f_lo + cp;
+      int* f_tl = f_dc + cp;
+      int* f_ts = f_tl + cp;
+      int* f_tn = f_ts + cp;
+      hist[ct] = 0;
+      hist[ct + CN] = 0;
+      hist2[ct] = 0;
+      hist2[ct + CN] = 0;
+      fused_marks(dyn, C)[ct] = -1;  // FUSED_TILES * TILE == CN marks
+      if (ct == 0) {
+        s_max_idx = -1;
+        s_sel_count = 0;
+      }
+      // Every load below is unconditional (clamped indices; dummy address when
+      // there are no sinks): a branch around a load would make the next
+      // round's address wait also cover the loads issued before it.
+      // sinks: the first chain wave holds up to 256 positions and their maximum
+      int sv[CKV_MAX_SINKS / 64];
+      {
+        const int32_t* sp = ns > 0 ? a.cfg.sink_positions : a.st.community_counts + rh;
 #pragma unroll
-    for (int k = 0; k < OWN; ++k) {
-      const int c = cid(k);
-      if (c < count && (c < sh0 || c >= sh1)) need |= 1u << k;
-    }
-    for (int poll = 0; need != 0 && poll < COOP_POLLS; ++poll) {
-      uint64_t v[OWN];
+        for (int i = 0; i < CKV_MAX_SINKS / 64; ++i) sv[i] = gload_i32(sp + max(min(ct + 64 * i, ns - 1), 0));
+      }
+      // R1: every scored row's CSR start, delta count and tail chunk, then the current position
+      constexpr int CJ = OWN * SELECT_THREADS / CN;  // rows per chain thread (nscore <= OWN * SELECT_THREADS)
+      int lo[CJ], dc[CJ], tl[CJ];
 #pragma unroll
-      for (int k = 0; k < OWN; ++k) v[k] = ld_agent_u64(xrow + min(cid(k), C - 1));
+      for (int i = 0; i < CJ; ++i) {
+        const int c = min(ct + i * CN, C - 1);
+        lo[i] = gload_i32(a.csr.member_offsets + (int64_t)graph * (C + 1) + c);
+        dc[i] = gload_i32(a.dl.community_sizes + (int64_t)graph * C + c);
+        tl[i] = gload_i32(a.dl.community_tail + (int64_t)graph * C + c);
+      }
+      CKV_STAMP_AT(rh == 0 && part == 0 && ct == 0 && graph >= 0, 15);
+      const int cur_g = a.st.current_position[graph];
+      // R2: tail chunk start and fill, the window tokens' communities, the current key
+      int ts[CJ], tn[CJ];
+      const int64_t cbase = (int64_t)graph * cpg;
+      CKV_STAMP_AT(rh == 0 && part == 0 && ct == 0 && tl[0] > -2, 23);
+      const int cpg1 = max(cpg, 1);
+      const int32_t* cstart = cpg > 0 ? a.dl.chunk_start : a.st.community_counts + rh;
+      const int32_t* csz = cpg > 0 ? a.dl.chunk_size : a.st.community_counts + rh;
 #pragma unroll
-      for (int k = 0; k < OWN; ++k) {
-        if (((need >> k) & 1u) && (v[k] & 0xffffffff00000000ull) == tag) {
-          key16[cid(k)] = (uint16_t)v[k];
-          need &= ~(1u << k);
+      for (int i = 0; i < CJ; ++i) {
+        const int t = cpg > 0 ? min(max(tl[i], 0), cpg1 - 1) : 0;
+        ts[i] = gload_i32(cstart + (cpg > 0 ? cbase + t : 0));
+        tn[i] = gload_i32(csz + (cpg > 0 ? cbase + t : 0));
+      }
+      constexpr int WJ = CKV_MAX_WINDOW / CN;
+      int wc[WJ];
+      const int32_t* tcomm = a.st.token_communities + (int64_t)graph * a.st.token_capacity;
+#pragma unroll
+      for (int h = 0; h < WJ; ++h) {
+        // (entries past the window are clamped to its first token: same lines)
+        int64_t p = (int64_t)cur_g - W + ct + h * CN;
+        p = h * CN < W ? p : (int64_t)cur_g - W;
+        wc[h] = gload_i32(tcomm + (p < 0 ? 0 : (p >= a.st.token_capacity ? a.st.token_capacity - 1 : p)));
+      }
+      // the current key (nearest-centroid assignment only: its row is in the
+      // KV cache, a page this round would otherwise not touch); issued last, so
+      // the branch around it delays no other wait
+      float kv_cur = 0.0f;
+      if (nearest_mode) {
+        const int64_t pc = cur_g < 0 ? 0 : (cur_g >= a.kv.capacity ? a.kv.capacity - 1 : cur_g);
+        kv_cur = load_elem<DT>(a.kv.key, kvh * a.kv.head_stride + pc * a.kv.token_stride + ct);
+      }
+      if (ct < 64) {
+        int m = -1;
+#pragma unroll
+        for (int i = 0; i < CKV_MAX_SINKS / 64; ++i) {
+          if (ct + 64 * i < ns) {
+            sink_s[ct + 64 * i] = sv[i];
+            m = max(m, sv[i]);
+          }
+        }
+        m = wave_max_i32(m);
+        if (ct == 0) s_sink_max = m;
+      }
+#pragma unroll
+      for (int i = 0; i < CJ; ++i) {
+        const int c = ct + i * CN;
+        if (c < nscore) {
+          const bool alive = c < count;
+          const bool has = alive && dc[i] > 0 && tl[i] >= 0 && tl[i] < cpg;
+          f_lo[c] = alive ? lo[i] : 0;
+          f_dc[c] = alive ? dc[i] : 0;
+          f_tl[c] = alive ? tl[i] : -1;
+          f_ts[c] = has ? ts[i] : 0;
+          f_tn[c] = has ? tn[i] : 0;
         }
       }
-      if (need != 0) __builtin_amdgcn_s_sleep(8);
+#pragma unroll
+      for (int h = 0; h < WJ; ++h) {
+        if (ct + h * CN < W) slot_lds[ct + h * CN] = wc[h];
+      }
+      if (nearest_mode) key_s[ct] = (cur_g >= 0 && cur_g < a.kv.capacity) ? kv_cur : 0.0f;
+      if (ct == 0) s_cur = cur_g;
+#ifdef CKV_PHASE_TIMING
+      if (rh == 0 && part == 0 && ts[0] > -2) atomicMax(&phase_stamp[28], (unsigned long long)wall_clock64());
+#endif
+    } else {
+      // ---- this part's rows, published as (epoch + 1) << 32 | fp16 bits ------
+      // The query-pair groups' maxima are combined lower group first, so the
+      // result equals the sequential maximum over the group's queries (for
+      // every non-NaN score).
+      const int st_ = tid;  // scoring thread (waves 0 .. COOP_SCORE_WAVES - 1)
+      if (ri == 0) {  // the query group in LDS for the fallback scoring
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            const int g = 2 * qp + (2 << qps_log) * j + u;
+            if (g < G) {
+#pragma unroll
+              for (int e = 0; e < 16; ++e) {
+                const uint4 w = qraw[j][u][e >> 3];
+                const uint32_t x = (e & 7) < 2 ? w.x : (e & 7) < 4 ? w.y : (e & 7) < 6 ? w.z : w.w;
+                q_s[g * D + 16 * lane8 + e] = ckv_u2f((e & 1) ? (x & 0xffff0000u) : (x << 16));
+              }
+            }
+          }
+        }
+      }
+      const int npass = (rpp + rows_pass - 1) / rows_pass;
+      for (int ps = 0; ps < npass; ++ps) {
+        const int i0 = ps * rows_pass;
+        if (part + parts * i0 >= count) break;  // no live row in this pass or later ones (uniform)
+        CentroidFrag<CT> f;
+        int fsize = 0;
+        const int i = i0 + ri;
+        const int row = part + parts * min(i, rpp - 1);
+        if (ps < COOP_PRE) {
+#pragma unroll
+          for (int k = 0; k < COOP_PRE; ++k) {
+            if (k == ps) {
+              f = cfrag[k];
+              fsize = csize[k];
+            }
+          }
+        } else {
+          load_frag<CT>(a.st.centroids, (int64_t)rh * C + min(row, nscore - 1), 16 * lane8, f);
+          fsize = gload_i32(a.st.community_sizes + (int64_t)rh * C + min(row, nscore - 1));
+        }
+        float cv[16];
+        decode_frag<CT>(f, cv);
+        float best = NEG_INF;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int g = 2 * qp + (2 << qps_log) * j;
+          if (g < G) {
+            float qa[16], qb[16];
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+              const uint4 wa = qraw[j][0][e >> 3], wb = qraw[j][1][e >> 3];
+              const int w4 = (e & 7) >> 1;
+              const uint32_t xa = w4 == 0 ? wa.x : w4 == 1 ? wa.y : w4 == 2 ? wa.z : wa.w;
+              const uint32_t xb = w4 == 0 ? wb.x : w4 == 1 ? wb.y : w4 == 2 ? wb.z : wb.w;
+              qa[e] = ckv_u2f((e & 1) ? (xa & 0xffff0000u) : (xa << 16));
+              qb[e] = ckv_u2f((e & 1) ? (xb & 0xffff0000u) : (xb << 16));
+            }
+            float a0, a1;
+            dot16_pair<CT, DT>(qa, qb, cv, a0, a1);
+            best = fmax_exact(best, a0);
+            if (g + 1 < G) best = fmax_exact(best, a1);
+          }
+        }
+        if (qps_log >= 1) best = fmax_exact(best, xor_f32<8>(best));
+        const bool in = i < rpp && row < count;
+        const bool live = in && fsize > 0;
+        const uint16_t bits = f16_bits_hw(live ? best : NEG_INF);
+        if (lane8 == 0 && qp == 0 && in) {
+          key16[row] = bits;
+          if (xcd_local) st_xcd_u64(xrow + row, tag | bits); else st_agent_u64(xrow + row, tag | bits);
+        }
+      }
+      // this wave's rows are out: its done word (no wait for their stores; the
+      // rows carry their own tag)
+      if ((tid & 63) == 0) {
+        uint64_t* done = xrow + C + COOP_FLAGS_OFF + part * COOP_WAVES + (tid >> 6);
+        if (xcd_local) st_xcd_u64(done, tag); else st_agent_u64(done, tag);
+      }
+      CKV_TS(14);
+      CKV_STAMP_MAX(rh == 0, 27);
+      {
+        // Each scoring wave polls the parts' done words (a few words per round:
+        // polling the score rows themselves from every part would load the
+        // memory system enough to slow every other round of the launch), then
+        // loads the other parts' rows among its threads' rows st_, st_ + 384,
+        // ... once, checked by tag (a row whose store has not landed yet is
+        // loaded again, bounded); a part that still misses rows scores every
+        // community itself.
+        const int lane = tid & 63;
+        const int nflag = parts * COOP_WAVES;
+        int poll = 0;
+        bool all = false;
+        for (; poll < COOP_POLLS; ++poll) {
+          uint64_t f[COOP_MAX_PARTS * COOP_WAVES / 64];
+#pragma unroll
+          for (int q = 0; q < COOP_MAX_PARTS * COOP_WAVES / 64; ++q) {
+            const int e = lane + 64 * q;
+            f[q] = ld_agent_u64(xrow + C + COOP_FLAGS_OFF + min(e, nflag - 1));
+          }
+          bool ok = true;
+#pragma unroll
+          for (int q = 0; q < COOP_MAX_PARTS * COOP_WAVES / 64; ++q) {
+            const int e = lane + 64 * q;
+            ok = ok & (e >= nflag || (e & (COOP_WAVES - 1)) >= COOP_SCORE_WAVES || f[q] == tag);
+          }
+          all = __ballot(!ok) == 0ull;
+          if (all) break;
+          __builtin_amdgcn_s_sleep(4);
+        }
+#ifdef CKV_PHASE_TIMING
+        if (rh == 0 && part == 0 && tid == 0) {
+          phase_stamp[6] = wall_clock64();
+          phase_stamp[11] = 1000000ull + poll;
+        }
+#endif
+        constexpr int SN = COOP_SCORE_WAVES * 64;
+        constexpr int PJ = (OWN * SELECT_THREADS + SN - 1) / SN;
+#pragma unroll
+        for (int k = 0; k < PJ; ++k) {
+          const int c = st_ + k * SN;
+          if (c < count && c % parts != part) need |= 1u << k;
+        }
+        for (int pr = 0; need != 0 && pr < (all ? COOP_POLLS : 1); ++pr) {
+          uint64_t v[PJ];
+#pragma unroll
+          for (int k = 0; k < PJ; ++k) v[k] = ld_agent_u64(xrow + min(st_ + k * SN, C - 1));
+#pragma unroll
+          for (int k = 0; k < PJ; ++k) {
+            if (((need >> k) & 1u) && (v[k] & 0xffffffff00000000ull) == tag) {
+              key16[st_ + k * SN] = (uint16_t)v[k];
+              need &= ~(1u << k);
+            }
+          }
+          if (need != 0) __builtin_amdgcn_s_sleep(4);
+        }
+      }
     }
-    score_all = __syncthreads_or(need != 0);
+    CKV_STAMP_AT(rh == 0 && part == 0 && tid == 0, 13);
+    score_all = __syncthreads_or(need != 0);  // key16 complete (or fallback), chain fields in LDS
+    cur = s_cur;
+    if (nearest_mode) {
+      // squared distance of the current key to this part's live rows (scoring
+      // waves; the fragments are still in registers), one minimum per wave of
+      // every part, tagged with the epoch's low 16 bits:
+      // distance bits << 32 | row << 16 | tag
+      uint64_t best_share = ~0ull;
+      if (!chain_wave) {
+        const int npass = (rpp + rows_pass - 1) / rows_pass;
+        for (int ps = 0; ps < npass; ++ps) {
+          const int i0 = ps * rows_pass;
+          if (part + parts * i0 >= count) break;
+          CentroidFrag<CT> f;
+          int fsize = 0;
+          const int i = i0 + ri;
+          const int row = part + parts * min(i, rpp - 1);
+          if (ps < COOP_PRE) {
+#pragma unroll
+            for (int k = 0; k < COOP_PRE; ++k) {
+              if (k == ps) {
+                f = cfrag[k];
+                fsize = csize[k];
+              }
+            }
+          } else {
+            load_frag<CT>(a.st.centroids, (int64_t)rh * C + min(row, nscore - 1), 16 * lane8, f);
+            fsize = gload_i32(a.st.community_sizes + (int64_t)rh * C + min(row, nscore - 1));
+          }
+          float cv[16];
+          decode_frag<CT>(f, cv);
+          float acc;
+          {
+            const float d0 = key_s[16 * lane8] - cv[0];
+            acc = d0 * d0;
+          }
+#pragma unroll
+          for (int e = 1; e < 16; ++e) {
+            const float di = key_s[16 * lane8 + e] - cv[e];
+            acc = acc + di * di;
+          }
+          acc = add_xor_f32<4>(acc);
+          acc = add_xor_f32<2>(acc);
+          acc = add_xor_f32<1>(acc);
+          if (i < rpp && row < count && fsize > 0 && qp == 0) {
+            const uint64_t cand = ((uint64_t)ckv_f2u(acc) << 32) | ((uint64_t)(uint32_t)row << 16);
+            best_share = cand < best_share ? cand : best_share;
+          }
+        }
+      }
+      const uint64_t w = wave_min_u64(best_share);
+      if ((tid & 63) == 0) st_agent_u64(xrow + C + part * WAVES + (tid >> 6), (w | 0xffffull) ^ 0xffffull ^ near_tag16(epoch));
+    }
   }
   if constexpr (PRE) {
 #pragma unroll
@@ -593,7 +871,6 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
   // barrier to broadcast them.
   int hb, above_hb;
   wave_find_bin(hist, target, hb, above_hb);
-  CKV_TS(13);
   int threshold;  // 16-bit key threshold; -1 selects every non-empty community
   if (hb < 0) {
     threshold = -1;
@@ -719,12 +996,14 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
       if (st >= 0) {
         f_idx[c] = idx;
         f_size[c] = size;
-        f_lo[c] = o_lo[k];
-        f_dc[c] = o_dc[k];
-        f_tl[c] = o_tl[k];
-        const bool has = o_dc[k] > 0 && o_tl[k] >= 0 && o_tl[k] < cpg;
-        f_ts[c] = has ? o_ts[k] : 0;
-        f_tn[c] = has ? o_tn[k] : 0;
+        if constexpr (!COOP) {  // (COOP: written by the chain waves)
+          f_lo[c] = o_lo[k];
+          f_dc[c] = o_dc[k];
+          f_tl[c] = o_tl[k];
+          const bool has = o_dc[k] > 0 && o_tl[k] >= 0 && o_tl[k] < cpg;
+          f_ts[c] = has ? o_ts[k] : 0;
+          f_tn[c] = has ? o_tn[k] : 0;
+        }
 #pragma unroll
         for (int w = 0; w < FUSED_TILES; ++w) {
           const int t0 = (part * FUSED_TILES + w) * TILE - ns;
@@ -741,6 +1020,7 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
         }
       }
     }
+    CKV_TS(16);
     {  // totals: one DPP maximum per wave, then one LDS atomic per wave
       const int wmax = wave_max_i32(my_max);
       const int wend = wave_max_i32(my_end);
@@ -749,10 +1029,12 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
         atomicMax(&s_sel_count, wend);
       }
     }
+    if constexpr (!COOP) {
 #pragma unroll
-    for (int h = 0; h < WIN_PER_THREAD; ++h) {
-      const int i = tid + h * SELECT_THREADS;
-      if (i < W) slot_lds[i] = wcomm[h];
+      for (int h = 0; h < WIN_PER_THREAD; ++h) {
+        const int i = tid + h * SELECT_THREADS;
+        if (i < W) slot_lds[i] = wcomm[h];
+      }
     }
     CKV_TS(10);
     __syncthreads();  // fields, marks, totals, window communities

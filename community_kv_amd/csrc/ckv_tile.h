@@ -311,39 +311,46 @@ __device__ inline void attend_part(const DecodeArgs& a, const int rh, const int 
   }
   __syncthreads();
   CKV_TS(20);
+  // per (wave, query) rescale factor exp(m_w - M) of the combine below
+  __shared__ float wsc_s[W][CKV_MAX_GROUP];
+  __shared__ float wM_s[CKV_MAX_GROUP];
+  if (tid < W * G) {
+    const int w = tid / G, g = tid % G;
+    float M = NEG_INF;
+#pragma unroll
+    for (int x = 0; x < W; ++x) M = fmax_exact(M, wm_s[x * CKV_MAX_GROUP + g]);
+    const float mw = wm_s[w * CKV_MAX_GROUP + g];
+    wsc_s[w][g] = mw != NEG_INF ? __expf(mw - M) : 0.0f;
+    if (w == 0) wM_s[g] = M;
+  }
   if (want_topk && wave < TP) {
     const int tile = part * TP + wave;
     if (tile < tiles) a.ws.slot_scores[(int64_t)rh * a.ws.slot_capacity + tile * TILE + lane] = cand_all[wave * TILE + lane];
   }
+  __syncthreads();
   // Combine the W wave partials into this part's split partial.
   for (int i = tid; i < G * D; i += 64 * W) {
     const int g = i >> 7;
     const int d = i & (D - 1);
-    float M = NEG_INF;
-#pragma unroll
-    for (int w = 0; w < W; ++w) M = fmax_exact(M, wm_s[w * CKV_MAX_GROUP + g]);
     float acc = 0.0f;
 #pragma unroll
     for (int w = 0; w < W; ++w) {
-      const float mw = wm_s[w * CKV_MAX_GROUP + g];
-      if (mw != NEG_INF) {
+      if (wm_s[w * CKV_MAX_GROUP + g] != NEG_INF) {
         const float* ow = reinterpret_cast<const float*>(reinterpret_cast<uint16_t*>(lds) + w * (QROWS * D));
-        acc = acc + ow[g * D + d] * __expf(mw - M);
+        acc = acc + ow[g * D + d] * wsc_s[w][g];
       }
     }
     float* dst = a.ws.partial_acc + (((int64_t)rh * G + g) * parts + part) * D + d;
     if constexpr (AGENT) st_agent_f32(dst, acc); else *dst = acc;
   }
+  CKV_TS(22);
   if (tid < G) {
-    float M = NEG_INF;
-#pragma unroll
-    for (int w = 0; w < W; ++w) M = fmax_exact(M, wm_s[w * CKV_MAX_GROUP + tid]);
     float lsum = 0.0f;
 #pragma unroll
     for (int w = 0; w < W; ++w) {
-      const float mw = wm_s[w * CKV_MAX_GROUP + tid];
-      if (mw != NEG_INF) lsum = lsum + wl_s[w * CKV_MAX_GROUP + tid] * __expf(mw - M);
+      if (wm_s[w * CKV_MAX_GROUP + tid] != NEG_INF) lsum = lsum + wl_s[w * CKV_MAX_GROUP + tid] * wsc_s[w][tid];
     }
+    const float M = wM_s[tid];
     float* pm = a.ws.partial_max + ((int64_t)rh * G + tid) * parts + part;
     float* pl = a.ws.partial_sum + ((int64_t)rh * G + tid) * parts + part;
     if constexpr (AGENT) {

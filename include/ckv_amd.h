@@ -156,9 +156,10 @@ typedef struct ckv_decode_workspace {
   int32_t* tile_descriptors;   /* [retrieval_heads][budget_tiles] */
   int32_t* selected_counts;    /* [retrieval_heads] */
   int32_t* slot_positions;     /* [retrieval_heads][slot_capacity] KV position per attended slot, -1 = none */
-  uint64_t* exchange;          /* [retrieval_heads][community_capacity + 512], zero before first use, or null:
-                                  the fused launch's workgroups of a head hand each other their share of the
-                                  centroid scores (epoch-tagged) and nearest-centroid minima through it */
+  uint64_t* exchange;          /* [retrieval_heads][community_capacity + 1024], zero before first use, or
+                                  null: the fused launch's workgroups of a head hand each other their share of
+                                  the centroid scores, done words and nearest-centroid minima through it,
+                                  epoch-tagged */
   int32_t* nearest;            /* [retrieval_heads] */
   uint32_t* block_counters;    /* [4 * retrieval_heads], zero before first use: arrival counters (the kernels
                                   leave them zero) and, at [2R, 3R), the fused launch's epoch per head */
