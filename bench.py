@@ -563,9 +563,13 @@ def run_generate(args, device):
             with torch.inference_mode():
                 out = runtime.generate(model, prompt, max_new_tokens=new_tokens)
             torch.cuda.synchronize(device)
-            return time.perf_counter() - t0, out
+            dt = time.perf_counter() - t0
+            print(f"generate: {new_tokens} new tokens after a {prompt_len}-token prompt in {dt:.2f} s",
+                  file=sys.stderr, flush=True)
+            return dt, out
 
-        for _ in range(max(0, args.warmup)):
+        # every generation repeats the prefill (and its partitions), so one warm-up is enough
+        for _ in range(min(max(0, args.warmup), 1)):
             timed(2)
         t_prefill, _ = timed(1)
         t_full, out = timed(steps + 1)

@@ -19,7 +19,7 @@ REPO_DIR = os.path.dirname(PACKAGE_DIR)
 LIB_PATH = os.path.join(PACKAGE_DIR, "libckv_amd.so")
 SOURCES = [os.path.join(PACKAGE_DIR, "csrc", name)
            for name in ("ckv_decode.hip", "ckv_select.hip", "ckv_attend.hip", "ckv_prefill.hip", "ckv_diag.hip",
-                                "ckv_state.hip", "ckv_leiden.hip", "ckv_noalloc.hip")]
+                                "ckv_state.hip", "ckv_leiden.hip", "ckv_noalloc.hip", "ckv_select_large.hip")]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 HIP_FLAGS = [
     "--offload-arch=gfx950",
@@ -42,7 +42,8 @@ TILE = 64
 KAPPA = 8
 SCORE_BLOCK = 64
 MAX_GROUP = 16
-MAX_COMMUNITIES = 8192
+MAX_COMMUNITIES = 65536
+MAX_SELECT_ROWS = 8192
 MAX_DESCRIPTORS = 4096
 MAX_SINKS = 256
 MAX_WINDOW = 1024

@@ -47,7 +47,7 @@ int validate(const ckv_kv_cache* kv, const ckv_graph_state* st, const ckv_prefil
     return fail(CKV_E_INVALID, "incomplete graph state");
   if (st->retrieval_heads * cfg->group_size != kv->query_heads)
     return fail(CKV_E_INVALID, "query heads must equal retrieval heads x group size");
-  if (st->community_capacity > CKV_MAX_COMMUNITIES) return fail(CKV_E_LIMIT, "community capacity exceeds 8192");
+  if (st->community_capacity > CKV_MAX_COMMUNITIES) return fail(CKV_E_LIMIT, "community capacity exceeds 65536");
   if (ws->descriptor_capacity <= 0 || ws->descriptor_capacity > CKV_MAX_DESCRIPTORS)
     return fail(CKV_E_LIMIT, "descriptor capacity must be in [1, 4096]");
   if (ws->slot_capacity <= 0 || ws->slot_capacity % CKV_TILE || ws->slot_capacity > 2048 * CKV_TILE)
@@ -304,6 +304,8 @@ int validate_batch(const ckv_layer_args* items, int count, std::vector<ckv::Deco
     if (rc) return rc;
     const ckv::DecodeArgs a = pack(it.kv, it.state, it.csr, it.deltas, it.config, it.ws);
     if (a.kv.dtype != CKV_BF16) return fail(CKV_E_INVALID, "batched decode requires bf16 KV");
+    if (std::min(a.st.community_capacity, a.ws.score_blocks * CKV_SCORE_BLOCK) > CKV_MAX_SELECT_ROWS)
+      return fail(CKV_E_LIMIT, "batched decode scores at most 8192 communities per head (use ckv_decode_layer)");
     if (ckv::attention_batch_splits(a) == 0)
       return fail(CKV_E_LIMIT, "batched decode requires group_size * 128 <= 512 and at most 64 attention splits");
     if (i > 0) {
@@ -319,8 +321,9 @@ int validate_batch(const ckv_layer_args* items, int count, std::vector<ckv::Deco
     }
     packed->push_back(a);
     *max_nscore = std::max(*max_nscore, std::min(a.st.community_capacity, a.ws.score_blocks * CKV_SCORE_BLOCK));
-    *max_lds = std::max(*max_lds, ckv::select_lds_bytes(a.st.community_capacity, a.ws.descriptor_capacity,
-                                                        a.cfg.max_selected));
+    *max_lds = std::max(*max_lds, ckv::select_lds_bytes(std::min(a.st.community_capacity,
+                                                                 a.ws.score_blocks * CKV_SCORE_BLOCK),
+                                                        a.ws.descriptor_capacity, a.cfg.max_selected));
     if (a.st.retrieval_heads != a.st.graph_count) *any_shared = true;
   }
   return CKV_OK;

@@ -551,12 +551,16 @@ __device__ inline void wave_find_bin(const int* hist, int target, int& out_bin, 
 
 // Host-side launchers (one per translation unit), called after validation.
 int launch_score_select(const DecodeArgs& a, hipStream_t stream, const DecodeArgs* pending_update = nullptr);
+// More than CKV_MAX_SELECT_ROWS scored rows per head: score_rows_kernel on every
+// compute unit, then select_large_kernel (ckv_select_large.hip).
+bool large_selection(const DecodeArgs& a);
+int launch_select_large(const DecodeArgs& a, hipStream_t stream);
 int launch_sync_shared(const DecodeArgs& a, hipStream_t stream);
 int launch_attention(const DecodeArgs& a, hipStream_t stream, bool partials_only);
 int launch_update(const DecodeArgs& a, hipStream_t stream);
 // Merge of `splits` bf16 partials (group * 128 <= 512, splits <= 64) + online update in one launch.
 int launch_merge_update(const DecodeArgs& a, hipStream_t stream, int splits);
-size_t select_lds_bytes(int community_capacity, int descriptor_capacity, int max_selected);
+size_t select_lds_bytes(int scored_rows, int descriptor_capacity, int max_selected);
 int attention_batch_splits(const DecodeArgs& a);  // 0 when the batched attention cannot serve `a`
 int fused_parts(const DecodeArgs& a);              // 0 when the fused selection + attention cannot serve `a`
 size_t fused_lds_bytes(const DecodeArgs& a);

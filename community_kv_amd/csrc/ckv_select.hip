@@ -151,6 +151,7 @@ __device__ __forceinline__ void coop_finish(const DecodeArgs& a, const int rh, c
     st_agent_u32(a.ws.block_counters + 2 * a.st.retrieval_heads + rh, epoch + 1u);
   }
   CKV_STAMP(rh == 0, 25);
+  CKV_STAMP_MAX(true, 30);
 }
 
 // OWN: communities owned per thread (thread t owns [t*OWN, (t+1)*OWN), so id
@@ -223,7 +224,9 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
   unsigned char* dyn = dyn_all + (FUSED ? fused_slot_bytes(a.ws.slot_capacity) : 0);
   uint16_t* key16 = reinterpret_cast<uint16_t*>(dyn);  // masked fp16 score bits of every scored community
   const int dcap = a.ws.descriptor_capacity;
-  int* desc_comm = reinterpret_cast<int*>(dyn + (size_t)((C + 7) & ~7) * 2);
+  // (unfused: the key table holds the scored rows only, so a large capacity
+  // with few scored rows keeps the LDS small)
+  int* desc_comm = reinterpret_cast<int*>(dyn + (size_t)(((FUSED ? C : nscore) + 7) & ~7) * 2);
   int* desc_end = desc_comm + dcap;  // cumulative selected-token end
   int* desc_lo = desc_end + dcap;    // CSR start of the community
   int* desc_dc = desc_lo + dcap;     // decode-delta member count
@@ -1534,16 +1537,23 @@ __global__ __launch_bounds__(SELECT_THREADS) void select_batch_kernel(const Deco
   select_body<CT, DT, OWN>(table[blockIdx.x / heads], blockIdx.x % heads);
 }
 
-// key16 / community table, the descriptor arrays, the per-block descriptor index.
-size_t select_lds_bytes(int community_capacity, int descriptor_capacity, int max_selected) {
-  return (size_t)((community_capacity + 7) & ~7) * 2 + (size_t)descriptor_capacity * DESC_ARRAYS * 4 +
+// key16 / community table (scored rows), the descriptor arrays, the per-block descriptor index.
+size_t select_lds_bytes(int scored_rows, int descriptor_capacity, int max_selected) {
+  return (size_t)((scored_rows + 7) & ~7) * 2 + (size_t)descriptor_capacity * DESC_ARRAYS * 4 +
          (size_t)((max_selected + 63) / 64 + 2) * 4;
 }
 
 int launch_score_select(const DecodeArgs& a, hipStream_t s, const DecodeArgs* pending) {
-  const size_t lds = select_lds_bytes(a.st.community_capacity, a.ws.descriptor_capacity, a.cfg.max_selected);
+  if (large_selection(a)) {  // scoring on every compute unit, then the multi-kernel selection
+    if (pending != nullptr) {
+      const int rc = launch_update(*pending, s);
+      if (rc) return rc;
+    }
+    return launch_select_large(a, s);
+  }
   const int ct = a.st.centroid_dtype, dt = a.kv.dtype;
   const int nscore = std::min(a.st.community_capacity, a.ws.score_blocks * SCORE_BLOCK);
+  const size_t lds = select_lds_bytes(nscore, a.ws.descriptor_capacity, a.cfg.max_selected);
   const int own = (nscore + SELECT_THREADS - 1) / SELECT_THREADS;
   auto launch = [&](auto kernel) {
     if (lds > 48 * 1024) {
@@ -1564,7 +1574,7 @@ int launch_score_select(const DecodeArgs& a, hipStream_t s, const DecodeArgs* pe
     hipLaunchKernelGGL(kernel, dim3(a.st.retrieval_heads + extra), dim3(SELECT_THREADS), lds, s, a, u);
     return launch_check("select");
   };
-  constexpr int OWN_MAX = CKV_MAX_COMMUNITIES / SELECT_THREADS;
+  constexpr int OWN_MAX = CKV_MAX_SELECT_ROWS / SELECT_THREADS;
   auto by_own = [&](auto k1, auto k2, auto kmax) {
     return own <= 1 ? launch(k1) : own <= 2 ? launch(k2) : launch(kmax);
   };
@@ -1630,7 +1640,7 @@ int launch_select_attend(const DecodeArgs& a, hipStream_t s, const DecodeArgs* p
                        parts);
     return launch_check("select_attend");
   };
-  constexpr int OWN_MAX = CKV_MAX_COMMUNITIES / SELECT_THREADS;
+  constexpr int OWN_MAX = CKV_MAX_SELECT_ROWS / SELECT_THREADS;
   if (coop) {
     if (coop_parts(a) != parts) return limit_error("the cooperative fused launch cannot serve this layer");
     // the merge loads PMAX accumulators per output element (clamped to the parts)
@@ -1669,7 +1679,7 @@ int launch_batch_select_attend(const DecodeArgs& h, const DecodeArgs* table, int
                        h.st.retrieval_heads, parts);
     return launch_check("select_attend_batch");
   };
-  constexpr int OWN_MAX = CKV_MAX_COMMUNITIES / SELECT_THREADS;
+  constexpr int OWN_MAX = CKV_MAX_SELECT_ROWS / SELECT_THREADS;
   if (h.st.centroid_dtype == CKV_E4M3) {
     return own <= 1 ? launch(select_attend_batch_kernel<CKV_E4M3, CKV_BF16, 1>)
            : own <= 2 ? launch(select_attend_batch_kernel<CKV_E4M3, CKV_BF16, 2>)
@@ -1717,7 +1727,7 @@ int launch_batch_select(const DecodeArgs& h, const DecodeArgs* table, int count,
                        h.st.retrieval_heads);
     return launch_check("select_batch");
   };
-  constexpr int OWN_MAX = CKV_MAX_COMMUNITIES / SELECT_THREADS;
+  constexpr int OWN_MAX = CKV_MAX_SELECT_ROWS / SELECT_THREADS;
   if (pre) {
     if (h.st.centroid_dtype == CKV_E4M3) {
       return own <= 4 ? launch(select_prescored_batch_kernel<CKV_E4M3, CKV_BF16, 4>)

@@ -26,6 +26,8 @@
 //   weight_zero_kernel + topk_weight_kernel   the same weights from the prefill top-k edges
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include <stdint.h>
 
 #include "ckv_device.h"
@@ -40,6 +42,7 @@ constexpr int SUM_BLOCK = 64;            // members per centroid partial sum
 constexpr int COUNT_THREADS = 1024;
 constexpr int SCAN_THREADS = 1024;
 constexpr int HIST_THREADS = 256;
+constexpr int STATE_LDS_COMMUNITIES = 16384;  // per-community LDS counters of one kernel (64 KB)
 constexpr int CENTROID_WAVES = 4;        // community rows per centroid workgroup
 constexpr int EDGE_THREADS = 256;
 
@@ -120,23 +123,27 @@ __global__ __launch_bounds__(COUNT_THREADS) void label_count_kernel(const int32_
 }
 
 // hist[g][chunk][c]: members of community c among the chunk's positions.
+// Communities below lds_n are counted in LDS, the others in the output row.
 __global__ __launch_bounds__(HIST_THREADS) void chunk_hist_kernel(const int32_t* __restrict__ labels, int seq_len,
-                                                                  int num_sink, int maxc, int chunk_len, int chunks,
-                                                                  int32_t* __restrict__ hist) {
+                                                                  int num_sink, int maxc, int lds_n, int chunk_len,
+                                                                  int chunks, int32_t* __restrict__ hist) {
   extern __shared__ int h_s[];
   const int chunk = blockIdx.x, g = blockIdx.y;
-  for (int c = threadIdx.x; c < maxc; c += HIST_THREADS) h_s[c] = 0;
+  int32_t* out = hist + ((int64_t)g * chunks + chunk) * maxc;
+  for (int c = threadIdx.x; c < lds_n; c += HIST_THREADS) h_s[c] = 0;
+  for (int c = lds_n + threadIdx.x; c < maxc; c += HIST_THREADS) out[c] = 0;
+  wait_vm();  // the zeroed row is in place before any workgroup thread adds to it
   __syncthreads();
   const int32_t* row = labels + (int64_t)g * seq_len;
   const int p0 = num_sink + chunk * chunk_len;
   const int p1 = min(p0 + chunk_len, seq_len);
   for (int p = p0 + threadIdx.x; p < p1; p += HIST_THREADS) {
     const int c = row[p];
-    if (c >= 0 && c < maxc) atomicAdd(h_s + c, 1);
+    if (c >= 0 && c < lds_n) atomicAdd(h_s + c, 1);
+    else if (c >= lds_n && c < maxc) atomicAdd(out + c, 1);
   }
   __syncthreads();
-  int32_t* out = hist + ((int64_t)g * chunks + chunk) * maxc;
-  for (int c = threadIdx.x; c < maxc; c += HIST_THREADS) out[c] = h_s[c];
+  for (int c = threadIdx.x; c < lds_n; c += HIST_THREADS) out[c] = h_s[c];
 }
 
 // Per graph: offsets[c] = members of communities below c; then every chunk's
@@ -213,15 +220,17 @@ __global__ __launch_bounds__(SCAN_THREADS) void csr_scan_kernel(int maxc, int ch
 // down, 64 at a time (lane l takes the l-th newest); lanes with equal labels
 // are ranked by lane (newer first) one distinct label per round, and an LDS
 // cursor per community advances by each round's members.
+// Cursors of communities below lds_n live in LDS, the others in the chunk's
+// histogram row (which nothing reads afterwards).
 __global__ __launch_bounds__(64) void csr_scatter_kernel(const int32_t* __restrict__ labels, int seq_len, int num_sink,
-                                                         int maxc, int chunk_len, int chunks,
-                                                         const int32_t* __restrict__ hist,
+                                                         int maxc, int lds_n, int chunk_len, int chunks,
+                                                         int32_t* __restrict__ hist,
                                                          int32_t* __restrict__ member_positions) {
   extern __shared__ int cur_s[];
   const int chunk = blockIdx.x, g = blockIdx.y;
   const int lane = threadIdx.x;
-  const int32_t* h = hist + ((int64_t)g * chunks + chunk) * maxc;
-  for (int c = lane; c < maxc; c += 64) cur_s[c] = h[c];
+  int32_t* h = hist + ((int64_t)g * chunks + chunk) * maxc;
+  for (int c = lane; c < lds_n; c += 64) cur_s[c] = h[c];
   wave_sync();
   const int32_t* row = labels + (int64_t)g * seq_len;
   int32_t* out = member_positions + (int64_t)g * (seq_len - num_sink);
@@ -238,10 +247,14 @@ __global__ __launch_bounds__(64) void csr_scatter_kernel(const int32_t* __restri
       const int leader = __builtin_ctzll(todo);
       const int lc = __builtin_amdgcn_readlane(c, leader);
       const uint64_t m = __ballot(valid && c == lc);
-      const int base = cur_s[lc];
+      const int base = lc < lds_n ? cur_s[lc] : h[lc];
       if (valid && c == lc) out[base + __popcll(m & below)] = p;
       wave_sync();
-      if (lane == leader) cur_s[lc] = base + __popcll(m);
+      if (lane == leader) {
+        if (lc < lds_n) cur_s[lc] = base + __popcll(m);
+        else h[lc] = base + __popcll(m);
+      }
+      if (lc >= lds_n) wait_vm();  // (wave-uniform) the cursor store lands before a later round reads it
       wave_sync();
       todo &= ~m;
     }
@@ -537,7 +550,7 @@ extern "C" int ckv_build_layer_state(const ckv_state_build_args* a, void* stream
       a->retrieval_heads <= 0 || a->kv_heads <= 0)
     return ckv_internal::set_error(CKV_E_INVALID, "bad graph, head or sequence sizes (num_sink < seq_len)");
   if (a->max_communities <= 0 || a->max_communities > CKV_MAX_COMMUNITIES)
-    return ckv_internal::set_error(CKV_E_LIMIT, "max_communities must be in [1, 8192]");
+    return ckv_internal::set_error(CKV_E_LIMIT, "max_communities must be in [1, 65536]");
   if (a->community_capacity < a->max_communities)
     return ckv_internal::set_error(CKV_E_INVALID, "community_capacity must cover max_communities");
   if (a->token_capacity < a->seq_len) return ckv_internal::set_error(CKV_E_INVALID, "token_capacity < seq_len");
@@ -566,13 +579,15 @@ extern "C" int ckv_build_layer_state(const ckv_state_build_args* a, void* stream
   const int64_t mb = state_max_blocks(a->seq_len, a->num_sink, maxc);
   StateWorkspace w;
   state_ws_words(a->graphs, a->retrieval_heads, a->seq_len, a->num_sink, maxc, &w, a->workspace);
-  const size_t lds = (size_t)maxc * sizeof(int);
+  // communities past lds_n are counted in global memory (64 KB of LDS per kernel)
+  const int lds_n = std::min(maxc, STATE_LDS_COMMUNITIES);
+  const size_t lds = (size_t)lds_n * sizeof(int);
   hipLaunchKernelGGL(chunk_hist_kernel, dim3(chunks, a->graphs), dim3(HIST_THREADS), lds, s, a->labels, a->seq_len,
-                     a->num_sink, maxc, chunk_len, chunks, w.hist);
+                     a->num_sink, maxc, lds_n, chunk_len, chunks, w.hist);
   hipLaunchKernelGGL(csr_scan_kernel, dim3(a->graphs), dim3(SCAN_THREADS), 0, s, maxc, chunks, mb, w.hist,
                      a->member_offsets, w.blk_first, w.blk_comm);
   hipLaunchKernelGGL(csr_scatter_kernel, dim3(chunks, a->graphs), dim3(64), lds, s, a->labels, a->seq_len,
-                     a->num_sink, maxc, chunk_len, chunks, (const int32_t*)w.hist, a->member_positions);
+                     a->num_sink, maxc, lds_n, chunk_len, chunks, w.hist, a->member_positions);
   const dim3 bgrid((unsigned)((mb + CENTROID_WAVES - 1) / CENTROID_WAVES), a->retrieval_heads);
   auto sums = [&](auto kernel) {
     hipLaunchKernelGGL(kernel, bgrid, dim3(64 * CENTROID_WAVES), 0, s, a->keys, a->head_stride, a->token_stride,
@@ -599,14 +614,14 @@ extern "C" int ckv_build_layer_state(const ckv_state_build_args* a, void* stream
     if (a->topk_indices && a->topk_rows > 0) {
       hipLaunchKernelGGL(topk_weight_kernel,
                          dim3((a->topk_rows + TOPK_ROWS_PER_WG - 1) / TOPK_ROWS_PER_WG, a->topk_heads),
-                         dim3(TOPK_ROWS_PER_WG), (size_t)maxc * sizeof(float), s, a->labels,
-                         a->seq_len, a->community_capacity, maxc, a->topk_indices, a->topk_scores, a->topk_rows,
+                         dim3(TOPK_ROWS_PER_WG), (size_t)lds_n * sizeof(float), s, a->labels,
+                         a->seq_len, a->community_capacity, lds_n, a->topk_indices, a->topk_scores, a->topk_rows,
                          a->topk_kappa, a->topk_group, a->topk_row0, a->lam, a->community_weight, a->total_weight);
     }
     if (a->edges > 0) {
       hipLaunchKernelGGL(edge_weight_kernel, dim3((unsigned)((a->edges + EDGES_PER_WG - 1) / EDGES_PER_WG)),
-                         dim3(EDGE_THREADS), (size_t)maxc * sizeof(float), s, a->labels, a->seq_len, a->graphs,
-                         a->community_capacity, maxc, a->edge_src, a->edge_dst, a->edge_weight, a->edges, a->community_weight, a->total_weight);
+                         dim3(EDGE_THREADS), (size_t)lds_n * sizeof(float), s, a->labels, a->seq_len, a->graphs,
+                         a->community_capacity, lds_n, a->edge_src, a->edge_dst, a->edge_weight, a->edges, a->community_weight, a->total_weight);
     }
   }
   return launch_check();

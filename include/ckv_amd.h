@@ -55,7 +55,9 @@ extern "C" {
 #define CKV_KAPPA 8
 #define CKV_SCORE_BLOCK 64
 #define CKV_MAX_GROUP 16
-#define CKV_MAX_COMMUNITIES 8192
+#define CKV_MAX_COMMUNITIES 65536   /* community capacity per graph state */
+#define CKV_MAX_SELECT_ROWS 8192    /* scored rows per head that one selection workgroup holds in registers;
+                                       more go through the multi-kernel selection */
 #define CKV_MAX_DESCRIPTORS 4096
 #define CKV_MAX_SINKS 256
 #define CKV_MAX_WINDOW 1024

@@ -129,9 +129,12 @@ def build_layer(*, seed, query_heads, kv_heads, seq_len, communities, num_sink=1
     # members of its community, weight lam/2 * U(0.05, 0.5).
     src, dst, w = [], [], []
     for g in range(graphs):
-        lab = labels[g]
+        lab = labels[g, num_sink:]
+        # members of every community in ascending position order (one stable sort)
+        order = np.argsort(lab, kind="stable")
+        bounds = np.searchsorted(lab[order], np.arange(int(counts[g]) + 1))
         for c in range(int(counts[g])):
-            members = np.flatnonzero(lab[num_sink:] == c) + num_sink
+            members = order[bounds[c]:bounds[c + 1]] + num_sink
             if len(members) < 2:
                 continue
             for _ in range(2):

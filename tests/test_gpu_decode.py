@@ -86,6 +86,15 @@ CASES = {
                                       max_decode_tokens=8, aggregation=co.QUERY_GROUP),
                                  dict(group_size=4, num_sink=10, token_budget=1024, local_window=64,
                                       assignment="nearest_centroid")),
+    # more than 8192 scored communities per head: scoring on every compute unit,
+    # then the multi-kernel selection (the reference selector's 65,536-community range)
+    "communities_12000_bf16": (dict(query_heads=8, kv_heads=2, seq_len=49152, communities=12000, num_sink=10,
+                                    max_decode_tokens=8, aggregation=co.QUERY_GROUP),
+                               dict(group_size=4, num_sink=10, token_budget=2048, local_window=128)),
+    "communities_40000_nearest": (dict(query_heads=4, kv_heads=1, seq_len=98304, communities=40000, num_sink=10,
+                                       max_decode_tokens=8, aggregation=co.QUERY_GROUP),
+                                  dict(group_size=4, num_sink=10, token_budget=4096, local_window=256,
+                                       assignment="nearest_centroid")),
     # few large communities: decode deltas pile up in a few chains of several geometric chunks
     "deep_delta_chains_bf16": (dict(query_heads=8, kv_heads=2, seq_len=2048, communities=6, num_sink=10,
                                     max_decode_tokens=40, aggregation=co.QUERY_GROUP),
@@ -104,7 +113,8 @@ CASES = {
                          max_decode_tokens=16, aggregation=co.QUERY_GROUP),
                     dict(group_size=8, num_sink=10, token_budget=320, local_window=64)),
 }
-STEPS = {"communities_1500_bf16": 4, "communities_2600_nearest": 4, "deep_delta_chains_bf16": 36,
+STEPS = {"communities_1500_bf16": 4, "communities_2600_nearest": 4, "communities_12000_bf16": 3,
+         "communities_40000_nearest": 3, "deep_delta_chains_bf16": 36,
          "topk_all_nearest_bf16": 12}
 
 

@@ -45,6 +45,8 @@ CASES = [
     (1, 3000, 4, 40, [0, 0, 0, 0], [0, 1, 2, 3], torch.float32, False, False, 5000),
     (3, 64, 0, 1, [0, 1, 2], [2, 1, 0], torch.bfloat16, True, False, 0),
     (4, 9000, 10, 2000, [0, 1, 2, 3], [0, 1, 2, 3], torch.bfloat16, True, True, 0),
+    # more communities than the kernels' LDS counters (16,384): the rest counted in global memory
+    (2, 60000, 10, 30000, [0, 1], [0, 1], torch.bfloat16, True, False, 100000),
     # config 2 shape: 8 graphs x 32k positions, 512 Zipf communities, prefill-sized edge list
     (8, 32768, 10, 512, list(range(8)), list(range(8)), torch.bfloat16, True, True, 400000),
 ]
