@@ -344,7 +344,12 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_mfma_kernel(ckv_pref
     // PV^T MFMAs are issued: the rare branch runs while they drain.
     uint32_t thr = max(max(q_min, swap32_u32(q_min)), row_thr);
     float tf = prefilter(thr);
+#ifdef CKV_PF_NO_TOPK
+    const bool inspect = false;
+#else
     const bool inspect = lmax >= tf;
+#endif
+    bool inserted = false;
     if (inspect) {
       uint32_t qk[QN];
       load_queue(qk);
@@ -360,6 +365,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_mfma_kernel(ckv_pref
             if (sv >= tf && col >= num_sink) {
               const uint32_t cand = (quantise_score(sv) << 17) | (uint32_t)(col + 1);
               if (cand > thr) {
+                inserted = true;
                 queue_insert<QN>(qk, cand);
                 thr = max(thr, qk[QN - 1]);
                 tf = prefilter(thr);
@@ -376,7 +382,11 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_mfma_kernel(ckv_pref
     // over both halves' queues (the minimum of the bitonic top-QN of their
     // union).  No later candidate below it can reach the row's top QN, so it
     // is the tighter threshold for both halves.
+#ifdef CKV_PF_REFRESH_ON_INSERT
+    if (__builtin_amdgcn_ballot_w64(inserted)) {
+#else
     if (__builtin_amdgcn_ballot_w64(inspect)) {
+#endif
       uint32_t mine[QN];
       load_queue(mine);
       uint32_t rt = 0xffffffffu;
