@@ -328,18 +328,22 @@ __device__ inline void attend_part(const DecodeArgs& a, const int rh, const int 
     if (tile < tiles) a.ws.slot_scores[(int64_t)rh * a.ws.slot_capacity + tile * TILE + lane] = cand_all[wave * TILE + lane];
   }
   __syncthreads();
-  // Combine the W wave partials into this part's split partial.
+  // Combine the W wave partials into this part's split partial.  A wave
+  // without a valid slot has factor 0 and P.V rows of zeros, so adding its
+  // (signed) zero leaves the sum unchanged: no branch, every LDS read issued
+  // before the first multiply.
   for (int i = tid; i < G * D; i += 64 * W) {
     const int g = i >> 7;
     const int d = i & (D - 1);
-    float acc = 0.0f;
+    float ov[W], sc[W];
 #pragma unroll
     for (int w = 0; w < W; ++w) {
-      if (wm_s[w * CKV_MAX_GROUP + g] != NEG_INF) {
-        const float* ow = reinterpret_cast<const float*>(reinterpret_cast<uint16_t*>(lds) + w * (QROWS * D));
-        acc = acc + ow[g * D + d] * wsc_s[w][g];
-      }
+      ov[w] = reinterpret_cast<const float*>(reinterpret_cast<uint16_t*>(lds) + w * (QROWS * D))[g * D + d];
+      sc[w] = wsc_s[w][g];
     }
+    float acc = 0.0f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) acc = acc + ov[w] * sc[w];
     float* dst = a.ws.partial_acc + (((int64_t)rh * G + g) * parts + part) * D + d;
     if constexpr (AGENT) st_agent_f32(dst, acc); else *dst = acc;
   }
