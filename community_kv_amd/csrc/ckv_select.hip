@@ -51,9 +51,10 @@ int limit_error(const char* message) { return ckv_internal::set_error(CKV_E_LIMI
 constexpr int ROWS_PER_PASS = SELECT_THREADS / 8;          // centroid rows scored per pass
 constexpr int MAT_BATCH = 8;                               // 64-slot blocks per wave gathered together
 constexpr int DESC_ARRAYS = 7;                             // per-descriptor LDS arrays
-// Dynamic LDS the fused kernel may use (the selection's static arrays take
-// about 12 KB of the CU's 160 KB).
-constexpr size_t FUSED_LDS_LIMIT = 144 * 1024;
+// Dynamic LDS the fused kernel may use: a workgroup's 160 KB less the static
+// arrays (up to 24 KB in the fused instances, by the compiler's resource
+// report), with 2 KB to spare.
+constexpr size_t FUSED_LDS_LIMIT = 134 * 1024;
 // 64-slot tiles attended per workgroup of the fused path (parts per head = tiles / this).
 constexpr int FUSED_TILES = 2;
 // Cooperative fused launch: polling rounds (each a memory round trip plus a
