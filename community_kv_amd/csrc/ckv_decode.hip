@@ -168,6 +168,18 @@ extern "C" int ckv_attention_partials(const ckv_kv_cache* kv, const ckv_graph_st
   return ckv::launch_attention(pack(kv, st, csr, dl, cfg, ws), reinterpret_cast<hipStream_t>(stream), true);
 }
 
+// Parts per head of the fused launch for one layer, or 0 for the separate
+// selection, attention and merge launches: the cooperative launch shares the
+// scoring between a head's parts; without it every fused workgroup repeats
+// its head's whole selection, worth it only while the copies run side by
+// side, one per compute unit (with 32 per-query-head graphs and a 4,096-token
+// budget, 1,024 workgroups would run four rounds of full selections).
+static int single_fused_parts(const ckv::DecodeArgs& a) {
+  const int parts = ckv::fused_parts(a);
+  if (parts > 0 && ckv::coop_parts(a) == 0 && (int64_t)a.st.retrieval_heads * parts > FUSED_MAX_WORKGROUPS) return 0;
+  return parts;
+}
+
 extern "C" int ckv_decode_layer(const ckv_kv_cache* kv, const ckv_graph_state* st, const ckv_prefill_csr* csr,
                                 const ckv_delta_chunks* dl, const ckv_decode_config* cfg,
                                 ckv_decode_workspace* ws, void* stream) {
@@ -176,7 +188,7 @@ extern "C" int ckv_decode_layer(const ckv_kv_cache* kv, const ckv_graph_state* s
   if (rc) return rc;
   const ckv::DecodeArgs a = pack(kv, st, csr, dl, cfg, ws);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const int parts = ckv::fused_parts(a);
+  const int parts = single_fused_parts(a);
   if (ckv::coop_parts(a) > 0) {  // merged inside the launch; the update follows
     rc = ckv::launch_select_attend(a, s, nullptr, parts, true);
     return rc ? rc : ckv::launch_update(a, s);
@@ -222,7 +234,7 @@ extern "C" int ckv_decode_step_after_update(const ckv_layer_args* layer, const c
   if (rc) return rc;
   const ckv::DecodeArgs a = pack(layer->kv, layer->state, layer->csr, layer->deltas, layer->config, layer->ws);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const int parts = ckv::fused_parts(a);
+  const int parts = single_fused_parts(a);
   if (parts == 0) {
     rc = ckv_score_select_after_update(layer, pending, stream);
     return rc ? rc : ckv::launch_attention(a, s, false);

@@ -551,10 +551,12 @@ __device__ inline void wave_find_bin(const int* hist, int target, int& out_bin, 
 
 // Host-side launchers (one per translation unit), called after validation.
 int launch_score_select(const DecodeArgs& a, hipStream_t stream, const DecodeArgs* pending_update = nullptr);
-// More than CKV_MAX_SELECT_ROWS scored rows per head: score_rows_kernel on every
-// compute unit, then select_large_kernel (ckv_select_large.hip).
+// More than LARGE_MIN_ROWS (1,024) scored rows per head on the separate
+// selection launch: score_rows_kernel on every compute unit (with another
+// layer's pending update, same dtypes, on extra workgroups), then
+// select_large_kernel (ckv_select_large.hip).
 bool large_selection(const DecodeArgs& a);
-int launch_select_large(const DecodeArgs& a, hipStream_t stream);
+int launch_select_large(const DecodeArgs& a, hipStream_t stream, const DecodeArgs* pending = nullptr);
 int launch_sync_shared(const DecodeArgs& a, hipStream_t stream);
 int launch_attention(const DecodeArgs& a, hipStream_t stream, bool partials_only);
 int launch_update(const DecodeArgs& a, hipStream_t stream);

@@ -1545,13 +1545,8 @@ size_t select_lds_bytes(int scored_rows, int descriptor_capacity, int max_select
 }
 
 int launch_score_select(const DecodeArgs& a, hipStream_t s, const DecodeArgs* pending) {
-  if (large_selection(a)) {  // scoring on every compute unit, then the multi-kernel selection
-    if (pending != nullptr) {
-      const int rc = launch_update(*pending, s);
-      if (rc) return rc;
-    }
-    return launch_select_large(a, s);
-  }
+  if (large_selection(a))  // scoring (and the pending update) on every compute unit, then the selection
+    return launch_select_large(a, s, pending);
   const int ct = a.st.centroid_dtype, dt = a.kv.dtype;
   const int nscore = std::min(a.st.community_capacity, a.ws.score_blocks * SCORE_BLOCK);
   const size_t lds = select_lds_bytes(nscore, a.ws.descriptor_capacity, a.cfg.max_selected);

@@ -20,6 +20,7 @@
 // to the multi-kernel selector, attention/kernels/_csrc/descriptor_selection.cu:
 // 852-1189).
 #include <algorithm>
+#include <cstring>
 
 #include "ckv_device.h"
 #include "ckv_error.h"
@@ -31,6 +32,10 @@ namespace ckv {
 namespace {
 
 constexpr int ROWS = SELECT_THREADS / 8;  // rows scored per workgroup (8 lanes per row)
+// Scored rows per head above which the separate selection launch scores on
+// every compute unit and selects with 1,024 threads per head (one 512-thread
+// workgroup scoring and selecting 2,048 rows alone takes ~40 us)
+constexpr int LARGE_MIN_ROWS = 1024;
 constexpr int LT = 1024;                  // select_large_kernel threads
 constexpr int LWAVES = LT / 64;
 constexpr int MAT_BATCH_L = 4;            // 64-slot blocks per wave gathered together
@@ -41,9 +46,19 @@ int limit_error(const char* message) { return ckv_internal::set_error(CKV_E_LIMI
 
 // Scores (and, in nearest-centroid mode, block minima of the squared distance
 // to the current key: distance bits << 32 | row, into exchange[rh][C + block])
-// of rows [64 * blockIdx.x, +64) of head blockIdx.y.
-template <int CT, int DT>
-__global__ __launch_bounds__(SELECT_THREADS) void score_rows_kernel(DecodeArgs a) {
+// of rows [64 * blockIdx.x, +64) of head blockIdx.y.  UPD: the workgroups of
+// row blockIdx.y == a.st.retrieval_heads run the pending online update of
+// another layer `u` (same dtypes), heads blockIdx.x, blockIdx.x + gridDim.x, ...
+// on the compute units the scoring leaves idle.
+template <int CT, int DT, bool UPD = false>
+__global__ __launch_bounds__(SELECT_THREADS) void score_rows_kernel(DecodeArgs a, DecodeArgs u) {
+  if constexpr (UPD) {
+    if ((int)blockIdx.y >= a.st.retrieval_heads) {
+      for (int urh = blockIdx.x; urh < u.st.retrieval_heads; urh += gridDim.x)
+        owner_update<CT, DT>(u, urh, u.ws.lse[(int64_t)urh * u.cfg.group_size]);
+      return;
+    }
+  }
   __shared__ float q_s[CKV_MAX_GROUP * D];
   __shared__ float key_s[D];
   __shared__ uint64_t near_s[SELECT_THREADS / 64];
@@ -539,18 +554,25 @@ __global__ __launch_bounds__(LT) void select_large_kernel(DecodeArgs a) {
 }
 
 bool large_selection(const DecodeArgs& a) {
-  return std::min(a.st.community_capacity, a.ws.score_blocks * SCORE_BLOCK) > CKV_MAX_SELECT_ROWS;
+  return std::min(a.st.community_capacity, a.ws.score_blocks * SCORE_BLOCK) > LARGE_MIN_ROWS;
 }
 
-int launch_select_large(const DecodeArgs& a, hipStream_t s) {
+int launch_select_large(const DecodeArgs& a, hipStream_t s, const DecodeArgs* pending) {
   const int nscore = std::min(a.st.community_capacity, a.ws.score_blocks * SCORE_BLOCK);
   if (nscore > CKV_MAX_COMMUNITIES) return limit_error("more than 65536 scored communities per head");
   if (a.cfg.assignment == CKV_ASSIGN_NEAREST && a.ws.exchange == nullptr)
     return limit_error("nearest-centroid assignment above 8192 scored communities needs the exchange workspace");
   const size_t lds = large_lds_bytes(a.ws.descriptor_capacity, a.cfg.max_selected);
-  const dim3 sg((nscore + ROWS - 1) / ROWS, a.st.retrieval_heads);
-  auto go = [&](auto score, auto select) {
-    hipLaunchKernelGGL(score, sg, dim3(SELECT_THREADS), 0, s, a);
+  DecodeArgs u;
+  memset(&u, 0, sizeof(u));
+  const bool upd = pending != nullptr && pending->cfg.assignment != CKV_ASSIGN_NONE;
+  if (upd) u = *pending;
+  const dim3 sg((nscore + ROWS - 1) / ROWS, a.st.retrieval_heads + (upd ? 1 : 0));
+  auto go = [&](auto score, auto score_upd, auto select) {
+    if (upd)
+      hipLaunchKernelGGL(score_upd, sg, dim3(SELECT_THREADS), 0, s, a, u);
+    else
+      hipLaunchKernelGGL(score, sg, dim3(SELECT_THREADS), 0, s, a, u);
     int rc = launch_check("score_rows");
     if (rc) return rc;
     const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(select),
@@ -563,10 +585,17 @@ int launch_select_large(const DecodeArgs& a, hipStream_t s) {
     return launch_check("select_large");
   };
   const bool e4m3 = a.st.centroid_dtype == CKV_E4M3, bf16 = a.kv.dtype == CKV_BF16;
-  if (e4m3 && bf16) return go(score_rows_kernel<CKV_E4M3, CKV_BF16>, select_large_kernel<CKV_E4M3, CKV_BF16>);
-  if (e4m3) return go(score_rows_kernel<CKV_E4M3, CKV_F32>, select_large_kernel<CKV_E4M3, CKV_F32>);
-  if (bf16) return go(score_rows_kernel<CKV_F32, CKV_BF16>, select_large_kernel<CKV_F32, CKV_BF16>);
-  return go(score_rows_kernel<CKV_F32, CKV_F32>, select_large_kernel<CKV_F32, CKV_F32>);
+  if (e4m3 && bf16)
+    return go(score_rows_kernel<CKV_E4M3, CKV_BF16>, score_rows_kernel<CKV_E4M3, CKV_BF16, true>,
+              select_large_kernel<CKV_E4M3, CKV_BF16>);
+  if (e4m3)
+    return go(score_rows_kernel<CKV_E4M3, CKV_F32>, score_rows_kernel<CKV_E4M3, CKV_F32, true>,
+              select_large_kernel<CKV_E4M3, CKV_F32>);
+  if (bf16)
+    return go(score_rows_kernel<CKV_F32, CKV_BF16>, score_rows_kernel<CKV_F32, CKV_BF16, true>,
+              select_large_kernel<CKV_F32, CKV_BF16>);
+  return go(score_rows_kernel<CKV_F32, CKV_F32>, score_rows_kernel<CKV_F32, CKV_F32, true>,
+            select_large_kernel<CKV_F32, CKV_F32>);
 }
 
 }  // namespace ckv

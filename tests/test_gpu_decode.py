@@ -95,6 +95,11 @@ CASES = {
                                        max_decode_tokens=8, aggregation=co.QUERY_GROUP),
                                   dict(group_size=4, num_sink=10, token_budget=4096, local_window=256,
                                        assignment="nearest_centroid")),
+    # 32 per-query-head graphs of 1,500 communities, budget 2,048: separate
+    # selection (scoring on every compute unit) and attention launches
+    "per_query_head_1500_separate": (dict(query_heads=32, kv_heads=8, seq_len=16384, communities=1500,
+                                          num_sink=10, max_decode_tokens=8, aggregation=co.PER_QUERY_HEAD),
+                                     dict(group_size=1, num_sink=10, token_budget=2048, local_window=64)),
     # few large communities: decode deltas pile up in a few chains of several geometric chunks
     "deep_delta_chains_bf16": (dict(query_heads=8, kv_heads=2, seq_len=2048, communities=6, num_sink=10,
                                     max_decode_tokens=40, aggregation=co.QUERY_GROUP),
@@ -113,7 +118,7 @@ CASES = {
                          max_decode_tokens=16, aggregation=co.QUERY_GROUP),
                     dict(group_size=8, num_sink=10, token_budget=320, local_window=64)),
 }
-STEPS = {"communities_1500_bf16": 4, "communities_2600_nearest": 4, "communities_12000_bf16": 3,
+STEPS = {"communities_1500_bf16": 4, "per_query_head_1500_separate": 3, "communities_2600_nearest": 4, "communities_12000_bf16": 3,
          "communities_40000_nearest": 3, "deep_delta_chains_bf16": 36,
          "topk_all_nearest_bf16": 12}
 

@@ -25,12 +25,26 @@ def _layer(fx, params, device):
     return dict(state=state, cur=cur, q=q, ws=ws, call=call)
 
 
+SHAPES = {
+    # query groups of 4, 64 communities: the cooperative / fused launch
+    "small": (dict(query_heads=16, kv_heads=4, seq_len=4096, communities=64, aggregation=co.QUERY_GROUP),
+              dict(group_size=4, token_budget=512, local_window=64)),
+    # 32 per-query-head graphs of 1,500 communities and a 2,048-token budget:
+    # separate launches, the scoring on every compute unit carrying the
+    # pending update
+    "per_query_head_1500": (dict(query_heads=32, kv_heads=8, seq_len=16384, communities=1500,
+                                 aggregation=co.PER_QUERY_HEAD),
+                            dict(group_size=1, token_budget=2048, local_window=64)),
+}
+
+
+@pytest.mark.parametrize("shape", list(SHAPES))
 @pytest.mark.parametrize("fused", [True, False])
 @pytest.mark.parametrize("assignment", ["delta_q", "nearest_centroid"])
-def test_deferred_update_matches_serial(device, assignment, fused):
-    params = co.StepParams(group_size=4, num_sink=10, token_budget=512, local_window=64, assignment=assignment)
-    fxs = [syn.build_layer(seed=31 + i, query_heads=16, kv_heads=4, seq_len=4096, communities=64, num_sink=10,
-                           max_decode_tokens=16, aggregation=co.QUERY_GROUP) for i in range(3)]
+def test_deferred_update_matches_serial(device, assignment, fused, shape):
+    build_kw, step_kw = SHAPES[shape]
+    params = co.StepParams(num_sink=10, assignment=assignment, **step_kw)
+    fxs = [syn.build_layer(seed=31 + i, num_sink=10, max_decode_tokens=16, **build_kw) for i in range(3)]
     serial = [_layer(fx, params, device) for fx in fxs]
     deferred = [_layer(fx, params, device) for fx in fxs]
     rng = np.random.default_rng(7)
