@@ -17,10 +17,12 @@
 // mapping; V^T operands come from LDS with ds_read_b64_tr_b16.
 //
 // Top-kappa: each lane keeps a sorted queue of packed keys
-// (quantised score << 17 | column + 1) for the columns of its half; a tile is
-// inspected only when the lane's tile maximum reaches the current threshold
-// (the larger of the two halves' worst kept keys), and the two queues are
-// merged exactly at the end.
+// (quantised score << 17 | column + 1) for the columns of its half.  A tile is
+// inspected only when some lane's tile maximum reaches its threshold (a lower
+// bound of the row's kappa-th best key); candidates above it are appended to a
+// small unsorted per-lane buffer, and a wave merges its buffers into the
+// queues (sorting network + bitonic merge) only when one would overflow.  The
+// two halves' queues are merged exactly at the end.
 #include <hip/hip_runtime.h>
 
 #include <float.h>
@@ -46,10 +48,12 @@ constexpr int V_TILE = PF_KEYS * V_STRIDE;
 constexpr int STAGE = K_TILE + V_TILE;  // elements per pipeline stage
 constexpr int PF_STAGES = 3;
 constexpr size_t PF_STAGE_BYTES = PF_STAGES * STAGE * sizeof(uint16_t);
-// Per-lane top-kappa queues live in LDS after the two stages: entry block j
-// (entries 4 j .. 4 j + 3) of thread tid at 16 (j * threads + tid).
+// Per-lane top-kappa queues live in LDS after the stages: entry block j
+// (entries 4 j .. 4 j + 3) of thread tid at 16 (j * threads + tid); the
+// pending-candidate buffers (PF_BUF entries) follow in the same layout.
+constexpr int PF_BUF = 8;
 template <int QN>
-constexpr size_t pf_lds_bytes() { return PF_STAGE_BYTES + (size_t)QN * 4 * 64 * PF_WAVES; }
+constexpr size_t pf_lds_bytes() { return PF_STAGE_BYTES + (size_t)(QN + PF_BUF) * 4 * 64 * PF_WAVES; }
 constexpr int MAX_KAPPA = 16;
 constexpr int MAX_SEQ = (1 << 17) - 1;  // column + 1 must fit the 17-bit index field
 constexpr float NEG_INF = -__builtin_huge_valf();
@@ -111,18 +115,22 @@ __device__ inline float prefilter(uint32_t thr) {
   return key == 0 ? -FLT_MAX : __builtin_fmaf((float)key, 1.0f / 256.0f, -(48.0f + 0.504f / 256.0f));
 }
 
-// Insertion into a descending queue: the new entry i is the median of the
-// old entries i-1, i and the candidate (one v_med3_u32 per entry).
-template <int QN>
-__device__ inline void queue_insert(uint32_t (&q)[QN], uint32_t cand) {
-  uint32_t prev = q[0];
-  q[0] = max(q[0], cand);
-#pragma unroll
-  for (int i = 1; i < QN; ++i) {
-    const uint32_t cur = q[i];
-    q[i] = max(min(prev, cur), min(max(prev, cur), cand));
-    prev = cur;
-  }
+// Compare-exchange into descending order.
+__device__ inline void ce_desc(uint32_t& a, uint32_t& b) {
+  const uint32_t hi = max(a, b), lo = min(a, b);
+  a = hi;
+  b = lo;
+}
+
+// Descending sort of 8 keys: the 19-comparator network (Knuth, TAOCP vol. 3,
+// 5.3.4, optimal for n = 8), six rounds.
+__device__ inline void sort8_desc(uint32_t (&b)[8]) {
+  ce_desc(b[0], b[2]); ce_desc(b[1], b[3]); ce_desc(b[4], b[6]); ce_desc(b[5], b[7]);
+  ce_desc(b[0], b[4]); ce_desc(b[1], b[5]); ce_desc(b[2], b[6]); ce_desc(b[3], b[7]);
+  ce_desc(b[0], b[1]); ce_desc(b[2], b[3]); ce_desc(b[4], b[5]); ce_desc(b[6], b[7]);
+  ce_desc(b[2], b[4]); ce_desc(b[3], b[5]);
+  ce_desc(b[1], b[4]); ce_desc(b[3], b[6]);
+  ce_desc(b[1], b[2]); ce_desc(b[3], b[4]); ce_desc(b[5], b[6]);
 }
 
 template <int QN>
@@ -223,12 +231,61 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_mfma_kernel(ckv_pref
       q[4 * j + 3] = w.w;
     }
   };
+  // This lane's pending candidates (nbuf of PF_BUF, unsorted), entry e at
+  // buf_lds[(e / 4) * threads + e % 4].
+  uint32_t* buf_lds = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(pf_lds) + PF_STAGE_BYTES +
+                                                  (size_t)QN * 4 * 64 * PF_WAVES) + 4 * tid;
+  int nbuf = 0;
   uint32_t q_min = 0u;
   uint32_t row_thr = 0u;  // a lower bound of the row's QN-th best key (both halves)
+  // Candidate filter: thr = max(own worst kept key, the other half's, row_thr)
+  // and tf = prefilter(thr).  It changes only when the queues do, so it is
+  // recomputed there instead of on every tile.
+  uint32_t thr = 0u;
+  float tf = -FLT_MAX;
   float m = NEG_INF;  // reference max of the raw score (scale > 0)
   float l = 0.0f;     // this half's share of the softmax denominator
 
   const int num_sink = a.num_sink;
+
+  // Merges every lane's pending candidates into its queue (called wave-
+  // uniformly): sort the buffer, keep the best QN of queue and buffer (the
+  // larger of q[i] and b[QN-1-i] is bitonic; half-cleaners sort it), then
+  // refresh the row threshold, i.e. the QN-th best key of the row over both
+  // halves' queues, and the filter.
+  auto flush = [&]() __attribute__((always_inline)) {
+    uint32_t qk[QN];
+    load_queue(qk);
+    uint32_t b[8];
+    {
+      const uint4 w0 = *reinterpret_cast<const uint4*>(buf_lds);
+      const uint4 w1 = *reinterpret_cast<const uint4*>(buf_lds + 4 * 64 * PF_WAVES);
+      b[0] = w0.x; b[1] = w0.y; b[2] = w0.z; b[3] = w0.w;
+      b[4] = w1.x; b[5] = w1.y; b[6] = w1.z; b[7] = w1.w;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) b[i] = i < nbuf ? b[i] : 0u;
+    sort8_desc(b);
+#pragma unroll
+    for (int i = (QN > 8 ? QN - 8 : 0); i < QN; ++i) qk[i] = max(qk[i], b[QN - 1 - i]);
+#pragma unroll
+    for (int j = QN / 2; j >= 1; j >>= 1) {
+#pragma unroll
+      for (int i = 0; i < QN; ++i) {
+        if ((i & j) == 0) ce_desc(qk[i], qk[i + j]);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < QN / 4; ++j) q_lds[j * 64 * PF_WAVES] = uint4{qk[4 * j], qk[4 * j + 1], qk[4 * j + 2], qk[4 * j + 3]};
+    q_min = qk[QN - 1];
+    nbuf = 0;
+    uint32_t rt = 0xffffffffu;
+#pragma unroll
+    for (int i = 0; i < QN; ++i) rt = min(rt, max(qk[i], swap32_u32(qk[QN - 1 - i])));
+    row_thr = rt;
+    thr = max(max(q_min, swap32_u32(q_min)), row_thr);
+    tf = prefilter(thr);
+  };
 
   // S^T (keys x rows) of the tile staged in `stage`: accumulator b holds keys
   // 32 b + 8 (v / 4) + 4 half + v % 4 of the tile.
@@ -289,6 +346,38 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_mfma_kernel(ckv_pref
     }
     const float lmax = __builtin_fmaxf(__builtin_fmaxf(gmax[0], gmax[1]), __builtin_fmaxf(gmax[2], gmax[3]));
 
+    // Top-kappa candidates of this lane's 32 columns, by groups of 8: keys
+    // above the filter go to the pending buffer, which is merged first when
+    // this group could overflow it.  Placed before the tile's LDS reads are
+    // issued, so the rare branch waits for nothing outstanding.
+#ifndef CKV_PF_NO_TOPK
+    if (__builtin_amdgcn_ballot_w64(lmax >= tf)) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        if (__builtin_amdgcn_ballot_w64(gmax[g] >= tf)) {
+          int cnt = 0;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) cnt += sacc[g >> 1][8 * (g & 1) + e] >= tf ? 1 : 0;
+          if (__builtin_amdgcn_ballot_w64(nbuf + cnt > PF_BUF)) flush();
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const int b = g >> 1;
+            const int v = 8 * (g & 1) + e;
+            const float sv = sacc[b][v];
+            const int col = c0 + 32 * b + 8 * (v >> 2) + 4 * half + (v & 3);
+            if (sv >= tf && col >= num_sink) {
+              const uint32_t cand = (quantise_score(sv) << 17) | (uint32_t)(col + 1);
+              if (cand > thr) {
+                buf_lds[(nbuf >> 2) * (4 * 64 * PF_WAVES) + (nbuf & 3)] = cand;
+                ++nbuf;
+              }
+            }
+          }
+        }
+      }
+    }
+#endif
+
     // Online softmax in base 2 against a reference max m that moves only when
     // a tile exceeds it by more than 2^RESCALE_LOG2 (p <= 2^RESCALE_LOG2 stays
     // exact in float32 and bf16 range); both halves of a row share m.
@@ -339,62 +428,6 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_mfma_kernel(ckv_pref
         o[db] = mfma32(uint4{lo.x, lo.y, hi.x, hi.y}, bop, o[db]);
       }
     }
-    // Top-kappa candidates of this lane's 32 columns, inspected by group
-    // against the larger of the two halves' worst kept keys.  Placed after the
-    // PV^T MFMAs are issued: the rare branch runs while they drain.
-    uint32_t thr = max(max(q_min, swap32_u32(q_min)), row_thr);
-    float tf = prefilter(thr);
-#ifdef CKV_PF_NO_TOPK
-    const bool inspect = false;
-#else
-    const bool inspect = lmax >= tf;
-#endif
-    bool inserted = false;
-    if (inspect) {
-      uint32_t qk[QN];
-      load_queue(qk);
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        if (gmax[g] >= tf) {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const int b = g >> 1;
-            const int v = 8 * (g & 1) + e;
-            const float sv = sacc[b][v];
-            const int col = c0 + 32 * b + 8 * (v >> 2) + 4 * half + (v & 3);
-            if (sv >= tf && col >= num_sink) {
-              const uint32_t cand = (quantise_score(sv) << 17) | (uint32_t)(col + 1);
-              if (cand > thr) {
-                inserted = true;
-                queue_insert<QN>(qk, cand);
-                thr = max(thr, qk[QN - 1]);
-                tf = prefilter(thr);
-              }
-            }
-          }
-        }
-      }
-#pragma unroll
-      for (int j = 0; j < QN / 4; ++j) q_lds[j * 64 * PF_WAVES] = uint4{qk[4 * j], qk[4 * j + 1], qk[4 * j + 2], qk[4 * j + 3]};
-      q_min = qk[QN - 1];
-    }
-    // After an inspection anywhere in the wave: the QN-th best key of the row
-    // over both halves' queues (the minimum of the bitonic top-QN of their
-    // union).  No later candidate below it can reach the row's top QN, so it
-    // is the tighter threshold for both halves.
-#ifdef CKV_PF_REFRESH_ON_INSERT
-    if (__builtin_amdgcn_ballot_w64(inserted)) {
-#else
-    if (__builtin_amdgcn_ballot_w64(inspect)) {
-#endif
-      uint32_t mine[QN];
-      load_queue(mine);
-      uint32_t rt = 0xffffffffu;
-#pragma unroll
-      for (int i = 0; i < QN; ++i) rt = min(rt, max(mine[i], swap32_u32(mine[QN - 1 - i])));
-      row_thr = rt;
-    }
-
     sacc[0] = snext[0];
     sacc[1] = snext[1];
     __builtin_amdgcn_s_waitcnt(VMCNT0);
@@ -402,6 +435,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_mfma_kernel(ckv_pref
     stage = nstage;
   }
 
+  if (__builtin_amdgcn_ballot_w64(nbuf > 0)) flush();
   if (!row_ok) return;
   const float l_tot = add_xor32(l);
   const float inv = 1.0f / l_tot;
