@@ -238,10 +238,9 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_mfma_kernel(ckv_pref
   int nbuf = 0;
   uint32_t q_min = 0u;
   uint32_t row_thr = 0u;  // a lower bound of the row's QN-th best key (both halves)
-  // Candidate filter: thr = max(own worst kept key, the other half's, row_thr)
-  // and tf = prefilter(thr).  It changes only when the queues do, so it is
-  // recomputed there instead of on every tile.
-  uint32_t thr = 0u;
+  // Candidate filter: prefilter(max(own worst kept key, the other half's,
+  // row_thr)).  It changes only when the queues do, so it is recomputed there
+  // instead of on every tile.
   float tf = -FLT_MAX;
   float m = NEG_INF;  // reference max of the raw score (scale > 0)
   float l = 0.0f;     // this half's share of the softmax denominator
@@ -249,7 +248,8 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_mfma_kernel(ckv_pref
   const int num_sink = a.num_sink;
 
   // Merges every lane's pending candidates into its queue (called wave-
-  // uniformly): sort the buffer, keep the best QN of queue and buffer (the
+  // uniformly): drop sink columns, sort the buffer, keep the best QN of queue
+  // and buffer (the
   // larger of q[i] and b[QN-1-i] is bitonic; half-cleaners sort it), then
   // refresh the row threshold, i.e. the QN-th best key of the row over both
   // halves' queues, and the filter.
@@ -264,7 +264,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_mfma_kernel(ckv_pref
       b[4] = w1.x; b[5] = w1.y; b[6] = w1.z; b[7] = w1.w;
     }
 #pragma unroll
-    for (int i = 0; i < 8; ++i) b[i] = i < nbuf ? b[i] : 0u;
+    for (int i = 0; i < 8; ++i) b[i] = (i < nbuf && (int)(b[i] & 0x1ffffu) > num_sink) ? b[i] : 0u;
     sort8_desc(b);
 #pragma unroll
     for (int i = (QN > 8 ? QN - 8 : 0); i < QN; ++i) qk[i] = max(qk[i], b[QN - 1 - i]);
@@ -283,8 +283,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_mfma_kernel(ckv_pref
 #pragma unroll
     for (int i = 0; i < QN; ++i) rt = min(rt, max(qk[i], swap32_u32(qk[QN - 1 - i])));
     row_thr = rt;
-    thr = max(max(q_min, swap32_u32(q_min)), row_thr);
-    tf = prefilter(thr);
+    tf = prefilter(max(max(q_min, swap32_u32(q_min)), row_thr));
   };
 
   // S^T (keys x rows) of the tile staged in `stage`: accumulator b holds keys
@@ -346,10 +345,12 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_mfma_kernel(ckv_pref
     }
     const float lmax = __builtin_fmaxf(__builtin_fmaxf(gmax[0], gmax[1]), __builtin_fmaxf(gmax[2], gmax[3]));
 
-    // Top-kappa candidates of this lane's 32 columns, by groups of 8: keys
-    // above the filter go to the pending buffer, which is merged first when
-    // this group could overflow it.  Placed before the tile's LDS reads are
-    // issued, so the rare branch waits for nothing outstanding.
+    // Top-kappa candidates of this lane's 32 columns, by groups of 8: every
+    // score above the filter goes to the pending buffer (sinks and keys the
+    // queue would not keep are dropped by the merge, which is cheaper than
+    // testing each candidate), merged first when this group could overflow it.
+    // Placed before the tile's LDS reads are issued, so the rare branch waits
+    // for nothing outstanding.
 #ifndef CKV_PF_NO_TOPK
     if (__builtin_amdgcn_ballot_w64(lmax >= tf)) {
 #pragma unroll
@@ -365,12 +366,10 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_mfma_kernel(ckv_pref
             const int v = 8 * (g & 1) + e;
             const float sv = sacc[b][v];
             const int col = c0 + 32 * b + 8 * (v >> 2) + 4 * half + (v & 3);
-            if (sv >= tf && col >= num_sink) {
-              const uint32_t cand = (quantise_score(sv) << 17) | (uint32_t)(col + 1);
-              if (cand > thr) {
-                buf_lds[(nbuf >> 2) * (4 * 64 * PF_WAVES) + (nbuf & 3)] = cand;
-                ++nbuf;
-              }
+            if (sv >= tf) {
+              buf_lds[(nbuf >> 2) * (4 * 64 * PF_WAVES) + (nbuf & 3)] =
+                  (quantise_score(sv) << 17) | (uint32_t)(col + 1);
+              ++nbuf;
             }
           }
         }
