@@ -274,6 +274,17 @@ __device__ inline void attend_part(const DecodeArgs& a, const int rh, const int 
   }
   m = max_xor16(m);
   m = max_xor32(m);
+  // The part's maximum per query, shared before P.V (the barrier overlaps the
+  // V rows' loads), so every wave's numerators are on one scale and the
+  // combine below is a plain sum.
+  if (L == 0 && c16 < G) wm_s[wave * CKV_MAX_GROUP + c16] = m;
+  __syncthreads();
+  {
+    float M = NEG_INF;
+#pragma unroll
+    for (int x = 0; x < W; ++x) M = fmax_exact(M, wm_s[x * CKV_MAX_GROUP + min(c16, G - 1)]);
+    m = c16 < G ? M : m;  // lanes past the group keep their own (unused) rows finite
+  }
   float p[4];
   float l = 0.0f;
 #pragma unroll
@@ -297,10 +308,7 @@ __device__ inline void attend_part(const DecodeArgs& a, const int rh, const int 
   }
   wave_sync();  // every lane's V reads are done before the P.V rows reuse the buffer
   CKV_TS(19);
-  if (L == 0 && c16 < G) {
-    wm_s[wave * CKV_MAX_GROUP + c16] = m;
-    wl_s[wave * CKV_MAX_GROUP + c16] = l;
-  }
+  if (L == 0 && c16 < G) wl_s[wave * CKV_MAX_GROUP + c16] = l;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int g = 4 * L + i;
@@ -309,52 +317,37 @@ __device__ inline void attend_part(const DecodeArgs& a, const int rh, const int 
       for (int nb = 0; nb < 8; ++nb) o_s[g * D + 16 * nb + c16] = o[nb][i];
     }
   }
-  __syncthreads();
-  CKV_TS(20);
-  // per (wave, query) rescale factor exp(m_w - M) of the combine below
-  __shared__ float wsc_s[W][CKV_MAX_GROUP];
-  __shared__ float wM_s[CKV_MAX_GROUP];
-  if (tid < W * G) {
-    const int w = tid / G, g = tid % G;
-    float M = NEG_INF;
-#pragma unroll
-    for (int x = 0; x < W; ++x) M = fmax_exact(M, wm_s[x * CKV_MAX_GROUP + g]);
-    const float mw = wm_s[w * CKV_MAX_GROUP + g];
-    wsc_s[w][g] = mw != NEG_INF ? __expf(mw - M) : 0.0f;
-    if (w == 0) wM_s[g] = M;
-  }
   if (want_topk && wave < TP) {
     const int tile = part * TP + wave;
     if (tile < tiles) a.ws.slot_scores[(int64_t)rh * a.ws.slot_capacity + tile * TILE + lane] = cand_all[wave * TILE + lane];
   }
   __syncthreads();
-  // Combine the W wave partials into this part's split partial.  A wave
-  // without a valid slot has factor 0 and P.V rows of zeros, so adding its
-  // (signed) zero leaves the sum unchanged: no branch, every LDS read issued
-  // before the first multiply.
+  CKV_TS(20);
+  // Combine the W wave partials (one scale: the part's maximum) into this
+  // part's split partial, in wave order.  A wave without a valid slot has
+  // P.V rows of zeros.  Every LDS read is issued before the first add.
   for (int i = tid; i < G * D; i += 64 * W) {
     const int g = i >> 7;
     const int d = i & (D - 1);
-    float ov[W], sc[W];
+    float ov[W];
 #pragma unroll
-    for (int w = 0; w < W; ++w) {
+    for (int w = 0; w < W; ++w)
       ov[w] = reinterpret_cast<const float*>(reinterpret_cast<uint16_t*>(lds) + w * (QROWS * D))[g * D + d];
-      sc[w] = wsc_s[w][g];
-    }
     float acc = 0.0f;
 #pragma unroll
-    for (int w = 0; w < W; ++w) acc = acc + ov[w] * sc[w];
+    for (int w = 0; w < W; ++w) acc = acc + ov[w];
     float* dst = a.ws.partial_acc + (((int64_t)rh * G + g) * parts + part) * D + d;
     if constexpr (AGENT) st_agent_f32(dst, acc); else *dst = acc;
   }
   CKV_TS(22);
   if (tid < G) {
     float lsum = 0.0f;
+    float M = NEG_INF;
 #pragma unroll
     for (int w = 0; w < W; ++w) {
-      if (wm_s[w * CKV_MAX_GROUP + tid] != NEG_INF) lsum = lsum + wl_s[w * CKV_MAX_GROUP + tid] * wsc_s[w][tid];
+      lsum = lsum + wl_s[w * CKV_MAX_GROUP + tid];
+      M = fmax_exact(M, wm_s[w * CKV_MAX_GROUP + tid]);
     }
-    const float M = wM_s[tid];
     float* pm = a.ws.partial_max + ((int64_t)rh * G + tid) * parts + part;
     float* pl = a.ws.partial_sum + ((int64_t)rh * G + tid) * parts + part;
     if constexpr (AGENT) {
