@@ -50,8 +50,11 @@ constexpr int PF_STAGES = 3;
 constexpr size_t PF_STAGE_BYTES = PF_STAGES * STAGE * sizeof(uint16_t);
 // Per-lane top-kappa queues live in LDS after the stages: entry block j
 // (entries 4 j .. 4 j + 3) of thread tid at 16 (j * threads + tid); the
-// pending-candidate buffers (PF_BUF entries) follow in the same layout.
+// pending-candidate buffers follow, entry e of thread tid at 4 (e * threads + tid).
 constexpr int PF_BUF = 8;
+// Columns per candidate group: a group is inspected only when its maximum
+// reaches the filter (4 measured faster than 2 or 8).
+constexpr int PF_GROUP = 4;
 template <int QN>
 constexpr size_t pf_lds_bytes() { return PF_STAGE_BYTES + (size_t)(QN + PF_BUF) * 4 * 64 * PF_WAVES; }
 constexpr int MAX_KAPPA = 16;
@@ -232,9 +235,9 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_mfma_kernel(ckv_pref
     }
   };
   // This lane's pending candidates (nbuf of PF_BUF, unsorted), entry e at
-  // buf_lds[(e / 4) * threads + e % 4].
+  // buf_lds[e * threads].
   uint32_t* buf_lds = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(pf_lds) + PF_STAGE_BYTES +
-                                                  (size_t)QN * 4 * 64 * PF_WAVES) + 4 * tid;
+                                                  (size_t)QN * 4 * 64 * PF_WAVES) + tid;
   int nbuf = 0;
   uint32_t q_min = 0u;
   uint32_t row_thr = 0u;  // a lower bound of the row's QN-th best key (both halves)
@@ -257,12 +260,8 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_mfma_kernel(ckv_pref
     uint32_t qk[QN];
     load_queue(qk);
     uint32_t b[8];
-    {
-      const uint4 w0 = *reinterpret_cast<const uint4*>(buf_lds);
-      const uint4 w1 = *reinterpret_cast<const uint4*>(buf_lds + 4 * 64 * PF_WAVES);
-      b[0] = w0.x; b[1] = w0.y; b[2] = w0.z; b[3] = w0.w;
-      b[4] = w1.x; b[5] = w1.y; b[6] = w1.z; b[7] = w1.w;
-    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) b[i] = buf_lds[i * 64 * PF_WAVES];
 #pragma unroll
     for (int i = 0; i < 8; ++i) b[i] = (i < nbuf && (int)(b[i] & 0x1ffffu) > num_sink) ? b[i] : 0u;
     sort8_desc(b);
@@ -335,17 +334,21 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_mfma_kernel(ckv_pref
         }
       }
     }
-    // Maxima of the four groups of 8 (group g = accumulator g / 2, registers 8 (g % 2) ..).
-    float gmax[4];
+    // Maxima of the groups of PF_GROUP columns (group g = accumulator g / GPA,
+    // registers GS (g % GPA) ..).
+    constexpr int GS = PF_GROUP, NG = 32 / GS, GPA = 16 / GS;
+    float gmax[NG];
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      gmax[g] = sacc[g >> 1][8 * (g & 1)];
+    for (int g = 0; g < NG; ++g) {
+      gmax[g] = sacc[g / GPA][GS * (g % GPA)];
 #pragma unroll
-      for (int e = 1; e < 8; ++e) gmax[g] = __builtin_fmaxf(gmax[g], sacc[g >> 1][8 * (g & 1) + e]);
+      for (int e = 1; e < GS; ++e) gmax[g] = __builtin_fmaxf(gmax[g], sacc[g / GPA][GS * (g % GPA) + e]);
     }
-    const float lmax = __builtin_fmaxf(__builtin_fmaxf(gmax[0], gmax[1]), __builtin_fmaxf(gmax[2], gmax[3]));
+    float lmax = gmax[0];
+#pragma unroll
+    for (int g = 1; g < NG; ++g) lmax = __builtin_fmaxf(lmax, gmax[g]);
 
-    // Top-kappa candidates of this lane's 32 columns, by groups of 8: every
+    // Top-kappa candidates of this lane's 32 columns, by groups: every
     // score above the filter goes to the pending buffer (sinks and keys the
     // queue would not keep are dropped by the merge, which is cheaper than
     // testing each candidate), merged first when this group could overflow it.
@@ -354,20 +357,20 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_mfma_kernel(ckv_pref
 #ifndef CKV_PF_NO_TOPK
     if (__builtin_amdgcn_ballot_w64(lmax >= tf)) {
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
+      for (int g = 0; g < NG; ++g) {
         if (__builtin_amdgcn_ballot_w64(gmax[g] >= tf)) {
           int cnt = 0;
 #pragma unroll
-          for (int e = 0; e < 8; ++e) cnt += sacc[g >> 1][8 * (g & 1) + e] >= tf ? 1 : 0;
+          for (int e = 0; e < GS; ++e) cnt += sacc[g / GPA][GS * (g % GPA) + e] >= tf ? 1 : 0;
           if (__builtin_amdgcn_ballot_w64(nbuf + cnt > PF_BUF)) flush();
 #pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const int b = g >> 1;
-            const int v = 8 * (g & 1) + e;
+          for (int e = 0; e < GS; ++e) {
+            const int b = g / GPA;
+            const int v = GS * (g % GPA) + e;
             const float sv = sacc[b][v];
             const int col = c0 + 32 * b + 8 * (v >> 2) + 4 * half + (v & 3);
             if (sv >= tf) {
-              buf_lds[(nbuf >> 2) * (4 * 64 * PF_WAVES) + (nbuf & 3)] =
+              buf_lds[nbuf * (64 * PF_WAVES)] =
                   (quantise_score(sv) << 17) | (uint32_t)(col + 1);
               ++nbuf;
             }
