@@ -26,8 +26,8 @@ SCORE_BLOCK_N = nat.SCORE_BLOCK
 
 def exchange_words(community_capacity: int) -> int:
     """uint64 words per retrieval head of the fused launch's exchange row:
-    tagged scores, then tagged nearest-centroid minima and done words (8 waves
-    x 64 parts each) (ckv_exchange_words in csrc/ckv_device.h)."""
+    tagged scores, then tagged nearest-centroid minima (8 waves x 64 parts)
+    and as many reserved words (ckv_exchange_words in csrc/ckv_device.h)."""
     return community_capacity + 2 * 64 * 8
 
 
@@ -44,7 +44,7 @@ class CentroidSelectionWorkspace:
     selected_counts: torch.Tensor   # [R] int32
     slot_positions: torch.Tensor    # [R, slot capacity] int32
     exchange: torch.Tensor          # [R, exchange_words(C)] uint64 (zeros): a fused launch's workgroups hand each
-                                    # other centroid scores, done words and nearest-centroid minima through it
+                                    # other centroid scores and nearest-centroid minima through it
     nearest: torch.Tensor           # [R] int32
     block_counters: torch.Tensor    # [4R] int32 arrival counters and epochs (zeros; kernel-maintained)
     token_budget: int

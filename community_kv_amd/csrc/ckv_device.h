@@ -66,8 +66,8 @@ constexpr float NEG_INF = -__builtin_huge_valf();
 
 // Words (uint64) of one retrieval head's row of the fused launch's exchange
 // buffer: the epoch-tagged centroid scores (one per community), then the
-// tagged nearest-centroid minima and the scoring waves' done words (eight
-// waves of at most 64 parts each).
+// tagged nearest-centroid minima (eight waves of at most 64 parts each) and as
+// many reserved words.
 __host__ __device__ inline int64_t ckv_exchange_words(int community_capacity) {
   return (int64_t)community_capacity + 2 * 64 * 8;
 }

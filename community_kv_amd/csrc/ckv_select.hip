@@ -66,9 +66,8 @@ constexpr int COOP_SCORE_WAVES = 6;  // waves that score and poll; the others wa
 constexpr int COOP_MAX_PARTS = 64;
 constexpr int COOP_WAVES = SELECT_THREADS / 64;
 // Exchange row layout after the C tagged scores: the nearest-centroid minima
-// (part * COOP_WAVES + wave), then the scoring waves' done words (same indexing).
+// (part * COOP_WAVES + wave), then COOP_MAX_PARTS * COOP_WAVES reserved words.
 constexpr int COOP_NEAR_OFF = 0;
-constexpr int COOP_FLAGS_OFF = COOP_MAX_PARTS * COOP_WAVES;
 }  // namespace
 
 __host__ __device__ inline int64_t exchange_stride(int community_capacity) {
@@ -279,8 +278,8 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
   uint32_t epoch = 0;
   const bool chain_wave = COOP && (tid >> 6) >= COOP_SCORE_WAVES;
   // Blocks go to the eight XCDs round robin and the parts of head rh are blocks
-  // rh + R * part, so with R a multiple of 8 they share one XCD: scores and
-  // done words then stay in its L2 (st_xcd_u64), else they are written through.
+  // rh + R * part, so with R a multiple of 8 they share one XCD: the scores
+  // then stay in its L2 (st_xcd_u64), else they are written through.
   const bool xcd_local = (a.st.retrieval_heads & 7) == 0;
   const int npairs = (G + 1) >> 1;
   const int rpp = (nscore + max(parts, 1) - 1) / max(parts, 1);  // rows per part
@@ -683,49 +682,15 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
           if (xcd_local) st_xcd_u64(xrow + row, tag | bits); else st_agent_u64(xrow + row, tag | bits);
         }
       }
-      // this wave's rows are out: its done word (no wait for their stores; the
-      // rows carry their own tag)
-      if ((tid & 63) == 0) {
-        uint64_t* done = xrow + C + COOP_FLAGS_OFF + part * COOP_WAVES + (tid >> 6);
-        if (xcd_local) st_xcd_u64(done, tag); else st_agent_u64(done, tag);
-      }
       CKV_TS(14);
       CKV_STAMP_MAX(rh == 0, 27);
       {
-        // Each scoring wave polls the parts' done words (a few words per round:
-        // polling the score rows themselves from every part would load the
-        // memory system enough to slow every other round of the launch), then
-        // loads the other parts' rows among its threads' rows st_, st_ + 384,
-        // ... once, checked by tag (a row whose store has not landed yet is
-        // loaded again, bounded); a part that still misses rows scores every
-        // community itself.
-        const int lane = tid & 63;
-        const int nflag = parts * COOP_WAVES;
-        int poll = 0;
-        bool all = false;
-        for (; poll < COOP_POLLS; ++poll) {
-          uint64_t f[COOP_MAX_PARTS * COOP_WAVES / 64];
-#pragma unroll
-          for (int q = 0; q < COOP_MAX_PARTS * COOP_WAVES / 64; ++q) {
-            const int e = lane + 64 * q;
-            f[q] = ld_agent_u64(xrow + C + COOP_FLAGS_OFF + min(e, nflag - 1));
-          }
-          bool ok = true;
-#pragma unroll
-          for (int q = 0; q < COOP_MAX_PARTS * COOP_WAVES / 64; ++q) {
-            const int e = lane + 64 * q;
-            ok = ok & (e >= nflag || (e & (COOP_WAVES - 1)) >= COOP_SCORE_WAVES || f[q] == tag);
-          }
-          all = __ballot(!ok) == 0ull;
-          if (all) break;
-          __builtin_amdgcn_s_sleep(4);
-        }
-#ifdef CKV_PHASE_TIMING
-        if (rh == 0 && part == 0 && tid == 0) {
-          phase_stamp[6] = wall_clock64();
-          phase_stamp[11] = 1000000ull + poll;
-        }
-#endif
+        // Each scoring thread polls the other parts' rows among its rows st_,
+        // st_ + 384, ... until every one carries this launch's tag (a wave
+        // leaves once all its rows have arrived; bounded: a part that still
+        // misses rows scores every community itself).  One tagged word per
+        // row, so a row is taken as soon as its own store lands, without a
+        // per-part completion word and the second round it would need.
         constexpr int SN = COOP_SCORE_WAVES * 64;
         constexpr int PJ = (OWN * SELECT_THREADS + SN - 1) / SN;
 #pragma unroll
@@ -733,7 +698,7 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
           const int c = st_ + k * SN;
           if (c < count && c % parts != part) need |= 1u << k;
         }
-        for (int pr = 0; need != 0 && pr < (all ? COOP_POLLS : 1); ++pr) {
+        for (int pr = 0; pr < COOP_POLLS && __ballot(need != 0) != 0ull; ++pr) {
           uint64_t v[PJ];
 #pragma unroll
           for (int k = 0; k < PJ; ++k) v[k] = ld_agent_u64(xrow + min(st_ + k * SN, C - 1));
@@ -744,7 +709,7 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
               need &= ~(1u << k);
             }
           }
-          if (need != 0) __builtin_amdgcn_s_sleep(4);
+          if (__ballot(need != 0) != 0ull) __builtin_amdgcn_s_sleep(4);
         }
       }
     }

@@ -160,7 +160,7 @@ typedef struct ckv_decode_workspace {
   int32_t* slot_positions;     /* [retrieval_heads][slot_capacity] KV position per attended slot, -1 = none */
   uint64_t* exchange;          /* [retrieval_heads][community_capacity + 1024], zero before first use, or
                                   null: the fused launch's workgroups of a head hand each other their share of
-                                  the centroid scores, done words and nearest-centroid minima through it,
+                                  the centroid scores and nearest-centroid minima through it,
                                   epoch-tagged */
   int32_t* nearest;            /* [retrieval_heads] */
   uint32_t* block_counters;    /* [4 * retrieval_heads], zero before first use: arrival counters (the kernels
