@@ -78,6 +78,10 @@ SMALL = [
     (257, 6, 2, 10, 8, True),    # G = 3: packed rows straddle positions
     (64, 4, 4, 10, 8, True),
     (20, 4, 1, 10, 16, False),   # fewer rows than the skip: empty top-k output
+    # long rows of tied coarse scores: the pending candidates are merged into
+    # the queues many times per row (queue sizes 8 and 4)
+    (1536, 8, 2, 10, 8, True),
+    (1024, 4, 1, 0, 4, True),
 ]
 
 
