@@ -100,6 +100,12 @@ CASES = {
     "per_query_head_1500_separate": (dict(query_heads=32, kv_heads=8, seq_len=16384, communities=1500,
                                           num_sink=10, max_decode_tokens=8, aggregation=co.PER_QUERY_HEAD),
                                      dict(group_size=1, num_sink=10, token_budget=2048, local_window=64)),
+    # few live communities but 10,000 decode tokens of headroom: a community
+    # capacity (10,064) above the single-workgroup selection's 8,192 rows,
+    # while only the 64 live rows are scored
+    "headroom_10000_bf16": (dict(query_heads=8, kv_heads=2, seq_len=2048, communities=64, num_sink=10,
+                                 max_decode_tokens=10000, aggregation=co.QUERY_GROUP),
+                            dict(group_size=4, num_sink=10, token_budget=512, local_window=32)),
     # few large communities: decode deltas pile up in a few chains of several geometric chunks
     "deep_delta_chains_bf16": (dict(query_heads=8, kv_heads=2, seq_len=2048, communities=6, num_sink=10,
                                     max_decode_tokens=40, aggregation=co.QUERY_GROUP),
@@ -118,7 +124,7 @@ CASES = {
                          max_decode_tokens=16, aggregation=co.QUERY_GROUP),
                     dict(group_size=8, num_sink=10, token_budget=320, local_window=64)),
 }
-STEPS = {"communities_1500_bf16": 4, "per_query_head_1500_separate": 3, "communities_2600_nearest": 4, "communities_12000_bf16": 3,
+STEPS = {"headroom_10000_bf16": 3, "communities_1500_bf16": 4, "per_query_head_1500_separate": 3, "communities_2600_nearest": 4, "communities_12000_bf16": 3,
          "communities_40000_nearest": 3, "deep_delta_chains_bf16": 36,
          "topk_all_nearest_bf16": 12}
 
