@@ -46,19 +46,9 @@ int limit_error(const char* message) { return ckv_internal::set_error(CKV_E_LIMI
 
 // Scores (and, in nearest-centroid mode, block minima of the squared distance
 // to the current key: distance bits << 32 | row, into exchange[rh][C + block])
-// of rows [64 * blockIdx.x, +64) of head blockIdx.y.  UPD: the workgroups of
-// row blockIdx.y == a.st.retrieval_heads run the pending online update of
-// another layer `u` (same dtypes), heads blockIdx.x, blockIdx.x + gridDim.x, ...
-// on the compute units the scoring leaves idle.
-template <int CT, int DT, bool UPD = false>
-__global__ __launch_bounds__(SELECT_THREADS) void score_rows_kernel(DecodeArgs a, DecodeArgs u) {
-  if constexpr (UPD) {
-    if ((int)blockIdx.y >= a.st.retrieval_heads) {
-      for (int urh = blockIdx.x; urh < u.st.retrieval_heads; urh += gridDim.x)
-        owner_update<CT, DT>(u, urh, u.ws.lse[(int64_t)urh * u.cfg.group_size]);
-      return;
-    }
-  }
+// of rows [64 * blockIdx.x, +64) of head blockIdx.y.
+template <int CT, int DT>
+__global__ __launch_bounds__(SELECT_THREADS) void score_rows_kernel(DecodeArgs a) {
   __shared__ float q_s[CKV_MAX_GROUP * D];
   __shared__ float key_s[D];
   __shared__ uint64_t near_s[SELECT_THREADS / 64];
@@ -136,8 +126,16 @@ __host__ __device__ inline size_t large_lds_bytes(int descriptor_capacity, int m
   return (size_t)descriptor_capacity * 7 * 4 + (size_t)((max_selected + 63) / 64 + 2) * 4;
 }
 
+// Workgroups past a.st.retrieval_heads run the pending online update of
+// another layer `u` (same dtypes), one retrieval head each, on the compute
+// units this launch leaves idle (the selection is one workgroup per head).
 template <int CT, int DT>
-__global__ __launch_bounds__(LT) void select_large_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(LT) void select_large_kernel(DecodeArgs a, DecodeArgs u) {
+  if ((int)blockIdx.x >= a.st.retrieval_heads) {
+    const int urh = (int)blockIdx.x - a.st.retrieval_heads;
+    owner_update<CT, DT>(u, urh, u.ws.lse[(int64_t)urh * u.cfg.group_size]);
+    return;
+  }
   __shared__ __align__(16) int hist[256];
   __shared__ __align__(16) int hist2[256];
   __shared__ int scan_s[4 * LWAVES];
@@ -567,12 +565,14 @@ int launch_select_large(const DecodeArgs& a, hipStream_t s, const DecodeArgs* pe
   memset(&u, 0, sizeof(u));
   const bool upd = pending != nullptr && pending->cfg.assignment != CKV_ASSIGN_NONE;
   if (upd) u = *pending;
-  const dim3 sg((nscore + ROWS - 1) / ROWS, a.st.retrieval_heads + (upd ? 1 : 0));
-  auto go = [&](auto score, auto score_upd, auto select) {
-    if (upd)
-      hipLaunchKernelGGL(score_upd, sg, dim3(SELECT_THREADS), 0, s, a, u);
-    else
-      hipLaunchKernelGGL(score, sg, dim3(SELECT_THREADS), 0, s, a, u);
+  const dim3 sg((nscore + ROWS - 1) / ROWS, a.st.retrieval_heads);
+  // The pending update rides in the selection launch (one workgroup per head
+  // beside the selection's one per head), not in the scoring launch: the
+  // update's dependent chain is longer than the scoring but shorter than the
+  // selection.
+  const int select_blocks = a.st.retrieval_heads + (upd ? u.st.retrieval_heads : 0);
+  auto go = [&](auto score, auto select) {
+    hipLaunchKernelGGL(score, sg, dim3(SELECT_THREADS), 0, s, a);
     int rc = launch_check("score_rows");
     if (rc) return rc;
     const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(select),
@@ -581,21 +581,14 @@ int launch_select_large(const DecodeArgs& a, hipStream_t s, const DecodeArgs* pe
       (void)hipGetLastError();
       return limit_error("large selection LDS (descriptors x 28 + selected / 16 bytes) exceeds the device limit");
     }
-    hipLaunchKernelGGL(select, dim3(a.st.retrieval_heads), dim3(LT), lds, s, a);
+    hipLaunchKernelGGL(select, dim3(select_blocks), dim3(LT), lds, s, a, u);
     return launch_check("select_large");
   };
   const bool e4m3 = a.st.centroid_dtype == CKV_E4M3, bf16 = a.kv.dtype == CKV_BF16;
-  if (e4m3 && bf16)
-    return go(score_rows_kernel<CKV_E4M3, CKV_BF16>, score_rows_kernel<CKV_E4M3, CKV_BF16, true>,
-              select_large_kernel<CKV_E4M3, CKV_BF16>);
-  if (e4m3)
-    return go(score_rows_kernel<CKV_E4M3, CKV_F32>, score_rows_kernel<CKV_E4M3, CKV_F32, true>,
-              select_large_kernel<CKV_E4M3, CKV_F32>);
-  if (bf16)
-    return go(score_rows_kernel<CKV_F32, CKV_BF16>, score_rows_kernel<CKV_F32, CKV_BF16, true>,
-              select_large_kernel<CKV_F32, CKV_BF16>);
-  return go(score_rows_kernel<CKV_F32, CKV_F32>, score_rows_kernel<CKV_F32, CKV_F32, true>,
-            select_large_kernel<CKV_F32, CKV_F32>);
+  if (e4m3 && bf16) return go(score_rows_kernel<CKV_E4M3, CKV_BF16>, select_large_kernel<CKV_E4M3, CKV_BF16>);
+  if (e4m3) return go(score_rows_kernel<CKV_E4M3, CKV_F32>, select_large_kernel<CKV_E4M3, CKV_F32>);
+  if (bf16) return go(score_rows_kernel<CKV_F32, CKV_BF16>, select_large_kernel<CKV_F32, CKV_BF16>);
+  return go(score_rows_kernel<CKV_F32, CKV_F32>, select_large_kernel<CKV_F32, CKV_F32>);
 }
 
 }  // namespace ckv

@@ -9,7 +9,8 @@ namespace ckv {
 // Online update of the graph owned by retrieval head rh (no-op for
 // non-owners and assignment NONE): exact top-8 merge over the splits'
 // candidates, assignment, running-mean centroid, delta append, overflow.
-// s_lse0 is the merged lse of the head's first query.  Block size 128..512.
+// s_lse0 is the merged lse of the head's first query.  Block size 128..1024
+// (the top-8 stage uses the first 512 threads).
 //
 // Dependent memory rounds: (1) candidates + cursor/count/total and the free
 // lists, (2) candidate communities + current key row, (3) per-candidate
@@ -67,7 +68,7 @@ __device__ void owner_update(const DecodeArgs& a, const int rh, const float s_ls
     __shared__ uint64_t cand_s[64];
     __shared__ uint64_t s_t8;
     __shared__ int s_ncand;
-    const int nt = blockDim.x;
+    const int nt = min((int)blockDim.x, 512);  // threads of this stage
     const int lane = tid & 63, wave = tid >> 6;
     const int scap = a.ws.slot_capacity;
     const float* scs = a.ws.slot_scores + (int64_t)rh * scap;
@@ -93,7 +94,7 @@ __device__ void owner_update(const DecodeArgs& a, const int rh, const float s_ls
 #pragma unroll
       for (int c = 0; c < CH; ++c) {
         const int s = s0 + c * nt + tid;
-        const bool ok = s < scap && s >= a.cfg.num_sink && pv[c] >= 0 && pv[c] < a.kv.capacity;
+        const bool ok = tid < nt && s < scap && s >= a.cfg.num_sink && pv[c] >= 0 && pv[c] < a.kv.capacity;
         v[c] = ok ? pack_candidate(sv[c], pv[c]) : 0ull;
       }
       cas(v[0], v[2]); cas(v[1], v[3]); cas(v[4], v[6]); cas(v[5], v[7]);
@@ -118,7 +119,7 @@ __device__ void owner_update(const DecodeArgs& a, const int rh, const float s_ls
     uint64_t tmax = loc[0];
     for (int r = 0; r < KAPPA; ++r) {
       const uint64_t best = wave_max_u64(tmax);
-      if (lane == 0) wtop[wave * KAPPA + r] = best;
+      if (lane == 0 && wave < 8) wtop[wave * KAPPA + r] = best;
       if (tmax == best) tmax = 0ull;  // keys are unique (they hold the position)
     }
     __syncthreads();
