@@ -1573,9 +1573,29 @@ size_t fused_lds_bytes(const DecodeArgs& a) {
          attend_part_lds_bytes(SELECT_THREADS / 64);
 }
 
+// Compute units of the current device (cached per device).
+int compute_units() {
+  static int cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
 int coop_parts(const DecodeArgs& a) {
   const int parts = fused_parts(a);
   if (parts == 0 || parts > COOP_MAX_PARTS || a.ws.exchange == nullptr || a.st.centroid_dtype != CKV_E4M3) return 0;
+  // Every part polls for the other parts' scores: the whole grid (with one
+  // pending-update workgroup per head) must be resident at once, one
+  // workgroup per compute unit; a larger layer takes the separate launches
+  // (8 heads x 34 parts at a 4,096-token budget: 293 against 535 us for 8
+  // such sequences, the parts that could not start leaving the others
+  // polling until they scored every community themselves).
+  if ((int64_t)a.st.retrieval_heads * (parts + 1) > compute_units()) return 0;
   return a.st.community_capacity <= 4 * SELECT_THREADS ? parts : 0;
 }
 
