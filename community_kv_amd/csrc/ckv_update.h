@@ -17,8 +17,11 @@ namespace ckv {
 // weight/size/delta tail and centroid rows (slot KAPPA holds the community a
 // new token would open, or the nearest centroid), (4) every candidate's
 // tail-chunk state, in flight during the assignment; then the stores.
-template <int CT, int DT>
+// CH: slots each thread loads per round of the top-8 stage (8 or 9; 9 lets
+// 512 threads take a 4,096-token budget's 4,235 slots in one round).
+template <int CT, int DT, int CH = 8>
 __device__ void owner_update(const DecodeArgs& a, const int rh, const float s_lse0) {
+  static_assert(CH == 8 || CH == 9, "the top-8 stage sorts 8 or 9 keys per round");
   const int tid = threadIdx.x;
   const int graph = a.st.retrieval_to_graph[rh];
   if (a.cfg.assignment == CKV_ASSIGN_NONE || rh != graph) return;
@@ -56,14 +59,13 @@ __device__ void owner_update(const DecodeArgs& a, const int rh, const float s_ls
 
   // ---- stage 1: exact top-8 over every attended non-sink slot (score desc,
   // position asc, as one packed 64-bit key each).  Each thread keeps a sorted
-  // top-8 of its strided share (loaded 8 at a time, one round per chunk;
+  // top-8 of its strided share (loaded CH at a time, one round per chunk;
   // sorted by a 19-comparator network, merged into the running list).  The
   // eighth largest of the threads' maxima, T8, bounds the answer from below:
   // every global top-8 key is at least T8, and only the (at most 8) threads
   // whose maximum reaches T8 hold such keys, so at most 64 candidates remain;
   // wave 0 sorts them.
   {
-    constexpr int CH = 8;
     __shared__ uint64_t wtop[8 * KAPPA];
     __shared__ uint64_t cand_s[64];
     __shared__ uint64_t s_t8;
@@ -103,6 +105,10 @@ __device__ void owner_update(const DecodeArgs& a, const int rh, const float s_ls
       cas(v[2], v[4]); cas(v[3], v[5]);
       cas(v[1], v[4]); cas(v[3], v[6]);
       cas(v[1], v[2]); cas(v[3], v[4]); cas(v[5], v[6]);
+      if constexpr (CH == 9) {  // the ninth key bubbles into the sorted eight
+#pragma unroll
+        for (int k = 7; k >= 0; --k) cas(v[k], v[k + 1]);
+      }
       if (s0 == 0) {
 #pragma unroll
         for (int k = 0; k < KAPPA; ++k) loc[k] = v[k];
