@@ -367,3 +367,86 @@ def test_sync_shared_position_outside_capacity_updates_size_only():
     co.sync_shared(st, assigned=np.array([1]), overflow=np.array([0]), keys_f32=keys, sequence_capacity=8)
     assert st.community_sizes[1, 1] == before.community_sizes[1, 1] + 1
     assert np.array_equal(st.centroids, before.centroids)
+
+
+# ---------------------------------------------------------------------------
+# init_modularity_state (graph/partition.py:495-535)
+# ---------------------------------------------------------------------------
+
+
+def _dense_degrees(labels, edges, capacity):
+    """Community degree sums from a dense symmetric adjacency matrix per graph:
+    an edge {u, v} of weight w adds w to A[u, v] and to A[v, u] (a self loop
+    therefore adds 2w to A[v, v]), a community's weight is the sum of its
+    vertices' rows, and a graph's total is the sum of its matrix (2m in the
+    modularity definition).  Hand-built, unrelated to the scatter formula."""
+    graphs, seq = labels.shape
+    cw = np.zeros((graphs, capacity), np.float64)
+    tw = np.zeros(graphs, np.float64)
+    for g in range(graphs):
+        A = np.zeros((seq, seq), np.float64)
+        for (gg, u, v, w) in edges:
+            if gg != g:
+                continue
+            A[u, v] += w
+            A[v, u] += w
+        deg = A.sum(axis=1)
+        for vtx in range(seq):
+            cw[g, labels[g, vtx]] += deg[vtx]
+        tw[g] = A.sum()
+    return cw, tw
+
+
+def _modularity_case(edges, labels, capacity):
+    labels = np.asarray(labels, np.int32)
+    seq = labels.shape[1]
+    src = np.array([g * seq + u for (g, u, v, w) in edges], np.int64)
+    dst = np.array([g * seq + v for (g, u, v, w) in edges], np.int64)
+    wts = np.array([w for (g, u, v, w) in edges], np.float32)
+    cw, tw = co.init_modularity_state(labels, src, dst, wts, community_capacity=capacity, seq_len=seq)
+    want_cw, want_tw = _dense_degrees(labels, edges, capacity)
+    return cw, tw, want_cw, want_tw
+
+
+def test_init_modularity_state_hand_graphs():
+    # graph 0: vertices 0,1 in community 0; 2,3 in community 1; 4 in community 2 (isolated)
+    # graph 1: vertices 0..2 in community 1; 3,4 in community 0
+    labels = [[0, 0, 1, 1, 2], [1, 1, 1, 0, 0]]
+    edges = [
+        (0, 0, 1, 1.5),    # inside community 0: counted at both endpoints -> +3.0
+        (0, 1, 2, 0.25),   # across 0 and 1
+        (0, 3, 3, 2.0),    # self loop in community 1 -> +4.0
+        (0, 2, 3, 0.0),    # zero weight
+        (1, 0, 4, 0.5),    # across 1 and 0
+        (1, 2, 1, 0.75),   # inside community 1, destination < source
+    ]
+    cw, tw, want_cw, want_tw = _modularity_case(edges, labels, capacity=4)
+    # the hand answer, written out
+    assert cw[0].tolist() == [3.25, 4.25, 0.0, 0.0]
+    assert cw[1].tolist() == [0.5, 2.0, 0.0, 0.0]
+    assert tw.tolist() == [7.5, 2.5]
+    assert np.array_equal(cw.astype(np.float64), want_cw)
+    assert np.array_equal(tw.astype(np.float64), want_tw)
+
+
+def test_init_modularity_state_empty_graph():
+    cw, tw = co.init_modularity_state(np.zeros((2, 3), np.int32), np.zeros(0, np.int64), np.zeros(0, np.int64),
+                                      np.zeros(0, np.float32), community_capacity=5, seq_len=3)
+    assert cw.shape == (2, 5) and tw.shape == (2,)
+    assert not cw.any() and not tw.any()
+
+
+def test_init_modularity_state_random_against_dense_adjacency():
+    rng = np.random.default_rng(7)
+    graphs, seq, capacity = 3, 24, 6
+    labels = rng.integers(0, capacity, size=(graphs, seq))
+    edges = []
+    for _ in range(120):
+        g = int(rng.integers(graphs))
+        u, v = (int(x) for x in rng.integers(seq, size=2))
+        edges.append((g, u, v, float(rng.integers(0, 16)) / 8.0))  # dyadic: float32 sums are exact
+    cw, tw, want_cw, want_tw = _modularity_case(edges, labels, capacity)
+    assert np.array_equal(cw.astype(np.float64), want_cw)
+    assert np.array_equal(tw.astype(np.float64), want_tw)
+    # every community weight is a share of its graph's total
+    assert np.allclose(cw.sum(axis=1), tw)
