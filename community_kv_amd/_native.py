@@ -71,6 +71,7 @@ EXPORTED_SYMBOLS = (
     "ckv_build_layer_state",
     "ckv_leiden_workspace_bytes",
     "ckv_batched_leiden",
+    "ckv_leiden_test_raise_overflow",
     "ckv_aggregate_coo_workspace_bytes",
     "ckv_aggregate_coo",
     "ckv_densify_workspace_bytes",
@@ -251,6 +252,8 @@ def lib() -> ctypes.CDLL:
     handle.ckv_batched_leiden.argtypes = [_p, _p, _p, _i64, _i32, _i32, _f32, _f32, _i32, _i32, _i32, _p, _p, _p,
                                           _p]
     handle.ckv_batched_leiden.restype = ctypes.c_int
+    handle.ckv_leiden_test_raise_overflow.argtypes = [_i32]
+    handle.ckv_leiden_test_raise_overflow.restype = None
     handle.ckv_aggregate_coo_workspace_bytes.argtypes = [_i64]
     handle.ckv_aggregate_coo_workspace_bytes.restype = ctypes.c_size_t
     handle.ckv_aggregate_coo.argtypes = [_p, _p, _p, _i64, _p, _i32, _p, _p, _p, _p, _p, _p]

@@ -419,7 +419,12 @@ __global__ void refine_init_kernel(const int32_t* __restrict__ lm, int32_t V, in
     parent[v] = lm[v];
     labels[v] = v;
   }
-  if (v < CTL_WORDS) ctl[v] = 0;
+  if (v < CTL_WORDS && v != CTL_OVERFLOW) ctl[v] = 0;  // an overflow of the local-moving sweeps stays raised
+}
+
+// Test hook: raises the overflow word as a broken local-moving table would.
+__global__ void raise_overflow_kernel(int32_t* __restrict__ ctl) {
+  if (threadIdx.x == 0) ctl[CTL_OVERFLOW] = 1;
 }
 
 template <int CAP>
@@ -1256,6 +1261,10 @@ inline int64_t adjacency_entries(int32_t graphs, int32_t rows, int32_t kappa, fl
 
 using namespace ckv;
 
+static bool g_test_raise_overflow = false;
+
+extern "C" void ckv_leiden_test_raise_overflow(int32_t enable) { g_test_raise_overflow = enable != 0; }
+
 extern "C" size_t ckv_leiden_workspace_bytes(int64_t edges, int32_t graphs, int32_t seq_len) {
   if (edges < 0 || graphs <= 0 || seq_len <= 0) return 0;
   return leiden_layout(edges, graphs, seq_len).total;
@@ -1339,6 +1348,7 @@ extern "C" int ckv_batched_leiden(const int32_t* edge_src, const int32_t* edge_d
     lm_control_kernel<<<1, 64, 0, st>>>(ctl);
     cur ^= 1;
   }
+  if (g_test_raise_overflow) raise_overflow_kernel<<<1, 64, 0, st>>>(ctl);
   // refinement from singletons inside the local-moving communities
   refine_init_kernel<<<egrid, ETHREADS, 0, st>>>(lab[cur], V, parent, lab[cur ^ 1], ctl);
   cur ^= 1;

@@ -319,6 +319,13 @@ int ckv_batched_leiden(const int32_t* edge_src, const int32_t* edge_dst, const f
                        int32_t seed, int32_t use_boltzmann, int32_t* labels, double* modularity,
                        void* workspace, void* stream);
 
+/* Test hook with no counterpart in the reference: while enabled, every
+ * ckv_batched_leiden call raises its table-overflow word after the
+ * local-moving sweeps, as a broken neighbour-table bound would, so a test can
+ * check that the flag survives refinement and turns the level's modularity
+ * into NaN (run_leiden then raises).  Process-wide, not thread-safe. */
+void ckv_leiden_test_raise_overflow(int32_t enable);
+
 /* Contract an upper-triangular COO by `labels` (super-vertex per vertex, in
  * [0, super_vertices)): both ends relabelled, (min, max) order, duplicates
  * summed, sorted by (src, dst).  Outputs have room for `edges` entries;
@@ -474,7 +481,11 @@ int ckv_decode_layer(const ckv_kv_cache* kv, const ckv_graph_state* state,
  * ceil((num_sink + max_selected + local_window + include_current) / 64) * 64).
  * A layer needing more scratch than the limit (ckv_decode_static_scratch_bytes)
  * fails with CKV_E_LIMIT.  Calls on one GPU share the array and must not
- * overlap (another stream or host thread): they race.  Calls no allocator. */
+ * overlap (another stream or host thread): they race.  Each call first runs a
+ * one-workgroup kernel that clears the exchange row and counters when the
+ * layout stored on the device differs from its own, so eager calls, captured
+ * calls and graph replays may follow each other in any order.  Calls no
+ * allocator. */
 int ckv_decode_layer_static(const ckv_kv_cache* kv, const ckv_graph_state* state,
                             const ckv_prefill_csr* csr, const ckv_delta_chunks* deltas,
                             const ckv_decode_config* config, void* output, float* lse, float* topk_scores,

@@ -218,3 +218,24 @@ def test_run_leiden_rejects_edges_across_graphs(device):
     s, d, w = _dev(device, np.array([0, 3], np.int32), np.array([1, 5], np.int32), np.ones(2, np.float32))
     with pytest.raises(ValueError, match="same graph"):
         algorithm.run_leiden(s, d, w, G=2, seq_len=4)
+
+
+def test_overflow_raised_during_local_moving_reaches_the_caller(device):
+    """A table overflow flagged by the local-moving sweeps must survive the
+    refinement's control reset and make run_leiden raise (the hook raises the
+    device flag after local moving, as a broken table bound would)."""
+    from community_kv_amd import _native
+
+    src, dst, w = lg.planted(3, 2, 300, 6)
+    s, d, x = _dev(device, src, dst, w)
+    print("overflow flag after local moving", flush=True)
+    lib = _native.lib()
+    lib.ckv_leiden_test_raise_overflow(1)
+    try:
+        with pytest.raises(RuntimeError, match="overflowed"):
+            algorithm.run_leiden(s, d, x, G=2, seq_len=300)
+    finally:
+        lib.ckv_leiden_test_raise_overflow(0)
+    torch.cuda.synchronize()
+    _vertex, _part, q = algorithm.run_leiden(s, d, x, G=2, seq_len=300)
+    assert np.isfinite(q)
