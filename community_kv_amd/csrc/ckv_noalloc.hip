@@ -9,10 +9,15 @@
 // shares it and it keeps the last call's contents: calls that overlap on one
 // GPU (two streams, two host threads) race and must not be issued.  The fused
 // launch's counters and epoch-tagged exchange row must start at zero for a
-// given layout (retrieval heads, community capacity and their place in the
-// array); a call whose layout differs from the previous call's on the same
-// GPU (the first call on a GPU included) clears them first with a fill kernel
-// (no memset node, so the call stays capturable).
+// given layout (retrieval heads, community capacity, score coverage and their
+// place in the array).  The array's first 256 bytes hold the key of the
+// layout that last used it, on the device: every call first launches a
+// one-workgroup kernel that compares that key with its own and, when they
+// differ, zeroes the exchange row and counters and stores the new key.  The
+// decision is therefore taken in stream order on the device, so eager calls,
+// captured calls and their replays can be mixed in any order, and a launch
+// that fails leaves the stored key unchanged (no memset node: the call stays
+// capturable).
 #include <mutex>
 
 #include "ckv_device.h"
@@ -27,17 +32,34 @@ constexpr int MAX_DEVICES = 64;
 
 static __device__ __align__(256) unsigned char scratch[SCRATCH_BYTES];
 
+constexpr size_t KEY_BYTES = 256;   // the layout key at the start of the array
+constexpr int KEY_WORDS = 6;
+
 std::mutex g_mutex;
 unsigned char* g_ptr[MAX_DEVICES] = {};   // device address of `scratch` per GPU
-struct ExchangeLayout {  // where the last call on a GPU kept its exchange row and counters
-  int32_t heads, capacity;
-  size_t offset, end;
-};
-ExchangeLayout g_layout[MAX_DEVICES] = {};
 
-__global__ void fill_u32_kernel(uint32_t* __restrict__ p, int64_t n) {
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
-    p[i] = 0u;
+struct LayoutKey {
+  uint32_t w[KEY_WORDS];
+};
+
+// One workgroup: compare the stored key, clear the exchange row and counters
+// (`vecs` 16-byte words) when it differs, then store the new key.  A key word
+// is never zero (heads, capacity and coverage are positive), so the zeroed
+// array of a fresh process never matches.
+__global__ void __launch_bounds__(1024) clear_on_layout_change_kernel(uint32_t* __restrict__ key, LayoutKey now,
+                                                                        uint4* __restrict__ region, int64_t vecs) {
+  __shared__ int differ;
+  if (threadIdx.x == 0) {
+    int d = 0;
+    for (int i = 0; i < KEY_WORDS; ++i) d |= key[i] != now.w[i];
+    differ = d;
+  }
+  __syncthreads();
+  if (differ) {
+    for (int64_t i = threadIdx.x; i < vecs; i += blockDim.x) region[i] = make_uint4(0u, 0u, 0u, 0u);
+    __syncthreads();
+    if (threadIdx.x < KEY_WORDS) key[threadIdx.x] = now.w[threadIdx.x];
+  }
 }
 
 size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
@@ -79,7 +101,7 @@ Layout layout_of(const ckv_graph_state* st, const ckv_decode_config* cfg, int qu
       (size_t)query_heads * l.tiles * CKV_HEAD_DIM * 4,  // partial accumulators
       (size_t)R * l.slot_cap * 4,                 // slot scores
       0};
-  size_t at = 0;
+  size_t at = KEY_BYTES;
   for (int i = 0; i < 15; ++i) {
     l.off[i] = at;
     at += align256(sizes[i]);
@@ -119,7 +141,6 @@ extern "C" int ckv_decode_layer_static(const ckv_kv_cache* kv, const ckv_graph_s
     return ckv_internal::set_error(CKV_E_LAUNCH, "no current HIP device");
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   unsigned char* base = nullptr;
-  bool clear = false;
   {
     std::lock_guard<std::mutex> lock(g_mutex);
     if (g_ptr[dev] == nullptr) {
@@ -132,10 +153,6 @@ extern "C" int ckv_decode_layer_static(const ckv_kv_cache* kv, const ckv_graph_s
       g_ptr[dev] = static_cast<unsigned char*>(p);
     }
     base = g_ptr[dev];
-    const ExchangeLayout now{st->retrieval_heads, st->community_capacity, l.off[7], l.off[10]};
-    const ExchangeLayout& was = g_layout[dev];
-    clear = was.heads != now.heads || was.capacity != now.capacity || was.offset != now.offset || was.end != now.end;
-    g_layout[dev] = now;
   }
   ckv_decode_workspace ws;
   ws.scores = reinterpret_cast<uint16_t*>(base + l.off[0]);
@@ -162,11 +179,16 @@ extern "C" int ckv_decode_layer_static(const ckv_kv_cache* kv, const ckv_graph_s
   ws.slot_capacity = l.slot_cap;
   ws.budget_tiles = l.budget_tiles;
   ws.score_blocks = l.score_blocks;
-  if (clear) {
-    // exchange row and block counters are contiguous: zero both
-    const int64_t words = (int64_t)(l.off[10] - l.off[7]) / 4;
-    hipLaunchKernelGGL(fill_u32_kernel, dim3((unsigned)std::min<int64_t>((words + 255) / 256, 1024)), dim3(256), 0,
-                       s, reinterpret_cast<uint32_t*>(base + l.off[7]), words);
+  {
+    // exchange row and block counters are contiguous (256-byte aligned): zero both on a layout change.
+    // The score coverage is part of the key because the fused and the multi-kernel selections write the
+    // nearest-centroid words of the exchange row in different formats.
+    const LayoutKey now{{(uint32_t)st->retrieval_heads, (uint32_t)st->community_capacity,
+                         (uint32_t)cfg->score_coverage, (uint32_t)l.off[7], (uint32_t)l.off[10],
+                         (uint32_t)kv->query_heads}};
+    const int64_t vecs = (int64_t)(l.off[10] - l.off[7]) / 16;
+    hipLaunchKernelGGL(clear_on_layout_change_kernel, dim3(1), dim3(1024), 0, s, reinterpret_cast<uint32_t*>(base),
+                       now, reinterpret_cast<uint4*>(base + l.off[7]), vecs);
     const int rc = ckv::launch_check("static scratch clear");
     if (rc) return rc;
   }

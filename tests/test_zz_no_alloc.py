@@ -108,3 +108,52 @@ def test_static_decode_rejects_layers_over_the_limit(device):
         out["topk_positions"].data_ptr(), out["assigned"].data_ptr(), out["overflow"].data_ptr(),
         ctypes.c_void_p(nat.stream_handle(device)))
     assert rc != 0 and b"static decode scratch" in lib.ckv_last_error()
+
+
+def test_static_decode_captured_and_replayed_between_other_layouts(device):
+    """ckv_decode_layer_static captured in a HIP graph: each replay must equal
+    ckv_decode_layer on a twin layer, also when eager static calls of another
+    layout (other head count and community capacity) run between replays."""
+    params = co.StepParams(group_size=4, num_sink=10, token_budget=1024, local_window=128)
+    fx = syn.build_layer(seed=91, query_heads=32, kv_heads=8, seq_len=16384, communities=400, num_sink=10,
+                         max_decode_tokens=8, aggregation=co.QUERY_GROUP)
+    other_params = co.StepParams(group_size=4, num_sink=10, token_budget=256, local_window=32,
+                                 assignment="nearest_centroid")
+    other_fx = syn.build_layer(seed=92, query_heads=8, kv_heads=2, seq_len=2048, communities=40, num_sink=10,
+                               max_decode_tokens=16, aggregation=co.QUERY_GROUP)
+    print("no-alloc graph capture: 32/8 heads 16384 tokens between 8/2 heads 2048 tokens", flush=True)
+    ref = _layer(fx, params, device)
+    tst = _layer(fx, params, device)
+    other = _layer(other_fx, other_params, device)
+    out = _outputs(fx, device)
+    other_out = _outputs(other_fx, device)
+    torch.cuda.synchronize(device)
+    stream = torch.cuda.Stream(device)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        _static_decode(tst, out, device)       # warm-up outside the capture (first-call set-up)
+        stream.synchronize()
+        ref["call"].decode()
+        stream.synchronize()
+        # the warm-up advanced both layers by one identical step
+        with torch.cuda.graph(graph, stream=stream):
+            _static_decode(tst, out, device)
+    torch.cuda.synchronize(device)
+    rng = np.random.default_rng(5)
+    for replay in range(3):
+        _static_decode(other, other_out, device)          # another layout in between
+        torch.cuda.synchronize(device)
+        graph.replay()
+        ref["call"].decode()
+        torch.cuda.synchronize(device)
+        att = ref["ws"].attention
+        assert torch.equal(att.output, out["output"]), (replay, "output")
+        assert torch.equal(att.lse, out["lse"]), (replay, "lse")
+        assert torch.equal(att.topk_positions, out["topk_positions"]), (replay, "topk positions")
+        assert torch.equal(ref["ws"].update.assigned_communities, out["assigned"]), (replay, "assigned")
+        h.assert_states_equal(h.state_to_numpy(ref["state"], ref["cur"], True),
+                              h.state_to_numpy(tst["state"], tst["cur"], True))
+        q = h.torch_values(syn.fresh_query(fx, rng), fx.dtype, device)
+        ref["q"].copy_(q)
+        tst["q"].copy_(q)
+        torch.cuda.synchronize(device)
