@@ -161,5 +161,78 @@ def consistent_topk(raw_scores, chosen_cols, *, num_sink, row, kappa, eps=1e-4):
     return True, ""
 
 
+# ---------------------------------------------------------------------------
+# The reference's approximate top-8 (WarpSelect<2, 8, 16>, patch:477-723)
+# ---------------------------------------------------------------------------
+
+LANE_QUEUE = 6      # LocalK: packed candidates one lane keeps (patch:501)
+ROW_LANES = 4       # LogicalWarp: lanes that share one accumulator row (patch:502)
+
+
+def warpselect_lane(col):
+    """Lane (of the four row-mates) that holds column ``col`` of the QK
+    accumulator: an SM90 wgmma C fragment gives lane l of a quad the column
+    pairs 8j + 2l, 8j + 2l + 1 of its rows (the coordinates ``update_row``
+    reads through tScS_selector, patch:282-286, 586-589).  Tiles start at
+    multiples of kBlockN (a multiple of 8), so the class is a function of the
+    absolute column."""
+    return (np.asarray(col, dtype=np.int64) % 8) // 2
+
+
+def warpselect_topk(raw_scores, *, row, num_sink, kappa=8, tile=128):
+    """The reference's approximate top-8 of one query row, restated.
+
+    Each lane keeps the ``LANE_QUEUE`` largest packed keys (quantised score <<
+    17 | column) among the eligible columns of its class (``insert`` keeps a
+    sorted queue and admits a candidate only above its last entry,
+    patch:556-596), and ``write_row`` merges the four sorted queues by
+    repeatedly taking the largest head (patch:640-690), i.e. the top 8 of
+    their union.  The tile skip (a tile is passed over when every lane's own
+    tile max is at most its sixth key's score, patch:578-583) is applied per
+    lane over tiles of ``tile`` columns in the kernel's order, the diagonal tile
+    first and then backwards; it can only pass over a candidate whose key equals
+    the lane's sixth key, and every such candidate has a smaller column than
+    the resident key (it comes from a later-processed, lower tile), so it would
+    not have been admitted either: the result equals the per-lane top-6
+    without the skip.  Both are computed and the equality asserted.  Masked
+    columns (beyond the row) never reach the output for rows with at least
+    kappa eligible columns, so they are left out.
+
+    ``raw_scores`` holds the scores of columns 0..row (float64 or float32;
+    quantised in float32).  Returns the 8 chosen columns in the merge's
+    output order (descending packed key)."""
+    if kappa != 8:
+        raise ValueError("the reference's WarpSelect is specialised for kappa = 8 only")
+    s = np.asarray(raw_scores)[:row + 1].astype(np.float32)
+    cols = np.arange(num_sink, row + 1)
+    packed = pack_candidates(quantise_score(s[num_sink:row + 1]), cols)
+    lanes = warpselect_lane(cols)
+    queues = []
+    for lane in range(ROW_LANES):
+        own = np.sort(packed[lanes == lane])[::-1][:LANE_QUEUE]
+        queues.append(own)
+    # the streaming form with the tile skip, lane by lane
+    for lane in range(ROW_LANES):
+        q = []                                  # sorted descending, at most LANE_QUEUE
+        last_tile = row // tile
+        for t in range(last_tile, -1, -1):
+            lo, hi = t * tile, min(row, t * tile + tile - 1)
+            sel = (cols >= lo) & (cols <= hi) & (lanes == lane)
+            if not sel.any():
+                continue
+            tile_keys = packed[sel]
+            tile_max = s[cols[sel]].max()
+            if len(q) == LANE_QUEUE and tile_max <= dequantise_key(q[-1] >> INDEX_BITS):
+                continue
+            for cand in tile_keys:              # ascending columns inside the tile
+                if len(q) < LANE_QUEUE or cand > q[-1]:
+                    q.append(int(cand))
+                    q.sort(reverse=True)
+                    del q[LANE_QUEUE:]
+        assert q == queues[lane].tolist(), "the tile skip changed a lane queue"
+    merged = np.sort(np.concatenate(queues))[::-1][:kappa]
+    return (merged & ((1 << INDEX_BITS) - 1)).astype(np.int64)
+
+
 __all__ = ["consistent_topk", "dequantise_key", "pack_candidates", "prefill_attention_topk", "prefill_rows",
-           "quantise_score", "row_scores", "topk_row_skip"]
+           "quantise_score", "row_scores", "topk_row_skip", "warpselect_lane", "warpselect_topk"]

@@ -94,3 +94,88 @@ def test_consistent_topk_accepts_exact_and_rejects_swaps():
     assert not op.consistent_topk(s, worse, num_sink=sinks, row=row, kappa=kappa)[0]
     assert not op.consistent_topk(s, np.r_[best[:-1], 2], num_sink=sinks, row=row, kappa=kappa)[0]
     assert not op.consistent_topk(s, np.r_[best[:-1], best[0]], num_sink=sinks, row=row, kappa=kappa)[0]
+
+
+# ---------------------------------------------------------------------------
+# The reference's approximate top-8 (WarpSelect<2, 8, 16>, community-kv.patch:477-723)
+# ---------------------------------------------------------------------------
+
+
+def test_warpselect_lane_classes_are_column_pairs():
+    # lane l of a quad owns columns 8j + 2l and 8j + 2l + 1
+    assert op.warpselect_lane(np.arange(16)).tolist() == [0, 0, 1, 1, 2, 2, 3, 3] * 2
+    assert op.warpselect_lane([130, 133, 1023]).tolist() == [1, 2, 3]
+
+
+def test_warpselect_drops_the_seventh_of_one_lane():
+    """Eight best columns: seven in lane 0's class (0, 1, 8, 9, 16, 17, 24) and
+    column 2 (lane 1).  Lane 0 keeps only six, so its weakest (24) is replaced
+    by the best remaining column of another class (column 11, lane 1)."""
+    row = 40
+    s = np.full(row + 1, -1.0)
+    for rank, c in enumerate([0, 1, 8, 9, 16, 17, 24]):
+        s[c] = 10.0 - rank            # 10, 9, ..., 4
+    s[2] = 3.5
+    s[11] = 2.0                       # next best outside the seven
+    s[25] = 1.5                       # lane 0 again: below lane 0's sixth, and lane 0 is full
+    got = op.warpselect_topk(s, row=row, num_sink=0)
+    assert got.tolist() == [0, 1, 8, 9, 16, 17, 2, 11]
+    exact = [0, 1, 8, 9, 16, 17, 24, 2]
+    assert sorted(got.tolist()) != sorted(exact)
+
+
+def test_warpselect_six_per_lane_is_exact():
+    """Six of the best eight in one class still fit its queue: same set and
+    order as the exact top-8."""
+    row = 70
+    s = np.zeros(row + 1)
+    best = [64, 65, 56, 57, 48, 49, 3, 13]     # six in lane 0, then lanes 1 and 2
+    for rank, c in enumerate(best):
+        s[c] = 20.0 - rank
+    assert op.warpselect_topk(s, row=row, num_sink=0).tolist() == best
+
+
+def test_warpselect_respects_sinks_and_ties():
+    """Sinks are never candidates; equal quantised scores go to the larger column."""
+    row = 30
+    s = np.zeros(row + 1)
+    s[:4] = 50.0                      # sinks: the highest scores, excluded
+    got = op.warpselect_topk(s, row=row, num_sink=4)
+    # every eligible column ties: the largest columns win, at most six per lane
+    want = sorted(range(4, row + 1), reverse=True)[:8]
+    assert got.tolist() == want      # 30..23 covers each lane twice
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_warpselect_differs_only_when_a_lane_holds_seven(seed):
+    """Against a brute force over random rows: the approximate set equals the
+    exact top-8 exactly when no lane class holds seven or more of the exact
+    eight; otherwise it holds six of that lane and the best of the rest."""
+    rng = np.random.default_rng(seed)
+    differ = 0
+    for trial in range(300):
+        row = int(rng.integers(20, 200))
+        sinks = int(rng.integers(0, 8))
+        s = rng.standard_normal(row + 1) * (0.02 if trial % 3 == 0 else 2.0)   # some rows full of ties
+        if trial % 5 == 0:                                                       # plant a crowded lane
+            cls = int(rng.integers(4))
+            cols = [c for c in range(sinks, row + 1) if (c % 8) // 2 == cls]
+            for c in rng.choice(cols, size=min(8, len(cols)), replace=False):
+                s[c] += 6.0
+        keys = op.quantise_score(s.astype(np.float32))
+        cand = sorted(range(sinks, row + 1), key=lambda c: (keys[c], c), reverse=True)
+        exact = cand[:8]
+        per_lane = {}
+        for c in exact:
+            per_lane.setdefault((c % 8) // 2, []).append(c)
+        crowded = [l for l, v in per_lane.items() if len(v) >= 7]
+        got = op.warpselect_topk(s, row=row, num_sink=sinks).tolist()
+        if not crowded:
+            assert got == exact
+        else:
+            differ += 1
+            lane = crowded[0]
+            kept = [c for c in cand if (c % 8) // 2 == lane][:6]
+            rest = [c for c in cand if (c % 8) // 2 != lane][:2]
+            assert sorted(got) == sorted(kept + rest)
+    assert differ > 0
