@@ -232,10 +232,22 @@ def profiled_traffic():
 
 
 def cpu_workers():
-    """Host cores the CPU baselines use: the box's CPU share (OMP_NUM_THREADS
-    there), at most os.cpu_count() and at most 16."""
-    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
-    return max(1, min(share, os.cpu_count() or 1, 16))
+    """Host cores the CPU baselines use: every core this process may use.  On
+    a machine that sets OMP_NUM_THREADS to the job's CPU share (the one-GPU box
+    sets 16 and counts worker processes against it, while os.cpu_count()
+    reports the whole host), that share; otherwise os.cpu_count()."""
+    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    total = os.cpu_count() or 1
+    return max(1, min(share, total) if share > 0 else total)
+
+
+def cpu_core_note(workers):
+    """How the core count was chosen, for cpu_baseline.sample."""
+    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    if share > 0 and workers == min(share, os.cpu_count() or 1):
+        return (f"{workers} worker processes = this job's CPU share (OMP_NUM_THREADS={share}; "
+                f"os.cpu_count() reports {os.cpu_count()} host-wide)")
+    return f"{workers} worker processes = os.cpu_count()"
 
 
 def run_cpu_workers(kind, arrays, seconds):
@@ -289,7 +301,8 @@ def cpu_baseline(entry, seconds=20.0):
     rate = sum(o["steps"] / o["seconds"] for o in outs)  # layer-steps per second over all cores
     return {"value": rate / LAYERS, "unit": "tokens/s", "cores": workers, "kind": "port",
             "sample": f"{steps} decode layer-steps of one config-2 layer through the numpy oracle on {workers} "
-                      f"host cores ({workers / rate * 1e3:.1f} ms per layer-step per core), scaled to 36 layers"}
+                      f"host cores ({workers / rate * 1e3:.1f} ms per layer-step per core), scaled to 36 layers; "
+                      f"{cpu_core_note(workers)}"}
 
 
 MFMA_BF16_PEAK_TFLOPS = 2500.0
@@ -311,7 +324,7 @@ def prefill_cpu_baseline(q, k, v, scale, sinks, kappa, seconds):
                       f"{workers} host cores, scaled by causal columns to the whole prefill"}
 
 
-def run_prefill(args, device):
+def run_prefill(args, device, emit=True):
     from community_kv_amd.attention.flash_attention import prefill_attention_topk
 
     q, k, v = planted_prefill_inputs(device, seq=args.prefill_seq)
@@ -350,9 +363,12 @@ def run_prefill(args, device):
                      "frac": tflops / MFMA_BF16_PEAK_TFLOPS, "traffic": None,
                      "kernel": "prefill_mfma_kernel<16>", "flops_per_launch": flops},
     }
+    if not emit:
+        return result
     if not args.no_cpu:
         result["cpu_baseline"] = prefill_cpu_baseline(q, k, v, scale, SINKS, PREFILL_KAPPA, args.cpu_seconds)
     print(json.dumps(result), flush=True)
+    return result
 
 
 STATE_KAPPA = 8  # the prefill edge width the runtime requests
@@ -607,7 +623,7 @@ BATCH_MIN, BATCH_MAX = 16384, 131072
 BATCH_BUDGET = 4096
 
 
-def run_batched(args, device):
+def run_batched(args, device, emit=True):
     """a ragged batch of 8 sequences (lengths uniform in
     [16k, 128k], length/64 Zipf communities per KV head, 4096-token budget +
     128 window), one Qwen3-8B-shaped layer; a step decodes one token of every
@@ -650,6 +666,7 @@ def run_batched(args, device):
     att_graph.replay()
     part_ms = time_graph(att_graph, max(10, args.steps), device)
     achieved = float(np.sum(att_bytes)) / (part_ms * 1e-3) / 1e9
+    step_bytes = algorithmic_bytes(stack)[1] * len(stack)
     overflow = sum(int(e["layer"].workspace.update.overflow.sum().item()) for e in stack)
     result = {
         "metric": "batched_ragged_decode_tokens_per_s_qwen3_8b_layer",
@@ -669,6 +686,8 @@ def run_batched(args, device):
                    "context_lengths": [int(n) for n in lens], "token_budget": BATCH_BUDGET, "local_window": WINDOW},
         "us_per_batch_step": ms * 1e3,
         "us_per_batch_step_sequence_by_sequence": serial_ms * 1e3,
+        "step_algorithmic_bytes": step_bytes,
+        "step_hbm_frac": step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
         "overflow_flags": overflow,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": None,
@@ -676,7 +695,36 @@ def run_batched(args, device):
                      "bytes_per_launch": float(np.sum(att_bytes))},
         "attention_partials_kernel_us": part_ms * 1e3,
     }
-    print(json.dumps(result), flush=True)
+    if emit:
+        print(json.dumps(result), flush=True)
+    return result
+
+
+def side_configs(args, device):
+    """Short timed runs of configs 5 (prefill edge export) and 4 (batched
+    ragged decode) for the default line, each with its own roofline: a few
+    launches / graph replays, so the default command stays short."""
+    import types
+
+    out = {}
+    pre = run_prefill(types.SimpleNamespace(prefill_seq=PREFILL_SEQ, warmup=1, steps=5, no_cpu=True), device,
+                      emit=False)
+    out["prefill_ms"] = pre["value"]
+    out["prefill_tflops"] = pre["roofline"]["achieved"]
+    out["prefill_mfma_frac"] = pre["roofline"]["frac"]
+    torch.cuda.empty_cache()
+    bat = run_batched(types.SimpleNamespace(warmup=3, steps=20), device, emit=False)
+    out["batched_us_per_step"] = bat["us_per_batch_step"]
+    out["batched_tokens_per_s"] = bat["value"]
+    out["batched_attention_kernel_us"] = bat["attention_partials_kernel_us"]
+    out["batched_hbm_frac"] = bat["roofline"]["frac"]
+    out["batched_step_hbm_frac"] = bat["step_hbm_frac"]
+    out["side_configs"] = ("prefill_*: BASELINE config 5 (32,768-token causal prefill, 32/8 heads, top-16 edges), "
+                           "mean of 5 launches after 1 warm-up, MFMA roofline = 4*128*32*S(S+1)/2 FLOP / time / "
+                           "2.5 PFLOP/s; batched_*: BASELINE config 4 (8 ragged sequences), mean of 20 graph-replayed "
+                           "steps after 3, batched_hbm_frac = the batched attention kernel's algorithmic bytes / its "
+                           "time / 8 TB/s, batched_step_hbm_frac = the whole step's algorithmic bytes / step time")
+    return out
 
 
 def dense_decode_ms(stack, seq, reps, device):
@@ -770,6 +818,8 @@ def main():
     ap.add_argument("--layers", type=int, default=LAYERS)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--no-side", action="store_true",
+                    help="decode: leave out the short config-5 prefill and config-4 batched runs of the default line")
     ap.add_argument("--leiden", action="store_true",
                     help="generate: partition every prompt layer with the native Leiden instead of synthetic labels")
     ap.add_argument("--partition-inline", action="store_true",
@@ -912,6 +962,8 @@ def main():
                                "selection, slot resolution, KV gather + MFMA attention, in-launch split merge)",
                      "bytes_per_launch": fused_bytes},
     }
+    if not args.no_side:
+        result.update(side_configs(args, device))
     if args.copy_probe:
         src = torch.empty(64 << 20, dtype=torch.int32, device=device)
         dst = torch.empty_like(src)
