@@ -31,6 +31,11 @@ HIP_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
 
+# Flags for single sources.  The prefill attention takes maxima of MFMA
+# results that are finite or -inf: without NaNs to honour, fmaxf needs no
+# NaN-quieting moves in front of v_max3_f32.
+FILE_FLAGS = {"ckv_prefill.hip": ["-fno-honor-nans"]}
+
 ABI_VERSION = 3
 
 CKV_BF16, CKV_F32, CKV_E4M3 = 0, 1, 2
@@ -177,7 +182,8 @@ def build(verbose: bool = False) -> str:
     compile_flags = [f for f in HIP_FLAGS if f != "-shared"]
     with tempfile.TemporaryDirectory(prefix="ckv_build_") as tmp:
         objects = [os.path.join(tmp, os.path.basename(src) + ".o") for src in sources]
-        cmds = [[HIPCC, *compile_flags, *include, "-c", "-o", obj, src] for src, obj in zip(sources, objects)]
+        cmds = [[HIPCC, *compile_flags, *FILE_FLAGS.get(os.path.basename(src), []), *include, "-c", "-o", obj, src]
+                for src, obj in zip(sources, objects)]
 
         def run(cmd):
             return subprocess.run(cmd, capture_output=True, text=True)

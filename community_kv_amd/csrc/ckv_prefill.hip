@@ -314,11 +314,12 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_mfma_kernel(ckv_pref
   if (tiles > 1) issue_tile(tiles - 2, 1);
   __builtin_amdgcn_s_waitcnt(VMCNT0);
   __syncthreads();
-  f32x16_t sacc[2];
-  qk_tile(0, sacc);
+  f32x16_t sa[2], sb[2];  // this tile's scores / the next tile's, swapped by the two-tile unroll
+  qk_tile(0, sa);
 
   int stage = 0;
-  for (int t = tiles - 1; t >= 0; --t) {
+  // One tile: `cur` holds tile t's scores; the next tile's QK^T goes into `nxt`.
+  auto tile_step = [&](const int t, f32x16_t (&cur)[2], f32x16_t (&nxt)[2]) __attribute__((always_inline)) {
     const int nstage = stage == 2 ? 0 : stage + 1;
     if (t >= 2) issue_tile(t - 2, nstage == 2 ? 0 : nstage + 1);
     const int c0 = t * PF_KEYS;
@@ -330,44 +331,47 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_mfma_kernel(ckv_pref
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
           const int col = c0 + 32 * b + 8 * (v >> 2) + 4 * half + (v & 3);
-          if (col > pos) sacc[b][v] = NEG_INF;
+          if (col > pos) cur[b][v] = NEG_INF;
         }
       }
     }
-    // Maxima of the groups of PF_GROUP columns (group g = accumulator g / GPA,
-    // registers GS (g % GPA) ..).
-    constexpr int GS = PF_GROUP, NG = 32 / GS, GPA = 16 / GS;
-    float gmax[NG];
+    // The lane's tile maximum (three-input maxima); the group maxima are
+    // formed only inside the rare inspection below.
+    // (this file is compiled with -fno-honor-nans: no NaN-quieting moves
+    // before the maxima of MFMA results, which are finite or -inf)
+    auto at = [&](int i) { return cur[i >> 4][i & 15]; };
+    auto max3 = [](float x, float y, float z) { return __builtin_fmaxf(__builtin_fmaxf(x, y), z); };
+    float m3[11];
 #pragma unroll
-    for (int g = 0; g < NG; ++g) {
-      gmax[g] = sacc[g / GPA][GS * (g % GPA)];
-#pragma unroll
-      for (int e = 1; e < GS; ++e) gmax[g] = __builtin_fmaxf(gmax[g], sacc[g / GPA][GS * (g % GPA) + e]);
-    }
-    float lmax = gmax[0];
-#pragma unroll
-    for (int g = 1; g < NG; ++g) lmax = __builtin_fmaxf(lmax, gmax[g]);
+    for (int i = 0; i < 10; ++i) m3[i] = max3(at(3 * i), at(3 * i + 1), at(3 * i + 2));
+    m3[10] = max3(at(30), at(31), m3[9]);
+    const float lmax = max3(max3(m3[0], m3[1], m3[2]), max3(m3[3], m3[4], m3[5]),
+                            max3(m3[6], m3[7], __builtin_fmaxf(m3[8], m3[10])));
 
-    // Top-kappa candidates of this lane's 32 columns, by groups: every
-    // score above the filter goes to the pending buffer (sinks and keys the
-    // queue would not keep are dropped by the merge, which is cheaper than
-    // testing each candidate), merged first when this group could overflow it.
-    // Placed before the tile's LDS reads are issued, so the rare branch waits
-    // for nothing outstanding.
+    // Top-kappa candidates of this lane's 32 columns, by groups of PF_GROUP
+    // columns: every score above the filter goes to the pending buffer
+    // (sinks and keys the queue would not keep are dropped by the merge,
+    // which is cheaper than testing each candidate), merged first when this
+    // group could overflow it.  Placed before the tile's LDS reads are
+    // issued, so the rare branch waits for nothing outstanding.
 #ifndef CKV_PF_NO_TOPK
     if (__builtin_amdgcn_ballot_w64(lmax >= tf)) {
+      constexpr int GS = PF_GROUP, NG = 32 / GS, GPA = 16 / GS;
 #pragma unroll
       for (int g = 0; g < NG; ++g) {
-        if (__builtin_amdgcn_ballot_w64(gmax[g] >= tf)) {
+        float gmax = cur[g / GPA][GS * (g % GPA)];
+#pragma unroll
+        for (int e = 1; e < GS; ++e) gmax = __builtin_fmaxf(gmax, cur[g / GPA][GS * (g % GPA) + e]);
+        if (__builtin_amdgcn_ballot_w64(gmax >= tf)) {
           int cnt = 0;
 #pragma unroll
-          for (int e = 0; e < GS; ++e) cnt += sacc[g / GPA][GS * (g % GPA) + e] >= tf ? 1 : 0;
+          for (int e = 0; e < GS; ++e) cnt += cur[g / GPA][GS * (g % GPA) + e] >= tf ? 1 : 0;
           if (__builtin_amdgcn_ballot_w64(nbuf + cnt > PF_BUF)) flush();
 #pragma unroll
           for (int e = 0; e < GS; ++e) {
             const int b = g / GPA;
             const int v = GS * (g % GPA) + e;
-            const float sv = sacc[b][v];
+            const float sv = cur[b][v];
             const int col = c0 + 32 * b + 8 * (v >> 2) + 4 * half + (v & 3);
             if (sv >= tf) {
               buf_lds[nbuf * (64 * PF_WAVES)] =
@@ -397,15 +401,14 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_mfma_kernel(ckv_pref
 
     // Next tile's scores on the matrix cores while this tile's exponentials run
     // (on the last tile this reads a stale stage and the result is unused).
-    f32x16_t snext[2];
-    qk_tile(nstage, snext);
+    qk_tile(nstage, nxt);
     uint32_t pb[2][8];
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
 #pragma unroll
       for (int v = 0; v < 16; v += 2) {
-        const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[b][v], sl2, -mc));
-        const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[b][v + 1], sl2, -mc));
+        const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(cur[b][v], sl2, -mc));
+        const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(cur[b][v + 1], sl2, -mc));
         l += p0;
         l += p1;
         pb[b][v >> 1] = pack_bf16x2_hw(p0, p1);
@@ -430,11 +433,21 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_mfma_kernel(ckv_pref
         o[db] = mfma32(uint4{lo.x, lo.y, hi.x, hi.y}, bop, o[db]);
       }
     }
-    sacc[0] = snext[0];
-    sacc[1] = snext[1];
     __builtin_amdgcn_s_waitcnt(VMCNT0);
     __syncthreads();
     stage = nstage;
+  };
+  // Software pipeline over three LDS stages, diagonal tile first and then
+  // backwards (the nearest keys tend to score highest, which raises the
+  // top-kappa threshold early).  Iteration t: tile t's scores are in
+  // registers, tile t - 1 is resident in LDS and tile t - 2 is in flight.  The
+  // QK^T MFMAs of tile t - 1 are issued next to tile t's softmax, so the
+  // matrix cores work while the vector ALUs do.  Two tiles per loop trip, the
+  // score buffers alternating, so no accumulator is copied.
+  for (int t = tiles - 1; t >= 0; t -= 2) {
+    tile_step(t, sa, sb);
+    if (t == 0) break;
+    tile_step(t - 1, sb, sa);
   }
 
   if (__builtin_amdgcn_ballot_w64(nbuf > 0)) flush();
