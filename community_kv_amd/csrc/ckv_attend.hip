@@ -534,9 +534,8 @@ __global__ __launch_bounds__(256) void merge_kernel(DecodeArgs a, int splits) {
 // consecutive 64-slot tiles of one retrieval head; each wave runs mfma_tile on
 // one tile, the workgroup combines its waves in LDS into one split partial
 // (max, sum, unnormalised P.V per query) plus the first query's score of every
-// slot (the candidates of the online update's top-8).  With MERGE the
-// last workgroup of a head to finish merges the splits into output and lse.
-template <bool MERGE>
+// slot (the candidates of the online update's top-8); a separate launch
+// merges the splits.
 __device__ __forceinline__ void attend_mfma_body(const DecodeArgs& a, const int rh) {
   // Per-wave V half-tile buffers (8 KB each); reused for the waves' P.V rows
   // and, in the last workgroup, as the split-merge scratch.
@@ -561,7 +560,6 @@ __device__ __forceinline__ void attend_mfma_body(const DecodeArgs& a, const int 
   __shared__ float cand_s[ATT_WAVES][TILE];
   __shared__ float wm_s[ATT_WAVES][CKV_MAX_GROUP];
   __shared__ float wl_s[ATT_WAVES][CKV_MAX_GROUP];
-  __shared__ int last_block;
   __shared__ float s_lse0;
 
   const int tile = wgi * ATT_WAVES + wave;
@@ -646,36 +644,15 @@ __device__ __forceinline__ void attend_mfma_body(const DecodeArgs& a, const int 
   }
   CKV_STAMP(rh == 0 && wgi == 0, 11);
   CKV_STAMP(rh == 0 && wgi == 0, 2);
-  if (!MERGE) return;
-  // The last workgroup of this head to finish merges the splits.
-  CKV_STAMP_MAX(rh == 0, 12);
-  __threadfence();
-  __syncthreads();
-  CKV_STAMP_MAX(rh == 0, 13);
-  if (tid == 0) {
-    uint32_t* counter = a.ws.block_counters + a.st.retrieval_heads + rh;
-    const unsigned prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    last_block = (prev == (unsigned)splits - 1u) ? 1 : 0;
-    if (last_block) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  CKV_STAMP_MAX(rh == 0, 14);
-  __syncthreads();
-  if (!last_block) return;
-  __threadfence();
-  CKV_STAMP(rh == 0, 3);
-  merge_group<CKV_BF16>(a, rh, splits, reinterpret_cast<float*>(att_dyn), nullptr);
-  CKV_STAMP(rh == 0, 4);
-  CKV_STAMP_MAX(true, 15);
 }
 
-template <bool MERGE>
 __global__ __launch_bounds__(64 * ATT_WAVES) void attend_mfma_kernel(DecodeArgs a) {
-  attend_mfma_body<MERGE>(a, blockIdx.y);
+  attend_mfma_body(a, blockIdx.y);
 }
 
 __global__ __launch_bounds__(64 * ATT_WAVES) void attend_mfma_batch_kernel(const DecodeArgs* __restrict__ table,
                                                                            int heads) {
-  attend_mfma_body<false>(table[blockIdx.y / heads], blockIdx.y % heads);
+  attend_mfma_body(table[blockIdx.y / heads], blockIdx.y % heads);
 }
 
 // Dense bf16 decode baseline: each wave streams `chunk_tiles` consecutive
@@ -777,7 +754,7 @@ int launch_attention(const DecodeArgs& a, hipStream_t s, bool partials_only) {
       return ckv_internal::set_error(CKV_E_LIMIT, "too many attention splits for the merge scratch");
     }
     const dim3 grid(splits, a.st.retrieval_heads);
-    hipLaunchKernelGGL(attend_mfma_kernel<false>, grid, dim3(64 * ATT_WAVES), 0, s, a);
+    hipLaunchKernelGGL(attend_mfma_kernel, grid, dim3(64 * ATT_WAVES), 0, s, a);
     const int r = launch_check("attend_mfma");
     if (r || partials_only) return r;
     return launch_merge(a, s, splits);

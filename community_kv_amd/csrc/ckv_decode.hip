@@ -304,10 +304,11 @@ namespace {
 // group size, retrieval heads, slot capacity and assignment mode; items must
 // not share state or workspace.
 int validate_batch(const ckv_layer_args* items, int count, std::vector<ckv::DecodeArgs>* packed, int* max_nscore,
-                   size_t* max_lds, bool* any_shared) {
+                   size_t* max_lds, bool* any_shared, size_t* max_large_lds) {
   if (!items || count <= 0) return fail(CKV_E_INVALID, "empty batch");
   *max_nscore = 0;
   *max_lds = 0;
+  *max_large_lds = 0;
   *any_shared = false;
   for (int i = 0; i < count; ++i) {
     const ckv_layer_args& it = items[i];
@@ -316,8 +317,11 @@ int validate_batch(const ckv_layer_args* items, int count, std::vector<ckv::Deco
     if (rc) return rc;
     const ckv::DecodeArgs a = pack(it.kv, it.state, it.csr, it.deltas, it.config, it.ws);
     if (a.kv.dtype != CKV_BF16) return fail(CKV_E_INVALID, "batched decode requires bf16 KV");
-    if (std::min(a.st.community_capacity, a.ws.score_blocks * CKV_SCORE_BLOCK) > CKV_MAX_SELECT_ROWS)
-      return fail(CKV_E_LIMIT, "batched decode scores at most 8192 communities per head (use ckv_decode_layer)");
+    if (std::min(a.st.community_capacity, a.ws.score_blocks * CKV_SCORE_BLOCK) > CKV_MAX_COMMUNITIES)
+      return fail(CKV_E_LIMIT, "batched decode scores at most 65536 communities per head");
+    if (a.cfg.assignment == CKV_ASSIGN_NEAREST && a.ws.exchange == nullptr &&
+        std::min(a.st.community_capacity, a.ws.score_blocks * CKV_SCORE_BLOCK) > CKV_MAX_SELECT_ROWS)
+      return fail(CKV_E_LIMIT, "nearest-centroid assignment above 8192 scored communities needs the exchange workspace");
     if (ckv::attention_batch_splits(a) == 0)
       return fail(CKV_E_LIMIT, "batched decode requires group_size * 128 <= 512 and at most 64 attention splits");
     if (i > 0) {
@@ -336,6 +340,7 @@ int validate_batch(const ckv_layer_args* items, int count, std::vector<ckv::Deco
     *max_lds = std::max(*max_lds, ckv::select_lds_bytes(std::min(a.st.community_capacity,
                                                                  a.ws.score_blocks * CKV_SCORE_BLOCK),
                                                         a.ws.descriptor_capacity, a.cfg.max_selected));
+    *max_large_lds = std::max(*max_large_lds, ckv::select_large_lds_bytes(a));
     if (a.st.retrieval_heads != a.st.graph_count) *any_shared = true;
   }
   return CKV_OK;
@@ -352,7 +357,8 @@ extern "C" int ckv_batch_prepare(const ckv_layer_args* items, int32_t count, voi
   int max_nscore;
   size_t max_lds;
   bool any_shared;
-  const int rc = validate_batch(items, count, &packed, &max_nscore, &max_lds, &any_shared);
+  size_t max_large_lds;
+  const int rc = validate_batch(items, count, &packed, &max_nscore, &max_lds, &any_shared, &max_large_lds);
   if (rc) return rc;
   if (!table) return fail(CKV_E_INVALID, "null batch table");
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
@@ -367,7 +373,8 @@ extern "C" int ckv_batch_decode(const ckv_layer_args* items, int32_t count, cons
   int max_nscore;
   size_t max_lds;
   bool any_shared;
-  int rc = validate_batch(items, count, &packed, &max_nscore, &max_lds, &any_shared);
+  size_t max_large_lds;
+  int rc = validate_batch(items, count, &packed, &max_nscore, &max_lds, &any_shared, &max_large_lds);
   if (rc) return rc;
   if (!table) return fail(CKV_E_INVALID, "null batch table");
   const ckv::DecodeArgs* t = reinterpret_cast<const ckv::DecodeArgs*>(table);
@@ -382,11 +389,16 @@ extern "C" int ckv_batch_decode(const ckv_layer_args* items, int32_t count, cons
   // Every fused workgroup repeats its head's selection: worth it only while
   // the copies run side by side, one per compute unit.
   if ((int64_t)count * h.st.retrieval_heads * parts > FUSED_MAX_WORKGROUPS) parts = 0;
+  // above 8,192 scored rows (one workgroup's registers) the whole batch takes
+  // the large selection: scoring on every compute unit, 1,024 threads per head
+  const bool large = max_nscore > CKV_MAX_SELECT_ROWS;
+  if (large) parts = 0;
   int splits = parts;
   if (parts > 0) {
     rc = ckv::launch_batch_select_attend(h, t, count, max_nscore, fused_lds, parts, s);
   } else {
-    rc = ckv::launch_batch_select(h, t, count, max_nscore, max_lds, s);
+    rc = large ? ckv::launch_batch_select_large(h, t, count, max_nscore, max_large_lds, s)
+               : ckv::launch_batch_select(h, t, count, max_nscore, max_lds, s);
     if (!rc) rc = ckv::launch_batch_attention(h, t, count, s, true);
     splits = ckv::attention_batch_splits(h);
   }
@@ -401,7 +413,8 @@ extern "C" int ckv_batch_attention_partials(const ckv_layer_args* items, int32_t
   int max_nscore;
   size_t max_lds;
   bool any_shared;
-  const int rc = validate_batch(items, count, &packed, &max_nscore, &max_lds, &any_shared);
+  size_t max_large_lds;
+  const int rc = validate_batch(items, count, &packed, &max_nscore, &max_lds, &any_shared, &max_large_lds);
   if (rc) return rc;
   if (!table) return fail(CKV_E_INVALID, "null batch table");
   return ckv::launch_batch_attention(packed[0], reinterpret_cast<const ckv::DecodeArgs*>(table), count,

@@ -566,6 +566,9 @@ int launch_score_select(const DecodeArgs& a, hipStream_t stream, const DecodeArg
 // select_large_kernel (ckv_select_large.hip).
 bool large_selection(const DecodeArgs& a);
 int launch_select_large(const DecodeArgs& a, hipStream_t stream, const DecodeArgs* pending = nullptr);
+int launch_batch_select_large(const DecodeArgs& h, const DecodeArgs* table, int count, int max_nscore,
+                              size_t max_lds, hipStream_t stream);
+size_t select_large_lds_bytes(const DecodeArgs& a);
 int launch_sync_shared(const DecodeArgs& a, hipStream_t stream);
 int launch_attention(const DecodeArgs& a, hipStream_t stream, bool partials_only);
 int launch_update(const DecodeArgs& a, hipStream_t stream);

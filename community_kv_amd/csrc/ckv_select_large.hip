@@ -45,23 +45,23 @@ int limit_error(const char* message) { return ckv_internal::set_error(CKV_E_LIMI
 }  // namespace
 
 // Scores (and, in nearest-centroid mode, block minima of the squared distance
-// to the current key: distance bits << 32 | row, into exchange[rh][C + block])
-// of rows [64 * blockIdx.x, +64) of head blockIdx.y.
+// to the current key: distance bits << 32 | row, into exchange[rh][C + blk])
+// of rows [64 * blk, +64) of head rh.
 template <int CT, int DT>
-__global__ __launch_bounds__(SELECT_THREADS) void score_rows_kernel(DecodeArgs a) {
+__device__ __forceinline__ void score_rows_body(const DecodeArgs& a, const int rh, const int blk) {
   __shared__ float q_s[CKV_MAX_GROUP * D];
   __shared__ float key_s[D];
   __shared__ uint64_t near_s[SELECT_THREADS / 64];
-  const int rh = blockIdx.y;
   const int tid = threadIdx.x;
   const int C = a.st.community_capacity;
   const int nscore = min(C, a.ws.score_blocks * SCORE_BLOCK);
+  if (blk * ROWS >= nscore) return;  // (batched grids cover the largest item)
   int count = a.st.community_counts[rh];
   count = count < 0 ? 0 : (count > nscore ? nscore : count);
-  const int r0 = blockIdx.x * ROWS;
+  const int r0 = blk * ROWS;
   const bool nearest_mode = a.cfg.assignment == CKV_ASSIGN_NEAREST;
   if (r0 >= count) {
-    if (nearest_mode && tid == 0) a.ws.exchange[(int64_t)rh * ckv_exchange_words(C) + C + blockIdx.x] = ~0ull;
+    if (nearest_mode && tid == 0) a.ws.exchange[(int64_t)rh * ckv_exchange_words(C) + C + blk] = ~0ull;
     return;
   }
   const int G = a.cfg.group_size;
@@ -115,9 +115,21 @@ __global__ __launch_bounds__(SELECT_THREADS) void score_rows_kernel(DecodeArgs a
     if (tid == 0) {
       uint64_t m = ~0ull;
       for (int w = 0; w < SELECT_THREADS / 64; ++w) m = near_s[w] < m ? near_s[w] : m;
-      a.ws.exchange[(int64_t)rh * ckv_exchange_words(C) + C + blockIdx.x] = m;
+      a.ws.exchange[(int64_t)rh * ckv_exchange_words(C) + C + blk] = m;
     }
   }
+}
+
+template <int CT, int DT>
+__global__ __launch_bounds__(SELECT_THREADS) void score_rows_kernel(DecodeArgs a) {
+  score_rows_body<CT, DT>(a, blockIdx.y, blockIdx.x);
+}
+
+// Batched: head blockIdx.y % heads of item blockIdx.y / heads.
+template <int CT, int DT>
+__global__ __launch_bounds__(SELECT_THREADS) void score_rows_large_batch_kernel(const DecodeArgs* __restrict__ table,
+                                                                                int heads) {
+  score_rows_body<CT, DT>(table[blockIdx.y / heads], blockIdx.y % heads, blockIdx.x);
 }
 
 // LDS of select_large_kernel: seven descriptor arrays and the per-block first
@@ -130,19 +142,13 @@ __host__ __device__ inline size_t large_lds_bytes(int descriptor_capacity, int m
 // another layer `u` (same dtypes), one retrieval head each, on the compute
 // units this launch leaves idle (the selection is one workgroup per head).
 template <int CT, int DT>
-__global__ __launch_bounds__(LT) void select_large_kernel(DecodeArgs a, DecodeArgs u) {
-  if ((int)blockIdx.x >= a.st.retrieval_heads) {
-    const int urh = (int)blockIdx.x - a.st.retrieval_heads;
-    owner_update<CT, DT>(u, urh, u.ws.lse[(int64_t)urh * u.cfg.group_size]);
-    return;
-  }
+__device__ __forceinline__ void select_large_body(const DecodeArgs& a, const int rh) {
   __shared__ __align__(16) int hist[256];
   __shared__ __align__(16) int hist2[256];
   __shared__ int scan_s[4 * LWAVES];
   __shared__ int sink_s[CKV_MAX_SINKS];
   __shared__ int s_max_idx, s_hb, s_above_hb, s_lb, s_last_size, s_last_sel_pos, s_sink_max;
   extern __shared__ __align__(16) int dyn_l[];
-  const int rh = blockIdx.x;
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int C = a.st.community_capacity;
@@ -551,6 +557,25 @@ __global__ __launch_bounds__(LT) void select_large_kernel(DecodeArgs a, DecodeAr
   }
 }
 
+// Workgroups past a.st.retrieval_heads run the pending online update of
+// another layer `u` (same dtypes), one retrieval head each, on the compute
+// units this launch leaves idle (the selection is one workgroup per head).
+template <int CT, int DT>
+__global__ __launch_bounds__(LT) void select_large_kernel(DecodeArgs a, DecodeArgs u) {
+  if ((int)blockIdx.x >= a.st.retrieval_heads) {
+    const int urh = (int)blockIdx.x - a.st.retrieval_heads;
+    owner_update<CT, DT>(u, urh, u.ws.lse[(int64_t)urh * u.cfg.group_size]);
+    return;
+  }
+  select_large_body<CT, DT>(a, blockIdx.x);
+}
+
+// Batched: head blockIdx.x % heads of item blockIdx.x / heads.
+template <int CT, int DT>
+__global__ __launch_bounds__(LT) void select_large_batch_kernel(const DecodeArgs* __restrict__ table, int heads) {
+  select_large_body<CT, DT>(table[blockIdx.x / heads], blockIdx.x % heads);
+}
+
 bool large_selection(const DecodeArgs& a) {
   return std::min(a.st.community_capacity, a.ws.score_blocks * SCORE_BLOCK) > LARGE_MIN_ROWS;
 }
@@ -589,6 +614,37 @@ int launch_select_large(const DecodeArgs& a, hipStream_t s, const DecodeArgs* pe
   if (e4m3) return go(score_rows_kernel<CKV_E4M3, CKV_F32>, select_large_kernel<CKV_E4M3, CKV_F32>);
   if (bf16) return go(score_rows_kernel<CKV_F32, CKV_BF16>, select_large_kernel<CKV_F32, CKV_BF16>);
   return go(score_rows_kernel<CKV_F32, CKV_F32>, select_large_kernel<CKV_F32, CKV_F32>);
+}
+
+// The large selection for every item of a batch (bf16 KV): scoring of every
+// item's rows on all compute units, then one 1,024-thread workgroup per
+// (item, head).  h is the first item (dtypes, heads); max_nscore and max_lds
+// the largest item's scored rows and selection LDS.
+int launch_batch_select_large(const DecodeArgs& h, const DecodeArgs* table, int count, int max_nscore,
+                              size_t max_lds, hipStream_t s) {
+  if (max_nscore > CKV_MAX_COMMUNITIES) return limit_error("more than 65536 scored communities per head");
+  const int heads = h.st.retrieval_heads;
+  const dim3 sg((max_nscore + ROWS - 1) / ROWS, count * heads);
+  auto go = [&](auto score, auto select) {
+    hipLaunchKernelGGL(score, sg, dim3(SELECT_THREADS), 0, s, table, heads);
+    int rc = launch_check("score_rows_large_batch");
+    if (rc) return rc;
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(select),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)max_lds);
+    if (e != hipSuccess) {
+      (void)hipGetLastError();
+      return limit_error("large selection LDS (descriptors x 28 + selected / 16 bytes) exceeds the device limit");
+    }
+    hipLaunchKernelGGL(select, dim3(count * heads), dim3(LT), max_lds, s, table, heads);
+    return launch_check("select_large_batch");
+  };
+  if (h.st.centroid_dtype == CKV_E4M3)
+    return go(score_rows_large_batch_kernel<CKV_E4M3, CKV_BF16>, select_large_batch_kernel<CKV_E4M3, CKV_BF16>);
+  return go(score_rows_large_batch_kernel<CKV_F32, CKV_BF16>, select_large_batch_kernel<CKV_F32, CKV_BF16>);
+}
+
+size_t select_large_lds_bytes(const DecodeArgs& a) {
+  return large_lds_bytes(a.ws.descriptor_capacity, a.cfg.max_selected);
 }
 
 }  // namespace ckv

@@ -439,7 +439,12 @@ int ckv_score_select_after_update(const ckv_layer_args* layer, const ckv_layer_a
  * copies their packed arguments into it, synchronising `stream` (a set-up call:
  * the items' tensors sit at fixed addresses, so one table serves every step).
  * ckv_batch_decode validates the host items again, allocates nothing and does
- * not synchronise; results are identical to ckv_decode_layer on each item. */
+ * not synchronise; results are identical to ckv_decode_layer on each item.
+ * Items may score up to 65536 communities per head; when one item scores more
+ * than 8192 the whole batch takes the multi-kernel selection (scoring on
+ * every compute unit, 1,024 threads per head) and the separate attention, so
+ * an item that alone would take the fused launch gets the same selection and
+ * outputs equal up to the order of the split-partial sums. */
 size_t ckv_batch_table_bytes(int32_t count);
 int ckv_batch_prepare(const ckv_layer_args* items, int32_t count, void* table, void* stream);
 int ckv_batch_decode(const ckv_layer_args* items, int32_t count, const void* table, void* stream);

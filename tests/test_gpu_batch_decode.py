@@ -41,9 +41,20 @@ ITEMS_LARGE = [
 ]
 
 
+# more than 8192 scored rows per head: the batch takes the large selection
+# (scoring on every compute unit, 1,024 threads per (item, head)), as each
+# item's single call does
+ITEMS_HUGE = [
+    dict(seq_len=49152, communities=12000),
+    dict(seq_len=40000, communities=8500),
+    dict(seq_len=32768, communities=9000),
+]
+
+
 @pytest.mark.parametrize("aggregation,assignment,group,items", [
     (co.QUERY_GROUP, "delta_q", 4, ITEMS), (co.QUERY_GROUP, "nearest_centroid", 4, ITEMS),
-    (co.LAYER_WISE, "delta_q", 2, ITEMS), (co.QUERY_GROUP, "delta_q", 4, ITEMS_LARGE)])
+    (co.LAYER_WISE, "delta_q", 2, ITEMS), (co.QUERY_GROUP, "delta_q", 4, ITEMS_LARGE),
+    (co.QUERY_GROUP, "delta_q", 4, ITEMS_HUGE), (co.QUERY_GROUP, "nearest_centroid", 4, ITEMS_HUGE)])
 def test_batch_decode_matches_single_items(device, aggregation, assignment, group, items):
     print(f"batch decode {aggregation} {assignment} communities={[kw['communities'] for kw in items]}", flush=True)
     params = co.StepParams(group_size=group, num_sink=10, token_budget=512, local_window=64, assignment=assignment)
@@ -84,3 +95,32 @@ def test_batch_rejects_mismatched_items(device):
         BatchDecode([a["call"], b["call"]])
     with pytest.raises(RuntimeError, match="must not share"):
         BatchDecode([a["call"], a["call"]])
+
+
+def test_batch_with_one_huge_item_matches_single_selection(device):
+    """A batch mixing an item above 8192 scored communities with small ones:
+    the whole batch takes the large selection and the separate attention,
+    while a small item's single call takes the cooperative fused launch, whose
+    split partials are summed in another order.  Selections (slot tables,
+    descriptors) must be identical; outputs agree within bf16 rounding."""
+    params = co.StepParams(group_size=4, num_sink=10, token_budget=512, local_window=64)
+    items = [dict(seq_len=49152, communities=12000), dict(seq_len=3000, communities=60),
+             dict(seq_len=6000, communities=300)]
+    print("batch decode mixed huge/small", flush=True)
+    fxs = [syn.build_layer(seed=80 + i, query_heads=16, kv_heads=4, num_sink=10, max_decode_tokens=4,
+                           aggregation=co.QUERY_GROUP, **kw) for i, kw in enumerate(items)]
+    single = [_item(fx, params, device) for fx in fxs]
+    batched = [_item(fx, params, device) for fx in fxs]
+    batch = BatchDecode([b["call"] for b in batched])
+    for it in single:
+        it["call"].decode()
+    batch.decode()
+    torch.cuda.synchronize(device)
+    for i, (a, b) in enumerate(zip(single, batched)):
+        sa, sb = a["ws"].selection, b["ws"].selection
+        assert torch.equal(sa.slot_positions, sb.slot_positions), i
+        assert torch.equal(sa.communities, sb.communities), i
+        assert torch.equal(sa.descriptor_counts, sb.descriptor_counts), i
+        oa, ob = a["ws"].attention.output.float(), b["ws"].attention.output.float()
+        assert (oa - ob).abs().max().item() < 2e-2, i
+        assert (a["ws"].attention.lse - b["ws"].attention.lse).abs().max().item() < 1e-4, i
