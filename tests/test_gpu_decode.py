@@ -139,6 +139,7 @@ def test_decode_steps_match_oracle(device, name):
     ws = h.workspace_for(fx, params, device)
     rng = np.random.default_rng(5)
     steps = STEPS.get(name, 12)
+    robust_checks = 0
     for step in range(steps):
         before = fx.state.copy()
         dstate, ws, out, lse, tks, tkp = _run_step(fx, params, device, dstate, ws)
@@ -151,6 +152,11 @@ def test_decode_steps_match_oracle(device, name):
             if int(before.to_graph[r]) == r:
                 h.check_topk(tkp[r].cpu().numpy(), tks[r].cpu().numpy(), _scores0(fx, before, ref, r, params),
                              ref.positions[r], params.num_sink)
+        # update un-forced (the oracle's own top-8 and lse) on the first steps: same assignment where robust
+        if params.assignment != "none" and step < 3:
+            ref_u = co.decode_step(before.copy(), fx.query, fx.keys, fx.values, params)
+            robust_checks += _unforced_checks(before, fx, params, ref_u, tkp,
+                                              ws.update.assigned_communities.cpu().tolist(), f"step {step}")
         # update, teacher-forced with the device's top-8 and lse: bit-exact state
         co.decode_step(fx.state, fx.query, fx.keys, fx.values, params,
                        gpu_topk=(tks.cpu().numpy(), tkp.cpu().numpy()), gpu_lse=lse.cpu().numpy())
@@ -159,6 +165,40 @@ def test_decode_steps_match_oracle(device, name):
         # next query
         fx.query = syn.fresh_query(fx, rng)
         dstate[3].copy_(h.torch_values(fx.query, fx.dtype, device))
+    if params.assignment != "none":
+        assert robust_checks > 0, name
+
+
+def _robust_assignment(before, fx, params, ref_u):
+    """The oracle's un-forced assignment per graph, or None where a 1e-4
+    relative perturbation of its top-8 scores / lse can change it."""
+    base = ref_u.assigned
+    robust = [True] * len(base)
+    rng = np.random.default_rng(0)
+    for trial in range(4):
+        sign = rng.choice([-1.0, 1.0], size=ref_u.topk_scores.shape)
+        sc = (ref_u.topk_scores * (1.0 + 1e-4 * sign)).astype(np.float32)
+        lse = (ref_u.lse * (1.0 + 1e-4 * (1 if trial % 2 else -1))).astype(np.float32)
+        alt = co.decode_step(before.copy(), fx.query, fx.keys, fx.values, params,
+                             gpu_topk=(sc, ref_u.topk_positions), gpu_lse=lse)
+        for g in range(len(base)):
+            robust[g] &= int(alt.assigned[g]) == int(base[g])
+    return [int(a) if ok else None for a, ok in zip(base, robust)]
+
+
+def _unforced_checks(before, fx, params, ref_u, tkp, gpu_assigned, case):
+    """The device's assignment of each graph against the oracle run on its own
+    float64 top-8 and lse (no teacher forcing), wherever that assignment is
+    robust (same top-8 set, unchanged by a 1e-4 perturbation).  Returns the
+    number of graphs checked."""
+    expect = _robust_assignment(before, fx, params, ref_u)
+    checked = 0
+    for g, a in enumerate(expect):
+        same_set = set(tkp[g].cpu().tolist()) == set(ref_u.topk_positions[g].tolist())
+        if a is not None and same_set:
+            assert gpu_assigned[g] == a, f"{case} graph {g}: device assigned {gpu_assigned[g]}, oracle {a}"
+            checked += 1
+    return checked
 
 
 def _scores0(fx, st, ref, r, params):

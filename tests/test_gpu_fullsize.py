@@ -26,26 +26,9 @@ import torch
 from oracle import ckv_oracle as co
 from oracle import synthetic as syn
 from tests import _helpers as h
-from tests.test_gpu_decode import _check_attention, _check_selection, _run_step, _scores0
+from tests.test_gpu_decode import _check_attention, _check_selection, _run_step, _scores0, _unforced_checks
 
 pytestmark = pytest.mark.gpu
-
-
-def _robust_assignment(before, fx, params, ref_u):
-    """The oracle's un-forced assignment per graph, or None where a 1e-4
-    relative perturbation of its top-8 scores / lse can change it."""
-    base = ref_u.assigned
-    robust = [True] * len(base)
-    rng = np.random.default_rng(0)
-    for trial in range(4):
-        sign = rng.choice([-1.0, 1.0], size=ref_u.topk_scores.shape)
-        sc = (ref_u.topk_scores * (1.0 + 1e-4 * sign)).astype(np.float32)
-        lse = (ref_u.lse * (1.0 + 1e-4 * (1 if trial % 2 else -1))).astype(np.float32)
-        alt = co.decode_step(before.copy(), fx.query, fx.keys, fx.values, params,
-                             gpu_topk=(sc, ref_u.topk_positions), gpu_lse=lse)
-        for g in range(len(base)):
-            robust[g] &= int(alt.assigned[g]) == int(base[g])
-    return [int(a) if ok else None for a, ok in zip(base, robust)]
 
 
 def test_config2_full_size(device):
@@ -70,12 +53,7 @@ def test_config2_full_size(device):
             h.check_topk(tkp[r].cpu().numpy(), tks[r].cpu().numpy(), _scores0(fx, before, ref_u, r, params),
                          ref_u.positions[r], params.num_sink)
         # un-forced: the oracle's own float64 top-8 and lse
-        expect = _robust_assignment(before, fx, params, ref_u)
-        for g, a in enumerate(expect):
-            same_set = set(tkp[g].cpu().tolist()) == set(ref_u.topk_positions[g].tolist())
-            if a is not None and same_set:
-                assert gpu_assigned[g] == a, f"step {step} graph {g}: device assigned {gpu_assigned[g]}, oracle {a}"
-                robust_checks += 1
+        robust_checks += _unforced_checks(before, fx, params, ref_u, tkp, gpu_assigned, f"step {step}")
         # teacher-forced update: bit-exact state
         co.decode_step(fx.state, fx.query, fx.keys, fx.values, params,
                        gpu_topk=(tks.cpu().numpy(), tkp.cpu().numpy()), gpu_lse=lse.cpu().numpy())
@@ -135,6 +113,7 @@ def test_config4_batched_full_size(device):
         items.append(dict(state=state, cur=cur, q=q, ws=ws, call=call, initial=h.state_to_numpy(state, cur, True)))
     batch = BatchDecode([it["call"] for it in items])
     qrng = np.random.default_rng(8)
+    robust_checks = 0
     for step in range(steps):
         befores = [fx.state.copy() for fx in fxs] if step < 2 else None
         batch.decode()
@@ -147,6 +126,10 @@ def test_config4_batched_full_size(device):
                                      co.StepParams(**{**params.__dict__, "assignment": "none"}))
                 _check_selection(before, params, it["ws"], ref)
                 _check_attention(fx, params, att.output, att.lse, ref, fx.dtype)
+                ref_u = co.decode_step(before.copy(), fx.query, fx.keys, fx.values, params)
+                robust_checks += _unforced_checks(before, fx, params, ref_u, att.topk_positions,
+                                                  it["ws"].update.assigned_communities.cpu().tolist(),
+                                                  f"step {step} item {i}")
                 co.decode_step(fx.state, fx.query, fx.keys, fx.values, params,
                                gpu_topk=(att.topk_scores.cpu().numpy(), att.topk_positions.cpu().numpy()),
                                gpu_lse=att.lse.cpu().numpy())
@@ -156,6 +139,7 @@ def test_config4_batched_full_size(device):
             it["q"].copy_(h.torch_values(fx.query, fx.dtype, device))
         if step % 16 == 15:
             print(f"config 4 step {step}", flush=True)
+    assert robust_checks >= 64, robust_checks  # 8 items x 8 graphs x 2 steps, near-ties aside
     for i, it in enumerate(items):
         assert it["ws"].update.overflow.cpu().tolist() == [0] * 8, i
         assert torch.isfinite(it["ws"].attention.output.float()).all(), i
