@@ -810,6 +810,74 @@ def run_paper(args, device):
     print(json.dumps(result), flush=True)
 
 
+
+def run_floor(args, device):
+    """Latency probes behind the decode step's cost model: the launch floor of
+    a graph-replayed kernel (empty kernels of the cooperative launch's shape),
+    the dependent-load round trip at three working-set sizes (L2-, Infinity
+    Cache- and HBM-resident random cycles), an agent-scope atomic round trip
+    and a workgroup-to-workgroup hand-off.  One JSON line; the model that
+    adds them up is written out in the design notes."""
+    import ctypes
+
+    from community_kv_amd import _native as nat
+
+    lib = nat.lib()
+    out = torch.zeros(2, dtype=torch.int64, device=device)
+    stream = lambda: ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+    def empty_us(blocks, threads, lds, n=36):
+        def body():
+            for _ in range(n):
+                nat.check(lib.ckv_latency_probe(0, None, 0, 0, blocks, threads, lds, None, stream()))
+        g = capture(body, device)
+        g.replay()
+        torch.cuda.synchronize(device)
+        return time_graph(g, 50, device) * 1e3 / n
+
+    clock = {}
+
+    def ticks(kind, buf, nbytes, hops):
+        """ns per hop from the host's event timing of the one-thread kernel
+        (hops long enough that the launch is noise), and the device wall
+        clock's tick rate from the same run."""
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        t0.record()
+        nat.check(lib.ckv_latency_probe(kind, ctypes.c_void_p(buf.data_ptr()), nbytes, hops, 0, 0, 0,
+                                        ctypes.c_void_p(out.data_ptr()), stream()))
+        t1.record()
+        torch.cuda.synchronize(device)
+        ms = t0.elapsed_time(t1)
+        clock.setdefault("mhz", []).append(int(out[0].item()) / (ms * 1e3))
+        return ms * 1e6 / hops
+
+    def chase_ns(nbytes, agent, hops=4000):
+        stride = 256  # uint32 entries (1 KiB) between nodes: every hop a new line
+        nodes = max(2, nbytes // (4 * stride))
+        buf = torch.zeros(nodes * stride, dtype=torch.int32, device=device)
+        order = torch.cat([torch.zeros(1, dtype=torch.int64, device=device),
+                           1 + torch.randperm(nodes - 1, device=device, dtype=torch.int64)])  # node 0 first
+        idx = order * stride
+        buf[idx] = torch.roll(idx, -1).to(torch.int32)  # one cycle through every node
+        ticks(2 if agent else 1, buf, nbytes, 200)  # warm-up pass
+        return ticks(2 if agent else 1, buf, nbytes, hops)
+
+    word = torch.zeros(64, dtype=torch.int32, device=device)
+    res = {"metric": "decode_latency_floor_components", "unit": "ns (us where named)", "n_gpus": 1,
+           "data": "synthetic probes", "config": {"workload": "latency probes for the decode-step cost model"}}
+    res["empty_launch_us_1x64"] = empty_us(1, 64, 0)
+    res["empty_launch_us_144x512"] = empty_us(144, 512, 0)
+    res["empty_launch_us_144x512_lds130k"] = empty_us(144, 512, 130 * 1024)
+    for name, nbytes in (("l2_1MiB", 1 << 20), ("mall_64MiB", 64 << 20), ("hbm_4GiB", 4 << 30)):
+        res[f"chase_plain_ns_{name}"] = chase_ns(nbytes, False)
+        res[f"chase_agent_ns_{name}"] = chase_ns(nbytes, True)
+    res["atomic_agent_rtt_ns"] = ticks(3, word, 256, 4000)
+    word.zero_()
+    res["handoff_agent_ns"] = ticks(4, word, 256, 2000)
+    res["wall_clock_mhz_implied"] = float(np.median(clock["mhz"]))
+    print(json.dumps(res), flush=True)
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -824,7 +892,7 @@ def main():
                     help="generate: partition every prompt layer with the native Leiden instead of synthetic labels")
     ap.add_argument("--partition-inline", action="store_true",
                     help="generate --leiden: partition each layer inline instead of on the overlapping worker")
-    ap.add_argument("--workload", choices=["decode", "prefill", "generate", "batched", "state", "partition", "paper"],
+    ap.add_argument("--workload", choices=["decode", "prefill", "generate", "batched", "state", "partition", "paper", "floor"],
                     default="decode",
                     help="decode: the 36-layer sparse decode step (default); prefill: config-5 edge export; "
                          "generate: config-3 model decode loop; batched: config-4 ragged batch; "
@@ -856,6 +924,9 @@ def main():
         return
     if args.workload == "paper":
         run_paper(args, device)
+        return
+    if args.workload == "floor":
+        run_floor(args, device)
         return
     max_decode = args.warmup + args.steps + max(5, args.steps // 2) + 17  # every full step appends one token
     runtime, stack = build_stack(device, args.layers, max_decode, query_sets=QUERY_SETS)

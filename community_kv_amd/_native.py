@@ -89,6 +89,7 @@ EXPORTED_SYMBOLS = (
     "ckv_build_adjacency",
     "ckv_host_numerics",
     "ckv_device_numerics",
+    "ckv_latency_probe",
     "ckv_abi_version",
     "ckv_last_error",
 )
@@ -284,6 +285,8 @@ def lib() -> ctypes.CDLL:
     handle.ckv_host_numerics.restype = ctypes.c_int
     handle.ckv_device_numerics.argtypes = [ctypes.c_int, _p, _p, _i64, _p]
     handle.ckv_device_numerics.restype = ctypes.c_int
+    handle.ckv_latency_probe.argtypes = [_i32, _p, _i64, _i32, _i32, _i32, _i32, _p, _p]
+    handle.ckv_latency_probe.restype = ctypes.c_int
     handle.ckv_last_error.restype = ctypes.c_char_p
     handle.ckv_abi_version.restype = ctypes.c_int
     if handle.ckv_abi_version() != ABI_VERSION:

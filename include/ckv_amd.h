@@ -506,6 +506,18 @@ int ckv_dense_decode(const ckv_kv_cache* kv, int32_t seq_len, float softmax_scal
                      float* partial_max, float* partial_sum, float* partial_acc,
                      void* output, float* lse, void* stream);
 
+/* Diagnostic, no counterpart in the reference: latency probes behind the
+ * decode step's measured cost model (bench.py --workload floor).  kind 0: one
+ * empty kernel of blocks x threads with lds_bytes of dynamic LDS (the host
+ * times graphs of them); 1 / 2: `hops` dependent plain / agent-scope loads
+ * through the uint32 index cycle in `buffer` (`bytes` long, caller-written);
+ * 3: `hops` dependent agent-scope fetch-and-adds on buffer[0]; 4: `hops`
+ * hand-offs between two workgroups through buffer[0] (zeroed by the caller,
+ * bounded polling).  Kinds 1-4 write the elapsed 100 MHz wall-clock ticks to
+ * out[0] (two device uint64). */
+int ckv_latency_probe(int32_t kind, void* buffer, int64_t bytes, int32_t hops, int32_t blocks, int32_t threads,
+                      int32_t lds_bytes, uint64_t* out, void* stream);
+
 /* Diagnostic, no counterpart in the reference: evaluates the library's scalar
  * numerics on the host over n inputs, for parity tests without a GPU.
  * op 0 exp -> f32, 1 log -> f32, 2 fp16 bits -> u16, 3 bf16 bits -> u16,
