@@ -99,18 +99,24 @@ __device__ __forceinline__ void coop_finish(const DecodeArgs& a, const int rh, c
 #if CKV_HANDOFF_FENCES
   // Every wave's partial stores (agent-scope, written through) complete
   // before the barrier; the barrier orders them before thread 0's agent-scope
-  // release increment (HRF-indirect: workgroup synchronisation, then agent
-  // synchronisation), and the part that reads parts - 1 acquires through the
-  // same acq_rel increment before the barrier that releases its other threads
-  // to load the partials.  Release/acquire in the language's terms, valid
-  // whichever XCDs the parts run on.  (Measured at config 2: 17.04 against
-  // 16.53 us per layer-step with a relaxed increment; an agent-scope release
-  // fence in every thread instead, which writes back the XCD's L2 once per
-  // wave, took 25.5 us.)
+  // release increment (workgroup synchronisation, then agent
+  // synchronisation).  Increments continue the counter's release sequence, so
+  // the part that reads parts - 1 acquires every other part's stores with an
+  // agent-scope acquire fence, before the barrier that lets its threads load
+  // the partials.  Release/acquire in the language's terms, valid whichever
+  // XCDs the parts run on.  (Measured at config 2: 16.70 against 16.58 us per
+  // layer-step with a relaxed increment; an acq_rel increment in every part,
+  // whose acquire invalidates the XCD's L2 once per part, 17.09 us; an
+  // agent-scope release fence in every thread, one L2 write-back per wave,
+  // 25.5 us.)
   wait_vm();
   __syncthreads();
-  if (tid == 0)
-    s_last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(parts - 1);
+  if (tid == 0) {
+    const bool last =
+        __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(parts - 1);
+    if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    s_last = last;
+  }
   __syncthreads();
   if (!s_last) return;
 #else
