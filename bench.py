@@ -707,7 +707,7 @@ def side_configs(args, device):
     import types
 
     out = {}
-    pre = run_prefill(types.SimpleNamespace(prefill_seq=PREFILL_SEQ, warmup=1, steps=5, no_cpu=True), device,
+    pre = run_prefill(types.SimpleNamespace(prefill_seq=PREFILL_SEQ, warmup=3, steps=5, no_cpu=True), device,
                       emit=False)
     out["prefill_ms"] = pre["value"]
     out["prefill_tflops"] = pre["roofline"]["achieved"]
@@ -720,7 +720,7 @@ def side_configs(args, device):
     out["batched_hbm_frac"] = bat["roofline"]["frac"]
     out["batched_step_hbm_frac"] = bat["step_hbm_frac"]
     out["side_configs"] = ("prefill_*: BASELINE config 5 (32,768-token causal prefill, 32/8 heads, top-16 edges), "
-                           "mean of 5 launches after 1 warm-up, MFMA roofline = 4*128*32*S(S+1)/2 FLOP / time / "
+                           "mean of 5 launches after 3 warm-up launches (the clock ramps over the first), MFMA roofline = 4*128*32*S(S+1)/2 FLOP / time / "
                            "2.5 PFLOP/s; batched_*: BASELINE config 4 (8 ragged sequences), mean of 20 graph-replayed "
                            "steps after 3, batched_hbm_frac = the batched attention kernel's algorithmic bytes / its "
                            "time / 8 TB/s, batched_step_hbm_frac = the whole step's algorithmic bytes / step time")
