@@ -541,7 +541,7 @@ def qwen3_8b_config(layers):
                        rope_theta=1e6, rms_norm_eps=1e-6, tie_word_embeddings=False)
 
 
-def run_generate(args, device):
+def run_generate(args, device, emit=True):
     """random-init Qwen3-8B-architecture model, synthetic
     prompt, greedy decode through CommunityKVRuntime.generate with
     nearest-centroid assignment.  Decode throughput = (steps) / (wall time of a
@@ -615,7 +615,9 @@ def run_generate(args, device):
         "prefill_plus_first_token_s": t_prefill,
         "generated_tokens": int(out.shape[-1] - prompt_len),
     }
-    print(json.dumps(result), flush=True)
+    if emit:
+        print(json.dumps(result), flush=True)
+    return result
 
 
 BATCH = 8
@@ -719,11 +721,20 @@ def side_configs(args, device):
     out["batched_attention_kernel_us"] = bat["attention_partials_kernel_us"]
     out["batched_hbm_frac"] = bat["roofline"]["frac"]
     out["batched_step_hbm_frac"] = bat["step_hbm_frac"]
+    torch.cuda.empty_cache()
+    gen = run_generate(types.SimpleNamespace(gen_layers=GEN_LAYERS, gen_prompt=GEN_PROMPT, gen_steps=GEN_STEPS,
+                                             warmup=10, leiden=False, partition_inline=False, no_cpu=True),
+                       device, emit=False)
+    out["generate_tokens_per_s"] = gen["value"]
+    out["generate_ms_per_token"] = gen["ms_per_step"]
+    out["generate_prefill_plus_first_token_s"] = gen["prefill_plus_first_token_s"]
     out["side_configs"] = ("prefill_*: BASELINE config 5 (32,768-token causal prefill, 32/8 heads, top-16 edges), "
                            "mean of 5 launches after 3 warm-up launches (the clock ramps over the first), MFMA roofline = 4*128*32*S(S+1)/2 FLOP / time / "
                            "2.5 PFLOP/s; batched_*: BASELINE config 4 (8 ragged sequences), mean of 20 graph-replayed "
                            "steps after 3, batched_hbm_frac = the batched attention kernel's algorithmic bytes / its "
-                           "time / 8 TB/s, batched_step_hbm_frac = the whole step's algorithmic bytes / step time")
+                           "time / 8 TB/s, batched_step_hbm_frac = the whole step's algorithmic bytes / step time; generate_*: "
+                           "BASELINE config 3 (random-init Qwen3-8B, 65,536-token prompt, 128 greedy steps through "
+                           "CommunityKVRuntime.generate, the whole step replayed from one HIP graph)")
     return out
 
 
