@@ -39,9 +39,6 @@
 #include "ckv_update.h"
 #include "ckv_score.h"
 
-#ifndef CKV_HANDOFF_FENCES
-#define CKV_HANDOFF_FENCES 1
-#endif
 #ifndef CKV_R2_LATE
 #define CKV_R2_LATE 0
 #endif
@@ -96,7 +93,6 @@ __device__ __forceinline__ void coop_finish(const DecodeArgs& a, const int rh, c
   const int wave = tid >> 6;
   uint32_t* counter = a.ws.block_counters + rh;
   CKV_STAMP_MAX(rh == 0, 29);
-#if CKV_HANDOFF_FENCES
   // Every wave's partial stores (agent-scope, written through) complete
   // before the barrier; the barrier orders them before thread 0's agent-scope
   // release increment (workgroup synchronisation, then agent
@@ -119,14 +115,6 @@ __device__ __forceinline__ void coop_finish(const DecodeArgs& a, const int rh, c
   }
   __syncthreads();
   if (!s_last) return;
-#else
-  wait_vm();
-  __syncthreads();  // every store of the part has completed
-  if (tid == 0)
-    s_last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(parts - 1);
-  __syncthreads();
-  if (!s_last) return;
-#endif
   CKV_STAMP(rh == 0, 24);
   const int G = a.cfg.group_size;
   const int C = a.st.community_capacity;
