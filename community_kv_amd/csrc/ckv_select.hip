@@ -64,6 +64,13 @@ constexpr int COOP_POLLS = 64;
 constexpr int COOP_PRE = 2;  // passes of the cooperative scoring share loaded with the first round
 constexpr int COOP_SCORE_WAVES = 6;  // waves that score and poll; the others walk the graph-indexed chain
 constexpr int COOP_MAX_PARTS = 64;
+// Prescored batched selection: workgroups per (item, head) at most, and the
+// compute units one round of them should fill (MI355X: 256).
+#ifndef CKV_PRESELECT_MAX_PARTS
+#define CKV_PRESELECT_MAX_PARTS 4
+#endif
+constexpr int PRESELECT_MAX_PARTS = CKV_PRESELECT_MAX_PARTS;
+constexpr int64_t CKV_DEVICE_CUS = 256;
 constexpr int COOP_WAVES = SELECT_THREADS / 64;
 // Exchange row layout after the C tagged scores: the nearest-centroid minima
 // (part * COOP_WAVES + wave), then COOP_MAX_PARTS * COOP_WAVES reserved words.
@@ -1303,14 +1310,17 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
         // (coalesced gathers): a lane's descriptor is the block's first descriptor
         // plus the number of descriptor ends at or before it, read off a wave-wide
         // bit mask of the ends that fall inside the block (no search chains).
+        // (parts > 1: this workgroup resolves the blocks b with b % parts == part;
+        // every part ran the same selection)
         const int nblk_sel = (sel_count + 63) / 64;
-        for (int b0 = wave; b0 < nblk_sel; b0 += WAVES * MAT_BATCH) {
+        const int nblk_own = nblk_sel > part ? (nblk_sel - part + parts - 1) / parts : 0;
+        for (int b0 = wave; b0 < nblk_own; b0 += WAVES * MAT_BATCH) {
           const int32_t* src[MAT_BATCH];
           bool gathered[MAT_BATCH];
           int slow_d[MAT_BATCH], slow_rem[MAT_BATCH];
   #pragma unroll
           for (int q = 0; q < MAT_BATCH; ++q) {
-            const int b = b0 + q * WAVES;
+            const int b = part + parts * (b0 + q * WAVES);
             src[q] = a.st.community_counts + rh;  // in-bounds dummy address when nothing is gathered
             gathered[q] = false;
             slow_d[q] = -1;
@@ -1341,24 +1351,28 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
           }
   #pragma unroll
           for (int q = 0; q < MAT_BATCH; ++q) {
-            const int j = 64 * (b0 + q * WAVES) + lane;
+            const int j = 64 * (part + parts * (b0 + q * WAVES)) + lane;
             if (j < sel_count) {
               slots[ns + j] = val[q];
               if (j == sel_count - 1) s_last_sel_pos = val[q];
             }
           }
         }
-        if (tid < ns) slots[tid] = sink_s[tid];
+        if (tid < ns && part == 0) slots[tid] = sink_s[tid];
         __syncthreads();  // s_last_sel_pos
         CKV_TS(4);
-        const int last_pos = s_last_sel_pos;
+        // the window, the current token and the padding: the part that resolved
+        // the selection's last block (it knows the oldest attended member)
+        if (part == (nblk_sel > 0 ? (nblk_sel - 1) % parts : 0)) {
+          const int last_pos = s_last_sel_pos;
   #pragma unroll
-        for (int h = 0; h < WIN_PER_THREAD; ++h) {
-          const int i = tid + h * SELECT_THREADS;
-          if (i < W) slots[wbeg + i] = window_pos(i, wcomm[h], last_pos);
+          for (int h = 0; h < WIN_PER_THREAD; ++h) {
+            const int i = tid + h * SELECT_THREADS;
+            if (i < W) slots[wbeg + i] = window_pos(i, wcomm[h], last_pos);
+          }
+          if (inc && tid == 0) slots[wbeg + W] = cur;
+          for (int s = wbeg + W + inc + tid; s < slot_cap; s += SELECT_THREADS) slots[s] = -1;
         }
-        if (inc && tid == 0) slots[wbeg + W] = cur;
-        for (int s = wbeg + W + inc + tid; s < slot_cap; s += SELECT_THREADS) slots[s] = -1;
       }
     }
     // ---- outputs that nothing in this kernel reads back --------------------------
@@ -1367,7 +1381,7 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
     // past the selection arrays, so the tile waves start attending at once)
     CKV_TS(11);
     {
-      const int wp = 0, wn = 1;
+      const int wp = part, wn = parts;
       const int ot = tid;
       const int stride = SELECT_THREADS;
       if (ot == 0 && wp == 0) {
@@ -1507,9 +1521,13 @@ __global__ __launch_bounds__(SELECT_THREADS) void score_rows_batch_kernel(const 
 }
 
 template <int CT, int DT, int OWN>
+// `parts` workgroups per (item, head) each run the selection and resolve a
+// strided share of the slot table's 64-slot blocks (and of the other outputs).
 __global__ __launch_bounds__(SELECT_THREADS) void select_prescored_batch_kernel(const DecodeArgs* __restrict__ table,
-                                                                               int heads) {
-  select_body<CT, DT, OWN, false, true>(table[blockIdx.x / heads], blockIdx.x % heads);
+                                                                               int heads, int parts) {
+  const int per_item = heads * parts;
+  const int r = blockIdx.x % per_item;
+  select_body<CT, DT, OWN, false, true>(table[blockIdx.x / per_item], r % heads, r / heads, parts);
 }
 
 // Batched selection: workgroup w serves item w / heads, head w % heads of the
@@ -1711,7 +1729,7 @@ int launch_batch_select(const DecodeArgs& h, const DecodeArgs* table, int count,
     const int rc = launch_check("score_rows_batch");
     if (rc) return rc;
   }
-  auto launch = [&](auto kernel) {
+  auto set_lds = [&](auto kernel) {
     if (max_lds > 48 * 1024) {
       const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)max_lds);
@@ -1720,18 +1738,34 @@ int launch_batch_select(const DecodeArgs& h, const DecodeArgs* table, int count,
         return limit_error("batched selection LDS exceeds the device limit");
       }
     }
+    return 0;
+  };
+  auto launch = [&](auto kernel) {
+    if (const int rc = set_lds(kernel)) return rc;
     hipLaunchKernelGGL(kernel, dim3(count * h.st.retrieval_heads), dim3(SELECT_THREADS), max_lds, s, table,
                        h.st.retrieval_heads);
     return launch_check("select_batch");
   };
+  // The prescored selection leaves most compute units idle (one workgroup per
+  // (item, head)) while its slot resolution is instruction-bound: `parts`
+  // workgroups per (item, head) repeat the selection side by side and split
+  // the slot blocks, as many as one round of workgroups on the device holds.
+  const int pre_parts = (int)std::max<int64_t>(1, std::min<int64_t>(PRESELECT_MAX_PARTS,
+                                                   CKV_DEVICE_CUS / ((int64_t)count * h.st.retrieval_heads)));
+  auto launch_pre = [&](auto kernel) {
+    if (const int rc = set_lds(kernel)) return rc;
+    hipLaunchKernelGGL(kernel, dim3(count * h.st.retrieval_heads * pre_parts), dim3(SELECT_THREADS), max_lds, s,
+                       table, h.st.retrieval_heads, pre_parts);
+    return launch_check("select_prescored_batch");
+  };
   constexpr int OWN_MAX = CKV_MAX_SELECT_ROWS / SELECT_THREADS;
   if (pre) {
     if (h.st.centroid_dtype == CKV_E4M3) {
-      return own <= 4 ? launch(select_prescored_batch_kernel<CKV_E4M3, CKV_BF16, 4>)
-                      : launch(select_prescored_batch_kernel<CKV_E4M3, CKV_BF16, OWN_MAX>);
+      return own <= 4 ? launch_pre(select_prescored_batch_kernel<CKV_E4M3, CKV_BF16, 4>)
+                      : launch_pre(select_prescored_batch_kernel<CKV_E4M3, CKV_BF16, OWN_MAX>);
     }
-    return own <= 4 ? launch(select_prescored_batch_kernel<CKV_F32, CKV_BF16, 4>)
-                    : launch(select_prescored_batch_kernel<CKV_F32, CKV_BF16, OWN_MAX>);
+    return own <= 4 ? launch_pre(select_prescored_batch_kernel<CKV_F32, CKV_BF16, 4>)
+                    : launch_pre(select_prescored_batch_kernel<CKV_F32, CKV_BF16, OWN_MAX>);
   }
   if (h.st.centroid_dtype == CKV_E4M3) {
     return own <= 1 ? launch(select_batch_kernel<CKV_E4M3, CKV_BF16, 1>)
