@@ -39,6 +39,11 @@ constexpr int LARGE_MIN_ROWS = 1024;
 constexpr int LT = 1024;                  // select_large_kernel threads
 constexpr int LWAVES = LT / 64;
 constexpr int MAT_BATCH_L = 4;            // 64-slot blocks per wave gathered together
+#ifndef CKV_LARGE_MAX_PARTS
+#define CKV_LARGE_MAX_PARTS 4
+#endif
+constexpr int LARGE_MAX_PARTS = CKV_LARGE_MAX_PARTS;  // selection workgroups per head at most
+constexpr int DEVICE_CUS = 256;                       // compute units one round of workgroups fills
 
 int limit_error(const char* message) { return ckv_internal::set_error(CKV_E_LIMIT, message); }
 
@@ -142,7 +147,11 @@ __host__ __device__ inline size_t large_lds_bytes(int descriptor_capacity, int m
 // another layer `u` (same dtypes), one retrieval head each, on the compute
 // units this launch leaves idle (the selection is one workgroup per head).
 template <int CT, int DT>
-__device__ __forceinline__ void select_large_body(const DecodeArgs& a, const int rh) {
+// parts > 1: this workgroup (part `part` of the head's `parts`) repeats the
+// selection and resolves every parts-th 64-slot block of the slot table and a
+// strided share of the other outputs.
+__device__ __forceinline__ void select_large_body(const DecodeArgs& a, const int rh, const int part = 0,
+                                                  const int parts = 1) {
   __shared__ __align__(16) int hist[256];
   __shared__ __align__(16) int hist2[256];
   __shared__ int scan_s[4 * LWAVES];
@@ -399,13 +408,14 @@ __device__ __forceinline__ void select_large_body(const DecodeArgs& a, const int
     const int32_t* members = a.csr.member_positions + (int64_t)graph * a.csr.member_stride;
     const int32_t* dpos = a.dl.positions + (int64_t)graph * a.dl.position_capacity;
     const int nblk_sel = (sel_count + 63) / 64;
-    for (int b0 = wave; b0 < nblk_sel; b0 += LWAVES * MAT_BATCH_L) {
+    const int nblk_own = nblk_sel > part ? (nblk_sel - part + parts - 1) / parts : 0;
+    for (int b0 = wave; b0 < nblk_own; b0 += LWAVES * MAT_BATCH_L) {
       const int32_t* src[MAT_BATCH_L];
       bool gathered[MAT_BATCH_L];
       int slow_d[MAT_BATCH_L], slow_rem[MAT_BATCH_L];
 #pragma unroll
       for (int q = 0; q < MAT_BATCH_L; ++q) {
-        const int b = b0 + q * LWAVES;
+        const int b = part + parts * (b0 + q * LWAVES);
         src[q] = a.st.community_counts + rh;  // in-bounds dummy address when nothing is gathered
         gathered[q] = false;
         slow_d[q] = -1;
@@ -468,15 +478,17 @@ __device__ __forceinline__ void select_large_body(const DecodeArgs& a, const int
             }
           }
         }
-        const int j = 64 * (b0 + q * LWAVES) + lane;
+        const int j = 64 * (part + parts * (b0 + q * LWAVES)) + lane;
         if (j < sel_count) {
           slots[ns + j] = val[q];
           if (j == sel_count - 1) s_last_sel_pos = val[q];
         }
       }
     }
-    if (tid < ns) slots[tid] = sink_s[tid];
+    if (tid < ns && part == 0) slots[tid] = sink_s[tid];
     __syncthreads();  // s_last_sel_pos
+    // the window, the current token and the padding: the part that resolved the last block
+    const bool tail_part = part == (nblk_sel > 0 ? (nblk_sel - 1) % parts : 0);
     // Window slot i (position cur - W + i), or -1 when that token is already
     // attended: a sink, or a member of a selected community at or after the
     // selection's oldest attended position.  Selected communities are two
@@ -499,7 +511,7 @@ __device__ __forceinline__ void select_large_body(const DecodeArgs& a, const int
     };
     const int last_pos = s_last_sel_pos;
     const int32_t* tcomm = a.st.token_communities + (int64_t)graph * a.st.token_capacity;
-    for (int i = tid; i < W; i += LT) {
+    for (int i = tail_part ? tid : W; i < W; i += LT) {
       const int p = cur - W + i;
       int pos = p < 0 ? -1 : p;
       if (pos >= 0 && p <= s_sink_max) {
@@ -520,19 +532,22 @@ __device__ __forceinline__ void select_large_body(const DecodeArgs& a, const int
       }
       slots[wbeg + i] = pos;
     }
-    if (inc && tid == 0) slots[wbeg + W] = cur;
-    for (int s = wbeg + W + inc + tid; s < slot_cap; s += LT) slots[s] = -1;
+    if (tail_part) {
+      if (inc && tid == 0) slots[wbeg + W] = cur;
+      for (int s = wbeg + W + inc + tid; s < slot_cap; s += LT) slots[s] = -1;
+    }
   }
-  // ---- the other selection outputs ----------------------------------------------
-  if (tid == 0) {
+  // ---- the other selection outputs (strided over the parts) ------------------------
+  if (tid == 0 && part == 0) {
     a.ws.descriptor_counts[rh] = n_desc;
     a.ws.selected_counts[rh] = sel_count;
   }
-  for (int i = tid; i < n_desc; i += LT) {
+  const int pt = part + parts * tid, pstride = parts * LT;
+  for (int i = pt; i < n_desc; i += pstride) {
     a.ws.communities[(int64_t)rh * dcap + i] = desc_comm[i];
     a.ws.cumulative_ends[(int64_t)rh * dcap + i] = desc_end[i];
   }
-  for (int t = tid; t < a.ws.budget_tiles; t += LT) {
+  for (int t = pt; t < a.ws.budget_tiles; t += pstride) {
     // first descriptor ending after the tile's first selected slot
     const int off = max(t * TILE - ns, 0);
     int lo = n_desc - 1;
@@ -546,8 +561,8 @@ __device__ __forceinline__ void select_large_body(const DecodeArgs& a, const int
     }
     a.ws.tile_descriptors[(int64_t)rh * a.ws.budget_tiles + t] = max(0, min(lo, n_desc - 1));
   }
-  for (int c = count + tid; c < nscore; c += LT) a.ws.scores[(int64_t)rh * C + c] = (uint16_t)0xfc00u;
-  if (nearest_mode && wave == 0) {
+  for (int c = count + pt; c < nscore; c += pstride) a.ws.scores[(int64_t)rh * C + c] = (uint16_t)0xfc00u;
+  if (nearest_mode && wave == 0 && part == 0) {
     const uint64_t* bm = a.ws.exchange + (int64_t)rh * ckv_exchange_words(C) + C;
     const int nb = (count + ROWS - 1) / ROWS;
     uint64_t m = ~0ull;
@@ -561,19 +576,23 @@ __device__ __forceinline__ void select_large_body(const DecodeArgs& a, const int
 // another layer `u` (same dtypes), one retrieval head each, on the compute
 // units this launch leaves idle (the selection is one workgroup per head).
 template <int CT, int DT>
-__global__ __launch_bounds__(LT) void select_large_kernel(DecodeArgs a, DecodeArgs u) {
-  if ((int)blockIdx.x >= a.st.retrieval_heads) {
-    const int urh = (int)blockIdx.x - a.st.retrieval_heads;
+__global__ __launch_bounds__(LT) void select_large_kernel(DecodeArgs a, DecodeArgs u, int parts) {
+  const int nsel = a.st.retrieval_heads * parts;
+  if ((int)blockIdx.x >= nsel) {
+    const int urh = (int)blockIdx.x - nsel;
     owner_update<CT, DT>(u, urh, u.ws.lse[(int64_t)urh * u.cfg.group_size]);
     return;
   }
-  select_large_body<CT, DT>(a, blockIdx.x);
+  select_large_body<CT, DT>(a, blockIdx.x % a.st.retrieval_heads, blockIdx.x / a.st.retrieval_heads, parts);
 }
 
 // Batched: head blockIdx.x % heads of item blockIdx.x / heads.
 template <int CT, int DT>
-__global__ __launch_bounds__(LT) void select_large_batch_kernel(const DecodeArgs* __restrict__ table, int heads) {
-  select_large_body<CT, DT>(table[blockIdx.x / heads], blockIdx.x % heads);
+__global__ __launch_bounds__(LT) void select_large_batch_kernel(const DecodeArgs* __restrict__ table, int heads,
+                                                                 int parts) {
+  const int per_item = heads * parts;
+  const int r = blockIdx.x % per_item;
+  select_large_body<CT, DT>(table[blockIdx.x / per_item], r % heads, r / heads, parts);
 }
 
 bool large_selection(const DecodeArgs& a) {
@@ -595,7 +614,11 @@ int launch_select_large(const DecodeArgs& a, hipStream_t s, const DecodeArgs* pe
   // beside the selection's one per head), not in the scoring launch: the
   // update's dependent chain is longer than the scoring but shorter than the
   // selection.
-  const int select_blocks = a.st.retrieval_heads + (upd ? u.st.retrieval_heads : 0);
+  // parts per head: the selection repeats side by side on otherwise idle
+  // compute units and splits the (instruction-bound) slot resolution
+  const int ublocks = upd ? u.st.retrieval_heads : 0;
+  const int parts = std::max(1, std::min(LARGE_MAX_PARTS, (DEVICE_CUS - ublocks) / std::max(1, a.st.retrieval_heads)));
+  const int select_blocks = a.st.retrieval_heads * parts + ublocks;
   auto go = [&](auto score, auto select) {
     hipLaunchKernelGGL(score, sg, dim3(SELECT_THREADS), 0, s, a);
     int rc = launch_check("score_rows");
@@ -606,7 +629,7 @@ int launch_select_large(const DecodeArgs& a, hipStream_t s, const DecodeArgs* pe
       (void)hipGetLastError();
       return limit_error("large selection LDS (descriptors x 28 + selected / 16 bytes) exceeds the device limit");
     }
-    hipLaunchKernelGGL(select, dim3(select_blocks), dim3(LT), lds, s, a, u);
+    hipLaunchKernelGGL(select, dim3(select_blocks), dim3(LT), lds, s, a, u, parts);
     return launch_check("select_large");
   };
   const bool e4m3 = a.st.centroid_dtype == CKV_E4M3, bf16 = a.kv.dtype == CKV_BF16;
@@ -635,7 +658,8 @@ int launch_batch_select_large(const DecodeArgs& h, const DecodeArgs* table, int 
       (void)hipGetLastError();
       return limit_error("large selection LDS (descriptors x 28 + selected / 16 bytes) exceeds the device limit");
     }
-    hipLaunchKernelGGL(select, dim3(count * heads), dim3(LT), max_lds, s, table, heads);
+    const int parts = std::max(1, std::min(LARGE_MAX_PARTS, DEVICE_CUS / std::max(1, count * heads)));
+    hipLaunchKernelGGL(select, dim3(count * heads * parts), dim3(LT), max_lds, s, table, heads, parts);
     return launch_check("select_large_batch");
   };
   if (h.st.centroid_dtype == CKV_E4M3)
