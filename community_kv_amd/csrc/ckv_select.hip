@@ -64,7 +64,7 @@ constexpr int COOP_POLLS = 64;
 constexpr int COOP_PRE = 2;  // passes of the cooperative scoring share loaded with the first round
 constexpr int COOP_SCORE_WAVES = 6;  // waves that score and poll; the others walk the graph-indexed chain
 constexpr int COOP_MAX_PARTS = 64;
-// Prescored batched selection: workgroups per (item, head) at most, and the
+// Separate (non-fused) selections: workgroups per head at most, and the
 // compute units one round of them should fill (MI355X: 256).
 #ifndef CKV_PRESELECT_MAX_PARTS
 #define CKV_PRESELECT_MAX_PARTS 4
@@ -1438,13 +1438,16 @@ __device__ __forceinline__ void select_body(const DecodeArgs& a, const int rh, c
 }
 
 template <int CT, int DT, int OWN>
-__global__ __launch_bounds__(SELECT_THREADS) void select_kernel(DecodeArgs a, DecodeArgs u) {
-  if ((int)blockIdx.x >= a.st.retrieval_heads) {
-    const int urh = (int)blockIdx.x - a.st.retrieval_heads;
+// `parts` workgroups per head each run the selection and resolve a strided
+// share of the slot blocks and outputs.
+__global__ __launch_bounds__(SELECT_THREADS) void select_kernel(DecodeArgs a, DecodeArgs u, int parts) {
+  const int nsel = a.st.retrieval_heads * parts;
+  if ((int)blockIdx.x >= nsel) {
+    const int urh = (int)blockIdx.x - nsel;
     owner_update<CT, DT>(u, urh, u.ws.lse[(int64_t)urh * u.cfg.group_size]);
     return;
   }
-  select_body<CT, DT, OWN>(a, blockIdx.x);
+  select_body<CT, DT, OWN>(a, blockIdx.x % a.st.retrieval_heads, blockIdx.x / a.st.retrieval_heads, parts);
 }
 
 // Fused selection + attention partials: `parts` workgroups per retrieval head
@@ -1566,7 +1569,10 @@ int launch_score_select(const DecodeArgs& a, hipStream_t s, const DecodeArgs* pe
       u = *pending;
       extra = pending->st.retrieval_heads;
     }
-    hipLaunchKernelGGL(kernel, dim3(a.st.retrieval_heads + extra), dim3(SELECT_THREADS), lds, s, a, u);
+    const int parts = (int)std::max<int64_t>(
+        1, std::min<int64_t>(PRESELECT_MAX_PARTS, (CKV_DEVICE_CUS - extra) / std::max(1, a.st.retrieval_heads)));
+    hipLaunchKernelGGL(kernel, dim3(a.st.retrieval_heads * parts + extra), dim3(SELECT_THREADS), lds, s, a, u,
+                       parts);
     return launch_check("select");
   };
   constexpr int OWN_MAX = CKV_MAX_SELECT_ROWS / SELECT_THREADS;
