@@ -147,27 +147,29 @@ def test_prefill_config5_sampled_rows(device):
     _check_rows(q, k, v, res, rows, heads, scale=scale, num_sink=sinks, kappa=kappa, exact_sets=False)
 
 
-def test_prefill_config5_coarse_grid_exact_sets(device):
-    """Config 5's full shape (32,768 tokens, 32/8 heads, kappa 16) with the
-    planted inputs moved onto a coarse grid: q and k rounded to multiples of
-    1/64 in [-1, 1] (at most 6 significant bits, so every product is a multiple
-    of 2^-12 and every partial sum of 128 of them is exact in float32 whatever
-    the MMA's accumulation order).  Index sets and their order must then be
-    bit-identical to the oracle's exact top-16 on 1,000 sampled (row, head)
-    pairs plus the first and last eligible rows of several heads."""
+@pytest.mark.parametrize("kappa", [16, 8])
+def test_prefill_config5_coarse_grid_exact_sets(device, kappa):
+    """Config 5's full shape (32,768 tokens, 32/8 heads; kappa 16, and the
+    reference's width 8) with the planted inputs moved onto a coarse grid: q
+    and k rounded to multiples of 1/64 in [-1, 1] (at most 6 significant bits,
+    so every product is a multiple of 2^-12 and every partial sum of 128 of
+    them is exact in float32 whatever the MMA's accumulation order).  Index
+    sets and their order must then be bit-identical to the oracle's exact
+    top-kappa on 1,000 sampled (row, head) pairs plus the first and last
+    eligible rows of several heads."""
     import bench
 
-    print("prefill config 5 coarse grid (S=32768, 32/8 heads, kappa 16, exact sets)", flush=True)
+    print(f"prefill config 5 coarse grid (S=32768, 32/8 heads, kappa {kappa}, exact sets)", flush=True)
     q, k, v = bench.planted_prefill_inputs(device)
     q = ((q.float() * 64).round().clamp(-64, 64) / 64).to(torch.bfloat16)
     k = ((k.float() * 64).round().clamp(-64, 64) / 64).to(torch.bfloat16)
     S, Hq = q.shape[1], q.shape[2]
-    kappa, sinks = 16, 10
+    sinks = 10
     scale = 128 ** -0.5
     res = prefill_attention_topk(q, k, v, softmax_scale=scale, num_sink=sinks, kappa=kappa)
     torch.cuda.synchronize()
     skip = op.topk_row_skip(sinks, kappa)
-    rng = np.random.default_rng(17)
+    rng = np.random.default_rng(17 + kappa)
     rows = np.r_[rng.integers(skip, S, 1000), [skip] * 4, [S - 1] * 4]
     heads = np.r_[rng.integers(0, Hq, 1000), 0, 7, 16, Hq - 1, 0, 9, 22, Hq - 1]
     _check_rows(q, k, v, res, rows, heads, scale=scale, num_sink=sinks, kappa=kappa, exact_sets=True)
