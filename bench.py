@@ -889,6 +889,20 @@ def run_floor(args, device):
     word.zero_()
     res["handoff_agent_ns"] = ticks(4, word, 256, 2000)
     res["wall_clock_mhz_implied"] = float(np.median(clock["mhz"]))
+    # placement of the cooperative decode grid's workgroups on the XCDs
+    # (head h's parts are blocks h, h + 8, ...: they share an XCD when block b
+    # runs on XCD b % 8)
+    blocks = 144
+    xcc = torch.zeros(blocks, dtype=torch.int32, device=device)
+    for _ in range(20):
+        nat.check(lib.ckv_latency_probe(5, ctypes.c_void_p(xcc.data_ptr()), blocks * 4, 0, blocks, 512, 130 * 1024,
+                                        None, stream()))
+        torch.cuda.synchronize(device)
+        ids = xcc.cpu().numpy()
+        res.setdefault("xcd_block_mod8_runs", 0)
+        res["xcd_block_mod8_runs"] += int(all(ids[b] == ids[b % 8] for b in range(blocks)))
+    res["xcd_ids_first_16_blocks"] = [int(x) for x in ids[:16]]
+    res["xcd_probe_runs"] = 20
     print(json.dumps(res), flush=True)
 
 def main():

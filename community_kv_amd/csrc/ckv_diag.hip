@@ -82,6 +82,14 @@ __global__ void probe_handoff_kernel(uint32_t* word, int32_t hops, uint64_t* out
   }
 }
 
+// Each workgroup writes the id of the XCD (accelerator complex die) it runs
+// on to xcc[blockIdx.x]: the placement of a grid's workgroups on the dies.
+// (The launch's dynamic LDS size occupies the compute units as the decode
+// launch does; the kernel does not touch it.)  HW_REG_XCC_ID: hwreg 20, bits 0-15.
+__global__ void probe_xcc_kernel(uint32_t* xcc) {
+  if (threadIdx.x == 0) xcc[blockIdx.x] = __builtin_amdgcn_s_getreg(20 | (15 << 11));
+}
+
 }  // namespace ckv
 
 extern "C" int ckv_device_numerics(int op, const float* in, void* out, int64_t n, void* stream) {
@@ -100,7 +108,9 @@ extern "C" int ckv_device_numerics(int op, const float* in, void* out, int64_t n
 // on the host); 1 / 2: `hops` dependent plain / agent-scope loads through the
 // uint32 cycle in `buffer` (`bytes` long, written by the caller); 3: `hops`
 // dependent agent-scope fetch-and-adds on buffer[0]; 4: `hops` hand-offs
-// between two workgroups through buffer[0] (zeroed by the caller).  Kinds 1-4
+// between two workgroups through buffer[0] (zeroed by the caller); 5: a grid
+// of `blocks` x `threads` with `lds_bytes` of dynamic LDS whose workgroup b
+// writes the id of the XCD it runs on to ((uint32_t*)buffer)[b].  Kinds 1-4
 // write elapsed 100 MHz wall-clock ticks to out[0] (out: 2 uint64, device).
 extern "C" int ckv_latency_probe(int32_t kind, void* buffer, int64_t bytes, int32_t hops, int32_t blocks,
                                  int32_t threads, int32_t lds_bytes, uint64_t* out, void* stream) {
@@ -117,7 +127,8 @@ extern "C" int ckv_latency_probe(int32_t kind, void* buffer, int64_t bytes, int3
     hipLaunchKernelGGL(ckv::probe_empty_kernel, dim3(blocks), dim3(threads), (size_t)lds_bytes, s, nullptr);
     return ckv::launch_check("probe_empty");
   }
-  if (!buffer || !out || hops <= 0) return ckv_internal::set_error(CKV_E_INVALID, "null probe buffer or no hops");
+  if (!buffer || ((!out || hops <= 0) && kind != 5))
+    return ckv_internal::set_error(CKV_E_INVALID, "null probe buffer or no hops");
   uint32_t* b = reinterpret_cast<uint32_t*>(buffer);
   switch (kind) {
     case 1:
@@ -128,6 +139,18 @@ extern "C" int ckv_latency_probe(int32_t kind, void* buffer, int64_t bytes, int3
       break;
     case 3: hipLaunchKernelGGL(ckv::probe_atomic_kernel, dim3(1), dim3(64), 0, s, b, hops, out); break;
     case 4: hipLaunchKernelGGL(ckv::probe_handoff_kernel, dim3(2), dim3(64), 0, s, b, hops, out); break;
+    case 5:
+      if (blocks <= 0 || threads <= 0 || threads > 1024 || lds_bytes < 0 || lds_bytes > 160 * 1024 ||
+          bytes < (int64_t)blocks * 4)
+        return ckv_internal::set_error(CKV_E_INVALID, "bad placement-probe shape");
+      if (lds_bytes > 64 * 1024 &&
+          hipFuncSetAttribute(reinterpret_cast<const void*>(ckv::probe_xcc_kernel),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes) != hipSuccess) {
+        (void)hipGetLastError();
+        return ckv_internal::set_error(CKV_E_LAUNCH, "dynamic LDS size refused");
+      }
+      hipLaunchKernelGGL(ckv::probe_xcc_kernel, dim3(blocks), dim3(threads), (size_t)lds_bytes, s, b);
+      break;
     default: return ckv_internal::set_error(CKV_E_INVALID, "unknown probe kind");
   }
   return ckv::launch_check("latency_probe");

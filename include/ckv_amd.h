@@ -513,8 +513,11 @@ int ckv_dense_decode(const ckv_kv_cache* kv, int32_t seq_len, float softmax_scal
  * through the uint32 index cycle in `buffer` (`bytes` long, caller-written);
  * 3: `hops` dependent agent-scope fetch-and-adds on buffer[0]; 4: `hops`
  * hand-offs between two workgroups through buffer[0] (zeroed by the caller,
- * bounded polling).  Kinds 1-4 write the elapsed 100 MHz wall-clock ticks to
- * out[0] (two device uint64). */
+ * bounded polling); 5: a grid of blocks x threads with lds_bytes of dynamic
+ * LDS whose workgroup b writes the id of the XCD it runs on to
+ * ((uint32_t*)buffer)[b] (the dispatcher's placement, behind the decode
+ * launch's same-XCD score exchange).  Kinds 1-4 write the elapsed 100 MHz
+ * wall-clock ticks to out[0] (two device uint64). */
 int ckv_latency_probe(int32_t kind, void* buffer, int64_t bytes, int32_t hops, int32_t blocks, int32_t threads,
                       int32_t lds_bytes, uint64_t* out, void* stream);
 

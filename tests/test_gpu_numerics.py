@@ -49,3 +49,36 @@ def test_device_exp_log_match_oracle_bitwise(device):
     y = np.exp(rng.uniform(0, 80, 300_000)).astype(np.float32)
     y = np.concatenate([y, np.float32([1.0, 2.0, 1.41421356, 1.0000001])])
     assert np.array_equal(_device(1, y, np.float32, device).view(np.uint32), nm.ckv_log(y).view(np.uint32))
+
+
+def test_latency_probes_run(device):
+    """The diagnostics behind the decode cost model run and return sane
+    values: a dependent-load chase, the atomic round trip and the XCD
+    placement of the cooperative grid (ids in [0, 8); whether block b shares
+    the XCD of block b % 8, which the score exchange's speed relies on, is
+    printed, not asserted: results never depend on it)."""
+    import ctypes
+
+    from community_kv_amd import _native as nat
+
+    lib = nat.lib()
+    s = ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+    out = torch.zeros(2, dtype=torch.int64, device=device)
+    n = 1024
+    nxt = ((torch.arange(n, device=device) + 1) % n).to(torch.int32)
+    nat.check(lib.ckv_latency_probe(1, ctypes.c_void_p(nxt.data_ptr()), n * 4, 500, 0, 0, 0,
+                                    ctypes.c_void_p(out.data_ptr()), s))
+    torch.cuda.synchronize(device)
+    assert int(out[1]) == 500 % n and int(out[0]) > 0
+    word = torch.zeros(64, dtype=torch.int32, device=device)
+    nat.check(lib.ckv_latency_probe(3, ctypes.c_void_p(word.data_ptr()), 256, 100, 0, 0, 0,
+                                    ctypes.c_void_p(out.data_ptr()), s))
+    torch.cuda.synchronize(device)
+    assert int(word[0]) == 100
+    xcc = torch.full((144,), -1, dtype=torch.int32, device=device)
+    nat.check(lib.ckv_latency_probe(5, ctypes.c_void_p(xcc.data_ptr()), 144 * 4, 0, 144, 512, 130 * 1024, None, s))
+    torch.cuda.synchronize(device)
+    ids = xcc.cpu().numpy()
+    assert ((ids >= 0) & (ids < 8)).all()
+    periodic = all(ids[b] == ids[b % 8] for b in range(144))
+    print(f"XCD of blocks 0-15: {ids[:16].tolist()}; block b on the XCD of b % 8: {periodic}", flush=True)
