@@ -636,7 +636,8 @@ def run_batched(args, device, emit=True):
     rng = np.random.default_rng(3)
     lens = rng.integers(BATCH_MIN, BATCH_MAX + 1, BATCH)
     comms = [int(n) // 64 for n in lens]
-    max_decode = 2 * args.warmup + args.steps + max(5, args.steps // 4) + 12  # every replay appends one token
+    # every replay appends one token (the deferred pair below: one per layer)
+    max_decode = 2 * args.warmup + 2 * args.steps + max(5, args.steps // 4) + 16
     runtime, stack = build_stack(device, BATCH, max_decode, seed=1, seq_lens=lens, communities=comms,
                                  budget=BATCH_BUDGET)
     torch.cuda.synchronize(device)
@@ -660,6 +661,27 @@ def run_batched(args, device, emit=True):
     serial_graph = capture(serial_step, device)
     serial_graph.replay()
     serial_ms = time_graph(serial_graph, max(5, args.steps // 4), device)
+    # A second layer's batch (the same 8 contexts): the two layers step
+    # alternately, each leaving its online update pending to run inside the
+    # other's selection launch, as a model's consecutive layers would
+    # (ckv_batch_decode_after_update).  Per layer-step = replay / 2.
+    _, stack2 = build_stack(device, BATCH, max_decode, seed=2, seq_lens=lens, communities=comms,
+                            budget=BATCH_BUDGET)
+    batch2 = BatchDecode([e["call"] for e in stack2])
+    batch.decode_after(None)
+    batch2.decode_after(batch)
+
+    def deferred_pair():
+        batch.decode_after(batch2)
+        batch2.decode_after(batch)
+
+    deferred_graph = capture(deferred_pair, device)
+    for _ in range(args.warmup):
+        deferred_graph.replay()
+    deferred_ms = time_graph(deferred_graph, args.steps, device) / 2
+    batch2.update()
+    overflow2 = sum(int(e["layer"].workspace.update.overflow.sum().item()) for e in stack2)
+    del deferred_graph, batch2, stack2
     att_bytes = []
     for e in stack:
         slots = e["layer"].workspace.selection.slot_positions
@@ -690,9 +712,13 @@ def run_batched(args, device, emit=True):
                    "context_lengths": [int(n) for n in lens], "token_budget": BATCH_BUDGET, "local_window": WINDOW},
         "us_per_batch_step": ms * 1e3,
         "us_per_batch_step_sequence_by_sequence": serial_ms * 1e3,
+        "us_per_layer_step_deferred_update": deferred_ms * 1e3,
+        "deferred_update_note": ("two layers' batches stepped alternately, each layer's online update run inside "
+                                 "the other layer's selection launch (ckv_batch_decode_after_update); "
+                                 "us_per_batch_step keeps every update inline in its own step"),
         "step_algorithmic_bytes": step_bytes,
         "step_hbm_frac": step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
-        "overflow_flags": overflow,
+        "overflow_flags": overflow + overflow2,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": None,
                      "kernel": "attend_mfma_batch_kernel (gather + split partials of all 8 sequences)",
@@ -719,6 +745,7 @@ def side_configs(args, device):
     torch.cuda.empty_cache()
     bat = run_batched(types.SimpleNamespace(warmup=3, steps=20), device, emit=False)
     out["batched_us_per_step"] = bat["us_per_batch_step"]
+    out["batched_us_per_layer_step_deferred_update"] = bat["us_per_layer_step_deferred_update"]
     out["batched_tokens_per_s"] = bat["value"]
     out["batched_attention_kernel_us"] = bat["attention_partials_kernel_us"]
     out["batched_hbm_frac"] = bat["roofline"]["frac"]
@@ -818,7 +845,7 @@ def run_paper(args, device):
         "dense_us_per_step_layer": dense_ms * 1e3 / len(stack),
         "speedup_vs_dense": dense_ms / ms,
         "paper_h100_retrieval_plus_attention_us_per_layer": PAPER_H100_US_PER_LAYER,
-        "overflow_flags": overflow,
+        "overflow_flags": overflow + overflow2,
     }
     print(json.dumps(result), flush=True)
 
@@ -1053,7 +1080,7 @@ def main():
         "attended_tokens_per_head": tokens_per_head,
         "step_algorithmic_bytes_per_layer": step_bytes,
         "step_hbm_frac": step_bytes / (us_layer * 1e-6) / 1e9 / HBM_PEAK_GBS,
-        "overflow_flags": overflow,
+        "overflow_flags": overflow + overflow2,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": profiled_traffic(),
                      "kernel": "select_attend_kernel<e4m3, bf16, OWN, 24> (cooperative: shared centroid scoring, exact "

@@ -68,6 +68,8 @@ EXPORTED_SYMBOLS = (
     "ckv_batch_table_bytes",
     "ckv_batch_prepare",
     "ckv_batch_decode",
+    "ckv_batch_decode_after_update",
+    "ckv_batch_online_update",
     "ckv_batch_attention_partials",
     "ckv_dense_decode",
     "ckv_prefill_attention_topk",
@@ -241,6 +243,11 @@ def lib() -> ctypes.CDLL:
     handle.ckv_batch_prepare.restype = ctypes.c_int
     handle.ckv_batch_decode.argtypes = [ctypes.POINTER(LayerArgs), _i32, _p, _p]
     handle.ckv_batch_decode.restype = ctypes.c_int
+    handle.ckv_batch_decode_after_update.argtypes = [ctypes.POINTER(LayerArgs), _i32, _p, ctypes.POINTER(LayerArgs),
+                                                     _i32, _p, _p]
+    handle.ckv_batch_decode_after_update.restype = ctypes.c_int
+    handle.ckv_batch_online_update.argtypes = [ctypes.POINTER(LayerArgs), _i32, _p, _p]
+    handle.ckv_batch_online_update.restype = ctypes.c_int
     handle.ckv_batch_attention_partials.argtypes = [ctypes.POINTER(LayerArgs), _i32, _p, _p]
     handle.ckv_batch_attention_partials.restype = ctypes.c_int
     handle.ckv_dense_decode.argtypes = [ctypes.POINTER(KvCache), _i32, _f32, _p, _p, _p, _p, _p, _p]

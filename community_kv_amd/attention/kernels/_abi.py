@@ -168,6 +168,26 @@ class BatchDecode:
         nat.check(nat.lib().ckv_batch_decode(self.items, len(self.calls), ctypes.c_void_p(self.table.data_ptr()),
                                              ctypes.c_void_p(s)))
 
+    def decode_after(self, pending: "BatchDecode | None", stream=None) -> None:
+        """One step of this batch with its online update left pending, and
+        the pending update of ``pending`` (another layer's batch whose step
+        has run) in the same selection launch (``ckv_batch_decode_after_update``)."""
+        s = nat.stream_handle(self.device) if stream is None else stream
+        if pending is None:
+            nat.check(nat.lib().ckv_batch_decode_after_update(
+                self.items, len(self.calls), ctypes.c_void_p(self.table.data_ptr()), None, 0, None,
+                ctypes.c_void_p(s)))
+        else:
+            nat.check(nat.lib().ckv_batch_decode_after_update(
+                self.items, len(self.calls), ctypes.c_void_p(self.table.data_ptr()), pending.items,
+                len(pending.calls), ctypes.c_void_p(pending.table.data_ptr()), ctypes.c_void_p(s)))
+
+    def update(self, stream=None) -> None:
+        """This batch's pending online update by itself (``ckv_batch_online_update``)."""
+        s = nat.stream_handle(self.device) if stream is None else stream
+        nat.check(nat.lib().ckv_batch_online_update(self.items, len(self.calls),
+                                                    ctypes.c_void_p(self.table.data_ptr()), ctypes.c_void_p(s)))
+
     def attention_partials(self, stream=None) -> None:
         """The batched attention launch alone (profiling)."""
         s = nat.stream_handle(self.device) if stream is None else stream

@@ -834,6 +834,16 @@ int launch_batch_attention(const DecodeArgs& h, const DecodeArgs* table, int cou
   return launch_batch_merge(h, table, count, splits, s);
 }
 
+// Layer-wise aggregation of a batch: copy each owner's updated community
+// state to the heads sharing its graph.
+int launch_batch_sync_shared(const DecodeArgs& h, const DecodeArgs* table, int count, hipStream_t s) {
+  const int heads = h.st.retrieval_heads;
+  const dim3 g(count * heads);
+  if (h.st.centroid_dtype == CKV_E4M3) hipLaunchKernelGGL((sync_shared_batch_kernel<CKV_E4M3, CKV_BF16>), g, dim3(REDUCE_THREADS), 0, s, table, heads);
+  else hipLaunchKernelGGL((sync_shared_batch_kernel<CKV_F32, CKV_BF16>), g, dim3(REDUCE_THREADS), 0, s, table, heads);
+  return launch_check("sync_shared_batch");
+}
+
 int launch_batch_merge_update(const DecodeArgs& h, const DecodeArgs* table, int count, int splits,
                               bool any_shared, hipStream_t s) {
   const int heads = h.st.retrieval_heads;
@@ -854,9 +864,7 @@ int launch_batch_merge_update(const DecodeArgs& h, const DecodeArgs* table, int 
   }
   int r = launch_check("merge_update_batch");
   if (r || !any_shared) return r;
-  if (h.st.centroid_dtype == CKV_E4M3) hipLaunchKernelGGL((sync_shared_batch_kernel<CKV_E4M3, CKV_BF16>), g, dim3(REDUCE_THREADS), 0, s, table, heads);
-  else hipLaunchKernelGGL((sync_shared_batch_kernel<CKV_F32, CKV_BF16>), g, dim3(REDUCE_THREADS), 0, s, table, heads);
-  return launch_check("sync_shared_batch");
+  return launch_batch_sync_shared(h, table, count, s);
 }
 
 int launch_batch_update(const DecodeArgs& h, const DecodeArgs* table, int count, bool any_shared, hipStream_t s) {
@@ -866,9 +874,7 @@ int launch_batch_update(const DecodeArgs& h, const DecodeArgs* table, int count,
   else hipLaunchKernelGGL((update_batch_kernel<CKV_F32, CKV_BF16>), g, dim3(256), 0, s, table, heads);
   int r = launch_check("update_batch");
   if (r || !any_shared) return r;
-  if (h.st.centroid_dtype == CKV_E4M3) hipLaunchKernelGGL((sync_shared_batch_kernel<CKV_E4M3, CKV_BF16>), g, dim3(REDUCE_THREADS), 0, s, table, heads);
-  else hipLaunchKernelGGL((sync_shared_batch_kernel<CKV_F32, CKV_BF16>), g, dim3(REDUCE_THREADS), 0, s, table, heads);
-  return launch_check("sync_shared_batch");
+  return launch_batch_sync_shared(h, table, count, s);
 }
 
 int dense_chunks(int seq_len, int chunk_tiles) { return (seq_len + TILE * chunk_tiles - 1) / (TILE * chunk_tiles); }

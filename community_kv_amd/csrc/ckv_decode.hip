@@ -368,7 +368,15 @@ extern "C" int ckv_batch_prepare(const ckv_layer_args* items, int32_t count, voi
   return CKV_OK;
 }
 
-extern "C" int ckv_batch_decode(const ckv_layer_args* items, int32_t count, const void* table, void* stream) {
+namespace {
+
+// One batched step of `items`; `defer`: leave the items' online update
+// pending (the split merge alone ends the step).  `pending` (null: none): a
+// batch whose update is pending, run in extra workgroups of the selection
+// launch where the selection path has them, else in a launch of its own
+// before the step.
+int batch_step(const ckv_layer_args* items, int32_t count, const void* table, const ckv_layer_args* pending,
+               int32_t pending_count, const void* pending_table, bool defer, void* stream) {
   std::vector<ckv::DecodeArgs> packed;
   int max_nscore;
   size_t max_lds;
@@ -380,6 +388,25 @@ extern "C" int ckv_batch_decode(const ckv_layer_args* items, int32_t count, cons
   const ckv::DecodeArgs* t = reinterpret_cast<const ckv::DecodeArgs*>(table);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const ckv::DecodeArgs& h = packed[0];
+
+  std::vector<ckv::DecodeArgs> upacked;
+  bool u_shared = false;
+  const ckv::DecodeArgs* ut = nullptr;
+  if (pending) {
+    int u_nscore;
+    size_t u_lds, u_large;
+    rc = validate_batch(pending, pending_count, &upacked, &u_nscore, &u_lds, &u_shared, &u_large);
+    if (rc) return rc;
+    if (!pending_table) return fail(CKV_E_INVALID, "null pending batch table");
+    for (const ckv::DecodeArgs& u : upacked) {
+      for (const ckv::DecodeArgs& it : packed) {
+        if (u.st.centroids == it.st.centroids || u.ws.lse == it.ws.lse || u.ws.slot_positions == it.ws.slot_positions)
+          return fail(CKV_E_INVALID, "the pending batch must not share state or workspace with this batch");
+      }
+    }
+    if (upacked[0].cfg.assignment != CKV_ASSIGN_NONE) ut = reinterpret_cast<const ckv::DecodeArgs*>(pending_table);
+  }
+
   int parts = ckv::fused_parts(h);
   size_t fused_lds = 0;
   for (const ckv::DecodeArgs& it : packed) {
@@ -393,18 +420,56 @@ extern "C" int ckv_batch_decode(const ckv_layer_args* items, int32_t count, cons
   // the large selection: scoring on every compute unit, 1,024 threads per head
   const bool large = max_nscore > CKV_MAX_SELECT_ROWS;
   if (large) parts = 0;
+  const bool ride = ut != nullptr && parts == 0 && !large && upacked[0].st.centroid_dtype == h.st.centroid_dtype;
+  if (ut != nullptr && !ride) {  // the pending update in a launch of its own
+    rc = ckv::launch_batch_update(upacked[0], ut, pending_count, u_shared, s);
+    if (rc) return rc;
+  }
   int splits = parts;
   if (parts > 0) {
     rc = ckv::launch_batch_select_attend(h, t, count, max_nscore, fused_lds, parts, s);
   } else {
-    rc = large ? ckv::launch_batch_select_large(h, t, count, max_nscore, max_large_lds, s)
-               : ckv::launch_batch_select(h, t, count, max_nscore, max_lds, s);
+    if (large) {
+      rc = ckv::launch_batch_select_large(h, t, count, max_nscore, max_large_lds, s);
+    } else if (ride) {
+      rc = ckv::launch_batch_select(h, t, count, max_nscore, max_lds, s, ut, pending_count,
+                                    upacked[0].st.retrieval_heads);
+      if (!rc && u_shared) rc = ckv::launch_batch_sync_shared(upacked[0], ut, pending_count, s);
+    } else {
+      rc = ckv::launch_batch_select(h, t, count, max_nscore, max_lds, s);
+    }
     if (!rc) rc = ckv::launch_batch_attention(h, t, count, s, true);
     splits = ckv::attention_batch_splits(h);
   }
   if (rc) return rc;
-  if (h.cfg.assignment == CKV_ASSIGN_NONE) return ckv::launch_batch_merge(h, t, count, splits, s);
+  if (defer || h.cfg.assignment == CKV_ASSIGN_NONE) return ckv::launch_batch_merge(h, t, count, splits, s);
   return ckv::launch_batch_merge_update(h, t, count, splits, any_shared, s);
+}
+
+}  // namespace
+
+extern "C" int ckv_batch_decode(const ckv_layer_args* items, int32_t count, const void* table, void* stream) {
+  return batch_step(items, count, table, nullptr, 0, nullptr, false, stream);
+}
+
+extern "C" int ckv_batch_decode_after_update(const ckv_layer_args* items, int32_t count, const void* table,
+                                             const ckv_layer_args* pending, int32_t pending_count,
+                                             const void* pending_table, void* stream) {
+  return batch_step(items, count, table, pending, pending_count, pending_table, true, stream);
+}
+
+extern "C" int ckv_batch_online_update(const ckv_layer_args* items, int32_t count, const void* table, void* stream) {
+  std::vector<ckv::DecodeArgs> packed;
+  int max_nscore;
+  size_t max_lds;
+  bool any_shared;
+  size_t max_large_lds;
+  const int rc = validate_batch(items, count, &packed, &max_nscore, &max_lds, &any_shared, &max_large_lds);
+  if (rc) return rc;
+  if (!table) return fail(CKV_E_INVALID, "null batch table");
+  if (packed[0].cfg.assignment == CKV_ASSIGN_NONE) return CKV_OK;
+  return ckv::launch_batch_update(packed[0], reinterpret_cast<const ckv::DecodeArgs*>(table), count, any_shared,
+                                  reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int ckv_batch_attention_partials(const ckv_layer_args* items, int32_t count, const void* table,

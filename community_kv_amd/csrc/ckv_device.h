@@ -586,10 +586,13 @@ int launch_batch_select_attend(const DecodeArgs& h, const DecodeArgs* table, int
                                size_t max_lds, int parts, hipStream_t stream);
 int launch_merge(const DecodeArgs& a, hipStream_t stream, int splits);
 int launch_batch_merge(const DecodeArgs& h, const DecodeArgs* table, int count, int splits, hipStream_t stream);
+// `utable` (null: none): a batch of `ucount` items of `uheads` heads whose
+// online update is pending; it runs in extra workgroups of the selection launch.
 int launch_batch_select(const DecodeArgs& h, const DecodeArgs* table, int count, int max_nscore, size_t max_lds,
-                        hipStream_t stream);
+                        hipStream_t stream, const DecodeArgs* utable = nullptr, int ucount = 0, int uheads = 0);
 int launch_batch_attention(const DecodeArgs& h, const DecodeArgs* table, int count, hipStream_t stream,
                            bool partials_only = false);
+int launch_batch_sync_shared(const DecodeArgs& h, const DecodeArgs* table, int count, hipStream_t stream);
 int launch_batch_update(const DecodeArgs& h, const DecodeArgs* table, int count, bool any_shared, hipStream_t stream);
 // Merge of `splits` partials and the online update in one launch (+ the shared-graph sync).
 int launch_batch_merge_update(const DecodeArgs& h, const DecodeArgs* table, int count, int splits, bool any_shared,

@@ -1523,11 +1523,26 @@ __global__ __launch_bounds__(SELECT_THREADS) void score_rows_batch_kernel(const 
     reinterpret_cast<uint16_t*>(a.ws.scores)[(int64_t)rh * C + c] = f16_bits_hw(size > 0 ? best : NEG_INF);
 }
 
+// Workgroups from `nsel` on run the pending online update of another batch
+// `utable` (workgroup nsel + w: item w / uheads, head w % uheads).
+template <int CT, int DT>
+__device__ __forceinline__ void pending_batch_update(const DecodeArgs* __restrict__ utable, int uheads, int w) {
+  const DecodeArgs& u = utable[w / uheads];
+  const int urh = w % uheads;
+  owner_update<CT, DT>(u, urh, u.ws.lse[(int64_t)urh * u.cfg.group_size]);
+}
+
 template <int CT, int DT, int OWN>
 // `parts` workgroups per (item, head) each run the selection and resolve a
 // strided share of the slot table's 64-slot blocks (and of the other outputs).
 __global__ __launch_bounds__(SELECT_THREADS) void select_prescored_batch_kernel(const DecodeArgs* __restrict__ table,
-                                                                               int heads, int parts) {
+                                                                               int heads, int parts, int nsel,
+                                                                               const DecodeArgs* __restrict__ utable,
+                                                                               int uheads) {
+  if ((int)blockIdx.x >= nsel) {
+    pending_batch_update<CT, DT>(utable, uheads, (int)blockIdx.x - nsel);
+    return;
+  }
   const int per_item = heads * parts;
   const int r = blockIdx.x % per_item;
   select_body<CT, DT, OWN, false, true>(table[blockIdx.x / per_item], r % heads, r / heads, parts);
@@ -1536,7 +1551,13 @@ __global__ __launch_bounds__(SELECT_THREADS) void select_prescored_batch_kernel(
 // Batched selection: workgroup w serves item w / heads, head w % heads of the
 // device table.
 template <int CT, int DT, int OWN>
-__global__ __launch_bounds__(SELECT_THREADS) void select_batch_kernel(const DecodeArgs* __restrict__ table, int heads) {
+__global__ __launch_bounds__(SELECT_THREADS) void select_batch_kernel(const DecodeArgs* __restrict__ table, int heads,
+                                                                      int nsel, const DecodeArgs* __restrict__ utable,
+                                                                      int uheads) {
+  if ((int)blockIdx.x >= nsel) {
+    pending_batch_update<CT, DT>(utable, uheads, (int)blockIdx.x - nsel);
+    return;
+  }
   select_body<CT, DT, OWN>(table[blockIdx.x / heads], blockIdx.x % heads);
 }
 
@@ -1721,7 +1742,8 @@ int launch_batch_select_attend(const DecodeArgs& h, const DecodeArgs* table, int
 constexpr int PRESCORE_MIN_ROWS = 2 * SELECT_THREADS;
 
 int launch_batch_select(const DecodeArgs& h, const DecodeArgs* table, int count, int max_nscore, size_t max_lds,
-                        hipStream_t s) {
+                        hipStream_t s, const DecodeArgs* utable, int ucount, int uheads) {
+  const int extra = utable ? ucount * uheads : 0;  // pending-update workgroups
   const int own = (max_nscore + SELECT_THREADS - 1) / SELECT_THREADS;
   const bool pre = max_nscore > PRESCORE_MIN_ROWS && h.cfg.assignment != CKV_ASSIGN_NEAREST;
   if (pre) {
@@ -1748,20 +1770,24 @@ int launch_batch_select(const DecodeArgs& h, const DecodeArgs* table, int count,
   };
   auto launch = [&](auto kernel) {
     if (const int rc = set_lds(kernel)) return rc;
-    hipLaunchKernelGGL(kernel, dim3(count * h.st.retrieval_heads), dim3(SELECT_THREADS), max_lds, s, table,
-                       h.st.retrieval_heads);
+    const int nsel = count * h.st.retrieval_heads;
+    hipLaunchKernelGGL(kernel, dim3(nsel + extra), dim3(SELECT_THREADS), max_lds, s, table, h.st.retrieval_heads,
+                       nsel, utable, uheads);
     return launch_check("select_batch");
   };
   // The prescored selection leaves most compute units idle (one workgroup per
   // (item, head)) while its slot resolution is instruction-bound: `parts`
   // workgroups per (item, head) repeat the selection side by side and split
-  // the slot blocks, as many as one round of workgroups on the device holds.
-  const int pre_parts = (int)std::max<int64_t>(1, std::min<int64_t>(PRESELECT_MAX_PARTS,
-                                                   CKV_DEVICE_CUS / ((int64_t)count * h.st.retrieval_heads)));
+  // the slot blocks, as many as one round of workgroups on the device holds
+  // beside the pending-update workgroups.
+  const int pre_parts = (int)std::max<int64_t>(
+      1, std::min<int64_t>(PRESELECT_MAX_PARTS,
+                           std::max<int64_t>(0, (int64_t)CKV_DEVICE_CUS - extra) / ((int64_t)count * h.st.retrieval_heads)));
   auto launch_pre = [&](auto kernel) {
     if (const int rc = set_lds(kernel)) return rc;
-    hipLaunchKernelGGL(kernel, dim3(count * h.st.retrieval_heads * pre_parts), dim3(SELECT_THREADS), max_lds, s,
-                       table, h.st.retrieval_heads, pre_parts);
+    const int nsel = count * h.st.retrieval_heads * pre_parts;
+    hipLaunchKernelGGL(kernel, dim3(nsel + extra), dim3(SELECT_THREADS), max_lds, s, table, h.st.retrieval_heads,
+                       pre_parts, nsel, utable, uheads);
     return launch_check("select_prescored_batch");
   };
   constexpr int OWN_MAX = CKV_MAX_SELECT_ROWS / SELECT_THREADS;

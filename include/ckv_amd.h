@@ -448,6 +448,22 @@ int ckv_score_select_after_update(const ckv_layer_args* layer, const ckv_layer_a
 size_t ckv_batch_table_bytes(int32_t count);
 int ckv_batch_prepare(const ckv_layer_args* items, int32_t count, void* table, void* stream);
 int ckv_batch_decode(const ckv_layer_args* items, int32_t count, const void* table, void* stream);
+/* Scheduling variant of ckv_batch_decode, no counterpart in the reference
+ * (whose update is fused into its attention kernel): one step of `items`
+ * whose online update is left pending (the step ends with the split merge),
+ * and, on otherwise idle compute units of its selection launch, the pending
+ * update of another batch `pending` (null: none; `pending_count` items,
+ * `pending_table` prepared by ckv_batch_prepare) whose step has already run on
+ * this stream -- the previous layer's batch, so the update leaves the critical
+ * path as it does for ckv_decode_step_after_update.  Where the batch takes
+ * the fused or the multi-kernel selection the pending update runs in a launch
+ * of its own before the step.  The two batches must not share state or
+ * workspace.  ckv_batch_online_update runs a batch's pending update by itself
+ * (the flush after the last layer).  Results equal ckv_batch_decode's. */
+int ckv_batch_decode_after_update(const ckv_layer_args* items, int32_t count, const void* table,
+                                  const ckv_layer_args* pending, int32_t pending_count, const void* pending_table,
+                                  void* stream);
+int ckv_batch_online_update(const ckv_layer_args* items, int32_t count, const void* table, void* stream);
 /* (diagnostics) the attention launch of ckv_batch_decode alone, writing split partials. */
 int ckv_batch_attention_partials(const ckv_layer_args* items, int32_t count, const void* table, void* stream);
 

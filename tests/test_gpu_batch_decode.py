@@ -124,3 +124,65 @@ def test_batch_with_one_huge_item_matches_single_selection(device):
         oa, ob = a["ws"].attention.output.float(), b["ws"].attention.output.float()
         assert (oa - ob).abs().max().item() < 2e-2, i
         assert (a["ws"].attention.lse - b["ws"].attention.lse).abs().max().item() < 1e-4, i
+
+
+@pytest.mark.parametrize("aggregation,assignment,group,items", [
+    (co.QUERY_GROUP, "delta_q", 4, ITEMS_LARGE), (co.QUERY_GROUP, "nearest_centroid", 4, ITEMS_LARGE),
+    (co.LAYER_WISE, "delta_q", 2, ITEMS_LARGE), (co.QUERY_GROUP, "delta_q", 4, ITEMS),
+    (co.QUERY_GROUP, "delta_q", 4, ITEMS_HUGE)])
+def test_deferred_batch_updates_match_inline(device, aggregation, assignment, group, items):
+    """Two layers' batches stepped alternately: ``ckv_batch_decode_after_update``
+    (each batch's update left pending and run inside the other batch's
+    selection launch, or in a launch of its own where that selection has no
+    room for it; the last one flushed with ``ckv_batch_online_update``) must
+    give outputs, selections and graph state bit-identical to ``ckv_batch_decode``
+    with every update inline."""
+    print(f"deferred batch {aggregation} {assignment} communities={[kw['communities'] for kw in items]}",
+          flush=True)
+    params = co.StepParams(group_size=group, num_sink=10, token_budget=512, local_window=64, assignment=assignment)
+    qh = 4 * group
+    layers = [[syn.build_layer(seed=base + i, query_heads=qh, kv_heads=4, num_sink=10, max_decode_tokens=16,
+                               aggregation=aggregation, **kw) for i, kw in enumerate(items)] for base in (50, 70)]
+    inline = [[_item(fx, params, device) for fx in fxs] for fxs in layers]
+    deferred = [[_item(fx, params, device) for fx in fxs] for fxs in layers]
+    inline_b = [BatchDecode([it["call"] for it in lay]) for lay in inline]
+    deferred_b = [BatchDecode([it["call"] for it in lay]) for lay in deferred]
+    rng = np.random.default_rng(11)
+
+    def check(lay, step, with_state):
+        for i, (a, b) in enumerate(zip(inline[lay], deferred[lay])):
+            case = f"layer {lay} step {step} item {i}"
+            assert torch.equal(a["ws"].attention.output, b["ws"].attention.output), case
+            assert torch.equal(a["ws"].attention.lse, b["ws"].attention.lse), case
+            assert torch.equal(a["ws"].selection.slot_positions, b["ws"].selection.slot_positions), case
+            if with_state:
+                h.assert_states_equal(h.state_to_numpy(a["state"], a["cur"], True),
+                                      h.state_to_numpy(b["state"], b["cur"], True))
+
+    pending = None
+    for step in range(6):
+        for lay in range(2):
+            inline_b[lay].decode()
+            deferred_b[lay].decode_after(pending)
+            pending = deferred_b[lay]
+        torch.cuda.synchronize(device)
+        check(0, step, True)  # layer 0's update ran in layer 1's selection launch
+        check(1, step, False)  # layer 1's update is still pending
+        for lay in range(2):
+            for fx, a, b in zip(layers[lay], inline[lay], deferred[lay]):
+                q = syn.fresh_query(fx, rng)
+                a["q"].copy_(h.torch_values(q, fx.dtype, device))
+                b["q"].copy_(h.torch_values(q, fx.dtype, device))
+    pending.update()
+    torch.cuda.synchronize(device)
+    check(1, "flush", True)
+
+
+def test_deferred_batch_rejects_shared_state(device):
+    params = co.StepParams(group_size=4, num_sink=10, token_budget=512)
+    fx = syn.build_layer(seed=3, query_heads=16, kv_heads=4, seq_len=4096, communities=64, num_sink=10,
+                         max_decode_tokens=4, aggregation=co.QUERY_GROUP)
+    a = _item(fx, params, device)
+    batch = BatchDecode([a["call"]])
+    with pytest.raises(RuntimeError, match="must not share"):
+        batch.decode_after(batch)
