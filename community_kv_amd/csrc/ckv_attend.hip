@@ -215,10 +215,10 @@ __global__ __launch_bounds__(UPDATE_THREADS) void update_kernel(DecodeArgs a) {
 // Batched launches read each item's arguments from a device table
 // (workgroup w serves item w / heads, head w % heads).
 template <int CT, int DT>
-__global__ __launch_bounds__(256) void update_batch_kernel(const DecodeArgs* __restrict__ table, int heads) {
+__global__ __launch_bounds__(UPDATE_THREADS) void update_batch_kernel(const DecodeArgs* __restrict__ table, int heads) {
   const DecodeArgs& a = table[blockIdx.x / heads];
   const int rh = blockIdx.x % heads;
-  owner_update<CT, DT>(a, rh, a.ws.lse[(int64_t)rh * a.cfg.group_size]);
+  owner_update<CT, DT, 9>(a, rh, a.ws.lse[(int64_t)rh * a.cfg.group_size]);
 }
 
 template <int CT, int DT>
@@ -870,8 +870,8 @@ int launch_batch_merge_update(const DecodeArgs& h, const DecodeArgs* table, int 
 int launch_batch_update(const DecodeArgs& h, const DecodeArgs* table, int count, bool any_shared, hipStream_t s) {
   const int heads = h.st.retrieval_heads;
   const dim3 g(count * heads);
-  if (h.st.centroid_dtype == CKV_E4M3) hipLaunchKernelGGL((update_batch_kernel<CKV_E4M3, CKV_BF16>), g, dim3(256), 0, s, table, heads);
-  else hipLaunchKernelGGL((update_batch_kernel<CKV_F32, CKV_BF16>), g, dim3(256), 0, s, table, heads);
+  if (h.st.centroid_dtype == CKV_E4M3) hipLaunchKernelGGL((update_batch_kernel<CKV_E4M3, CKV_BF16>), g, dim3(UPDATE_THREADS), 0, s, table, heads);
+  else hipLaunchKernelGGL((update_batch_kernel<CKV_F32, CKV_BF16>), g, dim3(UPDATE_THREADS), 0, s, table, heads);
   int r = launch_check("update_batch");
   if (r || !any_shared) return r;
   return launch_batch_sync_shared(h, table, count, s);

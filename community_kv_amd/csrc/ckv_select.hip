@@ -1793,8 +1793,9 @@ int launch_batch_select(const DecodeArgs& h, const DecodeArgs* table, int count,
   constexpr int OWN_MAX = CKV_MAX_SELECT_ROWS / SELECT_THREADS;
   if (pre) {
     if (h.st.centroid_dtype == CKV_E4M3) {
-      return own <= 4 ? launch_pre(select_prescored_batch_kernel<CKV_E4M3, CKV_BF16, 4>)
-                      : launch_pre(select_prescored_batch_kernel<CKV_E4M3, CKV_BF16, OWN_MAX>);
+      return own <= 4   ? launch_pre(select_prescored_batch_kernel<CKV_E4M3, CKV_BF16, 4>)
+             : own <= 8 ? launch_pre(select_prescored_batch_kernel<CKV_E4M3, CKV_BF16, 8>)
+                        : launch_pre(select_prescored_batch_kernel<CKV_E4M3, CKV_BF16, OWN_MAX>);
     }
     return own <= 4 ? launch_pre(select_prescored_batch_kernel<CKV_F32, CKV_BF16, 4>)
                     : launch_pre(select_prescored_batch_kernel<CKV_F32, CKV_BF16, OWN_MAX>);
