@@ -726,6 +726,7 @@ int launch_merge(const DecodeArgs& a, hipStream_t s, int splits) {
     if (splits <= 8) hipLaunchKernelGGL(merge_wide_kernel<8>, mg, dim3(MERGE_WIDE_THREADS), 0, s, a, splits);
     else if (splits <= 16) hipLaunchKernelGGL(merge_wide_kernel<16>, mg, dim3(MERGE_WIDE_THREADS), 0, s, a, splits);
     else if (splits <= 32) hipLaunchKernelGGL(merge_wide_kernel<32>, mg, dim3(MERGE_WIDE_THREADS), 0, s, a, splits);
+    else if (splits <= 40) hipLaunchKernelGGL(merge_wide_kernel<40>, mg, dim3(MERGE_WIDE_THREADS), 0, s, a, splits);
     else hipLaunchKernelGGL(merge_wide_kernel<64>, mg, dim3(MERGE_WIDE_THREADS), 0, s, a, splits);
   } else {
     if (3 * a.cfg.group_size * splits > MERGE_SCRATCH) {
@@ -742,6 +743,7 @@ int launch_batch_merge(const DecodeArgs& h, const DecodeArgs* table, int count, 
   if (splits <= 8) hipLaunchKernelGGL(merge_wide_batch_kernel<8>, mg, dim3(MERGE_WIDE_THREADS), 0, s, table, heads, splits);
   else if (splits <= 16) hipLaunchKernelGGL(merge_wide_batch_kernel<16>, mg, dim3(MERGE_WIDE_THREADS), 0, s, table, heads, splits);
   else if (splits <= 32) hipLaunchKernelGGL(merge_wide_batch_kernel<32>, mg, dim3(MERGE_WIDE_THREADS), 0, s, table, heads, splits);
+  else if (splits <= 40) hipLaunchKernelGGL(merge_wide_batch_kernel<40>, mg, dim3(MERGE_WIDE_THREADS), 0, s, table, heads, splits);
   else hipLaunchKernelGGL(merge_wide_batch_kernel<64>, mg, dim3(MERGE_WIDE_THREADS), 0, s, table, heads, splits);
   return launch_check("merge_batch");
 }
@@ -855,11 +857,13 @@ int launch_batch_merge_update(const DecodeArgs& h, const DecodeArgs* table, int 
     if (splits <= 8) go(merge_update_batch_kernel<8, CKV_E4M3, CKV_BF16>);
     else if (splits <= 16) go(merge_update_batch_kernel<16, CKV_E4M3, CKV_BF16>);
     else if (splits <= 32) go(merge_update_batch_kernel<32, CKV_E4M3, CKV_BF16>);
+    else if (splits <= 40) go(merge_update_batch_kernel<40, CKV_E4M3, CKV_BF16>);
     else go(merge_update_batch_kernel<64, CKV_E4M3, CKV_BF16>);
   } else {
     if (splits <= 8) go(merge_update_batch_kernel<8, CKV_F32, CKV_BF16>);
     else if (splits <= 16) go(merge_update_batch_kernel<16, CKV_F32, CKV_BF16>);
     else if (splits <= 32) go(merge_update_batch_kernel<32, CKV_F32, CKV_BF16>);
+    else if (splits <= 40) go(merge_update_batch_kernel<40, CKV_F32, CKV_BF16>);
     else go(merge_update_batch_kernel<64, CKV_F32, CKV_BF16>);
   }
   int r = launch_check("merge_update_batch");
