@@ -1687,6 +1687,9 @@ int launch_select_attend(const DecodeArgs& a, hipStream_t s, const DecodeArgs* p
     if (coop_parts(a) != parts) return limit_error("the cooperative fused launch cannot serve this layer");
     // the merge loads PMAX accumulators per output element (clamped to the parts)
     auto by_own = [&](auto k1, auto k2, auto k4) { return own <= 1 ? launch(k1) : own <= 2 ? launch(k2) : launch(k4); };
+    if (parts <= 18)
+      return by_own(select_attend_kernel<CKV_E4M3, CKV_BF16, 1, 18>, select_attend_kernel<CKV_E4M3, CKV_BF16, 2, 18>,
+                    select_attend_kernel<CKV_E4M3, CKV_BF16, 4, 18>);
     if (parts <= 24)
       return by_own(select_attend_kernel<CKV_E4M3, CKV_BF16, 1, 24>, select_attend_kernel<CKV_E4M3, CKV_BF16, 2, 24>,
                     select_attend_kernel<CKV_E4M3, CKV_BF16, 4, 24>);
