@@ -1109,7 +1109,7 @@ def main():
         "overflow_flags": overflow,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": profiled_traffic(),
-                     "kernel": "select_attend_kernel<e4m3, bf16, OWN, 24> (cooperative: shared centroid scoring, exact "
+                     "kernel": "select_attend_kernel<e4m3, bf16, OWN, 18> (cooperative: shared centroid scoring, exact "
                                "selection, slot resolution, KV gather + MFMA attention, in-launch split merge)",
                      "bytes_per_launch": fused_bytes},
     }
