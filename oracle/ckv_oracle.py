@@ -24,7 +24,11 @@ Pinning (see tests/test_oracle_*.py):
     assignment, top-k selection, slot materialisation with the window union
     and the layer-wise centroid sync: tests/test_oracle_pins.py (exact
     rational / float64 brute force, brute-force set construction, the
-    reference's materialisation answer, hand-computed sync answers).
+    reference's materialisation answer, hand-computed sync answers);
+  * init_modularity_state (community and total weights of the partition
+    fixture): tests/test_oracle_pins.py, against hand graphs (an edge inside
+    one community, one across two, a zero-weight edge, several graphs), an
+    empty graph and a dense symmetric adjacency built by brute force.
 """
 
 from __future__ import annotations
