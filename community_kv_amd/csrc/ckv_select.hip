@@ -57,10 +57,6 @@ constexpr int DESC_ARRAYS = 7;                             // per-descriptor LDS
 constexpr size_t FUSED_LDS_LIMIT = 134 * 1024;
 // 64-slot tiles attended per workgroup of the fused path (parts per head = tiles / this).
 constexpr int FUSED_TILES = 2;
-#ifndef CKV_PREFETCH_WGS
-#define CKV_PREFETCH_WGS 2
-#endif
-constexpr int PREFETCH_WGS = CKV_PREFETCH_WGS;  // CSR prefetch workgroups per head in the cooperative launch
 // Cooperative fused launch: polling rounds (each a memory round trip plus a
 // short sleep, about 1 us) before a part scores the missing communities
 // itself; at most 64 parts per head.
@@ -1454,29 +1450,6 @@ __global__ __launch_bounds__(SELECT_THREADS) void select_kernel(DecodeArgs a, De
   select_body<CT, DT, OWN>(a, blockIdx.x % a.st.retrieval_heads, blockIdx.x / a.st.retrieval_heads, parts);
 }
 
-// Workgroups past the parts and the pending update pull the CSR member
-// positions of their head's graph into L2: prefetch workgroup w serves head
-// w % R and the w / R-th of PREFETCH_WGS slices of the row, one 4-byte load
-// per 128-byte line.  With R a multiple of 8 (and the workgroups before it a
-// multiple of 8) its block index is congruent to the head's parts modulo 8,
-// so it runs on their XCD and the slot gather of the selected members hits
-// that L2 instead of memory.  The loaded words are never used; the kernel
-// simply waits for them before the workgroup exits.
-__device__ __forceinline__ void csr_prefetch(const DecodeArgs& a, const int w) {
-  const int R = a.st.retrieval_heads;
-  if (a.csr.member_positions == nullptr) return;
-  const int h = w % R;
-  const int slice = w / R;
-  const int graph = a.st.retrieval_to_graph[h];
-  const int64_t lines = (a.csr.member_stride + 31) / 32;
-  const int64_t per = (lines + PREFETCH_WGS - 1) / PREFETCH_WGS;
-  const int32_t* row = a.csr.member_positions + (int64_t)graph * a.csr.member_stride;
-  uint32_t acc = 0;
-  for (int64_t l = slice * per + threadIdx.x; l < min(lines, (slice + 1) * per); l += blockDim.x)
-    acc |= (uint32_t)gload_i32(row + 32 * l);
-  if (acc == 0x9e3779b9u && threadIdx.x == 1023) a.ws.nearest[0] = (int)acc;  // keeps the loads (never true)
-}
-
 // Fused selection + attention partials: `parts` workgroups per retrieval head
 // (workgroup w: head w / parts, part w % parts); workgroups beyond them run the
 // pending online update of another layer `u`.
@@ -1486,13 +1459,8 @@ __device__ __forceinline__ void csr_prefetch(const DecodeArgs& a, const int w) {
 // part of a head shares one XCD's L2, and each head's parts span the whole
 // dispatch order instead of its tail.
 template <int CT, int DT, int OWN, int PMAX = 0>
-__global__ __launch_bounds__(SELECT_THREADS) void select_attend_kernel(DecodeArgs a, DecodeArgs u, int parts,
-                                                                      int nupd) {
+__global__ __launch_bounds__(SELECT_THREADS) void select_attend_kernel(DecodeArgs a, DecodeArgs u, int parts) {
   const int nsel = a.st.retrieval_heads * parts;
-  if ((int)blockIdx.x >= nsel + nupd) {
-    csr_prefetch(a, (int)blockIdx.x - nsel - nupd);
-    return;
-  }
   if ((int)blockIdx.x >= nsel) {
     const int urh = (int)blockIdx.x - nsel;
     owner_update<CT, DT>(u, urh, u.ws.lse[(int64_t)urh * u.cfg.group_size]);
@@ -1710,14 +1678,8 @@ int launch_select_attend(const DecodeArgs& a, hipStream_t s, const DecodeArgs* p
       u = *pending;
       extra = pending->st.retrieval_heads;
     }
-    // CSR prefetch workgroups only where they still fit the one-workgroup-
-    // per-compute-unit residency of the cooperative launch.
-    const int pf = (coop && PREFETCH_WGS > 0 &&
-                    (int64_t)a.st.retrieval_heads * (parts + PREFETCH_WGS) + extra <= compute_units())
-                       ? a.st.retrieval_heads * PREFETCH_WGS
-                       : 0;
-    hipLaunchKernelGGL(kernel, dim3(a.st.retrieval_heads * parts + extra + pf), dim3(SELECT_THREADS), lds, s, a, u,
-                       parts, extra);
+    hipLaunchKernelGGL(kernel, dim3(a.st.retrieval_heads * parts + extra), dim3(SELECT_THREADS), lds, s, a, u,
+                       parts);
     return launch_check("select_attend");
   };
   constexpr int OWN_MAX = CKV_MAX_SELECT_ROWS / SELECT_THREADS;
