@@ -1529,7 +1529,8 @@ template <int CT, int DT>
 __device__ __forceinline__ void pending_batch_update(const DecodeArgs* __restrict__ utable, int uheads, int w) {
   const DecodeArgs& u = utable[w / uheads];
   const int urh = w % uheads;
-  owner_update<CT, DT>(u, urh, u.ws.lse[(int64_t)urh * u.cfg.group_size]);
+  // nine slots per thread: a 4,096-token budget's 4,235 slots in one load round
+  owner_update<CT, DT, 9>(u, urh, u.ws.lse[(int64_t)urh * u.cfg.group_size]);
 }
 
 template <int CT, int DT, int OWN>
