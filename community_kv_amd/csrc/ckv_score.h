@@ -1,5 +1,6 @@
-// Centroid scoring arithmetic shared by the selection kernels
-// (ckv_select.hip) and the cooperative decode step (ckv_coop.hip): the row
+// Centroid scoring arithmetic shared by every scoring path (the selection
+// kernels and the cooperative decode launch in ckv_select.hip, the
+// prescoring kernels in ckv_select.hip and ckv_select_large.hip): the row
 // fragments one lane holds and the pinned-order dot products, so that every
 // path produces the same fp16 score bits.
 //
