@@ -957,6 +957,25 @@ def run_floor(args, device):
         res["xcd_block_mod8_runs"] += int(all(ids[b] == ids[b % 8] for b in range(blocks)))
     res["xcd_ids_first_16_blocks"] = [int(x) for x in ids[:16]]
     res["xcd_probe_runs"] = 20
+    # practical streaming bandwidth of this GPU, for scale: torch's own copy
+    # (read + write) and sum (read) kernels over buffers below and above the
+    # 256 MB Infinity Cache, HIP events around 10 launches after 3
+    for mib in (256, 4096):
+        a = torch.ones((mib << 20) // 4, dtype=torch.float32, device=device)
+        b = torch.empty_like(a)
+        for name, fn, moved in (("copy", lambda: b.copy_(a), 2), ("sum", lambda: a.sum(), 1)):
+            for _ in range(3):
+                fn()
+            torch.cuda.synchronize(device)
+            t0 = torch.cuda.Event(enable_timing=True)
+            t1 = torch.cuda.Event(enable_timing=True)
+            t0.record()
+            for _ in range(10):
+                fn()
+            t1.record()
+            torch.cuda.synchronize(device)
+            res[f"torch_{name}_{mib}MiB_TBps"] = moved * (mib << 20) / (t0.elapsed_time(t1) / 10 * 1e-3) / 1e12
+        del a, b
     print(json.dumps(res), flush=True)
 
 def main():
