@@ -60,16 +60,11 @@ __device__ void owner_update(const DecodeArgs& a, const int rh, const float s_ls
   // ---- stage 1: exact top-8 over every attended non-sink slot (score desc,
   // position asc, as one packed 64-bit key each).  Each thread keeps a sorted
   // top-8 of its strided share (loaded CH at a time, one round per chunk;
-  // sorted by a 19-comparator network, merged into the running list).  The
-  // eighth largest of the threads' maxima, T8, bounds the answer from below:
-  // every global top-8 key is at least T8, and only the (at most 8) threads
-  // whose maximum reaches T8 hold such keys, so at most 64 candidates remain;
-  // wave 0 sorts them.
+  // sorted by a 19-comparator network, merged into the running list); each
+  // wave then pops its exact top-8 and wave 0 sorts the waves' 64 keys (no
+  // thread's or wave's ninth key can be among the head's best eight).
   {
     __shared__ uint64_t wtop[8 * KAPPA];
-    __shared__ uint64_t cand_s[64];
-    __shared__ uint64_t s_t8;
-    __shared__ int s_ncand;
     const int nt = min((int)blockDim.x, 512);  // threads of this stage
     const int lane = tid & 63, wave = tid >> 6;
     const int scap = a.ws.slot_capacity;
@@ -122,34 +117,23 @@ __device__ void owner_update(const DecodeArgs& a, const int rh, const float s_ls
         cas(loc[0], loc[1]); cas(loc[2], loc[3]); cas(loc[4], loc[5]); cas(loc[6], loc[7]);
       }
     }
-    uint64_t tmax = loc[0];
+    // Exact top-8 of each wave: eight pops of the wave maximum, the lane that
+    // held it advancing to its next key (its list is sorted; keys are unique,
+    // they hold the position).  The eight waves' lists contain the head's
+    // top-8, so one sort of their 64 keys ends the stage.
     for (int r = 0; r < KAPPA; ++r) {
-      const uint64_t best = wave_max_u64(tmax);
+      const uint64_t best = wave_max_u64(loc[0]);
       if (lane == 0 && wave < 8) wtop[wave * KAPPA + r] = best;
-      if (tmax == best) tmax = 0ull;  // keys are unique (they hold the position)
+      const bool pop = best != 0ull && loc[0] == best;
+#pragma unroll
+      for (int k = 0; k < KAPPA - 1; ++k) loc[k] = pop ? loc[k + 1] : loc[k];
+      loc[KAPPA - 1] = pop ? 0ull : loc[KAPPA - 1];
     }
     __syncthreads();
     if (wave == 0) {
       const int n = (nt >> 6) * KAPPA;  // at most 64 (blocks of at most 512 threads)
       const uint64_t srt = wave_sort_desc_u64(lane < n ? wtop[lane] : 0ull);
-      const uint64_t t8 = ((uint64_t)__builtin_amdgcn_readlane((uint32_t)(srt >> 32), KAPPA - 1) << 32) |
-                          (uint32_t)__builtin_amdgcn_readlane((uint32_t)(srt & 0xffffffffu), KAPPA - 1);
-      if (lane == 0) {
-        s_t8 = t8;
-        s_ncand = 0;
-      }
-    }
-    __syncthreads();
-    const uint64_t t8 = s_t8;
-#pragma unroll
-    for (int k = 0; k < KAPPA; ++k) {
-      if (loc[k] != 0ull && loc[k] >= t8) cand_s[atomicAdd(&s_ncand, 1)] = loc[k];
-    }
-    __syncthreads();
-    if (wave == 0) {
-      const int n = s_ncand;
-      const uint64_t v = wave_sort_desc_u64(lane < n ? cand_s[lane] : 0ull);
-      if (lane < KAPPA) top[lane] = v;
+      if (lane < KAPPA) top[lane] = srt;
     }
   }
   if (tid == 64) {
