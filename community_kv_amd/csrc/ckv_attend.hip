@@ -500,9 +500,11 @@ __global__ __launch_bounds__(MERGE_WIDE_THREADS) void merge_wide_batch_kernel(co
 
 template <int PRE, int CT, int DT>
 __global__ __launch_bounds__(MERGE_WIDE_THREADS) void merge_update_kernel(DecodeArgs a, int splits) {
+  Top8First<9> pre;  // the update's first load round, in flight with the merge's
+  top8_first_load<9>(a, blockIdx.x, pre);
   MergeOut mo;
   const float lse0 = merge_wide_body<PRE, true>(a, blockIdx.x, splits, &mo);
-  owner_update<CT, DT>(a, blockIdx.x, lse0);
+  owner_update<CT, DT, 9>(a, blockIdx.x, lse0, &pre);
   merge_store(a, blockIdx.x, mo);
 }
 
@@ -514,9 +516,11 @@ __global__ __launch_bounds__(MERGE_WIDE_THREADS) void merge_update_batch_kernel(
     const DecodeArgs* __restrict__ table, int heads, int splits) {
   const DecodeArgs& a = table[blockIdx.x / heads];
   const int rh = blockIdx.x % heads;
+  Top8First<9> pre;  // the update's first load round, in flight with the merge's
+  top8_first_load<9>(a, rh, pre);
   MergeOut mo;
   const float lse0 = merge_wide_body<PRE, true>(a, rh, splits, &mo);
-  owner_update<CT, DT, 9>(a, rh, lse0);  // 71.0 against 72.3 us per config-4 step with 8
+  owner_update<CT, DT, 9>(a, rh, lse0, &pre);  // nine slots per thread: one round at config 4
   merge_store(a, rh, mo);
 }
 

@@ -19,8 +19,31 @@ namespace ckv {
 // tail-chunk state, in flight during the assignment; then the stores.
 // CH: slots each thread loads per round of the top-8 stage (8 or 9; 9 lets
 // 512 threads take a 4,096-token budget's 4,235 slots in one round).
+// The top-8 stage's first load round (scores and positions of slots
+// c * nt + tid, c < CH), issued early by a caller that has a load round of its
+// own to overlap it with (the split merge before the update).
+template <int CH>
+struct Top8First {
+  float sv[CH];
+  int pv[CH];
+};
+
+template <int CH>
+__device__ __forceinline__ void top8_first_load(const DecodeArgs& a, const int rh, Top8First<CH>& f) {
+  const int tid = threadIdx.x;
+  const int nt = min((int)blockDim.x, 512);
+  const int scap = a.ws.slot_capacity;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int s = min(c * nt + tid, scap - 1);
+    f.sv[c] = gload_f32(a.ws.slot_scores + (int64_t)rh * scap + s);
+    f.pv[c] = gload_i32(a.ws.slot_positions + (int64_t)rh * scap + s);
+  }
+}
+
 template <int CT, int DT, int CH = 8>
-__device__ void owner_update(const DecodeArgs& a, const int rh, const float s_lse0) {
+__device__ void owner_update(const DecodeArgs& a, const int rh, const float s_lse0,
+                             const Top8First<CH>* pre = nullptr) {
   static_assert(CH == 8 || CH == 9, "the top-8 stage sorts 8 or 9 keys per round");
   const int tid = threadIdx.x;
   const int graph = a.st.retrieval_to_graph[rh];
@@ -81,11 +104,19 @@ __device__ void owner_update(const DecodeArgs& a, const int rh, const float s_ls
     for (int s0 = 0; s0 < scap; s0 += CH * nt) {
       float sv[CH];
       int pv[CH];
+      if (s0 == 0 && pre != nullptr) {
 #pragma unroll
-      for (int c = 0; c < CH; ++c) {
-        const int s = min(s0 + c * nt + tid, scap - 1);
-        sv[c] = gload_f32(scs + s);
-        pv[c] = gload_i32(sps + s);
+        for (int c = 0; c < CH; ++c) {
+          sv[c] = pre->sv[c];
+          pv[c] = pre->pv[c];
+        }
+      } else {
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+          const int s = min(s0 + c * nt + tid, scap - 1);
+          sv[c] = gload_f32(scs + s);
+          pv[c] = gload_i32(sps + s);
+        }
       }
       uint64_t v[CH];
 #pragma unroll
